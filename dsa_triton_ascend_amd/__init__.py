@@ -1,0 +1,13 @@
+"""MI355X-native DSA operator set (gfx950 HIP kernels behind a C ABI).
+
+Public API, mirroring the reference's operator modules:
+
+* ``sparse_flash_attention_triton`` / ``SparseFlashAttentionTriton``
+"""
+from .sparse_flash_attention import (  # noqa: F401
+    INT64_MAX,
+    SparseFlashAttentionTriton,
+    sparse_flash_attention_triton,
+)
+
+sparse_flash_attention = sparse_flash_attention_triton

@@ -1,0 +1,99 @@
+"""ctypes binding of libdsa_hip.so (declared in include/dsa_capi.h).
+
+torch is imported before the library is loaded so that the library binds to
+the HIP runtime torch already carries (both use the soname libamdhip64.so.7);
+streams and device pointers handed over from torch are then valid inside the
+library.  There is no CPU fallback: a missing library raises at first use.
+"""
+import ctypes
+import os
+
+import torch  # noqa: F401  (must be loaded before the HIP library)
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("DSA_HIP_LIB", os.path.join(_PKG, "libdsa_hip.so"))
+
+DSA_OK = 0
+DSA_ERR_INVALID = 1
+DSA_ERR_UNSUPPORTED = 2
+DSA_ERR_HIP = 3
+DSA_ERR_WORKSPACE = 4
+
+DTYPE_BF16 = 0
+DTYPE_FP16 = 1
+DTYPE_FP32 = 2
+
+LAYOUT = {"BSND": 0, "TND": 1, "PA_BSND": 2}
+
+_c = ctypes
+_vp = _c.c_void_p
+_i32p = _c.c_void_p
+_i64 = _c.c_int64
+_i32 = _c.c_int32
+_f32 = _c.c_float
+_sz = _c.c_size_t
+
+# name -> (restype, argtypes); mirrors include/dsa_capi.h
+SIGNATURES = {
+    "dsa_last_error": (_c.c_char_p, []),
+    "dsa_abi_version": (_c.c_int, []),
+    "dsa_sfa_fwd": (_c.c_int, [
+        _vp, _vp, _vp, _vp, _i32p,           # query, query_rope, key, key_rope, sparse_indices
+        _vp, _vp, _vp,                        # attention_out, softmax_max, softmax_sum
+        _i32p, _i32p, _i32p,                  # actual_seq_q, actual_seq_kv, block_table
+        _i64, _i64, _i64, _i64, _i64, _i64,   # batch, s1, s2, n1, d, d_rope
+        _i64, _i64, _i64, _i64, _i64,         # sparse_count, q_rows, kv_rows, max_blocks, page_size
+        _i32, _i32, _i32, _i32, _i32,         # sparse_block_size, sparse_mode, layout_q, layout_kv, dtype
+        _f32, _i32,                           # scale_value, return_lse
+        _vp, _sz, _vp,                        # workspace, workspace_bytes, stream
+    ]),
+    "dsa_sfa_fwd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32]),
+}
+
+_lib = None
+
+
+def load():
+    """Load (once) and return the ctypes library; raises if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"libdsa_hip.so not found at {LIB_PATH}; build it with "
+            "`python -m dsa_triton_ascend_amd.build_lib` (no CPU fallback exists)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(status, what):
+    if status == DSA_OK:
+        return
+    msg = load().dsa_last_error().decode(errors="replace")
+    if status in (DSA_ERR_INVALID, DSA_ERR_UNSUPPORTED, DSA_ERR_WORKSPACE):
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: {msg}")
+
+
+def ptr(t):
+    """Device pointer of a tensor (None -> NULL)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dt):
+    if dt == torch.bfloat16:
+        return DTYPE_BF16
+    if dt == torch.float16:
+        return DTYPE_FP16
+    if dt == torch.float32:
+        return DTYPE_FP32
+    raise ValueError(f"unsupported dtype {dt}")

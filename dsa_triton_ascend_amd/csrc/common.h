@@ -1,0 +1,113 @@
+// Shared device/host helpers for the DSA HIP library (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/dsa_capi.h"
+
+namespace dsa {
+
+// ---------------------------------------------------------------------------
+// element types and MFMA operand vectors
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16;
+typedef _Float16 f16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Element traits: storage type <-> fp32, and the 16x16x32 MFMA for it.
+template <typename T> struct Elem;
+
+template <> struct Elem<bf16> {
+  typedef bf16x8 v8;
+  static __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+  static __device__ __forceinline__ bf16 from_f32(float x) { return (bf16)x; }
+  static __device__ __forceinline__ f32x4 mfma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <> struct Elem<f16> {
+  typedef f16x8 v8;
+  static __device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
+  static __device__ __forceinline__ f16 from_f32(float x) { return (f16)x; }
+  static __device__ __forceinline__ f32x4 mfma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// 16-byte <-> 8-element vector reinterpretation.
+template <typename V>
+__device__ __forceinline__ V as_v8(u32x4 x) { return __builtin_bit_cast(V, x); }
+template <typename V>
+__device__ __forceinline__ u32x4 as_u4(V x) { return __builtin_bit_cast(u32x4, x); }
+
+// Hardware exp2 (v_exp_f32); callers keep arguments <= 0 or -inf.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Butterfly max/sum across the four 16-lane groups that share lane%16.
+__device__ __forceinline__ float xgroup_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ float xgroup_sum(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// LDS chunk swizzle for 16-byte chunks of token rows: the low three bits of
+// the chunk index are XORed with a per-token permutation so that (a) eight
+// consecutive tokens reading the same chunk hit eight distinct 16-byte bank
+// groups, and (b) the four rows read together by one 16-lane group of a
+// transposed 8-byte load land in disjoint bank groups.
+__device__ __forceinline__ int chunk_swz(int tok) { return ((tok & 3) << 1) | ((tok >> 2) & 1); }
+__device__ __forceinline__ int swz_chunk(int chunk, int tok) { return chunk ^ chunk_swz(tok); }
+
+}  // namespace dsa
+
+// ---------------------------------------------------------------------------
+// host-side error plumbing shared by the C-ABI entry points
+// ---------------------------------------------------------------------------
+namespace dsa {
+void set_error(const char* fmt, ...);
+int hip_fail(hipError_t e, const char* what);
+}  // namespace dsa
+
+#define DSA_CHECK_ARG(cond, ...)                                  \
+  do {                                                            \
+    if (!(cond)) {                                                \
+      ::dsa::set_error(__VA_ARGS__);                              \
+      return DSA_ERR_INVALID;                                     \
+    }                                                             \
+  } while (0)
+
+#define DSA_CHECK_SUPPORTED(cond, ...)                            \
+  do {                                                            \
+    if (!(cond)) {                                                \
+      ::dsa::set_error(__VA_ARGS__);                              \
+      return DSA_ERR_UNSUPPORTED;                                 \
+    }                                                             \
+  } while (0)
+
+#define DSA_HIP(expr)                                             \
+  do {                                                            \
+    hipError_t _e = (expr);                                       \
+    if (_e != hipSuccess) return ::dsa::hip_fail(_e, #expr);      \
+  } while (0)

@@ -1,0 +1,597 @@
+// Sparse flash attention forward for gfx950 (MLA-absorb, MQA).
+//
+// Semantics follow the reference kernel `_sfa_kernel`
+// (sparse_flash_attention_triton.py:150-332): a token of query row (b, s1) is
+// attended iff its id is not -1, id < threshold and id < act_k, where
+// threshold = act_k (mode 0) or act_k - act_q + s1 + 1 (mode 3), and the row
+// is active iff s1 < act_q and threshold > 0 (247-254, 270-272); scores are
+// (q_nope.k_nope + q_rope.k_rope) * scale in fp32; value = key[:, :D];
+// softmax_max / softmax_sum are the row max and sum of exp(score - max)
+// (326-332).  Paged KV (block_table), TND rows and block-wise ids are
+// resolved in the kernel instead of on the host
+// (sparse_flash_attention_triton.py:345-421).
+//
+// Design (one workgroup = one query row, all heads; 4 waves x 32 heads):
+//  * The row's index range is compacted into an LDS list of physical KV rows
+//    (invalid ids dropped), so ragged / -1 padded rows cost nothing.
+//  * Tiles of 32 tokens are gathered HBM -> registers -> LDS (16-byte loads,
+//    double-buffered: the next tile's loads are in flight during the current
+//    tile's MFMAs).  Token rows are stored with an XOR chunk swizzle.
+//  * Each wave keeps its 32 heads of Q (D + 64 columns, bf16) in registers
+//    as MFMA B operands and its O^T accumulator [D x 32] in fp32 registers.
+//  * S^T = K . Q^T on v_mfma_f32_16x16x32 (K rows from LDS, ds_read_b128):
+//    the result layout puts one head per lane column, so the online softmax
+//    (exp2 domain) is lane-local plus a 4-lane butterfly, and P^T is already
+//    in B-operand layout for the second product.
+//  * O^T += V^T . P^T with V^T fragments read straight from the row-major K
+//    tile by ds_read_b64_tr_b16 (the transposing LDS read of gfx950).
+//  * When there are fewer rows than CUs the row's tokens are split across
+//    workgroups (all on one XCD) and a combine kernel merges the partial
+//    (O, max, sum) triples.
+#include "common.h"
+
+namespace dsa {
+
+struct SfaFwdParams {
+  const void* q;
+  const void* qr;
+  const void* k;
+  const void* kr;
+  const int32_t* idx;
+  const int32_t* act_q;
+  const int32_t* act_k;
+  const int32_t* block_table;
+  void* out;
+  float* smax;
+  float* ssum;
+  float* part_o;   // [splits, R, N1, D] unnormalised partial O (splits > 1)
+  float* part_ml;  // [splits, R, N1, 4]: reference max, sum, exact max (log2 units), pad
+  int64_t rows;
+  int64_t kv_rows;
+  int32_t batch, s1, s2, n1, K;
+  int32_t bs;  // sparse_block_size
+  int32_t mode, layout_q, layout_kv;
+  int32_t max_blocks, page_size;
+  int32_t splits, rows_per_xcd, pos_per_split;
+  float scale_log2;
+  int32_t return_lse;
+};
+
+constexpr int kSfaTile = 32;
+constexpr int kSfaMaxList = 4096;
+constexpr int kSfaThreads = 256;
+constexpr float kRescaleLog2 = 8.f;
+
+struct RowInfo {
+  int b, s1, act_q, act_k, threshold;
+  int64_t kv_base;
+  bool active;
+};
+
+__device__ __forceinline__ RowInfo sfa_row_info(const SfaFwdParams& p, int row) {
+  RowInfo ri;
+  if (p.layout_q == DSA_LAYOUT_TND) {
+    // cumulative lengths: first b with cu[b] > row
+    int lo = 0, hi = p.batch - 1;
+    while (lo < hi) {
+      int mid = (lo + hi) >> 1;
+      if (p.act_q[mid] > row) hi = mid; else lo = mid + 1;
+    }
+    ri.b = lo;
+    int start = lo ? p.act_q[lo - 1] : 0;
+    ri.s1 = row - start;
+    ri.act_q = p.act_q[lo] - start;
+  } else {
+    ri.b = row / p.s1;
+    ri.s1 = row - ri.b * p.s1;
+    ri.act_q = p.act_q ? p.act_q[ri.b] : p.s1;
+  }
+  if (p.layout_kv == DSA_LAYOUT_TND) {
+    int start = ri.b ? p.act_k[ri.b - 1] : 0;
+    ri.kv_base = start;
+    ri.act_k = p.act_k[ri.b] - start;
+  } else {
+    ri.kv_base = (int64_t)ri.b * p.s2;  // unused for PA_BSND
+    ri.act_k = p.act_k ? p.act_k[ri.b] : p.s2;
+  }
+  ri.threshold = p.mode == 0 ? ri.act_k : ri.act_k - ri.act_q + ri.s1 + 1;
+  ri.active = (ri.s1 < ri.act_q) && (ri.threshold > 0);
+  return ri;
+}
+
+// Resolve index position `pos` of a row to a physical KV row.
+// Returns false if the position is not attended; *phys = -1 marks a token that
+// is attended but lives in a -1 / out-of-range page (reads as a zero row, as
+// the reference's de-paging leaves such spans zero, lines 391-397).
+__device__ __forceinline__ bool sfa_resolve(const SfaFwdParams& p, const RowInfo& ri,
+                                            const int32_t* idx_row, int pos, int* phys) {
+  int id = idx_row[pos / p.bs];
+  if (id < 0) return false;
+  int64_t tok = (int64_t)id * p.bs + (pos % p.bs);
+  if (tok >= ri.threshold || tok >= ri.act_k) return false;
+  if (p.layout_kv == DSA_LAYOUT_PA_BSND) {
+    if (tok >= (int64_t)p.max_blocks * p.page_size) return false;
+    int blk = p.block_table[(int64_t)ri.b * p.max_blocks + tok / p.page_size];
+    int64_t r = (int64_t)blk * p.page_size + tok % p.page_size;
+    *phys = (blk < 0 || r >= p.kv_rows) ? -1 : (int)r;
+    return true;
+  }
+  if (p.layout_kv == DSA_LAYOUT_BSND && tok >= p.s2) return false;
+  int64_t r = ri.kv_base + tok;
+  if (r >= p.kv_rows) return false;
+  *phys = (int)r;
+  return true;
+}
+
+// HT = head tiles (of 16 heads) per wave; a workgroup covers 4*HT*16 heads.
+template <int D, typename T, int HT>
+__global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p) {
+  using E = Elem<T>;
+  using V8 = typename E::v8;
+  constexpr int DR = 64;
+  constexpr int KS = (D + DR) / 32;  // GEMM1 k-steps
+  constexpr int KSN = D / 32;        // of which from the nope part
+  constexpr int NDT = D / 16;        // GEMM2 d-tiles
+  constexpr int TILE = kSfaTile;
+  constexpr int NOPE_BYTES = TILE * D * 2;
+  constexpr int BUF_BYTES = NOPE_BYTES + TILE * DR * 2;
+  constexpr int NOPE_CH = D / 8;                         // 16-byte chunks per nope row
+  constexpr int NLOAD = (TILE * (NOPE_CH + 8)) / kSfaThreads;
+  constexpr int NLOAD_NOPE = (TILE * NOPE_CH) / kSfaThreads;
+  static_assert(TILE * NOPE_CH % kSfaThreads == 0, "tile split");
+
+  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * BUF_BYTES];
+  __shared__ int s_list[kSfaMaxList];
+  __shared__ int s_wcnt[4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int li = lane & 15;  // lane within 16-lane group
+  const int lg = lane >> 4;  // 16-lane group
+
+  // ---- block -> (row, split, head group); a row's blocks share an XCD ----
+  constexpr int HEADS_PER_WG = 4 * HT * 16;
+  const int hgroups = (p.n1 + HEADS_PER_WG - 1) / HEADS_PER_WG;
+  const int bid = blockIdx.x;
+  const int jj = bid >> 3;
+  const int hg = jj % hgroups;
+  const int jr = jj / hgroups;
+  const int64_t row = (int64_t)(bid & 7) * p.rows_per_xcd + jr / p.splits;
+  const int split = jr % p.splits;
+  if (row >= p.rows) return;
+
+  const RowInfo ri = sfa_row_info(p, (int)row);
+  const int32_t* idx_row = p.idx + row * p.K;
+  const int total_pos = p.K * p.bs;
+  const int p0 = split * p.pos_per_split;
+  const int p1 = min(total_pos, p0 + p.pos_per_split);
+
+  // ---- compact attended positions into s_list (stable order) ----
+  int n_valid = 0;
+  for (int c0 = p0; c0 < p1; c0 += kSfaThreads) {
+    int pos = c0 + tid;
+    int phys = 0;
+    bool valid = false;
+    if (ri.active && pos < p1) valid = sfa_resolve(p, ri, idx_row, pos, &phys);
+    unsigned long long m = __ballot(valid);
+    if (lane == 0) s_wcnt[wave] = __popcll(m);
+    __syncthreads();
+    int off = n_valid;
+    int tot = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      int c = s_wcnt[w];
+      off += (w < wave) ? c : 0;
+      tot += c;
+    }
+    if (valid) s_list[off + __popcll(m & ((1ull << lane) - 1ull))] = phys;
+    n_valid += tot;
+    __syncthreads();
+  }
+
+  const int head0 = hg * HEADS_PER_WG + wave * HT * 16;
+  const bool wave_active = head0 < p.n1;
+
+  // ---- Q fragments (B operand of S^T = K.Q^T): lane -> head li, k = 8*lg.. ----
+  V8 qf[HT][KS];
+#pragma unroll
+  for (int ht = 0; ht < HT; ++ht) {
+    const int head = head0 + ht * 16 + li;
+    const bool hv = head < p.n1;
+    const int64_t hsafe = row * p.n1 + (hv ? head : 0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 v;
+      if (ks < KSN) v = *(const u32x4*)((const T*)p.q + hsafe * D + ks * 32 + lg * 8);
+      else v = *(const u32x4*)((const T*)p.qr + hsafe * DR + (ks - KSN) * 32 + lg * 8);
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      qf[ht][ks] = as_v8<V8>(hv ? v : z);
+    }
+  }
+
+  f32x4 acc_o[NDT][HT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) acc_o[dt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  float m_ref[HT], m_true[HT], l_run[HT];
+#pragma unroll
+  for (int ht = 0; ht < HT; ++ht) {
+    m_ref[ht] = -INFINITY;   // reference max of P and O (log2 units)
+    m_true[ht] = -INFINITY;  // exact running max (log2 units)
+    l_run[ht] = 0.f;         // lane-partial sum of exp2(s - m_ref)
+  }
+
+  const int n_tiles = (n_valid + TILE - 1) / TILE;
+
+  // ---- tile loader: global -> registers, registers -> swizzled LDS ----
+  u32x4 stage[NLOAD];
+  auto load_tile = [&](int t) {
+#pragma unroll
+    for (int it = 0; it < NLOAD; ++it) {
+      const int c = it * kSfaThreads + tid;
+      int tk, cc;
+      if (it < NLOAD_NOPE) { tk = c / NOPE_CH; cc = c % NOPE_CH; }
+      else { const int c2 = c - TILE * NOPE_CH; tk = c2 >> 3; cc = c2 & 7; }
+      const int slot = t * TILE + tk;
+      const int phys = slot < n_valid ? s_list[slot] : -1;
+      const int64_t ps = phys >= 0 ? phys : 0;  // row 0 is a safe address
+      u32x4 v;
+      if (it < NLOAD_NOPE) v = *(const u32x4*)((const T*)p.k + ps * D + cc * 8);
+      else v = *(const u32x4*)((const T*)p.kr + ps * DR + cc * 8);
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      stage[it] = phys >= 0 ? v : z;
+    }
+  };
+  auto store_tile = [&](int buf) {
+    unsigned char* base = smem + buf * BUF_BYTES;
+#pragma unroll
+    for (int it = 0; it < NLOAD; ++it) {
+      const int c = it * kSfaThreads + tid;
+      if (it < NLOAD_NOPE) {
+        const int tk = c / NOPE_CH, cc = c % NOPE_CH;
+        *(u32x4*)(base + tk * (D * 2) + swz_chunk(cc, tk) * 16) = stage[it];
+      } else {
+        const int c2 = c - TILE * NOPE_CH;
+        const int tk = c2 >> 3, cc = c2 & 7;
+        *(u32x4*)(base + NOPE_BYTES + tk * (DR * 2) + swz_chunk(cc, tk) * 16) = stage[it];
+      }
+    }
+  };
+
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+
+  if (!wave_active) {
+    // waves without heads (N1 < 128) only help with the gather
+    for (int t = 0; t < n_tiles; ++t) {
+      if (t + 1 < n_tiles) load_tile(t + 1);
+      __syncthreads();
+      if (t + 1 < n_tiles) store_tile((t & 1) ^ 1);
+    }
+    return;
+  }
+
+  for (int t = 0; t < n_tiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < n_tiles) load_tile(t + 1);
+    __syncthreads();
+
+    {
+      const unsigned char* base = smem + buf * BUF_BYTES;
+      // ---- GEMM1: S^T[32 tok x HT*16 heads] ----
+      f32x4 acc_s[2][HT];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) acc_s[tt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          const int tk = tt * 16 + li;
+          u32x4 a;
+          if (ks < KSN) {
+            a = *(const u32x4*)(base + tk * (D * 2) + swz_chunk(ks * 4 + lg, tk) * 16);
+          } else {
+            a = *(const u32x4*)(base + NOPE_BYTES + tk * (DR * 2) +
+                                swz_chunk((ks - KSN) * 4 + lg, tk) * 16);
+          }
+          const V8 av = as_v8<V8>(a);
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) acc_s[tt][ht] = E::mfma(av, qf[ht][ks], acc_s[tt][ht]);
+        }
+      }
+
+      // ---- online softmax (log2 domain), P^T fragments ----
+      // Lazy rescaling: probabilities are taken relative to a reference max
+      // m_ref that is only raised (and O rescaled) when a head's max grows
+      // by more than 2^kRescaleLog2; m_true tracks the exact max for the
+      // returned statistics.  P values stay <= 2^kRescaleLog2.
+      V8 pf[HT];
+      bool need = false;
+      float m_new_ref[HT];
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) {
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int tok = t * TILE + tt * 16 + lg * 4 + r;
+            float v = acc_s[tt][ht][r] * p.scale_log2;
+            v = tok < n_valid ? v : -INFINITY;
+            acc_s[tt][ht][r] = v;
+            tmax = fmaxf(tmax, v);
+          }
+        }
+        tmax = xgroup_max(tmax);
+        m_true[ht] = fmaxf(m_true[ht], tmax);
+        float mr = m_ref[ht];
+        if (mr == -INFINITY) {
+          mr = tmax;  // nothing accumulated yet for this head
+        } else if (tmax > mr + kRescaleLog2) {
+          mr = tmax;
+          need = true;
+        }
+        m_new_ref[ht] = mr;
+      }
+      if (__builtin_expect(__any(need), 0)) {
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) {
+          const float alpha = m_ref[ht] == -INFINITY ? 1.f : fast_exp2(m_ref[ht] - m_new_ref[ht]);
+          l_run[ht] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) acc_o[dt][ht] *= alpha;
+        }
+      }
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) {
+        m_ref[ht] = m_new_ref[ht];
+        V8 pvv;
+        float lsum = 0.f;
+        if (m_ref[ht] == -INFINITY) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) pvv[j] = E::from_f32(0.f);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float e = fast_exp2(acc_s[j >> 2][ht][j & 3] - m_ref[ht]);
+            lsum += e;
+            pvv[j] = E::from_f32(e);
+          }
+        }
+        l_run[ht] += lsum;
+        pf[ht] = pvv;
+      }
+
+      // ---- GEMM2: O^T[D x HT*16 heads] += V^T . P^T ----
+      const int r1 = lg * 4 + (li >> 2);
+      const int r2 = 16 + r1;
+      const int byte_in = ((li & 3) & 1) * 8;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int ch = dt * 2 + ((li & 3) >> 1);
+        const unsigned char* a1 = base + r1 * (D * 2) + swz_chunk(ch, r1) * 16 + byte_in;
+        const unsigned char* a2 = base + r2 * (D * 2) + swz_chunk(ch, r2) * 16 + byte_in;
+        const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)a1);
+        const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)a2);
+        const i16x4 w1 = __builtin_bit_cast(i16x4, v1);
+        const i16x4 w2 = __builtin_bit_cast(i16x4, v2);
+        const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
+        const V8 av = __builtin_bit_cast(V8, w);
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) acc_o[dt][ht] = E::mfma(av, pf[ht], acc_o[dt][ht]);
+      }
+    }
+
+    if (t + 1 < n_tiles) store_tile(buf ^ 1);
+  }
+
+  // ---- epilogue ----
+#pragma unroll
+  for (int ht = 0; ht < HT; ++ht) {
+    const int head = head0 + ht * 16 + li;
+    const float l_tot = xgroup_sum(l_run[ht]);
+    if (head >= p.n1) continue;
+    const int64_t orow = row * p.n1 + head;
+    if (p.splits == 1) {
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+      T* op = (T*)p.out + orow * D;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const f32x4 v = acc_o[dt][ht];
+        typedef T T4 __attribute__((ext_vector_type(4)));
+        T4 o;
+        o[0] = E::from_f32(v[0] * inv);
+        o[1] = E::from_f32(v[1] * inv);
+        o[2] = E::from_f32(v[2] * inv);
+        o[3] = E::from_f32(v[3] * inv);
+        *(T4*)(op + dt * 16 + lg * 4) = o;
+      }
+      if (p.return_lse && lg == 0) {
+        const bool any = l_tot > 0.f;
+        p.smax[orow] = any ? m_true[ht] * kLn2 : 0.f;
+        p.ssum[orow] = any ? l_tot * fast_exp2(m_ref[ht] - m_true[ht]) : 0.f;
+      }
+    } else {
+      const int64_t prow = (int64_t)split * p.rows * p.n1 + orow;
+      float* po = p.part_o + prow * D;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) *(f32x4*)(po + dt * 16 + lg * 4) = acc_o[dt][ht];
+      if (lg == 0) {
+        f32x4 ml = {m_ref[ht], l_tot, m_true[ht], 0.f};
+        *(f32x4*)(p.part_ml + prow * 4) = ml;
+      }
+    }
+  }
+}
+
+// Merge per-split partials: one wave per (row, head).  Partial i holds
+// O_i and l_i relative to its reference max r_i and its exact max t_i (log2
+// units); the merged output is sum_i 2^(r_i-M) O_i / sum_i 2^(r_i-M) l_i.
+template <int D, typename T>
+__global__ __launch_bounds__(256) void sfa_combine_kernel(SfaFwdParams p) {
+  using E = Elem<T>;
+  const int lane = threadIdx.x & 63;
+  const int64_t rh = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (rh >= p.rows * p.n1) return;
+  float mref = -INFINITY, mtrue = -INFINITY;
+  for (int s = 0; s < p.splits; ++s) {
+    const f32x4 ml = *(const f32x4*)(p.part_ml + ((int64_t)s * p.rows * p.n1 + rh) * 4);
+    if (ml[1] > 0.f) {
+      mref = fmaxf(mref, ml[0]);
+      mtrue = fmaxf(mtrue, ml[2]);
+    }
+  }
+  constexpr int PER = D / 64;
+  float acc[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) acc[j] = 0.f;
+  float L = 0.f;
+  if (mref != -INFINITY) {
+    for (int s = 0; s < p.splits; ++s) {
+      const int64_t prow = (int64_t)s * p.rows * p.n1 + rh;
+      const f32x4 ml = *(const f32x4*)(p.part_ml + prow * 4);
+      if (!(ml[1] > 0.f)) continue;
+      const float w = fast_exp2(ml[0] - mref);
+      L += w * ml[1];
+      const float* po = p.part_o + prow * D + lane * PER;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) acc[j] += w * po[j];
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  T* op = (T*)p.out + rh * D + lane * PER;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) op[j] = E::from_f32(acc[j] * inv);
+  if (p.return_lse && lane == 0) {
+    p.smax[rh] = L > 0.f ? mtrue * kLn2 : 0.f;
+    p.ssum[rh] = L > 0.f ? L * fast_exp2(mref - mtrue) : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+static int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+int sfa_fwd_head_groups(int64_t n1, int64_t d);
+
+int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
+  const int cus = device_cu_count();
+  const int64_t units = rows * sfa_fwd_head_groups(n1, d);
+  int64_t splits = 1;
+  if (units < cus) {
+    const int64_t want = (cus + units - 1) / units;
+    const int64_t by_len = (total_pos + 255) / 256;
+    splits = want < by_len ? want : by_len;
+    if (splits < 1) splits = 1;
+  }
+  while ((total_pos + splits - 1) / splits > kSfaMaxList) ++splits;
+  return (int)splits;
+}
+
+size_t sfa_fwd_workspace_bytes(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
+  const int splits = sfa_fwd_splits(rows, n1, d, total_pos);
+  if (splits <= 1) return 0;
+  return (size_t)splits * rows * n1 * (d + 4) * sizeof(float);
+}
+
+// Head tiles per wave: D=512 keeps 16 heads per wave so that the O
+// accumulator (D x 16 fp32) and Q fragments fit the register file.
+template <int D> struct SfaHT { static constexpr int value = D >= 512 ? 1 : 2; };
+
+int sfa_fwd_head_groups(int64_t n1, int64_t d) {
+  const int heads_per_wg = 4 * 16 * (d >= 512 ? 1 : 2);
+  return (int)((n1 + heads_per_wg - 1) / heads_per_wg);
+}
+
+template <int D, typename T>
+static hipError_t launch_sfa_fwd(SfaFwdParams& p, hipStream_t stream) {
+  const int64_t rows_per_xcd = (p.rows + 7) / 8;
+  p.rows_per_xcd = (int)rows_per_xcd;
+  const int64_t blocks = 8 * rows_per_xcd * p.splits * sfa_fwd_head_groups(p.n1, D);
+  hipLaunchKernelGGL((sfa_fwd_kernel<D, T, SfaHT<D>::value>), dim3((unsigned)blocks),
+                     dim3(kSfaThreads), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.splits == 1) return e;
+  const int64_t cblocks = (p.rows * p.n1 + 3) / 4;
+  hipLaunchKernelGGL((sfa_combine_kernel<D, T>), dim3((unsigned)cblocks), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+int sfa_fwd_run(const void* query, const void* query_rope, const void* key, const void* key_rope,
+                const int32_t* sparse_indices, void* attention_out, float* softmax_max,
+                float* softmax_sum, const int32_t* actual_seq_q, const int32_t* actual_seq_kv,
+                const int32_t* block_table, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
+                int64_t d, int64_t sparse_count, int64_t q_rows, int64_t kv_rows,
+                int64_t max_blocks, int64_t page_size, int32_t sparse_block_size,
+                int32_t sparse_mode, int32_t layout_query, int32_t layout_kv, int32_t dtype,
+                float scale_value, int32_t return_lse, void* workspace, hipStream_t stream) {
+  SfaFwdParams p;
+  p.q = query;
+  p.qr = query_rope;
+  p.k = key;
+  p.kr = key_rope;
+  p.idx = sparse_indices;
+  p.act_q = actual_seq_q;
+  p.act_k = actual_seq_kv;
+  p.block_table = block_table;
+  p.out = attention_out;
+  p.smax = softmax_max;
+  p.ssum = softmax_sum;
+  p.rows = q_rows;
+  p.kv_rows = kv_rows;
+  p.batch = (int32_t)batch;
+  p.s1 = (int32_t)s1;
+  p.s2 = layout_kv == DSA_LAYOUT_PA_BSND ? (int32_t)(max_blocks * page_size) : (int32_t)s2;
+  p.n1 = (int32_t)n1;
+  p.K = (int32_t)sparse_count;
+  p.bs = sparse_block_size;
+  p.mode = sparse_mode;
+  p.layout_q = layout_query;
+  p.layout_kv = layout_kv;
+  p.max_blocks = (int32_t)max_blocks;
+  p.page_size = (int32_t)page_size;
+  const int64_t total_pos = sparse_count * (int64_t)sparse_block_size;
+  p.splits = sfa_fwd_splits(q_rows, n1, d, total_pos);
+  p.pos_per_split = (int32_t)((total_pos + p.splits - 1) / p.splits);
+  p.part_o = nullptr;
+  p.part_ml = nullptr;
+  if (p.splits > 1) {
+    p.part_o = (float*)workspace;
+    p.part_ml = p.part_o + (size_t)p.splits * q_rows * n1 * d;
+  }
+  p.scale_log2 = scale_value * kLog2e;
+  p.return_lse = return_lse;
+  p.rows_per_xcd = 0;
+  hipError_t e;
+  if (dtype == DSA_DTYPE_BF16) {
+    e = d == 512 ? launch_sfa_fwd<512, bf16>(p, stream)
+      : d == 256 ? launch_sfa_fwd<256, bf16>(p, stream)
+                 : launch_sfa_fwd<128, bf16>(p, stream);
+  } else {
+    e = d == 512 ? launch_sfa_fwd<512, f16>(p, stream)
+      : d == 256 ? launch_sfa_fwd<256, f16>(p, stream)
+                 : launch_sfa_fwd<128, f16>(p, stream);
+  }
+  if (e != hipSuccess) return hip_fail(e, "sfa_fwd launch");
+  return DSA_OK;
+}
+
+}  // namespace dsa

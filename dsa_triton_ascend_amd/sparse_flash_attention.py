@@ -1,0 +1,232 @@
+"""sparse_flash_attention forward on MI355X: the reference's public API over
+the HIP library.
+
+Drop-in for ``sparse_flash_attention_triton`` / ``SparseFlashAttentionTriton``
+(sparse_flash_attention_triton.py:483-695): same argument names, defaults,
+guards (ValueError on the same conditions, 529-539 and 579-586), layouts
+(BSND / TND query; BSND / TND / PA_BSND key) and return tuple
+``(attention_out, softmax_max, softmax_sum)``.  The host-side layout
+normalisation of the reference (TND unpacking, PA de-paging, block-id
+expansion, lines 551-611) is done inside the kernel instead: no host loops,
+no device->host synchronisation.
+
+Deliberate differences, all on inputs the reference does not handle:
+* a block_table entry outside [0, blocks) reads as a zero row like -1
+  (the reference would raise while slicing);
+* ``block_size`` must equal key.shape[1] when given (the reference mixes the
+  two sizes in its de-paging loop, lines 569-571 vs 388).
+"""
+import torch
+
+from . import _lib
+
+INT64_MAX = 9223372036854775807
+
+_VALID_D = (128, 256, 512)
+_D_ROPE = 64
+_VALID_N1 = (1, 2, 4, 8, 16, 32, 64, 128)
+
+
+def _seq_tensor(x, device):
+    if x is None:
+        return None
+    if isinstance(x, torch.Tensor):
+        return x.to(device=device, dtype=torch.int32).contiguous()
+    return torch.tensor(list(x), dtype=torch.int32, device=device)
+
+
+def _check_device(*tensors):
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("sparse_flash_attention requires tensors on a ROCm GPU device "
+                             "(this implementation has no CPU path)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError("all tensors must be on the same device")
+    return dev
+
+
+def sparse_flash_attention_triton(
+    query,
+    key,
+    value,
+    sparse_indices,
+    scale_value=1.0,
+    block_table=None,
+    actual_seq_lengths_query=None,
+    actual_seq_lengths_kv=None,
+    query_rope=None,
+    key_rope=None,
+    sparse_block_size=1,
+    layout_query="BSND",
+    layout_kv="BSND",
+    sparse_mode=0,
+    pre_tokens=INT64_MAX,
+    next_tokens=INT64_MAX,
+    attention_mode=2,
+    return_softmax_lse=False,
+    block_size=0,
+):
+    """Sparse flash attention forward (MLA-absorb, MQA); see module docstring.
+
+    Args mirror sparse_flash_attention_triton.py:505-526.  ``value`` is
+    ignored (value = key[..., :D]).  Returns (attention_out, softmax_max,
+    softmax_sum); the stats are (B,1,S1,N1) for BSND queries or (1,T1,N1) for
+    TND queries, fp32, zeros unless return_softmax_lse.
+    """
+    if attention_mode != 2:
+        raise ValueError("Only attention_mode=2 (MLA-absorb) is supported")
+    if pre_tokens != INT64_MAX or next_tokens != INT64_MAX:
+        raise ValueError("pre_tokens/next_tokens only support default INT64_MAX")
+    if sparse_mode not in (0, 3):
+        raise ValueError("Only sparse_mode 0 (full) / 3 (rightDownCausal) supported")
+    if query_rope is None or key_rope is None:
+        raise ValueError("query_rope and key_rope are required (no empty rope)")
+    if sparse_block_size < 1 or (sparse_block_size & (sparse_block_size - 1)) != 0 \
+            or sparse_block_size > 128:
+        raise ValueError("sparse_block_size must be a power of 2 in [1,128]")
+    if layout_query not in ("BSND", "TND"):
+        raise ValueError(f"layout_query must be BSND or TND, got {layout_query}")
+    if layout_kv not in ("BSND", "TND", "PA_BSND"):
+        raise ValueError(f"layout_kv must be BSND, TND or PA_BSND, got {layout_kv}")
+
+    is_tnd_q = layout_query == "TND"
+    is_tnd_kv = layout_kv == "TND"
+    is_pa = layout_kv == "PA_BSND"
+    device = _check_device(query, key, query_rope, key_rope, sparse_indices, block_table)
+
+    # ---- shapes (reference 577-586) ----
+    if is_tnd_q:
+        if actual_seq_lengths_query is None:
+            raise ValueError("TND layout requires actual_seq_lengths_query (cumulative)")
+        T1, N1, D = query.shape
+        act_q = _seq_tensor(actual_seq_lengths_query, device)
+        B = act_q.numel()
+        S1 = 0
+        q_rows = T1
+    else:
+        B, S1, N1, D = query.shape
+        act_q = _seq_tensor(actual_seq_lengths_query, device)
+        q_rows = B * S1
+    D_ROPE = query_rope.shape[-1]
+    if is_pa:
+        if block_table is None:
+            raise ValueError("PA_BSND requires block_table")
+        if actual_seq_lengths_kv is None:
+            raise TypeError("PA_BSND requires actual_seq_lengths_kv")
+        nblk, page, n2 = key.shape[0], key.shape[1], key.shape[2]
+        if block_size and block_size != page:
+            raise ValueError(f"block_size ({block_size}) must equal key.shape[1] ({page})")
+        max_blocks = block_table.shape[1]
+        S2 = max_blocks * page
+        kv_rows = nblk * page
+        act_k = _seq_tensor(actual_seq_lengths_kv, device)
+        bt = block_table.to(dtype=torch.int32).contiguous()
+    elif is_tnd_kv:
+        if actual_seq_lengths_kv is None:
+            raise ValueError("TND layout requires actual_seq_lengths_kv (cumulative)")
+        kv_rows, n2 = key.shape[0], key.shape[1]
+        act_k = _seq_tensor(actual_seq_lengths_kv, device)
+        S2, max_blocks, page, bt = 0, 0, 0, None
+    else:
+        Bk, S2, n2 = key.shape[0], key.shape[1], key.shape[2]
+        kv_rows = Bk * S2
+        act_k = _seq_tensor(actual_seq_lengths_kv, device)
+        max_blocks, page, bt = 0, 0, None
+        if Bk != B:
+            raise ValueError(f"key batch {Bk} != query batch {B}")
+
+    if D not in _VALID_D:
+        raise ValueError(f"D must be one of {_VALID_D}, got {D}")
+    if D_ROPE != _D_ROPE:
+        raise ValueError(f"rope dim must be {_D_ROPE}, got {D_ROPE}")
+    if n2 != 1:
+        raise ValueError("Only N2=1 (MQA) is supported")
+    if N1 not in _VALID_N1:
+        raise ValueError(f"N1 must be one of {_VALID_N1}, got {N1}")
+    if query.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"query dtype must be bfloat16 or float16, got {query.dtype}")
+    for name, t in (("key", key), ("query_rope", query_rope), ("key_rope", key_rope)):
+        if t.dtype != query.dtype:
+            raise ValueError(f"{name} dtype {t.dtype} differs from query dtype {query.dtype}")
+    if (act_k is not None and act_k.numel() != B) or (act_q is not None and act_q.numel() != B):
+        raise ValueError("actual sequence length arrays must have one entry per batch")
+
+    K = sparse_indices.shape[-1]
+    if sparse_indices.numel() != q_rows * K:
+        raise ValueError(f"sparse_indices shape {tuple(sparse_indices.shape)} does not match "
+                         f"{q_rows} query rows")
+
+    q = query.contiguous()
+    qr = query_rope.contiguous()
+    k = key.contiguous()
+    kr = key_rope.contiguous()
+    si = sparse_indices.to(dtype=torch.int32).contiguous()
+
+    out_shape = (q_rows, N1, D) if is_tnd_q else (B, S1, N1, D)
+    lse_shape = (1, q_rows, N1) if is_tnd_q else (B, 1, S1, N1)
+    out = torch.empty(out_shape, dtype=query.dtype, device=device)
+    if return_softmax_lse:
+        smax = torch.empty(lse_shape, dtype=torch.float32, device=device)
+        ssum = torch.empty(lse_shape, dtype=torch.float32, device=device)
+    else:
+        smax = torch.zeros(lse_shape, dtype=torch.float32, device=device)
+        ssum = torch.zeros(lse_shape, dtype=torch.float32, device=device)
+    if q_rows == 0:
+        return out, smax, ssum
+
+    lib = _lib.load()
+    ws_bytes = lib.dsa_sfa_fwd_workspace_size(q_rows, N1, D, K, sparse_block_size)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device) if ws_bytes else None
+    status = lib.dsa_sfa_fwd(
+        _lib.ptr(q), _lib.ptr(qr), _lib.ptr(k), _lib.ptr(kr), _lib.ptr(si),
+        _lib.ptr(out), _lib.ptr(smax) if return_softmax_lse else None,
+        _lib.ptr(ssum) if return_softmax_lse else None,
+        _lib.ptr(act_q), _lib.ptr(act_k), _lib.ptr(bt),
+        B, S1, S2, N1, D, D_ROPE, K, q_rows, kv_rows, max_blocks, page,
+        sparse_block_size, sparse_mode, _lib.LAYOUT[layout_query], _lib.LAYOUT[layout_kv],
+        _lib.dtype_code(query.dtype), float(scale_value), 1 if return_softmax_lse else 0,
+        _lib.ptr(ws), ws_bytes, _lib.stream_handle(device))
+    _lib.check(status, "dsa_sfa_fwd")
+    return out, smax, ssum
+
+
+class SparseFlashAttentionTriton(torch.nn.Module):
+    """Module wrapper of sparse_flash_attention_triton (reference Cell at
+    sparse_flash_attention_triton.py:644-695); ``forward`` takes the Cell's
+    ``construct`` arguments in the same order."""
+
+    def __init__(self, scale_value=1.0, sparse_block_size=1, layout_query="BSND",
+                 layout_kv="BSND", sparse_mode=0, attention_mode=2, return_softmax_lse=False,
+                 pre_tokens=INT64_MAX, next_tokens=INT64_MAX, block_size=0):
+        super().__init__()
+        self.scale_value = scale_value
+        self.sparse_block_size = sparse_block_size
+        self.layout_query = layout_query
+        self.layout_kv = layout_kv
+        self.sparse_mode = sparse_mode
+        self.attention_mode = attention_mode
+        self.return_softmax_lse = return_softmax_lse
+        self.pre_tokens = pre_tokens
+        self.next_tokens = next_tokens
+        self.block_size = block_size
+
+    def forward(self, query, key, value, sparse_indices, query_rope=None, key_rope=None,
+                actual_seq_lengths_query=None, actual_seq_lengths_kv=None, block_table=None):
+        return sparse_flash_attention_triton(
+            query, key, value, sparse_indices,
+            scale_value=self.scale_value, block_table=block_table,
+            actual_seq_lengths_query=actual_seq_lengths_query,
+            actual_seq_lengths_kv=actual_seq_lengths_kv,
+            query_rope=query_rope, key_rope=key_rope,
+            sparse_block_size=self.sparse_block_size, layout_query=self.layout_query,
+            layout_kv=self.layout_kv, sparse_mode=self.sparse_mode,
+            pre_tokens=self.pre_tokens, next_tokens=self.next_tokens,
+            attention_mode=self.attention_mode, return_softmax_lse=self.return_softmax_lse,
+            block_size=self.block_size)
+
+    construct = forward

@@ -1,0 +1,90 @@
+/*
+ * dsa_capi.h -- C ABI of the MI355X (gfx950) DSA operator library, libdsa_hip.so.
+ *
+ * Every entry point takes plain device pointers, 64-bit sizes and a HIP
+ * stream (passed as void*), launches only on that stream, never
+ * synchronises, and returns a status code.  Arguments are validated by
+ * HIP-free host code before any launch, so every error path can be exercised
+ * without a GPU.  The caller owns all memory: outputs and the workspace are
+ * allocated by the caller; `*_workspace_size` reports how many workspace
+ * bytes a call needs (a two-phase pattern like the aclnn
+ * GetWorkspaceSize/execute pair used by the reference's CANN baselines,
+ * sfa_grad_cann.py:40-55).
+ *
+ * Tensor conventions (row-major, contiguous):
+ *   rows  R  = B*S1 (query layout BSND) or T1 (query layout TND)
+ *   query [R, N1, D], query_rope [R, N1, Dr], sparse_indices [R, K] int32
+ *   key / key_rope  [KV, D] / [KV, Dr] with KV = B*S2 (BSND), T2 (TND) or
+ *                   blocks*page_size (PA_BSND, with block_table [B, max_blocks])
+ *   softmax_max / softmax_sum [R, N1] fp32 (the reference's [B,1,S1,N1] or
+ *                   [1,T1,N1] tensors, which have the same memory order).
+ * actual_seq_q / actual_seq_kv are int32 device arrays of B entries: per-batch
+ * lengths for BSND and PA_BSND (NULL = full length), cumulative lengths for
+ * TND (required), exactly as the reference's Python API receives them.
+ */
+#ifndef DSA_CAPI_H
+#define DSA_CAPI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define DSA_OK 0
+#define DSA_ERR_INVALID 1     /* bad argument: the reference raises ValueError */
+#define DSA_ERR_UNSUPPORTED 2 /* configuration outside the supported set (ValueError) */
+#define DSA_ERR_HIP 3         /* HIP runtime error (RuntimeError) */
+#define DSA_ERR_WORKSPACE 4   /* workspace missing or smaller than *_workspace_size */
+
+/* element types */
+#define DSA_DTYPE_BF16 0
+#define DSA_DTYPE_FP16 1
+#define DSA_DTYPE_FP32 2
+
+/* layouts */
+#define DSA_LAYOUT_BSND 0
+#define DSA_LAYOUT_TND 1
+#define DSA_LAYOUT_PA_BSND 2
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* dsa_last_error(void);
+
+/* Library ABI version (bumped on any signature change). */
+int dsa_abi_version(void);
+
+/*
+ * Sparse flash attention forward, MLA-absorb (value = key[..., :D]), MQA (N2 = 1).
+ * Replaces the reference core `_sfa_core` (sparse_flash_attention_triton.py:445-477)
+ * and the host-side layout normalisation around it (551-611): TND rows,
+ * PA_BSND block_table paging and block-wise indices (sparse_block_size > 1)
+ * are handled inside the kernel.
+ *   D in {128, 256, 512}, d_rope = 64, 1 <= N1 <= 128, dtype BF16 or FP16,
+ *   sparse_mode 0 (full) or 3 (rightDownCausal).
+ * Writes attention_out [R, N1, D]; when return_lse != 0 also softmax_max /
+ * softmax_sum [R, N1] (entries of rows without a visible token are 0; the
+ * caller pre-zeroes them when return_lse == 0).
+ */
+int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key,
+                const void* key_rope, const int32_t* sparse_indices,
+                void* attention_out, float* softmax_max, float* softmax_sum,
+                const int32_t* actual_seq_q, const int32_t* actual_seq_kv,
+                const int32_t* block_table, int64_t batch, int64_t s1, int64_t s2,
+                int64_t n1, int64_t d, int64_t d_rope, int64_t sparse_count,
+                int64_t q_rows, int64_t kv_rows, int64_t max_blocks,
+                int64_t page_size, int32_t sparse_block_size, int32_t sparse_mode,
+                int32_t layout_query, int32_t layout_kv, int32_t dtype,
+                float scale_value, int32_t return_lse, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/* Workspace bytes dsa_sfa_fwd needs for these sizes on the current device. */
+size_t dsa_sfa_fwd_workspace_size(int64_t q_rows, int64_t n1, int64_t d,
+                                  int64_t sparse_count, int32_t sparse_block_size);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSA_CAPI_H */
