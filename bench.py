@@ -1,0 +1,221 @@
+"""Benchmark of the DSA operator set on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Headline (BASELINE.json metric): sparse flash attention forward at the
+DeepSeek-V3.2 decode shape (PA_BSND, block 64, B=32, S1=1, ctx 32768,
+N1=128, D=512+64, topK=2048, bf16, sparse_mode 0, scale 1/sqrt(576)), in
+TFLOP/s of algorithmic work and % of the bf16 dense MFMA peak.  A "step" is
+one forward over the whole batch.  Inputs are resident in HBM before timing;
+six independent input sets (KV cache, block table, indices, queries) are
+rotated so the 256 MiB Infinity Cache cannot serve the ~75 MB each step
+reads.  Timing: HIP events on the launch stream around exactly K steps,
+with device synchronisation on both sides.  The roofline object is for the
+dominant kernel (sfa_fwd_kernel).  The CPU baseline is the numpy oracle
+(tests-only port of the reference golden) on the host.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--sets", type=int, default=6)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a plain copy kernel of known size (for PMC calibration)")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# SFA decode workload
+# ---------------------------------------------------------------------------
+B, N1, D, DR, K, CTX, PAGE = 32, 128, 512, 64, 2048, 32768, 64
+
+
+def make_decode_sets(nsets, device):
+    import torch
+    sets = []
+    g = torch.Generator(device=device).manual_seed(1234)
+    nblk = B * CTX // PAGE
+    for _ in range(nsets):
+        s = {}
+        s["cache"] = torch.randn(nblk, PAGE, 1, D, generator=g, device=device).to(torch.bfloat16)
+        s["cache_r"] = torch.randn(nblk, PAGE, 1, DR, generator=g, device=device).to(torch.bfloat16)
+        s["q"] = torch.randn(B, 1, N1, D, generator=g, device=device).to(torch.bfloat16)
+        s["qr"] = torch.randn(B, 1, N1, DR, generator=g, device=device).to(torch.bfloat16)
+        s["bt"] = torch.randperm(nblk, generator=g, device=device).to(torch.int32).reshape(B, CTX // PAGE)
+        idx = torch.argsort(torch.rand(B, CTX, generator=g, device=device), dim=1)[:, :K]
+        s["si"] = idx.to(torch.int32).reshape(B, 1, 1, K).contiguous()
+        sets.append(s)
+    return sets
+
+
+def decode_algorithmic(n_valid):
+    """Flops and HBM bytes of one decode step (per-unit figures x units)."""
+    flops = 2.0 * N1 * (2 * D + DR) * n_valid
+    kv_bytes = n_valid * (D + DR) * 2
+    q_bytes = B * N1 * (D + DR) * 2
+    o_bytes = B * N1 * D * 2
+    idx_bytes = B * K * 4 + B * (CTX // PAGE) * 4
+    return flops, kv_bytes + q_bytes + o_bytes + idx_bytes
+
+
+def time_decode(sets, steps, warmup):
+    import torch
+    from dsa_triton_ascend_amd import _lib
+    lib = _lib.load()
+    dev = sets[0]["q"].device
+    out = torch.empty(B, 1, N1, D, dtype=torch.bfloat16, device=dev)
+    ws_bytes = lib.dsa_sfa_fwd_workspace_size(B, N1, D, K, 1)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    act_k = torch.full((B,), CTX, dtype=torch.int32, device=dev)
+    stream = _lib.stream_handle(dev)
+    scale = 1.0 / math.sqrt(D + DR)
+    nblk = B * CTX // PAGE
+
+    def step(s):
+        st = lib.dsa_sfa_fwd(
+            s["q"].data_ptr(), s["qr"].data_ptr(), s["cache"].data_ptr(), s["cache_r"].data_ptr(),
+            s["si"].data_ptr(), out.data_ptr(), None, None, None, act_k.data_ptr(), s["bt"].data_ptr(),
+            B, 1, CTX, N1, D, DR, K, B, nblk * PAGE, CTX // PAGE, PAGE, 1, 0,
+            _lib.LAYOUT["BSND"], _lib.LAYOUT["PA_BSND"], _lib.DTYPE_BF16, scale, 0,
+            ws.data_ptr(), ws_bytes, stream)
+        if st != 0:
+            _lib.check(st, "dsa_sfa_fwd")
+
+    for i in range(warmup):
+        step(sets[i % len(sets)])
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        step(sets[i % len(sets)])
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    # per-step distribution (median / p20 / p80 like the reference harness)
+    per = []
+    for i in range(min(steps, 50)):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        step(sets[i % len(sets)])
+        e1.record()
+        e1.synchronize()
+        per.append(e0.elapsed_time(e1))
+    per.sort()
+    return total_ms / steps, per
+
+
+def cpu_baseline_decode(sets):
+    """numpy oracle over the full decode batch of one input set (host cores)."""
+    import numpy as np
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max(int(i.get("num_threads", 1)) for i in threadpool_info()) if threadpool_info() else 1
+    except Exception:
+        cores = len(os.sched_getaffinity(0))
+    from oracle.sfa import sfa_fwd_bsnd
+    s = sets[0]
+    si = s["si"].cpu().numpy()
+    bt = s["bt"].cpu().numpy()
+    cache = s["cache"].reshape(-1, D)
+    cache_r = s["cache_r"].reshape(-1, DR)
+    q = s["q"].float().cpu().numpy()
+    qr = s["qr"].float().cpu().numpy()
+    rows = list(range(B))
+    # gather each row's selected KV (the reference de-pages on the host too)
+    ks, krs = [], []
+    for b in rows:
+        toks = si[b, 0, 0]
+        phys = bt[b, toks // PAGE].astype(np.int64) * PAGE + toks % PAGE
+        import torch
+        pt = torch.from_numpy(phys).to(cache.device)
+        ks.append(cache[pt].float().cpu().numpy())
+        krs.append(cache_r[pt].float().cpu().numpy())
+    idx = np.arange(K, dtype=np.int32).reshape(1, 1, 1, K)
+    scale = 1.0 / math.sqrt(D + DR)
+    t0 = time.perf_counter()
+    for b in rows:
+        sfa_fwd_bsnd(q[b:b + 1], ks[b][None, :, None, :], idx, qr[b:b + 1],
+                     krs[b][None, :, None, :], scale, [1], [K], 1, 0, True, "bfloat16",
+                     positions="kernel")
+    dt = time.perf_counter() - t0
+    flops, _ = decode_algorithmic(B * K)
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"numpy oracle (port of sparse_flash_attention_numpy.py) over the full "
+                      f"decode batch of one input set ({B} rows x {K} tokens x {N1} heads), "
+                      f"{dt:.2f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    sets = make_decode_sets(args.sets, dev)
+    torch.cuda.synchronize()
+    ms, per = time_decode(sets, args.steps, args.warmup)
+    n_valid = B * K
+    flops, nbytes = decode_algorithmic(n_valid)
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    attainable = min(PEAK_BF16_TFLOPS, flops / nbytes * PEAK_HBM_GBS / 1e3)
+    result = {
+        "metric": "SFA fwd TFLOP/s (decode, DeepSeek-V3.2 shape)",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded torch.randn, 6 rotating input sets)",
+        "config": {"workload": "sfa_fwd decode: PA_BSND block 64, B=32, S1=1, ctx 32768, "
+                               "N1=128, D=512+64, topK=2048, sparse_mode 0",
+                   "input_sets": args.sets},
+        "pct_of_bf16_peak": round(100.0 * tflops / PEAK_BF16_TFLOPS, 3),
+        "pct_of_attainable_roofline": round(100.0 * tflops / attainable, 2),
+        "per_step_ms": {"median": round(per[len(per) // 2], 5), "p20": round(per[len(per) // 5], 5),
+                        "p80": round(per[4 * len(per) // 5], 5)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "sfa_fwd_kernel + sfa_combine_kernel",
+                     "algorithmic_bytes_per_launch": int(nbytes),
+                     "algorithmic_flops_per_launch": int(flops)},
+    }
+    if args.calib_copy:
+        src = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline_decode(sets)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

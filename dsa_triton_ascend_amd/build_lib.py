@@ -42,6 +42,10 @@ def common_flags():
         "-Wno-unused-function", "-Wno-unused-variable",
         # packed fp32 VALU forms are kept out of the generated code
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA accumulators in VGPRs: with AGPR-form accumulators the
+        # register allocator keeps loop-carried accumulators in VGPRs anyway
+        # and copies them across on every iteration
+        "-mllvm", "-amdgpu-mfma-vgpr-form=true",
         "-I", os.path.join(ROOT, "include"),
     ]
 

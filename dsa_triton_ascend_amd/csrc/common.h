@@ -72,13 +72,27 @@ __device__ __forceinline__ float xgroup_sum(float v) {
   return v;
 }
 
-// LDS chunk swizzle for 16-byte chunks of token rows: the low three bits of
-// the chunk index are XORed with a per-token permutation so that (a) eight
-// consecutive tokens reading the same chunk hit eight distinct 16-byte bank
-// groups, and (b) the four rows read together by one 16-lane group of a
-// transposed 8-byte load land in disjoint bank groups.
-__device__ __forceinline__ int chunk_swz(int tok) { return ((tok & 3) << 1) | ((tok >> 2) & 1); }
-__device__ __forceinline__ int swz_chunk(int chunk, int tok) { return chunk ^ chunk_swz(tok); }
+// Workgroup barrier that orders LDS only.  __syncthreads() also fences
+// global memory, which makes the compiler drain every outstanding global
+// load (s_waitcnt vmcnt(0)) before the barrier and kills load/compute
+// overlap; tiles staged through registers stay in flight across this one.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// LDS swizzles for token rows stored as 16-byte chunks.  LDS is modelled as
+// 64 banks x 4 bytes (a 256-byte window per cycle).
+//  * nope rows (D*2 bytes, >= 16 chunks): chunk c of token t is stored at
+//    chunk c ^ nope_swz(t) (low four bits only).  Sixteen consecutive tokens
+//    reading one chunk (GEMM1 A fragments, 16 lanes x 16 bytes) hit sixteen
+//    distinct 16-byte bank groups, and the 8 rows x 2 chunks read by 32 lanes
+//    of a transposed 8-byte load (rows 8h..8h+7) cover all 64 banks.
+//  * rope rows (128 bytes = 8 chunks): chunk c of token t at c ^ rope_swz(t);
+//    token parity selects the 128-byte half of the window.
+__device__ __forceinline__ int nope_swz(int tok) { return ((tok & 7) << 1) | ((tok >> 3) & 1); }
+__device__ __forceinline__ int rope_swz(int tok) { return (tok >> 1) & 7; }
 
 }  // namespace dsa
 

@@ -57,10 +57,14 @@ struct SfaFwdParams {
   int32_t return_lse;
 };
 
+#ifndef DSA_SCHED_GROUPS
+#define DSA_SCHED_GROUPS 1
+#endif
+
 constexpr int kSfaTile = 32;
 constexpr int kSfaMaxList = 4096;
 constexpr int kSfaThreads = 256;
-constexpr float kRescaleLog2 = 8.f;
+constexpr float kRefSlack = 64.f;  // log2 units
 
 struct RowInfo {
   int b, s1, act_q, act_k, threshold;
@@ -124,10 +128,14 @@ __device__ __forceinline__ bool sfa_resolve(const SfaFwdParams& p, const RowInfo
 }
 
 // HT = head tiles (of 16 heads) per wave; a workgroup covers 4*HT*16 heads.
-template <int D, typename T, int HT>
+// BUF: gather through buffer loads with 32-bit offsets (key tensors under
+// 2 GiB); the hardware range check returns zeros for padding slots and -1
+// pages, so no selects are needed.  Otherwise 64-bit global loads.
+template <int D, typename T, int HT, bool BUF>
 __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   using E = Elem<T>;
   using V8 = typename E::v8;
+  constexpr bool kSplitP = sizeof(T) == 2 && __is_same(T, bf16);
   constexpr int DR = 64;
   constexpr int KS = (D + DR) / 32;  // GEMM1 k-steps
   constexpr int KSN = D / 32;        // of which from the nope part
@@ -141,7 +149,7 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
   static_assert(TILE * NOPE_CH % kSfaThreads == 0, "tile split");
 
   __shared__ __attribute__((aligned(16))) unsigned char smem[2 * BUF_BYTES];
-  __shared__ int s_list[kSfaMaxList];
+  __shared__ int s_list[kSfaMaxList + kSfaTile];
   __shared__ int s_wcnt[4];
 
   const int tid = threadIdx.x;
@@ -176,7 +184,7 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
     if (ri.active && pos < p1) valid = sfa_resolve(p, ri, idx_row, pos, &phys);
     unsigned long long m = __ballot(valid);
     if (lane == 0) s_wcnt[wave] = __popcll(m);
-    __syncthreads();
+    lds_barrier();
     int off = n_valid;
     int tot = 0;
 #pragma unroll
@@ -187,8 +195,12 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
     }
     if (valid) s_list[off + __popcll(m & ((1ull << lane) - 1ull))] = phys;
     n_valid += tot;
-    __syncthreads();
+    lds_barrier();
   }
+
+  // pad the list to a whole tile with -1 so tile loads index it unconditionally
+  if (tid < TILE) s_list[n_valid + tid] = -1;
+  lds_barrier();
 
   const int head0 = hg * HEADS_PER_WG + wave * HT * 16;
   const bool wave_active = head0 < p.n1;
@@ -211,184 +223,260 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
   }
 
   f32x4 acc_o[NDT][HT];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int ht = 0; ht < HT; ++ht) acc_o[dt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
   float m_ref[HT], m_true[HT], l_run[HT];
+  // m_ref: reference max (log2 units) that P and O are taken relative to.
+  // It is fixed by the first tile with a visible token and never raised
+  // inside the tile loop (raising it would rescale O, which the register
+  // allocator can only do by cycling the accumulator through VGPRs every
+  // tile).  P = 2^(s - m_ref) may therefore exceed 1; up to 2^kRefSlack is
+  // exact in fp32/bf16.  A head whose max exceeds m_ref + kRefSlack sets
+  // `overflow`, and the row is recomputed once with m_ref = exact max.
+  // m_true tracks the exact max for the returned statistics.
 #pragma unroll
   for (int ht = 0; ht < HT; ++ht) {
-    m_ref[ht] = -INFINITY;   // reference max of P and O (log2 units)
-    m_true[ht] = -INFINITY;  // exact running max (log2 units)
-    l_run[ht] = 0.f;         // lane-partial sum of exp2(s - m_ref)
+    m_ref[ht] = -INFINITY;
+    m_true[ht] = -INFINITY;
+    l_run[ht] = 0.f;  // lane-partial sum of 2^(s - m_ref)
   }
+  bool overflow = false;
 
   const int n_tiles = (n_valid + TILE - 1) / TILE;
 
   // ---- tile loader: global -> registers, registers -> swizzled LDS ----
+  // Slots past n_valid and attended tokens of -1 pages read as zero rows.
+  // The loads of tile t+1 stay in flight while tile t is computed.
   u32x4 stage[NLOAD];
+  unsigned stage_ok = 0;
+  __amdgpu_buffer_rsrc_t rsrc_k, rsrc_r;
+  if constexpr (BUF) {
+    rsrc_k = __builtin_amdgcn_make_buffer_rsrc((void*)p.k, (short)0, (int)(p.kv_rows * D * 2), 0x00020000);
+    rsrc_r = __builtin_amdgcn_make_buffer_rsrc((void*)p.kr, (short)0, (int)(p.kv_rows * DR * 2), 0x00020000);
+  }
   auto load_tile = [&](int t) {
+    stage_ok = 0;
 #pragma unroll
     for (int it = 0; it < NLOAD; ++it) {
       const int c = it * kSfaThreads + tid;
       int tk, cc;
       if (it < NLOAD_NOPE) { tk = c / NOPE_CH; cc = c % NOPE_CH; }
       else { const int c2 = c - TILE * NOPE_CH; tk = c2 >> 3; cc = c2 & 7; }
-      const int slot = t * TILE + tk;
-      const int phys = slot < n_valid ? s_list[slot] : -1;
-      const int64_t ps = phys >= 0 ? phys : 0;  // row 0 is a safe address
-      u32x4 v;
-      if (it < NLOAD_NOPE) v = *(const u32x4*)((const T*)p.k + ps * D + cc * 8);
-      else v = *(const u32x4*)((const T*)p.kr + ps * DR + cc * 8);
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      stage[it] = phys >= 0 ? v : z;
+      const int phys = s_list[t * TILE + tk];  // -1 past n_valid
+      if constexpr (BUF) {
+        const unsigned row_bytes = it < NLOAD_NOPE ? D * 2 : DR * 2;
+        const unsigned off = phys >= 0 ? (unsigned)phys * row_bytes + cc * 16 : 0x80000000u;
+        stage[it] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(it < NLOAD_NOPE ? rsrc_k : rsrc_r, (int)off, 0, 0));
+      } else {
+        const int64_t ps = phys >= 0 ? phys : 0;  // row 0 is a safe address
+        if (it < NLOAD_NOPE) stage[it] = *(const u32x4*)((const T*)p.k + ps * D + cc * 8);
+        else stage[it] = *(const u32x4*)((const T*)p.kr + ps * DR + cc * 8);
+        stage_ok |= (phys >= 0 ? 1u : 0u) << it;
+      }
     }
   };
   auto store_tile = [&](int buf) {
     unsigned char* base = smem + buf * BUF_BYTES;
+    const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int it = 0; it < NLOAD; ++it) {
       const int c = it * kSfaThreads + tid;
+      u32x4 v = stage[it];
+      if constexpr (!BUF) v = ((stage_ok >> it) & 1u) ? v : z;
       if (it < NLOAD_NOPE) {
         const int tk = c / NOPE_CH, cc = c % NOPE_CH;
-        *(u32x4*)(base + tk * (D * 2) + swz_chunk(cc, tk) * 16) = stage[it];
+        *(u32x4*)(base + tk * (D * 2) + (cc ^ nope_swz(tk)) * 16) = v;
       } else {
         const int c2 = c - TILE * NOPE_CH;
         const int tk = c2 >> 3, cc = c2 & 7;
-        *(u32x4*)(base + NOPE_BYTES + tk * (DR * 2) + swz_chunk(cc, tk) * 16) = stage[it];
+        *(u32x4*)(base + NOPE_BYTES + tk * (DR * 2) + (cc ^ rope_swz(tk)) * 16) = v;
       }
     }
   };
 
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
+  // ---- per-lane LDS byte offsets; every read below is offset + immediate ----
+  // GEMM1 A fragment: token tk = tt*16 + li, chunk ks*4 + lg.  The swizzle
+  // XORs the low four chunk bits, so ks mod 4 selects one of four bases and
+  // the rest is a multiple of 256 bytes; rope chunks (ks-KSN)*4 + lg < 8.
+  int g1[2][4], g1r[2][2];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int tk = tt * 16 + li;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) g1[tt][m] = tk * (D * 2) + (((4 * m + lg) ^ nope_swz(tk)) * 16);
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+      g1r[tt][m] = NOPE_BYTES + tk * (DR * 2) + (((4 * m + lg) ^ rope_swz(tk)) * 16);
   }
+  // GEMM2 transposed reads: row r1 = 4*lg + li/4 (and r1 + 16, same swizzle),
+  // chunk dt*2 + (li&3)/2, 8-byte half (li&1): dt mod 8 selects the base.
+  int g2[8];
+  {
+    const int r1 = lg * 4 + (li >> 2);
+    const int b = (li & 3) >> 1;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) g2[m] = r1 * (D * 2) + ((((2 * m) | b) ^ nope_swz(r1)) * 16) + (li & 1) * 8;
+  }
+  constexpr int NS1 = KS * 2;  // GEMM1 steps (k-step x token tile)
+  constexpr int PF1 = 4;       // GEMM1 fragments in flight
+  constexpr int PF2 = 4;       // GEMM2 fragments in flight
 
-  if (!wave_active) {
-    // waves without heads (N1 < 128) only help with the gather
-    for (int t = 0; t < n_tiles; ++t) {
-      if (t + 1 < n_tiles) load_tile(t + 1);
-      __syncthreads();
-      if (t + 1 < n_tiles) store_tile((t & 1) ^ 1);
+  auto run_tiles = [&]() {
+    if (n_tiles > 0) {
+      load_tile(0);
+      store_tile(0);
     }
-    return;
-  }
+    // tile loop unrolled by two: the LDS buffer of each copy is a constant
+    for (int t0 = 0; t0 < n_tiles; t0 += 2)
+#pragma unroll
+    for (int buf = 0; buf < 2; ++buf) {
+      const int t = t0 + buf;
+      if (t >= n_tiles) break;
+      if (t + 1 < n_tiles) load_tile(t + 1);
+      lds_barrier();
+      {
+        const unsigned char* base = smem + buf * BUF_BYTES;
+        auto a1 = [&](int st) -> u32x4 {
+          const int ks = st >> 1, tt = st & 1;
+          if (ks < KSN) return *(const u32x4*)(base + g1[tt][ks & 3] + (ks >> 2) * 256);
+          return *(const u32x4*)(base + g1r[tt][ks - KSN]);
+        };
+        auto a2 = [&](int dt) -> V8 {
+          const unsigned char* p1 = base + g2[dt & 7] + (dt >> 3) * 256;
+          const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1);
+          const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p1 + 16 * D * 2));
+          const i16x4 w1 = __builtin_bit_cast(i16x4, v1);
+          const i16x4 w2 = __builtin_bit_cast(i16x4, v2);
+          const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
+          return __builtin_bit_cast(V8, w);
+        };
 
-  for (int t = 0; t < n_tiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < n_tiles) load_tile(t + 1);
-    __syncthreads();
-
-    {
-      const unsigned char* base = smem + buf * BUF_BYTES;
-      // ---- GEMM1: S^T[32 tok x HT*16 heads] ----
-      f32x4 acc_s[2][HT];
+        // ---- GEMM1: S^T[32 tok x HT*16 heads], fragments PF1 steps ahead ----
+        f32x4 acc_s[2][HT];
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
+        for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-        for (int ht = 0; ht < HT; ++ht) acc_s[tt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
+          for (int ht = 0; ht < HT; ++ht) acc_s[tt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        u32x4 fa[PF1];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
+        for (int i = 0; i < PF1; ++i) fa[i] = a1(i);
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const int tk = tt * 16 + li;
-          u32x4 a;
-          if (ks < KSN) {
-            a = *(const u32x4*)(base + tk * (D * 2) + swz_chunk(ks * 4 + lg, tk) * 16);
-          } else {
-            a = *(const u32x4*)(base + NOPE_BYTES + tk * (DR * 2) +
-                                swz_chunk((ks - KSN) * 4 + lg, tk) * 16);
-          }
-          const V8 av = as_v8<V8>(a);
+        for (int st = 0; st < NS1; ++st) {
+          const int ks = st >> 1, tt = st & 1;
+          const V8 av = as_v8<V8>(fa[st % PF1]);
+          if (st + PF1 < NS1) fa[st % PF1] = a1(st + PF1);
 #pragma unroll
           for (int ht = 0; ht < HT; ++ht) acc_s[tt][ht] = E::mfma(av, qf[ht][ks], acc_s[tt][ht]);
         }
-      }
+#if DSA_SCHED_GROUPS
+        __builtin_amdgcn_sched_group_barrier(0x100, PF1, 0);
+#pragma unroll
+        for (int st = 0; st < NS1; ++st) {
+          __builtin_amdgcn_sched_group_barrier(0x008, HT, 0);
+          if (st + PF1 < NS1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+#endif
+        // first V^T fragments go out before the softmax arithmetic
+        V8 fv[PF2];
+#pragma unroll
+        for (int i = 0; i < PF2; ++i) fv[i] = a2(i);
 
-      // ---- online softmax (log2 domain), P^T fragments ----
-      // Lazy rescaling: probabilities are taken relative to a reference max
-      // m_ref that is only raised (and O rescaled) when a head's max grows
-      // by more than 2^kRescaleLog2; m_true tracks the exact max for the
-      // returned statistics.  P values stay <= 2^kRescaleLog2.
-      V8 pf[HT];
-      bool need = false;
-      float m_new_ref[HT];
-#pragma unroll
-      for (int ht = 0; ht < HT; ++ht) {
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int tok = t * TILE + tt * 16 + lg * 4 + r;
-            float v = acc_s[tt][ht][r] * p.scale_log2;
-            v = tok < n_valid ? v : -INFINITY;
-            acc_s[tt][ht][r] = v;
-            tmax = fmaxf(tmax, v);
-          }
-        }
-        tmax = xgroup_max(tmax);
-        m_true[ht] = fmaxf(m_true[ht], tmax);
-        float mr = m_ref[ht];
-        if (mr == -INFINITY) {
-          mr = tmax;  // nothing accumulated yet for this head
-        } else if (tmax > mr + kRescaleLog2) {
-          mr = tmax;
-          need = true;
-        }
-        m_new_ref[ht] = mr;
-      }
-      if (__builtin_expect(__any(need), 0)) {
+        // ---- softmax numerators (log2 domain) as P^T fragments ----
+        // P^T is split into bf16 hi + lo parts for bf16 I/O (fp16 keeps 11
+        // bits in one part): the P.V product then carries ~16 bits of P, so
+        // its error is that of the final output rounding.
+        V8 pf[HT], pf_lo[HT];
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht) {
-          const float alpha = m_ref[ht] == -INFINITY ? 1.f : fast_exp2(m_ref[ht] - m_new_ref[ht]);
-          l_run[ht] *= alpha;
+          float tmax = -INFINITY;
 #pragma unroll
-          for (int dt = 0; dt < NDT; ++dt) acc_o[dt][ht] *= alpha;
-        }
-      }
+          for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
-      for (int ht = 0; ht < HT; ++ht) {
-        m_ref[ht] = m_new_ref[ht];
-        V8 pvv;
-        float lsum = 0.f;
-        if (m_ref[ht] == -INFINITY) {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) pvv[j] = E::from_f32(0.f);
-        } else {
+            for (int r = 0; r < 4; ++r) {
+              const int tok = t * TILE + tt * 16 + lg * 4 + r;
+              float v = acc_s[tt][ht][r] * p.scale_log2;
+              v = tok < n_valid ? v : -INFINITY;
+              acc_s[tt][ht][r] = v;
+              tmax = fmaxf(tmax, v);
+            }
+          }
+          tmax = xgroup_max(tmax);
+          m_true[ht] = fmaxf(m_true[ht], tmax);
+          if (m_ref[ht] == -INFINITY) m_ref[ht] = tmax;
+          overflow |= tmax > m_ref[ht] + kRefSlack;
+          V8 hi, lo;
+          float lsum = 0.f;
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            const float e = fast_exp2(acc_s[j >> 2][ht][j & 3] - m_ref[ht]);
+            // m_ref == -inf only while no token is visible: all s are -inf too
+            const float e = m_ref[ht] == -INFINITY ? 0.f : fast_exp2(acc_s[j >> 2][ht][j & 3] - m_ref[ht]);
             lsum += e;
-            pvv[j] = E::from_f32(e);
+            const T h = E::from_f32(e);
+            hi[j] = h;
+            lo[j] = E::from_f32(e - E::to_f32(h));
+          }
+          l_run[ht] += lsum;
+          pf[ht] = hi;
+          pf_lo[ht] = lo;
+        }
+
+        // ---- GEMM2: O^T[D x HT*16 heads] += V^T . P^T, fragments PF2 ahead ----
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const V8 av = fv[dt % PF2];
+          if (dt + PF2 < NDT) fv[dt % PF2] = a2(dt + PF2);
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) {
+            acc_o[dt][ht] = E::mfma(av, pf[ht], acc_o[dt][ht]);
+            if (kSplitP) acc_o[dt][ht] = E::mfma(av, pf_lo[ht], acc_o[dt][ht]);
           }
         }
-        l_run[ht] += lsum;
-        pf[ht] = pvv;
-      }
-
-      // ---- GEMM2: O^T[D x HT*16 heads] += V^T . P^T ----
-      const int r1 = lg * 4 + (li >> 2);
-      const int r2 = 16 + r1;
-      const int byte_in = ((li & 3) & 1) * 8;
+#if DSA_SCHED_GROUPS
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const int ch = dt * 2 + ((li & 3) >> 1);
-        const unsigned char* a1 = base + r1 * (D * 2) + swz_chunk(ch, r1) * 16 + byte_in;
-        const unsigned char* a2 = base + r2 * (D * 2) + swz_chunk(ch, r2) * 16 + byte_in;
-        const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)a1);
-        const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)a2);
-        const i16x4 w1 = __builtin_bit_cast(i16x4, v1);
-        const i16x4 w2 = __builtin_bit_cast(i16x4, v2);
-        const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
-        const V8 av = __builtin_bit_cast(V8, w);
-#pragma unroll
-        for (int ht = 0; ht < HT; ++ht) acc_o[dt][ht] = E::mfma(av, pf[ht], acc_o[dt][ht]);
+        for (int dt = 0; dt < NDT; ++dt) {
+          __builtin_amdgcn_sched_group_barrier(0x008, HT * (kSplitP ? 2 : 1), 1);
+          if (dt + PF2 < NDT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+        }
+#endif
       }
+      if (t + 1 < n_tiles) store_tile(buf ^ 1);
     }
+  };
 
-    if (t + 1 < n_tiles) store_tile(buf ^ 1);
+  // Barrier sequence (identical for every wave): pass-0 tiles, one vote
+  // barrier, and only if the vote is set, pass-1 tiles.
+  if (!wave_active) {
+    // waves without heads (N1 < 128) only help with the gather
+    auto gather_only = [&]() {
+      if (n_tiles > 0) { load_tile(0); store_tile(0); }
+      for (int t = 0; t < n_tiles; ++t) {
+        if (t + 1 < n_tiles) load_tile(t + 1);
+        lds_barrier();
+        if (t + 1 < n_tiles) store_tile((t & 1) ^ 1);
+      }
+    };
+    gather_only();
+    if (__syncthreads_or(0)) gather_only();
+    return;
+  }
+
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) acc_o[dt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  run_tiles();
+  if (__syncthreads_or(overflow ? 1 : 0)) {
+    // rare: some head's score exceeded the reference by 2^kRefSlack; redo
+    // the row with the exact maxima found by the first pass
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+      m_ref[ht] = m_true[ht];
+      l_run[ht] = 0.f;
+    }
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) acc_o[dt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    run_tiles();
   }
 
   // ---- epilogue ----
@@ -526,8 +614,13 @@ static hipError_t launch_sfa_fwd(SfaFwdParams& p, hipStream_t stream) {
   const int64_t rows_per_xcd = (p.rows + 7) / 8;
   p.rows_per_xcd = (int)rows_per_xcd;
   const int64_t blocks = 8 * rows_per_xcd * p.splits * sfa_fwd_head_groups(p.n1, D);
-  hipLaunchKernelGGL((sfa_fwd_kernel<D, T, SfaHT<D>::value>), dim3((unsigned)blocks),
-                     dim3(kSfaThreads), 0, stream, p);
+  const bool buf = p.kv_rows * (int64_t)D * 2 < (1ll << 31);
+  if (buf)
+    hipLaunchKernelGGL((sfa_fwd_kernel<D, T, SfaHT<D>::value, true>), dim3((unsigned)blocks),
+                       dim3(kSfaThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((sfa_fwd_kernel<D, T, SfaHT<D>::value, false>), dim3((unsigned)blocks),
+                       dim3(kSfaThreads), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) return e;
   const int64_t cblocks = (p.rows * p.n1 + 3) / 4;

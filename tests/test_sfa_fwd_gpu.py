@@ -1,9 +1,15 @@
 """GPU parity of the HIP sparse flash attention forward against the oracle.
 
-Tolerance (north star): rtol 2e-2 / atol 2e-3 for the bf16/fp16 output
-against the oracle of the fp32 golden (which rounds probabilities and the
-output to the I/O dtype like the reference golden); softmax_max /
-softmax_sum with the same tolerance.
+Tolerances:
+* north star: rtol 2e-2 / atol 2e-3 for the bf16/fp16 output and the fp32
+  softmax_max / softmax_sum against the fp32 golden (the oracle evaluated
+  with dtype="float32": no rounding of probabilities or output);
+* against the reference golden's own dtype-rounded vectors (fixtures written
+  by sparse_flash_attention_numpy.py) the reference's test tolerance,
+  rtol = atol = 4e-2 for bf16 and 2e-2 for fp16 (test_sfa_triton.py:88-95):
+  the golden rounds p/sum to bf16 while the kernels (the reference's Triton
+  kernel and this one) round unnormalised p, so near-zero outputs of a peaked
+  softmax differ by about 2^-9 * |v| between the two.
 """
 import glob
 import os
@@ -14,11 +20,12 @@ import torch
 
 from oracle.sfa import sfa_fwd_bsnd, sparse_flash_attention
 from tests.conftest import GOLDEN_DIR
-from tests.helpers import assert_close, dev, np_dtype_name, sfa_inputs, sparse_indices
+from tests.helpers import assert_close, dev, sfa_inputs, sparse_indices
 
 pytestmark = pytest.mark.gpu
 
 RTOL, ATOL = 2e-2, 2e-3
+REF_TOL = {torch.bfloat16: 4e-2, torch.float16: 2e-2}
 FIXTURES = sorted(glob.glob(os.path.join(GOLDEN_DIR, "sfa_*.npz")))
 
 
@@ -46,18 +53,21 @@ def test_fwd_matches_reference_golden_fixture(path):
     out, smax, ssum = _run(f["q"], f["k"], f["qr"], f["kr"], f["sparse_indices"], dtype,
                            float(f["scale"]), int(f["sparse_mode"]), int(f["sparse_block_size"]),
                            act_q=[int(x) for x in f["act_q"]], act_k=[int(x) for x in f["act_k"]])
+    args = (f["q"], f["k"], f["sparse_indices"], f["qr"], f["kr"], float(f["scale"]),
+            f["act_q"], f["act_k"], int(f["sparse_block_size"]), int(f["sparse_mode"]), True)
     if "mid_minus1" in path:
         # the golden stops scanning a row at the first -1 (CANN gatherKV
         # contract); the device kernels mask per entry -> use the oracle's
         # kernel rule for this one fixture
-        ref = sfa_fwd_bsnd(f["q"], f["k"], f["sparse_indices"], f["qr"], f["kr"], float(f["scale"]),
-                           f["act_q"], f["act_k"], int(f["sparse_block_size"]), int(f["sparse_mode"]),
-                           True, str(f["dtype"]), positions="kernel")
+        ref = sfa_fwd_bsnd(*args, str(f["dtype"]), positions="kernel")
     else:
         ref = (f["out"], f["softmax_max"], f["softmax_sum"])
-    assert_close(out, ref[0], RTOL, ATOL, "attention_out")
-    assert_close(smax, ref[1], RTOL, ATOL, "softmax_max")
-    assert_close(ssum, ref[2], RTOL, ATOL, "softmax_sum")
+    tol = REF_TOL[dtype]
+    assert_close(out, ref[0], tol, tol, "attention_out vs golden")
+    assert_close(smax, ref[1], RTOL, ATOL, "softmax_max vs golden")
+    assert_close(ssum, ref[2], RTOL, ATOL, "softmax_sum vs golden")
+    fp32 = sfa_fwd_bsnd(*args, "float32", positions="kernel")
+    assert_close(out, fp32[0], RTOL, ATOL, "attention_out vs fp32 golden")
 
 
 CASES = [
@@ -85,7 +95,7 @@ def test_fwd_matches_oracle(B, S1, S2, N1, K, bs, mode, D, dtype):
     scale = 1.0 / np.sqrt(D + 64)
     out, smax, ssum = _run(q, k, qr, kr, si, dtype, scale, mode, bs)
     ref = sfa_fwd_bsnd(q, k, si, qr, kr, scale, [S1] * B, [S2] * B, bs, mode, True,
-                       np_dtype_name(dtype), positions="kernel")
+                       "float32", positions="kernel")
     assert_close(out, ref[0], RTOL, ATOL, "attention_out")
     assert_close(smax, ref[1], RTOL, ATOL, "softmax_max")
     assert_close(ssum, ref[2], RTOL, ATOL, "softmax_sum")
@@ -101,7 +111,7 @@ def test_fwd_actual_lengths_and_hidden_rows():
         si = sparse_indices(B, S1, S2, K, 1, mode, act_q, act_k, seed=5)
         si[1, 2, 0, 3] = 63      # beyond act_k of batch 1: masked
         out, smax, ssum = _run(q, k, qr, kr, si, dtype, 0.07, mode, act_q=act_q, act_k=act_k)
-        ref = sfa_fwd_bsnd(q, k, si, qr, kr, 0.07, act_q, act_k, 1, mode, True, "bfloat16",
+        ref = sfa_fwd_bsnd(q, k, si, qr, kr, 0.07, act_q, act_k, 1, mode, True, "float32",
                            positions="kernel")
         assert_close(out, ref[0], RTOL, ATOL, f"out mode{mode}")
         assert_close(smax, ref[1], RTOL, ATOL, f"smax mode{mode}")
@@ -118,7 +128,7 @@ def test_fwd_unsorted_ids_minus1_in_middle_and_duplicates():
     si = rng.randint(-1, S2, size=(B, S1, 1, K)).astype(np.int32)
     si[0, 0, 0, 5] = si[0, 0, 0, 6]
     out, smax, ssum = _run(q, k, qr, kr, si, dtype, 0.1, 0)
-    ref = sfa_fwd_bsnd(q, k, si, qr, kr, 0.1, [S1], [S2], 1, 0, True, "bfloat16", positions="kernel")
+    ref = sfa_fwd_bsnd(q, k, si, qr, kr, 0.1, [S1], [S2], 1, 0, True, "float32", positions="kernel")
     assert_close(out, ref[0], RTOL, ATOL, "out")
     assert_close(ssum, ref[2], RTOL, ATOL, "ssum")
 
@@ -145,7 +155,7 @@ def test_fwd_tnd_layout():
     assert out.shape == (sum(lens), N1, D) and smax.shape == (1, sum(lens), N1)
     ref = sparse_flash_attention(Q, Kt, SI, 0.05, QR, KR, actual_seq_lengths_query=cum,
                                  actual_seq_lengths_kv=cum, layout_query="TND", layout_kv="TND",
-                                 sparse_mode=3, return_softmax_lse=True)
+                                 sparse_mode=3, return_softmax_lse=True, dtype="float32")
     assert_close(out.float().cpu().numpy(), ref[0], RTOL, ATOL, "out")
     assert_close(smax.cpu().numpy(), ref[1], RTOL, ATOL, "smax")
     assert_close(ssum.cpu().numpy(), ref[2], RTOL, ATOL, "ssum")
@@ -188,7 +198,7 @@ def test_fwd_paged_kv(holes):
     ref = sparse_flash_attention(q, dev(cache, dtype).float().cpu().numpy(), si, 0.04, qr,
                                  dev(cache_r, dtype).float().cpu().numpy(), block_table=bt,
                                  actual_seq_lengths_kv=act_k, layout_kv="PA_BSND", sparse_mode=0,
-                                 return_softmax_lse=True)
+                                 return_softmax_lse=True, dtype="float32")
     assert_close(out.float().cpu().numpy(), ref[0], RTOL, ATOL, "out")
     assert_close(smax.cpu().numpy(), ref[1], RTOL, ATOL, "smax")
     assert_close(ssum.cpu().numpy(), ref[2], RTOL, ATOL, "ssum")
@@ -227,7 +237,7 @@ def test_fwd_decode_shape_sampled_rows():
         idx = np.arange(K, dtype=np.int32).reshape(1, 1, 1, K)
         ref = sfa_fwd_bsnd(q[b:b + 1].float().cpu().numpy(), kk[None, :, None, :], idx,
                            qr[b:b + 1].float().cpu().numpy(), kkr[None, :, None, :], scale,
-                           [1], [K], 1, 0, True, "bfloat16", positions="kernel")
+                           [1], [K], 1, 0, True, "float32", positions="kernel")
         assert_close(out[b:b + 1].float().cpu().numpy(), ref[0], RTOL, ATOL, f"out row {b}")
         assert_close(smax[b:b + 1].cpu().numpy(), ref[1], RTOL, ATOL, f"smax row {b}")
         assert_close(ssum[b:b + 1].cpu().numpy(), ref[2], RTOL, ATOL, f"ssum row {b}")
@@ -266,7 +276,7 @@ def test_fwd_prefill_shape_sampled_rows():
         qq = q[s].float().cpu().numpy()[None, None]
         qqr = qr[s].float().cpu().numpy()[None, None]
         ref = sfa_fwd_bsnd(qq, kk, si_np[s][None, None], qqr, kkr, scale, [1], [s + 1], 1, 3,
-                           True, "bfloat16", positions="kernel")
+                           True, "float32", positions="kernel")
         assert_close(out[s].float().cpu().numpy(), ref[0][0, 0], RTOL, ATOL, f"out row {s}")
         assert_close(smax[0, s].cpu().numpy(), ref[1][0, 0, 0], RTOL, ATOL, f"smax row {s}")
         assert_close(ssum[0, s].cpu().numpy(), ref[2][0, 0, 0], RTOL, ATOL, f"ssum row {s}")
