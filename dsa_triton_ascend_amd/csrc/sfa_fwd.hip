@@ -127,15 +127,35 @@ __device__ __forceinline__ bool sfa_resolve(const SfaFwdParams& p, const RowInfo
   return true;
 }
 
+// Zero row for padding slots of the 64-bit gather path (the buffer path
+// gets zeros from the hardware range check instead).
+__device__ __attribute__((aligned(16))) unsigned char g_sfa_zero_row[1024];
+
+// One 16-byte-per-lane DMA from global memory straight into LDS: lane L's
+// 16 bytes land at lds_base + 16*L (LDS address taken from M0).  Issued via
+// inline asm so that the compiler does not drain all outstanding DMA before
+// every LDS read; the tile loop waits with explicit vmcnt counts instead.
+__device__ __forceinline__ void dma_buf16(unsigned lds_base, int voff, __amdgpu_buffer_rsrc_t rsrc) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(lds_base), "v"(voff), "s"(rsrc) : "memory");
+}
+__device__ __forceinline__ void dma_glb16(unsigned lds_base, const void* gaddr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(lds_base), "v"(gaddr) : "memory");
+}
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
 // HT = head tiles (of 16 heads) per wave; a workgroup covers 4*HT*16 heads.
-// BUF: gather through buffer loads with 32-bit offsets (key tensors under
-// 2 GiB); the hardware range check returns zeros for padding slots and -1
-// pages, so no selects are needed.  Otherwise 64-bit global loads.
+// BUF: gather with buffer loads (32-bit offsets, key tensors under 2 GiB;
+// the hardware range check yields the zero rows); otherwise 64-bit global
+// addresses with an explicit zero row.
 template <int D, typename T, int HT, bool BUF>
 __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   using E = Elem<T>;
   using V8 = typename E::v8;
-  constexpr bool kSplitP = sizeof(T) == 2 && __is_same(T, bf16);
+  constexpr bool kSplitP = __is_same(T, bf16);
   constexpr int DR = 64;
   constexpr int KS = (D + DR) / 32;  // GEMM1 k-steps
   constexpr int KSN = D / 32;        // of which from the nope part
@@ -143,12 +163,21 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
   constexpr int TILE = kSfaTile;
   constexpr int NOPE_BYTES = TILE * D * 2;
   constexpr int BUF_BYTES = NOPE_BYTES + TILE * DR * 2;
-  constexpr int NOPE_CH = D / 8;                         // 16-byte chunks per nope row
-  constexpr int NLOAD = (TILE * (NOPE_CH + 8)) / kSfaThreads;
-  constexpr int NLOAD_NOPE = (TILE * NOPE_CH) / kSfaThreads;
-  static_assert(TILE * NOPE_CH % kSfaThreads == 0, "tile split");
+  constexpr int NBUF = 3;                    // DMA ring: tiles t+1, t+2 in flight during t
+  constexpr int CPT = D / 8;                 // 16-byte chunks per nope row
+  constexpr int TPI = 64 / CPT;              // nope tokens per wave-wide DMA (1 KB)
+  constexpr int NI = TILE / TPI / 4;         // nope DMAs per wave per tile
+  constexpr int LW = NI + 1;                 // + one rope DMA (8 tokens x 128 B)
+  // LDS layout: the NBUF tile buffers are interleaved in 1 KB blocks (one
+  // DMA each) so that a buffer index only adds a small immediate to a read
+  // address: nope block k (tokens k*TPI..) of buffer b at (k*NBUF + b) KB,
+  // rope block k (tokens 8k..8k+7) of buffer b at ROPE0 + (k*NBUF + b) KB.
+  constexpr int ROPE0 = NBUF * NOPE_BYTES;
+  auto nope_off = [](int tk, int b) { return ((tk / TPI) * NBUF + b) * 1024 + (tk % TPI) * (D * 2); };
+  auto rope_off = [](int tk, int b) { return ROPE0 + ((tk >> 3) * NBUF + b) * 1024 + (tk & 7) * (DR * 2); };
+  static_assert(kSfaThreads == 256 && TILE == 32, "tile/wave layout");
 
-  __shared__ __attribute__((aligned(16))) unsigned char smem[2 * BUF_BYTES];
+  __shared__ __attribute__((aligned(16))) unsigned char smem[NBUF * BUF_BYTES];
   __shared__ int s_list[kSfaMaxList + kSfaTile];
   __shared__ int s_wcnt[4];
 
@@ -197,13 +226,87 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
     n_valid += tot;
     lds_barrier();
   }
-
   // pad the list to a whole tile with -1 so tile loads index it unconditionally
   if (tid < TILE) s_list[n_valid + tid] = -1;
   lds_barrier();
+  const int n_tiles = (n_valid + TILE - 1) / TILE;
+
+  // ---- tile gather: global -> LDS by DMA, swizzled rows ----
+  // nope: DMA i of wave w covers tokens (i*4 + w)*TPI .. +TPI, lane L holds
+  // chunk L % CPT of token tk0 + L / CPT and loads source chunk
+  // (L % CPT) ^ nope_swz(tk), so that LDS chunk c holds chunk c ^ nope_swz.
+  // rope: wave w covers tokens 8w .. 8w+7, lane L -> token 8w + L/8.
+  const unsigned smem_base = (unsigned)(uintptr_t)smem;
+  __amdgpu_buffer_rsrc_t rsrc_k, rsrc_r;
+  if constexpr (BUF) {
+    rsrc_k = __builtin_amdgcn_make_buffer_rsrc((void*)p.k, (short)0, (int)(p.kv_rows * D * 2), 0x00020000);
+    rsrc_r = __builtin_amdgcn_make_buffer_rsrc((void*)p.kr, (short)0, (int)(p.kv_rows * DR * 2), 0x00020000);
+  }
+  auto issue_tile = [&](int t, int b) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int tk0 = (i * 4 + wave) * TPI;
+      const int tk = tk0 + lane / CPT;
+      const int ch = (lane % CPT) ^ nope_swz(tk);
+      const int phys = s_list[t * TILE + tk];  // -1 past n_valid / for -1 pages
+      const unsigned dst = __builtin_amdgcn_readfirstlane(smem_base + nope_off(tk0, b));
+      if constexpr (BUF) {
+        dma_buf16(dst, phys >= 0 ? phys * (D * 2) + ch * 16 : (int)0x80000000, rsrc_k);
+      } else {
+        const void* src = phys >= 0 ? (const void*)((const unsigned char*)p.k + (int64_t)phys * (D * 2) + ch * 16)
+                                    : (const void*)(g_sfa_zero_row + ch * 16);
+        dma_glb16(dst, src);
+      }
+    }
+    {
+      const int tk = wave * 8 + (lane >> 3);
+      const int ch = (lane & 7) ^ rope_swz(tk);
+      const int phys = s_list[t * TILE + tk];
+      const unsigned dst = __builtin_amdgcn_readfirstlane(smem_base + rope_off(wave * 8, b));
+      if constexpr (BUF) {
+        dma_buf16(dst, phys >= 0 ? phys * (DR * 2) + ch * 16 : (int)0x80000000, rsrc_r);
+      } else {
+        const void* src = phys >= 0 ? (const void*)((const unsigned char*)p.kr + (int64_t)phys * (DR * 2) + ch * 16)
+                                    : (const void*)(g_sfa_zero_row + ch * 16);
+        dma_glb16(dst, src);
+      }
+    }
+  };
 
   const int head0 = hg * HEADS_PER_WG + wave * HT * 16;
   const bool wave_active = head0 < p.n1;
+
+  // Barrier sequence, identical for every wave: per tile one barrier, then
+  // one vote barrier, and (only if the vote is set) a second pass of tiles.
+  // Tile t is waited for (vmcnt) before the barrier; tile t+2 is issued
+  // after it, into the buffer tile t-1 used (all waves are past it).
+  auto gather_loop_prologue = [&]() {
+    if (n_tiles > 0) issue_tile(0, 0);
+    if (n_tiles > 1) issue_tile(1, 1);
+  };
+  auto tile_sync = [&](int t, int b) {
+    if (t + 1 < n_tiles) wait_vmcnt<LW>();
+    else wait_vmcnt<0>();
+    lds_barrier();
+    if (t + 2 < n_tiles) issue_tile(t + 2, b == 0 ? 2 : b - 1);
+  };
+
+  if (!wave_active) {
+    // waves without heads (N1 < HEADS_PER_WG) only help with the gather
+    auto gather_only = [&]() {
+      gather_loop_prologue();
+      for (int t0 = 0; t0 < n_tiles; t0 += NBUF)
+#pragma unroll
+        for (int b = 0; b < NBUF; ++b) {
+          const int t = t0 + b;
+          if (t >= n_tiles) break;
+          tile_sync(t, b);
+        }
+    };
+    gather_only();
+    if (__syncthreads_or(0)) gather_only();
+    return;
+  }
 
   // ---- Q fragments (B operand of S^T = K.Q^T): lane -> head li, k = 8*lg.. ----
   V8 qf[HT][KS];
@@ -240,59 +343,6 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
   }
   bool overflow = false;
 
-  const int n_tiles = (n_valid + TILE - 1) / TILE;
-
-  // ---- tile loader: global -> registers, registers -> swizzled LDS ----
-  // Slots past n_valid and attended tokens of -1 pages read as zero rows.
-  // The loads of tile t+1 stay in flight while tile t is computed.
-  u32x4 stage[NLOAD];
-  unsigned stage_ok = 0;
-  __amdgpu_buffer_rsrc_t rsrc_k, rsrc_r;
-  if constexpr (BUF) {
-    rsrc_k = __builtin_amdgcn_make_buffer_rsrc((void*)p.k, (short)0, (int)(p.kv_rows * D * 2), 0x00020000);
-    rsrc_r = __builtin_amdgcn_make_buffer_rsrc((void*)p.kr, (short)0, (int)(p.kv_rows * DR * 2), 0x00020000);
-  }
-  auto load_tile = [&](int t) {
-    stage_ok = 0;
-#pragma unroll
-    for (int it = 0; it < NLOAD; ++it) {
-      const int c = it * kSfaThreads + tid;
-      int tk, cc;
-      if (it < NLOAD_NOPE) { tk = c / NOPE_CH; cc = c % NOPE_CH; }
-      else { const int c2 = c - TILE * NOPE_CH; tk = c2 >> 3; cc = c2 & 7; }
-      const int phys = s_list[t * TILE + tk];  // -1 past n_valid
-      if constexpr (BUF) {
-        const unsigned row_bytes = it < NLOAD_NOPE ? D * 2 : DR * 2;
-        const unsigned off = phys >= 0 ? (unsigned)phys * row_bytes + cc * 16 : 0x80000000u;
-        stage[it] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(it < NLOAD_NOPE ? rsrc_k : rsrc_r, (int)off, 0, 0));
-      } else {
-        const int64_t ps = phys >= 0 ? phys : 0;  // row 0 is a safe address
-        if (it < NLOAD_NOPE) stage[it] = *(const u32x4*)((const T*)p.k + ps * D + cc * 8);
-        else stage[it] = *(const u32x4*)((const T*)p.kr + ps * DR + cc * 8);
-        stage_ok |= (phys >= 0 ? 1u : 0u) << it;
-      }
-    }
-  };
-  auto store_tile = [&](int buf) {
-    unsigned char* base = smem + buf * BUF_BYTES;
-    const u32x4 z = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int it = 0; it < NLOAD; ++it) {
-      const int c = it * kSfaThreads + tid;
-      u32x4 v = stage[it];
-      if constexpr (!BUF) v = ((stage_ok >> it) & 1u) ? v : z;
-      if (it < NLOAD_NOPE) {
-        const int tk = c / NOPE_CH, cc = c % NOPE_CH;
-        *(u32x4*)(base + tk * (D * 2) + (cc ^ nope_swz(tk)) * 16) = v;
-      } else {
-        const int c2 = c - TILE * NOPE_CH;
-        const int tk = c2 >> 3, cc = c2 & 7;
-        *(u32x4*)(base + NOPE_BYTES + tk * (DR * 2) + (cc ^ rope_swz(tk)) * 16) = v;
-      }
-    }
-  };
-
   // ---- per-lane LDS byte offsets; every read below is offset + immediate ----
   // GEMM1 A fragment: token tk = tt*16 + li, chunk ks*4 + lg.  The swizzle
   // XORs the low four chunk bits, so ks mod 4 selects one of four bases and
@@ -302,10 +352,9 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
   for (int tt = 0; tt < 2; ++tt) {
     const int tk = tt * 16 + li;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) g1[tt][m] = tk * (D * 2) + (((4 * m + lg) ^ nope_swz(tk)) * 16);
+    for (int m = 0; m < 4; ++m) g1[tt][m] = nope_off(tk, 0) + (((4 * m + lg) ^ nope_swz(tk)) * 16);
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
-      g1r[tt][m] = NOPE_BYTES + tk * (DR * 2) + (((4 * m + lg) ^ rope_swz(tk)) * 16);
+    for (int m = 0; m < 2; ++m) g1r[tt][m] = rope_off(tk, 0) + (((4 * m + lg) ^ rope_swz(tk)) * 16);
   }
   // GEMM2 transposed reads: row r1 = 4*lg + li/4 (and r1 + 16, same swizzle),
   // chunk dt*2 + (li&3)/2, 8-byte half (li&1): dt mod 8 selects the base.
@@ -314,150 +363,130 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
     const int r1 = lg * 4 + (li >> 2);
     const int b = (li & 3) >> 1;
 #pragma unroll
-    for (int m = 0; m < 8; ++m) g2[m] = r1 * (D * 2) + ((((2 * m) | b) ^ nope_swz(r1)) * 16) + (li & 1) * 8;
+    for (int m = 0; m < 8; ++m) g2[m] = nope_off(r1, 0) + ((((2 * m) | b) ^ nope_swz(r1)) * 16) + (li & 1) * 8;
   }
+  constexpr int G2_ROW16 = (16 / TPI) * NBUF * 1024;  // row r1 -> r1 + 16
   constexpr int NS1 = KS * 2;  // GEMM1 steps (k-step x token tile)
-  constexpr int PF1 = 4;       // GEMM1 fragments in flight
-  constexpr int PF2 = 4;       // GEMM2 fragments in flight
+  constexpr int PF1 = HT == 1 ? 8 : 4;  // GEMM1 fragments in flight
+  constexpr int PF2 = HT == 1 ? 8 : 4;  // GEMM2 fragments in flight
 
-  auto run_tiles = [&]() {
-    if (n_tiles > 0) {
-      load_tile(0);
-      store_tile(0);
+  auto compute_tile = [&](int t, int b) {
+    auto a1 = [&](int st) -> u32x4 {
+      const int ks = st >> 1, tt = st & 1;
+      if (ks < KSN) return *(const u32x4*)(smem + g1[tt][ks & 3] + b * 1024 + (ks >> 2) * 256);
+      return *(const u32x4*)(smem + g1r[tt][ks - KSN] + b * 1024);
+    };
+    auto a2 = [&](int dt) -> V8 {
+      const unsigned char* p1 = smem + g2[dt & 7] + b * 1024 + (dt >> 3) * 256;
+      const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1);
+      const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p1 + G2_ROW16));
+      const i16x4 w1 = __builtin_bit_cast(i16x4, v1);
+      const i16x4 w2 = __builtin_bit_cast(i16x4, v2);
+      const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
+      return __builtin_bit_cast(V8, w);
+    };
+
+    // ---- GEMM1: S^T[32 tok x HT*16 heads], fragments PF1 steps ahead ----
+    f32x4 acc_s[2][HT];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) acc_s[tt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    u32x4 fa[PF1];
+#pragma unroll
+    for (int i = 0; i < PF1; ++i) fa[i] = a1(i);
+#pragma unroll
+    for (int st = 0; st < NS1; ++st) {
+      const int ks = st >> 1, tt = st & 1;
+      const V8 av = as_v8<V8>(fa[st % PF1]);
+      if (st + PF1 < NS1) fa[st % PF1] = a1(st + PF1);
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) acc_s[tt][ht] = E::mfma(av, qf[ht][ks], acc_s[tt][ht]);
     }
-    // tile loop unrolled by two: the LDS buffer of each copy is a constant
-    for (int t0 = 0; t0 < n_tiles; t0 += 2)
-#pragma unroll
-    for (int buf = 0; buf < 2; ++buf) {
-      const int t = t0 + buf;
-      if (t >= n_tiles) break;
-      if (t + 1 < n_tiles) load_tile(t + 1);
-      lds_barrier();
-      {
-        const unsigned char* base = smem + buf * BUF_BYTES;
-        auto a1 = [&](int st) -> u32x4 {
-          const int ks = st >> 1, tt = st & 1;
-          if (ks < KSN) return *(const u32x4*)(base + g1[tt][ks & 3] + (ks >> 2) * 256);
-          return *(const u32x4*)(base + g1r[tt][ks - KSN]);
-        };
-        auto a2 = [&](int dt) -> V8 {
-          const unsigned char* p1 = base + g2[dt & 7] + (dt >> 3) * 256;
-          const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1);
-          const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p1 + 16 * D * 2));
-          const i16x4 w1 = __builtin_bit_cast(i16x4, v1);
-          const i16x4 w2 = __builtin_bit_cast(i16x4, v2);
-          const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
-          return __builtin_bit_cast(V8, w);
-        };
-
-        // ---- GEMM1: S^T[32 tok x HT*16 heads], fragments PF1 steps ahead ----
-        f32x4 acc_s[2][HT];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-          for (int ht = 0; ht < HT; ++ht) acc_s[tt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
-        u32x4 fa[PF1];
-#pragma unroll
-        for (int i = 0; i < PF1; ++i) fa[i] = a1(i);
-#pragma unroll
-        for (int st = 0; st < NS1; ++st) {
-          const int ks = st >> 1, tt = st & 1;
-          const V8 av = as_v8<V8>(fa[st % PF1]);
-          if (st + PF1 < NS1) fa[st % PF1] = a1(st + PF1);
-#pragma unroll
-          for (int ht = 0; ht < HT; ++ht) acc_s[tt][ht] = E::mfma(av, qf[ht][ks], acc_s[tt][ht]);
-        }
 #if DSA_SCHED_GROUPS
-        __builtin_amdgcn_sched_group_barrier(0x100, PF1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, PF1, 0);
 #pragma unroll
-        for (int st = 0; st < NS1; ++st) {
-          __builtin_amdgcn_sched_group_barrier(0x008, HT, 0);
-          if (st + PF1 < NS1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
+    for (int st = 0; st < NS1; ++st) {
+      __builtin_amdgcn_sched_group_barrier(0x008, HT, 0);
+      if (st + PF1 < NS1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
 #endif
-        // first V^T fragments go out before the softmax arithmetic
-        V8 fv[PF2];
+    // first V^T fragments go out before the softmax arithmetic
+    V8 fv[PF2];
 #pragma unroll
-        for (int i = 0; i < PF2; ++i) fv[i] = a2(i);
+    for (int i = 0; i < PF2; ++i) fv[i] = a2(i);
 
-        // ---- softmax numerators (log2 domain) as P^T fragments ----
-        // P^T is split into bf16 hi + lo parts for bf16 I/O (fp16 keeps 11
-        // bits in one part): the P.V product then carries ~16 bits of P, so
-        // its error is that of the final output rounding.
-        V8 pf[HT], pf_lo[HT];
+    // ---- softmax numerators (log2 domain) as P^T fragments ----
+    // P^T is split into bf16 hi + lo parts for bf16 I/O (fp16 keeps 11 bits
+    // in one part): the P.V product then carries ~16 bits of P, so its error
+    // is that of the final output rounding.
+    V8 pf[HT], pf_lo[HT];
 #pragma unroll
-        for (int ht = 0; ht < HT; ++ht) {
-          float tmax = -INFINITY;
+    for (int ht = 0; ht < HT; ++ht) {
+      float tmax = -INFINITY;
 #pragma unroll
-          for (int tt = 0; tt < 2; ++tt) {
+      for (int tt = 0; tt < 2; ++tt) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int tok = t * TILE + tt * 16 + lg * 4 + r;
-              float v = acc_s[tt][ht][r] * p.scale_log2;
-              v = tok < n_valid ? v : -INFINITY;
-              acc_s[tt][ht][r] = v;
-              tmax = fmaxf(tmax, v);
-            }
-          }
-          tmax = xgroup_max(tmax);
-          m_true[ht] = fmaxf(m_true[ht], tmax);
-          if (m_ref[ht] == -INFINITY) m_ref[ht] = tmax;
-          overflow |= tmax > m_ref[ht] + kRefSlack;
-          V8 hi, lo;
-          float lsum = 0.f;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            // m_ref == -inf only while no token is visible: all s are -inf too
-            const float e = m_ref[ht] == -INFINITY ? 0.f : fast_exp2(acc_s[j >> 2][ht][j & 3] - m_ref[ht]);
-            lsum += e;
-            const T h = E::from_f32(e);
-            hi[j] = h;
-            lo[j] = E::from_f32(e - E::to_f32(h));
-          }
-          l_run[ht] += lsum;
-          pf[ht] = hi;
-          pf_lo[ht] = lo;
+        for (int r = 0; r < 4; ++r) {
+          const int tok = t * TILE + tt * 16 + lg * 4 + r;
+          float v = acc_s[tt][ht][r] * p.scale_log2;
+          v = tok < n_valid ? v : -INFINITY;
+          acc_s[tt][ht][r] = v;
+          tmax = fmaxf(tmax, v);
         }
-
-        // ---- GEMM2: O^T[D x HT*16 heads] += V^T . P^T, fragments PF2 ahead ----
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          const V8 av = fv[dt % PF2];
-          if (dt + PF2 < NDT) fv[dt % PF2] = a2(dt + PF2);
-#pragma unroll
-          for (int ht = 0; ht < HT; ++ht) {
-            acc_o[dt][ht] = E::mfma(av, pf[ht], acc_o[dt][ht]);
-            if (kSplitP) acc_o[dt][ht] = E::mfma(av, pf_lo[ht], acc_o[dt][ht]);
-          }
-        }
-#if DSA_SCHED_GROUPS
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          __builtin_amdgcn_sched_group_barrier(0x008, HT * (kSplitP ? 2 : 1), 1);
-          if (dt + PF2 < NDT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-        }
-#endif
       }
-      if (t + 1 < n_tiles) store_tile(buf ^ 1);
+      tmax = xgroup_max(tmax);
+      m_true[ht] = fmaxf(m_true[ht], tmax);
+      if (m_ref[ht] == -INFINITY) m_ref[ht] = tmax;
+      overflow |= tmax > m_ref[ht] + kRefSlack;
+      V8 hi, lo;
+      float lsum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        // m_ref == -inf only while no token is visible: all s are -inf too
+        const float e = m_ref[ht] == -INFINITY ? 0.f : fast_exp2(acc_s[j >> 2][ht][j & 3] - m_ref[ht]);
+        lsum += e;
+        const T h = E::from_f32(e);
+        hi[j] = h;
+        lo[j] = E::from_f32(e - E::to_f32(h));
+      }
+      l_run[ht] += lsum;
+      pf[ht] = hi;
+      pf_lo[ht] = lo;
     }
+
+    // ---- GEMM2: O^T[D x HT*16 heads] += V^T . P^T, fragments PF2 ahead ----
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const V8 av = fv[dt % PF2];
+      if (dt + PF2 < NDT) fv[dt % PF2] = a2(dt + PF2);
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht) {
+        acc_o[dt][ht] = E::mfma(av, pf[ht], acc_o[dt][ht]);
+        if (kSplitP) acc_o[dt][ht] = E::mfma(av, pf_lo[ht], acc_o[dt][ht]);
+      }
+    }
+#if DSA_SCHED_GROUPS
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      __builtin_amdgcn_sched_group_barrier(0x008, HT * (kSplitP ? 2 : 1), 1);
+      if (dt + PF2 < NDT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+    }
+#endif
   };
 
-  // Barrier sequence (identical for every wave): pass-0 tiles, one vote
-  // barrier, and only if the vote is set, pass-1 tiles.
-  if (!wave_active) {
-    // waves without heads (N1 < 128) only help with the gather
-    auto gather_only = [&]() {
-      if (n_tiles > 0) { load_tile(0); store_tile(0); }
-      for (int t = 0; t < n_tiles; ++t) {
-        if (t + 1 < n_tiles) load_tile(t + 1);
-        lds_barrier();
-        if (t + 1 < n_tiles) store_tile((t & 1) ^ 1);
+  auto run_tiles = [&]() {
+    gather_loop_prologue();
+    // unrolled by the ring size so every copy has a constant LDS buffer
+    for (int t0 = 0; t0 < n_tiles; t0 += NBUF)
+#pragma unroll
+      for (int b = 0; b < NBUF; ++b) {
+        const int t = t0 + b;
+        if (t >= n_tiles) break;
+        tile_sync(t, b);
+        compute_tile(t, b);
       }
-    };
-    gather_only();
-    if (__syncthreads_or(0)) gather_only();
-    return;
-  }
+  };
 
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
@@ -600,8 +629,9 @@ size_t sfa_fwd_workspace_bytes(int64_t rows, int64_t n1, int64_t d, int64_t tota
   return (size_t)splits * rows * n1 * (d + 4) * sizeof(float);
 }
 
-// Head tiles per wave: D=512 keeps 16 heads per wave so that the O
-// accumulator (D x 16 fp32) and Q fragments fit the register file.
+// Head tiles (of 16 heads) per wave.  D=512 keeps 16 heads per wave (two
+// workgroups per row, on one XCD): 32 heads would need 256 accumulator plus
+// 144 Q-fragment registers, which leaves too little for the pipeline.
 template <int D> struct SfaHT { static constexpr int value = D >= 512 ? 1 : 2; };
 
 int sfa_fwd_head_groups(int64_t n1, int64_t d) {
