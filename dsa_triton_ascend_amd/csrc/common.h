@@ -82,16 +82,17 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// LDS swizzles for token rows stored as 16-byte chunks.  LDS is modelled as
-// 64 banks x 4 bytes (a 256-byte window per cycle).
-//  * nope rows (D*2 bytes, >= 16 chunks): chunk c of token t is stored at
-//    chunk c ^ nope_swz(t) (low four bits only).  Sixteen consecutive tokens
-//    reading one chunk (GEMM1 A fragments, 16 lanes x 16 bytes) hit sixteen
-//    distinct 16-byte bank groups, and the 8 rows x 2 chunks read by 32 lanes
-//    of a transposed 8-byte load (rows 8h..8h+7) cover all 64 banks.
-//  * rope rows (128 bytes = 8 chunks): chunk c of token t at c ^ rope_swz(t);
-//    token parity selects the 128-byte half of the window.
-__device__ __forceinline__ int nope_swz(int tok) { return ((tok & 7) << 1) | ((tok >> 3) & 1); }
+// LDS swizzles for token rows stored as 16-byte chunks (chunk c of token t
+// is stored at c ^ swz(t), low four bits only).  Chosen by measurement on
+// gfx950 (SQ_LDS_BANK_CONFLICT over the exact access patterns): the nope
+// swizzle is conflict-free both for ds_read_b128 of 16 tokens x 4 chunk
+// columns (the A fragment of K.Q^T) and for ds_read_b64_tr_b16 over 16 rows
+// x 2 chunks (the V^T fragment); the simpler ((t & 7) << 1 | t >> 3 & 1)
+// form costs the b128 reads a 2-way conflict.  Rope rows are 128 bytes (8
+// chunks) and only read by ds_read_b128.  Both depend on t mod 16 only.
+__device__ __forceinline__ int nope_swz(int tok) {
+  return (((tok & 3) << 2) | (((tok >> 2) & 1) * 3)) ^ (((tok >> 3) & 1) << 1);
+}
 __device__ __forceinline__ int rope_swz(int tok) { return (tok >> 1) & 7; }
 
 }  // namespace dsa

@@ -44,8 +44,12 @@ struct SfaFwdParams {
   void* out;
   float* smax;
   float* ssum;
-  float* part_o;   // [splits, R, N1, D] unnormalised partial O (splits > 1)
-  float* part_ml;  // [splits, R, N1, 4]: reference max, sum, exact max (log2 units), pad
+  // split partials (splits > 1): part_o[s, r, h, :] = O_s / (l_s * scale_s)
+  // in fp16, scale_s = 2^e >= max |O_s / l_s| (so |values| < 1: fp16 keeps
+  // 11 bits for the largest ones); part_ml[s, r, h] = {reference max (log2
+  // units), l_s, exact max (log2 units), scale_s}
+  _Float16* part_o;
+  float* part_ml;
   int64_t rows;
   int64_t kv_rows;
   int32_t batch, s1, s2, n1, K;
@@ -63,7 +67,6 @@ struct SfaFwdParams {
 
 constexpr int kSfaTile = 32;
 constexpr int kSfaMaxList = 4096;
-constexpr int kSfaThreads = 256;
 constexpr float kRefSlack = 64.f;  // log2 units
 
 struct RowInfo {
@@ -147,12 +150,13 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
 }
 
-// HT = head tiles (of 16 heads) per wave; a workgroup covers 4*HT*16 heads.
+// HT = head tiles (of 16 heads) per wave, NW = waves; a workgroup covers
+// NW*HT*16 heads.
 // BUF: gather with buffer loads (32-bit offsets, key tensors under 2 GiB;
 // the hardware range check yields the zero rows); otherwise 64-bit global
 // addresses with an explicit zero row.
-template <int D, typename T, int HT, bool BUF>
-__global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p) {
+template <int D, typename T, int HT, int NW, bool BUF>
+__global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   using E = Elem<T>;
   using V8 = typename E::v8;
   constexpr bool kSplitP = __is_same(T, bf16);
@@ -166,8 +170,9 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
   constexpr int NBUF = 3;                    // DMA ring: tiles t+1, t+2 in flight during t
   constexpr int CPT = D / 8;                 // 16-byte chunks per nope row
   constexpr int TPI = 64 / CPT;              // nope tokens per wave-wide DMA (1 KB)
-  constexpr int NI = TILE / TPI / 4;         // nope DMAs per wave per tile
-  constexpr int LW = NI + 1;                 // + one rope DMA (8 tokens x 128 B)
+  constexpr int NI = TILE / TPI / NW;        // nope DMAs per wave per tile
+  constexpr int NTHR = NW * 64;
+  // + one rope DMA (8 tokens x 128 B) for waves 0..3
   // LDS layout: the NBUF tile buffers are interleaved in 1 KB blocks (one
   // DMA each) so that a buffer index only adds a small immediate to a read
   // address: nope block k (tokens k*TPI..) of buffer b at (k*NBUF + b) KB,
@@ -175,11 +180,11 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
   constexpr int ROPE0 = NBUF * NOPE_BYTES;
   auto nope_off = [](int tk, int b) { return ((tk / TPI) * NBUF + b) * 1024 + (tk % TPI) * (D * 2); };
   auto rope_off = [](int tk, int b) { return ROPE0 + ((tk >> 3) * NBUF + b) * 1024 + (tk & 7) * (DR * 2); };
-  static_assert(kSfaThreads == 256 && TILE == 32, "tile/wave layout");
+  static_assert(TILE == 32 && (NW == 4 || NW == 8) && NI >= 1, "tile/wave layout");
 
   __shared__ __attribute__((aligned(16))) unsigned char smem[NBUF * BUF_BYTES];
   __shared__ int s_list[kSfaMaxList + kSfaTile];
-  __shared__ int s_wcnt[4];
+  __shared__ int s_wcnt[NW];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -188,7 +193,7 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
   const int lg = lane >> 4;  // 16-lane group
 
   // ---- block -> (row, split, head group); a row's blocks share an XCD ----
-  constexpr int HEADS_PER_WG = 4 * HT * 16;
+  constexpr int HEADS_PER_WG = NW * HT * 16;
   const int hgroups = (p.n1 + HEADS_PER_WG - 1) / HEADS_PER_WG;
   const int bid = blockIdx.x;
   const int jj = bid >> 3;
@@ -206,7 +211,7 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
 
   // ---- compact attended positions into s_list (stable order) ----
   int n_valid = 0;
-  for (int c0 = p0; c0 < p1; c0 += kSfaThreads) {
+  for (int c0 = p0; c0 < p1; c0 += NTHR) {
     int pos = c0 + tid;
     int phys = 0;
     bool valid = false;
@@ -217,7 +222,7 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
     int off = n_valid;
     int tot = 0;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < NW; ++w) {
       int c = s_wcnt[w];
       off += (w < wave) ? c : 0;
       tot += c;
@@ -232,24 +237,36 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
   const int n_tiles = (n_valid + TILE - 1) / TILE;
 
   // ---- tile gather: global -> LDS by DMA, swizzled rows ----
-  // nope: DMA i of wave w covers tokens (i*4 + w)*TPI .. +TPI, lane L holds
+  // nope: DMA i of wave w covers tokens (i*NW + w)*TPI .. +TPI, lane L holds
   // chunk L % CPT of token tk0 + L / CPT and loads source chunk
   // (L % CPT) ^ nope_swz(tk), so that LDS chunk c holds chunk c ^ nope_swz.
-  // rope: wave w covers tokens 8w .. 8w+7, lane L -> token 8w + L/8.
+  // rope: wave w < 4 covers tokens 8w .. 8w+7, lane L -> token 8w + L/8.
   const unsigned smem_base = (unsigned)(uintptr_t)smem;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  // wave-uniform DMA destinations: nope block (j*NW + wave), rope block (wave & 3)
+  const unsigned smem_wave = smem_base + nope_off(wave_s * TPI, 0);
+  const unsigned smem_rope_wave = smem_base + rope_off((wave_s & 3) * 8, 0) - rope_off(0, 0);
   __amdgpu_buffer_rsrc_t rsrc_k, rsrc_r;
   if constexpr (BUF) {
     rsrc_k = __builtin_amdgcn_make_buffer_rsrc((void*)p.k, (short)0, (int)(p.kv_rows * D * 2), 0x00020000);
     rsrc_r = __builtin_amdgcn_make_buffer_rsrc((void*)p.kr, (short)0, (int)(p.kv_rows * DR * 2), 0x00020000);
   }
-  auto issue_tile = [&](int t, int b) {
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int tk0 = (i * 4 + wave) * TPI;
-      const int tk = tk0 + lane / CPT;
+  // DMA j < NI of a wave loads nope block (j*NW + wave); DMA NI loads rope
+  // block (wave & 3) (with eight waves, waves w and w + 4 load the same rope
+  // block: identical bytes to the same place, which keeps the per-wave DMA
+  // count uniform and the issue code branch-free).  A tile past the end
+  // (phys = -1 everywhere) loads zeros and touches no memory.
+  constexpr int NDMA = NI + 1;
+  auto dma_phys = [&](int t, bool live, int j) -> int {
+    const int tk = j < NI ? (j * NW + wave) * TPI + lane / CPT : (wave & 3) * 8 + (lane >> 3);
+    const int v = s_list[t * TILE + tk];  // -1 past n_valid / for -1 pages
+    return live ? v : -1;
+  };
+  auto dma_issue = [&](int j, int phys, int b) {
+    if (j < NI) {
+      const int tk = (j * NW + wave) * TPI + lane / CPT;
       const int ch = (lane % CPT) ^ nope_swz(tk);
-      const int phys = s_list[t * TILE + tk];  // -1 past n_valid / for -1 pages
-      const unsigned dst = __builtin_amdgcn_readfirstlane(smem_base + nope_off(tk0, b));
+      const unsigned dst = smem_wave + nope_off(j * NW * TPI, b);
       if constexpr (BUF) {
         dma_buf16(dst, phys >= 0 ? phys * (D * 2) + ch * 16 : (int)0x80000000, rsrc_k);
       } else {
@@ -257,12 +274,10 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
                                     : (const void*)(g_sfa_zero_row + ch * 16);
         dma_glb16(dst, src);
       }
-    }
-    {
-      const int tk = wave * 8 + (lane >> 3);
+    } else {
+      const int tk = (wave & 3) * 8 + (lane >> 3);
       const int ch = (lane & 7) ^ rope_swz(tk);
-      const int phys = s_list[t * TILE + tk];
-      const unsigned dst = __builtin_amdgcn_readfirstlane(smem_base + rope_off(wave * 8, b));
+      const unsigned dst = smem_rope_wave + rope_off(0, b);
       if constexpr (BUF) {
         dma_buf16(dst, phys >= 0 ? phys * (DR * 2) + ch * 16 : (int)0x80000000, rsrc_r);
       } else {
@@ -272,6 +287,16 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
       }
     }
   };
+  // whole tile at once (prologue and gather-only waves); the s_list reads
+  // all go first: the DMA asm is a compiler memory barrier, so a read placed
+  // between two DMAs would wait for its own LDS round trip
+  auto issue_tile = [&](int t, int b) {
+    int ph[NDMA];
+#pragma unroll
+    for (int j = 0; j < NDMA; ++j) ph[j] = dma_phys(t, true, j);
+#pragma unroll
+    for (int j = 0; j < NDMA; ++j) dma_issue(j, ph[j], b);
+  };
 
   const int head0 = hg * HEADS_PER_WG + wave * HT * 16;
   const bool wave_active = head0 < p.n1;
@@ -279,17 +304,19 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
   // Barrier sequence, identical for every wave: per tile one barrier, then
   // one vote barrier, and (only if the vote is set) a second pass of tiles.
   // Tile t is waited for (vmcnt) before the barrier; tile t+2 is issued
-  // after it, into the buffer tile t-1 used (all waves are past it).
+  // after it, into the buffer tile t-1 used (all waves are past it), spread
+  // over the tile's first product so that the address unit drains while the
+  // MFMAs run.  Every wave issues NDMA loads per tile (zeros past the end).
   auto gather_loop_prologue = [&]() {
     if (n_tiles > 0) issue_tile(0, 0);
     if (n_tiles > 1) issue_tile(1, 1);
   };
-  auto tile_sync = [&](int t, int b) {
-    if (t + 1 < n_tiles) wait_vmcnt<LW>();
-    else wait_vmcnt<0>();
+  auto tile_sync = [&](int t) {
+    if (t + 1 >= n_tiles) wait_vmcnt<0>();
+    else wait_vmcnt<NDMA>();
     lds_barrier();
-    if (t + 2 < n_tiles) issue_tile(t + 2, b == 0 ? 2 : b - 1);
   };
+  auto next_buf = [](int b) { return b == 0 ? NBUF - 1 : b - 1; };
 
   if (!wave_active) {
     // waves without heads (N1 < HEADS_PER_WG) only help with the gather
@@ -300,8 +327,10 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
         for (int b = 0; b < NBUF; ++b) {
           const int t = t0 + b;
           if (t >= n_tiles) break;
-          tile_sync(t, b);
+          tile_sync(t);
+          if (t + 2 < n_tiles) issue_tile(t + 2, next_buf(b));
         }
+      wait_vmcnt<0>();
     };
     gather_only();
     if (__syncthreads_or(0)) gather_only();
@@ -343,41 +372,44 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
   }
   bool overflow = false;
 
-  // ---- per-lane LDS byte offsets; every read below is offset + immediate ----
-  // GEMM1 A fragment: token tk = tt*16 + li, chunk ks*4 + lg.  The swizzle
-  // XORs the low four chunk bits, so ks mod 4 selects one of four bases and
-  // the rest is a multiple of 256 bytes; rope chunks (ks-KSN)*4 + lg < 8.
-  int g1[2][4], g1r[2][2];
-#pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
-    const int tk = tt * 16 + li;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) g1[tt][m] = nope_off(tk, 0) + (((4 * m + lg) ^ nope_swz(tk)) * 16);
-#pragma unroll
-    for (int m = 0; m < 2; ++m) g1r[tt][m] = rope_off(tk, 0) + (((4 * m + lg) ^ rope_swz(tk)) * 16);
-  }
+  // ---- per-lane LDS byte offsets ----
+  // GEMM1 A fragment: token tk = tt*16 + li, chunk ks*4 + lg.  Row starts
+  // are multiples of 256 bytes and the swizzle only XORs the low four chunk
+  // bits, so chunk (4m + lg) ^ swz lies at g1 ^ (m << 6) (m = ks mod 4) plus
+  // 256 bytes per further group of four k-steps; rope chunks (4m + lg) ^ swz
+  // at g1r ^ (m << 6).  Tokens 16..31 share the swizzle of tokens 0..15 and
+  // sit a constant distance further on.  The XORs are recomputed per tile
+  // from one base each (the bases are re-derived through an empty asm so the
+  // compiler cannot hoist fourteen loop-invariant addresses into registers).
+  const int g1_0 = nope_off(li, 0) + ((lg ^ nope_swz(li)) * 16);
+  const int g1r_0 = rope_off(li, 0) + ((lg ^ rope_swz(li)) * 16);
+  constexpr int G1_TT = nope_off(16, 0) - nope_off(0, 0);
+  constexpr int G1R_TT = rope_off(16, 0) - rope_off(0, 0);
   // GEMM2 transposed reads: row r1 = 4*lg + li/4 (and r1 + 16, same swizzle),
-  // chunk dt*2 + (li&3)/2, 8-byte half (li&1): dt mod 8 selects the base.
-  int g2[8];
-  {
+  // chunk dt*2 + (li&3)/2, 8-byte half (li&1): chunk (2m | h) ^ swz is at
+  // g2 ^ (m << 5) for m = dt mod 8, plus 256 bytes per further eight d-tiles.
+  const int g2_0 = [&]() {
     const int r1 = lg * 4 + (li >> 2);
-    const int b = (li & 3) >> 1;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) g2[m] = nope_off(r1, 0) + ((((2 * m) | b) ^ nope_swz(r1)) * 16) + (li & 1) * 8;
-  }
+    const int h = (li & 3) >> 1;
+    return nope_off(r1, 0) + ((h ^ nope_swz(r1)) * 16) + (li & 1) * 8;
+  }();
   constexpr int G2_ROW16 = (16 / TPI) * NBUF * 1024;  // row r1 -> r1 + 16
   constexpr int NS1 = KS * 2;  // GEMM1 steps (k-step x token tile)
-  constexpr int PF1 = HT == 1 ? 8 : 4;  // GEMM1 fragments in flight
-  constexpr int PF2 = HT == 1 ? 8 : 4;  // GEMM2 fragments in flight
+  // fragments in flight: with two waves per SIMD the other wave covers LDS
+  // latency, and the registers are needed for the accumulators
+  constexpr int PF1 = NW == 8 ? 2 : (HT == 1 ? 8 : 4);  // GEMM1
+  constexpr int PF2 = NW == 8 ? 2 : (HT == 1 ? 8 : (D >= 512 ? 2 : 4));  // GEMM2
 
   auto compute_tile = [&](int t, int b) {
+    int g1b = g1_0, g1rb = g1r_0, g2b = g2_0;
+    asm volatile("" : "+v"(g1b), "+v"(g1rb), "+v"(g2b));
     auto a1 = [&](int st) -> u32x4 {
       const int ks = st >> 1, tt = st & 1;
-      if (ks < KSN) return *(const u32x4*)(smem + g1[tt][ks & 3] + b * 1024 + (ks >> 2) * 256);
-      return *(const u32x4*)(smem + g1r[tt][ks - KSN] + b * 1024);
+      if (ks < KSN) return *(const u32x4*)(smem + ((g1b ^ ((ks & 3) << 6)) + tt * G1_TT + b * 1024 + (ks >> 2) * 256));
+      return *(const u32x4*)(smem + ((g1rb ^ ((ks - KSN) << 6)) + tt * G1R_TT + b * 1024));
     };
     auto a2 = [&](int dt) -> V8 {
-      const unsigned char* p1 = smem + g2[dt & 7] + b * 1024 + (dt >> 3) * 256;
+      const unsigned char* p1 = smem + ((g2b ^ ((dt & 7) << 5)) + b * 1024 + (dt >> 3) * 256);
       const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1);
       const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p1 + G2_ROW16));
       const i16x4 w1 = __builtin_bit_cast(i16x4, v1);
@@ -385,6 +417,14 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
       const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
       return __builtin_bit_cast(V8, w);
     };
+
+    // s_list entries of tile t+2 for this wave's DMAs
+    const bool pf_live = t + 2 < n_tiles;
+    int dph[NDMA];
+#pragma unroll
+    for (int j = 0; j < NDMA; ++j) dph[j] = dma_phys(pf_live ? t + 2 : 0, pf_live, j);
+    const int nb = next_buf(b);
+    static_assert(2 + 4 * (NDMA - 1) < NS1, "DMA slots inside GEMM1");
 
     // ---- GEMM1: S^T[32 tok x HT*16 heads], fragments PF1 steps ahead ----
     f32x4 acc_s[2][HT];
@@ -402,6 +442,7 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
       if (st + PF1 < NS1) fa[st % PF1] = a1(st + PF1);
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) acc_s[tt][ht] = E::mfma(av, qf[ht][ks], acc_s[tt][ht]);
+      if ((st & 3) == 2 && (st >> 2) < NDMA) dma_issue(st >> 2, dph[st >> 2], nb);
     }
 #if DSA_SCHED_GROUPS
     __builtin_amdgcn_sched_group_barrier(0x100, PF1, 0);
@@ -483,9 +524,10 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
       for (int b = 0; b < NBUF; ++b) {
         const int t = t0 + b;
         if (t >= n_tiles) break;
-        tile_sync(t, b);
+        tile_sync(t);
         compute_tile(t, b);
       }
+    wait_vmcnt<0>();  // tail loads of tiles past the end
   };
 
 #pragma unroll
@@ -509,47 +551,91 @@ __global__ __launch_bounds__(kSfaThreads, 1) void sfa_fwd_kernel(SfaFwdParams p)
   }
 
   // ---- epilogue ----
+  // per head tile: total sum, statistics, and for split partials the fp16
+  // scale 2^ex >= max |O / l| of the head
+  float mul[HT];
 #pragma unroll
   for (int ht = 0; ht < HT; ++ht) {
     const int head = head0 + ht * 16 + li;
     const float l_tot = xgroup_sum(l_run[ht]);
-    if (head >= p.n1) continue;
-    const int64_t orow = row * p.n1 + head;
-    if (p.splits == 1) {
-      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-      T* op = (T*)p.out + orow * D;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    int ex = 0;
+    if (p.splits > 1) {
+      float a = 0.f;
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const f32x4 v = acc_o[dt][ht];
-        typedef T T4 __attribute__((ext_vector_type(4)));
-        T4 o;
-        o[0] = E::from_f32(v[0] * inv);
-        o[1] = E::from_f32(v[1] * inv);
-        o[2] = E::from_f32(v[2] * inv);
-        o[3] = E::from_f32(v[3] * inv);
-        *(T4*)(op + dt * 16 + lg * 4) = o;
-      }
-      if (p.return_lse && lg == 0) {
-        const bool any = l_tot > 0.f;
-        p.smax[orow] = any ? m_true[ht] * kLn2 : 0.f;
-        p.ssum[orow] = any ? l_tot * fast_exp2(m_ref[ht] - m_true[ht]) : 0.f;
-      }
-    } else {
-      const int64_t prow = (int64_t)split * p.rows * p.n1 + orow;
-      float* po = p.part_o + prow * D;
+      for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) *(f32x4*)(po + dt * 16 + lg * 4) = acc_o[dt][ht];
-      if (lg == 0) {
-        f32x4 ml = {m_ref[ht], l_tot, m_true[ht], 0.f};
+        for (int r = 0; r < 4; ++r) a = fmaxf(a, fabsf(acc_o[dt][ht][r]));
+      a = xgroup_max(a) * inv;
+      if (a > 0.f) (void)frexpf(a, &ex);  // a < 2^ex
+    }
+    mul[ht] = ldexpf(inv, -ex);
+    if (head < p.n1 && lg == 0) {
+      const int64_t orow = row * p.n1 + head;
+      if (p.splits == 1) {
+        if (p.return_lse) {
+          const bool any = l_tot > 0.f;
+          p.smax[orow] = any ? m_true[ht] * kLn2 : 0.f;
+          p.ssum[orow] = any ? l_tot * fast_exp2(m_ref[ht] - m_true[ht]) : 0.f;
+        }
+      } else {
+        const int64_t prow = (int64_t)split * p.rows * p.n1 + orow;
+        const f32x4 ml = {m_ref[ht], l_tot, m_true[ht], ldexpf(1.f, ex)};
         *(f32x4*)(p.part_ml + prow * 4) = ml;
+      }
+    }
+  }
+  // O rows (output in T, or split partials in fp16) are staged through this
+  // wave's own LDS region, half of D at a time (the tile ring is idle now),
+  // so that global stores are whole 16-byte-per-lane row segments rather
+  // than 8-byte pieces of 16 different rows.
+  constexpr int HALF = D / 2;
+  constexpr int SROW = HALF * 2 + 16;  // padded staging row (bytes)
+  constexpr int ROWS = HT * 16;
+  constexpr int CPR = HALF * 2 / 16;   // 16-byte chunks per staged row
+  constexpr int ITER = ROWS * CPR / 64;
+  static_assert(NW * ROWS * SROW <= NBUF * BUF_BYTES && ITER * 64 == ROWS * CPR, "epilogue staging");
+  typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  unsigned char* stg = smem + wave * (ROWS * SROW);
+  const bool to_out = p.splits == 1;
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+      for (int dq = 0; dq < NDT / 2; ++dq) {
+        const f32x4 v = acc_o[hh * (NDT / 2) + dq][ht] * mul[ht];
+        u16x4 w;
+        if (to_out) {
+          const T4 o = {E::from_f32(v[0]), E::from_f32(v[1]), E::from_f32(v[2]), E::from_f32(v[3])};
+          w = __builtin_bit_cast(u16x4, o);
+        } else {
+          const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+          w = __builtin_bit_cast(u16x4, o);
+        }
+        *(u16x4*)(stg + (ht * 16 + li) * SROW + (dq * 16 + lg * 4) * 2) = w;
+      }
+#pragma unroll
+    for (int i = 0; i < ITER; ++i) {
+      const int c = i * 64 + lane;
+      const int r = c / CPR, col = c % CPR;
+      const u32x4 val = *(const u32x4*)(stg + r * SROW + col * 16);
+      const int head = head0 + r;
+      if (head < p.n1) {
+        const int64_t orow = row * p.n1 + head;
+        unsigned char* dst = to_out ? (unsigned char*)p.out + orow * (D * 2)
+                                    : (unsigned char*)(p.part_o + ((int64_t)split * p.rows * p.n1 + orow) * D);
+        *(u32x4*)(dst + hh * (HALF * 2) + col * 16) = val;
       }
     }
   }
 }
 
 // Merge per-split partials: one wave per (row, head).  Partial i holds
-// O_i and l_i relative to its reference max r_i and its exact max t_i (log2
-// units); the merged output is sum_i 2^(r_i-M) O_i / sum_i 2^(r_i-M) l_i.
+// O_i / l_i (as scale_i * stored value), l_i relative to its reference max
+// r_i, and its exact max t_i (log2 units); the merged output is
+// sum_i w_i O_i / l_i / sum_i w_i with w_i = 2^(r_i - M) l_i.
 template <int D, typename T>
 __global__ __launch_bounds__(256) void sfa_combine_kernel(SfaFwdParams p) {
   using E = Elem<T>;
@@ -574,11 +660,12 @@ __global__ __launch_bounds__(256) void sfa_combine_kernel(SfaFwdParams p) {
       const int64_t prow = (int64_t)s * p.rows * p.n1 + rh;
       const f32x4 ml = *(const f32x4*)(p.part_ml + prow * 4);
       if (!(ml[1] > 0.f)) continue;
-      const float w = fast_exp2(ml[0] - mref);
-      L += w * ml[1];
-      const float* po = p.part_o + prow * D + lane * PER;
+      const float w = fast_exp2(ml[0] - mref) * ml[1];
+      L += w;
+      const float ws = w * ml[3];
+      const f16* po = p.part_o + prow * D + lane * PER;
 #pragma unroll
-      for (int j = 0; j < PER; ++j) acc[j] += w * po[j];
+      for (int j = 0; j < PER; ++j) acc[j] += ws * (float)po[j];
     }
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -626,17 +713,23 @@ int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
 size_t sfa_fwd_workspace_bytes(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
   const int splits = sfa_fwd_splits(rows, n1, d, total_pos);
   if (splits <= 1) return 0;
-  return (size_t)splits * rows * n1 * (d + 4) * sizeof(float);
+  return (size_t)splits * rows * n1 * (d * sizeof(_Float16) + 4 * sizeof(float));
 }
 
-// Head tiles (of 16 heads) per wave.  D=512 keeps 16 heads per wave (two
-// workgroups per row, on one XCD): 32 heads would need 256 accumulator plus
-// 144 Q-fragment registers, which leaves too little for the pipeline.
-template <int D> struct SfaHT { static constexpr int value = D >= 512 ? 1 : 2; };
+// Waves and head tiles (of 16 heads) per wave; every configuration covers
+// 128 heads per workgroup, so one gathered KV row serves all heads of a row.
+// D=512 runs two waves per SIMD (8 x 16 heads): LDS reads from a single wave
+// per SIMD are latency-bound, and 16 heads keep the O accumulator (128
+// registers) plus Q fragments within the 256 registers of a half SIMD.
+template <int D> struct SfaCfg {
+  static constexpr int NW = D >= 512 ? 8 : 4;
+  static constexpr int HT = D >= 512 ? 1 : 2;
+};
+constexpr int kSfaHeadsPerWg = 128;
 
 int sfa_fwd_head_groups(int64_t n1, int64_t d) {
-  const int heads_per_wg = 4 * 16 * (d >= 512 ? 1 : 2);
-  return (int)((n1 + heads_per_wg - 1) / heads_per_wg);
+  (void)d;
+  return (int)((n1 + kSfaHeadsPerWg - 1) / kSfaHeadsPerWg);
 }
 
 template <int D, typename T>
@@ -645,12 +738,14 @@ static hipError_t launch_sfa_fwd(SfaFwdParams& p, hipStream_t stream) {
   p.rows_per_xcd = (int)rows_per_xcd;
   const int64_t blocks = 8 * rows_per_xcd * p.splits * sfa_fwd_head_groups(p.n1, D);
   const bool buf = p.kv_rows * (int64_t)D * 2 < (1ll << 31);
+  using C = SfaCfg<D>;
+  static_assert(C::NW * C::HT * 16 == kSfaHeadsPerWg, "heads per workgroup");
   if (buf)
-    hipLaunchKernelGGL((sfa_fwd_kernel<D, T, SfaHT<D>::value, true>), dim3((unsigned)blocks),
-                       dim3(kSfaThreads), 0, stream, p);
+    hipLaunchKernelGGL((sfa_fwd_kernel<D, T, C::HT, C::NW, true>), dim3((unsigned)blocks),
+                       dim3(C::NW * 64), 0, stream, p);
   else
-    hipLaunchKernelGGL((sfa_fwd_kernel<D, T, SfaHT<D>::value, false>), dim3((unsigned)blocks),
-                       dim3(kSfaThreads), 0, stream, p);
+    hipLaunchKernelGGL((sfa_fwd_kernel<D, T, C::HT, C::NW, false>), dim3((unsigned)blocks),
+                       dim3(C::NW * 64), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) return e;
   const int64_t cblocks = (p.rows * p.n1 + 3) / 4;
@@ -697,8 +792,8 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
   p.part_o = nullptr;
   p.part_ml = nullptr;
   if (p.splits > 1) {
-    p.part_o = (float*)workspace;
-    p.part_ml = p.part_o + (size_t)p.splits * q_rows * n1 * d;
+    p.part_o = (_Float16*)workspace;
+    p.part_ml = (float*)(p.part_o + (size_t)p.splits * q_rows * n1 * d);
   }
   p.scale_log2 = scale_value * kLog2e;
   p.return_lse = return_lse;
