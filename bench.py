@@ -207,10 +207,12 @@ def main():
                      "algorithmic_flops_per_launch": int(flops)},
     }
     if args.calib_copy:
-        src = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
+        # a plain streaming kernel of known traffic (256 MiB read + 256 MiB
+        # written) with a distinctive name, to scale FETCH_SIZE / WRITE_SIZE
+        src = torch.zeros(1 << 26, dtype=torch.int32, device=dev)
         dst = torch.empty_like(src)
         for _ in range(3):
-            dst.copy_(src)
+            torch.bitwise_not(src, out=dst)
         torch.cuda.synchronize()
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_decode(sets)

@@ -28,6 +28,8 @@
 //  * When there are fewer rows than CUs the row's tokens are split across
 //    workgroups (all on one XCD) and a combine kernel merges the partial
 //    (O, max, sum) triples.
+#include <type_traits>
+
 #include "common.h"
 
 namespace dsa {
@@ -66,7 +68,7 @@ struct SfaFwdParams {
 #endif
 
 constexpr int kSfaTile = 32;
-constexpr int kSfaMaxList = 4096;
+constexpr int kSfaMaxList = 2048;
 constexpr float kRefSlack = 64.f;  // log2 units
 
 struct RowInfo {
@@ -170,9 +172,11 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   constexpr int NBUF = 3;                    // DMA ring: tiles t+1, t+2 in flight during t
   constexpr int CPT = D / 8;                 // 16-byte chunks per nope row
   constexpr int TPI = 64 / CPT;              // nope tokens per wave-wide DMA (1 KB)
-  constexpr int NI = TILE / TPI / NW;        // nope DMAs per wave per tile
+  // Four waves issue the tile loads (all of them with NW = 4, waves 4..7
+  // with NW = 8): NI nope DMAs (1 KB each) plus one rope DMA (8 tokens x
+  // 128 B) per issuing wave per tile.
+  constexpr int NI = TILE / TPI / 4;
   constexpr int NTHR = NW * 64;
-  // + one rope DMA (8 tokens x 128 B) for waves 0..3
   // LDS layout: the NBUF tile buffers are interleaved in 1 KB blocks (one
   // DMA each) so that a buffer index only adds a small immediate to a read
   // address: nope block k (tokens k*TPI..) of buffer b at (k*NBUF + b) KB,
@@ -181,9 +185,17 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   auto nope_off = [](int tk, int b) { return ((tk / TPI) * NBUF + b) * 1024 + (tk % TPI) * (D * 2); };
   auto rope_off = [](int tk, int b) { return ROPE0 + ((tk >> 3) * NBUF + b) * 1024 + (tk & 7) * (DR * 2); };
   static_assert(TILE == 32 && (NW == 4 || NW == 8) && NI >= 1, "tile/wave layout");
+  constexpr int HEADS_PER_WG = NW * HT * 16;
+  constexpr int QL = 4;        // Q k-steps staged in LDS
+  constexpr int KQR = KS - QL; // Q k-steps held in registers
+  static_assert(KQR >= 0 && KS - KSN <= QL, "Q staging covers the rope part");
 
   __shared__ __attribute__((aligned(16))) unsigned char smem[NBUF * BUF_BYTES];
   __shared__ int s_list[kSfaMaxList + kSfaTile];
+  // The last QL k-steps of Q (the rope part and the end of the nope part)
+  // of the workgroup's heads, QL * 64 bytes per head (nope swizzle): read
+  // from LDS by GEMM1's last k-steps instead of held in registers
+  __shared__ __attribute__((aligned(16))) unsigned char s_q[HEADS_PER_WG * QL * 64];
   __shared__ int s_wcnt[NW];
 
   const int tid = threadIdx.x;
@@ -193,7 +205,6 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   const int lg = lane >> 4;  // 16-lane group
 
   // ---- block -> (row, split, head group); a row's blocks share an XCD ----
-  constexpr int HEADS_PER_WG = NW * HT * 16;
   const int hgroups = (p.n1 + HEADS_PER_WG - 1) / HEADS_PER_WG;
   const int bid = blockIdx.x;
   const int jj = bid >> 3;
@@ -243,30 +254,32 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   // rope: wave w < 4 covers tokens 8w .. 8w+7, lane L -> token 8w + L/8.
   const unsigned smem_base = (unsigned)(uintptr_t)smem;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-  // wave-uniform DMA destinations: nope block (j*NW + wave), rope block (wave & 3)
-  const unsigned smem_wave = smem_base + nope_off(wave_s * TPI, 0);
-  const unsigned smem_rope_wave = smem_base + rope_off((wave_s & 3) * 8, 0) - rope_off(0, 0);
+  const bool issuer = NW == 4 || wave_s >= 4;
+  const int wiss = wave_s & 3;  // index among the issuing waves
+  // wave-uniform DMA destinations: nope block (j*4 + wiss), rope block wiss
+  const unsigned smem_wave = smem_base + nope_off(wiss * TPI, 0);
+  const unsigned smem_rope_wave = smem_base + rope_off(wiss * 8, 0) - rope_off(0, 0);
   __amdgpu_buffer_rsrc_t rsrc_k, rsrc_r;
   if constexpr (BUF) {
     rsrc_k = __builtin_amdgcn_make_buffer_rsrc((void*)p.k, (short)0, (int)(p.kv_rows * D * 2), 0x00020000);
     rsrc_r = __builtin_amdgcn_make_buffer_rsrc((void*)p.kr, (short)0, (int)(p.kv_rows * DR * 2), 0x00020000);
   }
-  // DMA j < NI of a wave loads nope block (j*NW + wave); DMA NI loads rope
-  // block (wave & 3) (with eight waves, waves w and w + 4 load the same rope
-  // block: identical bytes to the same place, which keeps the per-wave DMA
-  // count uniform and the issue code branch-free).  A tile past the end
-  // (phys = -1 everywhere) loads zeros and touches no memory.
+  // DMA j < NI of an issuing wave loads nope block (j*4 + wiss); DMA NI
+  // loads rope block wiss.  A tile past the end (phys = -1 everywhere) loads
+  // zeros and touches no memory.  With one token per nope DMA (D = 512) the
+  // row id is wave-uniform and kept in a scalar register.
   constexpr int NDMA = NI + 1;
   auto dma_phys = [&](int t, bool live, int j) -> int {
-    const int tk = j < NI ? (j * NW + wave) * TPI + lane / CPT : (wave & 3) * 8 + (lane >> 3);
-    const int v = s_list[t * TILE + tk];  // -1 past n_valid / for -1 pages
+    const int tk = j < NI ? (j * 4 + wiss) * TPI + lane / CPT : wiss * 8 + (lane >> 3);
+    int v = s_list[t * TILE + tk];  // -1 past n_valid / for -1 pages
+    if (TPI == 1 && j < NI) v = __builtin_amdgcn_readfirstlane(v);
     return live ? v : -1;
   };
   auto dma_issue = [&](int j, int phys, int b) {
     if (j < NI) {
-      const int tk = (j * NW + wave) * TPI + lane / CPT;
+      const int tk = (j * 4 + wiss) * TPI + lane / CPT;
       const int ch = (lane % CPT) ^ nope_swz(tk);
-      const unsigned dst = smem_wave + nope_off(j * NW * TPI, b);
+      const unsigned dst = smem_wave + nope_off(j * 4 * TPI, b);
       if constexpr (BUF) {
         dma_buf16(dst, phys >= 0 ? phys * (D * 2) + ch * 16 : (int)0x80000000, rsrc_k);
       } else {
@@ -275,7 +288,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
         dma_glb16(dst, src);
       }
     } else {
-      const int tk = (wave & 3) * 8 + (lane >> 3);
+      const int tk = wiss * 8 + (lane >> 3);
       const int ch = (lane & 7) ^ rope_swz(tk);
       const unsigned dst = smem_rope_wave + rope_off(0, b);
       if constexpr (BUF) {
@@ -297,17 +310,27 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
 #pragma unroll
     for (int j = 0; j < NDMA; ++j) dma_issue(j, ph[j], b);
   };
+  // the same for any t: a tile past the end loads zeros
+  auto issue_tile_or_zero = [&](int t, int b) {
+    const bool live = t < n_tiles;
+    int ph[NDMA];
+#pragma unroll
+    for (int j = 0; j < NDMA; ++j) ph[j] = dma_phys(live ? t : 0, live, j);
+#pragma unroll
+    for (int j = 0; j < NDMA; ++j) dma_issue(j, ph[j], b);
+  };
 
   const int head0 = hg * HEADS_PER_WG + wave * HT * 16;
   const bool wave_active = head0 < p.n1;
 
   // Barrier sequence, identical for every wave: per tile one barrier, then
   // one vote barrier, and (only if the vote is set) a second pass of tiles.
-  // Tile t is waited for (vmcnt) before the barrier; tile t+2 is issued
-  // after it, into the buffer tile t-1 used (all waves are past it), spread
-  // over the tile's first product so that the address unit drains while the
-  // MFMAs run.  Every wave issues NDMA loads per tile (zeros past the end).
+  // Tile t is waited for (vmcnt) before its barrier and tile t+2 is issued
+  // after it, into the buffer tile t-1 used (all waves are past it).  Each
+  // issuing wave issues NDMA loads per tile (zeros past the end), so the
+  // vmcnt counts hold; the other waves have none outstanding.
   auto gather_loop_prologue = [&]() {
+    if (!issuer) return;
     if (n_tiles > 0) issue_tile(0, 0);
     if (n_tiles > 1) issue_tile(1, 1);
   };
@@ -319,7 +342,8 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   auto next_buf = [](int b) { return b == 0 ? NBUF - 1 : b - 1; };
 
   if (!wave_active) {
-    // waves without heads (N1 < HEADS_PER_WG) only help with the gather
+    // waves without heads (N1 < HEADS_PER_WG) only take their share of the
+    // gather, with the same barrier and load sequence as the other waves
     auto gather_only = [&]() {
       gather_loop_prologue();
       for (int t0 = 0; t0 < n_tiles; t0 += NBUF)
@@ -328,7 +352,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
           const int t = t0 + b;
           if (t >= n_tiles) break;
           tile_sync(t);
-          if (t + 2 < n_tiles) issue_tile(t + 2, next_buf(b));
+          if (issuer) issue_tile_or_zero(t + 2, next_buf(b));
         }
       wait_vmcnt<0>();
     };
@@ -338,20 +362,43 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   }
 
   // ---- Q fragments (B operand of S^T = K.Q^T): lane -> head li, k = 8*lg.. ----
-  V8 qf[HT][KS];
+  // Q fragments: k-steps < KQR in registers, the last QL in LDS (loaded
+  // first, stored to LDS once the register part's loads are out)
+  V8 qf[HT][KQR > 0 ? KQR : 1];
+  u32x4 qlv[HT][QL];
+  const u32x4 z4 = {0u, 0u, 0u, 0u};
+  auto q_chunk = [&](int64_t hsafe, int ks) -> u32x4 {
+    if (ks < KSN) return *(const u32x4*)((const T*)p.q + hsafe * D + ks * 32 + lg * 8);
+    return *(const u32x4*)((const T*)p.qr + hsafe * DR + (ks - KSN) * 32 + lg * 8);
+  };
 #pragma unroll
   for (int ht = 0; ht < HT; ++ht) {
     const int head = head0 + ht * 16 + li;
     const bool hv = head < p.n1;
     const int64_t hsafe = row * p.n1 + (hv ? head : 0);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      u32x4 v;
-      if (ks < KSN) v = *(const u32x4*)((const T*)p.q + hsafe * D + ks * 32 + lg * 8);
-      else v = *(const u32x4*)((const T*)p.qr + hsafe * DR + (ks - KSN) * 32 + lg * 8);
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      qf[ht][ks] = as_v8<V8>(hv ? v : z);
-    }
+    for (int m = 0; m < QL; ++m) qlv[ht][m] = hv ? q_chunk(hsafe, KQR + m) : z4;
+  }
+#pragma unroll
+  for (int ht = 0; ht < HT; ++ht) {
+    const int head = head0 + ht * 16 + li;
+    const bool hv = head < p.n1;
+    const int64_t hsafe = row * p.n1 + (hv ? head : 0);
+#pragma unroll
+    for (int ks = 0; ks < KQR; ++ks) qf[ht][ks] = as_v8<V8>(hv ? q_chunk(hsafe, ks) : z4);
+  }
+  // staged Q fragment (head li of head tile ht, chunk 4m + lg) at
+  // ql_base ^ (m << 6) + ht * (16 * QL * 64)
+  auto ql_base = [&](int ln) {
+    const int l = ln & 15, g = ln >> 4;
+    return (wave_s * HT * 16 + l) * (QL * 64) + ((g ^ nope_swz(l)) * 16);
+  };
+  {
+    const int qb = ql_base(lane);
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht)
+#pragma unroll
+      for (int m = 0; m < QL; ++m) *(u32x4*)(s_q + ((qb ^ (m << 6)) + ht * (16 * QL * 64))) = qlv[ht][m];
   }
 
   f32x4 acc_o[NDT][HT];
@@ -381,68 +428,93 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   // sit a constant distance further on.  The XORs are recomputed per tile
   // from one base each (the bases are re-derived through an empty asm so the
   // compiler cannot hoist fourteen loop-invariant addresses into registers).
-  const int g1_0 = nope_off(li, 0) + ((lg ^ nope_swz(li)) * 16);
-  const int g1r_0 = rope_off(li, 0) + ((lg ^ rope_swz(li)) * 16);
+  // The per-lane bases are recomputed from the lane id at every use (a few
+  // VALU ops): kept live across the tile loop they would be spilled, and a
+  // spill reload waits for all outstanding loads, the tile DMAs included.
+  auto fresh_lane = []() {
+    int ln = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    asm volatile("" : "+v"(ln));
+    return ln;
+  };
+  auto g1_base = [&](int ln) { const int l = ln & 15, g = ln >> 4; return nope_off(l, 0) + ((g ^ nope_swz(l)) * 16); };
+  auto g1r_base = [&](int ln) { const int l = ln & 15, g = ln >> 4; return rope_off(l, 0) + ((g ^ rope_swz(l)) * 16); };
   constexpr int G1_TT = nope_off(16, 0) - nope_off(0, 0);
   constexpr int G1R_TT = rope_off(16, 0) - rope_off(0, 0);
   // GEMM2 transposed reads: row r1 = 4*lg + li/4 (and r1 + 16, same swizzle),
   // chunk dt*2 + (li&3)/2, 8-byte half (li&1): chunk (2m | h) ^ swz is at
   // g2 ^ (m << 5) for m = dt mod 8, plus 256 bytes per further eight d-tiles.
-  const int g2_0 = [&]() {
-    const int r1 = lg * 4 + (li >> 2);
-    const int h = (li & 3) >> 1;
-    return nope_off(r1, 0) + ((h ^ nope_swz(r1)) * 16) + (li & 1) * 8;
-  }();
+  auto g2_base = [&](int ln) {
+    const int l = ln & 15, g = ln >> 4;
+    const int r1 = g * 4 + (l >> 2);
+    const int h = (l & 3) >> 1;
+    return nope_off(r1, 0) + ((h ^ nope_swz(r1)) * 16) + (l & 1) * 8;
+  };
   constexpr int G2_ROW16 = (16 / TPI) * NBUF * 1024;  // row r1 -> r1 + 16
   constexpr int NS1 = KS * 2;  // GEMM1 steps (k-step x token tile)
   // fragments in flight: with two waves per SIMD the other wave covers LDS
   // latency, and the registers are needed for the accumulators
-  constexpr int PF1 = NW == 8 ? 2 : (HT == 1 ? 8 : 4);  // GEMM1
-  constexpr int PF2 = NW == 8 ? 2 : (HT == 1 ? 8 : (D >= 512 ? 2 : 4));  // GEMM2
+  constexpr int PF1 = NW == 8 ? 4 : (HT == 1 ? 8 : 4);  // GEMM1
+  constexpr int PF2 = NW == 8 ? 4 : (HT == 1 ? 8 : (D >= 512 ? 2 : 4));  // GEMM2
 
-  auto compute_tile = [&](int t, int b) {
-    int g1b = g1_0, g1rb = g1r_0, g2b = g2_0;
-    asm volatile("" : "+v"(g1b), "+v"(g1rb), "+v"(g2b));
-    auto a1 = [&](int st) -> u32x4 {
-      const int ks = st >> 1, tt = st & 1;
-      if (ks < KSN) return *(const u32x4*)(smem + ((g1b ^ ((ks & 3) << 6)) + tt * G1_TT + b * 1024 + (ks >> 2) * 256));
-      return *(const u32x4*)(smem + ((g1rb ^ ((ks - KSN) << 6)) + tt * G1R_TT + b * 1024));
-    };
-    auto a2 = [&](int dt) -> V8 {
-      const unsigned char* p1 = smem + ((g2b ^ ((dt & 7) << 5)) + b * 1024 + (dt >> 3) * 256);
-      const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1);
-      const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p1 + G2_ROW16));
-      const i16x4 w1 = __builtin_bit_cast(i16x4, v1);
-      const i16x4 w2 = __builtin_bit_cast(i16x4, v2);
-      const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
-      return __builtin_bit_cast(V8, w);
-    };
-
-    // s_list entries of tile t+2 for this wave's DMAs
-    const bool pf_live = t + 2 < n_tiles;
-    int dph[NDMA];
+  // LDS fragment readers for buffer b
+  auto a1 = [&](int g1b, int g1rb, int b, int st) -> u32x4 {
+    const int ks = st >> 1, tt = st & 1;
+    if (ks < KSN) return *(const u32x4*)(smem + ((g1b ^ ((ks & 3) << 6)) + tt * G1_TT + b * 1024 + (ks >> 2) * 256));
+    return *(const u32x4*)(smem + ((g1rb ^ ((ks - KSN) << 6)) + tt * G1R_TT + b * 1024));
+  };
+  auto a2 = [&](int g2b, int b, int dt) -> V8 {
+    const unsigned char* p1 = smem + ((g2b ^ ((dt & 7) << 5)) + b * 1024 + (dt >> 3) * 256);
+    const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1);
+    const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p1 + G2_ROW16));
+    const i16x4 w1 = __builtin_bit_cast(i16x4, v1);
+    const i16x4 w2 = __builtin_bit_cast(i16x4, v2);
+    const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
+    return __builtin_bit_cast(V8, w);
+  };
+  // s_list entries of tile tn (zeros past the end) for this wave's DMAs
+  auto dma_plan = [&](int tn, int (&dph)[NDMA]) {
+    const bool live = tn < n_tiles;
 #pragma unroll
-    for (int j = 0; j < NDMA; ++j) dph[j] = dma_phys(pf_live ? t + 2 : 0, pf_live, j);
-    const int nb = next_buf(b);
-    static_assert(2 + 4 * (NDMA - 1) < NS1, "DMA slots inside GEMM1");
+    for (int j = 0; j < NDMA; ++j) dph[j] = dma_phys(live ? tn : 0, live, j);
+  };
 
-    // ---- GEMM1: S^T[32 tok x HT*16 heads], fragments PF1 steps ahead ----
-    f32x4 acc_s[2][HT];
+  // ---- GEMM1 of tile t (buffer b): S^T[32 tok x HT*16 heads] ----
+  // With DMA, this wave's loads of tile tn into buffer bn go out one every
+  // four steps, so that the address unit drains while the MFMAs run.
+  auto gemm1 = [&](int t, int b, f32x4 (&acc_s)[2][HT], auto with_dma, int tn, int bn) {
+    const int ln = fresh_lane();
+    const int g1b = g1_base(ln), g1rb = g1r_base(ln), qlb = ql_base(ln);
+    // staged Q fragments, read two k-steps ahead of use
+    V8 ql[HT][QL];
+    auto ql_read = [&](int m) {
+#pragma unroll
+      for (int ht = 0; ht < HT; ++ht)
+        ql[ht][m] = as_v8<V8>(*(const u32x4*)(s_q + ((qlb ^ (m << 6)) + ht * (16 * QL * 64))));
+    };
+    constexpr bool kDma = decltype(with_dma)::value;
+    int dph[NDMA];
+    if constexpr (kDma) dma_plan(tn, dph);
+    static_assert(2 + 4 * (NDMA - 1) < NS1, "DMA slots inside GEMM1");
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) acc_s[tt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
     u32x4 fa[PF1];
 #pragma unroll
-    for (int i = 0; i < PF1; ++i) fa[i] = a1(i);
+    for (int i = 0; i < PF1; ++i) fa[i] = a1(g1b, g1rb, b, i);
+#pragma unroll
+    for (int m = 0; m < QL && KQR + m < 2; ++m) ql_read(m);
 #pragma unroll
     for (int st = 0; st < NS1; ++st) {
       const int ks = st >> 1, tt = st & 1;
+      if (tt == 0 && ks + 2 >= KQR && ks + 2 < KS && ks + 2 - KQR >= 0) ql_read(ks + 2 - KQR);
       const V8 av = as_v8<V8>(fa[st % PF1]);
-      if (st + PF1 < NS1) fa[st % PF1] = a1(st + PF1);
+      if (st + PF1 < NS1) fa[st % PF1] = a1(g1b, g1rb, b, st + PF1);
 #pragma unroll
-      for (int ht = 0; ht < HT; ++ht) acc_s[tt][ht] = E::mfma(av, qf[ht][ks], acc_s[tt][ht]);
-      if ((st & 3) == 2 && (st >> 2) < NDMA) dma_issue(st >> 2, dph[st >> 2], nb);
+      for (int ht = 0; ht < HT; ++ht)
+        acc_s[tt][ht] = E::mfma(av, ks < KQR ? qf[ht][ks < KQR ? ks : 0] : ql[ht][ks < KQR ? 0 : ks - KQR], acc_s[tt][ht]);
+      if constexpr (kDma)
+        if ((st & 3) == 2 && (st >> 2) < NDMA) dma_issue(st >> 2, dph[st >> 2], bn);
     }
 #if DSA_SCHED_GROUPS
     __builtin_amdgcn_sched_group_barrier(0x100, PF1, 0);
@@ -452,12 +524,16 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
       if (st + PF1 < NS1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
 #endif
+  };
+
+  // ---- softmax numerators of tile t and O^T += V^T . P^T (buffer b) ----
+  auto sm_gemm2 = [&](int t, int b, f32x4 (&acc_s)[2][HT]) {
+    const int g2b = g2_base(fresh_lane());
     // first V^T fragments go out before the softmax arithmetic
     V8 fv[PF2];
 #pragma unroll
-    for (int i = 0; i < PF2; ++i) fv[i] = a2(i);
+    for (int i = 0; i < PF2; ++i) fv[i] = a2(g2b, b, i);
 
-    // ---- softmax numerators (log2 domain) as P^T fragments ----
     // P^T is split into bf16 hi + lo parts for bf16 I/O (fp16 keeps 11 bits
     // in one part): the P.V product then carries ~16 bits of P, so its error
     // is that of the final output rounding.
@@ -496,11 +572,10 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
       pf_lo[ht] = lo;
     }
 
-    // ---- GEMM2: O^T[D x HT*16 heads] += V^T . P^T, fragments PF2 ahead ----
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       const V8 av = fv[dt % PF2];
-      if (dt + PF2 < NDT) fv[dt % PF2] = a2(dt + PF2);
+      if (dt + PF2 < NDT) fv[dt % PF2] = a2(g2b, b, dt + PF2);
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) {
         acc_o[dt][ht] = E::mfma(av, pf[ht], acc_o[dt][ht]);
@@ -516,16 +591,27 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
 #endif
   };
 
+  using DmaOff = std::integral_constant<bool, false>;
+  using DmaSpread = std::integral_constant<bool, true>;
+
+  // Tile t: wait for its loads, barrier, GEMM1 (the issuing waves load tile
+  // t+2 into the buffer tile t-1 used, one DMA every four steps: every
+  // workgroup runs the same schedule, and bursts would queue at the memory
+  // system), softmax, GEMM2.  (A two-group ping-pong schedule, GEMM1 of one
+  // group beside softmax + GEMM2 of the other, measured slower here: the
+  // per-wave LDS read rate, not MFMA issue, bounds each phase.)
   auto run_tiles = [&]() {
     gather_loop_prologue();
-    // unrolled by the ring size so every copy has a constant LDS buffer
     for (int t0 = 0; t0 < n_tiles; t0 += NBUF)
 #pragma unroll
       for (int b = 0; b < NBUF; ++b) {
         const int t = t0 + b;
         if (t >= n_tiles) break;
         tile_sync(t);
-        compute_tile(t, b);
+        f32x4 sc[2][HT];
+        if (issuer) gemm1(t, b, sc, DmaSpread{}, t + 2, next_buf(b));
+        else gemm1(t, b, sc, DmaOff{}, 0, 0);
+        sm_gemm2(t, b, sc);
       }
     wait_vmcnt<0>();  // tail loads of tiles past the end
   };
