@@ -163,6 +163,17 @@ def cpu_baseline_decode(sets):
                       f"{dt:.2f} s"}
 
 
+def measured_traffic():
+    """HBM bytes per step from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (scaled by a copy kernel of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "sfa_fwd_decode_traffic.json")
+    try:
+        with open(path) as f:
+            return int(json.load(f)["traffic_bytes_per_step"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -201,10 +212,13 @@ def main():
         "per_step_ms": {"median": round(per[len(per) // 2], 5), "p20": round(per[len(per) // 5], 5),
                         "p80": round(per[4 * len(per) // 5], 5)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "sfa_fwd_kernel + sfa_combine_kernel",
+                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "traffic": measured_traffic(),
+                     "kernel": "sfa_fwd_kernel + sfa_combine_kernel (one step)",
                      "algorithmic_bytes_per_launch": int(nbytes),
-                     "algorithmic_flops_per_launch": int(flops)},
+                     "algorithmic_flops_per_launch": int(flops),
+                     "mfma_tflops": round(tflops, 2),
+                     "mfma_frac_of_bf16_peak": round(tflops / PEAK_BF16_TFLOPS, 4)},
     }
     if args.calib_copy:
         # a plain streaming kernel of known traffic (256 MiB read + 256 MiB
