@@ -48,6 +48,23 @@ SIGNATURES = {
         _vp, _sz, _vp,                        # workspace, workspace_bytes, stream
     ]),
     "dsa_sfa_fwd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32]),
+    "dsa_li_fwd": (_c.c_int, [
+        _vp, _vp, _vp, _i32p, _i32p,          # query, key, weights, actual_seq_q, actual_seq_k
+        _i32p, _vp,                           # sparse_indices, sparse_values
+        _i64, _i64, _i64, _i64, _i64, _i64,   # batch, s1, s2, n1, n2, d
+        _i64, _i64, _i64,                     # sparse_count, q_rows, k_rows
+        _i32, _i32, _i32, _i32, _i32, _i32,   # sparse_mode, layout_q, layout_k, dtype, w_dtype, return_value
+        _vp, _sz, _vp,                        # workspace, workspace_bytes, stream
+    ]),
+    "dsa_li_fwd_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "dsa_li_scores": (_c.c_int, [
+        _vp, _vp, _vp, _i32p, _i32p, _vp,     # query, key, weights, actual_seq_q, actual_seq_k, scores
+        _i64, _i64, _i64, _i64, _i64, _i64,   # batch, s1, s2, n1, n2, d
+        _i64, _i64,                           # q_rows, k_rows
+        _i32, _i32, _i32, _i32, _i32,         # sparse_mode, layout_q, layout_k, dtype, w_dtype
+        _vp,                                  # stream
+    ]),
+    "dsa_li_topk_from_scores": (_c.c_int, [_vp, _i64, _i64, _i64, _i32p, _vp, _vp]),
 }
 
 _lib = None

@@ -20,6 +20,7 @@ BUILD_DIR = os.path.join(ROOT, "_build")
 SOURCES = [
     "capi.cpp",
     "sfa_fwd.hip",
+    "li_fwd.hip",
 ]
 
 ARCH = os.environ.get("DSA_OFFLOAD_ARCH", "gfx950")

@@ -36,7 +36,56 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
                 int32_t sparse_mode, int32_t layout_query, int32_t layout_kv, int32_t dtype,
                 float scale_value, int32_t return_lse, void* workspace, hipStream_t stream);
 
+// li_fwd.hip
+int li_scores_run(const void* query, const void* key, const void* weights, const int32_t* act_q,
+                  const int32_t* act_k, float* scores, int64_t batch, int64_t s1, int64_t s2,
+                  int64_t n1, int64_t n2, int64_t d, int64_t q_rows, int64_t k_rows,
+                  int32_t sparse_mode, int32_t layout_q, int32_t layout_k, int32_t dtype,
+                  int32_t w_dtype, hipStream_t stream);
+int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_t* indices,
+                void* values, int32_t val_dtype, hipStream_t stream);
+constexpr int64_t kLiMaxK = 4096;
+
 static bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+// shared validation of the indexer score inputs
+static int li_check_scores(const void* query, const void* key, const void* weights,
+                           const int32_t* act_q, const int32_t* act_k, int64_t batch, int64_t s1,
+                           int64_t s2, int64_t n1, int64_t n2, int64_t d, int64_t q_rows,
+                           int64_t k_rows, int32_t sparse_mode, int32_t layout_q,
+                           int32_t layout_k, int32_t dtype, int32_t w_dtype) {
+  DSA_CHECK_ARG(query && key && weights, "null tensor pointer");
+  DSA_CHECK_SUPPORTED(d == 64 || d == 128 || d == 256, "head dim D must be one of (64, 128, 256), got %lld",
+                      (long long)d);
+  DSA_CHECK_ARG(n2 >= 1 && n1 >= 1, "N1 and N2 must be >= 1");
+  DSA_CHECK_ARG(n1 % n2 == 0, "N1(%lld) must be divisible by N2(%lld)", (long long)n1, (long long)n2);
+  DSA_CHECK_SUPPORTED(n1 / n2 <= 128, "N1/N2 (query heads per key head) must be <= 128, got %lld",
+                      (long long)(n1 / n2));
+  DSA_CHECK_SUPPORTED(sparse_mode == 0 || sparse_mode == 3,
+                      "Only sparse_mode 0 (full) / 3 (rightDownCausal) supported");
+  DSA_CHECK_SUPPORTED(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_FP16,
+                      "query/key dtype must be bfloat16 or float16");
+  DSA_CHECK_SUPPORTED(w_dtype == DSA_DTYPE_BF16 || w_dtype == DSA_DTYPE_FP16 || w_dtype == DSA_DTYPE_FP32,
+                      "weights dtype must be bfloat16, float16 or float32");
+  DSA_CHECK_SUPPORTED(layout_q == DSA_LAYOUT_BSND || layout_q == DSA_LAYOUT_TND,
+                      "layout_query must be BSND or TND");
+  DSA_CHECK_SUPPORTED(layout_k == DSA_LAYOUT_BSND || layout_k == DSA_LAYOUT_TND,
+                      "layout_key must be BSND or TND (block_table / PA_BSND is not supported)");
+  DSA_CHECK_ARG(!(layout_q == DSA_LAYOUT_BSND && layout_k == DSA_LAYOUT_TND),
+                "a TND key needs a TND query");
+  DSA_CHECK_ARG(batch >= 1 && batch <= (1 << 24), "batch must be >= 1");
+  DSA_CHECK_ARG(s2 >= 1 && s2 <= 65535ll * 1024, "S2 must be in [1, 67107840]");
+  if (layout_q == DSA_LAYOUT_TND) {
+    DSA_CHECK_ARG(act_q && act_k, "TND layout requires cumulative actual_seq_lengths_query and _key");
+    DSA_CHECK_ARG(q_rows >= 1, "TND query must have at least one row");
+  } else {
+    DSA_CHECK_ARG(s1 >= 1 && q_rows == batch * s1, "q_rows must equal B*S1 for BSND query");
+  }
+  if (layout_k == DSA_LAYOUT_BSND) DSA_CHECK_ARG(k_rows == batch * s2, "k_rows must equal B*S2 for BSND key");
+  DSA_CHECK_ARG(k_rows >= 1 && k_rows < (1ll << 31), "key must have between 1 and 2^31-1 rows");
+  DSA_CHECK_ARG(q_rows * n2 < (1ll << 31), "too many query rows");
+  return DSA_OK;
+}
 
 }  // namespace dsa
 
@@ -116,6 +165,67 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, cons
                      sparse_count, q_rows, kv_rows, max_blocks, page_size, sparse_block_size,
                      sparse_mode, layout_query, layout_kv, dtype, scale_value, return_lse,
                      workspace, (hipStream_t)stream);
+}
+
+size_t dsa_li_fwd_workspace_size(int64_t q_rows, int64_t n2, int64_t s2) {
+  if (q_rows <= 0 || n2 <= 0 || s2 <= 0) return 0;
+  return (size_t)q_rows * n2 * s2 * sizeof(float);
+}
+
+int dsa_li_scores(const void* query, const void* key, const void* weights, const int32_t* actual_seq_q,
+                  const int32_t* actual_seq_k, float* scores, int64_t batch, int64_t s1, int64_t s2,
+                  int64_t n1, int64_t n2, int64_t d, int64_t q_rows, int64_t k_rows,
+                  int32_t sparse_mode, int32_t layout_query, int32_t layout_key, int32_t dtype,
+                  int32_t weights_dtype, void* stream) {
+  g_err[0] = '\0';
+  int st = li_check_scores(query, key, weights, actual_seq_q, actual_seq_k, batch, s1, s2, n1, n2, d,
+                           q_rows, k_rows, sparse_mode, layout_query, layout_key, dtype, weights_dtype);
+  if (st != DSA_OK) return st;
+  DSA_CHECK_ARG(scores, "null scores pointer");
+  return li_scores_run(query, key, weights, actual_seq_q, actual_seq_k, scores, batch, s1, s2, n1, n2,
+                       d, q_rows, k_rows, sparse_mode, layout_query, layout_key, dtype, weights_dtype,
+                       (hipStream_t)stream);
+}
+
+int dsa_li_topk_from_scores(const float* scores, int64_t rows, int64_t s2, int64_t sparse_count,
+                            int32_t* indices, float* values, void* stream) {
+  g_err[0] = '\0';
+  DSA_CHECK_ARG(scores && indices, "null tensor pointer");
+  DSA_CHECK_ARG(rows >= 0 && rows < (1ll << 31), "rows out of range");
+  DSA_CHECK_ARG(s2 >= 1 && s2 < (1ll << 31), "S2 must be >= 1");
+  DSA_CHECK_SUPPORTED(sparse_count >= 1 && sparse_count <= kLiMaxK,
+                      "sparse_count must be in [1, %lld], got %lld", (long long)kLiMaxK,
+                      (long long)sparse_count);
+  return li_topk_run(scores, rows, s2, sparse_count, indices, values, DSA_DTYPE_FP32, (hipStream_t)stream);
+}
+
+int dsa_li_fwd(const void* query, const void* key, const void* weights, const int32_t* actual_seq_q,
+               const int32_t* actual_seq_k, int32_t* sparse_indices, void* sparse_values,
+               int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t n2, int64_t d,
+               int64_t sparse_count, int64_t q_rows, int64_t k_rows, int32_t sparse_mode,
+               int32_t layout_query, int32_t layout_key, int32_t dtype, int32_t weights_dtype,
+               int32_t return_value, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = '\0';
+  int st = li_check_scores(query, key, weights, actual_seq_q, actual_seq_k, batch, s1, s2, n1, n2, d,
+                           q_rows, k_rows, sparse_mode, layout_query, layout_key, dtype, weights_dtype);
+  if (st != DSA_OK) return st;
+  DSA_CHECK_ARG(sparse_indices, "null sparse_indices pointer");
+  DSA_CHECK_ARG(!return_value || sparse_values, "return_value requires a sparse_values buffer");
+  DSA_CHECK_SUPPORTED(sparse_count >= 1 && sparse_count <= kLiMaxK,
+                      "sparse_count must be in [1, %lld], got %lld", (long long)kLiMaxK,
+                      (long long)sparse_count);
+  const size_t need = dsa_li_fwd_workspace_size(q_rows, n2, s2);
+  if (workspace == nullptr || workspace_bytes < need) {
+    set_error("workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    return DSA_ERR_WORKSPACE;
+  }
+  float* scores = (float*)workspace;
+  st = li_scores_run(query, key, weights, actual_seq_q, actual_seq_k, scores, batch, s1, s2, n1, n2, d,
+                     q_rows, k_rows, sparse_mode, layout_query, layout_key, dtype, weights_dtype,
+                     (hipStream_t)stream);
+  if (st != DSA_OK) return st;
+  return li_topk_run(scores, q_rows * n2, s2, sparse_count, sparse_indices,
+                     return_value ? sparse_values : nullptr, dtype, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -1,0 +1,479 @@
+// Lightning indexer for gfx950: MFMA score kernel + stable radix top-k.
+//
+// Semantics follow the reference score kernel
+// `_lightning_indexer_score_kernel` (lightning_indexer_triton.py:147-280) and
+// the stable top-k the readme specifies (readme.md:63-69; `_stable_topk`,
+// lightning_indexer_triton.py:339-357):
+//   score[b, s1, n2, s2] = sum_g max(q[b,s1,n2*G+g,:] . k[b,s2,n2,:], 0) * w[b,s1,n2*G+g]
+// in fp32 with no scale (264-269); keys s2 >= act_k are masked (274); in
+// sparse_mode 3 keys s2 >= min(max(act_k-act_q+s1+1, 0), S2) are masked
+// (219-224, 272-273); rows with s1 >= act_q see nothing (227, 275-276).
+// Masked entries are -inf.  The top-k order is score descending, index
+// ascending on ties; -inf entries (and padding when fewer than K keys are
+// visible) are reported as index -1 with value -inf.
+//
+// Score kernel: one workgroup per (query row, n2, chunk of keys).  The G
+// heads of the row live in registers as MFMA A operands (16 heads x 32 d per
+// fragment); K fragments (32 d x 16 keys) are loaded straight from HBM as B
+// operands, 16 bytes per lane, two groups ahead, so the kernel streams K at
+// the memory rate (decode is HBM-bound: 64 flop per key byte at G=64, D=128).
+// C[head][key] is reduced over heads after ReLU and weighting: lane-local
+// over registers and head tiles, then a 4-lane butterfly.
+//
+// Top-k kernel: one workgroup (1024 threads) per row.  Scores map to
+// order-preserving uint32 keys; four 8-bit radix passes find the K-th
+// largest key T among the finite scores and how many entries equal to T are
+// taken (the lowest indices: an ordered block scan, no atomics), the
+// selected (key, index) pairs are bitonic-sorted in LDS on the composite
+// (~key << 32 | index), which is exactly score descending / index ascending.
+#include <type_traits>
+
+#include "common.h"
+
+namespace dsa {
+
+// ---------------------------------------------------------------------------
+// score kernel
+// ---------------------------------------------------------------------------
+struct LiParams {
+  const void* q;
+  const void* k;
+  const void* w;
+  const int32_t* act_q;
+  const int32_t* act_k;
+  float* scores;       // [q_rows * n2, s2] (row stride s2)
+  int64_t q_rows, k_rows;
+  int32_t batch, s1, s2, n1, n2, g;
+  int32_t mode, layout_q, layout_k, w_dtype;
+  int32_t chunk;       // keys per workgroup
+};
+
+constexpr int kLiThreads = 256;
+constexpr int kLiChunk = 1024;
+
+struct LiRow {
+  int b, s1, lim;       // visible keys are [0, lim)
+  int64_t k_base;       // first key row of batch b
+};
+
+__device__ __forceinline__ LiRow li_row_info(const LiParams& p, int row) {
+  LiRow r;
+  int aq, ak;
+  if (p.layout_q == DSA_LAYOUT_TND) {
+    int lo = 0, hi = p.batch - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (p.act_q[mid] > row) hi = mid; else lo = mid + 1;
+    }
+    r.b = lo;
+    const int start = lo ? p.act_q[lo - 1] : 0;
+    r.s1 = row - start;
+    aq = p.act_q[lo] - start;
+  } else {
+    r.b = row / p.s1;
+    r.s1 = row - r.b * p.s1;
+    aq = p.act_q ? p.act_q[r.b] : p.s1;
+  }
+  if (p.layout_k == DSA_LAYOUT_TND || p.layout_q == DSA_LAYOUT_TND) {
+    // with a TND query both length arrays are cumulative (the reference
+    // converts both, lightning_indexer_triton.py:500-506)
+    const int start = r.b ? p.act_k[r.b - 1] : 0;
+    r.k_base = p.layout_k == DSA_LAYOUT_TND ? (int64_t)start : (int64_t)r.b * p.s2;
+    ak = p.act_k[r.b] - start;
+  } else {
+    r.k_base = (int64_t)r.b * p.s2;
+    ak = p.act_k ? p.act_k[r.b] : p.s2;
+  }
+  int lim;
+  if (r.s1 >= aq) lim = 0;
+  else if (p.mode == 3) lim = min(ak, min(max(ak - aq + r.s1 + 1, 0), p.s2));
+  else lim = min(ak, p.s2);
+  r.lim = max(lim, 0);
+  return r;
+}
+
+__device__ __forceinline__ float li_load_w(const LiParams& p, int64_t idx) {
+  if (p.w_dtype == DSA_DTYPE_FP32) return ((const float*)p.w)[idx];
+  if (p.w_dtype == DSA_DTYPE_BF16) return (float)((const bf16*)p.w)[idx];
+  return (float)((const f16*)p.w)[idx];
+}
+
+// D = head dim, GT = head tiles of 16 (G <= 16*GT)
+template <int D, typename T, int GT>
+__global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
+  using E = Elem<T>;
+  using V8 = typename E::v8;
+  constexpr int KS = D / 32;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int rn = blockIdx.x;  // row * n2 + n2 index
+  const int row = rn / p.n2;
+  const int kh = rn - row * p.n2;
+  const LiRow ri = li_row_info(p, row);
+  const int c0 = blockIdx.y * p.chunk;
+  const int c1 = min(p.s2, c0 + p.chunk);
+  float* srow = p.scores + (int64_t)rn * p.s2;
+  if (c0 >= ri.lim) {
+    // nothing visible in this chunk
+    for (int j = c0 + threadIdx.x; j < c1; j += kLiThreads) srow[j] = -INFINITY;
+    return;
+  }
+
+  // Q fragments (A operand): lane -> head ht*16 + li, d = ks*32 + 8*lg ..
+  V8 qf[GT][KS];
+  float wv[GT][4];  // weight of head ht*16 + 4*lg + r (C-layout rows of this lane)
+#pragma unroll
+  for (int ht = 0; ht < GT; ++ht) {
+    const int g = ht * 16 + li;
+    const bool gv = g < p.g;
+    const int64_t qrow = (int64_t)row * p.n1 + kh * p.g + (gv ? g : 0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const u32x4 v = *(const u32x4*)((const T*)p.q + qrow * D + ks * 32 + lg * 8);
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      qf[ht][ks] = as_v8<V8>(gv ? v : z);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int gg = ht * 16 + lg * 4 + r;
+      wv[ht][r] = gg < p.g ? li_load_w(p, (int64_t)row * p.n1 + kh * p.g + gg) : 0.f;
+    }
+  }
+
+  // key groups of 16: wave w takes groups w, w+4, ...; K fragment of group
+  // kg (B operand): lane -> key kg*16 + li, d = ks*32 + 8*lg ..
+  const int ngroups = (c1 - c0 + 15) >> 4;
+  const int lastvis = ri.lim - 1;
+  auto kload = [&](int grp, u32x4 (&kf)[KS]) {
+    int key = c0 + grp * 16 + li;
+    key = key < lastvis ? key : lastvis;  // stays in the batch's rows; masked below
+    int64_t krow = ri.k_base + key;
+    krow = krow < p.k_rows ? krow : p.k_rows - 1;  // inconsistent cumulative lengths stay in bounds
+    const T* kp = (const T*)p.k + (krow * p.n2 + kh) * D + lg * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = *(const u32x4*)(kp + ks * 32);
+  };
+  u32x4 kfa[KS], kfb[KS];
+  int grp = wave;
+  if (grp < ngroups) kload(grp, kfa);
+  if (grp + 4 < ngroups) kload(grp + 4, kfb);
+  auto process = [&](int gi, const u32x4 (&kf)[KS]) {
+    f32x4 acc[GT];
+#pragma unroll
+    for (int ht = 0; ht < GT; ++ht) acc[ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const V8 bv = as_v8<V8>(kf[ks]);
+#pragma unroll
+      for (int ht = 0; ht < GT; ++ht) acc[ht] = E::mfma(qf[ht][ks], bv, acc[ht]);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int ht = 0; ht < GT; ++ht)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s += fmaxf(acc[ht][r], 0.f) * wv[ht][r];
+    s = xgroup_sum(s);
+    const int key = c0 + gi * 16 + li;
+    if (lg == 0 && key < c1) srow[key] = key < ri.lim ? s : -INFINITY;
+  };
+  for (; grp < ngroups; grp += 8) {
+    process(grp, kfa);
+    if (grp + 8 < ngroups) kload(grp + 8, kfa);
+    if (grp + 4 < ngroups) {
+      process(grp + 4, kfb);
+      if (grp + 12 < ngroups) kload(grp + 12, kfb);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// top-k kernel
+// ---------------------------------------------------------------------------
+constexpr int kTopkThreads = 1024;
+constexpr int kTopkMaxK = 4096;
+constexpr int kTopkLdsKeys = 16384;  // rows up to this width are kept in LDS
+
+// order-preserving map fp32 -> uint32 (larger score -> larger key); -0.0
+// maps to the key of +0.0, so the two tie as they compare equal
+__device__ __forceinline__ unsigned sort_key(float f) {
+  const unsigned u = __float_as_uint(f == 0.f ? 0.f : f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+constexpr unsigned kNegInfKey = 0x007fffffu;  // sort_key(-inf)
+
+struct TopkParams {
+  const float* scores;  // [rows, s2]
+  int32_t* indices;     // [rows, k]
+  void* values;         // [rows, k] in val_dtype, or null
+  int64_t rows;
+  int32_t s2, k, val_dtype;
+};
+
+// block-wide exclusive scan of one int per thread (1024 threads); returns
+// the exclusive prefix, *total = sum
+__device__ __forceinline__ int block_scan_excl(int v, int* total, int* s_wsum) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) s_wsum[wave] = x;
+  __syncthreads();
+  if (wave == 0) {
+    int t = lane < kTopkThreads / 64 ? s_wsum[lane] : 0;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const int y = __shfl_up(t, o);
+      if (lane >= o) t += y;
+    }
+    if (lane < kTopkThreads / 64) s_wsum[lane] = t;  // inclusive per-wave sums
+  }
+  __syncthreads();
+  const int wbase = wave ? s_wsum[wave - 1] : 0;
+  *total = s_wsum[kTopkThreads / 64 - 1];
+  __syncthreads();
+  return wbase + x - v;
+}
+
+template <bool IN_LDS>
+__global__ __launch_bounds__(kTopkThreads) void li_topk_kernel(TopkParams p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char tk_smem[];
+  unsigned long long* sel = (unsigned long long*)tk_smem;   // kTopkMaxK entries
+  unsigned* hist = (unsigned*)(sel + kTopkMaxK);             // 256
+  int* s_wsum = (int*)(hist + 256);                          // 16
+  unsigned* s_misc = (unsigned*)(s_wsum + 16);               // 4
+  unsigned* s_keys = s_misc + 4;                             // s2 (IN_LDS)
+
+  const int tid = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const float* srow = p.scores + row * (int64_t)p.s2;
+  const int S = p.s2;
+  auto key_at = [&](int j) -> unsigned {
+    if constexpr (IN_LDS) return s_keys[j];
+    return sort_key(srow[j]);
+  };
+  if constexpr (IN_LDS) {
+    for (int j = tid; j < S; j += kTopkThreads) s_keys[j] = sort_key(srow[j]);
+    __syncthreads();
+  }
+
+  // number of finite (visible) entries
+  int nv = 0;
+  for (int j = tid; j < S; j += kTopkThreads) nv += key_at(j) > kNegInfKey ? 1 : 0;
+  int n_valid = 0;
+  (void)block_scan_excl(nv, &n_valid, s_wsum);
+  const int K = p.k;
+  const int take = min(K, n_valid);
+
+  // radix select: T = take-th largest valid key; need = entries == T to take
+  unsigned thr = kNegInfKey;  // with take == n_valid every valid entry (> -inf) is taken
+  int need = 0;
+  if (take > 0 && take < n_valid) {
+    unsigned prefix = 0, pmask = 0;
+    int remaining = take;
+    for (int pass = 0; pass < 4; ++pass) {
+      const int shift = 24 - 8 * pass;
+      if (tid < 256) hist[tid] = 0;
+      __syncthreads();
+      for (int j = tid; j < S; j += kTopkThreads) {
+        const unsigned kk = key_at(j);
+        if (kk > kNegInfKey && (kk & pmask) == prefix) atomicAdd(&hist[(kk >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (tid < 64) {
+        // bins 255..0 in descending order: lane l owns bins 255-4l .. 252-4l
+        unsigned c[4];
+        unsigned loc = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { c[i] = hist[255 - 4 * tid - i]; loc += c[i]; }
+        unsigned incl = loc;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const unsigned y = __shfl_up(incl, o);
+          if (tid >= o) incl += y;
+        }
+        unsigned run = incl - loc;  // count in bins above this lane's
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (run < (unsigned)remaining && run + c[i] >= (unsigned)remaining) {
+            s_misc[0] = 255u - 4u * tid - i;  // digit of the K-th largest
+            s_misc[1] = run;                  // entries in higher bins
+          }
+          run += c[i];
+        }
+      }
+      __syncthreads();
+      const unsigned dgt = s_misc[0];
+      remaining -= (int)s_misc[1];
+      prefix |= dgt << shift;
+      pmask |= 255u << shift;
+      __syncthreads();
+    }
+    thr = prefix;
+    need = remaining;
+  }
+
+  // ordered selection: each thread scans a contiguous index range; entries
+  // > thr are all taken, entries == thr only while their rank < need
+  const int per = (S + kTopkThreads - 1) / kTopkThreads;
+  const int j0 = min(S, tid * per), j1 = min(S, j0 + per);
+  int ngt = 0, neq = 0;
+  for (int j = j0; j < j1; ++j) {
+    const unsigned kk = key_at(j);
+    ngt += kk > thr ? 1 : 0;
+    neq += (need > 0 && kk == thr) ? 1 : 0;
+  }
+  int tot_gt = 0, tot_eq = 0;
+  int off_gt = block_scan_excl(ngt, &tot_gt, s_wsum);
+  int off_eq = block_scan_excl(neq, &tot_eq, s_wsum);
+  for (int j = j0; j < j1; ++j) {
+    const unsigned kk = key_at(j);
+    if (kk > thr) {
+      if (off_gt < take) sel[off_gt] = ((unsigned long long)(~kk) << 32) | (unsigned)j;
+      ++off_gt;
+    } else if (need > 0 && kk == thr) {
+      const int at = tot_gt + off_eq;
+      if (off_eq < need && at < take) sel[at] = ((unsigned long long)(~kk) << 32) | (unsigned)j;
+      ++off_eq;
+    }
+  }
+  const int nsel = min(take, tot_gt + min(tot_eq, need));  // == take
+  int npow = 1;
+  while (npow < max(nsel, 1)) npow <<= 1;
+  for (int i = nsel + tid; i < npow; i += kTopkThreads) sel[i] = ~0ull;
+  __syncthreads();
+
+  // bitonic sort ascending of sel[0, npow)
+  for (int size = 2; size <= npow; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int t = tid; t < (npow >> 1); t += kTopkThreads) {
+        const int i = 2 * t - (t & (stride - 1));
+        const int jj = i + stride;
+        const bool up = (i & size) == 0;
+        const unsigned long long a = sel[i], bq = sel[jj];
+        if ((a > bq) == up) { sel[i] = bq; sel[jj] = a; }
+      }
+      __syncthreads();
+    }
+  }
+
+  // outputs
+  int32_t* irow = p.indices + row * (int64_t)K;
+  for (int i = tid; i < K; i += kTopkThreads) {
+    int idx = -1;
+    float v = -INFINITY;
+    if (i < nsel) {
+      idx = (int)(unsigned)(sel[i] & 0xffffffffu);
+      v = srow[idx];  // the score itself (keeps the sign of a zero)
+    }
+    irow[i] = idx;
+    if (p.values) {
+      const int64_t o = row * (int64_t)K + i;
+      if (p.val_dtype == DSA_DTYPE_FP32) ((float*)p.values)[o] = v;
+      else if (p.val_dtype == DSA_DTYPE_BF16) ((bf16*)p.values)[o] = (bf16)v;
+      else ((f16*)p.values)[o] = (f16)v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+size_t li_topk_lds_bytes(int64_t s2) {
+  size_t b = (size_t)kTopkMaxK * 8 + 256 * 4 + 16 * 4 + 4 * 4;
+  if (s2 <= kTopkLdsKeys) b += (size_t)s2 * 4;
+  return b;
+}
+
+int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_t* indices,
+                void* values, int32_t val_dtype, hipStream_t stream) {
+  if (rows <= 0) return DSA_OK;
+  TopkParams p;
+  p.scores = scores;
+  p.indices = indices;
+  p.values = values;
+  p.rows = rows;
+  p.s2 = (int32_t)s2;
+  p.k = (int32_t)k;
+  p.val_dtype = val_dtype;
+  // dynamic LDS above 64 KB needs the per-function limit raised (once)
+  static bool attr_set[2] = {false, false};
+  const size_t lds = li_topk_lds_bytes(s2);
+  if (s2 <= kTopkLdsKeys) {
+    if (!attr_set[1]) {
+      DSA_HIP(hipFuncSetAttribute((const void*)li_topk_kernel<true>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)li_topk_lds_bytes(kTopkLdsKeys)));
+      attr_set[1] = true;
+    }
+    hipLaunchKernelGGL(li_topk_kernel<true>, dim3((unsigned)rows), dim3(kTopkThreads), lds, stream, p);
+  } else {
+    if (!attr_set[0]) {
+      DSA_HIP(hipFuncSetAttribute((const void*)li_topk_kernel<false>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+      attr_set[0] = true;
+    }
+    hipLaunchKernelGGL(li_topk_kernel<false>, dim3((unsigned)rows), dim3(kTopkThreads), lds, stream, p);
+  }
+  DSA_HIP(hipGetLastError());
+  return DSA_OK;
+}
+
+template <int D, typename T, int GT>
+static hipError_t launch_score(const LiParams& p, hipStream_t stream) {
+  const unsigned chunks = (unsigned)((p.s2 + p.chunk - 1) / p.chunk);
+  hipLaunchKernelGGL((li_score_kernel<D, T, GT>), dim3((unsigned)(p.q_rows * p.n2), chunks),
+                     dim3(kLiThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int D, typename T>
+static hipError_t launch_score_g(const LiParams& p, hipStream_t stream) {
+  if (p.g <= 16) return launch_score<D, T, 1>(p, stream);
+  if (p.g <= 32) return launch_score<D, T, 2>(p, stream);
+  if (p.g <= 64) return launch_score<D, T, 4>(p, stream);
+  return launch_score<D, T, 8>(p, stream);
+}
+
+template <typename T>
+static hipError_t launch_score_d(const LiParams& p, int64_t d, hipStream_t stream) {
+  if (d == 64) return launch_score_g<64, T>(p, stream);
+  if (d == 128) return launch_score_g<128, T>(p, stream);
+  return launch_score_g<256, T>(p, stream);
+}
+
+int li_scores_run(const void* query, const void* key, const void* weights, const int32_t* act_q,
+                  const int32_t* act_k, float* scores, int64_t batch, int64_t s1, int64_t s2,
+                  int64_t n1, int64_t n2, int64_t d, int64_t q_rows, int64_t k_rows,
+                  int32_t sparse_mode, int32_t layout_q, int32_t layout_k, int32_t dtype,
+                  int32_t w_dtype, hipStream_t stream) {
+  if (q_rows <= 0 || s2 <= 0) return DSA_OK;
+  LiParams p;
+  p.q = query;
+  p.k = key;
+  p.w = weights;
+  p.act_q = act_q;
+  p.act_k = act_k;
+  p.scores = scores;
+  p.q_rows = q_rows;
+  p.k_rows = k_rows;
+  p.batch = (int32_t)batch;
+  p.s1 = (int32_t)s1;
+  p.s2 = (int32_t)s2;
+  p.n1 = (int32_t)n1;
+  p.n2 = (int32_t)n2;
+  p.g = (int32_t)(n1 / n2);
+  p.mode = sparse_mode;
+  p.layout_q = layout_q;
+  p.layout_k = layout_k;
+  p.w_dtype = w_dtype;
+  p.chunk = kLiChunk;
+  hipError_t e = dtype == DSA_DTYPE_BF16 ? launch_score_d<bf16>(p, d, stream)
+                                         : launch_score_d<f16>(p, d, stream);
+  DSA_HIP(e);
+  return DSA_OK;
+}
+
+}  // namespace dsa

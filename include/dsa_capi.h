@@ -83,6 +83,54 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key,
 size_t dsa_sfa_fwd_workspace_size(int64_t q_rows, int64_t n1, int64_t d,
                                   int64_t sparse_count, int32_t sparse_block_size);
 
+/*
+ * Lightning indexer: scores + stable top-k.  Replaces the reference core
+ * `_lightning_indexer_score_core` (lightning_indexer_triton.py:382-413) and the
+ * top-k after it (`_stable_topk`, 339-357, called at 539), with the stable
+ * order the readme specifies (readme.md:63-69): score descending, index
+ * ascending on ties, -inf entries and padding reported as index -1.
+ *   query [R1, N1, D] (R1 = B*S1 BSND or T1 TND), key [R2, N2, D] (R2 = B*S2
+ *   BSND or T2 TND), weights [R1, N1] (weights_dtype BF16 / FP16 / FP32),
+ *   D in {64, 128, 256}, N1 % N2 == 0, N1/N2 <= 128, dtype BF16 or FP16,
+ *   sparse_mode 0 or 3.  With a TND query both length arrays are cumulative
+ *   (as the reference converts both, 500-506); a TND key needs a TND query.
+ *   For a TND key, s2 is the largest per-batch key length (the width of the
+ *   score rows).
+ * Writes sparse_indices [R1, N2, K] int32 and, when return_value != 0,
+ * sparse_values [R1, N2, K] in the query dtype (-inf where the index is -1).
+ * The workspace holds the fp32 scores [R1*N2, s2].  K <= 4096.
+ */
+int dsa_li_fwd(const void* query, const void* key, const void* weights,
+               const int32_t* actual_seq_q, const int32_t* actual_seq_k,
+               int32_t* sparse_indices, void* sparse_values, int64_t batch, int64_t s1,
+               int64_t s2, int64_t n1, int64_t n2, int64_t d, int64_t sparse_count,
+               int64_t q_rows, int64_t k_rows, int32_t sparse_mode, int32_t layout_query,
+               int32_t layout_key, int32_t dtype, int32_t weights_dtype, int32_t return_value,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of dsa_li_fwd: the fp32 score rows, q_rows * n2 * s2 * 4. */
+size_t dsa_li_fwd_workspace_size(int64_t q_rows, int64_t n2, int64_t s2);
+
+/*
+ * Indexer scores only (the first stage of dsa_li_fwd; the reference's
+ * `_lightning_indexer_score_core`, lightning_indexer_triton.py:382-413):
+ * scores [R1*N2, s2] fp32, -inf where masked.  Arguments as dsa_li_fwd.
+ */
+int dsa_li_scores(const void* query, const void* key, const void* weights,
+                  const int32_t* actual_seq_q, const int32_t* actual_seq_k, float* scores,
+                  int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t n2, int64_t d,
+                  int64_t q_rows, int64_t k_rows, int32_t sparse_mode, int32_t layout_query,
+                  int32_t layout_key, int32_t dtype, int32_t weights_dtype, void* stream);
+
+/*
+ * Stable top-k of fp32 score rows (the second stage of dsa_li_fwd; replaces
+ * `_stable_topk`, lightning_indexer_triton.py:339-357): scores [rows, s2] ->
+ * indices [rows, K] int32 and, if values != NULL, values [rows, K] fp32.
+ * Bit-exact on given scores; K <= 4096; K > s2 pads with -1 / -inf.
+ */
+int dsa_li_topk_from_scores(const float* scores, int64_t rows, int64_t s2, int64_t sparse_count,
+                            int32_t* indices, float* values, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

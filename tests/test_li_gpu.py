@@ -1,0 +1,254 @@
+"""GPU parity of the HIP lightning indexer against the oracle.
+
+* Top-k (``dsa_li_topk_from_scores``): bit-exact against ``oracle.indexer.
+  stable_topk`` on the same fp32 scores (score descending, index ascending on
+  ties, -inf -> -1), including heavy ties, all-masked rows, rows with fewer
+  visible keys than K, K > S2, and rows wider than the LDS-resident limit.
+* Scores (``dsa_li_scores``): against the oracle's fp32 scores; both sum
+  exact bf16 x bf16 products in fp32, in different orders, so the tolerance
+  is a few fp32 ulps of the magnitude of the terms: rtol 1e-5 plus an
+  absolute 1e-5 * sum_g |w_g| * |q_g| * |k| bound.  Masked entries must be
+  -inf at exactly the same places.
+* The full operator (``lightning_indexer_triton``): indices equal to the
+  oracle's top-k of the oracle's scores except at near-ties (two candidates
+  whose oracle scores differ by less than the score tolerance); the number
+  of such tie flips is printed and must be a small fraction.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.indexer import indexer_scores, lightning_indexer, stable_topk
+from tests.helpers import dev, to_dtype_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _api():
+    import dsa_triton_ascend_amd as dsa
+    return dsa
+
+
+def _inputs(B, S1, S2, N1, N2, D, dtype, wdtype=torch.float32, seed=42):
+    rng = np.random.RandomState(seed)
+    q = to_dtype_np(rng.randn(B, S1, N1, D).astype(np.float16).astype(np.float32), dtype)
+    k = to_dtype_np(rng.randn(B, S2, N2, D).astype(np.float16).astype(np.float32), dtype)
+    w = to_dtype_np(rng.rand(B, S1, N1).astype(np.float32), wdtype)
+    return q, k, w
+
+
+# ---------------------------------------------------------------------------
+# top-k
+# ---------------------------------------------------------------------------
+def _topk_gpu(scores_np, k):
+    from dsa_triton_ascend_amd.lightning_indexer import stable_topk as gpu_topk
+    idx, val = gpu_topk(torch.from_numpy(scores_np).cuda(), k)
+    torch.cuda.synchronize()
+    return idx.cpu().numpy(), val.cpu().numpy()
+
+
+@pytest.mark.parametrize("S2,k,kind", [
+    (64, 16, "random"), (300, 64, "ties"), (1000, 2048, "k_gt_s2"), (4096, 2048, "mixed"),
+    (4096, 2048, "ties"), (16384, 2048, "random"), (20000, 2048, "ties"), (32768, 2048, "random"),
+    (32768, 4096, "mixed"), (5000, 1, "ties"), (2049, 2048, "masked_tail"),
+])
+def test_topk_bit_exact(S2, k, kind):
+    print(f"[li topk] S2={S2} k={k} {kind}", flush=True)
+    rng = np.random.RandomState(S2 + k)
+    R = 6
+    if kind == "ties":
+        sc = rng.randint(0, 7, size=(R, S2)).astype(np.float32) * 0.5
+    else:
+        sc = (rng.randn(R, S2) * 10).astype(np.float32)
+    if kind in ("mixed", "masked_tail", "k_gt_s2"):
+        # visible prefixes of different lengths, -inf beyond; one all-masked row
+        lens = [S2, S2 // 2, k - 1, 1, 0, S2 - 3]
+        for r, L in enumerate(lens):
+            sc[r, max(L, 0):] = -np.inf
+    if kind == "mixed":
+        sc[1, :100] = 0.0          # a block of exact ties inside a row
+        sc[5, ::7] = -0.0          # signed zeros tie with +0
+        sc[5, 1::7] = 0.0
+    ie, ve = stable_topk(sc, k)
+    ig, vg = _topk_gpu(sc, k)
+    np.testing.assert_array_equal(ig, ie)
+    # values: identical fp32 (-inf where the index is -1); -0.0 == 0.0 compares equal
+    np.testing.assert_array_equal(vg, ve)
+
+
+# ---------------------------------------------------------------------------
+# scores
+# ---------------------------------------------------------------------------
+def _score_tol(q, k, w, N2):
+    """Per (b, s1, n2, s2) bound on fp32 reassociation error of the score."""
+    B, S1, N1, D = q.shape
+    G = N1 // N2
+    aq = np.abs(q).reshape(B, S1, N2, G, D)
+    ak = np.abs(k)                                   # [B, S2, N2, D]
+    aw = np.abs(w).reshape(B, S1, N2, G)
+    # sum_g |w_g| * sum_d |q_gd||k_d|
+    t = np.einsum("bsngd,btnd->bsnt", aq * aw[..., None], ak)
+    return 1e-5 * t + 1e-6
+
+
+@pytest.mark.parametrize("B,S1,S2,N1,N2,D,mode,dtype,wdtype", [
+    (2, 8, 300, 64, 1, 128, 3, torch.bfloat16, torch.float32),
+    (2, 8, 300, 64, 1, 128, 0, torch.bfloat16, torch.float32),
+    (1, 5, 1100, 32, 2, 64, 3, torch.float16, torch.bfloat16),
+    (2, 3, 257, 8, 1, 256, 0, torch.bfloat16, torch.float16),
+    (1, 4, 2100, 128, 1, 128, 3, torch.bfloat16, torch.float32),
+    (1, 2, 333, 24, 1, 128, 0, torch.float16, torch.float32),
+])
+def test_scores_match_oracle(B, S1, S2, N1, N2, D, mode, dtype, wdtype):
+    print(f"[li scores] B={B} S1={S1} S2={S2} N1={N1} N2={N2} D={D} mode={mode} {dtype}", flush=True)
+    q, k, w = _inputs(B, S1, S2, N1, N2, D, dtype, wdtype)
+    act_q = [S1] * B
+    act_k = [S2 - 7 * b for b in range(B)]
+    if B > 1:
+        act_q[1] = max(1, S1 - 2)
+    e = indexer_scores(q, k, w, act_q, act_k, mode)            # [B,S1,N2,S2]
+    from dsa_triton_ascend_amd.lightning_indexer import indexer_scores as gpu_scores
+    g = gpu_scores(dev(q, dtype), dev(k, dtype), dev(w, wdtype), act_q, act_k, mode)
+    torch.cuda.synchronize()
+    g = g.cpu().numpy().reshape(e.shape)
+    assert np.array_equal(np.isneginf(g), np.isneginf(e)), "masked positions differ"
+    fin = np.isfinite(e)
+    tol = _score_tol(q, k, w, N2)
+    err = np.abs(g[fin] - e[fin])
+    assert np.all(err <= tol[fin] + 1e-5 * np.abs(e[fin])), f"max err {err.max():.3g}"
+
+
+# ---------------------------------------------------------------------------
+# full operator
+# ---------------------------------------------------------------------------
+def _check_topk_with_ties(idx_g, sc_rows, k, score_tol_rows, what):
+    """idx_g [R, k] from the GPU; sc_rows [R, S2] oracle fp32 scores."""
+    ie, _ = stable_topk(sc_rows, k)
+    flips = 0
+    for r in range(ie.shape[0]):
+        if np.array_equal(idx_g[r], ie[r]):
+            continue
+        d = np.nonzero(idx_g[r] != ie[r])[0]
+        for j in d:
+            a, b = idx_g[r, j], ie[r, j]
+            assert a >= 0 and b >= 0, f"{what}: row {r} pos {j}: -1 mismatch ({a} vs {b})"
+            gap = abs(float(sc_rows[r, a]) - float(sc_rows[r, b]))
+            assert gap <= 2 * score_tol_rows[r], f"{what}: row {r} pos {j}: {a} vs {b}, score gap {gap:.3g}"
+        flips += len(d)
+    print(f"  {what}: tie flips {flips} of {idx_g.size} entries", flush=True)
+    assert flips <= max(4, idx_g.size // 500)
+
+
+def _full_case(B, S1, S2, N1, N2, D, k, mode, dtype, rows=None, act_q=None, act_k=None, seed=42):
+    dsa = _api()
+    q, k_, w = _inputs(B, S1, S2, N1, N2, D, dtype, seed=seed)
+    idx, val = dsa.lightning_indexer_triton(
+        dev(q, dtype), dev(k_, dtype), dev(w, torch.float32), act_q, act_k,
+        sparse_count=k, sparse_mode=mode, return_value=True)
+    torch.cuda.synchronize()
+    idx = idx.cpu().numpy()
+    val = val.float().cpu().numpy()
+    aq = [S1] * B if act_q is None else act_q
+    ak = [S2] * B if act_k is None else act_k
+    sc = indexer_scores(q, k_, w, aq, ak, mode, rows=rows)  # [B,S1,N2,S2]
+    G = N1 // N2
+    sel = rows if rows is not None else [(b, s) for b in range(B) for s in range(S1)]
+    for (b, s) in sel:
+        rs = sc[b, s]                                     # [N2, S2]
+        # reassociation bound of each score: 1e-5 * sum_g |w_g| sum_d |q_gd||k_d|
+        a = (np.abs(q[b, s]) * np.abs(w[b, s])[:, None]).reshape(N2, G, D).sum(axis=1)   # [N2, D]
+        t = 1e-5 * np.einsum("nd,tnd->nt", a, np.abs(k_[b])) + 1e-6                       # [N2, S2]
+        _check_topk_with_ties(idx[b, s], rs, k, (np.where(np.isfinite(rs), t, 0.0).max(axis=1)
+                                                 + 1e-5 * np.abs(np.where(np.isfinite(rs), rs, 0)).max()),
+                              f"row ({b},{s})")
+        # values: the query dtype rounding of the score at the returned index
+        for n2 in range(N2):
+            ii = idx[b, s, n2]
+            exp_v = np.where(ii >= 0, rs[n2, np.maximum(ii, 0)], -np.inf)
+            exp_v = to_dtype_np(exp_v, dtype)
+            ok = (ii < 0) | (np.abs(val[b, s, n2] - exp_v) <= 1e-2 * np.abs(exp_v) + 1e-3)
+            assert ok.all() and np.array_equal(np.isneginf(val[b, s, n2]), ii < 0)
+    return idx
+
+
+def test_indexer_small_mode3_hidden_rows():
+    print("[li full] small mode3 with actual lengths", flush=True)
+    idx = _full_case(2, 12, 40, 64, 1, 128, 16, 3, torch.bfloat16, act_q=[12, 9], act_k=[40, 20])
+    # rows s1 >= act_q see nothing: all -1
+    assert (idx[1, 9:] == -1).all()
+    # mode 3: row s1 of batch 1 sees min(max(20 - 9 + s1 + 1, 0), 40) keys
+    for s in range(9):
+        vis = min(max(20 - 9 + s + 1, 0), 20)
+        assert (idx[1, s, 0, :min(vis, 16)] >= 0).all() and (idx[1, s, 0, min(vis, 16):] == -1).all()
+
+
+def test_indexer_gqa_fp16_mode0():
+    print("[li full] gqa fp16 mode0", flush=True)
+    _full_case(1, 6, 700, 32, 2, 64, 64, 0, torch.float16)
+
+
+def test_indexer_cfg2_sampled_rows():
+    """cfg2 (B=2, S1=S2=4096, N1=64, D=128, k=2048, mode 3), 16 sampled rows."""
+    print("[li full] cfg2 sampled rows", flush=True)
+    rng = np.random.RandomState(3)
+    rows = [(int(b), int(s)) for b, s in zip(rng.randint(0, 2, 16), rng.randint(0, 4096, 16))]
+    rows += [(0, 0), (1, 4095), (0, 2047), (1, 2048)]
+    _full_case(2, 4096, 4096, 64, 1, 128, 2048, 3, torch.bfloat16, rows=rows)
+
+
+def test_indexer_decode_32k_sampled_rows():
+    """Decode at 32K context (S1=1, S2=32768, N1=64, D=128, k=2048, mode 3), B=4."""
+    print("[li full] decode 32k", flush=True)
+    _full_case(4, 1, 32768, 64, 1, 128, 2048, 3, torch.bfloat16)
+
+
+def test_indexer_tnd_matches_bsnd():
+    """TND packing (cumulative lengths) gives the per-sequence BSND results."""
+    print("[li full] TND vs BSND", flush=True)
+    dsa = _api()
+    dtype = torch.bfloat16
+    lens_q, lens_k = [5, 9], [30, 50]
+    N1, D, K = 64, 128, 24
+    rng = np.random.RandomState(5)
+    qs = [to_dtype_np(rng.randn(L, N1, D).astype(np.float32), dtype) for L in lens_q]
+    ks = [to_dtype_np(rng.randn(L, 1, D).astype(np.float32), dtype) for L in lens_k]
+    ws = [rng.rand(L, N1).astype(np.float32) for L in lens_q]
+    cq, ck = list(np.cumsum(lens_q)), list(np.cumsum(lens_k))
+    idx_t, val_t = dsa.lightning_indexer_triton(
+        dev(np.concatenate(qs), dtype), dev(np.concatenate(ks), dtype), dev(np.concatenate(ws), torch.float32),
+        cq, ck, layout_query="TND", layout_key="TND", sparse_count=K, sparse_mode=3, return_value=True)
+    torch.cuda.synchronize()
+    idx_t = idx_t.cpu().numpy()
+    exp_i, _ = lightning_indexer(np.concatenate(qs), np.concatenate(ks), np.concatenate(ws), cq, ck,
+                                 layout_query="TND", layout_key="TND", sparse_count=K, sparse_mode=3)
+    # the oracle uses the same scores up to reassociation; these sizes have no near-ties
+    np.testing.assert_array_equal(idx_t, exp_i)
+    off = 0
+    for b in range(2):
+        i_b, _ = dsa.lightning_indexer_triton(
+            dev(qs[b][None], dtype), dev(ks[b][None], dtype), dev(ws[b][None], torch.float32),
+            sparse_count=K, sparse_mode=3)
+        np.testing.assert_array_equal(idx_t[off:off + lens_q[b]], i_b.cpu().numpy()[0])
+        off += lens_q[b]
+
+
+def test_indexer_guards():
+    dsa = _api()
+    q = torch.zeros(1, 2, 8, 128, dtype=torch.bfloat16, device="cuda")
+    k = torch.zeros(1, 4, 3, 128, dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(1, 2, 8, device="cuda")
+    with pytest.raises(ValueError):
+        dsa.lightning_indexer_triton(q, k, w, sparse_count=2)      # N1 % N2
+    with pytest.raises(ValueError):
+        dsa.lightning_indexer_triton(q, k[:, :, :1], w, block_table=torch.zeros(1, 1, dtype=torch.int32))
+
+
+def test_indexer_repeatable():
+    dsa = _api()
+    q, k, w = _inputs(1, 4, 5000, 64, 1, 128, torch.bfloat16)
+    a = dsa.lightning_indexer_triton(dev(q, torch.bfloat16), dev(k, torch.bfloat16), dev(w, torch.float32),
+                                     sparse_count=512, return_value=True)
+    b = dsa.lightning_indexer_triton(dev(q, torch.bfloat16), dev(k, torch.bfloat16), dev(w, torch.float32),
+                                     sparse_count=512, return_value=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
