@@ -163,6 +163,64 @@ def cpu_baseline_decode(sets):
                       f"{dt:.2f} s"}
 
 
+# ---------------------------------------------------------------------------
+# lightning indexer decode workload (secondary metric: us/query at 32K ctx)
+# ---------------------------------------------------------------------------
+LI_B, LI_S2, LI_N1, LI_D, LI_K = 32, 32768, 64, 128, 2048
+
+
+def make_li_sets(nsets, device):
+    import torch
+    g = torch.Generator(device=device).manual_seed(4321)
+    sets = []
+    for _ in range(nsets):
+        sets.append({
+            "q": torch.randn(LI_B, 1, LI_N1, LI_D, generator=g, device=device).to(torch.bfloat16),
+            "k": torch.randn(LI_B, LI_S2, 1, LI_D, generator=g, device=device).to(torch.bfloat16),
+            "w": torch.rand(LI_B, 1, LI_N1, generator=g, device=device),
+        })
+    return sets
+
+
+def li_algorithmic():
+    """Flops and HBM bytes of one indexer decode step (all keys visible)."""
+    pairs = LI_B * LI_S2
+    flops = 2.0 * LI_N1 * LI_D * pairs
+    nbytes = pairs * LI_D * 2 + LI_B * LI_N1 * (LI_D * 2 + 4) + LI_B * LI_K * 4
+    return flops, nbytes
+
+
+def time_li(sets, steps, warmup):
+    import torch
+    from dsa_triton_ascend_amd import _lib
+    lib = _lib.load()
+    dev = sets[0]["q"].device
+    idx = torch.empty(LI_B, 1, 1, LI_K, dtype=torch.int32, device=dev)
+    ws_bytes = lib.dsa_li_fwd_workspace_size(LI_B, 1, LI_S2)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = _lib.stream_handle(dev)
+
+    def step(s):
+        st = lib.dsa_li_fwd(s["q"].data_ptr(), s["k"].data_ptr(), s["w"].data_ptr(), None, None,
+                            idx.data_ptr(), None, LI_B, 1, LI_S2, LI_N1, 1, LI_D, LI_K, LI_B,
+                            LI_B * LI_S2, 3, _lib.LAYOUT["BSND"], _lib.LAYOUT["BSND"], _lib.DTYPE_BF16,
+                            _lib.DTYPE_FP32, 0, ws.data_ptr(), ws_bytes, stream)
+        if st != 0:
+            _lib.check(st, "dsa_li_fwd")
+
+    for i in range(warmup):
+        step(sets[i % len(sets)])
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        step(sets[i % len(sets)])
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
 def measured_traffic():
     """HBM bytes per step from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     summary (scaled by a copy kernel of known size), or None."""
@@ -228,8 +286,28 @@ def main():
         for _ in range(3):
             torch.bitwise_not(src, out=dst)
         torch.cuda.synchronize()
+    # secondary metric: lightning indexer, us/query at 32K context
+    del sets
+    torch.cuda.empty_cache()
+    li_sets = make_li_sets(max(2, min(args.sets, 4)), dev)
+    li_ms = time_li(li_sets, args.steps, args.warmup)
+    li_flops, li_bytes = li_algorithmic()
+    li_gbs = li_bytes / (li_ms * 1e-3) / 1e9
+    result["lightning_indexer"] = {
+        "metric": "lightning_indexer us/query at 32K ctx (decode)",
+        "value": round(li_ms * 1e3 / LI_B, 4), "unit": "us/query", "higher_is_better": False,
+        "ms_per_step": round(li_ms, 5),
+        "config": {"workload": "lightning_indexer decode: BSND, B=32, S1=1, S2=32768, N1=64, N2=1, "
+                               "D=128, k=2048, sparse_mode 3, bf16 q/k, fp32 weights",
+                   "input_sets": len(li_sets)},
+        "roofline": {"bound": "hbm", "achieved": round(li_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(li_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "li_score_kernel + li_topk_kernel (one step)",
+                     "algorithmic_bytes_per_launch": int(li_bytes),
+                     "algorithmic_flops_per_launch": int(li_flops)},
+    }
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline_decode(sets)
+        result["cpu_baseline"] = cpu_baseline_decode(make_decode_sets(1, dev))
     print(json.dumps(result), flush=True)
 
 

@@ -23,6 +23,19 @@ int hip_fail(hipError_t e, const char* what) {
   return DSA_ERR_HIP;
 }
 
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
 // sfa_fwd.hip
 struct SfaFwdParams;
 int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos);

@@ -103,6 +103,8 @@ __device__ __forceinline__ int rope_swz(int tok) { return (tok >> 1) & 7; }
 namespace dsa {
 void set_error(const char* fmt, ...);
 int hip_fail(hipError_t e, const char* what);
+// CUs of the current device (cached per device; 256 when it cannot be queried)
+int device_cu_count();
 }  // namespace dsa
 
 #define DSA_CHECK_ARG(cond, ...)                                  \

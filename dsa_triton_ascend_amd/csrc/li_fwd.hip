@@ -49,7 +49,7 @@ struct LiParams {
 };
 
 constexpr int kLiThreads = 256;
-constexpr int kLiChunk = 1024;
+constexpr int kLiChunk = 1024;  // default keys per workgroup (resized at launch)
 
 struct LiRow {
   int b, s1, lim;       // visible keys are [0, lim)
@@ -154,10 +154,12 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) kf[ks] = *(const u32x4*)(kp + ks * 32);
   };
-  u32x4 kfa[KS], kfb[KS];
-  int grp = wave;
-  if (grp < ngroups) kload(grp, kfa);
-  if (grp + 4 < ngroups) kload(grp + 4, kfb);
+  // NP groups in flight per wave (ring of K fragment registers)
+  constexpr int NP = 3;
+  u32x4 kf[NP][KS];
+#pragma unroll
+  for (int i = 0; i < NP; ++i)
+    if (wave + 4 * i < ngroups) kload(wave + 4 * i, kf[i]);
   auto process = [&](int gi, const u32x4 (&kf)[KS]) {
     f32x4 acc[GT];
 #pragma unroll
@@ -177,12 +179,14 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
     const int key = c0 + gi * 16 + li;
     if (lg == 0 && key < c1) srow[key] = key < ri.lim ? s : -INFINITY;
   };
-  for (; grp < ngroups; grp += 8) {
-    process(grp, kfa);
-    if (grp + 8 < ngroups) kload(grp + 8, kfa);
-    if (grp + 4 < ngroups) {
-      process(grp + 4, kfb);
-      if (grp + 12 < ngroups) kload(grp + 12, kfb);
+  for (int grp = wave; grp < ngroups; grp += 4 * NP) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int gi = grp + 4 * i;
+      if (gi < ngroups) {
+        process(gi, kf[i]);
+        if (gi + 4 * NP < ngroups) kload(gi + 4 * NP, kf[i]);
+      }
     }
   }
 }
@@ -191,8 +195,7 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
 // top-k kernel
 // ---------------------------------------------------------------------------
 constexpr int kTopkThreads = 1024;
-constexpr int kTopkMaxK = 4096;
-constexpr int kTopkLdsKeys = 16384;  // rows up to this width are kept in LDS
+constexpr int kTopkLdsBudget = 160 * 1024;  // LDS per workgroup on gfx950
 
 // order-preserving map fp32 -> uint32 (larger score -> larger key); -0.0
 // maps to the key of +0.0, so the two tie as they compare equal
@@ -208,41 +211,14 @@ struct TopkParams {
   void* values;         // [rows, k] in val_dtype, or null
   int64_t rows;
   int32_t s2, k, val_dtype;
+  int32_t sel_cap;      // power of two >= k: entries of the LDS sort buffer
 };
-
-// block-wide exclusive scan of one int per thread (1024 threads); returns
-// the exclusive prefix, *total = sum
-__device__ __forceinline__ int block_scan_excl(int v, int* total, int* s_wsum) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  if (lane == 63) s_wsum[wave] = x;
-  __syncthreads();
-  if (wave == 0) {
-    int t = lane < kTopkThreads / 64 ? s_wsum[lane] : 0;
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-      const int y = __shfl_up(t, o);
-      if (lane >= o) t += y;
-    }
-    if (lane < kTopkThreads / 64) s_wsum[lane] = t;  // inclusive per-wave sums
-  }
-  __syncthreads();
-  const int wbase = wave ? s_wsum[wave - 1] : 0;
-  *total = s_wsum[kTopkThreads / 64 - 1];
-  __syncthreads();
-  return wbase + x - v;
-}
 
 template <bool IN_LDS>
 __global__ __launch_bounds__(kTopkThreads) void li_topk_kernel(TopkParams p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char tk_smem[];
-  unsigned long long* sel = (unsigned long long*)tk_smem;   // kTopkMaxK entries
-  unsigned* hist = (unsigned*)(sel + kTopkMaxK);             // 256
+  unsigned long long* sel = (unsigned long long*)tk_smem;   // p.sel_cap entries
+  unsigned* hist = (unsigned*)(sel + p.sel_cap);             // 256
   int* s_wsum = (int*)(hist + 256);                          // 16
   unsigned* s_misc = (unsigned*)(s_wsum + 16);               // 4
   unsigned* s_keys = s_misc + 4;                             // s2 (IN_LDS)
@@ -256,35 +232,117 @@ __global__ __launch_bounds__(kTopkThreads) void li_topk_kernel(TopkParams p) {
     return sort_key(srow[j]);
   };
   if constexpr (IN_LDS) {
-    for (int j = tid; j < S; j += kTopkThreads) s_keys[j] = sort_key(srow[j]);
+    // 16-byte loads, all independent, then the scalar tail
+    const int S4 = (((uintptr_t)srow & 15) == 0) ? (S >> 2) : 0;
+    for (int j = tid; j < S4; j += kTopkThreads) {
+      const float4 v = ((const float4*)srow)[j];
+      s_keys[4 * j] = sort_key(v.x);
+      s_keys[4 * j + 1] = sort_key(v.y);
+      s_keys[4 * j + 2] = sort_key(v.z);
+      s_keys[4 * j + 3] = sort_key(v.w);
+    }
+    for (int j = 4 * S4 + tid; j < S; j += kTopkThreads) s_keys[j] = sort_key(srow[j]);
     __syncthreads();
   }
 
-  // number of finite (visible) entries
+  const int lane = tid & 63, wave = tid >> 6;
+  constexpr int NW = kTopkThreads / 64;
+  const unsigned long long lt_mask = (1ull << lane) - 1ull;
+
+  // number of finite (visible) entries, and their smallest and largest key
   int nv = 0;
-  for (int j = tid; j < S; j += kTopkThreads) nv += key_at(j) > kNegInfKey ? 1 : 0;
+  unsigned kmin = 0xffffffffu, kmax = 0u;
+  constexpr int UN = 4;  // keys read ahead per thread (independent LDS reads in flight)
+  for (int base = 0; base < S; base += UN * kTopkThreads) {
+    unsigned kq[UN];
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int j = base + u * kTopkThreads + tid;
+      kq[u] = j < S ? key_at(j) : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      if (kq[u] > kNegInfKey) {
+        ++nv;
+        kmin = min(kmin, kq[u]);
+        kmax = max(kmax, kq[u]);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    nv += __shfl_xor(nv, o);
+    kmin = min(kmin, (unsigned)__shfl_xor((int)kmin, o));
+    kmax = max(kmax, (unsigned)__shfl_xor((int)kmax, o));
+  }
+  unsigned* s_red = s_misc + 4 + (IN_LDS ? S : 0);  // 3 * NW words after the keys
+  if (lane == 0) {
+    s_red[wave] = (unsigned)nv;
+    s_red[NW + wave] = kmin;
+    s_red[2 * NW + wave] = kmax;
+  }
+  __syncthreads();
   int n_valid = 0;
-  (void)block_scan_excl(nv, &n_valid, s_wsum);
+  kmin = 0xffffffffu;
+  kmax = 0u;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    n_valid += (int)s_red[w];
+    kmin = min(kmin, s_red[NW + w]);
+    kmax = max(kmax, s_red[2 * NW + w]);
+  }
   const int K = p.k;
   const int take = min(K, n_valid);
 
-  // radix select: T = take-th largest valid key; need = entries == T to take
+  // radix select: thr = take-th largest valid key; need = entries == thr to
+  // take.  The bits above the highest bit in which the finite keys differ
+  // are common to all of them and skipped, so the digits of the first pass
+  // are spread over the bins (the sign and exponent bits of real scores are
+  // nearly constant, and one hot bin would serialise the LDS atomics).
   unsigned thr = kNegInfKey;  // with take == n_valid every valid entry (> -inf) is taken
   int need = 0;
   if (take > 0 && take < n_valid) {
-    unsigned prefix = 0, pmask = 0;
+    const unsigned diff = kmin ^ kmax;
+    int bits = diff ? 32 - __clz((int)diff) : 0;
+    unsigned pmask = bits >= 32 ? 0u : ~((1u << bits) - 1u);
+    unsigned prefix = kmin & pmask;
     int remaining = take;
-    for (int pass = 0; pass < 4; ++pass) {
-      const int shift = 24 - 8 * pass;
+    while (bits > 0) {
+      const int width = bits < 8 ? bits : 8;
+      const int shift = bits - width;
+      const unsigned dmask = (1u << width) - 1u;
       if (tid < 256) hist[tid] = 0;
       __syncthreads();
-      for (int j = tid; j < S; j += kTopkThreads) {
-        const unsigned kk = key_at(j);
-        if (kk > kNegInfKey && (kk & pmask) == prefix) atomicAdd(&hist[(kk >> shift) & 255u], 1u);
+      for (int base = 0; base < S; base += UN * kTopkThreads) {
+        unsigned kq[UN];
+#pragma unroll
+        for (int u = 0; u < UN; ++u) {
+          const int j = base + u * kTopkThreads + tid;
+          kq[u] = j < S ? key_at(j) : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < UN; ++u) {
+          const unsigned kk = kq[u];
+          const bool act = kk > kNegInfKey && (kk & pmask) == prefix;
+          const unsigned d = (kk >> shift) & dmask;
+          // a wave whose active lanes share one digit adds once
+          const unsigned long long am = __ballot(act);
+          if (am) {
+            const int first = __ffsll((long long)am) - 1;
+            const unsigned d0 = (unsigned)__builtin_amdgcn_readlane((int)d, first);
+            const unsigned long long same = __ballot(act && d == d0);
+            if (same == am) {
+              if (lane == first) atomicAdd(&hist[d0], (unsigned)__popcll(am));
+            } else if (act) {
+              atomicAdd(&hist[d], 1u);
+            }
+          }
+        }
       }
       __syncthreads();
       if (tid < 64) {
         // bins 255..0 in descending order: lane l owns bins 255-4l .. 252-4l
+        // (bins at or above 2^width stay zero)
         unsigned c[4];
         unsigned loc = 0;
 #pragma unroll
@@ -299,65 +357,169 @@ __global__ __launch_bounds__(kTopkThreads) void li_topk_kernel(TopkParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           if (run < (unsigned)remaining && run + c[i] >= (unsigned)remaining) {
-            s_misc[0] = 255u - 4u * tid - i;  // digit of the K-th largest
+            s_misc[0] = 255u - 4u * tid - i;  // digit of the take-th largest
             s_misc[1] = run;                  // entries in higher bins
           }
           run += c[i];
         }
       }
       __syncthreads();
-      const unsigned dgt = s_misc[0];
       remaining -= (int)s_misc[1];
-      prefix |= dgt << shift;
-      pmask |= 255u << shift;
+      prefix |= s_misc[0] << shift;
+      pmask |= dmask << shift;
+      bits -= width;
       __syncthreads();
     }
     thr = prefix;
     need = remaining;
   }
 
-  // ordered selection: each thread scans a contiguous index range; entries
-  // > thr are all taken, entries == thr only while their rank < need
-  const int per = (S + kTopkThreads - 1) / kTopkThreads;
-  const int j0 = min(S, tid * per), j1 = min(S, j0 + per);
-  int ngt = 0, neq = 0;
-  for (int j = j0; j < j1; ++j) {
-    const unsigned kk = key_at(j);
-    ngt += kk > thr ? 1 : 0;
-    neq += (need > 0 && kk == thr) ? 1 : 0;
-  }
-  int tot_gt = 0, tot_eq = 0;
-  int off_gt = block_scan_excl(ngt, &tot_gt, s_wsum);
-  int off_eq = block_scan_excl(neq, &tot_eq, s_wsum);
-  for (int j = j0; j < j1; ++j) {
-    const unsigned kk = key_at(j);
-    if (kk > thr) {
-      if (off_gt < take) sel[off_gt] = ((unsigned long long)(~kk) << 32) | (unsigned)j;
-      ++off_gt;
-    } else if (need > 0 && kk == thr) {
-      const int at = tot_gt + off_eq;
-      if (off_eq < need && at < take) sel[at] = ((unsigned long long)(~kk) << 32) | (unsigned)j;
-      ++off_eq;
+  // ordered selection, one contiguous index range per wave, 64 consecutive
+  // entries per step (conflict-free LDS reads); ballots give each entry its
+  // rank in index order.  Entries > thr are all taken; entries == thr only
+  // while their rank among them is < need (the lowest indices).
+  const int per_wave = (((S + NW - 1) / NW) + 63) / 64 * 64;
+  const int w0 = min(S, wave * per_wave), w1 = min(S, w0 + per_wave);
+  int cgt = 0, ceq = 0;
+  for (int base = w0; base < w1; base += UN * 64) {
+    unsigned kq[UN];
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int j = base + u * 64 + lane;
+      kq[u] = j < w1 ? key_at(j) : 0u;
     }
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int j = base + u * 64 + lane;
+      cgt += __popcll(__ballot(j < w1 && kq[u] > thr));
+      ceq += __popcll(__ballot(j < w1 && need > 0 && kq[u] == thr));
+    }
+  }
+  int* s_cnt = (int*)(s_red + 3 * NW);  // 2 * NW words
+  if (lane == 0) {
+    s_cnt[wave] = cgt;
+    s_cnt[NW + wave] = ceq;
+  }
+  __syncthreads();
+  int off_gt = 0, off_eq = 0, tot_gt = 0, tot_eq = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    off_gt += w < wave ? s_cnt[w] : 0;
+    off_eq += w < wave ? s_cnt[NW + w] : 0;
+    tot_gt += s_cnt[w];
+    tot_eq += s_cnt[NW + w];
+  }
+  for (int base0 = w0; base0 < w1; base0 += UN * 64) {
+   unsigned kq[UN];
+#pragma unroll
+   for (int u = 0; u < UN; ++u) {
+     const int j = base0 + u * 64 + lane;
+     kq[u] = j < w1 ? key_at(j) : 0u;
+   }
+#pragma unroll
+   for (int u = 0; u < UN; ++u) {
+    const int j = base0 + u * 64 + lane;
+    const unsigned kk = kq[u];
+    const bool gt = j < w1 && kk > thr;
+    const bool eq = j < w1 && need > 0 && kk == thr;
+    const unsigned long long mg = __ballot(gt), me = __ballot(eq);
+    const unsigned long long ck = ((unsigned long long)(~kk) << 32) | (unsigned)j;
+    if (gt) {
+      const int pos = off_gt + __popcll(mg & lt_mask);
+      if (pos < take) sel[pos] = ck;
+    }
+    if (eq) {
+      const int rank = off_eq + __popcll(me & lt_mask);
+      if (rank < need && tot_gt + rank < take) sel[tot_gt + rank] = ck;
+    }
+    off_gt += __popcll(mg);
+    off_eq += __popcll(me);
+   }
   }
   const int nsel = min(take, tot_gt + min(tot_eq, need));  // == take
   int npow = 1;
   while (npow < max(nsel, 1)) npow <<= 1;
-  for (int i = nsel + tid; i < npow; i += kTopkThreads) sel[i] = ~0ull;
+  for (int i = nsel + tid; i < npow; i += kTopkThreads) sel[i] = ~0ull;  // npow <= p.sel_cap
   __syncthreads();
 
-  // bitonic sort ascending of sel[0, npow)
-  for (int size = 2; size <= npow; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int t = tid; t < (npow >> 1); t += kTopkThreads) {
-        const int i = 2 * t - (t & (stride - 1));
-        const int jj = i + stride;
-        const bool up = (i & size) == 0;
-        const unsigned long long a = sel[i], bq = sel[jj];
-        if ((a > bq) == up) { sel[i] = bq; sel[jj] = a; }
-      }
-      __syncthreads();
+  // bitonic sort ascending of sel[0, npow).  Stages with stride >= 128 go
+  // through LDS (one barrier each); the stages with stride < 128 run in
+  // registers: wave w holds 128-entry blocks w and w + 16 (two entries per
+  // lane, index base + lane and base + 64 + lane) and exchanges partners with
+  // lane shuffles, so most of the 66 stages of a 2048-entry sort need no
+  // barrier.
+  auto lds_stage = [&](int size, int stride) {
+    for (int t = tid; t < (npow >> 1); t += kTopkThreads) {
+      const int i = 2 * t - (t & (stride - 1));
+      const int jj = i + stride;
+      const bool up = (i & size) == 0;
+      const unsigned long long a = sel[i], bq = sel[jj];
+      if ((a > bq) == up) { sel[i] = bq; sel[jj] = a; }
     }
+    __syncthreads();
+  };
+  if (npow < 256) {
+    for (int size = 2; size <= npow; size <<= 1)
+      for (int stride = size >> 1; stride > 0; stride >>= 1) lds_stage(size, stride);
+  } else {
+    const int nblk = npow >> 7;  // <= 32
+    unsigned long long x[2][2];
+    auto load_blocks = [&]() {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int blk = wave + 16 * h;
+        if (blk < nblk) {
+          x[h][0] = sel[blk * 128 + lane];
+          x[h][1] = sel[blk * 128 + 64 + lane];
+        }
+      }
+    };
+    auto store_blocks = [&]() {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int blk = wave + 16 * h;
+        if (blk < nblk) {
+          sel[blk * 128 + lane] = x[h][0];
+          sel[blk * 128 + 64 + lane] = x[h][1];
+        }
+      }
+    };
+    auto reg_stages = [&](int size, int smax) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int blk = wave + 16 * h;
+        if (blk >= nblk) continue;
+        const int base = blk * 128;
+        for (int stride = smax; stride > 0; stride >>= 1) {
+          if (stride == 64) {
+            const bool up = ((base + lane) & size) == 0;
+            const unsigned long long a = x[h][0], bq = x[h][1];
+            if ((a > bq) == up) { x[h][0] = bq; x[h][1] = a; }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const int idx = base + 64 * e + lane;
+              const unsigned long long v = x[h][e];
+              const unsigned long long y = __shfl_xor(v, stride);
+              const bool lower = (lane & stride) == 0;
+              const bool up = (idx & size) == 0;
+              x[h][e] = (lower == up) ? (v < y ? v : y) : (v > y ? v : y);
+            }
+          }
+        }
+      }
+    };
+    load_blocks();
+    for (int size = 2; size <= 128; size <<= 1) reg_stages(size, size >> 1);
+    for (int size = 256; size <= npow; size <<= 1) {
+      store_blocks();
+      __syncthreads();
+      for (int stride = size >> 1; stride >= 128; stride >>= 1) lds_stage(size, stride);
+      load_blocks();
+      reg_stages(size, 64);
+    }
+    store_blocks();
+    __syncthreads();
   }
 
   // outputs
@@ -382,10 +544,20 @@ __global__ __launch_bounds__(kTopkThreads) void li_topk_kernel(TopkParams p) {
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-size_t li_topk_lds_bytes(int64_t s2) {
-  size_t b = (size_t)kTopkMaxK * 8 + 256 * 4 + 16 * 4 + 4 * 4;
-  if (s2 <= kTopkLdsKeys) b += (size_t)s2 * 4;
-  return b;
+static int64_t pow2_at_least(int64_t x) {
+  int64_t n = 1;
+  while (n < x) n <<= 1;
+  return n;
+}
+
+// LDS bytes of li_topk_kernel: sort buffer, histogram, scan and misc words,
+// and (rows kept in LDS) the row's keys
+static size_t li_topk_fixed_bytes(int64_t k) {
+  // sort buffer, histogram, scan words, misc words, reduction + count words
+  return (size_t)pow2_at_least(k) * 8 + 256 * 4 + 16 * 4 + 4 * 4 + 5 * (kTopkThreads / 64) * 4;
+}
+static bool li_topk_row_in_lds(int64_t s2, int64_t k) {
+  return li_topk_fixed_bytes(k) + (size_t)s2 * 4 <= (size_t)kTopkLdsBudget;
 }
 
 int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_t* indices,
@@ -399,33 +571,46 @@ int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_
   p.s2 = (int32_t)s2;
   p.k = (int32_t)k;
   p.val_dtype = val_dtype;
-  // dynamic LDS above 64 KB needs the per-function limit raised (once)
+  p.sel_cap = (int32_t)pow2_at_least(k);
+  // dynamic LDS above 64 KB needs the per-function limit raised (once, to
+  // the full budget)
   static bool attr_set[2] = {false, false};
-  const size_t lds = li_topk_lds_bytes(s2);
-  if (s2 <= kTopkLdsKeys) {
-    if (!attr_set[1]) {
-      DSA_HIP(hipFuncSetAttribute((const void*)li_topk_kernel<true>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)li_topk_lds_bytes(kTopkLdsKeys)));
-      attr_set[1] = true;
-    }
-    hipLaunchKernelGGL(li_topk_kernel<true>, dim3((unsigned)rows), dim3(kTopkThreads), lds, stream, p);
-  } else {
-    if (!attr_set[0]) {
-      DSA_HIP(hipFuncSetAttribute((const void*)li_topk_kernel<false>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-      attr_set[0] = true;
-    }
-    hipLaunchKernelGGL(li_topk_kernel<false>, dim3((unsigned)rows), dim3(kTopkThreads), lds, stream, p);
+  const bool in_lds = li_topk_row_in_lds(s2, k);
+  const size_t lds = li_topk_fixed_bytes(k) + (in_lds ? (size_t)s2 * 4 : 0);
+  const void* fn = in_lds ? (const void*)li_topk_kernel<true> : (const void*)li_topk_kernel<false>;
+  if (!attr_set[in_lds]) {
+    DSA_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kTopkLdsBudget));
+    attr_set[in_lds] = true;
   }
+  if (in_lds)
+    hipLaunchKernelGGL(li_topk_kernel<true>, dim3((unsigned)rows), dim3(kTopkThreads), lds, stream, p);
+  else
+    hipLaunchKernelGGL(li_topk_kernel<false>, dim3((unsigned)rows), dim3(kTopkThreads), lds, stream, p);
   DSA_HIP(hipGetLastError());
   return DSA_OK;
 }
 
+// Keys per workgroup: enough chunks per row that the grid fills every CU
+// with as many workgroups as fit at once, in one round (a partial second
+// round would leave most CUs idle while it runs).
 template <int D, typename T, int GT>
-static hipError_t launch_score(const LiParams& p, hipStream_t stream) {
+static hipError_t launch_score(LiParams p, hipStream_t stream) {
+  static int occ = 0;
+  if (!occ) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, li_score_kernel<D, T, GT>, kLiThreads, 0) != hipSuccess ||
+        n < 1)
+      n = 1;
+    occ = n;
+  }
+  const int64_t rows = p.q_rows * p.n2;
+  const int64_t target = (int64_t)device_cu_count() * occ;
+  const int64_t per_row = rows >= target ? 1 : (target + rows - 1) / rows;
+  int64_t chunk = (p.s2 + per_row - 1) / per_row;
+  chunk = ((chunk + 63) / 64) * 64;
+  p.chunk = (int32_t)(chunk < 64 ? 64 : chunk);
   const unsigned chunks = (unsigned)((p.s2 + p.chunk - 1) / p.chunk);
-  hipLaunchKernelGGL((li_score_kernel<D, T, GT>), dim3((unsigned)(p.q_rows * p.n2), chunks),
-                     dim3(kLiThreads), 0, stream, p);
+  hipLaunchKernelGGL((li_score_kernel<D, T, GT>), dim3((unsigned)rows, chunks), dim3(kLiThreads), 0, stream, p);
   return hipGetLastError();
 }
 

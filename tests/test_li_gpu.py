@@ -50,7 +50,8 @@ def _topk_gpu(scores_np, k):
 @pytest.mark.parametrize("S2,k,kind", [
     (64, 16, "random"), (300, 64, "ties"), (1000, 2048, "k_gt_s2"), (4096, 2048, "mixed"),
     (4096, 2048, "ties"), (16384, 2048, "random"), (20000, 2048, "ties"), (32768, 2048, "random"),
-    (32768, 4096, "mixed"), (5000, 1, "ties"), (2049, 2048, "masked_tail"),
+    (32768, 4096, "mixed"), (5000, 1, "ties"), (2049, 2048, "masked_tail"), (3000, 100, "equal"),
+    (32768, 2048, "narrow"),
 ])
 def test_topk_bit_exact(S2, k, kind):
     print(f"[li topk] S2={S2} k={k} {kind}", flush=True)
@@ -58,6 +59,12 @@ def test_topk_bit_exact(S2, k, kind):
     R = 6
     if kind == "ties":
         sc = rng.randint(0, 7, size=(R, S2)).astype(np.float32) * 0.5
+    elif kind == "equal":
+        sc = np.full((R, S2), 3.25, np.float32)
+    elif kind == "narrow":
+        # all scores within a few ulps: the radix digits come from the low bits
+        sc = (np.float32(100.0) + rng.randint(0, 40, size=(R, S2)).astype(np.float32) * np.float32(2 ** -17))
+        sc = sc.astype(np.float32)
     else:
         sc = (rng.randn(R, S2) * 10).astype(np.float32)
     if kind in ("mixed", "masked_tail", "k_gt_s2"):
