@@ -3,12 +3,18 @@
 Public API, mirroring the reference's operator modules:
 
 * ``sparse_flash_attention_triton`` / ``SparseFlashAttentionTriton``
+* ``sparse_flash_attention_grad_triton`` / ``SparseFlashAttentionGradTriton``
 * ``lightning_indexer_triton`` / ``LightningIndexerTriton``
 """
 from .sparse_flash_attention import (  # noqa: F401
     INT64_MAX,
     SparseFlashAttentionTriton,
     sparse_flash_attention_triton,
+)
+
+from .sparse_flash_attention_grad import (  # noqa: F401
+    SparseFlashAttentionGradTriton,
+    sparse_flash_attention_grad_triton,
 )
 
 from .lightning_indexer import (  # noqa: F401
@@ -18,3 +24,4 @@ from .lightning_indexer import (  # noqa: F401
 
 sparse_flash_attention = sparse_flash_attention_triton
 lightning_indexer = lightning_indexer_triton
+sparse_flash_attention_grad = sparse_flash_attention_grad_triton

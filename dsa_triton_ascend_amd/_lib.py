@@ -48,6 +48,18 @@ SIGNATURES = {
         _vp, _sz, _vp,                        # workspace, workspace_bytes, stream
     ]),
     "dsa_sfa_fwd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32]),
+    "dsa_sfa_bwd": (_c.c_int, [
+        _vp, _vp, _vp, _vp, _i32p,           # query, query_rope, key, key_rope, sparse_indices
+        _vp, _vp, _vp, _vp,                   # d_out, out, softmax_max, softmax_sum
+        _i32p, _i32p,                         # actual_seq_q, actual_seq_kv
+        _vp, _vp, _vp, _vp, _vp,              # d_query, d_query_rope, d_key, d_key_rope, d_value
+        _i64, _i64, _i64, _i64, _i64, _i64,   # batch, s1, s2, n1, d, d_rope
+        _i64, _i64, _i64,                     # sparse_count, q_rows, kv_rows
+        _i32, _i32, _i32, _i32,               # sparse_block_size, sparse_mode, layout, dtype
+        _f32,                                 # scale_value
+        _vp, _sz, _vp,                        # workspace, workspace_bytes, stream
+    ]),
+    "dsa_sfa_bwd_workspace_size": (_sz, [_i64, _i64]),
     "dsa_li_fwd": (_c.c_int, [
         _vp, _vp, _vp, _i32p, _i32p,          # query, key, weights, actual_seq_q, actual_seq_k
         _i32p, _vp,                           # sparse_indices, sparse_values

@@ -20,6 +20,7 @@ BUILD_DIR = os.path.join(ROOT, "_build")
 SOURCES = [
     "capi.cpp",
     "sfa_fwd.hip",
+    "sfa_bwd.hip",
     "li_fwd.hip",
 ]
 
@@ -43,12 +44,20 @@ def common_flags():
         "-Wno-unused-function", "-Wno-unused-variable",
         # packed fp32 VALU forms are kept out of the generated code
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        # MFMA accumulators in VGPRs: with AGPR-form accumulators the
-        # register allocator keeps loop-carried accumulators in VGPRs anyway
-        # and copies them across on every iteration
-        "-mllvm", "-amdgpu-mfma-vgpr-form=true",
         "-I", os.path.join(ROOT, "include"),
     ]
+
+
+# MFMA accumulators in VGPRs: with AGPR-form accumulators the register
+# allocator keeps loop-carried accumulators in VGPRs anyway and copies them
+# across on every iteration.  Not for sfa_bwd.hip: its D=512 kernel needs the
+# AGPR file for its resident fragments, and the VGPR form crashes LLVM's
+# AGPR-rewrite pass on it (ROCm 7.2 clang-22).
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]
+PER_SOURCE_FLAGS = {
+    "sfa_fwd.hip": VGPR_FORM,
+    "li_fwd.hip": VGPR_FORM,
+}
 
 
 def _filter(text):
@@ -63,7 +72,8 @@ def _filter(text):
 def _compile(src, extra):
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
     lang = ["-x", "hip"] if src.endswith(".cpp") else []
-    cmd = [hipcc()] + lang + common_flags() + extra + ["-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = ([hipcc()] + lang + common_flags() + PER_SOURCE_FLAGS.get(src, []) + extra
+           + ["-c", os.path.join(CSRC, src), "-o", obj])
     r = subprocess.run(cmd, capture_output=True, text=True)
     return src, obj, r.returncode, _filter(r.stdout + r.stderr), cmd
 

@@ -49,6 +49,16 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
                 int32_t sparse_mode, int32_t layout_query, int32_t layout_kv, int32_t dtype,
                 float scale_value, int32_t return_lse, void* workspace, hipStream_t stream);
 
+// sfa_bwd.hip
+size_t sfa_bwd_workspace_bytes(int64_t kv_rows, int64_t d);
+int sfa_bwd_run(const void* query, const void* query_rope, const void* key, const void* key_rope,
+                const int32_t* sparse_indices, const void* d_out, const void* out, const float* softmax_max,
+                const float* softmax_sum, const int32_t* actual_seq_q, const int32_t* actual_seq_kv,
+                void* d_query, void* d_query_rope, void* d_key, void* d_key_rope, void* d_value,
+                int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t d, int64_t sparse_count,
+                int64_t q_rows, int64_t kv_rows, int32_t sparse_block_size, int32_t sparse_mode,
+                int32_t layout, int32_t dtype, float scale_value, void* workspace, hipStream_t stream);
+
 // li_fwd.hip
 int li_scores_run(const void* query, const void* key, const void* weights, const int32_t* act_q,
                   const int32_t* act_k, float* scores, int64_t batch, int64_t s1, int64_t s2,
@@ -178,6 +188,57 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, cons
                      sparse_count, q_rows, kv_rows, max_blocks, page_size, sparse_block_size,
                      sparse_mode, layout_query, layout_kv, dtype, scale_value, return_lse,
                      workspace, (hipStream_t)stream);
+}
+
+size_t dsa_sfa_bwd_workspace_size(int64_t kv_rows, int64_t d) {
+  if (kv_rows <= 0 || d <= 0) return 0;
+  return sfa_bwd_workspace_bytes(kv_rows, d);
+}
+
+int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
+                const int32_t* sparse_indices, const void* d_out, const void* out, const float* softmax_max,
+                const float* softmax_sum, const int32_t* actual_seq_q, const int32_t* actual_seq_kv,
+                void* d_query, void* d_query_rope, void* d_key, void* d_key_rope, void* d_value,
+                int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t d, int64_t d_rope,
+                int64_t sparse_count, int64_t q_rows, int64_t kv_rows, int32_t sparse_block_size,
+                int32_t sparse_mode, int32_t layout, int32_t dtype, float scale_value, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  g_err[0] = '\0';
+  DSA_CHECK_ARG(query && query_rope && key && key_rope && sparse_indices && d_out && out && softmax_max &&
+                    softmax_sum,
+                "null input tensor pointer");
+  DSA_CHECK_ARG(d_query && d_query_rope && d_key && d_key_rope && d_value, "null output tensor pointer");
+  DSA_CHECK_SUPPORTED(d == 128 || d == 256 || d == 512, "D must be one of (128, 256, 512), got %lld",
+                      (long long)d);
+  DSA_CHECK_SUPPORTED(d_rope == 64, "rope dim must be 64, got %lld", (long long)d_rope);
+  DSA_CHECK_SUPPORTED(n1 >= 1 && n1 <= 128, "N1 must be in [1, 128], got %lld", (long long)n1);
+  DSA_CHECK_SUPPORTED(sparse_mode == 0 || sparse_mode == 3,
+                      "Only sparse_mode 0 (full) / 3 (rightDownCausal) supported");
+  DSA_CHECK_SUPPORTED(is_pow2(sparse_block_size) && sparse_block_size <= 128,
+                      "sparse_block_size must be a power of 2 in [1,128]");
+  DSA_CHECK_SUPPORTED(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_FP16,
+                      "query/key dtype must be bfloat16 or float16");
+  DSA_CHECK_SUPPORTED(layout == DSA_LAYOUT_BSND || layout == DSA_LAYOUT_TND, "layout must be BSND or TND");
+  DSA_CHECK_ARG(batch >= 1 && batch <= (1 << 24), "batch must be >= 1");
+  DSA_CHECK_ARG(sparse_count >= 1 && sparse_count * (int64_t)sparse_block_size <= (1ll << 30),
+                "sparse_count out of range");
+  if (layout == DSA_LAYOUT_TND) {
+    DSA_CHECK_ARG(actual_seq_q && actual_seq_kv, "TND layout requires cumulative actual sequence lengths");
+    DSA_CHECK_ARG(q_rows >= 1, "TND query must have at least one row");
+  } else {
+    DSA_CHECK_ARG(s1 >= 1 && q_rows == batch * s1, "q_rows must equal B*S1 for BSND");
+    DSA_CHECK_ARG(s2 >= 1 && kv_rows == batch * s2, "kv_rows must equal B*S2 for BSND");
+  }
+  DSA_CHECK_ARG(q_rows < (1ll << 31) && kv_rows >= 1 && kv_rows < (1ll << 31), "row counts out of range");
+  const size_t need = sfa_bwd_workspace_bytes(kv_rows, d);
+  if (workspace == nullptr || workspace_bytes < need) {
+    set_error("workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    return DSA_ERR_WORKSPACE;
+  }
+  return sfa_bwd_run(query, query_rope, key, key_rope, sparse_indices, d_out, out, softmax_max, softmax_sum,
+                     actual_seq_q, actual_seq_kv, d_query, d_query_rope, d_key, d_key_rope, d_value, batch, s1,
+                     s2, n1, d, sparse_count, q_rows, kv_rows, sparse_block_size, sparse_mode, layout, dtype,
+                     scale_value, workspace, (hipStream_t)stream);
 }
 
 size_t dsa_li_fwd_workspace_size(int64_t q_rows, int64_t n2, int64_t s2) {

@@ -1,0 +1,77 @@
+// Row and index resolution shared by the sparse flash attention kernels
+// (forward and backward): the masks of the reference kernels
+// (sparse_flash_attention_triton.py:247-254, 270-272;
+// sparse_flash_attention_grad_triton.py:204-208, 246) and the layout
+// handling the reference does on the host (TND cumulative lengths, PA_BSND
+// block_table, block-wise ids; sparse_flash_attention_triton.py:345-421).
+// The parameter structs of both kernels carry the fields used here.
+#pragma once
+
+#include "common.h"
+
+namespace dsa {
+
+struct RowInfo {
+  int b, s1, act_q, act_k, threshold;
+  int64_t kv_base;
+  bool active;
+};
+
+template <typename P>
+__device__ __forceinline__ RowInfo sfa_row_info(const P& p, int row) {
+  RowInfo ri;
+  if (p.layout_q == DSA_LAYOUT_TND) {
+    // cumulative lengths: first b with cu[b] > row
+    int lo = 0, hi = p.batch - 1;
+    while (lo < hi) {
+      int mid = (lo + hi) >> 1;
+      if (p.act_q[mid] > row) hi = mid; else lo = mid + 1;
+    }
+    ri.b = lo;
+    int start = lo ? p.act_q[lo - 1] : 0;
+    ri.s1 = row - start;
+    ri.act_q = p.act_q[lo] - start;
+  } else {
+    ri.b = row / p.s1;
+    ri.s1 = row - ri.b * p.s1;
+    ri.act_q = p.act_q ? p.act_q[ri.b] : p.s1;
+  }
+  if (p.layout_kv == DSA_LAYOUT_TND) {
+    int start = ri.b ? p.act_k[ri.b - 1] : 0;
+    ri.kv_base = start;
+    ri.act_k = p.act_k[ri.b] - start;
+  } else {
+    ri.kv_base = (int64_t)ri.b * p.s2;  // unused for PA_BSND
+    ri.act_k = p.act_k ? p.act_k[ri.b] : p.s2;
+  }
+  ri.threshold = p.mode == 0 ? ri.act_k : ri.act_k - ri.act_q + ri.s1 + 1;
+  ri.active = (ri.s1 < ri.act_q) && (ri.threshold > 0);
+  return ri;
+}
+
+// Resolve index position `pos` of a row to a physical KV row.
+// Returns false if the position is not attended; *phys = -1 marks a token that
+// is attended but lives in a -1 / out-of-range page (reads as a zero row, as
+// the reference's de-paging leaves such spans zero, lines 391-397).
+template <typename P>
+__device__ __forceinline__ bool sfa_resolve(const P& p, const RowInfo& ri, const int32_t* idx_row,
+                                            int pos, int* phys) {
+  int id = idx_row[pos / p.bs];
+  if (id < 0) return false;
+  int64_t tok = (int64_t)id * p.bs + (pos % p.bs);
+  if (tok >= ri.threshold || tok >= ri.act_k) return false;
+  if (p.layout_kv == DSA_LAYOUT_PA_BSND) {
+    if (tok >= (int64_t)p.max_blocks * p.page_size) return false;
+    int blk = p.block_table[(int64_t)ri.b * p.max_blocks + tok / p.page_size];
+    int64_t r = (int64_t)blk * p.page_size + tok % p.page_size;
+    *phys = (blk < 0 || r >= p.kv_rows) ? -1 : (int)r;
+    return true;
+  }
+  if (p.layout_kv == DSA_LAYOUT_BSND && tok >= p.s2) return false;
+  int64_t r = ri.kv_base + tok;
+  if (r >= p.kv_rows) return false;
+  *phys = (int)r;
+  return true;
+}
+
+}  // namespace dsa

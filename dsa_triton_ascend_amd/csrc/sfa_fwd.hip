@@ -31,6 +31,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "sfa_common.h"
 
 namespace dsa {
 
@@ -70,67 +71,6 @@ struct SfaFwdParams {
 constexpr int kSfaTile = 32;
 constexpr int kSfaMaxList = 2048;
 constexpr float kRefSlack = 64.f;  // log2 units
-
-struct RowInfo {
-  int b, s1, act_q, act_k, threshold;
-  int64_t kv_base;
-  bool active;
-};
-
-__device__ __forceinline__ RowInfo sfa_row_info(const SfaFwdParams& p, int row) {
-  RowInfo ri;
-  if (p.layout_q == DSA_LAYOUT_TND) {
-    // cumulative lengths: first b with cu[b] > row
-    int lo = 0, hi = p.batch - 1;
-    while (lo < hi) {
-      int mid = (lo + hi) >> 1;
-      if (p.act_q[mid] > row) hi = mid; else lo = mid + 1;
-    }
-    ri.b = lo;
-    int start = lo ? p.act_q[lo - 1] : 0;
-    ri.s1 = row - start;
-    ri.act_q = p.act_q[lo] - start;
-  } else {
-    ri.b = row / p.s1;
-    ri.s1 = row - ri.b * p.s1;
-    ri.act_q = p.act_q ? p.act_q[ri.b] : p.s1;
-  }
-  if (p.layout_kv == DSA_LAYOUT_TND) {
-    int start = ri.b ? p.act_k[ri.b - 1] : 0;
-    ri.kv_base = start;
-    ri.act_k = p.act_k[ri.b] - start;
-  } else {
-    ri.kv_base = (int64_t)ri.b * p.s2;  // unused for PA_BSND
-    ri.act_k = p.act_k ? p.act_k[ri.b] : p.s2;
-  }
-  ri.threshold = p.mode == 0 ? ri.act_k : ri.act_k - ri.act_q + ri.s1 + 1;
-  ri.active = (ri.s1 < ri.act_q) && (ri.threshold > 0);
-  return ri;
-}
-
-// Resolve index position `pos` of a row to a physical KV row.
-// Returns false if the position is not attended; *phys = -1 marks a token that
-// is attended but lives in a -1 / out-of-range page (reads as a zero row, as
-// the reference's de-paging leaves such spans zero, lines 391-397).
-__device__ __forceinline__ bool sfa_resolve(const SfaFwdParams& p, const RowInfo& ri,
-                                            const int32_t* idx_row, int pos, int* phys) {
-  int id = idx_row[pos / p.bs];
-  if (id < 0) return false;
-  int64_t tok = (int64_t)id * p.bs + (pos % p.bs);
-  if (tok >= ri.threshold || tok >= ri.act_k) return false;
-  if (p.layout_kv == DSA_LAYOUT_PA_BSND) {
-    if (tok >= (int64_t)p.max_blocks * p.page_size) return false;
-    int blk = p.block_table[(int64_t)ri.b * p.max_blocks + tok / p.page_size];
-    int64_t r = (int64_t)blk * p.page_size + tok % p.page_size;
-    *phys = (blk < 0 || r >= p.kv_rows) ? -1 : (int)r;
-    return true;
-  }
-  if (p.layout_kv == DSA_LAYOUT_BSND && tok >= p.s2) return false;
-  int64_t r = ri.kv_base + tok;
-  if (r >= p.kv_rows) return false;
-  *phys = (int)r;
-  return true;
-}
 
 // Zero row for padding slots of the 64-bit gather path (the buffer path
 // gets zeros from the hardware range check instead).

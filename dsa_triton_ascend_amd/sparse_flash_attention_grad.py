@@ -1,0 +1,144 @@
+"""sparse_flash_attention backward on MI355X: the reference's public API over
+the HIP library.
+
+Drop-in for ``sparse_flash_attention_grad_triton`` /
+``SparseFlashAttentionGradTriton`` (sparse_flash_attention_grad_triton.py:
+382-586): same argument names and defaults (``layout="BSND"``,
+``sparse_mode=3``), the same guards (ValueError for non-default
+pre/next_tokens, sparse modes other than 0/3, missing rope,
+``deterministic=True``, a block size that is not a power of two <= 128, D,
+rope width, N2 != 1, N1 not a power of two <= 128) and the same return tuple
+``(d_query, d_key, d_value, d_query_rope, d_key_rope)`` with the shapes and
+dtypes of the corresponding inputs.  TND rows and block-wise indices are
+resolved in the kernel (no host unpacking).
+"""
+import torch
+
+from . import _lib
+from .sparse_flash_attention import INT64_MAX, _check_device, _seq_tensor, _VALID_D, _VALID_N1
+
+_D_ROPE = 64
+
+
+def sparse_flash_attention_grad_triton(
+    query,
+    key,
+    value,
+    sparse_indices,
+    d_out,
+    out,
+    softmax_max,
+    softmax_sum,
+    scale_value=1.0,
+    query_rope=None,
+    key_rope=None,
+    actual_seq_lengths_query=None,
+    actual_seq_lengths_kv=None,
+    sparse_block_size=1,
+    layout="BSND",
+    sparse_mode=3,
+    pre_tokens=INT64_MAX,
+    next_tokens=INT64_MAX,
+    deterministic=False,
+):
+    """SFA backward (MLA-absorb, MQA); see module docstring.  ``value`` is
+    only used for the dtype of d_value (value = key[..., :D])."""
+    if pre_tokens != INT64_MAX or next_tokens != INT64_MAX:
+        raise ValueError("pre_tokens/next_tokens only support default INT64_MAX")
+    if sparse_mode not in (0, 3):
+        raise ValueError("Only sparse_mode 0 (full) / 3 (rightDownCausal) supported")
+    if query_rope is None or key_rope is None:
+        raise ValueError("query_rope and key_rope are required (no empty rope)")
+    if deterministic:
+        raise ValueError("deterministic=True is not supported (scatter-add path)")
+    if sparse_block_size < 1 or (sparse_block_size & (sparse_block_size - 1)) != 0 \
+            or sparse_block_size > 128:
+        raise ValueError("sparse_block_size must be a power of 2 in [1,128]")
+    if layout not in ("BSND", "TND"):
+        raise ValueError(f"layout must be BSND or TND, got {layout}")
+    is_tnd = layout == "TND"
+    device = _check_device(query, key, query_rope, key_rope, sparse_indices, d_out, out,
+                           softmax_max, softmax_sum)
+
+    if is_tnd:
+        if actual_seq_lengths_query is None or actual_seq_lengths_kv is None:
+            raise ValueError("TND layout requires cumulative actual sequence lengths")
+        T1, N1, D = query.shape
+        act_q = _seq_tensor(actual_seq_lengths_query, device)
+        act_k = _seq_tensor(actual_seq_lengths_kv, device)
+        B = act_q.numel()
+        S1 = S2 = 0
+        q_rows, kv_rows = T1, key.shape[0]
+        if key.dim() != 3 or key.shape[1] != 1:
+            raise ValueError("Only N2=1 (MQA) is supported")
+    else:
+        B, S1, N1, D = query.shape
+        if key.dim() != 4 or key.shape[2] != 1:
+            raise ValueError("Only N2=1 (MQA) is supported")
+        S2 = key.shape[1]
+        act_q = _seq_tensor(actual_seq_lengths_query, device)
+        act_k = _seq_tensor(actual_seq_lengths_kv, device)
+        q_rows, kv_rows = B * S1, B * S2
+    D_ROPE = query_rope.shape[-1]
+    if D not in _VALID_D:
+        raise ValueError(f"D must be one of {_VALID_D}, got {D}")
+    if D_ROPE != _D_ROPE:
+        raise ValueError(f"rope dim must be {_D_ROPE}, got {D_ROPE}")
+    if N1 not in _VALID_N1:
+        raise ValueError(f"N1 must be one of {_VALID_N1}, got {N1}")
+    if query.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("query dtype must be bfloat16 or float16")
+    for t, nm in ((key, "key"), (query_rope, "query_rope"), (key_rope, "key_rope"), (d_out, "d_out"),
+                  (out, "out")):
+        if t.dtype != query.dtype:
+            raise ValueError(f"{nm} must have the query dtype")
+    K = sparse_indices.shape[-1]
+
+    dq = torch.empty_like(query)
+    dqr = torch.empty_like(query_rope)
+    dk = torch.empty_like(key)
+    dkr = torch.empty_like(key_rope)
+    dv = torch.empty(key.shape, dtype=value.dtype if value is not None else key.dtype, device=device)
+    if dv.dtype != key.dtype:
+        raise ValueError("value dtype must equal the key dtype")
+    lib = _lib.load()
+    ws_bytes = lib.dsa_sfa_bwd_workspace_size(kv_rows, D)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    c = [t.contiguous() for t in (query, query_rope, key, key_rope, d_out, out)]
+    si = sparse_indices.to(torch.int32).contiguous()
+    smax = softmax_max.to(torch.float32).contiguous()
+    ssum = softmax_sum.to(torch.float32).contiguous()
+    st = lib.dsa_sfa_bwd(
+        c[0].data_ptr(), c[1].data_ptr(), c[2].data_ptr(), c[3].data_ptr(), si.data_ptr(),
+        c[4].data_ptr(), c[5].data_ptr(), smax.data_ptr(), ssum.data_ptr(),
+        _lib.ptr(act_q), _lib.ptr(act_k),
+        dq.data_ptr(), dqr.data_ptr(), dk.data_ptr(), dkr.data_ptr(), dv.data_ptr(),
+        B, S1, S2, N1, D, D_ROPE, K, q_rows, kv_rows, sparse_block_size, sparse_mode,
+        _lib.LAYOUT[layout], _lib.dtype_code(query.dtype), float(scale_value),
+        ws.data_ptr(), ws_bytes, _lib.stream_handle(device))
+    _lib.check(st, "sparse_flash_attention_grad")
+    return dq, dk, dv, dqr, dkr
+
+
+class SparseFlashAttentionGradTriton(torch.nn.Module):
+    """Module form (sparse_flash_attention_grad_triton.py:544-586)."""
+
+    def __init__(self, scale_value=1.0, sparse_block_size=1, layout="BSND", sparse_mode=3,
+                 pre_tokens=INT64_MAX, next_tokens=INT64_MAX, deterministic=False):
+        super().__init__()
+        self.scale_value = scale_value
+        self.sparse_block_size = sparse_block_size
+        self.layout = layout
+        self.sparse_mode = sparse_mode
+        self.pre_tokens = pre_tokens
+        self.next_tokens = next_tokens
+        self.deterministic = deterministic
+
+    def forward(self, query, key, value, sparse_indices, d_out, out, softmax_max, softmax_sum,
+                query_rope=None, key_rope=None, actual_seq_lengths_query=None,
+                actual_seq_lengths_kv=None):
+        return sparse_flash_attention_grad_triton(
+            query, key, value, sparse_indices, d_out, out, softmax_max, softmax_sum,
+            self.scale_value, query_rope, key_rope, actual_seq_lengths_query, actual_seq_lengths_kv,
+            self.sparse_block_size, self.layout, self.sparse_mode, self.pre_tokens,
+            self.next_tokens, self.deterministic)

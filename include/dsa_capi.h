@@ -84,6 +84,33 @@ size_t dsa_sfa_fwd_workspace_size(int64_t q_rows, int64_t n1, int64_t d,
                                   int64_t sparse_count, int32_t sparse_block_size);
 
 /*
+ * Sparse flash attention backward, MLA-absorb, MQA.  Replaces the reference
+ * core `_sfa_grad_core` (sparse_flash_attention_grad_triton.py:334-376) and
+ * the layout handling around it (451-531): TND rows and block-wise indices
+ * are resolved in the kernel.  layout applies to query and key alike (BSND
+ * or TND), as in the reference.  Inputs as dsa_sfa_fwd plus d_out and out
+ * [R, N1, D] and the forward's softmax_max / softmax_sum [R, N1] fp32
+ * (natural-log units).  Writes d_query [R, N1, D], d_query_rope [R, N1, 64]
+ * in the query dtype and d_key / d_value [KV, D], d_key_rope [KV, 64] in the
+ * key dtype.  d_key (through the scores) and d_value (through P.dO) are
+ * separate, as in the reference; a caller sharing key and value sums them.
+ * The dK / dV scatter-add uses fp32 atomics: results may differ in the last
+ * bits between runs, as the reference's (deterministic mode is rejected by
+ * the reference API, 434-435).  The workspace holds the fp32 accumulators.
+ */
+int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
+                const int32_t* sparse_indices, const void* d_out, const void* out,
+                const float* softmax_max, const float* softmax_sum, const int32_t* actual_seq_q,
+                const int32_t* actual_seq_kv, void* d_query, void* d_query_rope, void* d_key,
+                void* d_key_rope, void* d_value, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
+                int64_t d, int64_t d_rope, int64_t sparse_count, int64_t q_rows, int64_t kv_rows,
+                int32_t sparse_block_size, int32_t sparse_mode, int32_t layout, int32_t dtype,
+                float scale_value, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of dsa_sfa_bwd: kv_rows * (2*d + 64) fp32. */
+size_t dsa_sfa_bwd_workspace_size(int64_t kv_rows, int64_t d);
+
+/*
  * Lightning indexer: scores + stable top-k.  Replaces the reference core
  * `_lightning_indexer_score_core` (lightning_indexer_triton.py:382-413) and the
  * top-k after it (`_stable_topk`, 339-357, called at 539), with the stable
