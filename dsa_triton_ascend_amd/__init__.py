@@ -5,6 +5,8 @@ Public API, mirroring the reference's operator modules:
 * ``sparse_flash_attention_triton`` / ``SparseFlashAttentionTriton``
 * ``sparse_flash_attention_grad_triton`` / ``SparseFlashAttentionGradTriton``
 * ``lightning_indexer_triton`` / ``LightningIndexerTriton``
+* ``sparse_lightning_indexer_grad_kl_loss_triton`` /
+  ``SparseLightningIndexerGradKLLossTriton``
 """
 from .sparse_flash_attention import (  # noqa: F401
     INT64_MAX,
@@ -22,6 +24,12 @@ from .lightning_indexer import (  # noqa: F401
     lightning_indexer_triton,
 )
 
+from .sparse_lightning_indexer_grad_kl_loss import (  # noqa: F401
+    SparseLightningIndexerGradKLLossTriton,
+    sparse_lightning_indexer_grad_kl_loss_triton,
+)
+
 sparse_flash_attention = sparse_flash_attention_triton
 lightning_indexer = lightning_indexer_triton
 sparse_flash_attention_grad = sparse_flash_attention_grad_triton
+sparse_lightning_indexer_grad_kl_loss = sparse_lightning_indexer_grad_kl_loss_triton

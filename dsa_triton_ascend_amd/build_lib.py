@@ -22,6 +22,7 @@ SOURCES = [
     "sfa_fwd.hip",
     "sfa_bwd.hip",
     "li_fwd.hip",
+    "kl_bwd.hip",
 ]
 
 ARCH = os.environ.get("DSA_OFFLOAD_ARCH", "gfx950")

@@ -51,6 +51,15 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
 
 // sfa_bwd.hip
 size_t sfa_bwd_workspace_bytes(int64_t kv_rows, int64_t d);
+size_t kl_bwd_workspace_bytes(int64_t batch, int64_t s1, int64_t s2, int64_t topk);
+int kl_bwd_max_topk();
+int kl_bwd_max_nidx();
+int kl_bwd_run(const void* query, const void* key, const void* query_rope, const void* key_rope,
+               const void* query_index, const void* key_index, const void* weights, const int32_t* sparse_indices,
+               const float* softmax_max, const float* softmax_sum, const int32_t* act_q, const int32_t* act_k,
+               void* d_query_index, void* d_key_index, void* d_weights, float* loss, int64_t batch, int64_t s1,
+               int64_t s2, int64_t n1, int64_t d, int64_t d_rope, int64_t nidx, int64_t topk, int32_t dtype,
+               int32_t w_dtype, float scale_value, void* workspace, hipStream_t stream);
 int sfa_bwd_run(const void* query, const void* query_rope, const void* key, const void* key_rope,
                 const int32_t* sparse_indices, const void* d_out, const void* out, const float* softmax_max,
                 const float* softmax_sum, const int32_t* actual_seq_q, const int32_t* actual_seq_kv,
@@ -239,6 +248,54 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
                      actual_seq_q, actual_seq_kv, d_query, d_query_rope, d_key, d_key_rope, d_value, batch, s1,
                      s2, n1, d, sparse_count, q_rows, kv_rows, sparse_block_size, sparse_mode, layout, dtype,
                      scale_value, workspace, (hipStream_t)stream);
+}
+
+size_t dsa_kl_bwd_workspace_size(int64_t batch, int64_t s1, int64_t s2, int64_t sparse_count, int64_t d_idx) {
+  if (batch <= 0 || s1 <= 0 || s2 <= 0 || sparse_count <= 0 || d_idx != 128) return 0;
+  return kl_bwd_workspace_bytes(batch, s1, s2, sparse_count);
+}
+
+int dsa_kl_bwd(const void* query, const void* key, const void* query_rope, const void* key_rope,
+               const void* query_index, const void* key_index, const void* weights,
+               const int32_t* sparse_indices, const float* softmax_max, const float* softmax_sum,
+               const int32_t* actual_seq_qlen, const int32_t* actual_seq_klen, void* d_query_index,
+               void* d_key_index, void* d_weights, float* loss, int64_t batch, int64_t s1, int64_t s2,
+               int64_t n1, int64_t d, int64_t d_rope, int64_t n_idx, int64_t d_idx, int64_t sparse_count,
+               int32_t dtype, int32_t weights_dtype, float scale_value, void* workspace,
+               size_t workspace_bytes, void* stream) {
+  g_err[0] = '\0';
+  DSA_CHECK_ARG(query && key && query_index && key_index && weights && sparse_indices && softmax_max &&
+                    softmax_sum,
+                "null input tensor pointer");
+  DSA_CHECK_ARG(d_query_index && d_key_index && d_weights && loss, "null output tensor pointer");
+  DSA_CHECK_SUPPORTED(d == 128 || d == 256 || d == 512, "D must be one of (128, 256, 512), got %lld",
+                      (long long)d);
+  DSA_CHECK_SUPPORTED(d_rope == 0 || d_rope == 64, "rope dim must be 64 (or 0 for no rope), got %lld",
+                      (long long)d_rope);
+  DSA_CHECK_ARG(d_rope == 0 || (query_rope && key_rope), "null rope tensor pointer");
+  DSA_CHECK_SUPPORTED(d_idx == 128, "index head dim must be 128, got %lld", (long long)d_idx);
+  DSA_CHECK_SUPPORTED(n_idx >= 1 && n_idx <= kl_bwd_max_nidx(), "Nidx1 must be in [1, %d], got %lld",
+                      kl_bwd_max_nidx(), (long long)n_idx);
+  DSA_CHECK_SUPPORTED(n1 >= 1 && n1 <= 128, "N1 must be in [1, 128], got %lld", (long long)n1);
+  DSA_CHECK_SUPPORTED(sparse_count >= 1 && sparse_count <= kl_bwd_max_topk(), "topK must be in [1, %d], got %lld",
+                      kl_bwd_max_topk(), (long long)sparse_count);
+  DSA_CHECK_SUPPORTED(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_FP16,
+                      "query/key/index dtype must be bfloat16 or float16");
+  DSA_CHECK_SUPPORTED(weights_dtype == DSA_DTYPE_FP32 || weights_dtype == DSA_DTYPE_BF16 ||
+                          weights_dtype == DSA_DTYPE_FP16,
+                      "weights dtype must be float32, bfloat16 or float16");
+  DSA_CHECK_ARG(batch >= 1 && s1 >= 1 && s2 >= 1, "batch, S1 and S2 must be >= 1");
+  DSA_CHECK_ARG(batch * s1 * sparse_count < (1ll << 31) && batch * s2 < (1ll << 31),
+                "rows x topK and B x S2 must stay below 2^31");
+  const size_t need = kl_bwd_workspace_bytes(batch, s1, s2, sparse_count);
+  if (workspace == nullptr || workspace_bytes < need) {
+    set_error("workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    return DSA_ERR_WORKSPACE;
+  }
+  return kl_bwd_run(query, key, d_rope ? query_rope : nullptr, d_rope ? key_rope : nullptr, query_index,
+                    key_index, weights, sparse_indices, softmax_max, softmax_sum, actual_seq_qlen,
+                    actual_seq_klen, d_query_index, d_key_index, d_weights, loss, batch, s1, s2, n1, d, d_rope,
+                    n_idx, sparse_count, dtype, weights_dtype, scale_value, workspace, (hipStream_t)stream);
 }
 
 size_t dsa_li_fwd_workspace_size(int64_t q_rows, int64_t n2, int64_t s2) {

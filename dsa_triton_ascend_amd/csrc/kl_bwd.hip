@@ -1,0 +1,796 @@
+// Sparse lightning-indexer KL-loss backward for gfx950.
+//
+// Semantics follow the reference kernels `_indexer_grad_kl_loss_kernel` and
+// `_scatter_dkey_index_kernel` (sparse_lightning_indexer_grad_kl_loss_triton.py:
+// 74-263, 266-317) and the golden `numpy_reference` (sli_grad_kl_loss_numpy.py:
+// 16-152).  For every query row (b, s1) with s1 < act_q, over the first
+// n = min(topK, max(act_k - act_q + s1 + 1, 0)) slots (kernel line 107), each
+// slot's token clamped to [0, S2) with no -1 test (lines 58, 63, 300):
+//   relu[g,k] = max(qi_g . ki_k, 0),  I[k] = sum_g w_g relu[g,k]     (119-136)
+//   p[k] = (1/N1) sum_h exp(s[h,k] - max_h) / (sum_h + 1e-8),
+//          s[h,k] = (q_h . k_k + qr_h . kr_k) * scale                 (145-177)
+//   sI = exp(I - max I) / (sum exp + 1e-8), dI = sI - p               (180-207)
+//   loss += sum_k P (log P - log Q), P = max(p, 1e-8), Q = max(sI, 1e-8) (208-216)
+//   dW_g = sum_k dI relu[g,k]; dQi_g = sum_k dI w_g 1[relu>0] ki_k  (224-260)
+//   dKi[token_k] += sum_g dI w_g 1[relu>0] qi_g                       (307-317)
+//
+// Design:
+//  * kl_bwd_row_kernel: one workgroup of 8 waves per query row.  Pass A
+//    streams tiles of 32 slots (K, K_rope, K_index rows gathered into LDS,
+//    the next tile's loads in flight during the current tile's MFMAs): each
+//    wave scores 16 heads of the teacher on MFMA (Q fragments resident in
+//    registers) and sums its heads' probabilities across lanes; waves 0-3
+//    score 16 index heads each.  I and p of the row stay in LDS.  Pass B is
+//    the softmax/KL over the row.  Pass C re-streams K_index: the index
+//    scores are recomputed (cheaper than storing Nidx1 x topK ReLUs), dW and
+//    dQi accumulate in registers (dQi^T = Ki^T . dS^T through the
+//    transposing LDS read), and the per-slot dKi contributions
+//    c[k] = dS[:,k]^T . Qi are written to a workspace.
+//  * dKi without atomics: the slots are bucketed by target token (count,
+//    scan, fill), and one wave per token sums its contributions in int64
+//    fixed point, with the exponent fixed by the largest row maximum among
+//    the token's slots: integer addition is associative, so the result does
+//    not depend on the bucket order and the output is deterministic.
+//  * The loss is written per row and summed by one workgroup in a fixed
+//    order (the reference adds rows with an atomic).
+#include "common.h"
+
+namespace dsa {
+
+struct KlParams {
+  const void* q;
+  const void* qr;
+  const void* k;
+  const void* kr;
+  const void* qi;
+  const void* ki;
+  const void* w;
+  const int32_t* idx;
+  const float* smax;
+  const float* ssum;
+  const int32_t* act_q;
+  const int32_t* act_k;
+  void* dqi;
+  void* dw;
+  float* cbuf;       // [rows][topK][128] dKi contribution of each slot
+  float* rowmax;     // [rows] max |c| over the row's slots
+  float* loss_part;  // [rows]
+  int32_t batch, s1, s2, n1, nidx, topk, w_dtype;
+  float scale_log2;  // scale * log2(e)
+};
+
+constexpr int kKlTile = 32;
+constexpr int kKlDi = 128;
+constexpr int kKlWaves = 8;
+constexpr int kKlMaxNidx = 64;
+constexpr int kKlMaxTopk = 8192;
+constexpr int kKlDsRow = kKlMaxNidx + 8;  // padded LDS row of dS^T (elements)
+
+struct KlRow {
+  int b, s1, n;
+  bool active;
+};
+
+__device__ __forceinline__ KlRow kl_row_info(const KlParams& p, int row) {
+  KlRow r;
+  r.b = row / p.s1;
+  r.s1 = row - r.b * p.s1;
+  const int aq = p.act_q ? p.act_q[r.b] : p.s1;
+  const int ak = p.act_k ? p.act_k[r.b] : p.s2;
+  r.active = r.s1 < aq;
+  r.n = r.active ? min(p.topk, max(ak - aq + r.s1 + 1, 0)) : 0;
+  return r;
+}
+
+__device__ __forceinline__ int kl_token(const KlParams& p, int row, int b, int k) {
+  const int t = p.idx[(int64_t)row * p.topk + k];
+  return b * p.s2 + min(max(t, 0), p.s2 - 1);
+}
+
+__device__ __forceinline__ float load_w(const void* w, int64_t i, int dt) {
+  if (dt == DSA_DTYPE_FP32) return ((const float*)w)[i];
+  if (dt == DSA_DTYPE_BF16) return (float)((const bf16*)w)[i];
+  return (float)((const f16*)w)[i];
+}
+
+__device__ __forceinline__ void store_w(void* w, int64_t i, int dt, float v) {
+  if (dt == DSA_DTYPE_FP32) ((float*)w)[i] = v;
+  else if (dt == DSA_DTYPE_BF16) ((bf16*)w)[i] = (bf16)v;
+  else ((f16*)w)[i] = (f16)v;
+}
+
+// sum over the 16 lanes of each 16-lane group
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 8);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+template <int D, int DR, typename T>
+__global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p) {
+  using E = Elem<T>;
+  using V8 = typename E::v8;
+  constexpr int DI = kKlDi;
+  constexpr int TILE = kKlTile;
+  constexpr int NT = kKlWaves * 64;
+  constexpr int KSN = D / 32, KSR = DR / 32, KS = KSN + KSR;
+  constexpr int ROW = D * 2;            // K row bytes in LDS
+  constexpr int IROW = DI * 2;          // K_index row bytes
+  constexpr int CN = D / 8, CR = DR / 8, CI = DI / 8;  // 16-byte chunks per row
+  constexpr int NCH_A = TILE * (CN + CR + CI);
+  constexpr int PF_A = (NCH_A + NT - 1) / NT;
+  static_assert(TILE * CI == NT, "one K_index chunk per thread");
+  constexpr bool kF16 = __is_same(T, f16);
+
+  __shared__ __attribute__((aligned(16))) unsigned char s_k[TILE * ROW];
+  __shared__ __attribute__((aligned(16))) unsigned char s_kr[DR > 0 ? TILE * DR * 2 : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char s_ki[TILE * IROW];
+  __shared__ float s_red[kKlWaves][TILE];
+  __shared__ float s_redi[4][TILE];
+  __shared__ __attribute__((aligned(16))) T s_ds[2][TILE][kKlDsRow];  // dS^T hi / lo: [slot][g]
+  __shared__ float s_misc[2 * kKlWaves + 4];
+  extern __shared__ float s_dyn[];  // I (then dI) and p of the row: 2 x topK floats
+  float* s_I = s_dyn;
+  float* s_p = s_dyn + p.topk;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int li = lane & 15, lg = lane >> 4;
+  const int rows = p.batch * p.s1;
+  const int row = rows - 1 - (int)blockIdx.x;  // long causal rows first
+  const KlRow ri = kl_row_info(p, row);
+  const int n = ri.n;
+
+  if (n <= 0) {
+    // inactive or empty row: zero gradients, no loss (kernel lines 103-105)
+    for (int e = tid; e < p.nidx * DI; e += NT) ((T*)p.dqi)[(int64_t)row * p.nidx * DI + e] = E::from_f32(0.f);
+    for (int g = tid; g < p.nidx; g += NT) store_w(p.dw, (int64_t)row * p.nidx + g, p.w_dtype, 0.f);
+    if (tid == 0) {
+      p.loss_part[row] = 0.f;
+      p.rowmax[row] = 0.f;
+    }
+    return;
+  }
+  const int nt = (n + TILE - 1) / TILE;
+  const u32x4 z4 = {0u, 0u, 0u, 0u};
+
+  // ---- resident fragments ----
+  const int head = wave * 16 + li;
+  const bool hv = head < p.n1;
+  const bool wave_heads = wave * 16 < p.n1;
+  const int64_t hrow = (int64_t)row * p.n1 + (hv ? head : 0);
+  V8 qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    u32x4 v;
+    if (ks < KSN) v = *(const u32x4*)((const T*)p.q + hrow * D + ks * 32 + lg * 8);
+    else v = *(const u32x4*)((const T*)p.qr + hrow * DR + (ks - KSN) * 32 + lg * 8);
+    qf[ks] = as_v8<V8>(hv ? v : z4);
+  }
+  float m2 = 0.f, inv = 0.f;
+  if (hv) {
+    m2 = p.smax[hrow] * kLog2e;
+    inv = 1.f / (p.ssum[hrow] + 1e-8f);
+  }
+  // index heads: waves 0-3, g = 16*wave + li
+  const bool iwave = wave < 4 && wave * 16 < p.nidx;
+  const int g = wave * 16 + li;
+  const bool gv = iwave && g < p.nidx;
+  const int64_t grow = (int64_t)row * p.nidx + (gv ? g : 0);
+  V8 qif[DI / 32];
+#pragma unroll
+  for (int ks = 0; ks < DI / 32; ++ks) {
+    const u32x4 v = *(const u32x4*)((const T*)p.qi + grow * DI + ks * 32 + lg * 8);
+    qif[ks] = as_v8<V8>(gv ? v : z4);
+  }
+  const float wg = gv ? load_w(p.w, grow, p.w_dtype) : 0.f;
+  // B operand of c = dS^T . Qi for this wave's 16 columns: Qi[g 32*ks + 8*lg + j][16*wave + li]
+  V8 qib[kKlMaxNidx / 32];
+#pragma unroll
+  for (int ks = 0; ks < kKlMaxNidx / 32; ++ks) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int gg = ks * 32 + lg * 8 + j;
+      T v = E::from_f32(0.f);
+      if (gg < p.nidx) v = ((const T*)p.qi)[((int64_t)row * p.nidx + gg) * DI + wave * 16 + li];
+      qib[ks][j] = v;
+    }
+  }
+  for (int e = tid; e < 2 * TILE * kKlDsRow; e += NT) (&s_ds[0][0][0])[e] = E::from_f32(0.f);
+
+  const unsigned char* kb = (const unsigned char*)p.k;
+  const unsigned char* krb = (const unsigned char*)p.kr;
+  const unsigned char* kib = (const unsigned char*)p.ki;
+
+  // ================= pass A: teacher p and index scores I =================
+  u32x4 pre[PF_A];
+  auto load_a = [&](int t) {
+#pragma unroll
+    for (int j = 0; j < PF_A; ++j) {
+      const int e = tid + j * NT;
+      u32x4 v = z4;
+      if (e < NCH_A) {
+        int tk, ch;
+        const unsigned char* base;
+        int64_t rb;
+        if (e < TILE * CN) {
+          tk = e / CN;
+          ch = e - tk * CN;
+          base = kb;
+          rb = ROW;
+        } else if (e < TILE * (CN + CR)) {
+          const int f = e - TILE * CN;
+          tk = f / (CR > 0 ? CR : 1);
+          ch = f - tk * CR;
+          base = krb;
+          rb = DR * 2;
+        } else {
+          const int f = e - TILE * (CN + CR);
+          tk = f / CI;
+          ch = f - tk * CI;
+          base = kib;
+          rb = IROW;
+        }
+        const int k = t * TILE + tk;
+        if (k < n) v = *(const u32x4*)(base + (int64_t)kl_token(p, row, ri.b, k) * rb + ch * 16);
+      }
+      pre[j] = v;
+    }
+  };
+  auto store_a = [&]() {
+#pragma unroll
+    for (int j = 0; j < PF_A; ++j) {
+      const int e = tid + j * NT;
+      if (e < NCH_A) {
+        if (e < TILE * CN) {
+          const int tk = e / CN, ch = e - tk * CN;
+          *(u32x4*)(s_k + tk * ROW + ((ch ^ nope_swz(tk)) * 16)) = pre[j];
+        } else if (e < TILE * (CN + CR)) {
+          const int f = e - TILE * CN;
+          const int tk = f / (CR > 0 ? CR : 1), ch = f - tk * CR;
+          *(u32x4*)(s_kr + tk * (DR * 2) + ((ch ^ rope_swz(tk)) * 16)) = pre[j];
+        } else {
+          const int f = e - TILE * (CN + CR);
+          const int tk = f / CI, ch = f - tk * CI;
+          *(u32x4*)(s_ki + tk * IROW + ((ch ^ nope_swz(tk)) * 16)) = pre[j];
+        }
+      }
+    }
+  };
+
+  load_a(0);
+  for (int t = 0; t < nt; ++t) {
+    lds_barrier();
+    store_a();
+    lds_barrier();
+    if (t + 1 < nt) load_a(t + 1);
+
+    // teacher: S^T[slot][head] = K . Q^T, 16 heads per wave
+    if (wave_heads) {
+      f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          const int tk = tt * 16 + li;
+          const unsigned char* a =
+              ks < KSN ? s_k + tk * ROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16)
+                       : s_kr + tk * (DR * 2) + ((((ks - KSN) * 4 + lg) ^ rope_swz(tk)) * 16);
+          acc[tt] = E::mfma(as_v8<V8>(*(const u32x4*)a), qf[ks], acc[tt]);
+        }
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float pr = hv ? fast_exp2(acc[tt][r] * p.scale_log2 - m2) * inv : 0.f;
+          pr = row16_sum(pr);
+          if (li == 0) s_red[wave][tt * 16 + lg * 4 + r] = pr;
+        }
+    }
+    // index scores: waves 0-3, 16 index heads each
+    if (iwave) {
+      f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int ks = 0; ks < DI / 32; ++ks)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          const int tk = tt * 16 + li;
+          const unsigned char* a = s_ki + tk * IROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16);
+          acc[tt] = E::mfma(as_v8<V8>(*(const u32x4*)a), qif[ks], acc[tt]);
+        }
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v = wg * fmaxf(acc[tt][r], 0.f);
+          v = row16_sum(v);
+          if (li == 0) s_redi[wave][tt * 16 + lg * 4 + r] = v;
+        }
+    }
+    lds_barrier();
+    if (tid < TILE) {
+      const int k = t * TILE + tid;
+      if (k < n) {
+        float ps = 0.f, is = 0.f;
+        for (int w2 = 0; w2 < kKlWaves; ++w2)
+          if (w2 * 16 < p.n1) ps += s_red[w2][tid];
+        for (int w2 = 0; w2 < 4; ++w2)
+          if (w2 * 16 < p.nidx) is += s_redi[w2][tid];
+        s_p[k] = ps * (1.f / (float)p.n1);
+        s_I[k] = is;
+      }
+    }
+  }
+  lds_barrier();
+
+  // ================= pass B: softmax(I), dI, KL =================
+  float mx = -INFINITY;
+  for (int k = tid; k < n; k += NT) mx = fmaxf(mx, s_I[k]);
+  mx = wave_max(mx);
+  if (lane == 0) s_misc[wave] = mx;
+  lds_barrier();
+  mx = s_misc[0];
+#pragma unroll
+  for (int w2 = 1; w2 < kKlWaves; ++w2) mx = fmaxf(mx, s_misc[w2]);
+  float sm = 0.f;
+  for (int k = tid; k < n; k += NT) sm += expf(s_I[k] - mx);
+  sm = wave_sum(sm);
+  lds_barrier();
+  if (lane == 0) s_misc[wave] = sm;
+  lds_barrier();
+  sm = 0.f;
+#pragma unroll
+  for (int w2 = 0; w2 < kKlWaves; ++w2) sm += s_misc[w2];
+  const float inv_sm = 1.f / (sm + 1e-8f);
+  float kl = 0.f, dmax = 0.f;
+  for (int k = tid; k < n; k += NT) {
+    const float si = expf(s_I[k] - mx) * inv_sm;
+    const float pk = s_p[k];
+    const float di = si - pk;
+    const float pc = fmaxf(pk, 1e-8f), sc = fmaxf(si, 1e-8f);
+    kl += pc * (logf(pc) - logf(sc));
+    s_I[k] = di;
+    dmax = fmaxf(dmax, fabsf(di));
+  }
+  kl = wave_sum(kl);
+  dmax = wave_max(dmax);
+  lds_barrier();
+  if (lane == 0) {
+    s_misc[wave] = kl;
+    s_misc[kKlWaves + wave] = dmax;
+  }
+  lds_barrier();
+  if (tid == 0) {
+    float s = 0.f;
+    for (int w2 = 0; w2 < kKlWaves; ++w2) s += s_misc[w2];
+    p.loss_part[row] = s;
+  }
+  // fp16 operands: dS is carried as 2^es * dS so that hi/lo parts stay in
+  // the fp16 normal range; the products are scaled back by 2^-es.
+  float ds_scale = 1.f, ds_unscale = 1.f;
+  if (kF16) {
+    float dm = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < kKlWaves; ++w2) dm = fmaxf(dm, s_misc[kKlWaves + w2]);
+    float wm = fabsf(wg);
+    wm = wave_max(wm);
+    if (lane == 0) s_misc[2 * kKlWaves] = 0.f;
+    lds_barrier();
+    if (lane == 0 && wave < 4) atomicMax((int*)&s_misc[2 * kKlWaves], __float_as_int(wm));
+    lds_barrier();
+    wm = s_misc[2 * kKlWaves];
+    const float bound = dm * wm;
+    int e = 0;
+    if (bound > 0.f) {
+      frexpf(bound, &e);  // bound < 2^e
+      e = 14 - e;         // scaled bound < 2^14
+      e = max(-60, min(60, e));
+    }
+    ds_scale = ldexpf(1.f, e);
+    ds_unscale = ldexpf(1.f, -e);
+  }
+
+  // ================= pass C: dW, dQi, dKi contributions =================
+  f32x4 acc_dqi[DI / 16];
+#pragma unroll
+  for (int dt = 0; dt < DI / 16; ++dt) acc_dqi[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  float dw_acc = 0.f, cmax = 0.f;
+  u32x4 prei;
+  auto load_c = [&](int t) {
+    const int tk = tid / CI, ch = tid - tk * CI;
+    const int k = t * TILE + tk;
+    prei = k < n ? *(const u32x4*)(kib + (int64_t)kl_token(p, row, ri.b, k) * IROW + ch * 16) : z4;
+  };
+  load_c(0);
+  for (int t = 0; t < nt; ++t) {
+    lds_barrier();
+    {
+      const int tk = tid / CI, ch = tid - tk * CI;
+      *(u32x4*)(s_ki + tk * IROW + ((ch ^ nope_swz(tk)) * 16)) = prei;
+    }
+    lds_barrier();
+    if (t + 1 < nt) load_c(t + 1);
+
+    if (iwave) {
+      f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int ks = 0; ks < DI / 32; ++ks)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          const int tk = tt * 16 + li;
+          const unsigned char* a = s_ki + tk * IROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16);
+          acc[tt] = E::mfma(as_v8<V8>(*(const u32x4*)a), qif[ks], acc[tt]);
+        }
+      // dS^T (slot 8*lg + j maps to slot (j>>2)*16 + 4*lg + (j&3)) as B operand
+      V8 dsf, dsl;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int tt = j >> 2, r = j & 3;
+        const int tk = tt * 16 + lg * 4 + r;
+        const int k = t * TILE + tk;
+        const float relu = fmaxf(acc[tt][r], 0.f);
+        const float di = (k < n && gv) ? s_I[k] : 0.f;
+        dw_acc += di * relu;
+        const float ds = relu > 0.f ? di * wg * ds_scale : 0.f;
+        const T hi = E::from_f32(ds);
+        const T lo = E::from_f32(ds - E::to_f32(hi));
+        dsf[j] = hi;
+        dsl[j] = lo;
+        s_ds[0][tk][g] = hi;
+        s_ds[1][tk][g] = lo;
+      }
+      // dQi^T[d][g] += Ki^T[d][slot] . dS^T[slot][g]; Ki^T fragment through
+      // the transposing read: rows 4*lg + li/4 (+16), chunk 2*dt + (li&3)/2
+      const int r1 = lg * 4 + (li >> 2);
+      const int hb = (li & 3) >> 1;
+#pragma unroll
+      for (int dt = 0; dt < DI / 16; ++dt) {
+        const int ch = 2 * dt + hb;
+        const unsigned char* p1 = s_ki + r1 * IROW + ((ch ^ nope_swz(r1)) * 16) + (li & 1) * 8;
+        const unsigned char* p2 = s_ki + (r1 + 16) * IROW + ((ch ^ nope_swz(r1 + 16)) * 16) + (li & 1) * 8;
+        const i16x4 w1 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1));
+        const i16x4 w2 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p2));
+        const i16x8 wv = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
+        acc_dqi[dt] = E::mfma(__builtin_bit_cast(V8, wv), dsf, acc_dqi[dt]);
+        acc_dqi[dt] = E::mfma(__builtin_bit_cast(V8, wv), dsl, acc_dqi[dt]);
+      }
+    }
+    lds_barrier();
+    // c[slot][16*wave + li] = sum_g dS^T[slot][g] Qi[g][16*wave + li]
+    {
+      f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int ks = 0; ks < kKlMaxNidx / 32; ++ks) {
+          const V8 ah = as_v8<V8>(*(const u32x4*)&s_ds[0][tt * 16 + li][ks * 32 + lg * 8]);
+          const V8 al = as_v8<V8>(*(const u32x4*)&s_ds[1][tt * 16 + li][ks * 32 + lg * 8]);
+          acc[tt] = E::mfma(ah, qib[ks], acc[tt]);
+          acc[tt] = E::mfma(al, qib[ks], acc[tt]);
+        }
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int k = t * TILE + tt * 16 + lg * 4 + r;
+          if (k < n) {
+            const float c = acc[tt][r] * ds_unscale;
+            cmax = fmaxf(cmax, fabsf(c));
+            p.cbuf[((int64_t)row * p.topk + k) * DI + wave * 16 + li] = c;
+          }
+        }
+    }
+  }
+
+  // ---- epilogue: dW, dQi, row maximum of |c| ----
+  if (iwave) {
+    const float dwv = xgroup_sum(dw_acc);
+    if (lg == 0 && gv) store_w(p.dw, grow, p.w_dtype, dwv);
+    if (gv) {
+      typedef T T4 __attribute__((ext_vector_type(4)));
+      T* dst = (T*)p.dqi + grow * DI;
+#pragma unroll
+      for (int dt = 0; dt < DI / 16; ++dt) {
+        const T4 o = {E::from_f32(acc_dqi[dt][0] * ds_unscale), E::from_f32(acc_dqi[dt][1] * ds_unscale),
+                      E::from_f32(acc_dqi[dt][2] * ds_unscale), E::from_f32(acc_dqi[dt][3] * ds_unscale)};
+        *(T4*)(dst + dt * 16 + lg * 4) = o;
+      }
+    }
+  }
+  cmax = wave_max(cmax);
+  lds_barrier();
+  if (lane == 0) s_misc[wave] = cmax;
+  lds_barrier();
+  if (tid == 0) {
+    float m = 0.f;
+    for (int w2 = 0; w2 < kKlWaves; ++w2) m = fmaxf(m, s_misc[w2]);
+    p.rowmax[row] = m;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dKi: bucket slots by target token, then a fixed-point sum per token
+// ---------------------------------------------------------------------------
+struct KlScatter {
+  const int32_t* idx;
+  const int32_t* act_q;
+  const int32_t* act_k;
+  int32_t* cnt;     // [tokens]
+  int32_t* offs;    // [tokens + 1]
+  int32_t* cur;     // [tokens]
+  int32_t* list;    // [rows * topK]
+  int32_t batch, s1, s2, topk;
+};
+
+__global__ __launch_bounds__(256) void kl_zero_kernel(int32_t* a, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) a[i] = 0;
+}
+
+template <bool FILL>
+__global__ __launch_bounds__(256) void kl_bucket_kernel(KlScatter s) {
+  const int row = blockIdx.x;
+  const int k = blockIdx.y * 256 + threadIdx.x;
+  const int b = row / s.s1, s1 = row - b * s.s1;
+  const int aq = s.act_q ? s.act_q[b] : s.s1;
+  const int ak = s.act_k ? s.act_k[b] : s.s2;
+  const int n = s1 < aq ? min(s.topk, max(ak - aq + s1 + 1, 0)) : 0;
+  if (k >= n) return;
+  const int ti = s.idx[(int64_t)row * s.topk + k];
+  const int t = b * s.s2 + min(max(ti, 0), s.s2 - 1);
+  if (!FILL) {
+    atomicAdd(&s.cnt[t], 1);
+  } else {
+    const int pos = s.offs[t] + atomicAdd(&s.cur[t], 1);
+    s.list[pos] = row * s.topk + k;
+  }
+}
+
+// exclusive scan of cnt[0..n) into offs[0..n] (one workgroup)
+__global__ __launch_bounds__(1024) void kl_scan_kernel(const int32_t* cnt, int32_t* offs, int n) {
+  __shared__ int32_t s_sum[1024];
+  const int tid = threadIdx.x;
+  const int per = (n + 1023) / 1024;
+  const int lo = min(n, tid * per), hi = min(n, lo + per);
+  int32_t s = 0;
+  for (int i = lo; i < hi; ++i) s += cnt[i];
+  s_sum[tid] = s;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    const int32_t v = tid >= o ? s_sum[tid - o] : 0;
+    __syncthreads();
+    s_sum[tid] += v;
+    __syncthreads();
+  }
+  int32_t run = tid > 0 ? s_sum[tid - 1] : 0;
+  for (int i = lo; i < hi; ++i) {
+    offs[i] = run;
+    run += cnt[i];
+  }
+  if (tid == 1023) offs[n] = s_sum[1023];
+}
+
+// one wave per token: dKi[t] = sum of its slots' contributions, in int64 fixed point
+template <typename T>
+__global__ __launch_bounds__(256) void kl_reduce_kernel(const float* cbuf, const float* rowmax,
+                                                        const int32_t* offs, const int32_t* list, T* dki,
+                                                        int ntok, int topk) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (t >= ntok) return;
+  const int o0 = offs[t], len = offs[t + 1] - o0;
+  float bm = 0.f;
+  for (int i = lane; i < len; i += 64) bm = fmaxf(bm, rowmax[list[o0 + i] / topk]);
+  bm = wave_max(bm);
+  long long a0 = 0, a1 = 0;
+  int e = 0;
+  T* dst = dki + (int64_t)t * kKlDi + 2 * lane;
+  if (!(bm < INFINITY)) {  // non-finite contributions: no fixed-point scale exists
+    dst[0] = Elem<T>::from_f32(NAN);
+    dst[1] = Elem<T>::from_f32(NAN);
+    return;
+  }
+  if (bm > 0.f) {
+    int ex;
+    frexp((double)bm * (double)len, &ex);  // len * bm < 2^ex
+    e = 62 - ex;
+    const double sc = ldexp(1.0, e);
+    int i = 0;
+    for (; i + 4 <= len; i += 4) {
+      float2 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = *(const float2*)(cbuf + (int64_t)list[o0 + i + u] * kKlDi + 2 * lane);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        a0 += __double2ll_rn((double)v[u].x * sc);
+        a1 += __double2ll_rn((double)v[u].y * sc);
+      }
+    }
+    for (; i < len; ++i) {
+      const float2 v = *(const float2*)(cbuf + (int64_t)list[o0 + i] * kKlDi + 2 * lane);
+      a0 += __double2ll_rn((double)v.x * sc);
+      a1 += __double2ll_rn((double)v.y * sc);
+    }
+  }
+  const double us = ldexp(1.0, -e);
+  dst[0] = Elem<T>::from_f32((float)((double)a0 * us));
+  dst[1] = Elem<T>::from_f32((float)((double)a1 * us));
+}
+
+// loss = sum of the per-row terms, in a fixed order (one workgroup)
+__global__ __launch_bounds__(256) void kl_loss_kernel(const float* part, int rows, float* loss) {
+  __shared__ double s[256];
+  double a = 0.0;
+  for (int i = threadIdx.x; i < rows; i += 256) a += (double)part[i];
+  s[threadIdx.x] = a;
+  __syncthreads();
+  for (int o = 128; o >= 1; o >>= 1) {
+    if ((int)threadIdx.x < o) s[threadIdx.x] += s[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) loss[0] = (float)s[0];
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct KlWs {
+  size_t cbuf, rowmax, loss, cnt, offs, cur, list, total;
+};
+
+static KlWs kl_ws_layout(int64_t rows, int64_t tokens, int64_t topk) {
+  KlWs w;
+  size_t o = 0;
+  w.cbuf = o;
+  o += align256((size_t)rows * topk * kKlDi * sizeof(float));
+  w.rowmax = o;
+  o += align256((size_t)rows * sizeof(float));
+  w.loss = o;
+  o += align256((size_t)rows * sizeof(float));
+  w.cnt = o;
+  o += align256((size_t)tokens * sizeof(int32_t));
+  w.cur = o;
+  o += align256((size_t)tokens * sizeof(int32_t));
+  w.offs = o;
+  o += align256((size_t)(tokens + 1) * sizeof(int32_t));
+  w.list = o;
+  o += align256((size_t)rows * topk * sizeof(int32_t));
+  w.total = o;
+  return w;
+}
+
+size_t kl_bwd_workspace_bytes(int64_t batch, int64_t s1, int64_t s2, int64_t topk) {
+  return kl_ws_layout(batch * s1, batch * s2, topk).total;
+}
+
+size_t kl_bwd_lds_bytes(int64_t topk) { return (size_t)2 * topk * sizeof(float); }
+int kl_bwd_max_topk() { return kKlMaxTopk; }
+int kl_bwd_max_nidx() { return kKlMaxNidx; }
+
+// the row kernel's dynamic LDS (I and p of a row) may exceed the default
+// dynamic limit: raise it once per instantiation
+template <int D, int DR, typename T>
+static hipError_t kl_row_lds_attr() {
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)kl_bwd_row_kernel<D, DR, T>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)(2 * kKlMaxTopk * 4));
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  return hipSuccess;
+}
+
+template <int D, int DR, typename T>
+static hipError_t run_kl_row(const KlParams& p, int rows, size_t dyn, hipStream_t stream) {
+  hipError_t e = kl_row_lds_attr<D, DR, T>();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((kl_bwd_row_kernel<D, DR, T>), dim3(rows), dim3(kKlWaves * 64), dyn, stream, p);
+  return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t dispatch_kl_row(const KlParams& p, int rows, int d, int dr, size_t dyn, hipStream_t stream) {
+  if (dr == 64) {
+    if (d == 128) return run_kl_row<128, 64, T>(p, rows, dyn, stream);
+    if (d == 256) return run_kl_row<256, 64, T>(p, rows, dyn, stream);
+    return run_kl_row<512, 64, T>(p, rows, dyn, stream);
+  }
+  if (d == 128) return run_kl_row<128, 0, T>(p, rows, dyn, stream);
+  if (d == 256) return run_kl_row<256, 0, T>(p, rows, dyn, stream);
+  return run_kl_row<512, 0, T>(p, rows, dyn, stream);
+}
+
+int kl_bwd_run(const void* query, const void* key, const void* query_rope, const void* key_rope,
+               const void* query_index, const void* key_index, const void* weights, const int32_t* sparse_indices,
+               const float* softmax_max, const float* softmax_sum, const int32_t* act_q, const int32_t* act_k,
+               void* d_query_index, void* d_key_index, void* d_weights, float* loss, int64_t batch, int64_t s1,
+               int64_t s2, int64_t n1, int64_t d, int64_t d_rope, int64_t nidx, int64_t topk, int32_t dtype,
+               int32_t w_dtype, float scale_value, void* workspace, hipStream_t stream) {
+  const int64_t rows = batch * s1, tokens = batch * s2;
+  const KlWs L = kl_ws_layout(rows, tokens, topk);
+  unsigned char* ws = (unsigned char*)workspace;
+  KlParams p;
+  p.q = query;
+  p.qr = query_rope;
+  p.k = key;
+  p.kr = key_rope;
+  p.qi = query_index;
+  p.ki = key_index;
+  p.w = weights;
+  p.idx = sparse_indices;
+  p.smax = softmax_max;
+  p.ssum = softmax_sum;
+  p.act_q = act_q;
+  p.act_k = act_k;
+  p.dqi = d_query_index;
+  p.dw = d_weights;
+  p.cbuf = (float*)(ws + L.cbuf);
+  p.rowmax = (float*)(ws + L.rowmax);
+  p.loss_part = (float*)(ws + L.loss);
+  p.batch = (int32_t)batch;
+  p.s1 = (int32_t)s1;
+  p.s2 = (int32_t)s2;
+  p.n1 = (int32_t)n1;
+  p.nidx = (int32_t)nidx;
+  p.topk = (int32_t)topk;
+  p.w_dtype = w_dtype;
+  p.scale_log2 = scale_value * kLog2e;
+
+  KlScatter s;
+  s.idx = sparse_indices;
+  s.act_q = act_q;
+  s.act_k = act_k;
+  s.cnt = (int32_t*)(ws + L.cnt);
+  s.offs = (int32_t*)(ws + L.offs);
+  s.cur = (int32_t*)(ws + L.cur);
+  s.list = (int32_t*)(ws + L.list);
+  s.batch = (int32_t)batch;
+  s.s1 = (int32_t)s1;
+  s.s2 = (int32_t)s2;
+  s.topk = (int32_t)topk;
+
+  // counters cleared by a kernel (no memset nodes when the caller captures)
+  const int64_t zn = (int64_t)((L.offs - L.cnt) / sizeof(int32_t));
+  hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((zn + 255) / 256)), dim3(256), 0, stream, s.cnt, zn);
+  DSA_HIP(hipGetLastError());
+  const size_t dyn = kl_bwd_lds_bytes(topk);
+  const bool bf = dtype == DSA_DTYPE_BF16;
+  DSA_HIP(bf ? dispatch_kl_row<bf16>(p, (int)rows, (int)d, (int)d_rope, dyn, stream)
+             : dispatch_kl_row<f16>(p, (int)rows, (int)d, (int)d_rope, dyn, stream));
+  const dim3 bgrid((unsigned)rows, (unsigned)((topk + 255) / 256));
+  hipLaunchKernelGGL(kl_bucket_kernel<false>, bgrid, dim3(256), 0, stream, s);
+  DSA_HIP(hipGetLastError());
+  hipLaunchKernelGGL(kl_scan_kernel, dim3(1), dim3(1024), 0, stream, s.cnt, s.offs, (int)tokens);
+  DSA_HIP(hipGetLastError());
+  hipLaunchKernelGGL(kl_bucket_kernel<true>, bgrid, dim3(256), 0, stream, s);
+  DSA_HIP(hipGetLastError());
+  const dim3 rgrid((unsigned)((tokens + 3) / 4));
+  if (bf)
+    hipLaunchKernelGGL(kl_reduce_kernel<bf16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowmax, s.offs, s.list,
+                       (bf16*)d_key_index, (int)tokens, (int)topk);
+  else
+    hipLaunchKernelGGL(kl_reduce_kernel<f16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowmax, s.offs, s.list,
+                       (f16*)d_key_index, (int)tokens, (int)topk);
+  DSA_HIP(hipGetLastError());
+  hipLaunchKernelGGL(kl_loss_kernel, dim3(1), dim3(256), 0, stream, p.loss_part, (int)rows, loss);
+  DSA_HIP(hipGetLastError());
+  return DSA_OK;
+}
+
+}  // namespace dsa

@@ -111,6 +111,39 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
 size_t dsa_sfa_bwd_workspace_size(int64_t kv_rows, int64_t d);
 
 /*
+ * Sparse lightning-indexer KL-loss backward.  Replaces the reference core
+ * `_sparse_lightning_indexer_grad_kl_loss_core`
+ * (sparse_lightning_indexer_grad_kl_loss_triton.py:355-464), i.e. its gather
+ * (39-71), fused KL / dQi / dW kernel (74-263), dKi scatter (266-317) and
+ * cast (320-327).  BSND only, N2 = Nidx2 = 1, sparse_mode 3 (the API guards,
+ * 534-538).  query [B,S1,N1,D], key [B,S2,1,D], query_rope [B,S1,N1,d_rope]
+ * and key_rope [B,S2,1,d_rope] (d_rope 0 = no rope, both NULL),
+ * query_index [B,S1,Nidx1,d_idx], key_index [B,S2,1,d_idx], weights
+ * [B,S1,Nidx1] (dtype weights_dtype), sparse_indices [B,S1,1,topK],
+ * softmax_max / softmax_sum [B,1,S1,N1] fp32, actual_seq_qlen /
+ * actual_seq_klen [B] (NULL = full lengths).  Writes d_query_index (query
+ * index dtype), d_key_index (key index dtype), d_weights (weights dtype)
+ * and loss[1] fp32 (sum over rows).  dKi is reduced without atomics in a
+ * fixed-point sum, so every output is deterministic.  The workspace
+ * (dsa_kl_bwd_workspace_size) holds rows * topK * d_idx fp32 slot
+ * contributions and the token buckets.  query/key/rope/index tensors share
+ * one dtype (bf16 or fp16); D in {128, 256, 512}; d_idx = 128;
+ * Nidx1 <= 64; N1 <= 128; topK <= 8192.
+ */
+int dsa_kl_bwd(const void* query, const void* key, const void* query_rope, const void* key_rope,
+               const void* query_index, const void* key_index, const void* weights,
+               const int32_t* sparse_indices, const float* softmax_max, const float* softmax_sum,
+               const int32_t* actual_seq_qlen, const int32_t* actual_seq_klen, void* d_query_index,
+               void* d_key_index, void* d_weights, float* loss, int64_t batch, int64_t s1, int64_t s2,
+               int64_t n1, int64_t d, int64_t d_rope, int64_t n_idx, int64_t d_idx, int64_t sparse_count,
+               int32_t dtype, int32_t weights_dtype, float scale_value, void* workspace,
+               size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of dsa_kl_bwd. */
+size_t dsa_kl_bwd_workspace_size(int64_t batch, int64_t s1, int64_t s2, int64_t sparse_count,
+                                 int64_t d_idx);
+
+/*
  * Lightning indexer: scores + stable top-k.  Replaces the reference core
  * `_lightning_indexer_score_core` (lightning_indexer_triton.py:382-413) and the
  * top-k after it (`_stable_topk`, 339-357, called at 539), with the stable

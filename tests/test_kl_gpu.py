@@ -1,0 +1,241 @@
+"""GPU parity of the HIP indexer KL-loss backward against the oracle.
+
+Inputs follow the reference test recipe (test_sli_grad_kl_loss_triton.py:
+26-70): RandomState(42) randn rounded to fp16 and then to the I/O dtype,
+|randn| weights, and its index patterns (random, causal_random, continuous,
+repeated, causal_continuous).  The teacher statistics are the dense causal
+softmax max / sum over all S2 keys (test_sli_grad_kl_loss_triton.py:79-116;
+computed here in fp64 without the fp16 rounding of the scores: the stats
+are inputs of the operator, and the oracle is fed the same arrays).
+
+Expected values: ``oracle.kl.kl_loss_bwd`` in fp64 with the device kernel's
+semantics (no rounding of dot products, out-of-range targets clamped:
+sparse_lightning_indexer_grad_kl_loss_triton.py:63, 300).  Tolerances: the
+outputs are computed in fp32 with split-precision MFMA operands, so dW
+(fp32 out) and the loss are checked at rtol 1e-3, and dQi / dKi (rounded
+to the I/O dtype) at rtol 1e-2 with atol 1e-3 of the tensor's largest
+magnitude (their entries span several orders of magnitude; the reference's
+own comparison uses atol = rtol = 1e-2 absolute, lines 9-10).  An
+absolute floor covers fp32's resolution of dI = softmax(I) - p: both terms
+are O(1) probabilities with an ulp near 6e-8, so a row whose exact dI is
+~1e-8 (a single slot: sI = 1/(1 + 1e-8) rounds to 1 in fp32) gets dI = 0;
+dQi / dKi carry dI times |w|.|ki| (<~ 10), dW carries dI times ReLU scores
+(<~ 100).
+"""
+ATOL_DQ = 1e-6
+ATOL_DW = 1e-5
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.kl import kl_loss_bwd
+from tests.helpers import assert_close, to_dtype_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _indices(B, S1, S2, topK, pattern, rng):
+    if pattern == "random":
+        return rng.randint(0, S2, (B, S1, 1, topK)).astype(np.int32)
+    si = np.zeros((B, S1, 1, topK), np.int32)
+    if pattern == "causal_random":
+        for b in range(B):
+            for s1 in range(S1):
+                vis = min(max(S2 - S1 + s1 + 1, 1), S2)
+                n = min(topK, vis)
+                si[b, s1, 0, :n] = rng.choice(vis, size=n, replace=False)
+    elif pattern == "continuous":
+        si[:] = (np.arange(topK) % S2).astype(np.int32)
+    elif pattern == "repeated":
+        row = np.zeros(topK, np.int32)
+        row[1::2] = min(S2 - 1, 7)
+        si[:] = row
+    elif pattern == "causal_continuous":
+        for s1 in range(S1):
+            vis = min(max(S2 - S1 + s1 + 1, 1), S2)
+            n = min(topK, vis)
+            si[:, s1, 0, :n] = np.arange(n)
+    else:
+        raise ValueError(pattern)
+    return si
+
+
+def _dense_stats(q, k, qr, kr, scale, act_q, act_k):
+    B, S1, N1, _ = q.shape
+    S2 = k.shape[1]
+    smax = np.full((B, 1, S1, N1), -np.inf, np.float32)
+    ssum = np.zeros((B, 1, S1, N1), np.float32)
+    for b in range(B):
+        for s1 in range(S1):
+            if s1 >= act_q[b]:
+                continue
+            lim = min(max(act_k[b] - act_q[b] + s1 + 1, 0), S2)
+            if lim <= 0:
+                continue
+            s = q[b, s1].astype(np.float64) @ k[b, :lim, 0].T.astype(np.float64)
+            if qr is not None:
+                s = s + qr[b, s1].astype(np.float64) @ kr[b, :lim, 0].T.astype(np.float64)
+            s = s * scale
+            m = s.max(1)
+            smax[b, 0, s1] = m
+            ssum[b, 0, s1] = np.exp(s - m[:, None]).sum(1)
+    return smax, ssum
+
+
+def _gpu_stats(q, k, qr, kr, scale):
+    """Dense causal stats (full lengths) in fp32 on the GPU, for shapes where
+    the host loop is too slow."""
+    B, S1, N1, _ = q.shape
+    S2 = k.shape[1]
+    smax = np.zeros((B, 1, S1, N1), np.float32)
+    ssum = np.zeros((B, 1, S1, N1), np.float32)
+    for b in range(B):
+        kk = torch.from_numpy(np.concatenate([k[b, :, 0], kr[b, :, 0]], 1)).cuda()
+        for r0 in range(0, S1, 64):
+            qq = torch.from_numpy(np.concatenate([q[b, r0:r0 + 64], qr[b, r0:r0 + 64]], 2)).cuda()
+            s = torch.matmul(qq, kk.T) * scale                      # [rows, N1, S2]
+            lim = torch.arange(r0, r0 + qq.shape[0], device="cuda") + (S2 - S1) + 1
+            mask = torch.arange(S2, device="cuda")[None, :] >= lim[:, None]
+            s = s.masked_fill(mask[:, None, :], float("-inf"))
+            m = s.amax(-1)
+            smax[b, 0, r0:r0 + qq.shape[0]] = m.cpu().numpy()
+            ssum[b, 0, r0:r0 + qq.shape[0]] = torch.exp(s - m[..., None]).sum(-1).cpu().numpy()
+    return smax, ssum
+
+
+def _case(B, S1, S2, N1, D, Ni, topK, dtype, pattern="causal_random", rope=True, w_dtype=torch.float32,
+          act_q=None, act_k=None, seed=42, gpu_stats=False):
+    rng = np.random.RandomState(seed)
+    f = lambda *s: to_dtype_np(rng.randn(*s).astype(np.float16).astype(np.float32), dtype)  # noqa: E731
+    q, k = f(B, S1, N1, D), f(B, S2, 1, D)
+    qr, kr = (f(B, S1, N1, 64), f(B, S2, 1, 64)) if rope else (None, None)
+    qi, ki = f(B, S1, Ni, 128), f(B, S2, 1, 128)
+    w = to_dtype_np(np.abs(rng.randn(B, S1, Ni)).astype(np.float32), w_dtype)
+    si = _indices(B, S1, S2, topK, pattern, rng)
+    aq = [S1] * B if act_q is None else list(act_q)
+    ak = [S2] * B if act_k is None else list(act_k)
+    scale = 1.0 / math.sqrt(D + (64 if rope else 0))
+    if gpu_stats:
+        smax, ssum = _gpu_stats(q, k, qr, kr, scale)
+    else:
+        smax, ssum = _dense_stats(q, k, qr, kr, scale, aq, ak)
+    return dict(q=q, k=k, qr=qr, kr=kr, qi=qi, ki=ki, w=w, si=si, smax=smax, ssum=ssum, scale=scale,
+                aq=aq, ak=ak, dtype=dtype, w_dtype=w_dtype, explicit_len=act_q is not None or act_k is not None)
+
+
+def _run_gpu(c):
+    import dsa_triton_ascend_amd as dsa
+    d = lambda x, dt: None if x is None else torch.from_numpy(np.ascontiguousarray(x)).to(  # noqa: E731
+        device="cuda", dtype=dt)
+    dt = c["dtype"]
+    res = dsa.sparse_lightning_indexer_grad_kl_loss_triton(
+        d(c["q"], dt), d(c["k"], dt), d(c["qi"], dt), d(c["ki"], dt), d(c["w"], c["w_dtype"]),
+        d(c["si"], torch.int32), d(c["smax"], torch.float32), d(c["ssum"], torch.float32),
+        query_rope=d(c["qr"], dt), key_rope=d(c["kr"], dt),
+        actual_seq_qlen=c["aq"] if c["explicit_len"] else None,
+        actual_seq_klen=c["ak"] if c["explicit_len"] else None, scale_value=c["scale"])
+    torch.cuda.synchronize()
+    return [r.float().cpu().numpy() for r in res]
+
+
+def _oracle(c, rows=None):
+    B, S1, N1 = c["q"].shape[:3]
+    S2 = c["k"].shape[1]
+    qr = c["qr"] if c["qr"] is not None else np.zeros((B, S1, N1, 1), np.float32)
+    kr = c["kr"] if c["kr"] is not None else np.zeros((B, S2, 1, 1), np.float32)
+    return kl_loss_bwd(c["q"], c["k"], qr, kr, c["qi"], c["ki"], c["w"], c["si"], c["smax"], c["ssum"],
+                       c["scale"], c["aq"], c["ak"], input_dtype=None, round_dots=False, dki_oob="clamp",
+                       rows=rows, compute_dtype=np.float64)
+
+
+def _check(got, exp, what, w_dtype=torch.float32):
+    dqi, dki, dw, loss = got
+    rt_w = 1e-3 if w_dtype == torch.float32 else 1e-2  # dW is stored in the weights dtype
+    assert np.isfinite(dqi).all() and np.isfinite(dki).all() and np.isfinite(dw).all()
+    for g, e, nm in ((dqi, exp["dQueryIndex"], "dQueryIndex"), (dki, exp["dKeyIndex"], "dKeyIndex")):
+        assert_close(g, e, 1e-2, 1e-3 * float(np.abs(e).max()) + ATOL_DQ, f"{what} {nm}")
+    assert_close(dw, exp["dW"], rt_w, 1e-5 * float(np.abs(exp["dW"]).max()) + ATOL_DW, f"{what} dW")
+    assert_close(loss, exp["loss"], 1e-3, 1e-6, f"{what} loss")
+
+
+CASES = [
+    # B, S1, S2, N1, D, Nidx1, topK, pattern
+    (1, 4, 256, 32, 512, 8, 128, "causal_random"),
+    (1, 8, 192, 16, 128, 16, 64, "random"),
+    (1, 6, 96, 8, 256, 12, 64, "continuous"),
+    (1, 5, 64, 32, 128, 8, 40, "repeated"),
+    (2, 7, 80, 64, 512, 64, 48, "causal_continuous"),
+    (1, 33, 33, 128, 512, 64, 32, "causal_random"),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("case", CASES, ids=[f"b{c[0]}s{c[1]}k{c[2]}n{c[3]}d{c[4]}i{c[5]}K{c[6]}{c[7]}"
+                                             for c in CASES])
+def test_kl_matches_oracle(case, dtype):
+    B, S1, S2, N1, D, Ni, topK, pattern = case
+    print(f"[kl_bwd] {case} {dtype}", flush=True)
+    c = _case(B, S1, S2, N1, D, Ni, topK, dtype, pattern)
+    _check(_run_gpu(c), _oracle(c), f"case {case}")
+
+
+def test_kl_no_rope_bf16_weights_and_lengths():
+    """Missing rope (zeros, API lines 543-546), bf16 weights, shorter actual
+    lengths (inactive rows and rows with no visible key)."""
+    print("[kl_bwd] no rope / bf16 weights / act lengths", flush=True)
+    c = _case(2, 9, 70, 16, 256, 16, 48, torch.bfloat16, "random", rope=False, w_dtype=torch.bfloat16,
+              act_q=[9, 6], act_k=[70, 4])
+    got = _run_gpu(c)
+    exp = _oracle(c)
+    _check(got, exp, "no-rope", torch.bfloat16)
+    assert np.all(got[0][1, 6:] == 0) and np.all(got[2][1, 6:] == 0)  # rows s1 >= act_q
+
+
+def test_kl_topk_larger_than_window():
+    """topK above the visible window: only the first n slots count (kernel line 107)."""
+    print("[kl_bwd] topK > window", flush=True)
+    c = _case(1, 6, 40, 16, 128, 8, 64, torch.bfloat16, "causal_random")
+    _check(_run_gpu(c), _oracle(c), "topK>window")
+
+
+def test_kl_deterministic():
+    """Two calls give bit-identical outputs (no atomics in the dKi reduction)."""
+    print("[kl_bwd] determinism", flush=True)
+    c = _case(1, 40, 48, 32, 128, 16, 32, torch.bfloat16, "causal_random")
+    a = _run_gpu(c)
+    b = _run_gpu(c)
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+
+
+def test_kl_large_rows_sampled():
+    """A larger shape (N1=128, D=512, Nidx1=64, topK=1024): dQi / dW of
+    sampled rows against the oracle, loss finite and >= 0."""
+    print("[kl_bwd] large sampled", flush=True)
+    c = _case(1, 1100, 1100, 128, 512, 64, 1024, torch.bfloat16, "causal_continuous", gpu_stats=True)
+    got = _run_gpu(c)
+    rows = [(0, 0), (0, 517), (0, 1023), (0, 1099)]
+    exp = _oracle(c, rows=rows)
+    for _, s1 in rows:
+        e = exp["dQueryIndex"][0, s1]
+        assert_close(got[0][0, s1], e, 1e-2, 1e-3 * float(np.abs(e).max()) + ATOL_DQ, f"row {s1} dQueryIndex")
+        e = exp["dW"][0, s1]
+        assert_close(got[2][0, s1], e, 1e-3, 1e-5 * float(np.abs(e).max()) + ATOL_DW, f"row {s1} dW")
+    assert np.isfinite(got[1]).all() and float(got[3][0]) >= 0.0
+
+
+def test_kl_guards():
+    import dsa_triton_ascend_amd as dsa
+    z = lambda *s: torch.zeros(*s, dtype=torch.bfloat16, device="cuda")  # noqa: E731
+    q, k, qi, ki = z(1, 2, 4, 128), z(1, 8, 1, 128), z(1, 2, 4, 128), z(1, 8, 1, 128)
+    w = torch.zeros(1, 2, 4, device="cuda")
+    si = torch.zeros(1, 2, 1, 4, dtype=torch.int32, device="cuda")
+    st = torch.zeros(1, 1, 2, 4, device="cuda")
+    with pytest.raises(ValueError):
+        dsa.sparse_lightning_indexer_grad_kl_loss_triton(q, k, qi, ki, w, si, st, st, layout="TND")
+    with pytest.raises(ValueError):
+        dsa.sparse_lightning_indexer_grad_kl_loss_triton(q, k, qi, ki, w, si, st, st, sparse_mode=0)
+    with pytest.raises(AssertionError):
+        dsa.sparse_lightning_indexer_grad_kl_loss_triton(q, k, qi, ki, w, si.reshape(1, 1, 2, 4), st, st)
