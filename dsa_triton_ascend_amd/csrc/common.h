@@ -57,6 +57,22 @@ __device__ __forceinline__ V as_v8(u32x4 x) { return __builtin_bit_cast(V, x); }
 template <typename V>
 __device__ __forceinline__ u32x4 as_u4(V x) { return __builtin_bit_cast(u32x4, x); }
 
+// v_mfma_f32_16x16x16 (bf16 / fp16): A lane l holds A[l%16][4*(l/16) + j],
+// B lane l holds B[4*(l/16) + j][l%16], C register r holds C[4*(l/16) + r][l%16].
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+template <typename T> struct Mfma16;
+template <> struct Mfma16<bf16> {
+  static __device__ __forceinline__ f32x4 run(s16x4 a, s16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<f16> {
+  static __device__ __forceinline__ f32x4 run(s16x4 a, s16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c,
+                                                 0, 0, 0);
+  }
+};
+
 // Hardware exp2 (v_exp_f32); callers keep arguments <= 0 or -inf.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -66,6 +66,30 @@ constexpr int kKlMaxNidx = 64;
 constexpr int kKlMaxTopk = 8192;
 constexpr int kKlDsRow = kKlMaxNidx + 8;  // padded LDS row of dS^T (elements)
 
+// x = hi + mid + lo exactly (bf16 parts of an fp32 value: 8 + 8 + 8 bits),
+// as the A operand of a 16x16x16 product whose k index is this lane's r
+struct Split3 {
+  s16x4 h, m, l;
+};
+__device__ __forceinline__ void split3_set(Split3& s, int r, float x) {
+  const bf16 h = (bf16)x;
+  const float r1 = x - (float)h;
+  const bf16 m = (bf16)r1;
+  const bf16 l = (bf16)(r1 - (float)m);
+  s.h[r] = __builtin_bit_cast(short, h);
+  s.m[r] = __builtin_bit_cast(short, m);
+  s.l[r] = __builtin_bit_cast(short, l);
+}
+// sum over k of A[row][k] (rows = MFMA rows of the A operand), all 16
+// output columns equal: B = ones
+__device__ __forceinline__ f32x4 split3_rowsum(const Split3& s) {
+  const short one = __builtin_bit_cast(short, (bf16)1.f);
+  const s16x4 ones = {one, one, one, one};
+  f32x4 c = Mfma16<bf16>::run(s.h, ones, (f32x4){0.f, 0.f, 0.f, 0.f});
+  c = Mfma16<bf16>::run(s.m, ones, c);
+  return Mfma16<bf16>::run(s.l, ones, c);
+}
+
 struct KlRow {
   int b, s1, n;
   bool active;
@@ -99,15 +123,6 @@ __device__ __forceinline__ void store_w(void* w, int64_t i, int dt, float v) {
   else ((f16*)w)[i] = (f16)v;
 }
 
-// sum over the 16 lanes of each 16-lane group
-__device__ __forceinline__ float row16_sum(float v) {
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 8);
-  return v;
-}
-
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
@@ -130,21 +145,24 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   constexpr int ROW = D * 2;            // K row bytes in LDS
   constexpr int IROW = DI * 2;          // K_index row bytes
   constexpr int CN = D / 8, CR = DR / 8, CI = DI / 8;  // 16-byte chunks per row
-  constexpr int NCH_A = TILE * (CN + CR + CI);
-  constexpr int PF_A = (NCH_A + NT - 1) / NT;
-  static_assert(TILE * CI == NT, "one K_index chunk per thread");
+  // gather assignment per tile: K chunks NJ_N per thread; the 256 rope
+  // chunks on threads 0-255; one K_index chunk per thread
+  constexpr int NJ_N = TILE * CN / NT;
+  static_assert(TILE * CN == NJ_N * NT && TILE * CI == NT && TILE * CR <= NT, "gather assignment");
   constexpr bool kF16 = __is_same(T, f16);
 
   __shared__ __attribute__((aligned(16))) unsigned char s_k[TILE * ROW];
   __shared__ __attribute__((aligned(16))) unsigned char s_kr[DR > 0 ? TILE * DR * 2 : 16];
   __shared__ __attribute__((aligned(16))) unsigned char s_ki[TILE * IROW];
-  __shared__ float s_red[kKlWaves][TILE];
-  __shared__ float s_redi[4][TILE];
+  __shared__ __attribute__((aligned(16))) float s_red[kKlWaves][TILE];
+  __shared__ __attribute__((aligned(16))) float s_redi[4][TILE];
   __shared__ __attribute__((aligned(16))) T s_ds[2][TILE][kKlDsRow];  // dS^T hi / lo: [slot][g]
   __shared__ float s_misc[2 * kKlWaves + 4];
-  extern __shared__ float s_dyn[];  // I (then dI) and p of the row: 2 x topK floats
+  // dynamic: I (then dI) and p of the row, and its clamped token rows
+  extern __shared__ float s_dyn[];
   float* s_I = s_dyn;
   float* s_p = s_dyn + p.topk;
+  int* s_tok = (int*)(s_dyn + 2 * p.topk);
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -180,10 +198,15 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     else v = *(const u32x4*)((const T*)p.qr + hrow * DR + (ks - KSN) * 32 + lg * 8);
     qf[ks] = as_v8<V8>(hv ? v : z4);
   }
-  float m2 = 0.f, inv = 0.f;
-  if (hv) {
-    m2 = p.smax[hrow] * kLog2e;
-    inv = 1.f / (p.ssum[hrow] + 1e-8f);
+  // pass A scores heads on MFMA rows: this lane's heads are 16*wave + 4*lg + r
+  float m2r[4], invr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int h = wave * 16 + lg * 4 + r;
+    const bool v = h < p.n1;
+    const int64_t hr = (int64_t)row * p.n1 + (v ? h : 0);
+    m2r[r] = v ? p.smax[hr] * kLog2e : 0.f;
+    invr[r] = v ? 1.f / (p.ssum[hr] + 1e-8f) : 0.f;  // 0 also masks heads >= N1
   }
   // index heads: waves 0-3, g = 16*wave + li
   const bool iwave = wave < 4 && wave * 16 < p.nidx;
@@ -197,6 +220,12 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     qif[ks] = as_v8<V8>(gv ? v : z4);
   }
   const float wg = gv ? load_w(p.w, grow, p.w_dtype) : 0.f;
+  float wr[4];  // weights of index heads 16*wave + 4*lg + r (pass A layout)
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int gg = wave * 16 + lg * 4 + r;
+    wr[r] = (iwave && gg < p.nidx) ? load_w(p.w, (int64_t)row * p.nidx + gg, p.w_dtype) : 0.f;
+  }
   // B operand of c = dS^T . Qi for this wave's 16 columns: Qi[g 32*ks + 8*lg + j][16*wave + li]
   V8 qib[kKlMaxNidx / 32];
 #pragma unroll
@@ -210,64 +239,54 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     }
   }
   for (int e = tid; e < 2 * TILE * kKlDsRow; e += NT) (&s_ds[0][0][0])[e] = E::from_f32(0.f);
+  // per-wave partial sums of a tile; waves without heads keep zeros
+  for (int e = tid; e < kKlWaves * TILE; e += NT) (&s_red[0][0])[e] = 0.f;
+  for (int e = tid; e < 4 * TILE; e += NT) (&s_redi[0][0])[e] = 0.f;
 
   const unsigned char* kb = (const unsigned char*)p.k;
   const unsigned char* krb = (const unsigned char*)p.kr;
   const unsigned char* kib = (const unsigned char*)p.ki;
 
   // ================= pass A: teacher p and index scores I =================
-  u32x4 pre[PF_A];
+  for (int k = tid; k < n; k += NT) s_tok[k] = kl_token(p, row, ri.b, k);
+  __syncthreads();
+
+  // per tile: K rows (NJ_N chunks per thread), rope rows (threads < 256),
+  // K_index rows (one chunk per thread); slots >= n read as zeros
+  u32x4 pre_n[NJ_N], pre_r, pre_i;
   auto load_a = [&](int t) {
 #pragma unroll
-    for (int j = 0; j < PF_A; ++j) {
+    for (int j = 0; j < NJ_N; ++j) {
       const int e = tid + j * NT;
-      u32x4 v = z4;
-      if (e < NCH_A) {
-        int tk, ch;
-        const unsigned char* base;
-        int64_t rb;
-        if (e < TILE * CN) {
-          tk = e / CN;
-          ch = e - tk * CN;
-          base = kb;
-          rb = ROW;
-        } else if (e < TILE * (CN + CR)) {
-          const int f = e - TILE * CN;
-          tk = f / (CR > 0 ? CR : 1);
-          ch = f - tk * CR;
-          base = krb;
-          rb = DR * 2;
-        } else {
-          const int f = e - TILE * (CN + CR);
-          tk = f / CI;
-          ch = f - tk * CI;
-          base = kib;
-          rb = IROW;
-        }
-        const int k = t * TILE + tk;
-        if (k < n) v = *(const u32x4*)(base + (int64_t)kl_token(p, row, ri.b, k) * rb + ch * 16);
-      }
-      pre[j] = v;
+      const int tk = e / CN, ch = e - tk * CN;
+      const int k = t * TILE + tk;
+      pre_n[j] = k < n ? *(const u32x4*)(kb + (int64_t)s_tok[k] * ROW + ch * 16) : z4;
+    }
+    if (DR > 0) {
+      const int tk = tid / (CR > 0 ? CR : 1), ch = tid - tk * CR;
+      const int k = t * TILE + tk;
+      pre_r = (tid < TILE * CR && k < n) ? *(const u32x4*)(krb + (int64_t)s_tok[k] * (DR * 2) + ch * 16) : z4;
+    }
+    {
+      const int tk = tid / CI, ch = tid - tk * CI;
+      const int k = t * TILE + tk;
+      pre_i = k < n ? *(const u32x4*)(kib + (int64_t)s_tok[k] * IROW + ch * 16) : z4;
     }
   };
   auto store_a = [&]() {
 #pragma unroll
-    for (int j = 0; j < PF_A; ++j) {
+    for (int j = 0; j < NJ_N; ++j) {
       const int e = tid + j * NT;
-      if (e < NCH_A) {
-        if (e < TILE * CN) {
-          const int tk = e / CN, ch = e - tk * CN;
-          *(u32x4*)(s_k + tk * ROW + ((ch ^ nope_swz(tk)) * 16)) = pre[j];
-        } else if (e < TILE * (CN + CR)) {
-          const int f = e - TILE * CN;
-          const int tk = f / (CR > 0 ? CR : 1), ch = f - tk * CR;
-          *(u32x4*)(s_kr + tk * (DR * 2) + ((ch ^ rope_swz(tk)) * 16)) = pre[j];
-        } else {
-          const int f = e - TILE * (CN + CR);
-          const int tk = f / CI, ch = f - tk * CI;
-          *(u32x4*)(s_ki + tk * IROW + ((ch ^ nope_swz(tk)) * 16)) = pre[j];
-        }
-      }
+      const int tk = e / CN, ch = e - tk * CN;
+      *(u32x4*)(s_k + tk * ROW + ((ch ^ nope_swz(tk)) * 16)) = pre_n[j];
+    }
+    if (DR > 0 && tid < TILE * CR) {
+      const int tk = tid / (CR > 0 ? CR : 1), ch = tid - tk * CR;
+      *(u32x4*)(s_kr + tk * (DR * 2) + ((ch ^ rope_swz(tk)) * 16)) = pre_r;
+    }
+    {
+      const int tk = tid / CI, ch = tid - tk * CI;
+      *(u32x4*)(s_ki + tk * IROW + ((ch ^ nope_swz(tk)) * 16)) = pre_i;
     }
   };
 
@@ -278,7 +297,12 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     lds_barrier();
     if (t + 1 < nt) load_a(t + 1);
 
-    // teacher: S^T[slot][head] = K . Q^T, 16 heads per wave
+    // Scores as S[head][slot] = Q . K^T (heads on MFMA rows, C register r =
+    // head 4*lg + r, column = slot li).  That C layout is the A layout of
+    // v_mfma_16x16x16 ([slot][head], k = 4*lg + j), so the sum over the
+    // wave's 16 heads is one more product with a ones matrix, run on an
+    // exact three-part bf16 split of the fp32 terms (fp32-level sums without
+    // cross-lane traffic).
     if (wave_heads) {
       f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -289,18 +313,19 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
           const unsigned char* a =
               ks < KSN ? s_k + tk * ROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16)
                        : s_kr + tk * (DR * 2) + ((((ks - KSN) * 4 + lg) ^ rope_swz(tk)) * 16);
-          acc[tt] = E::mfma(as_v8<V8>(*(const u32x4*)a), qf[ks], acc[tt]);
+          acc[tt] = E::mfma(qf[ks], as_v8<V8>(*(const u32x4*)a), acc[tt]);
         }
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
+      for (int tt = 0; tt < 2; ++tt) {
+        Split3 sp;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float pr = hv ? fast_exp2(acc[tt][r] * p.scale_log2 - m2) * inv : 0.f;
-          pr = row16_sum(pr);
-          if (li == 0) s_red[wave][tt * 16 + lg * 4 + r] = pr;
-        }
+        for (int r = 0; r < 4; ++r) split3_set(sp, r, fast_exp2(acc[tt][r] * p.scale_log2 - m2r[r]) * invr[r]);
+        // sum[r] = sum over the wave's heads for slot tt*16 + 4*lg + r
+        const f32x4 sum = split3_rowsum(sp);
+        if (li == 0) *(f32x4*)&s_red[wave][tt * 16 + lg * 4] = sum;
+      }
     }
-    // index scores: waves 0-3, 16 index heads each
+    // index scores I[slot] = sum_g w_g ReLU(qi_g . ki): waves 0-3, 16 index heads each
     if (iwave) {
       f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -309,26 +334,26 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
         for (int tt = 0; tt < 2; ++tt) {
           const int tk = tt * 16 + li;
           const unsigned char* a = s_ki + tk * IROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16);
-          acc[tt] = E::mfma(as_v8<V8>(*(const u32x4*)a), qif[ks], acc[tt]);
+          acc[tt] = E::mfma(qif[ks], as_v8<V8>(*(const u32x4*)a), acc[tt]);
         }
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
+      for (int tt = 0; tt < 2; ++tt) {
+        Split3 sp;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float v = wg * fmaxf(acc[tt][r], 0.f);
-          v = row16_sum(v);
-          if (li == 0) s_redi[wave][tt * 16 + lg * 4 + r] = v;
-        }
+        for (int r = 0; r < 4; ++r) split3_set(sp, r, wr[r] * fmaxf(acc[tt][r], 0.f));
+        const f32x4 sum = split3_rowsum(sp);
+        if (li == 0) *(f32x4*)&s_redi[wave][tt * 16 + lg * 4] = sum;
+      }
     }
     lds_barrier();
     if (tid < TILE) {
       const int k = t * TILE + tid;
       if (k < n) {
         float ps = 0.f, is = 0.f;
-        for (int w2 = 0; w2 < kKlWaves; ++w2)
-          if (w2 * 16 < p.n1) ps += s_red[w2][tid];
-        for (int w2 = 0; w2 < 4; ++w2)
-          if (w2 * 16 < p.nidx) is += s_redi[w2][tid];
+#pragma unroll
+        for (int w2 = 0; w2 < kKlWaves; ++w2) ps += s_red[w2][tid];
+#pragma unroll
+        for (int w2 = 0; w2 < 4; ++w2) is += s_redi[w2][tid];
         s_p[k] = ps * (1.f / (float)p.n1);
         s_I[k] = is;
       }
@@ -412,7 +437,7 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   auto load_c = [&](int t) {
     const int tk = tid / CI, ch = tid - tk * CI;
     const int k = t * TILE + tk;
-    prei = k < n ? *(const u32x4*)(kib + (int64_t)kl_token(p, row, ri.b, k) * IROW + ch * 16) : z4;
+    prei = k < n ? *(const u32x4*)(kib + (int64_t)s_tok[k] * IROW + ch * 16) : z4;
   };
   load_c(0);
   for (int t = 0; t < nt; ++t) {
@@ -678,7 +703,7 @@ size_t kl_bwd_workspace_bytes(int64_t batch, int64_t s1, int64_t s2, int64_t top
   return kl_ws_layout(batch * s1, batch * s2, topk).total;
 }
 
-size_t kl_bwd_lds_bytes(int64_t topk) { return (size_t)2 * topk * sizeof(float); }
+size_t kl_bwd_lds_bytes(int64_t topk) { return (size_t)3 * topk * sizeof(float); }
 int kl_bwd_max_topk() { return kKlMaxTopk; }
 int kl_bwd_max_nidx() { return kKlMaxNidx; }
 
@@ -689,7 +714,7 @@ static hipError_t kl_row_lds_attr() {
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute((const void*)kl_bwd_row_kernel<D, DR, T>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)(2 * kKlMaxTopk * 4));
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)(3 * kKlMaxTopk * 4));
     if (e != hipSuccess) return e;
     attr_set = true;
   }

@@ -61,20 +61,6 @@ struct SfaBwdParams {
 constexpr int kBwdTile = 32;
 constexpr int kBwdList = 2048;  // attended positions resolved per compaction round
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-template <typename T> struct Mfma16;
-template <> struct Mfma16<bf16> {
-  static __device__ __forceinline__ f32x4 run(s16x4 a, s16x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-  }
-};
-template <> struct Mfma16<f16> {
-  static __device__ __forceinline__ f32x4 run(s16x4 a, s16x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c,
-                                                 0, 0, 0);
-  }
-};
 
 template <typename T>
 __device__ __forceinline__ short to_bits(float x) {
