@@ -35,6 +35,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--sets", type=int, default=6)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--long-steps", type=int, default=3,
+                    help="timed steps of the prefill / backward legs (each step is milliseconds)")
+    ap.add_argument("--no-long", action="store_true", help="skip the prefill / backward legs")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain copy kernel of known size (for PMC calibration)")
     return ap.parse_args()
@@ -150,17 +153,23 @@ def cpu_baseline_decode(sets):
         krs.append(cache_r[pt].float().cpu().numpy())
     idx = np.arange(K, dtype=np.int32).reshape(1, 1, 1, K)
     scale = 1.0 / math.sqrt(D + DR)
+    # the whole batch, repeated until at least ~10 s of host work is timed
+    reps = 0
     t0 = time.perf_counter()
-    for b in rows:
-        sfa_fwd_bsnd(q[b:b + 1], ks[b][None, :, None, :], idx, qr[b:b + 1],
-                     krs[b][None, :, None, :], scale, [1], [K], 1, 0, True, "bfloat16",
-                     positions="kernel")
-    dt = time.perf_counter() - t0
+    while True:
+        for b in rows:
+            sfa_fwd_bsnd(q[b:b + 1], ks[b][None, :, None, :], idx, qr[b:b + 1],
+                         krs[b][None, :, None, :], scale, [1], [K], 1, 0, True, "bfloat16",
+                         positions="kernel")
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= 10.0:
+            break
     flops, _ = decode_algorithmic(B * K)
-    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+    return {"value": reps * flops / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
             "sample": f"numpy oracle (port of sparse_flash_attention_numpy.py) over the full "
                       f"decode batch of one input set ({B} rows x {K} tokens x {N1} heads), "
-                      f"{dt:.2f} s"}
+                      f"repeated {reps} times, {dt:.1f} s"}
 
 
 # ---------------------------------------------------------------------------
@@ -219,6 +228,101 @@ def time_li(sets, steps, warmup):
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
+
+
+# ---------------------------------------------------------------------------
+# prefill forward (cfg4) and the backward pair (cfg5a / cfg5b): reported
+# beside the headline, each in TFLOP/s of algorithmic work
+# ---------------------------------------------------------------------------
+def causal_indices(S, K, g, device):
+    """Row s1 holds min(K, s1+1) distinct uniform ids from [0, s1], sorted,
+    -1-padded to K (the prefill config's index recipe)."""
+    import torch
+    r = torch.rand(S, S, generator=g, device=device)
+    ar = torch.arange(S, device=device)
+    r[ar[None, :] > ar[:, None]] = 2.0
+    idx = torch.sort(torch.argsort(r, dim=1)[:, :K], dim=1).values.to(torch.int32)
+    del r
+    nval = torch.clamp(ar + 1, max=K)
+    idx[torch.arange(K, device=device)[None, :] >= nval[:, None]] = -1
+    return idx, int(nval.sum())
+
+
+def time_call(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def leg(metric, workload, flops, ms, n):
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"metric": metric, "value": round(tf, 2), "unit": "TFLOP/s", "higher_is_better": True,
+            "ms_per_step": round(ms, 4), "pct_of_bf16_peak": round(100.0 * tf / PEAK_BF16_TFLOPS, 3),
+            "algorithmic_flops": int(flops), "valid_pairs": n, "config": {"workload": workload}}
+
+
+def long_legs(dev, steps):
+    import torch
+    import dsa_triton_ascend_amd as dsa
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(42)
+    rn = lambda *s: torch.randn(*s, generator=g, device=dev).to(torch.bfloat16)  # noqa: E731
+    scale = 1.0 / math.sqrt(D + DR)
+    # cfg4: prefill, TND one sequence T=8192, mode 3, stats returned
+    T = 8192
+    q, qr, k, kr = rn(T, N1, D), rn(T, N1, DR), rn(T, 1, D), rn(T, 1, DR)
+    idx, n = causal_indices(T, K, g, dev)
+    si = idx.reshape(T, 1, K).contiguous()
+    cu = [T]
+
+    def fwd_tnd():
+        return dsa.sparse_flash_attention_triton(q, k, k, si, scale_value=scale, actual_seq_lengths_query=cu,
+                                                 actual_seq_lengths_kv=cu, query_rope=qr, key_rope=kr,
+                                                 layout_query="TND", layout_kv="TND", sparse_mode=3,
+                                                 return_softmax_lse=True)
+    ms = time_call(fwd_tnd, steps, 1)
+    out["sfa_fwd_prefill"] = leg("SFA fwd TFLOP/s (prefill)",
+                                 "sfa_fwd prefill: TND one sequence T=8192, N1=128, D=512+64, topK=2048 "
+                                 "causal, sparse_mode 3, stats returned", 2.0 * N1 * (2 * D + DR) * n, ms, n)
+    del q, qr, k, kr, idx, si
+    torch.cuda.empty_cache()
+    # cfg5a / cfg5b: backward pair at S=4096
+    S = 4096
+    q, qr, k, kr = rn(1, S, N1, D), rn(1, S, N1, DR), rn(1, S, 1, D), rn(1, S, 1, DR)
+    do = rn(1, S, N1, D)
+    idx, n = causal_indices(S, K, g, dev)
+    si = idx.reshape(1, S, 1, K).contiguous()
+    o, smax, ssum = dsa.sparse_flash_attention_triton(q, k, k, si, scale_value=scale, query_rope=qr, key_rope=kr,
+                                                      sparse_mode=3, return_softmax_lse=True)
+
+    def bwd():
+        return dsa.sparse_flash_attention_grad_triton(q, k, k, si, do, o, smax, ssum, scale_value=scale,
+                                                      query_rope=qr, key_rope=kr, sparse_mode=3)
+    ms = time_call(bwd, steps, 1)
+    out["sfa_bwd"] = leg("SFA bwd TFLOP/s", "sfa_bwd: BSND B=1, S1=S2=4096, N1=128, D=512+64, topK=2048 "
+                         "causal, sparse_mode 3, bf16", 2.0 * N1 * (3 * (D + DR) + 2 * D) * n, ms, n)
+    NI, DI = 64, 128
+    qi, ki = rn(1, S, NI, DI), rn(1, S, 1, DI)
+    w = torch.rand(1, S, NI, generator=g, device=dev)
+
+    def kl():
+        return dsa.sparse_lightning_indexer_grad_kl_loss_triton(q, k, qi, ki, w, si, smax, ssum, query_rope=qr,
+                                                                key_rope=kr, scale_value=scale)
+    ms = time_call(kl, steps, 1)
+    out["kl_bwd"] = leg("indexer KL-loss bwd TFLOP/s",
+                        "sparse_lightning_indexer_grad_kl_loss: B=1, S1=S2=4096, N1=128, D=512+64, Nidx1=64, "
+                        "D_idx=128, topK=2048 causal, bf16 (fp32 weights), stats from the SFA forward",
+                        n * (3 * 2 * NI * DI + 2 * N1 * (D + DR) + 2 * NI), ms, n)
+    return out
 
 
 def measured_traffic():
@@ -306,6 +410,11 @@ def main():
                      "algorithmic_bytes_per_launch": int(li_bytes),
                      "algorithmic_flops_per_launch": int(li_flops)},
     }
+    del li_sets
+    torch.cuda.empty_cache()
+    if not args.no_long:
+        result.update(long_legs(dev, args.long_steps))
+        torch.cuda.empty_cache()
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_decode(make_decode_sets(1, dev))
     print(json.dumps(result), flush=True)
