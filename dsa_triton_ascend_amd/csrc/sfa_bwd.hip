@@ -369,6 +369,306 @@ __global__ __launch_bounds__(64, 1) void sfa_bwd_kernel(SfaBwdParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Workgroup kernel: 4 waves x 16 heads = 64 heads of one query row.
+//
+// Per tile of 32 attended tokens (LDS ring of two buffers, filled by LDS DMA
+// right after the previous tile's barrier, so a tile's gather overlaps the
+// previous tile's products):
+//  * each wave: S^T, dP^T, P, dS and dq / dq_rope for its 16 heads, as the
+//    one-wave kernel above;
+//  * dS and P of the 64 heads go to LDS as [token][head] (bf16 / fp16);
+//  * each wave then owns a quarter of the 2D + 64 output columns (dK, dK_rope,
+//    dV) and sums them over all 64 heads on MFMA: A = dS^T or P^T [16 tokens
+//    x 32 heads] from LDS, B = Q / Q_rope / dO [32 heads x 16 columns]
+//    resident in registers for the row; the sums go to the fp32 workspaces.
+// The 64-head sum cuts the scatter payload by 4 against one wave per 16
+// heads.  One wave per SIMD: each wave has the whole 512-register file.
+// ---------------------------------------------------------------------------
+constexpr int kBwdWgWaves = 4;
+constexpr int kBwdWgHeads = 64;
+
+__device__ __forceinline__ void bwd_dma16(unsigned lds_base, int voff, __amdgpu_buffer_rsrc_t rsrc) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :: "s"(lds_base), "v"(voff), "s"(rsrc) : "memory");
+}
+__device__ __forceinline__ void bwd_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+template <int D, typename T>
+__global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdParams p) {
+  using E = Elem<T>;
+  using V8 = typename E::v8;
+  constexpr int DR = 64;
+  constexpr int DC = D + DR;
+  constexpr int KS = DC / 32, KSN = D / 32;
+  constexpr int NDT = D / 16;
+  constexpr int TILE = kBwdTile;
+  constexpr int NT = kBwdWgWaves * 64;
+  constexpr int ROW = D * 2;
+  constexpr int TPI = 1024 / ROW;            // nope rows per DMA (1 KB per DMA)
+  constexpr int NDN = TILE / TPI / kBwdWgWaves;  // nope DMAs per wave per tile
+  constexpr int NCOL = 2 * D + DR;           // dK | dK_rope | dV columns
+  constexpr int NCW = NCOL / 16 / kBwdWgWaves;   // column tiles per wave
+  constexpr int TR = kBwdWgHeads + 8;        // padded [token][head] row
+  static_assert(NCOL % (16 * kBwdWgWaves) == 0 && TILE % (TPI * kBwdWgWaves) == 0, "layout");
+
+  __shared__ __attribute__((aligned(1024))) unsigned char s_k[2][TILE * ROW];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_kr[2][TILE * DR * 2];
+  __shared__ int s_list[kBwdList + TILE];
+  __shared__ __attribute__((aligned(16))) T s_t[2][TILE][TR];  // dS, P of the 64 heads
+  __shared__ int s_wcnt[kBwdWgWaves];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int row = blockIdx.x;
+  const int hbase = blockIdx.y * kBwdWgHeads;
+  const RowInfo ri = sfa_row_info(p, row);
+  const int64_t total_pos = (int64_t)p.K * p.bs;
+  const int32_t* idx_row = p.idx + (int64_t)row * p.K;
+  const u32x4 z4 = {0u, 0u, 0u, 0u};
+
+  // ---- per-lane head hbase + 16*wave + li: fragments and statistics ----
+  const int head = hbase + wave * 16 + li;
+  const bool hv = head < p.n1;
+  const int64_t hrow = (int64_t)row * p.n1 + (hv ? head : 0);
+  V8 qf[KS], dof[KSN];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    u32x4 v;
+    if (ks < KSN) v = *(const u32x4*)((const T*)p.q + hrow * D + ks * 32 + lg * 8);
+    else v = *(const u32x4*)((const T*)p.qr + hrow * DR + (ks - KSN) * 32 + lg * 8);
+    qf[ks] = as_v8<V8>(hv ? v : z4);
+  }
+  float delta = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < KSN; ++ks) {
+    const u32x4 v = *(const u32x4*)((const T*)p.dout + hrow * D + ks * 32 + lg * 8);
+    const u32x4 o = *(const u32x4*)((const T*)p.out + hrow * D + ks * 32 + lg * 8);
+    dof[ks] = as_v8<V8>(hv ? v : z4);
+    const V8 dv8 = as_v8<V8>(v), ov8 = as_v8<V8>(o);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) delta += E::to_f32(dv8[j]) * E::to_f32(ov8[j]);
+  }
+  delta = xgroup_sum(delta);
+  float m2 = 0.f, inv = 0.f;
+  if (hv) {
+    m2 = p.smax[hrow] * kLog2e;
+    const float ss = p.ssum[hrow];
+    inv = 1.f / (ss > 0.f ? ss : 1.f);
+  } else {
+    delta = 0.f;
+  }
+  // B operands of the 64-head sums: column c = 16*(wave*NCW + i) + li of
+  // [Q nope | Q rope | dO], heads hbase + 32*ks + 8*lg + j
+  V8 xb[NCW][2];
+#pragma unroll
+  for (int i = 0; i < NCW; ++i) {
+    const int c = 16 * (wave * NCW + i) + li;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int h = hbase + ks * 32 + lg * 8 + j;
+        T v = E::from_f32(0.f);
+        if (h < p.n1) {
+          const int64_t r = (int64_t)row * p.n1 + h;
+          if (c < D) v = ((const T*)p.q)[r * D + c];
+          else if (c < D + DR) v = ((const T*)p.qr)[r * DR + (c - D)];
+          else v = ((const T*)p.dout)[r * D + (c - D - DR)];
+        }
+        xb[i][ks][j] = v;
+      }
+  }
+  f32x4 acc_dq[NDT], acc_dqr[DR / 16];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) acc_dq[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int dt = 0; dt < DR / 16; ++dt) acc_dqr[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+  // ---- tile DMA: wave w loads nope rows (j*4 + w)*TPI .. +TPI (lane L ->
+  // row + L/CPT, source chunk (L%CPT) ^ nope_swz) and rope rows 8w .. 8w+7 ----
+  constexpr int CPT = 64 / TPI;  // chunks per row covered by one DMA
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc((void*)p.k, (short)0, (int)(p.kv_rows * D * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rr =
+      __builtin_amdgcn_make_buffer_rsrc((void*)p.kr, (short)0, (int)(p.kv_rows * DR * 2), 0x00020000);
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  auto issue_tile = [&](int t, int b) {
+    int ph[NDN + 1];
+#pragma unroll
+    for (int j = 0; j < NDN; ++j) ph[j] = s_list[t * TILE + (j * kBwdWgWaves + wave_s) * TPI + lane / CPT];
+    ph[NDN] = s_list[t * TILE + wave_s * 8 + (lane >> 3)];
+#pragma unroll
+    for (int j = 0; j < NDN; ++j) {
+      const int tk = (j * kBwdWgWaves + wave_s) * TPI + lane / CPT;
+      const int ch = (lane % CPT) ^ nope_swz(tk);
+      const unsigned dst = (unsigned)(uintptr_t)&s_k[b][(j * kBwdWgWaves + wave_s) * TPI * ROW];
+      bwd_dma16(dst, ph[j] >= 0 ? ph[j] * ROW + ch * 16 : (int)0x80000000, rk);
+    }
+    {
+      const int tk = wave_s * 8 + (lane >> 3);
+      const int ch = (lane & 7) ^ rope_swz(tk);
+      const unsigned dst = (unsigned)(uintptr_t)&s_kr[b][wave_s * 8 * DR * 2];
+      bwd_dma16(dst, ph[NDN] >= 0 ? ph[NDN] * (DR * 2) + ch * 16 : (int)0x80000000, rr);
+    }
+  };
+
+  for (int64_t c0 = 0; c0 < total_pos; c0 += kBwdList) {
+    // ---- compact this range of positions into s_list (stable order) ----
+    const int64_t c1 = min(total_pos, c0 + (int64_t)kBwdList);
+    int n_valid = 0;
+    for (int64_t b0 = c0; b0 < c1; b0 += NT) {
+      const int64_t pos = b0 + tid;
+      int phys = 0;
+      bool valid = false;
+      if (ri.active && pos < c1) valid = sfa_resolve(p, ri, idx_row, (int)pos, &phys);
+      const unsigned long long m = __ballot(valid);
+      if (lane == 0) s_wcnt[wave] = __popcll(m);
+      lds_barrier();
+      int off = n_valid, tot = 0;
+#pragma unroll
+      for (int w = 0; w < kBwdWgWaves; ++w) {
+        const int c = s_wcnt[w];
+        off += w < wave ? c : 0;
+        tot += c;
+      }
+      if (valid) s_list[off + __popcll(m & ((1ull << lane) - 1ull))] = phys;
+      n_valid += tot;
+      lds_barrier();
+    }
+    if (tid < TILE) s_list[n_valid + tid] = -1;
+    lds_barrier();
+    const int n_tiles = (n_valid + TILE - 1) / TILE;
+    if (n_tiles > 0) issue_tile(0, 0);
+
+    for (int t = 0; t < n_tiles; ++t) {
+      const int b = t & 1;
+      bwd_wait_all();  // this tile's DMA (and everything older) has landed
+      lds_barrier();
+      if (t + 1 < n_tiles) issue_tile(t + 1, b ^ 1);
+      const unsigned char* kt = s_k[b];
+      const unsigned char* krt = s_kr[b];
+
+      // ---- S^T = K.Q^T and dP^T = K_nope.dO^T (shared K fragments) ----
+      f32x4 acc_s[2], acc_p[2];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        acc_s[tt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        acc_p[tt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          const int tk = tt * 16 + li;
+          const unsigned char* a = ks < KSN ? kt + tk * ROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16)
+                                            : krt + tk * (DR * 2) + ((((ks - KSN) * 4 + lg) ^ rope_swz(tk)) * 16);
+          const V8 av = as_v8<V8>(*(const u32x4*)a);
+          acc_s[tt] = E::mfma(av, qf[ks], acc_s[tt]);
+          if (ks < KSN) acc_p[tt] = E::mfma(av, dof[ks], acc_p[tt]);
+        }
+
+      // ---- P^T, dS^T (token tt*16 + 4*lg + r, head li) ----
+      constexpr bool kSplit = __is_same(T, bf16);
+      V8 dsf, dsl;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int tt = j >> 2, r = j & 3;
+        const int tk = tt * 16 + lg * 4 + r;
+        const bool tv = t * TILE + tk < n_valid;
+        const float pp = tv ? fast_exp2(acc_s[tt][r] * p.scale_log2 - m2) * inv : 0.f;
+        const float ds = pp * (acc_p[tt][r] - delta) * p.scale;
+        const T dh = E::from_f32(ds);
+        dsf[j] = dh;
+        dsl[j] = E::from_f32(ds - E::to_f32(dh));
+        s_t[0][tk][wave * 16 + li] = dh;
+        s_t[1][tk][wave * 16 + li] = E::from_f32(pp);
+      }
+
+      // ---- dq^T += K^T.dS^T, dq_rope^T += Kr^T.dS^T (transposing reads) ----
+      {
+        const int r1 = lg * 4 + (li >> 2);
+        const int hb = (li & 3) >> 1;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const int ch = 2 * dt + hb;
+          const unsigned char* p1 = kt + r1 * ROW + ((ch ^ nope_swz(r1)) * 16) + (li & 1) * 8;
+          const unsigned char* p2 = kt + (r1 + 16) * ROW + ((ch ^ nope_swz(r1 + 16)) * 16) + (li & 1) * 8;
+          const i16x4 w1 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1));
+          const i16x4 w2 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p2));
+          const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
+          acc_dq[dt] = E::mfma(__builtin_bit_cast(V8, w), dsf, acc_dq[dt]);
+          if (kSplit) acc_dq[dt] = E::mfma(__builtin_bit_cast(V8, w), dsl, acc_dq[dt]);
+        }
+#pragma unroll
+        for (int dt = 0; dt < DR / 16; ++dt) {
+          const int ch = 2 * dt + hb;
+          const unsigned char* p1 = krt + r1 * (DR * 2) + ((ch ^ rope_swz(r1)) * 16) + (li & 1) * 8;
+          const unsigned char* p2 = krt + (r1 + 16) * (DR * 2) + ((ch ^ rope_swz(r1 + 16)) * 16) + (li & 1) * 8;
+          const i16x4 w1 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1));
+          const i16x4 w2 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p2));
+          const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
+          acc_dqr[dt] = E::mfma(__builtin_bit_cast(V8, w), dsf, acc_dqr[dt]);
+          if (kSplit) acc_dqr[dt] = E::mfma(__builtin_bit_cast(V8, w), dsl, acc_dqr[dt]);
+        }
+      }
+      lds_barrier();  // dS / P of all 64 heads in LDS
+
+      // ---- dK | dK_rope | dV columns of this wave, summed over 64 heads ----
+      int ph[2][4];
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ph[tt][r] = s_list[t * TILE + tt * 16 + lg * 4 + r];
+#pragma unroll
+      for (int i = 0; i < NCW; ++i) {
+        const int ct = wave * NCW + i;
+        const int sel = ct < (D + DR) / 16 ? 0 : 1;  // dS for dK / dK_rope, P for dV
+        const int c = 16 * ct + li;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            const V8 a = as_v8<V8>(*(const u32x4*)&s_t[sel][tt * 16 + li][ks * 32 + lg * 8]);
+            acc = E::mfma(a, xb[i][ks], acc);
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int pr = ph[tt][r];
+            if (pr < 0) continue;
+            if (c < D) atomicAdd(p.dk + (int64_t)pr * D + c, acc[r]);
+            else if (c < D + DR) atomicAdd(p.dkr + (int64_t)pr * DR + (c - D), acc[r]);
+            else atomicAdd(p.dv + (int64_t)pr * D + (c - D - DR), acc[r]);
+          }
+        }
+      }
+    }
+    bwd_wait_all();
+    lds_barrier();  // s_list is rebuilt for the next range
+  }
+
+  // ---- dq, dq_rope (head li, columns 16*dt + 4*lg + r) ----
+  if (hv) {
+    typedef T T4 __attribute__((ext_vector_type(4)));
+    T* dqp = (T*)p.dq + hrow * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const T4 o = {E::from_f32(acc_dq[dt][0]), E::from_f32(acc_dq[dt][1]), E::from_f32(acc_dq[dt][2]),
+                    E::from_f32(acc_dq[dt][3])};
+      *(T4*)(dqp + dt * 16 + lg * 4) = o;
+    }
+    T* dqrp = (T*)p.dqr + hrow * DR;
+#pragma unroll
+    for (int dt = 0; dt < DR / 16; ++dt) {
+      const T4 o = {E::from_f32(acc_dqr[dt][0]), E::from_f32(acc_dqr[dt][1]), E::from_f32(acc_dqr[dt][2]),
+                    E::from_f32(acc_dqr[dt][3])};
+      *(T4*)(dqrp + dt * 16 + lg * 4) = o;
+    }
+  }
+}
+
 // fp32 workspace -> output dtype
 template <typename T>
 __global__ __launch_bounds__(256) void cast_f32_kernel(const float* src, T* dst, int64_t n) {
@@ -390,10 +690,17 @@ size_t sfa_bwd_workspace_bytes(int64_t kv_rows, int64_t d) {
   return (size_t)kv_rows * (size_t)(d + 64 + d) * sizeof(float);
 }
 
+// The workgroup kernel gathers with buffer loads (32-bit offsets): key
+// tensors of 2 GiB and more take the one-wave kernel.
 template <int D, typename T>
 static hipError_t launch_sfa_bwd(const SfaBwdParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL((sfa_bwd_kernel<D, T>), dim3((unsigned)p.rows, (unsigned)((p.n1 + 15) / 16)), dim3(64), 0,
-                     stream, p);
+  if ((int64_t)p.kv_rows * D * 2 < (1ll << 31)) {
+    hipLaunchKernelGGL((sfa_bwd_wg_kernel<D, T>), dim3((unsigned)p.rows, (unsigned)((p.n1 + kBwdWgHeads - 1) / kBwdWgHeads)),
+                       dim3(kBwdWgWaves * 64), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((sfa_bwd_kernel<D, T>), dim3((unsigned)p.rows, (unsigned)((p.n1 + 15) / 16)), dim3(64), 0,
+                       stream, p);
+  }
   return hipGetLastError();
 }
 
