@@ -88,6 +88,18 @@ __device__ __forceinline__ float xgroup_sum(float v) {
   return v;
 }
 
+// Butterfly max/sum over all 64 lanes of a wave.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
 // Workgroup barrier that orders LDS only.  __syncthreads() also fences
 // global memory, which makes the compiler drain every outstanding global
 // load (s_waitcnt vmcnt(0)) before the barrier and kills load/compute

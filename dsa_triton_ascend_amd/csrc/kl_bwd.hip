@@ -123,17 +123,6 @@ __device__ __forceinline__ void store_w(void* w, int64_t i, int dt, float v) {
   else ((f16*)w)[i] = (f16)v;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
 template <int D, int DR, typename T>
 __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p) {
   using E = Elem<T>;

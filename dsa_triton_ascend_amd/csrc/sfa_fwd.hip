@@ -64,10 +64,6 @@ struct SfaFwdParams {
   int32_t return_lse;
 };
 
-#ifndef DSA_SCHED_GROUPS
-#define DSA_SCHED_GROUPS 1
-#endif
-
 constexpr int kSfaTile = 32;
 constexpr int kSfaMaxList = 2048;
 constexpr float kRefSlack = 64.f;  // log2 units
@@ -159,6 +155,45 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   const int total_pos = p.K * p.bs;
   const int p0 = split * p.pos_per_split;
   const int p1 = min(total_pos, p0 + p.pos_per_split);
+
+  const int head0 = hg * HEADS_PER_WG + wave * HT * 16;
+  const bool wave_active = head0 < p.n1;
+
+  // ---- Q fragments (B operand of S^T = K.Q^T): lane -> head li, k = 8*lg.. ----
+  // Q fragments: k-steps < KQR in registers, the last QL in LDS (loaded
+  // first, stored to LDS once the register part's loads are out)
+  V8 qf[HT][KQR > 0 ? KQR : 1];
+  u32x4 qlv[HT][QL];
+  const u32x4 z4 = {0u, 0u, 0u, 0u};
+  auto q_chunk = [&](int64_t hsafe, int ks) -> u32x4 {
+    if (ks < KSN) return *(const u32x4*)((const T*)p.q + hsafe * D + ks * 32 + lg * 8);
+    return *(const u32x4*)((const T*)p.qr + hsafe * DR + (ks - KSN) * 32 + lg * 8);
+  };
+  auto load_q = [&]() {
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+      const int head = head0 + ht * 16 + li;
+      const bool hv = head < p.n1;
+      const int64_t hsafe = row * p.n1 + (hv ? head : 0);
+#pragma unroll
+      for (int m = 0; m < QL; ++m) qlv[ht][m] = hv ? q_chunk(hsafe, KQR + m) : z4;
+    }
+#pragma unroll
+    for (int ht = 0; ht < HT; ++ht) {
+      const int head = head0 + ht * 16 + li;
+      const bool hv = head < p.n1;
+      const int64_t hsafe = row * p.n1 + (hv ? head : 0);
+#pragma unroll
+      for (int ks = 0; ks < KQR; ++ks) qf[ht][ks] = as_v8<V8>(hv ? q_chunk(hsafe, ks) : z4);
+    }
+  };
+  // A wave with no index positions to resolve (the split has fewer than
+  // 64 * wave positions) loads its Q before the compaction: a wave's loads
+  // complete in issue order, so Q loads issued ahead of the index loads
+  // would make the index chain wait for them, and those issued after it
+  // start late.
+  const bool q_early = wave_active && (int64_t)wave * 64 >= (int64_t)(p1 - p0);
+  if (q_early) load_q();
 
   // ---- compact attended positions into s_list (stable order) ----
   int n_valid = 0;
@@ -260,9 +295,6 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
     for (int j = 0; j < NDMA; ++j) dma_issue(j, ph[j], b);
   };
 
-  const int head0 = hg * HEADS_PER_WG + wave * HT * 16;
-  const bool wave_active = head0 < p.n1;
-
   // Barrier sequence, identical for every wave: per tile one barrier, then
   // one vote barrier, and (only if the vote is set) a second pass of tiles.
   // Tile t is waited for (vmcnt) before its barrier and tile t+2 is issued
@@ -281,11 +313,16 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   };
   auto next_buf = [](int b) { return b == 0 ? NBUF - 1 : b - 1; };
 
+  // The first two tiles go out before the Q loads, so that their gather
+  // and the Q traffic are in flight together (the Q loads' own waits then
+  // also cover these older DMAs, which only makes them earlier).
+  gather_loop_prologue();
+
   if (!wave_active) {
     // waves without heads (N1 < HEADS_PER_WG) only take their share of the
     // gather, with the same barrier and load sequence as the other waves
-    auto gather_only = [&]() {
-      gather_loop_prologue();
+    auto gather_only = [&](bool prologue) {
+      if (prologue) gather_loop_prologue();
       for (int t0 = 0; t0 < n_tiles; t0 += NBUF)
 #pragma unroll
         for (int b = 0; b < NBUF; ++b) {
@@ -296,37 +333,13 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
         }
       wait_vmcnt<0>();
     };
-    gather_only();
-    if (__syncthreads_or(0)) gather_only();
+    gather_only(false);
+    if (__syncthreads_or(0)) gather_only(true);
     return;
   }
 
-  // ---- Q fragments (B operand of S^T = K.Q^T): lane -> head li, k = 8*lg.. ----
-  // Q fragments: k-steps < KQR in registers, the last QL in LDS (loaded
-  // first, stored to LDS once the register part's loads are out)
-  V8 qf[HT][KQR > 0 ? KQR : 1];
-  u32x4 qlv[HT][QL];
-  const u32x4 z4 = {0u, 0u, 0u, 0u};
-  auto q_chunk = [&](int64_t hsafe, int ks) -> u32x4 {
-    if (ks < KSN) return *(const u32x4*)((const T*)p.q + hsafe * D + ks * 32 + lg * 8);
-    return *(const u32x4*)((const T*)p.qr + hsafe * DR + (ks - KSN) * 32 + lg * 8);
-  };
-#pragma unroll
-  for (int ht = 0; ht < HT; ++ht) {
-    const int head = head0 + ht * 16 + li;
-    const bool hv = head < p.n1;
-    const int64_t hsafe = row * p.n1 + (hv ? head : 0);
-#pragma unroll
-    for (int m = 0; m < QL; ++m) qlv[ht][m] = hv ? q_chunk(hsafe, KQR + m) : z4;
-  }
-#pragma unroll
-  for (int ht = 0; ht < HT; ++ht) {
-    const int head = head0 + ht * 16 + li;
-    const bool hv = head < p.n1;
-    const int64_t hsafe = row * p.n1 + (hv ? head : 0);
-#pragma unroll
-    for (int ks = 0; ks < KQR; ++ks) qf[ht][ks] = as_v8<V8>(hv ? q_chunk(hsafe, ks) : z4);
-  }
+  if (!q_early) load_q();
+
   // staged Q fragment (head li of head tile ht, chunk 4m + lg) at
   // ql_base ^ (m << 6) + ht * (16 * QL * 64)
   auto ql_base = [&](int ln) {
@@ -455,15 +468,11 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
         acc_s[tt][ht] = E::mfma(av, ks < KQR ? qf[ht][ks < KQR ? ks : 0] : ql[ht][ks < KQR ? 0 : ks - KQR], acc_s[tt][ht]);
       if constexpr (kDma)
         if ((st & 3) == 2 && (st >> 2) < NDMA) dma_issue(st >> 2, dph[st >> 2], bn);
+      // keeps the prefetched fragment reads where they are: without it the
+      // scheduler sinks each read next to its MFMA to save registers, and
+      // every MFMA then waits out a full LDS round trip
+      __builtin_amdgcn_sched_barrier(0);
     }
-#if DSA_SCHED_GROUPS
-    __builtin_amdgcn_sched_group_barrier(0x100, PF1, 0);
-#pragma unroll
-    for (int st = 0; st < NS1; ++st) {
-      __builtin_amdgcn_sched_group_barrier(0x008, HT, 0);
-      if (st + PF1 < NS1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-#endif
   };
 
   // ---- softmax numerators of tile t and O^T += V^T . P^T (buffer b) ----
@@ -521,14 +530,8 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
         acc_o[dt][ht] = E::mfma(av, pf[ht], acc_o[dt][ht]);
         if (kSplitP) acc_o[dt][ht] = E::mfma(av, pf_lo[ht], acc_o[dt][ht]);
       }
+      __builtin_amdgcn_sched_barrier(0);  // PF2 fragments stay in flight
     }
-#if DSA_SCHED_GROUPS
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      __builtin_amdgcn_sched_group_barrier(0x008, HT * (kSplitP ? 2 : 1), 1);
-      if (dt + PF2 < NDT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
-    }
-#endif
   };
 
   using DmaOff = std::integral_constant<bool, false>;
@@ -540,8 +543,8 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   // system), softmax, GEMM2.  (A two-group ping-pong schedule, GEMM1 of one
   // group beside softmax + GEMM2 of the other, measured slower here: the
   // per-wave LDS read rate, not MFMA issue, bounds each phase.)
-  auto run_tiles = [&]() {
-    gather_loop_prologue();
+  auto run_tiles = [&](bool prologue) {
+    if (prologue) gather_loop_prologue();
     for (int t0 = 0; t0 < n_tiles; t0 += NBUF)
 #pragma unroll
       for (int b = 0; b < NBUF; ++b) {
@@ -560,7 +563,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) acc_o[dt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  run_tiles();
+  run_tiles(false);
   if (__syncthreads_or(overflow ? 1 : 0)) {
     // rare: some head's score exceeded the reference by 2^kRefSlack; redo
     // the row with the exact maxima found by the first pass
@@ -573,7 +576,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) acc_o[dt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    run_tiles();
+    run_tiles(true);
   }
 
   // ---- epilogue ----
@@ -662,36 +665,61 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
 // O_i / l_i (as scale_i * stored value), l_i relative to its reference max
 // r_i, and its exact max t_i (log2 units); the merged output is
 // sum_i w_i O_i / l_i / sum_i w_i with w_i = 2^(r_i - M) l_i.
+// Lane s reads the record of split s, the weights are formed on the lanes
+// and broadcast with readlane, and each lane then reads its D/64 columns of
+// up to eight splits before using any of them, so a wave waits for about
+// two memory round trips instead of two per split.
 template <int D, typename T>
 __global__ __launch_bounds__(256) void sfa_combine_kernel(SfaFwdParams p) {
   using E = Elem<T>;
+  constexpr int PER = D / 64;
+  typedef _Float16 hvec __attribute__((ext_vector_type(PER)));
   const int lane = threadIdx.x & 63;
   const int64_t rh = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (rh >= p.rows * p.n1) return;
+  const int64_t sstride = p.rows * p.n1;  // (row, head) records per split
   float mref = -INFINITY, mtrue = -INFINITY;
-  for (int s = 0; s < p.splits; ++s) {
-    const f32x4 ml = *(const f32x4*)(p.part_ml + ((int64_t)s * p.rows * p.n1 + rh) * 4);
+  for (int s = lane; s < p.splits; s += 64) {
+    const f32x4 ml = *(const f32x4*)(p.part_ml + ((int64_t)s * sstride + rh) * 4);
     if (ml[1] > 0.f) {
       mref = fmaxf(mref, ml[0]);
       mtrue = fmaxf(mtrue, ml[2]);
     }
   }
-  constexpr int PER = D / 64;
+  mref = wave_max(mref);
+  mtrue = wave_max(mtrue);
   float acc[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) acc[j] = 0.f;
   float L = 0.f;
   if (mref != -INFINITY) {
-    for (int s = 0; s < p.splits; ++s) {
-      const int64_t prow = (int64_t)s * p.rows * p.n1 + rh;
-      const f32x4 ml = *(const f32x4*)(p.part_ml + prow * 4);
-      if (!(ml[1] > 0.f)) continue;
-      const float w = fast_exp2(ml[0] - mref) * ml[1];
-      L += w;
-      const float ws = w * ml[3];
-      const f16* po = p.part_o + prow * D + lane * PER;
+    for (int s0 = 0; s0 < p.splits; s0 += 64) {
+      const int s = s0 + lane;
+      float w = 0.f, wsc = 0.f;
+      if (s < p.splits) {
+        const f32x4 ml = *(const f32x4*)(p.part_ml + ((int64_t)s * sstride + rh) * 4);
+        if (ml[1] > 0.f) {
+          w = fast_exp2(ml[0] - mref) * ml[1];
+          wsc = w * ml[3];
+        }
+      }
+      L += wave_sum(w);
+      const int n = min(64, p.splits - s0);
+      for (int j = 0; j < n; j += 8) {
+        hvec v[8];
 #pragma unroll
-      for (int j = 0; j < PER; ++j) acc[j] += ws * (float)po[j];
+        for (int u = 0; u < 8; ++u)
+          if (j + u < n)
+            v[u] = *(const hvec*)(p.part_o + ((int64_t)(s0 + j + u) * sstride + rh) * D + lane * PER);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (j + u >= n) break;
+          const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wsc), j + u));
+          if (wu == 0.f) continue;  // split without attended tokens
+#pragma unroll
+          for (int e = 0; e < PER; ++e) acc[e] += wu * (float)v[u][e];
+        }
+      }
     }
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
