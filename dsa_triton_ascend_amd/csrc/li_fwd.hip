@@ -214,9 +214,12 @@ struct TopkParams {
   int32_t sel_cap;      // power of two >= k: entries of the LDS sort buffer
 };
 
+// General selection of one row (any score distribution): radix select of
+// the K-th largest key over the whole row, ordered selection, bitonic sort.
+// The fast kernel below falls back to it for rows whose keys crowd into one
+// histogram bin.
 template <bool IN_LDS>
-__global__ __launch_bounds__(kTopkThreads) void li_topk_kernel(TopkParams p) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char tk_smem[];
+__device__ void topk_row_generic(const TopkParams& p, const int64_t row, unsigned char* tk_smem) {
   unsigned long long* sel = (unsigned long long*)tk_smem;   // p.sel_cap entries
   unsigned* hist = (unsigned*)(sel + p.sel_cap);             // 256
   int* s_wsum = (int*)(hist + 256);                          // 16
@@ -224,7 +227,6 @@ __global__ __launch_bounds__(kTopkThreads) void li_topk_kernel(TopkParams p) {
   unsigned* s_keys = s_misc + 4;                             // s2 (IN_LDS)
 
   const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
   const float* srow = p.scores + row * (int64_t)p.s2;
   const int S = p.s2;
   auto key_at = [&](int j) -> unsigned {
@@ -542,6 +544,267 @@ __global__ __launch_bounds__(kTopkThreads) void li_topk_kernel(TopkParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Fast selection, one workgroup per row of up to kFastMaxS2 scores, each
+// thread holding its kFastKpt keys in registers:
+//  1. n_valid, kmin and kmax of the row's finite keys.  All of them share the
+//     key bits above hb = bit length of (kmin ^ kmax).
+//  2. A 4096-bin histogram of the 12 key bits right below that common prefix;
+//     a scan from the top bin gives every bin's start in descending order
+//     and the bin b* that holds the take-th largest key.  The answer lies
+//     among the keys of bins >= b* (the candidates).
+//  3. Counting sort of the candidates by bin: each takes a slot in its bin's
+//     range (one LDS atomic per candidate).
+//  4. Within its bin, a candidate's final position is its rank by
+//     (~key << 32 | index) among the bin's candidates, i.e. score
+//     descending, then index ascending.  The first `take` are the answer.
+// Rows with more candidates than the buffer holds, or a bin above b* with
+// more than kSegCap keys (crowded keys, e.g. many equal scores), take the
+// general path above.
+// ---------------------------------------------------------------------------
+constexpr int kFastKpt = 32;                            // keys per thread
+constexpr int kFastMaxS2 = kFastKpt * kTopkThreads;     // 32768
+constexpr int kFastCap = 4096;                          // candidates (>= the largest K)
+constexpr int kFastBins = 4096;                         // 12-bit digits
+constexpr int kSegCap = 256;                            // keys per bin ranked directly
+constexpr int kTopkWaves = kTopkThreads / 64;
+// LDS of the fast path: bin counts, bin starts, bin cursors, candidate and
+// output buffers, misc words
+constexpr size_t kFastLds = 3 * (size_t)kFastBins * 4 + 2 * (size_t)kFastCap * 8 + 64 * 4;
+
+// Wave-wide operations on DPP lane moves (no LDS round trips).  DPP controls
+// of GFX9: row_shr:n = 0x110 + n, row_bcast:15 = 0x142, row_bcast:31 =
+// 0x143, quad_perm = 0x00..0xff, row_half_mirror = 0x141, row_mirror = 0x140.
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ unsigned dpp_u32(unsigned old, unsigned v) {
+  return (unsigned)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+// inclusive prefix sum over the 64 lanes
+__device__ __forceinline__ unsigned wave_incl_scan(unsigned v) {
+  v += dpp_u32<0x111>(0u, v);
+  v += dpp_u32<0x112>(0u, v);
+  v += dpp_u32<0x114>(0u, v);
+  v += dpp_u32<0x118>(0u, v);
+  v += dpp_u32<0x142, 0xa>(0u, v);
+  v += dpp_u32<0x143, 0xc>(0u, v);
+  return v;
+}
+// reductions whose result is valid in lane 63
+template <typename Op>
+__device__ __forceinline__ unsigned wave_reduce_to63(unsigned v, unsigned ident, Op op) {
+  v = op(v, dpp_u32<0xb1>(ident, v));   // quad_perm [1,0,3,2]
+  v = op(v, dpp_u32<0x4e>(ident, v));   // quad_perm [2,3,0,1]
+  v = op(v, dpp_u32<0x141>(ident, v));  // row_half_mirror
+  v = op(v, dpp_u32<0x140>(ident, v));  // row_mirror
+  v = op(v, dpp_u32<0x142, 0xa>(ident, v));
+  v = op(v, dpp_u32<0x143, 0xc>(ident, v));
+  return v;
+}
+
+// Exclusive scan of four values per thread over the workgroup, in (thread,
+// value) order; wsum: kTopkWaves words of LDS.  Contains two barriers.
+__device__ __forceinline__ void block_scan4(unsigned (&v)[4], unsigned* wsum) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const unsigned loc = v[0] + v[1] + v[2] + v[3];
+  const unsigned incl = wave_incl_scan(loc);
+  if (lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  unsigned before = 0;
+#pragma unroll
+  for (int w = 0; w < kTopkWaves; ++w) before += w < wave ? wsum[w] : 0u;
+  __syncthreads();  // wsum may be rewritten after this
+  unsigned run = before + incl - loc;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const unsigned c = v[i];
+    v[i] = run;
+    run += c;
+  }
+}
+
+template <bool IN_LDS>
+__global__ __launch_bounds__(kTopkThreads) void li_topk_kernel(TopkParams p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char tk_smem[];
+  const int64_t row = blockIdx.x;
+  const int S = p.s2;
+  if (S > kFastMaxS2) {
+    topk_row_generic<IN_LDS>(p, row, tk_smem);
+    return;
+  }
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* srow = p.scores + row * (int64_t)S;
+  const int K = p.k;
+  unsigned* const hcount = (unsigned*)tk_smem;         // kFastBins
+  unsigned* const hbase = hcount + kFastBins;          // kFastBins
+  unsigned* const cursor = hbase + kFastBins;          // kFastBins
+  unsigned long long* const cand = (unsigned long long*)(cursor + kFastBins);  // kFastCap
+  unsigned long long* const outb = cand + kFastCap;    // kFastCap
+  unsigned* const misc = (unsigned*)(outb + kFastCap); // 48 words
+  unsigned* const wsum = misc + 48;                    // kTopkWaves
+
+  // the row in registers, all loads in flight: 16-byte loads where the row
+  // is 16-byte aligned (key u = 4q + e is entry 4 * (q * 1024 + tid) + e),
+  // else entry u * 1024 + tid
+  const bool vec = (((uintptr_t)srow & 15) == 0);
+  auto entry = [&](int u) { return vec ? 4 * ((u >> 2) * kTopkThreads + tid) + (u & 3) : u * kTopkThreads + tid; };
+  unsigned kr[kFastKpt];
+  if (vec) {
+#pragma unroll
+    for (int q = 0; q < kFastKpt / 4; ++q) {
+      const int j = 4 * (q * kTopkThreads + tid);
+      float4 v = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      if (j + 3 < S) {
+        v = *(const float4*)(srow + j);
+      } else {
+        if (j < S) v.x = srow[j];
+        if (j + 1 < S) v.y = srow[j + 1];
+        if (j + 2 < S) v.z = srow[j + 2];
+      }
+      kr[4 * q] = sort_key(v.x);
+      kr[4 * q + 1] = sort_key(v.y);
+      kr[4 * q + 2] = sort_key(v.z);
+      kr[4 * q + 3] = sort_key(v.w);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < kFastKpt; ++u) {
+      const int j = u * kTopkThreads + tid;
+      kr[u] = j < S ? sort_key(srow[j]) : kNegInfKey;
+    }
+  }
+  for (int i = tid; i < kFastBins; i += kTopkThreads) hcount[i] = 0u;
+
+  // ---- 1. count and range of the finite keys ----
+  int nv = 0;
+  unsigned kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+  for (int u = 0; u < kFastKpt; ++u) {
+    const bool v = kr[u] > kNegInfKey;
+    nv += v;
+    kmin = v ? min(kmin, kr[u]) : kmin;
+    kmax = v ? max(kmax, kr[u]) : kmax;
+  }
+  {
+    const unsigned tn = wave_reduce_to63((unsigned)nv, 0u, [](unsigned a, unsigned b) { return a + b; });
+    const unsigned tmin = wave_reduce_to63(kmin, 0xffffffffu, [](unsigned a, unsigned b) { return min(a, b); });
+    const unsigned tmax = wave_reduce_to63(kmax, 0u, [](unsigned a, unsigned b) { return max(a, b); });
+    if (lane == 63) {
+      misc[wave] = tn;
+      misc[kTopkWaves + wave] = tmin;
+      misc[2 * kTopkWaves + wave] = tmax;
+    }
+  }
+  __syncthreads();
+  int n_valid = 0;
+  kmin = 0xffffffffu;
+  kmax = 0u;
+#pragma unroll
+  for (int w = 0; w < kTopkWaves; ++w) {
+    n_valid += (int)misc[w];
+    kmin = min(kmin, misc[kTopkWaves + w]);
+    kmax = max(kmax, misc[2 * kTopkWaves + w]);
+  }
+  const int take = min(K, n_valid);
+  const unsigned diff = kmin ^ kmax;
+  const int hb = diff ? 32 - __clz((int)diff) : 0;
+  const int shift = hb > 12 ? hb - 12 : 0;
+  auto digit = [&](unsigned kk) { return (kk >> shift) & (unsigned)(kFastBins - 1); };
+
+  // ---- 2. histogram, bin starts (descending), threshold bin ----
+  if (take > 0) {
+#pragma unroll
+    for (int u = 0; u < kFastKpt; ++u)
+      if (kr[u] > kNegInfKey) atomicAdd(&hcount[digit(kr[u])], 1u);
+  }
+  __syncthreads();  // also: misc reads done before misc is rewritten
+  int ncand = 0;
+  unsigned bstar = 0;
+  if (take > 0) {
+    // thread t owns bins 4095 - 4t - i (descending), i = 0..3
+    unsigned c[4], ex[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ex[i] = c[i] = hcount[kFastBins - 1 - 4 * tid - i];
+    block_scan4(ex, wsum);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int b = kFastBins - 1 - 4 * tid - i;
+      hbase[b] = ex[i];
+      cursor[b] = ex[i];
+      if (ex[i] < (unsigned)take && ex[i] + c[i] >= (unsigned)take) {
+        misc[0] = (unsigned)b;    // b*
+        misc[1] = ex[i] + c[i];   // keys in bins >= b*
+      }
+    }
+    if (tid == 0) misc[2] = 0u;
+    __syncthreads();
+    bstar = misc[0];
+    ncand = (int)misc[1];
+    // largest bin among the candidates' bins
+    unsigned cm = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cm = (unsigned)(kFastBins - 1 - 4 * tid - i) >= bstar ? max(cm, c[i]) : cm;
+    cm = wave_reduce_to63(cm, 0u, [](unsigned a, unsigned b) { return max(a, b); });
+    if (lane == 63 && cm) atomicMax(&misc[2], cm);
+    __syncthreads();
+    if (ncand > kFastCap || misc[2] > (unsigned)kSegCap) {
+      // crowded keys: the general selection (uniform branch)
+      __syncthreads();
+      topk_row_generic<IN_LDS>(p, row, tk_smem);
+      return;
+    }
+
+    // ---- 3. counting sort of the candidates by bin ----
+    // compact them (block scan of per-thread counts) into outb, then each
+    // takes a slot of its bin's range in cand
+    unsigned cmask = 0u;
+#pragma unroll
+    for (int u = 0; u < kFastKpt; ++u)
+      cmask |= (kr[u] > kNegInfKey && digit(kr[u]) >= bstar) ? (1u << u) : 0u;
+    unsigned off[4] = {(unsigned)__popc(cmask), 0u, 0u, 0u};
+    block_scan4(off, wsum);
+    unsigned o = off[0];
+#pragma unroll
+    for (int u = 0; u < kFastKpt; ++u)
+      if ((cmask >> u) & 1u) outb[o++] = ((unsigned long long)(~kr[u]) << 32) | (unsigned)entry(u);
+    __syncthreads();
+    for (int q = tid; q < ncand; q += kTopkThreads) {
+      const unsigned long long cv = outb[q];
+      const unsigned slot = atomicAdd(&cursor[digit(~(unsigned)(cv >> 32))], 1u);
+      cand[slot] = cv;
+    }
+    __syncthreads();
+
+    // ---- 4. rank within the bin ----
+    for (int q = tid; q < ncand; q += kTopkThreads) {
+      const unsigned long long cv = cand[q];
+      const unsigned d = digit(~(unsigned)(cv >> 32));
+      const int s0 = (int)hbase[d], s1 = s0 + (int)hcount[d];
+      int rank = 0;
+      for (int r = s0; r < s1; ++r) rank += cand[r] < cv;
+      outb[s0 + rank] = cv;
+    }
+    __syncthreads();
+  }
+
+  // ---- outputs ----
+  int32_t* irow = p.indices + row * (int64_t)K;
+  for (int i = tid; i < K; i += kTopkThreads) {
+    int idx = -1;
+    float val = -INFINITY;
+    if (i < take) {
+      idx = (int)(unsigned)(outb[i] & 0xffffffffull);
+      val = srow[idx];  // the score itself (keeps the sign of a zero)
+    }
+    irow[i] = idx;
+    if (p.values) {
+      const int64_t o = row * (int64_t)K + i;
+      if (p.val_dtype == DSA_DTYPE_FP32) ((float*)p.values)[o] = val;
+      else if (p.val_dtype == DSA_DTYPE_BF16) ((bf16*)p.values)[o] = (bf16)val;
+      else ((f16*)p.values)[o] = (f16)val;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 static int64_t pow2_at_least(int64_t x) {
@@ -576,7 +839,8 @@ int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_
   // the full budget)
   static bool attr_set[2] = {false, false};
   const bool in_lds = li_topk_row_in_lds(s2, k);
-  const size_t lds = li_topk_fixed_bytes(k) + (in_lds ? (size_t)s2 * 4 : 0);
+  size_t lds = li_topk_fixed_bytes(k) + (in_lds ? (size_t)s2 * 4 : 0);  // general path
+  if (lds < kFastLds) lds = kFastLds;
   const void* fn = in_lds ? (const void*)li_topk_kernel<true> : (const void*)li_topk_kernel<false>;
   if (!attr_set[in_lds]) {
     DSA_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kTopkLdsBudget));

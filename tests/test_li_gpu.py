@@ -51,7 +51,7 @@ def _topk_gpu(scores_np, k):
     (64, 16, "random"), (300, 64, "ties"), (1000, 2048, "k_gt_s2"), (4096, 2048, "mixed"),
     (4096, 2048, "ties"), (16384, 2048, "random"), (20000, 2048, "ties"), (32768, 2048, "random"),
     (32768, 4096, "mixed"), (5000, 1, "ties"), (2049, 2048, "masked_tail"), (3000, 100, "equal"),
-    (32768, 2048, "narrow"),
+    (32768, 2048, "narrow"), (32767, 2048, "random"), (40001, 2048, "ties"), (8191, 4096, "random"),
 ])
 def test_topk_bit_exact(S2, k, kind):
     print(f"[li topk] S2={S2} k={k} {kind}", flush=True)
