@@ -325,10 +325,10 @@ def long_legs(dev, steps):
     return out
 
 
-def measured_traffic():
+def measured_traffic(name="sfa_fwd_decode_traffic"):
     """HBM bytes per step from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
     summary (scaled by a copy kernel of known size), or None."""
-    path = os.path.join(ROOT, "profiles", "sfa_fwd_decode_traffic.json")
+    path = os.path.join(ROOT, "profiles", name + ".json")
     try:
         with open(path) as f:
             return int(json.load(f)["traffic_bytes_per_step"])
@@ -405,7 +405,8 @@ def main():
                                "D=128, k=2048, sparse_mode 3, bf16 q/k, fp32 weights",
                    "input_sets": len(li_sets)},
         "roofline": {"bound": "hbm", "achieved": round(li_gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(li_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "frac": round(li_gbs / PEAK_HBM_GBS, 4),
+                     "traffic": measured_traffic("lightning_indexer_decode_traffic"),
                      "kernel": "li_score_kernel + li_topk_kernel (one step)",
                      "algorithmic_bytes_per_launch": int(li_bytes),
                      "algorithmic_flops_per_launch": int(li_flops)},
