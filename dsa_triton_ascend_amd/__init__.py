@@ -7,6 +7,10 @@ Public API, mirroring the reference's operator modules:
 * ``lightning_indexer_triton`` / ``LightningIndexerTriton``
 * ``sparse_lightning_indexer_grad_kl_loss_triton`` /
   ``SparseLightningIndexerGradKLLossTriton``
+
+and the autograd pairing for training (``autograd.py``):
+``sparse_flash_attention_train`` / ``SparseFlashAttentionFunction`` and
+``sparse_lightning_indexer_kl_loss`` / ``SparseLightningIndexerKLLossFunction``.
 """
 from .sparse_flash_attention import (  # noqa: F401
     INT64_MAX,
@@ -33,3 +37,10 @@ sparse_flash_attention = sparse_flash_attention_triton
 lightning_indexer = lightning_indexer_triton
 sparse_flash_attention_grad = sparse_flash_attention_grad_triton
 sparse_lightning_indexer_grad_kl_loss = sparse_lightning_indexer_grad_kl_loss_triton
+
+from .autograd import (  # noqa: F401,E402
+    SparseFlashAttentionFunction,
+    SparseLightningIndexerKLLossFunction,
+    sparse_flash_attention_train,
+    sparse_lightning_indexer_kl_loss,
+)

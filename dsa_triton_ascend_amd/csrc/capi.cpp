@@ -216,7 +216,7 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
   DSA_CHECK_ARG(query && query_rope && key && key_rope && sparse_indices && d_out && out && softmax_max &&
                     softmax_sum,
                 "null input tensor pointer");
-  DSA_CHECK_ARG(d_query && d_query_rope && d_key && d_key_rope && d_value, "null output tensor pointer");
+  DSA_CHECK_ARG(d_query && d_query_rope && d_key && d_key_rope, "null output tensor pointer");
   DSA_CHECK_SUPPORTED(d == 128 || d == 256 || d == 512, "D must be one of (128, 256, 512), got %lld",
                       (long long)d);
   DSA_CHECK_SUPPORTED(d_rope == 64, "rope dim must be 64, got %lld", (long long)d_rope);

@@ -704,6 +704,29 @@ static hipError_t launch_sfa_bwd(const SfaBwdParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// d_key = dk + dv (fp32 workspaces summed before the cast)
+template <typename T>
+__global__ __launch_bounds__(256) void cast_sum_f32_kernel(const float* a, const float* b, T* dst, int64_t n) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i + 3 < n) {
+    const float4 x = *(const float4*)(a + i), y = *(const float4*)(b + i);
+    typedef T T4 __attribute__((ext_vector_type(4)));
+    const T4 o = {Elem<T>::from_f32(x.x + y.x), Elem<T>::from_f32(x.y + y.y), Elem<T>::from_f32(x.z + y.z),
+                  Elem<T>::from_f32(x.w + y.w)};
+    *(T4*)(dst + i) = o;
+  } else {
+    for (int64_t j = i; j < n; ++j) dst[j] = Elem<T>::from_f32(a[j] + b[j]);
+  }
+}
+
+template <typename T>
+static hipError_t launch_cast_sum(const float* a, const float* b, void* dst, int64_t n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  const int64_t blocks = (n + 1023) / 1024;
+  hipLaunchKernelGGL((cast_sum_f32_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, stream, a, b, (T*)dst, n);
+  return hipGetLastError();
+}
+
 template <typename T>
 static hipError_t launch_cast(const float* src, void* dst, int64_t n, hipStream_t stream) {
   if (n <= 0) return hipSuccess;
@@ -766,9 +789,15 @@ int sfa_bwd_run(const void* query, const void* query_rope, const void* key, cons
   auto cast = [&](const float* src, void* dst, int64_t n) {
     return bf ? launch_cast<bf16>(src, dst, n, stream) : launch_cast<f16>(src, dst, n, stream);
   };
-  DSA_HIP(cast(p.dk, d_key, kv_rows * d));
+  if (d_value) {
+    DSA_HIP(cast(p.dk, d_key, kv_rows * d));
+    DSA_HIP(cast(p.dv, d_value, kv_rows * d));
+  } else {
+    // shared latent: d_key = dk + dv
+    DSA_HIP(bf ? launch_cast_sum<bf16>(p.dk, p.dv, d_key, kv_rows * d, stream)
+               : launch_cast_sum<f16>(p.dk, p.dv, d_key, kv_rows * d, stream));
+  }
   DSA_HIP(cast(p.dkr, d_key_rope, kv_rows * 64));
-  DSA_HIP(cast(p.dv, d_value, kv_rows * d));
   return DSA_OK;
 }
 

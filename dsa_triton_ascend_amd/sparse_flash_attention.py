@@ -217,6 +217,22 @@ class SparseFlashAttentionTriton(torch.nn.Module):
 
     def forward(self, query, key, value, sparse_indices, query_rope=None, key_rope=None,
                 actual_seq_lengths_query=None, actual_seq_lengths_kv=None, block_table=None):
+        needs_grad = torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad for t in (query, key, query_rope, key_rope))
+        if needs_grad and self.layout_kv != "PA_BSND" and self.layout_query == self.layout_kv:
+            # training: the forward/backward pair as one autograd op (the
+            # reference's P.Morph bprop recipe, sparse_flash_attention_grad_triton.py:30-71)
+            from .autograd import sparse_flash_attention_train
+            if self.pre_tokens != INT64_MAX or self.next_tokens != INT64_MAX or self.attention_mode != 2:
+                raise ValueError("pre_tokens/next_tokens only support default and attention_mode must be 2")
+            out, smax, ssum = sparse_flash_attention_train(
+                query, key, sparse_indices, scale_value=self.scale_value, query_rope=query_rope,
+                key_rope=key_rope, actual_seq_lengths_query=actual_seq_lengths_query,
+                actual_seq_lengths_kv=actual_seq_lengths_kv, sparse_block_size=self.sparse_block_size,
+                layout=self.layout_query, sparse_mode=self.sparse_mode)
+            if not self.return_softmax_lse:
+                smax, ssum = torch.zeros_like(smax), torch.zeros_like(ssum)
+            return out, smax, ssum
         return sparse_flash_attention_triton(
             query, key, value, sparse_indices,
             scale_value=self.scale_value, block_table=block_table,

@@ -43,6 +43,18 @@ def sparse_flash_attention_grad_triton(
 ):
     """SFA backward (MLA-absorb, MQA); see module docstring.  ``value`` is
     only used for the dtype of d_value (value = key[..., :D])."""
+    return _sfa_grad(query, key, value, sparse_indices, d_out, out, softmax_max, softmax_sum,
+                     scale_value, query_rope, key_rope, actual_seq_lengths_query, actual_seq_lengths_kv,
+                     sparse_block_size, layout, sparse_mode, pre_tokens, next_tokens, deterministic,
+                     merge_kv=False)
+
+
+def _sfa_grad(query, key, value, sparse_indices, d_out, out, softmax_max, softmax_sum, scale_value,
+              query_rope, key_rope, actual_seq_lengths_query, actual_seq_lengths_kv, sparse_block_size,
+              layout, sparse_mode, pre_tokens, next_tokens, deterministic, merge_kv):
+    """Body of the backward.  With ``merge_kv`` the key gradient is dk + dv,
+    summed in fp32 before the cast (the shared-latent gradient), and d_value
+    is None."""
     if pre_tokens != INT64_MAX or next_tokens != INT64_MAX:
         raise ValueError("pre_tokens/next_tokens only support default INT64_MAX")
     if sparse_mode not in (0, 3):
@@ -98,9 +110,9 @@ def sparse_flash_attention_grad_triton(
     dqr = torch.empty_like(query_rope)
     dk = torch.empty_like(key)
     dkr = torch.empty_like(key_rope)
-    dv = torch.empty(key.shape, dtype=value.dtype if value is not None else key.dtype, device=device)
-    if dv.dtype != key.dtype:
+    if value is not None and value.dtype != key.dtype:
         raise ValueError("value dtype must equal the key dtype")
+    dv = None if merge_kv else torch.empty(key.shape, dtype=key.dtype, device=device)
     lib = _lib.load()
     ws_bytes = lib.dsa_sfa_bwd_workspace_size(kv_rows, D)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
@@ -112,7 +124,7 @@ def sparse_flash_attention_grad_triton(
         c[0].data_ptr(), c[1].data_ptr(), c[2].data_ptr(), c[3].data_ptr(), si.data_ptr(),
         c[4].data_ptr(), c[5].data_ptr(), smax.data_ptr(), ssum.data_ptr(),
         _lib.ptr(act_q), _lib.ptr(act_k),
-        dq.data_ptr(), dqr.data_ptr(), dk.data_ptr(), dkr.data_ptr(), dv.data_ptr(),
+        dq.data_ptr(), dqr.data_ptr(), dk.data_ptr(), dkr.data_ptr(), _lib.ptr(dv),
         B, S1, S2, N1, D, D_ROPE, K, q_rows, kv_rows, sparse_block_size, sparse_mode,
         _lib.LAYOUT[layout], _lib.dtype_code(query.dtype), float(scale_value),
         ws.data_ptr(), ws_bytes, _lib.stream_handle(device))

@@ -94,6 +94,9 @@ size_t dsa_sfa_fwd_workspace_size(int64_t q_rows, int64_t n1, int64_t d,
  * in the query dtype and d_key / d_value [KV, D], d_key_rope [KV, 64] in the
  * key dtype.  d_key (through the scores) and d_value (through P.dO) are
  * separate, as in the reference; a caller sharing key and value sums them.
+ * d_value may be NULL: d_key then receives dk + dv, summed in fp32 before
+ * the cast (MLA absorb, value = key[..., :D]: the gradient of the shared
+ * latent, which the reference's bprop recipe forms as dk + dv, 30-71).
  * The dK / dV scatter-add uses fp32 atomics: results may differ in the last
  * bits between runs, as the reference's (deterministic mode is rejected by
  * the reference API, 434-435).  The workspace holds the fp32 accumulators.
