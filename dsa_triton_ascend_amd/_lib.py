@@ -88,6 +88,22 @@ SIGNATURES = {
         _vp,                                  # stream
     ]),
     "dsa_li_topk_from_scores": (_c.c_int, [_vp, _i64, _i64, _i64, _i32p, _vp, _vp]),
+    "dsa_li_fwd_paged": (_c.c_int, [
+        _vp, _vp, _vp, _i32p, _i32p, _i32p,   # query, key_cache, weights, actual_seq_q, actual_seq_k, block_table
+        _i32p, _vp,                           # sparse_indices, sparse_values
+        _i64, _i64, _i64, _i64, _i64,         # batch, s1, n1, n2, d
+        _i64, _i64, _i64, _i64, _i64,         # sparse_count, q_rows, num_blocks, page_size, max_blocks
+        _i32, _i32, _i32, _i32, _i32,         # sparse_mode, layout_q, dtype, w_dtype, return_value
+        _vp, _sz, _vp,                        # workspace, workspace_bytes, stream
+    ]),
+    "dsa_li_scores_paged": (_c.c_int, [
+        _vp, _vp, _vp, _i32p, _i32p, _i32p,   # query, key_cache, weights, actual_seq_q, actual_seq_k, block_table
+        _vp,                                  # scores
+        _i64, _i64, _i64, _i64, _i64,         # batch, s1, n1, n2, d
+        _i64, _i64, _i64, _i64,               # q_rows, num_blocks, page_size, max_blocks
+        _i32, _i32, _i32, _i32,               # sparse_mode, layout_q, dtype, w_dtype
+        _vp,                                  # stream
+    ]),
 }
 
 _lib = None

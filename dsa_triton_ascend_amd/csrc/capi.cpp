@@ -73,7 +73,8 @@ int li_scores_run(const void* query, const void* key, const void* weights, const
                   const int32_t* act_k, float* scores, int64_t batch, int64_t s1, int64_t s2,
                   int64_t n1, int64_t n2, int64_t d, int64_t q_rows, int64_t k_rows,
                   int32_t sparse_mode, int32_t layout_q, int32_t layout_k, int32_t dtype,
-                  int32_t w_dtype, hipStream_t stream);
+                  int32_t w_dtype, hipStream_t stream, const int32_t* block_table = nullptr,
+                  int64_t max_blocks = 0, int64_t page_size = 1);
 int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_t* indices,
                 void* values, int32_t val_dtype, hipStream_t stream);
 constexpr int64_t kLiMaxK = 4096;
@@ -85,7 +86,7 @@ static int li_check_scores(const void* query, const void* key, const void* weigh
                            const int32_t* act_q, const int32_t* act_k, int64_t batch, int64_t s1,
                            int64_t s2, int64_t n1, int64_t n2, int64_t d, int64_t q_rows,
                            int64_t k_rows, int32_t sparse_mode, int32_t layout_q,
-                           int32_t layout_k, int32_t dtype, int32_t w_dtype) {
+                           int32_t layout_k, int32_t dtype, int32_t w_dtype, bool allow_pa = false) {
   DSA_CHECK_ARG(query && key && weights, "null tensor pointer");
   DSA_CHECK_SUPPORTED(d == 64 || d == 128 || d == 256, "head dim D must be one of (64, 128, 256), got %lld",
                       (long long)d);
@@ -101,12 +102,15 @@ static int li_check_scores(const void* query, const void* key, const void* weigh
                       "weights dtype must be bfloat16, float16 or float32");
   DSA_CHECK_SUPPORTED(layout_q == DSA_LAYOUT_BSND || layout_q == DSA_LAYOUT_TND,
                       "layout_query must be BSND or TND");
-  DSA_CHECK_SUPPORTED(layout_k == DSA_LAYOUT_BSND || layout_k == DSA_LAYOUT_TND,
-                      "layout_key must be BSND or TND (block_table / PA_BSND is not supported)");
+  DSA_CHECK_SUPPORTED(layout_k == DSA_LAYOUT_BSND || layout_k == DSA_LAYOUT_TND ||
+                          (allow_pa && layout_k == DSA_LAYOUT_PA_BSND),
+                      "layout_key must be BSND or TND here (a paged key cache goes through the _paged entry points)");
   DSA_CHECK_ARG(!(layout_q == DSA_LAYOUT_BSND && layout_k == DSA_LAYOUT_TND),
                 "a TND key needs a TND query");
   DSA_CHECK_ARG(batch >= 1 && batch <= (1 << 24), "batch must be >= 1");
   DSA_CHECK_ARG(s2 >= 1 && s2 <= 65535ll * 1024, "S2 must be in [1, 67107840]");
+  if (layout_k == DSA_LAYOUT_PA_BSND)
+    DSA_CHECK_ARG(act_k, "PA_BSND key requires actual_seq_lengths_key (per-batch lengths)");
   if (layout_q == DSA_LAYOUT_TND) {
     DSA_CHECK_ARG(act_q && act_k, "TND layout requires cumulative actual_seq_lengths_query and _key");
     DSA_CHECK_ARG(q_rows >= 1, "TND query must have at least one row");
@@ -354,6 +358,68 @@ int dsa_li_fwd(const void* query, const void* key, const void* weights, const in
   st = li_scores_run(query, key, weights, actual_seq_q, actual_seq_k, scores, batch, s1, s2, n1, n2, d,
                      q_rows, k_rows, sparse_mode, layout_query, layout_key, dtype, weights_dtype,
                      (hipStream_t)stream);
+  if (st != DSA_OK) return st;
+  return li_topk_run(scores, q_rows * n2, s2, sparse_count, sparse_indices,
+                     return_value ? sparse_values : nullptr, dtype, (hipStream_t)stream);
+}
+
+static int li_check_paged(const int32_t* block_table, int64_t num_blocks, int64_t page_size,
+                          int64_t max_blocks) {
+  DSA_CHECK_ARG(block_table, "PA_BSND key requires a block_table");
+  DSA_CHECK_ARG(page_size >= 1 && page_size <= (1 << 20), "page (block) size must be in [1, 2^20]");
+  DSA_CHECK_ARG(num_blocks >= 1 && max_blocks >= 1, "the cache and the block table need at least one block");
+  DSA_CHECK_ARG(max_blocks * page_size <= 65535ll * 1024, "max_blocks * page size must be <= 67107840");
+  DSA_CHECK_ARG(num_blocks * page_size < (1ll << 31), "the key cache must have fewer than 2^31 rows");
+  return DSA_OK;
+}
+
+int dsa_li_scores_paged(const void* query, const void* key_cache, const void* weights,
+                        const int32_t* actual_seq_q, const int32_t* actual_seq_k, const int32_t* block_table,
+                        float* scores, int64_t batch, int64_t s1, int64_t n1, int64_t n2, int64_t d,
+                        int64_t q_rows, int64_t num_blocks, int64_t page_size, int64_t max_blocks,
+                        int32_t sparse_mode, int32_t layout_query, int32_t dtype, int32_t weights_dtype,
+                        void* stream) {
+  g_err[0] = '\0';
+  int st = li_check_paged(block_table, num_blocks, page_size, max_blocks);
+  if (st != DSA_OK) return st;
+  const int64_t s2 = max_blocks * page_size, k_rows = num_blocks * page_size;
+  st = li_check_scores(query, key_cache, weights, actual_seq_q, actual_seq_k, batch, s1, s2, n1, n2, d, q_rows,
+                       k_rows, sparse_mode, layout_query, DSA_LAYOUT_PA_BSND, dtype, weights_dtype, true);
+  if (st != DSA_OK) return st;
+  DSA_CHECK_ARG(scores, "null scores pointer");
+  return li_scores_run(query, key_cache, weights, actual_seq_q, actual_seq_k, scores, batch, s1, s2, n1, n2, d,
+                       q_rows, k_rows, sparse_mode, layout_query, DSA_LAYOUT_PA_BSND, dtype, weights_dtype,
+                       (hipStream_t)stream, block_table, max_blocks, page_size);
+}
+
+int dsa_li_fwd_paged(const void* query, const void* key_cache, const void* weights, const int32_t* actual_seq_q,
+                     const int32_t* actual_seq_k, const int32_t* block_table, int32_t* sparse_indices,
+                     void* sparse_values, int64_t batch, int64_t s1, int64_t n1, int64_t n2, int64_t d,
+                     int64_t sparse_count, int64_t q_rows, int64_t num_blocks, int64_t page_size,
+                     int64_t max_blocks, int32_t sparse_mode, int32_t layout_query, int32_t dtype,
+                     int32_t weights_dtype, int32_t return_value, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+  g_err[0] = '\0';
+  int st = li_check_paged(block_table, num_blocks, page_size, max_blocks);
+  if (st != DSA_OK) return st;
+  const int64_t s2 = max_blocks * page_size, k_rows = num_blocks * page_size;
+  st = li_check_scores(query, key_cache, weights, actual_seq_q, actual_seq_k, batch, s1, s2, n1, n2, d, q_rows,
+                       k_rows, sparse_mode, layout_query, DSA_LAYOUT_PA_BSND, dtype, weights_dtype, true);
+  if (st != DSA_OK) return st;
+  DSA_CHECK_ARG(sparse_indices, "null sparse_indices pointer");
+  DSA_CHECK_ARG(!return_value || sparse_values, "return_value requires a sparse_values buffer");
+  DSA_CHECK_SUPPORTED(sparse_count >= 1 && sparse_count <= kLiMaxK,
+                      "sparse_count must be in [1, %lld], got %lld", (long long)kLiMaxK,
+                      (long long)sparse_count);
+  const size_t need = dsa_li_fwd_workspace_size(q_rows, n2, s2);
+  if (workspace == nullptr || workspace_bytes < need) {
+    set_error("workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    return DSA_ERR_WORKSPACE;
+  }
+  float* scores = (float*)workspace;
+  st = li_scores_run(query, key_cache, weights, actual_seq_q, actual_seq_k, scores, batch, s1, s2, n1, n2, d,
+                     q_rows, k_rows, sparse_mode, layout_query, DSA_LAYOUT_PA_BSND, dtype, weights_dtype,
+                     (hipStream_t)stream, block_table, max_blocks, page_size);
   if (st != DSA_OK) return st;
   return li_topk_run(scores, q_rows * n2, s2, sparse_count, sparse_indices,
                      return_value ? sparse_values : nullptr, dtype, (hipStream_t)stream);

@@ -46,6 +46,10 @@ struct LiParams {
   int32_t batch, s1, s2, n1, n2, g;
   int32_t mode, layout_q, layout_k, w_dtype;
   int32_t chunk;       // keys per workgroup
+  // PA_BSND key cache [blocks, page, N2, D]: key s2 of batch b is row
+  // block_table[b, s2 / page] * page + s2 % page (k_rows = blocks * page)
+  const int32_t* block_table;
+  int32_t max_blocks, page_size;
 };
 
 constexpr int kLiThreads = 256;
@@ -74,7 +78,12 @@ __device__ __forceinline__ LiRow li_row_info(const LiParams& p, int row) {
     r.s1 = row - r.b * p.s1;
     aq = p.act_q ? p.act_q[r.b] : p.s1;
   }
-  if (p.layout_k == DSA_LAYOUT_TND || p.layout_q == DSA_LAYOUT_TND) {
+  if (p.layout_k == DSA_LAYOUT_PA_BSND) {
+    // paged keys: per-batch lengths whatever the query layout (as the SFA
+    // forward's PA_BSND key); rows come from the block table
+    r.k_base = 0;
+    ak = p.act_k[r.b];
+  } else if (p.layout_k == DSA_LAYOUT_TND || p.layout_q == DSA_LAYOUT_TND) {
     // with a TND query both length arrays are cumulative (the reference
     // converts both, lightning_indexer_triton.py:500-506)
     const int start = r.b ? p.act_k[r.b - 1] : 0;
@@ -165,10 +174,18 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
   // NP groups in flight per wave (ring of K fragment registers).  Loads are
   // issued unconditionally (groups past the end reload the last one), so no
   // load sits under a branch.
+  const bool paged = p.layout_k == DSA_LAYOUT_PA_BSND;
+  const int32_t* btab = paged ? p.block_table + (int64_t)ri.b * p.max_blocks : nullptr;
   auto kload = [&](int grp, u32x4 (&kf)[KS]) {
     int key = c0 + grp * 16 + li;
     key = key < lastvis ? key : lastvis;  // stays in the batch's rows; masked below
     int64_t krow = ri.k_base + key;
+    if (paged) {
+      // a -1 or out-of-range page reads row 0; its scores are set to zero
+      // after the loop (a zero key row, as de-paging leaves it)
+      const int blk = btab[key / p.page_size];
+      krow = (int64_t)(blk < 0 ? 0 : blk) * p.page_size + key % p.page_size;
+    }
     krow = krow < p.k_rows ? krow : p.k_rows - 1;  // inconsistent cumulative lengths stay in bounds
     const T* kp = (const T*)p.k + (krow * p.n2 + kh) * D + lg * 8;
 #pragma unroll
@@ -206,9 +223,21 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
     }
   }
   __syncthreads();
+  const int n = c1 - c0;
+  if (paged) {
+    // keys in -1 (or out-of-range) pages are zero rows: score 0 while visible
+    const int64_t nblk = p.k_rows / p.page_size;
+    for (int j = threadIdx.x; j < n; j += kLiThreads) {
+      const int key = c0 + j;
+      if (key < ri.lim) {
+        const int blk = btab[key / p.page_size];
+        if (blk < 0 || blk >= nblk) s_sc[j] = 0.f;
+      }
+    }
+    __syncthreads();
+  }
   // coalesced stores of the chunk's scores (16 bytes per lane where the
   // destination is 16-byte aligned)
-  const int n = c1 - c0;
   float* dst = srow + c0;
   const int head = (int)(((16 - ((uintptr_t)dst & 15)) & 15) >> 2);  // scalars before 16-byte alignment
   const int h = head < n ? head : n;
@@ -928,7 +957,8 @@ int li_scores_run(const void* query, const void* key, const void* weights, const
                   const int32_t* act_k, float* scores, int64_t batch, int64_t s1, int64_t s2,
                   int64_t n1, int64_t n2, int64_t d, int64_t q_rows, int64_t k_rows,
                   int32_t sparse_mode, int32_t layout_q, int32_t layout_k, int32_t dtype,
-                  int32_t w_dtype, hipStream_t stream) {
+                  int32_t w_dtype, hipStream_t stream, const int32_t* block_table,
+                  int64_t max_blocks, int64_t page_size) {
   if (q_rows <= 0 || s2 <= 0) return DSA_OK;
   LiParams p;
   p.q = query;
@@ -949,6 +979,9 @@ int li_scores_run(const void* query, const void* key, const void* weights, const
   p.layout_q = layout_q;
   p.layout_k = layout_k;
   p.w_dtype = w_dtype;
+  p.block_table = block_table;
+  p.max_blocks = (int32_t)max_blocks;
+  p.page_size = (int32_t)(page_size > 0 ? page_size : 1);
   p.chunk = kLiChunk;
   hipError_t e = dtype == DSA_DTYPE_BF16 ? launch_score_d<bf16>(p, d, stream)
                                          : launch_score_d<f16>(p, d, stream);

@@ -12,6 +12,10 @@ resolved in the kernel from the cumulative lengths.  The top-k order is the
 stable one the reference's readme specifies (readme.md:63-69): score
 descending, index ascending on ties; entries whose score is -inf are -1.
 
+Extension: ``layout_key="PA_BSND"`` with a ``block_table`` runs the indexer
+over a paged key cache (``_lightning_indexer_paged``); the reference rejects
+a block_table, and still does here with any other key layout.
+
 Deliberate differences, on inputs the reference does not handle:
 * ``sparse_count`` larger than the key length pads with -1 (the reference's
   reshape fails, lines 341 vs 540);
@@ -55,12 +59,15 @@ def lightning_indexer_triton(
     Args mirror lightning_indexer_triton.py:462-494.  ``pre_tokens`` and
     ``next_tokens`` are accepted and ignored, as in the reference.
     """
-    if block_table is not None:
+    if block_table is not None and layout_key != "PA_BSND":
         raise ValueError("PA_BSND / block_table not supported in triton lightning_indexer")
     if layout_query not in ("BSND", "TND"):
         raise ValueError(f"layout_query must be BSND or TND, got {layout_query}")
-    if layout_key not in ("BSND", "TND"):
-        raise ValueError(f"layout_key must be BSND or TND, got {layout_key}")
+    if layout_key not in ("BSND", "TND", "PA_BSND"):
+        raise ValueError(f"layout_key must be BSND, TND or PA_BSND, got {layout_key}")
+    if layout_key == "PA_BSND":
+        return _lightning_indexer_paged(query, key, weights, actual_seq_lengths_query, actual_seq_lengths_key,
+                                        block_table, layout_query, sparse_count, sparse_mode, return_value)
     if sparse_mode not in (0, 3):
         raise ValueError("Only sparse_mode 0 (full) / 3 (rightDownCausal) supported")
     if query.dtype not in (torch.bfloat16, torch.float16) or key.dtype != query.dtype:
@@ -133,6 +140,74 @@ def lightning_indexer_triton(
         _weights_code(weights.dtype), 1 if return_value else 0,
         ws.data_ptr(), ws_bytes, _lib.stream_handle(device))
     _lib.check(st, "lightning_indexer")
+    return indices, values
+
+
+def _lightning_indexer_paged(query, key, weights, actual_seq_lengths_query, actual_seq_lengths_key,
+                             block_table, layout_query, sparse_count, sparse_mode, return_value):
+    """The indexer over a paged key cache [blocks, page, N2, D] (an extension:
+    the reference rejects block_table, lightning_indexer_triton.py:497-498).
+    Key s2 of batch b is cache row block_table[b, s2 // page] * page +
+    s2 % page; a -1 block reads as zero key rows, as the reference's SFA
+    de-paging leaves them (sparse_flash_attention_triton.py:382-403).
+    ``actual_seq_lengths_key`` holds per-batch key lengths."""
+    if block_table is None:
+        raise ValueError("PA_BSND key layout requires block_table")
+    if actual_seq_lengths_key is None:
+        raise ValueError("PA_BSND key layout requires actual_seq_lengths_key")
+    if sparse_mode not in (0, 3):
+        raise ValueError("Only sparse_mode 0 (full) / 3 (rightDownCausal) supported")
+    if query.dtype not in (torch.bfloat16, torch.float16) or key.dtype != query.dtype:
+        raise ValueError("query and key must both be bfloat16 or both float16")
+    if key.dim() != 4 or block_table.dim() != 2:
+        raise ValueError("PA_BSND key must be [blocks, page, N2, D] and block_table [B, max_blocks]")
+    device = _check_device(query, key, weights, block_table)
+    num_blocks, page, N2, Dk = key.shape
+    max_blocks = block_table.shape[1]
+    act_q = _seq_tensor(actual_seq_lengths_query, device)
+    act_k = _seq_tensor(actual_seq_lengths_key, device)
+    if layout_query == "TND":
+        if act_q is None:
+            raise ValueError("TND layout requires actual_seq_lengths_query")
+        T1, N1, D = query.shape
+        B, S1, q_rows = act_q.numel(), 0, T1
+        w_shape = (T1, N1)
+        out_shape = (q_rows, N2, int(sparse_count))
+    else:
+        B, S1, N1, D = query.shape
+        q_rows = B * S1
+        w_shape = (B, S1, N1)
+        out_shape = (B, S1, N2, int(sparse_count))
+    if block_table.shape[0] != B or act_k.numel() != B:
+        raise ValueError("block_table and actual_seq_lengths_key need one row / entry per batch")
+    if Dk != D:
+        raise ValueError("query and key head dims differ")
+    if N1 % N2 != 0:
+        raise ValueError(f"N1({N1}) must be divisible by N2({N2})")
+    if D not in _VALID_D:
+        raise ValueError(f"head dim must be one of {_VALID_D}, got {D}")
+    if tuple(weights.shape) != w_shape:
+        raise ValueError(f"weights must have shape {w_shape}, got {tuple(weights.shape)}")
+    K = int(sparse_count)
+    if K < 1 or K > 4096:
+        raise ValueError("sparse_count must be in [1, 4096]")
+    indices = torch.empty(out_shape, dtype=torch.int32, device=device)
+    values = torch.zeros(out_shape, dtype=query.dtype, device=device)
+    if q_rows == 0:
+        return indices, values
+    lib = _lib.load()
+    S2 = max_blocks * page
+    ws_bytes = lib.dsa_li_fwd_workspace_size(q_rows, N2, S2)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    qc, kc, wc = query.contiguous(), key.contiguous(), weights.contiguous()
+    bt = block_table.to(torch.int32).contiguous()
+    st = lib.dsa_li_fwd_paged(
+        qc.data_ptr(), kc.data_ptr(), wc.data_ptr(), _lib.ptr(act_q), act_k.data_ptr(), bt.data_ptr(),
+        indices.data_ptr(), values.data_ptr() if return_value else None,
+        B, S1, N1, N2, D, K, q_rows, num_blocks, page, max_blocks, sparse_mode,
+        _lib.LAYOUT[layout_query], _lib.dtype_code(query.dtype), _weights_code(weights.dtype),
+        1 if return_value else 0, ws.data_ptr(), ws_bytes, _lib.stream_handle(device))
+    _lib.check(st, "lightning_indexer (paged key)")
     return indices, values
 
 

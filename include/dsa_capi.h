@@ -194,6 +194,36 @@ int dsa_li_scores(const void* query, const void* key, const void* weights,
 int dsa_li_topk_from_scores(const float* scores, int64_t rows, int64_t s2, int64_t sparse_count,
                             int32_t* indices, float* values, void* stream);
 
+/*
+ * Lightning indexer over a paged key cache (PA_BSND).  The reference rejects
+ * a block_table (lightning_indexer_triton.py:497-498); this entry point is
+ * its extension to the paged indexer-key cache of decode, with the paging
+ * semantics of the reference's SFA de-paging (sparse_flash_attention_triton.py
+ * :382-403): key s2 of batch b is row block_table[b, s2 / page_size] *
+ * page_size + s2 % page_size of key_cache [num_blocks, page_size, N2, D], and a
+ * -1 (or out-of-range) block reads as a zero key row (score 0 while visible).
+ * actual_seq_k holds per-batch key lengths (required); the score rows are
+ * max_blocks * page_size wide.  Query, weights, outputs and workspace
+ * (dsa_li_fwd_workspace_size(q_rows, n2, max_blocks * page_size)) as
+ * dsa_li_fwd; layout_query BSND or TND (cumulative actual_seq_q).
+ */
+int dsa_li_fwd_paged(const void* query, const void* key_cache, const void* weights,
+                     const int32_t* actual_seq_q, const int32_t* actual_seq_k,
+                     const int32_t* block_table, int32_t* sparse_indices, void* sparse_values,
+                     int64_t batch, int64_t s1, int64_t n1, int64_t n2, int64_t d,
+                     int64_t sparse_count, int64_t q_rows, int64_t num_blocks, int64_t page_size,
+                     int64_t max_blocks, int32_t sparse_mode, int32_t layout_query, int32_t dtype,
+                     int32_t weights_dtype, int32_t return_value, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* Scores only of dsa_li_fwd_paged: scores [R1*N2, max_blocks * page_size] fp32. */
+int dsa_li_scores_paged(const void* query, const void* key_cache, const void* weights,
+                        const int32_t* actual_seq_q, const int32_t* actual_seq_k,
+                        const int32_t* block_table, float* scores, int64_t batch, int64_t s1,
+                        int64_t n1, int64_t n2, int64_t d, int64_t q_rows, int64_t num_blocks,
+                        int64_t page_size, int64_t max_blocks, int32_t sparse_mode,
+                        int32_t layout_query, int32_t dtype, int32_t weights_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,7 +17,7 @@ is padded with index -1 / value -inf (the reference's reshape fails there).
 """
 import numpy as np
 
-from .common import cumsum_to_lengths, tnd_to_bsnd, bsnd_to_tnd, round_to
+from .common import cumsum_to_lengths, tnd_to_bsnd, bsnd_to_tnd, round_to, pa_to_bsnd
 
 
 def visible_limit(sparse_mode, aq, ak, s1, S2):
@@ -77,16 +77,24 @@ def stable_topk(scores, k):
 def lightning_indexer(query, key, weights, actual_seq_lengths_query=None,
                       actual_seq_lengths_key=None, layout_query="BSND",
                       layout_key="BSND", sparse_count=2048, sparse_mode=3,
-                      return_value=False, value_dtype="bfloat16"):
+                      return_value=False, value_dtype="bfloat16", block_table=None):
     """Oracle of the public indexer API (lightning_indexer_triton.py:462-550).
 
     Returns (indices int32, values rounded to ``value_dtype``), BSND
-    [B,S1,N2,k] or TND [T1,N2,k].
+    [B,S1,N2,k] or TND [T1,N2,k].  ``layout_key="PA_BSND"`` (the build's
+    extension; the reference rejects a block_table, 497-498) de-pages the key
+    cache the way the reference's SFA does (``pa_to_bsnd``,
+    sparse_flash_attention_triton.py:382-403: -1 blocks stay zero rows) and
+    takes per-batch ``actual_seq_lengths_key``.
     """
     is_tnd = layout_query == "TND"
+    paged = layout_key == "PA_BSND"
+    if paged:
+        key = pa_to_bsnd(key, block_table, np.asarray(block_table).shape[1] * key.shape[1])
+        ak_paged = np.asarray(actual_seq_lengths_key)
     if is_tnd:
         aq = cumsum_to_lengths(actual_seq_lengths_query)
-        ak = cumsum_to_lengths(actual_seq_lengths_key)
+        ak = ak_paged if paged else cumsum_to_lengths(actual_seq_lengths_key)
         q = tnd_to_bsnd(query, aq)
         w = tnd_to_bsnd(weights, aq)
         k = tnd_to_bsnd(key, ak) if layout_key == "TND" else key
@@ -95,6 +103,8 @@ def lightning_indexer(query, key, weights, actual_seq_lengths_query=None,
         B = q.shape[0]
         aq = np.full(B, q.shape[1]) if actual_seq_lengths_query is None else np.asarray(actual_seq_lengths_query)
         ak = np.full(B, k.shape[1]) if actual_seq_lengths_key is None else np.asarray(actual_seq_lengths_key)
+        if paged:
+            ak = ak_paged
     B, S1 = q.shape[0], q.shape[1]
     S2, N2 = k.shape[1], k.shape[2]
     sc = indexer_scores(q, k, w, aq, ak, sparse_mode)

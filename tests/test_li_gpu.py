@@ -259,3 +259,100 @@ def test_indexer_repeatable():
                                      sparse_count=512, return_value=True)
     torch.cuda.synchronize()
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+# ---------------------------------------------------------------------------
+# paged key cache (PA_BSND; an extension, the reference rejects block_table)
+# ---------------------------------------------------------------------------
+def _paged_case(B, page, max_blocks, N2, D, dtype, seed, holes=True):
+    """A key cache of random blocks, each batch's table a random choice of
+    physical blocks, optionally with -1 holes; returns (cache, table, dense)."""
+    from oracle.common import pa_to_bsnd
+    rng = np.random.RandomState(seed)
+    nblk = B * max_blocks + 3
+    cache = to_dtype_np(rng.randn(nblk, page, N2, D).astype(np.float16).astype(np.float32), dtype)
+    table = rng.permutation(nblk)[:B * max_blocks].reshape(B, max_blocks).astype(np.int32)
+    if holes:
+        table[0, 1] = -1
+        table[B - 1, max_blocks - 1] = -1
+    dense = pa_to_bsnd(cache, table, max_blocks * page)
+    return cache, table, dense
+
+
+@pytest.mark.parametrize("layout_q", ["BSND", "TND"])
+def test_indexer_paged_matches_depaged(layout_q):
+    print(f"[li paged] query {layout_q}", flush=True)
+    dsa = _api()
+    dtype = torch.bfloat16
+    B, S1, N1, N2, D, page, mb, K = 3, 4, 16, 1, 128, 16, 8, 48
+    cache, table, dense = _paged_case(B, page, mb, N2, D, dtype, seed=41)
+    S2 = mb * page
+    q, _, w = _inputs(B, S1, S2, N1, N2, D, dtype, seed=43)
+    act_k = [100, S2, 37]
+    if layout_q == "TND":
+        lens_q = [4, 2, 3]
+        cu_q = list(np.cumsum(lens_q))
+        qt = np.concatenate([q[b, :lens_q[b]] for b in range(B)])
+        wt = np.concatenate([w[b, :lens_q[b]] for b in range(B)])
+        args = (dev(qt, dtype), dev(wt, torch.float32))
+        kw = dict(actual_seq_lengths_query=cu_q, layout_query="TND")
+        # the BSND-on-dense comparison per sequence
+        exp = []
+        for b in range(B):
+            i_b, _ = dsa.lightning_indexer_triton(dev(q[b:b + 1, :lens_q[b]], dtype), dev(dense[b:b + 1], dtype),
+                                                   dev(w[b:b + 1, :lens_q[b]], torch.float32),
+                                                   actual_seq_lengths_query=[lens_q[b]],
+                                                   actual_seq_lengths_key=[act_k[b]], sparse_count=K, sparse_mode=3)
+            exp.append(i_b.cpu().numpy()[0])
+        exp = np.concatenate(exp)
+        ref, _ = lightning_indexer(qt, cache, wt, actual_seq_lengths_query=cu_q, actual_seq_lengths_key=act_k,
+                                   layout_query="TND", layout_key="PA_BSND", sparse_count=K, sparse_mode=3,
+                                   block_table=table)
+    else:
+        args = (dev(q, dtype), dev(w, torch.float32))
+        kw = dict()
+        e, _ = dsa.lightning_indexer_triton(dev(q, dtype), dev(dense, dtype), dev(w, torch.float32),
+                                            actual_seq_lengths_key=act_k, sparse_count=K, sparse_mode=3)
+        exp = e.cpu().numpy()
+        ref, _ = lightning_indexer(q, cache, w, actual_seq_lengths_key=act_k, layout_key="PA_BSND",
+                                   sparse_count=K, sparse_mode=3, block_table=table)
+    got, val = dsa.lightning_indexer_triton(args[0], dev(cache, dtype), args[1], actual_seq_lengths_key=act_k,
+                                            block_table=dev(table, torch.int32), layout_key="PA_BSND",
+                                            sparse_count=K, sparse_mode=3, return_value=True, **kw)
+    torch.cuda.synchronize()
+    got = got.cpu().numpy()
+    # bit-exact against the BSND kernel on the de-paged keys (same scores, same order)
+    np.testing.assert_array_equal(got, exp)
+    # and against the oracle up to near-ties of its fp32 scores
+    flips = int((got != ref).sum())
+    print(f"[li paged] tie flips vs oracle: {flips}", flush=True)
+    assert flips <= max(2, got.size // 200)
+
+
+def test_indexer_paged_decode_scores():
+    print("[li paged] decode scores", flush=True)
+    dsa = _api()
+    from dsa_triton_ascend_amd import _lib
+    dtype = torch.bfloat16
+    B, N1, D, page, mb = 4, 64, 128, 64, 16
+    cache, table, dense = _paged_case(B, page, mb, 1, D, dtype, seed=47)
+    S2 = mb * page
+    q, _, w = _inputs(B, 1, S2, N1, 1, D, dtype, seed=49)
+    act_k = [S2, 700, 65, 1]
+    sc = torch.empty(B, S2, dtype=torch.float32, device="cuda")
+    ak = torch.tensor(act_k, dtype=torch.int32, device="cuda")
+    qd, cd, wd, td = dev(q, dtype), dev(cache, dtype), dev(w, torch.float32), dev(table, torch.int32)
+    lib = _lib.load()
+    st = lib.dsa_li_scores_paged(qd.data_ptr(), cd.data_ptr(), wd.data_ptr(), None, ak.data_ptr(), td.data_ptr(),
+                                 sc.data_ptr(), B, 1, N1, 1, D, B, cache.shape[0], page, mb, 3,
+                                 _lib.LAYOUT["BSND"], _lib.DTYPE_BF16, _lib.DTYPE_FP32, _lib.stream_handle(qd.device))
+    _lib.check(st, "dsa_li_scores_paged")
+    torch.cuda.synchronize()
+    ref = indexer_scores(q, dense, w, [1] * B, act_k, 3).reshape(B, S2)
+    got = sc.cpu().numpy()
+    assert np.array_equal(np.isinf(got), np.isinf(ref)), "masked entries differ"
+    fin = np.isfinite(ref)
+    tol = _score_tol(q, dense, w, 1).reshape(B, S2)
+    assert np.all(np.abs(got[fin] - ref[fin]) <= 1e-5 * np.abs(ref[fin]) + tol[fin])
+    # the -1 block of batch 0 (keys 64..127) scores exactly zero
+    assert np.all(got[0, page:2 * page] == 0.0)
