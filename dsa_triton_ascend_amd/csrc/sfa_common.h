@@ -53,10 +53,15 @@ __device__ __forceinline__ RowInfo sfa_row_info(const P& p, int row) {
 // Returns false if the position is not attended; *phys = -1 marks a token that
 // is attended but lives in a -1 / out-of-range page (reads as a zero row, as
 // the reference's de-paging leaves such spans zero, lines 391-397).
+// The index entry of position `pos` (split from the resolution below so the
+// load need not wait for the row's length loads).
 template <typename P>
-__device__ __forceinline__ bool sfa_resolve(const P& p, const RowInfo& ri, const int32_t* idx_row,
-                                            int pos, int* phys) {
-  int id = idx_row[pos / p.bs];
+__device__ __forceinline__ int sfa_load_id(const P& p, const int32_t* idx_row, int pos) {
+  return idx_row[pos / p.bs];
+}
+
+template <typename P>
+__device__ __forceinline__ bool sfa_resolve_id(const P& p, const RowInfo& ri, int id, int pos, int* phys) {
   if (id < 0) return false;
   int64_t tok = (int64_t)id * p.bs + (pos % p.bs);
   if (tok >= ri.threshold || tok >= ri.act_k) return false;
@@ -72,6 +77,12 @@ __device__ __forceinline__ bool sfa_resolve(const P& p, const RowInfo& ri, const
   if (r >= p.kv_rows) return false;
   *phys = (int)r;
   return true;
+}
+
+template <typename P>
+__device__ __forceinline__ bool sfa_resolve(const P& p, const RowInfo& ri, const int32_t* idx_row,
+                                            int pos, int* phys) {
+  return sfa_resolve_id(p, ri, sfa_load_id(p, idx_row, pos), pos, phys);
 }
 
 }  // namespace dsa

@@ -209,7 +209,9 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
     int pos = c0 + tid;
     int phys = 0;
     bool valid = false;
-    if (ri.active && pos < p1) valid = sfa_resolve(p, ri, idx_row, pos, &phys);
+    // the index load does not wait for the row's lengths (act_q / act_k)
+    const int id = pos < p1 ? sfa_load_id(p, idx_row, pos) : -1;
+    if (ri.active && pos < p1) valid = sfa_resolve_id(p, ri, id, pos, &phys);
     unsigned long long m = __ballot(valid);
     if (lane == 0) s_wcnt[wave] = __popcll(m);
     lds_barrier();
@@ -747,11 +749,24 @@ __global__ __launch_bounds__(256) void sfa_combine_kernel(SfaFwdParams p) {
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-int sfa_fwd_head_groups(int64_t n1, int64_t d);
+// Waves and head tiles (of 16 heads) per wave of the 128-head kernel; every
+// configuration covers 128 heads per workgroup, so one gathered KV row
+// serves all heads of a row.  D=512 runs two waves per SIMD (8 x 16 heads):
+// LDS reads from a single wave per SIMD are latency-bound, and 16 heads keep
+// the O accumulator (128 registers) plus Q fragments within the 256
+// registers of a half SIMD.
+template <int D> struct SfaCfg {
+  static constexpr int NW = D >= 512 ? 8 : 4;
+  static constexpr int HT = D >= 512 ? 1 : 2;
+};
+constexpr int kSfaHeadsPerWg = 128;
 
-int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
+// Token splits: enough (row, split) workgroups to fill the CUs, at least
+// 256 positions per split, at most kSfaMaxList.  The workspace query and
+// the launch use the same count.
+static int sfa_fwd_plan_splits(int64_t rows, int64_t n1, int64_t total_pos) {
   const int cus = device_cu_count();
-  const int64_t units = rows * sfa_fwd_head_groups(n1, d);
+  const int64_t units = rows * ((n1 + kSfaHeadsPerWg - 1) / kSfaHeadsPerWg);
   int64_t splits = 1;
   if (units < cus) {
     const int64_t want = (cus + units - 1) / units;
@@ -763,33 +778,22 @@ int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
   return (int)splits;
 }
 
+int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
+  (void)d;
+  return sfa_fwd_plan_splits(rows, n1, total_pos);
+}
+
 size_t sfa_fwd_workspace_bytes(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
   const int splits = sfa_fwd_splits(rows, n1, d, total_pos);
   if (splits <= 1) return 0;
   return (size_t)splits * rows * n1 * (d * sizeof(_Float16) + 4 * sizeof(float));
 }
 
-// Waves and head tiles (of 16 heads) per wave; every configuration covers
-// 128 heads per workgroup, so one gathered KV row serves all heads of a row.
-// D=512 runs two waves per SIMD (8 x 16 heads): LDS reads from a single wave
-// per SIMD are latency-bound, and 16 heads keep the O accumulator (128
-// registers) plus Q fragments within the 256 registers of a half SIMD.
-template <int D> struct SfaCfg {
-  static constexpr int NW = D >= 512 ? 8 : 4;
-  static constexpr int HT = D >= 512 ? 1 : 2;
-};
-constexpr int kSfaHeadsPerWg = 128;
-
-int sfa_fwd_head_groups(int64_t n1, int64_t d) {
-  (void)d;
-  return (int)((n1 + kSfaHeadsPerWg - 1) / kSfaHeadsPerWg);
-}
-
 template <int D, typename T>
 static hipError_t launch_sfa_fwd(SfaFwdParams& p, hipStream_t stream) {
   const int64_t rows_per_xcd = (p.rows + 7) / 8;
   p.rows_per_xcd = (int)rows_per_xcd;
-  const int64_t blocks = 8 * rows_per_xcd * p.splits * sfa_fwd_head_groups(p.n1, D);
+  const int64_t blocks = 8 * rows_per_xcd * p.splits * ((p.n1 + kSfaHeadsPerWg - 1) / kSfaHeadsPerWg);
   const bool buf = p.kv_rows * (int64_t)D * 2 < (1ll << 31);
   using C = SfaCfg<D>;
   static_assert(C::NW * C::HT * 16 == kSfaHeadsPerWg, "heads per workgroup");
@@ -840,7 +844,7 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
   p.max_blocks = (int32_t)max_blocks;
   p.page_size = (int32_t)page_size;
   const int64_t total_pos = sparse_count * (int64_t)sparse_block_size;
-  p.splits = sfa_fwd_splits(q_rows, n1, d, total_pos);
+  p.splits = sfa_fwd_plan_splits(q_rows, n1, total_pos);
   p.pos_per_split = (int32_t)((total_pos + p.splits - 1) / p.splits);
   p.part_o = nullptr;
   p.part_ml = nullptr;

@@ -293,3 +293,61 @@ def test_fwd_repeat_runs_bitwise_identical():
     b = _run(q, k, qr, kr, si, dtype, 0.04, 0)
     for x, y in zip(a, b):
         np.testing.assert_array_equal(x, y)
+
+
+# Few rows with long index lists: the token-split path.  At D = 512 it runs
+# the paired 64-head kernel (two waves per 16 heads, P exchanged through
+# LDS, half of D per wave) and the combine kernel; N1 < 64 leaves pairs
+# without heads, short causal rows take the bf16 lo part of P, fp16 the
+# single-part path.
+SPLIT_CASES = [
+    # B, S1, S2, N1, K, mode, D
+    (1, 2, 4096, 128, 2048, 0, 512),
+    (2, 1, 2048, 16, 1024, 0, 512),
+    (1, 3, 1024, 32, 1000, 3, 512),
+    (1, 4, 600, 64, 600, 3, 512),
+    (1, 2, 4096, 128, 2048, 0, 256),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("B,S1,S2,N1,K,mode,D", SPLIT_CASES)
+def test_fwd_token_split_rows(B, S1, S2, N1, K, mode, D, dtype):
+    print(f"[sfa_fwd split] B={B} S1={S1} S2={S2} N1={N1} K={K} mode={mode} D={D} {dtype}", flush=True)
+    q, k, qr, kr = sfa_inputs(B, S1, S2, N1, D, dtype, seed=51)
+    si = sparse_indices(B, S1, S2, K, 1, mode, seed=53)
+    if mode == 0:
+        si[0, 0, 0, K // 3:] = -1   # one short row inside a long batch
+    scale = 1.0 / np.sqrt(D + 64)
+    out, smax, ssum = _run(q, k, qr, kr, si, dtype, scale, mode)
+    ref = sfa_fwd_bsnd(q, k, si, qr, kr, scale, [S1] * B, [S2] * B, 1, mode, True, "float32",
+                       positions="kernel")
+    assert_close(out, ref[0], RTOL, ATOL, "attention_out")
+    assert_close(smax, ref[1], RTOL, ATOL, "softmax_max")
+    assert_close(ssum, ref[2], RTOL, ATOL, "softmax_sum")
+
+
+def test_fwd_token_split_paged_decode():
+    print("[sfa_fwd split] paged decode", flush=True)
+    dsa = _api()
+    dtype = torch.bfloat16
+    B, S2, N1, K, D, page = 4, 2048, 128, 1024, 512, 64
+    q, k, qr, kr = sfa_inputs(B, 1, S2, N1, D, dtype, seed=61)
+    rng = np.random.RandomState(62)
+    cache, cache_r, bt = _paged(k, kr, page, rng, holes=True)
+    si = sparse_indices(B, 1, S2, K, 1, 0, seed=63)
+    act_k = [2048, 1500, 2048, 700]
+    scale = 1.0 / np.sqrt(D + 64)
+    out, smax, ssum = dsa.sparse_flash_attention_triton(
+        dev(q, dtype), dev(cache, dtype), None, dev(si, torch.int32), scale_value=scale,
+        block_table=dev(bt, torch.int32), actual_seq_lengths_kv=act_k,
+        query_rope=dev(qr, dtype), key_rope=dev(cache_r, dtype), layout_kv="PA_BSND",
+        sparse_mode=0, return_softmax_lse=True, block_size=page)
+    torch.cuda.synchronize()
+    ref = sparse_flash_attention(q, dev(cache, dtype).float().cpu().numpy(), si, scale, qr,
+                                 dev(cache_r, dtype).float().cpu().numpy(), block_table=bt,
+                                 actual_seq_lengths_kv=act_k, layout_kv="PA_BSND", sparse_mode=0,
+                                 return_softmax_lse=True, dtype="float32")
+    assert_close(out.float().cpu().numpy(), ref[0], RTOL, ATOL, "out")
+    assert_close(smax.cpu().numpy(), ref[1], RTOL, ATOL, "smax")
+    assert_close(ssum.cpu().numpy(), ref[2], RTOL, ATOL, "ssum")
