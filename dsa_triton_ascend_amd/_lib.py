@@ -71,6 +71,18 @@ SIGNATURES = {
         _vp, _sz, _vp,                        # workspace, workspace_bytes, stream
     ]),
     "dsa_kl_bwd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "dsa_kl_bwd_ex": (_c.c_int, [
+        _vp, _vp, _vp, _vp,                   # query, key, query_rope, key_rope
+        _vp, _vp, _vp, _i32p,                 # query_index, key_index, weights, sparse_indices
+        _vp, _vp, _i32p, _i32p, _i32p,        # softmax_max, softmax_sum, actual_seq_qlen, actual_seq_klen, block_table
+        _vp, _vp, _vp, _vp,                   # d_query_index, d_key_index, d_weights, loss
+        _i64, _i64, _i64, _i64, _i64, _i64,   # batch, s1, s2, n1, d, d_rope
+        _i64, _i64, _i64,                     # n_idx, d_idx, sparse_count
+        _i64, _i64, _i64, _i64,               # q_rows, kv_rows, max_blocks, page_size
+        _i32, _i32, _i32, _i32, _f32,         # layout_query, layout_key, dtype, weights_dtype, scale_value
+        _vp, _sz, _vp,                        # workspace, workspace_bytes, stream
+    ]),
+    "dsa_kl_bwd_ex_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
     "dsa_li_fwd": (_c.c_int, [
         _vp, _vp, _vp, _i32p, _i32p,          # query, key, weights, actual_seq_q, actual_seq_k
         _i32p, _vp,                           # sparse_indices, sparse_values

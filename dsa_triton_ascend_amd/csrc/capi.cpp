@@ -51,15 +51,18 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
 
 // sfa_bwd.hip
 size_t sfa_bwd_workspace_bytes(int64_t kv_rows, int64_t d);
-size_t kl_bwd_workspace_bytes(int64_t batch, int64_t s1, int64_t s2, int64_t topk);
+// kl_bwd.hip
+size_t kl_bwd_workspace_bytes(int64_t q_rows, int64_t kv_rows, int64_t topk);
 int kl_bwd_max_topk();
 int kl_bwd_max_nidx();
 int kl_bwd_run(const void* query, const void* key, const void* query_rope, const void* key_rope,
                const void* query_index, const void* key_index, const void* weights, const int32_t* sparse_indices,
                const float* softmax_max, const float* softmax_sum, const int32_t* act_q, const int32_t* act_k,
-               void* d_query_index, void* d_key_index, void* d_weights, float* loss, int64_t batch, int64_t s1,
-               int64_t s2, int64_t n1, int64_t d, int64_t d_rope, int64_t nidx, int64_t topk, int32_t dtype,
-               int32_t w_dtype, float scale_value, void* workspace, hipStream_t stream);
+               const int32_t* block_table, void* d_query_index, void* d_key_index, void* d_weights, float* loss,
+               int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t d, int64_t d_rope, int64_t nidx,
+               int64_t topk, int64_t q_rows, int64_t kv_rows, int64_t max_blocks, int64_t page_size,
+               int32_t layout_q, int32_t layout_k, int32_t dtype, int32_t w_dtype, float scale_value,
+               void* workspace, hipStream_t stream);
 int sfa_bwd_run(const void* query, const void* query_rope, const void* key, const void* key_rope,
                 const int32_t* sparse_indices, const void* d_out, const void* out, const float* softmax_max,
                 const float* softmax_sum, const int32_t* actual_seq_q, const int32_t* actual_seq_kv,
@@ -256,18 +259,25 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
 
 size_t dsa_kl_bwd_workspace_size(int64_t batch, int64_t s1, int64_t s2, int64_t sparse_count, int64_t d_idx) {
   if (batch <= 0 || s1 <= 0 || s2 <= 0 || sparse_count <= 0 || d_idx != 128) return 0;
-  return kl_bwd_workspace_bytes(batch, s1, s2, sparse_count);
+  return kl_bwd_workspace_bytes(batch * s1, batch * s2, sparse_count);
 }
 
-int dsa_kl_bwd(const void* query, const void* key, const void* query_rope, const void* key_rope,
-               const void* query_index, const void* key_index, const void* weights,
-               const int32_t* sparse_indices, const float* softmax_max, const float* softmax_sum,
-               const int32_t* actual_seq_qlen, const int32_t* actual_seq_klen, void* d_query_index,
-               void* d_key_index, void* d_weights, float* loss, int64_t batch, int64_t s1, int64_t s2,
-               int64_t n1, int64_t d, int64_t d_rope, int64_t n_idx, int64_t d_idx, int64_t sparse_count,
-               int32_t dtype, int32_t weights_dtype, float scale_value, void* workspace,
-               size_t workspace_bytes, void* stream) {
-  g_err[0] = '\0';
+size_t dsa_kl_bwd_ex_workspace_size(int64_t q_rows, int64_t kv_rows, int64_t sparse_count, int64_t d_idx) {
+  if (q_rows <= 0 || kv_rows <= 0 || sparse_count <= 0 || d_idx != 128) return 0;
+  return kl_bwd_workspace_bytes(q_rows, kv_rows, sparse_count);
+}
+
+// Validation shared by dsa_kl_bwd and dsa_kl_bwd_ex.  For a TND side s1 / s2
+// are not used; for a paged key s2 = max_blocks * page_size.
+static int kl_check(const void* query, const void* key, const void* query_rope, const void* key_rope,
+                    const void* query_index, const void* key_index, const void* weights,
+                    const int32_t* sparse_indices, const float* softmax_max, const float* softmax_sum,
+                    const int32_t* act_q, const int32_t* act_k, const int32_t* block_table,
+                    const void* d_query_index, const void* d_key_index, const void* d_weights, const float* loss,
+                    int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t d, int64_t d_rope, int64_t n_idx,
+                    int64_t d_idx, int64_t sparse_count, int64_t q_rows, int64_t kv_rows, int64_t max_blocks,
+                    int64_t page_size, int32_t layout_q, int32_t layout_k, int32_t dtype, int32_t weights_dtype,
+                    const void* workspace, size_t workspace_bytes) {
   DSA_CHECK_ARG(query && key && query_index && key_index && weights && sparse_indices && softmax_max &&
                     softmax_sum,
                 "null input tensor pointer");
@@ -288,18 +298,85 @@ int dsa_kl_bwd(const void* query, const void* key, const void* query_rope, const
   DSA_CHECK_SUPPORTED(weights_dtype == DSA_DTYPE_FP32 || weights_dtype == DSA_DTYPE_BF16 ||
                           weights_dtype == DSA_DTYPE_FP16,
                       "weights dtype must be float32, bfloat16 or float16");
-  DSA_CHECK_ARG(batch >= 1 && s1 >= 1 && s2 >= 1, "batch, S1 and S2 must be >= 1");
-  DSA_CHECK_ARG(batch * s1 * sparse_count < (1ll << 31) && batch * s2 < (1ll << 31),
-                "rows x topK and B x S2 must stay below 2^31");
-  const size_t need = kl_bwd_workspace_bytes(batch, s1, s2, sparse_count);
+  DSA_CHECK_SUPPORTED(layout_q == DSA_LAYOUT_BSND || layout_q == DSA_LAYOUT_TND, "layout_query must be BSND or TND");
+  DSA_CHECK_SUPPORTED(layout_k == DSA_LAYOUT_BSND || layout_k == DSA_LAYOUT_TND || layout_k == DSA_LAYOUT_PA_BSND,
+                      "layout_key must be BSND, TND or PA_BSND");
+  DSA_CHECK_ARG(!(layout_q == DSA_LAYOUT_BSND && layout_k == DSA_LAYOUT_TND), "a TND key needs a TND query");
+  DSA_CHECK_ARG(batch >= 1 && batch <= (1 << 24), "batch must be in [1, 2^24]");
+  DSA_CHECK_ARG(q_rows >= 1 && kv_rows >= 1, "the query and the key need at least one row");
+  DSA_CHECK_ARG(q_rows * sparse_count < (1ll << 31) && kv_rows < (1ll << 31),
+                "rows x topK and the key rows must stay below 2^31");
+  if (layout_q == DSA_LAYOUT_TND) {
+    DSA_CHECK_ARG(act_q, "TND query requires cumulative actual_seq_qlen");
+  } else {
+    DSA_CHECK_ARG(s1 >= 1 && q_rows == batch * s1, "q_rows must equal B*S1 for a BSND query");
+  }
+  if (layout_k == DSA_LAYOUT_TND) {
+    DSA_CHECK_ARG(act_k, "TND key requires cumulative actual_seq_klen");
+  } else if (layout_k == DSA_LAYOUT_PA_BSND) {
+    DSA_CHECK_ARG(block_table, "PA_BSND key requires a block_table");
+    DSA_CHECK_ARG(act_k, "PA_BSND key requires actual_seq_klen (per-batch lengths)");
+    DSA_CHECK_ARG(page_size >= 1 && page_size <= (1 << 20), "page (block) size must be in [1, 2^20]");
+    DSA_CHECK_ARG(max_blocks >= 1 && max_blocks * page_size < (1ll << 31),
+                  "max_blocks * page size must be in [1, 2^31)");
+    DSA_CHECK_ARG(kv_rows % page_size == 0, "the paged key rows must be a whole number of pages");
+  } else {
+    DSA_CHECK_ARG(s2 >= 1 && kv_rows == batch * s2, "kv_rows must equal B*S2 for a BSND key");
+  }
+  const size_t need = kl_bwd_workspace_bytes(q_rows, kv_rows, sparse_count);
   if (workspace == nullptr || workspace_bytes < need) {
     set_error("workspace of %zu bytes required, %zu given", need, workspace_bytes);
     return DSA_ERR_WORKSPACE;
   }
+  return DSA_OK;
+}
+
+int dsa_kl_bwd(const void* query, const void* key, const void* query_rope, const void* key_rope,
+               const void* query_index, const void* key_index, const void* weights,
+               const int32_t* sparse_indices, const float* softmax_max, const float* softmax_sum,
+               const int32_t* actual_seq_qlen, const int32_t* actual_seq_klen, void* d_query_index,
+               void* d_key_index, void* d_weights, float* loss, int64_t batch, int64_t s1, int64_t s2,
+               int64_t n1, int64_t d, int64_t d_rope, int64_t n_idx, int64_t d_idx, int64_t sparse_count,
+               int32_t dtype, int32_t weights_dtype, float scale_value, void* workspace,
+               size_t workspace_bytes, void* stream) {
+  g_err[0] = '\0';
+  DSA_CHECK_ARG(batch >= 1 && s1 >= 1 && s2 >= 1, "batch, S1 and S2 must be >= 1");
+  const int st = kl_check(query, key, query_rope, key_rope, query_index, key_index, weights, sparse_indices,
+                          softmax_max, softmax_sum, actual_seq_qlen, actual_seq_klen, nullptr, d_query_index,
+                          d_key_index, d_weights, loss, batch, s1, s2, n1, d, d_rope, n_idx, d_idx, sparse_count,
+                          batch * s1, batch * s2, 0, 1, DSA_LAYOUT_BSND, DSA_LAYOUT_BSND, dtype, weights_dtype,
+                          workspace, workspace_bytes);
+  if (st != DSA_OK) return st;
   return kl_bwd_run(query, key, d_rope ? query_rope : nullptr, d_rope ? key_rope : nullptr, query_index,
                     key_index, weights, sparse_indices, softmax_max, softmax_sum, actual_seq_qlen,
-                    actual_seq_klen, d_query_index, d_key_index, d_weights, loss, batch, s1, s2, n1, d, d_rope,
-                    n_idx, sparse_count, dtype, weights_dtype, scale_value, workspace, (hipStream_t)stream);
+                    actual_seq_klen, nullptr, d_query_index, d_key_index, d_weights, loss, batch, s1, s2, n1, d,
+                    d_rope, n_idx, sparse_count, batch * s1, batch * s2, 0, 1, DSA_LAYOUT_BSND,
+                    DSA_LAYOUT_BSND, dtype, weights_dtype, scale_value, workspace, (hipStream_t)stream);
+}
+
+int dsa_kl_bwd_ex(const void* query, const void* key, const void* query_rope, const void* key_rope,
+                  const void* query_index, const void* key_index, const void* weights,
+                  const int32_t* sparse_indices, const float* softmax_max, const float* softmax_sum,
+                  const int32_t* actual_seq_qlen, const int32_t* actual_seq_klen, const int32_t* block_table,
+                  void* d_query_index, void* d_key_index, void* d_weights, float* loss, int64_t batch,
+                  int64_t s1, int64_t s2, int64_t n1, int64_t d, int64_t d_rope, int64_t n_idx, int64_t d_idx,
+                  int64_t sparse_count, int64_t q_rows, int64_t kv_rows, int64_t max_blocks, int64_t page_size,
+                  int32_t layout_query, int32_t layout_key, int32_t dtype, int32_t weights_dtype,
+                  float scale_value, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = '\0';
+  if (layout_key == DSA_LAYOUT_PA_BSND) s2 = max_blocks * page_size;
+  const int st = kl_check(query, key, query_rope, key_rope, query_index, key_index, weights, sparse_indices,
+                          softmax_max, softmax_sum, actual_seq_qlen, actual_seq_klen, block_table, d_query_index,
+                          d_key_index, d_weights, loss, batch, s1, s2, n1, d, d_rope, n_idx, d_idx, sparse_count,
+                          q_rows, kv_rows, max_blocks, page_size, layout_query, layout_key, dtype, weights_dtype,
+                          workspace, workspace_bytes);
+  if (st != DSA_OK) return st;
+  return kl_bwd_run(query, key, d_rope ? query_rope : nullptr, d_rope ? key_rope : nullptr, query_index,
+                    key_index, weights, sparse_indices, softmax_max, softmax_sum, actual_seq_qlen,
+                    actual_seq_klen, layout_key == DSA_LAYOUT_PA_BSND ? block_table : nullptr, d_query_index,
+                    d_key_index, d_weights, loss, batch, s1, s2, n1, d, d_rope, n_idx, sparse_count, q_rows,
+                    kv_rows, max_blocks, page_size, layout_query, layout_key, dtype, weights_dtype, scale_value,
+                    workspace, (hipStream_t)stream);
 }
 
 size_t dsa_li_fwd_workspace_size(int64_t q_rows, int64_t n2, int64_t s2) {

@@ -37,7 +37,21 @@
 
 namespace dsa {
 
+// Query-row and key-row addressing of one call.  Query rows are b*S1 + s1
+// (BSND) or packed with cumulative lengths (TND); key rows are b*S2 + t
+// (BSND), packed (TND) or pages of a cache through a block table (PA_BSND).
+// Length arrays are cumulative for a TND side, per-batch lengths otherwise.
+struct KlMap {
+  const int32_t* act_q;
+  const int32_t* act_k;
+  const int32_t* block_table;  // [batch, max_blocks] (PA_BSND key)
+  int64_t kv_rows;             // key rows in memory
+  int32_t batch, s1, s2, rows, topk, max_blocks, page_size;
+  int32_t layout_q, layout_k;
+};
+
 struct KlParams {
+  KlMap m;
   const void* q;
   const void* qr;
   const void* k;
@@ -48,14 +62,12 @@ struct KlParams {
   const int32_t* idx;
   const float* smax;
   const float* ssum;
-  const int32_t* act_q;
-  const int32_t* act_k;
   void* dqi;
   void* dw;
   float* cbuf;       // [rows][topK][128] dKi contribution of each slot
   float* rowmax;     // [rows] max |c| over the row's slots
   float* loss_part;  // [rows]
-  int32_t batch, s1, s2, n1, nidx, topk, w_dtype;
+  int32_t n1, nidx, topk, w_dtype;
   float scale_log2;  // scale * log2(e)
 };
 
@@ -92,23 +104,64 @@ __device__ __forceinline__ f32x4 split3_rowsum(const Split3& s) {
 
 struct KlRow {
   int b, s1, n;
+  int klen;       // clamp bound of the row's token ids (S2, or the packed / paged length)
+  int64_t kbase;  // first key row of the row's batch (BSND / TND)
   bool active;
 };
 
-__device__ __forceinline__ KlRow kl_row_info(const KlParams& p, int row) {
+// A row's batch, position and slot count n = min(topK, max(act_k - act_q +
+// s1 + 1, 0)) (kernel line 107); inactive rows (s1 >= act_q) have n = 0.
+__device__ __forceinline__ KlRow kl_row_info(const KlMap& m, int row) {
   KlRow r;
-  r.b = row / p.s1;
-  r.s1 = row - r.b * p.s1;
-  const int aq = p.act_q ? p.act_q[r.b] : p.s1;
-  const int ak = p.act_k ? p.act_k[r.b] : p.s2;
+  int aq, ak;
+  if (m.layout_q == DSA_LAYOUT_TND) {
+    int lo = 0, hi = m.batch - 1;  // first b with cu[b] > row
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (m.act_q[mid] > row) hi = mid; else lo = mid + 1;
+    }
+    r.b = lo;
+    const int start = lo ? m.act_q[lo - 1] : 0;
+    r.s1 = row - start;
+    aq = m.act_q[lo] - start;
+  } else {
+    r.b = row / m.s1;
+    r.s1 = row - r.b * m.s1;
+    aq = m.act_q ? m.act_q[r.b] : m.s1;
+  }
+  if (m.layout_k == DSA_LAYOUT_TND) {
+    const int start = r.b ? m.act_k[r.b - 1] : 0;
+    r.kbase = start;
+    ak = m.act_k[r.b] - start;
+    r.klen = ak;
+  } else if (m.layout_k == DSA_LAYOUT_PA_BSND) {
+    r.kbase = 0;
+    r.klen = m.max_blocks * m.page_size;
+    ak = m.act_k ? m.act_k[r.b] : r.klen;
+  } else {
+    r.kbase = (int64_t)r.b * m.s2;
+    r.klen = m.s2;
+    ak = m.act_k ? m.act_k[r.b] : m.s2;
+  }
   r.active = r.s1 < aq;
-  r.n = r.active ? min(p.topk, max(ak - aq + r.s1 + 1, 0)) : 0;
+  r.n = r.active ? min(m.topk, max(ak - aq + r.s1 + 1, 0)) : 0;
   return r;
 }
 
-__device__ __forceinline__ int kl_token(const KlParams& p, int row, int b, int k) {
-  const int t = p.idx[(int64_t)row * p.topk + k];
-  return b * p.s2 + min(max(t, 0), p.s2 - 1);
+// Key row of slot k: the token id clamped to [0, klen) with no -1 test (lines
+// 58, 63, 300), then translated through the block table for a paged cache.
+// -1 marks a token in a -1 (or out-of-range) page: it reads as a zero key
+// row and receives no gradient.  Key rows past the end of the key tensor
+// (cumulative lengths larger than it) are treated the same way.
+__device__ __forceinline__ int kl_token(const KlMap& m, const KlRow& r, const int32_t* idx, int row, int k) {
+  const int t = min(max(idx[(int64_t)row * m.topk + k], 0), r.klen - 1);
+  if (m.layout_k != DSA_LAYOUT_PA_BSND) {
+    const int64_t g = r.kbase + t;
+    return g < m.kv_rows ? (int)g : -1;
+  }
+  const int blk = m.block_table[(int64_t)r.b * m.max_blocks + t / m.page_size];
+  const int64_t phys = (int64_t)blk * m.page_size + t % m.page_size;
+  return (blk < 0 || phys >= m.kv_rows) ? -1 : (int)phys;
 }
 
 __device__ __forceinline__ float load_w(const void* w, int64_t i, int dt) {
@@ -156,9 +209,8 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int li = lane & 15, lg = lane >> 4;
-  const int rows = p.batch * p.s1;
-  const int row = rows - 1 - (int)blockIdx.x;  // long causal rows first
-  const KlRow ri = kl_row_info(p, row);
+  const int row = p.m.rows - 1 - (int)blockIdx.x;  // long causal rows first
+  const KlRow ri = kl_row_info(p.m, row);
   const int n = ri.n;
 
   if (n <= 0) {
@@ -237,29 +289,31 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   const unsigned char* kib = (const unsigned char*)p.ki;
 
   // ================= pass A: teacher p and index scores I =================
-  for (int k = tid; k < n; k += NT) s_tok[k] = kl_token(p, row, ri.b, k);
+  for (int k = tid; k < n; k += NT) s_tok[k] = kl_token(p.m, ri, p.idx, row, k);
   __syncthreads();
 
   // per tile: K rows (NJ_N chunks per thread), rope rows (threads < 256),
-  // K_index rows (one chunk per thread); slots >= n read as zeros
+  // K_index rows (one chunk per thread); slots >= n and tokens of -1 pages
+  // read as zeros
+  auto slot_tok = [&](int k) { return k < n ? s_tok[k] : -1; };
   u32x4 pre_n[NJ_N], pre_r, pre_i;
   auto load_a = [&](int t) {
 #pragma unroll
     for (int j = 0; j < NJ_N; ++j) {
       const int e = tid + j * NT;
       const int tk = e / CN, ch = e - tk * CN;
-      const int k = t * TILE + tk;
-      pre_n[j] = k < n ? *(const u32x4*)(kb + (int64_t)s_tok[k] * ROW + ch * 16) : z4;
+      const int tok = slot_tok(t * TILE + tk);
+      pre_n[j] = tok >= 0 ? *(const u32x4*)(kb + (int64_t)tok * ROW + ch * 16) : z4;
     }
     if (DR > 0) {
       const int tk = tid / (CR > 0 ? CR : 1), ch = tid - tk * CR;
-      const int k = t * TILE + tk;
-      pre_r = (tid < TILE * CR && k < n) ? *(const u32x4*)(krb + (int64_t)s_tok[k] * (DR * 2) + ch * 16) : z4;
+      const int tok = tid < TILE * CR ? slot_tok(t * TILE + tk) : -1;
+      pre_r = tok >= 0 ? *(const u32x4*)(krb + (int64_t)tok * (DR * 2) + ch * 16) : z4;
     }
     {
       const int tk = tid / CI, ch = tid - tk * CI;
-      const int k = t * TILE + tk;
-      pre_i = k < n ? *(const u32x4*)(kib + (int64_t)s_tok[k] * IROW + ch * 16) : z4;
+      const int tok = slot_tok(t * TILE + tk);
+      pre_i = tok >= 0 ? *(const u32x4*)(kib + (int64_t)tok * IROW + ch * 16) : z4;
     }
   };
   auto store_a = [&]() {
@@ -425,8 +479,8 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   u32x4 prei;
   auto load_c = [&](int t) {
     const int tk = tid / CI, ch = tid - tk * CI;
-    const int k = t * TILE + tk;
-    prei = k < n ? *(const u32x4*)(kib + (int64_t)s_tok[k] * IROW + ch * 16) : z4;
+    const int tok = slot_tok(t * TILE + tk);
+    prei = tok >= 0 ? *(const u32x4*)(kib + (int64_t)tok * IROW + ch * 16) : z4;
   };
   load_c(0);
   for (int t = 0; t < nt; ++t) {
@@ -539,14 +593,12 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
 // dKi: bucket slots by target token, then a fixed-point sum per token
 // ---------------------------------------------------------------------------
 struct KlScatter {
+  KlMap m;
   const int32_t* idx;
-  const int32_t* act_q;
-  const int32_t* act_k;
   int32_t* cnt;     // [tokens]
   int32_t* offs;    // [tokens + 1]
   int32_t* cur;     // [tokens]
   int32_t* list;    // [rows * topK]
-  int32_t batch, s1, s2, topk;
 };
 
 __global__ __launch_bounds__(256) void kl_zero_kernel(int32_t* a, int64_t n) {
@@ -558,18 +610,15 @@ template <bool FILL>
 __global__ __launch_bounds__(256) void kl_bucket_kernel(KlScatter s) {
   const int row = blockIdx.x;
   const int k = blockIdx.y * 256 + threadIdx.x;
-  const int b = row / s.s1, s1 = row - b * s.s1;
-  const int aq = s.act_q ? s.act_q[b] : s.s1;
-  const int ak = s.act_k ? s.act_k[b] : s.s2;
-  const int n = s1 < aq ? min(s.topk, max(ak - aq + s1 + 1, 0)) : 0;
-  if (k >= n) return;
-  const int ti = s.idx[(int64_t)row * s.topk + k];
-  const int t = b * s.s2 + min(max(ti, 0), s.s2 - 1);
+  const KlRow r = kl_row_info(s.m, row);
+  if (k >= r.n) return;
+  const int t = kl_token(s.m, r, s.idx, row, k);
+  if (t < 0) return;  // a -1 page: no gradient target
   if (!FILL) {
     atomicAdd(&s.cnt[t], 1);
   } else {
     const int pos = s.offs[t] + atomicAdd(&s.cur[t], 1);
-    s.list[pos] = row * s.topk + k;
+    s.list[pos] = row * s.m.topk + k;
   }
 }
 
@@ -688,8 +737,8 @@ static KlWs kl_ws_layout(int64_t rows, int64_t tokens, int64_t topk) {
   return w;
 }
 
-size_t kl_bwd_workspace_bytes(int64_t batch, int64_t s1, int64_t s2, int64_t topk) {
-  return kl_ws_layout(batch * s1, batch * s2, topk).total;
+size_t kl_bwd_workspace_bytes(int64_t q_rows, int64_t kv_rows, int64_t topk) {
+  return kl_ws_layout(q_rows, kv_rows, topk).total;
 }
 
 size_t kl_bwd_lds_bytes(int64_t topk) { return (size_t)3 * topk * sizeof(float); }
@@ -733,13 +782,31 @@ static hipError_t dispatch_kl_row(const KlParams& p, int rows, int d, int dr, si
 int kl_bwd_run(const void* query, const void* key, const void* query_rope, const void* key_rope,
                const void* query_index, const void* key_index, const void* weights, const int32_t* sparse_indices,
                const float* softmax_max, const float* softmax_sum, const int32_t* act_q, const int32_t* act_k,
-               void* d_query_index, void* d_key_index, void* d_weights, float* loss, int64_t batch, int64_t s1,
-               int64_t s2, int64_t n1, int64_t d, int64_t d_rope, int64_t nidx, int64_t topk, int32_t dtype,
-               int32_t w_dtype, float scale_value, void* workspace, hipStream_t stream) {
-  const int64_t rows = batch * s1, tokens = batch * s2;
+               const int32_t* block_table, void* d_query_index, void* d_key_index, void* d_weights, float* loss,
+               int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t d, int64_t d_rope, int64_t nidx,
+               int64_t topk, int64_t q_rows, int64_t kv_rows, int64_t max_blocks, int64_t page_size,
+               int32_t layout_q, int32_t layout_k, int32_t dtype, int32_t w_dtype, float scale_value,
+               void* workspace, hipStream_t stream) {
+  const int64_t rows = q_rows, tokens = kv_rows;
   const KlWs L = kl_ws_layout(rows, tokens, topk);
   unsigned char* ws = (unsigned char*)workspace;
+  KlMap m;
+  m.act_q = act_q;
+  m.act_k = act_k;
+  m.block_table = block_table;
+  m.kv_rows = kv_rows;
+  m.batch = (int32_t)batch;
+  m.s1 = (int32_t)s1;
+  m.s2 = (int32_t)s2;
+  m.rows = (int32_t)rows;
+  m.topk = (int32_t)topk;
+  m.max_blocks = (int32_t)max_blocks;
+  m.page_size = (int32_t)page_size;
+  m.layout_q = layout_q;
+  m.layout_k = layout_k;
+
   KlParams p;
+  p.m = m;
   p.q = query;
   p.qr = query_rope;
   p.k = key;
@@ -750,16 +817,11 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   p.idx = sparse_indices;
   p.smax = softmax_max;
   p.ssum = softmax_sum;
-  p.act_q = act_q;
-  p.act_k = act_k;
   p.dqi = d_query_index;
   p.dw = d_weights;
   p.cbuf = (float*)(ws + L.cbuf);
   p.rowmax = (float*)(ws + L.rowmax);
   p.loss_part = (float*)(ws + L.loss);
-  p.batch = (int32_t)batch;
-  p.s1 = (int32_t)s1;
-  p.s2 = (int32_t)s2;
   p.n1 = (int32_t)n1;
   p.nidx = (int32_t)nidx;
   p.topk = (int32_t)topk;
@@ -767,17 +829,12 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   p.scale_log2 = scale_value * kLog2e;
 
   KlScatter s;
+  s.m = m;
   s.idx = sparse_indices;
-  s.act_q = act_q;
-  s.act_k = act_k;
   s.cnt = (int32_t*)(ws + L.cnt);
   s.offs = (int32_t*)(ws + L.offs);
   s.cur = (int32_t*)(ws + L.cur);
   s.list = (int32_t*)(ws + L.list);
-  s.batch = (int32_t)batch;
-  s.s1 = (int32_t)s1;
-  s.s2 = (int32_t)s2;
-  s.topk = (int32_t)topk;
 
   // counters cleared by a kernel (no memset nodes when the caller captures)
   const int64_t zn = (int64_t)((L.offs - L.cnt) / sizeof(int32_t));

@@ -147,6 +147,39 @@ size_t dsa_kl_bwd_workspace_size(int64_t batch, int64_t s1, int64_t s2, int64_t 
                                  int64_t d_idx);
 
 /*
+ * dsa_kl_bwd over packed (TND) rows and a paged key cache.  The reference
+ * rejects every layout but BSND (sparse_lightning_indexer_grad_kl_loss_triton.py:
+ * 534-535); this entry point extends the same computation:
+ *   layout_query BSND: query [B*S1, N1, D] rows; TND: [T1 = q_rows, N1, D]
+ *     with cumulative actual_seq_qlen [B] (required).
+ *   layout_key BSND: key / key_rope / key_index [B*S2, 1, X]; TND:
+ *     [T2 = kv_rows, 1, X] with cumulative actual_seq_klen (needs a TND
+ *     query); PA_BSND: caches [kv_rows = blocks * page_size, 1, X] addressed
+ *     through block_table [B, max_blocks] (int32, -1 = no page), with
+ *     per-batch actual_seq_klen (required).
+ * Row semantics are dsa_kl_bwd's: row (b, s1) is active when s1 < its query
+ * length and covers the first n = min(topK, max(ak - aq + s1 + 1, 0)) slots;
+ * token ids are clamped to [0, L) with L = S2 (BSND), the batch's key length
+ * (TND) or max_blocks * page_size (PA_BSND).  A token in a -1 page reads as a
+ * zero key row and receives no gradient.  d_key_index has the key_index
+ * shape and holds the sum over every slot that targets a key row (shared
+ * pages included); rows no slot targets are zero.  s1 is read for a BSND
+ * query only, s2 for a BSND key only.
+ */
+int dsa_kl_bwd_ex(const void* query, const void* key, const void* query_rope, const void* key_rope,
+                  const void* query_index, const void* key_index, const void* weights,
+                  const int32_t* sparse_indices, const float* softmax_max, const float* softmax_sum,
+                  const int32_t* actual_seq_qlen, const int32_t* actual_seq_klen, const int32_t* block_table,
+                  void* d_query_index, void* d_key_index, void* d_weights, float* loss, int64_t batch,
+                  int64_t s1, int64_t s2, int64_t n1, int64_t d, int64_t d_rope, int64_t n_idx, int64_t d_idx,
+                  int64_t sparse_count, int64_t q_rows, int64_t kv_rows, int64_t max_blocks, int64_t page_size,
+                  int32_t layout_query, int32_t layout_key, int32_t dtype, int32_t weights_dtype,
+                  float scale_value, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of dsa_kl_bwd_ex. */
+size_t dsa_kl_bwd_ex_workspace_size(int64_t q_rows, int64_t kv_rows, int64_t sparse_count, int64_t d_idx);
+
+/*
  * Lightning indexer: scores + stable top-k.  Replaces the reference core
  * `_lightning_indexer_score_core` (lightning_indexer_triton.py:382-413) and the
  * top-k after it (`_stable_topk`, 339-357, called at 539), with the stable

@@ -25,10 +25,19 @@ n = min(topK, max(act_k - act_q + s1 + 1, 0)) (kernel lines 107-111, 58),
 which equals the golden's min(topK, S2 - S1 + s1 + 1) at full lengths.
 Out-of-range targets in step 6 are skipped by the golden (142-144) and
 clamped by the device scatter (kernel line 300); ``dki_oob`` selects.
+
+``kl_loss_bwd_tnd`` and ``kl_loss_bwd_paged`` extend the computation to the
+packed (TND) and paged key layouts the reference rejects (kernel file
+534-535).  They are compositions of ``kl_loss_bwd``: TND runs each batch as
+its own B = 1 problem with S1, S2 = the batch's lengths (so token ids clamp
+to the batch's key length), and a paged cache is de-paged with
+``pa_to_bsnd`` (sparse_flash_attention_triton.py:382-403; -1 pages read as
+zero rows), run as BSND with S2 = max_blocks * page, and the key-index
+gradient is summed back onto the cache rows (-1 pages receive nothing).
 """
 import numpy as np
 
-from .common import round_to
+from .common import cumsum_to_lengths, pa_to_bsnd, round_to
 
 EPS = np.float32(1e-8)
 
@@ -109,3 +118,70 @@ def kl_loss_bwd(q, k, qr, kr, qi, ki, w, sparse_indices, softmax_max, softmax_su
     return {"dQueryIndex": dqi, "dKeyIndex": dki, "dW": dw,
             "loss": np.array([loss], ct), "p": p_all,
             "softmax_I": sI_all, "dI": sI_all - p_all, "I": I_all}
+
+
+def _batch_problem(x, start, n):
+    """Rows [start, start + n) of a packed tensor as a B = 1 BSND tensor."""
+    return None if x is None else np.asarray(x)[start:start + n][None]
+
+
+def kl_loss_bwd_tnd(q, k, qr, kr, qi, ki, w, sparse_indices, softmax_max, softmax_sum, scale,
+                    cu_q, cu_k, **kw):
+    """TND: q [T1,N1,D], k [T2,1,D], qi [T1,Nidx1,Di], ki [T2,1,Di], w [T1,Nidx1],
+    sparse_indices [T1,1,topK], softmax stats with T1*N1 entries, cumulative
+    lengths cu_q / cu_k.  Returns dQueryIndex [T1,Nidx1,Di], dKeyIndex
+    [T2,1,Di], dW [T1,Nidx1] and loss [1]."""
+    lq, lk = cumsum_to_lengths(cu_q), cumsum_to_lengths(cu_k)
+    T1, N1 = q.shape[0], q.shape[1]
+    T2 = k.shape[0]
+    Nidx1, Di = qi.shape[1], qi.shape[2]
+    smax = np.asarray(softmax_max, np.float32).reshape(T1, N1)
+    ssum = np.asarray(softmax_sum, np.float32).reshape(T1, N1)
+    si = np.asarray(sparse_indices).reshape(T1, 1, -1)
+    ct = kw.get("compute_dtype", np.float32)
+    dqi = np.zeros((T1, Nidx1, Di), ct)
+    dki = np.zeros((T2, 1, Di), ct)
+    dw = np.zeros((T1, Nidx1), ct)
+    loss = ct(0.0)
+    sq = sk = 0
+    for nq, nk in zip(lq, lk):
+        nq, nk = int(nq), int(nk)
+        if nq > 0 and nk > 0:
+            r = kl_loss_bwd(
+                _batch_problem(q, sq, nq), _batch_problem(k, sk, nk), _batch_problem(qr, sq, nq),
+                _batch_problem(kr, sk, nk), _batch_problem(qi, sq, nq), _batch_problem(ki, sk, nk),
+                _batch_problem(w, sq, nq), si[sq:sq + nq][None], smax[sq:sq + nq][None, None],
+                ssum[sq:sq + nq][None, None], scale, **kw)
+            dqi[sq:sq + nq] = r["dQueryIndex"][0]
+            dki[sk:sk + nk] = r["dKeyIndex"][0]
+            dw[sq:sq + nq] = r["dW"][0]
+            loss = loss + r["loss"][0]
+        sq += nq
+        sk += nk
+    return {"dQueryIndex": dqi, "dKeyIndex": dki, "dW": dw, "loss": np.array([loss], ct)}
+
+
+def kl_loss_bwd_paged(q, k_cache, qr, kr_cache, qi, ki_cache, w, sparse_indices, softmax_max,
+                      softmax_sum, scale, block_table, act_k, act_q=None, **kw):
+    """BSND queries over paged caches [blocks, page, 1, X] addressed by
+    block_table [B, max_blocks] (-1 = no page); act_k per-batch lengths.
+    dKeyIndex comes back in the cache shape."""
+    bt = np.asarray(block_table)
+    page = k_cache.shape[1]
+    S2 = bt.shape[1] * page
+
+    def dense(c):
+        return None if c is None else pa_to_bsnd(np.asarray(c), bt, S2)
+
+    r = kl_loss_bwd(q, dense(k_cache), qr, dense(kr_cache), qi, dense(ki_cache), w, sparse_indices,
+                    softmax_max, softmax_sum, scale, act_q=act_q, act_k=act_k, **kw)
+    dk = r["dKeyIndex"]                                         # [B, S2, 1, Di]
+    out = np.zeros(ki_cache.shape, dk.dtype)
+    for b in range(bt.shape[0]):
+        for i in range(bt.shape[1]):
+            blk = int(bt[b, i])
+            if blk >= 0:
+                out[blk] += dk[b, i * page:(i + 1) * page]
+    r = dict(r)
+    r["dKeyIndex"] = out
+    return r

@@ -92,3 +92,42 @@ def test_workspace_size_query():
     # without a GPU the CU count defaults to 256: 4 rows split 1 way -> no workspace
     assert lib.dsa_sfa_fwd_workspace_size(8192, 128, 512, 2048, 1) == 0
     assert lib.dsa_sfa_fwd_workspace_size(32, 128, 512, 2048, 1) > 0
+
+
+def _kl_ex_args(**kw):
+    a = dict(query=1, key=1, query_rope=1, key_rope=1, query_index=1, key_index=1, weights=1,
+             sparse_indices=1, softmax_max=1, softmax_sum=1, actual_seq_qlen=None, actual_seq_klen=None,
+             block_table=None, d_query_index=1, d_key_index=1, d_weights=1, loss=1, batch=1, s1=4,
+             s2=64, n1=8, d=128, d_rope=64, n_idx=8, d_idx=128, sparse_count=16, q_rows=4, kv_rows=64,
+             max_blocks=0, page_size=1, layout_query=0, layout_key=0, dtype=0, weights_dtype=2,
+             scale=0.1, workspace=None, workspace_bytes=0, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(d=96), 2), (dict(n_idx=65), 2), (dict(sparse_count=8193), 2), (dict(layout_query=2), 2),
+    (dict(layout_key=5), 2), (dict(weights_dtype=7), 2),
+    (dict(query=None), 1), (dict(loss=None), 1), (dict(q_rows=5), 1), (dict(kv_rows=63), 1),
+    (dict(layout_query=1), 1),                                 # TND query without cumulative lengths
+    (dict(layout_key=1), 1),                                   # TND key with a BSND query
+    (dict(layout_key=2, actual_seq_klen=1, page_size=16, max_blocks=4), 1),   # no block_table
+    (dict(layout_key=2, block_table=1, page_size=16, max_blocks=4), 1),      # no key lengths
+    (dict(layout_key=2, block_table=1, actual_seq_klen=1, page_size=16, max_blocks=4, kv_rows=60), 1),
+    (dict(layout_key=2, block_table=1, actual_seq_klen=1, page_size=0, max_blocks=4), 1),
+    (dict(), 4),                                               # valid, but no workspace
+    (dict(layout_query=1, layout_key=1, actual_seq_qlen=1, actual_seq_klen=1, s1=0, s2=0), 4),
+    (dict(layout_key=2, block_table=1, actual_seq_klen=1, page_size=16, max_blocks=4), 4),
+])
+def test_kl_bwd_ex_rejects_bad_arguments(kw, code):
+    _, lib = _lib()
+    st = lib.dsa_kl_bwd_ex(*_kl_ex_args(**kw))
+    assert st == code
+    assert lib.dsa_last_error().decode()
+
+
+def test_kl_workspace_sizes_agree():
+    _, lib = _lib()
+    assert lib.dsa_kl_bwd_ex_workspace_size(2 * 7, 2 * 80, 48, 128) == lib.dsa_kl_bwd_workspace_size(2, 7, 80, 48, 128)
+    assert lib.dsa_kl_bwd_ex_workspace_size(0, 80, 48, 128) == 0
+    assert lib.dsa_kl_bwd_ex_workspace_size(7, 80, 48, 64) == 0

@@ -30,7 +30,8 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.kl import kl_loss_bwd
+from oracle.common import pa_to_bsnd
+from oracle.kl import kl_loss_bwd, kl_loss_bwd_paged, kl_loss_bwd_tnd
 from tests.helpers import assert_close, to_dtype_np
 
 pytestmark = pytest.mark.gpu
@@ -234,8 +235,160 @@ def test_kl_guards():
     si = torch.zeros(1, 2, 1, 4, dtype=torch.int32, device="cuda")
     st = torch.zeros(1, 1, 2, 4, device="cuda")
     with pytest.raises(ValueError):
-        dsa.sparse_lightning_indexer_grad_kl_loss_triton(q, k, qi, ki, w, si, st, st, layout="TND")
+        dsa.sparse_lightning_indexer_grad_kl_loss_triton(q, k, qi, ki, w, si, st, st, layout="BNSD")
+    with pytest.raises(ValueError):  # TND needs cumulative lengths
+        dsa.sparse_lightning_indexer_grad_kl_loss_triton(q[0], k[0], qi[0], ki[0], w[0], si[0], st, st,
+                                                         layout="TND")
     with pytest.raises(ValueError):
         dsa.sparse_lightning_indexer_grad_kl_loss_triton(q, k, qi, ki, w, si, st, st, sparse_mode=0)
     with pytest.raises(AssertionError):
         dsa.sparse_lightning_indexer_grad_kl_loss_triton(q, k, qi, ki, w, si.reshape(1, 1, 2, 4), st, st)
+
+
+# ---------------------------------------------------------------------------
+# packed (TND) rows and a paged key cache: extensions over the reference's
+# BSND-only API (sparse_lightning_indexer_grad_kl_loss_triton.py:534-535)
+# ---------------------------------------------------------------------------
+def _dev(x, dt):
+    return None if x is None else torch.from_numpy(np.ascontiguousarray(x)).to(device="cuda", dtype=dt)
+
+
+def _tnd_case(lq, lk, N1, D, Ni, topK, dtype, seed=7):
+    """Per-batch BSND problems (B = 1, S1 = lq[b], S2 = lk[b]) packed along
+    the token axis.  Indices of batch b are drawn from [0, lk[b]) and a few
+    are pushed past lk[b] (clamped to the batch's last key)."""
+    parts = []
+    for b, (nq, nk) in enumerate(zip(lq, lk)):
+        c = _case(1, nq, max(nk, 1), N1, D, Ni, topK, dtype, "causal_random", seed=seed + b)
+        if nk == 0:
+            c["k"], c["kr"], c["ki"] = (x[:, :0] for x in (c["k"], c["kr"], c["ki"]))
+        c["si"][0, :, 0, -1] = nk + 5  # out of the batch's range: clamped
+        parts.append(c)
+    cat = lambda key: np.concatenate([p[key][0] for p in parts], 0)  # noqa: E731
+    return dict(q=cat("q"), k=cat("k"), qr=cat("qr"), kr=cat("kr"), qi=cat("qi"), ki=cat("ki"), w=cat("w"),
+                si=cat("si"), smax=np.concatenate([p["smax"][0, 0] for p in parts], 0)[None],
+                ssum=np.concatenate([p["ssum"][0, 0] for p in parts], 0)[None], scale=parts[0]["scale"],
+                dtype=dtype, cu_q=np.cumsum(lq).astype(np.int32), cu_k=np.cumsum(lk).astype(np.int32))
+
+
+def _run_tnd(t):
+    import dsa_triton_ascend_amd as dsa
+    dt = t["dtype"]
+    res = dsa.sparse_lightning_indexer_grad_kl_loss_triton(
+        _dev(t["q"], dt), _dev(t["k"], dt), _dev(t["qi"], dt), _dev(t["ki"], dt), _dev(t["w"], torch.float32),
+        _dev(t["si"], torch.int32), _dev(t["smax"], torch.float32), _dev(t["ssum"], torch.float32),
+        query_rope=_dev(t["qr"], dt), key_rope=_dev(t["kr"], dt), actual_seq_qlen=t["cu_q"].tolist(),
+        actual_seq_klen=t["cu_k"].tolist(), scale_value=t["scale"], layout="TND")
+    torch.cuda.synchronize()
+    return [r.float().cpu().numpy() for r in res]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_kl_tnd_matches_oracle(dtype):
+    """Ragged packed batches (one with no query rows, one with fewer keys
+    than queries) against the TND oracle."""
+    lq, lk = [5, 0, 9, 3], [40, 12, 64, 2]
+    print(f"[kl_bwd] TND lq={lq} lk={lk} {dtype}", flush=True)
+    t = _tnd_case(lq, lk, 32, 256, 16, 48, dtype)
+    got = _run_tnd(t)
+    exp = kl_loss_bwd_tnd(t["q"], t["k"], t["qr"], t["kr"], t["qi"], t["ki"], t["w"], t["si"], t["smax"],
+                          t["ssum"], t["scale"], t["cu_q"], t["cu_k"], compute_dtype=np.float64)
+    assert got[0].shape == t["qi"].shape and got[1].shape == t["ki"].shape and got[2].shape == t["w"].shape
+    _check(got, exp, "TND")
+
+
+def test_kl_tnd_equal_lengths_bit_exact_to_bsnd():
+    """TND with equal per-batch lengths is the BSND problem with its batch
+    axis flattened: every output is bit-identical to the BSND call."""
+    print("[kl_bwd] TND == BSND bit-exact", flush=True)
+    B, S1, S2 = 3, 6, 50
+    c = _case(B, S1, S2, 16, 128, 8, 32, torch.bfloat16, "causal_random")
+    bsnd = _run_gpu(c)
+    t = dict(q=c["q"].reshape(B * S1, *c["q"].shape[2:]), k=c["k"].reshape(B * S2, 1, -1),
+             qr=c["qr"].reshape(B * S1, *c["qr"].shape[2:]), kr=c["kr"].reshape(B * S2, 1, -1),
+             qi=c["qi"].reshape(B * S1, *c["qi"].shape[2:]), ki=c["ki"].reshape(B * S2, 1, -1),
+             w=c["w"].reshape(B * S1, -1), si=c["si"].reshape(B * S1, 1, -1), smax=c["smax"], ssum=c["ssum"],
+             scale=c["scale"], dtype=torch.bfloat16, cu_q=np.cumsum([S1] * B).astype(np.int32),
+             cu_k=np.cumsum([S2] * B).astype(np.int32))
+    tnd = _run_tnd(t)
+    for a, b, nm in zip(bsnd, tnd, ("dQueryIndex", "dKeyIndex", "dW", "loss")):
+        assert np.array_equal(a.reshape(-1), b.reshape(-1)), nm
+
+
+def _paged_case(B, S1, N1, D, Ni, topK, page, max_blocks, nblk, table, act_k, dtype, seed=11):
+    rng = np.random.RandomState(seed)
+    f = lambda *s: to_dtype_np(rng.randn(*s).astype(np.float16).astype(np.float32), dtype)  # noqa: E731
+    q, qr, qi = f(B, S1, N1, D), f(B, S1, N1, 64), f(B, S1, Ni, 128)
+    kc, krc, kic = f(nblk, page, 1, D), f(nblk, page, 1, 64), f(nblk, page, 1, 128)
+    w = np.abs(rng.randn(B, S1, Ni)).astype(np.float32)
+    S2 = max_blocks * page
+    si = np.zeros((B, S1, 1, topK), np.int32)
+    for b in range(B):
+        for s1 in range(S1):
+            vis = max(act_k[b] - S1 + s1 + 1, 1)
+            n = min(topK, vis)
+            si[b, s1, 0, :n] = rng.choice(vis, size=n, replace=False)
+    scale = 1.0 / math.sqrt(D + 64)
+    kd, krd = pa_to_bsnd(kc, table, S2), pa_to_bsnd(krc, table, S2)
+    smax, ssum = _dense_stats(q, kd, qr, krd, scale, [S1] * B, act_k)
+    return dict(q=q, qr=qr, qi=qi, kc=kc, krc=krc, kic=kic, w=w, si=si, smax=smax, ssum=ssum, scale=scale,
+                table=np.asarray(table, np.int32), act_k=list(act_k), dtype=dtype, S2=S2)
+
+
+def _run_paged(c):
+    import dsa_triton_ascend_amd as dsa
+    dt = c["dtype"]
+    res = dsa.sparse_lightning_indexer_grad_kl_loss_triton(
+        _dev(c["q"], dt), _dev(c["kc"], dt), _dev(c["qi"], dt), _dev(c["kic"], dt), _dev(c["w"], torch.float32),
+        _dev(c["si"], torch.int32), _dev(c["smax"], torch.float32), _dev(c["ssum"], torch.float32),
+        query_rope=_dev(c["qr"], dt), key_rope=_dev(c["krc"], dt), actual_seq_klen=c["act_k"],
+        scale_value=c["scale"], block_table=_dev(c["table"], torch.int32))
+    torch.cuda.synchronize()
+    return [r.float().cpu().numpy() for r in res]
+
+
+def _paged_oracle(c):
+    return kl_loss_bwd_paged(c["q"], c["kc"], c["qr"], c["krc"], c["qi"], c["kic"], c["w"], c["si"],
+                             c["smax"], c["ssum"], c["scale"], c["table"], c["act_k"], compute_dtype=np.float64)
+
+
+def test_kl_paged_matches_oracle_and_bsnd():
+    """Disjoint pages in shuffled order, a -1 page inside a batch's visible
+    range (zero key rows, no gradient) and unused cache pages (zero
+    gradient).  Against the oracle, and bit-exact against the BSND kernel on
+    the de-paged cache (dKi gathered back to the pages)."""
+    print("[kl_bwd] paged", flush=True)
+    page, max_blocks, nblk = 16, 5, 12
+    table = [[7, 2, 10, -1, 4], [3, 11, 0, 5, 9]]
+    act_k = [80, 70]
+    c = _paged_case(2, 6, 16, 128, 8, 40, page, max_blocks, nblk, table, act_k, torch.bfloat16)
+    got = _run_paged(c)
+    assert got[1].shape == c["kic"].shape
+    _check(got, _paged_oracle(c), "paged")
+    # the same problem de-paged, through the BSND kernel
+    S2 = c["S2"]
+    bc = dict(q=c["q"], k=pa_to_bsnd(c["kc"], table, S2), qr=c["qr"], kr=pa_to_bsnd(c["krc"], table, S2),
+              qi=c["qi"], ki=pa_to_bsnd(c["kic"], table, S2), w=c["w"], si=c["si"], smax=c["smax"],
+              ssum=c["ssum"], scale=c["scale"], aq=[6, 6], ak=act_k, dtype=torch.bfloat16,
+              w_dtype=torch.float32, explicit_len=True)
+    ref = _run_gpu(bc)
+    for i, nm in ((0, "dQueryIndex"), (2, "dW"), (3, "loss")):
+        assert np.array_equal(got[i], ref[i]), nm
+    used = set()
+    for b in range(2):
+        for i, blk in enumerate(table[b]):
+            if blk >= 0:
+                assert np.array_equal(got[1][blk], ref[1][b, i * page:(i + 1) * page]), f"page {blk}"
+                used.add(blk)
+    for blk in range(nblk):
+        if blk not in used:
+            assert np.all(got[1][blk] == 0), f"unused page {blk}"
+
+
+def test_kl_paged_shared_prefix_page():
+    """Two batches share their first page (a common prefix): its gradient
+    is the sum over both batches' slots."""
+    print("[kl_bwd] paged shared page", flush=True)
+    table = [[4, 1, 6], [4, 0, 2]]
+    c = _paged_case(2, 5, 8, 128, 8, 24, 16, 3, 8, table, [48, 40], torch.float16, seed=3)
+    _check(_run_paged(c), _paged_oracle(c), "paged shared")

@@ -252,3 +252,78 @@ def test_kl_matches_scalar_brute_force():
     r2 = kl_loss_bwd(q, k, qr, kr, qi, ki, w, si, smax, ssum, scale, compute_dtype=np.float64,
                      dki_oob="skip")
     assert not np.allclose(r2["dKeyIndex"][0, S2 - 1], r["dKeyIndex"][0, S2 - 1])
+
+
+# ---------------------------------------------------------------------------
+# KL on packed (TND) rows and paged key caches: the compositions agree with
+# the BSND oracle where the layouts describe the same problem
+# ---------------------------------------------------------------------------
+def _kl_bsnd_problem(B=2, S1=5, S2=48, N1=4, D=16, Ni=3, topK=12, seed=5):
+    rng = np.random.RandomState(seed)
+    f = lambda *s: rng.randn(*s).astype(np.float32)  # noqa: E731
+    q, k, qr, kr = f(B, S1, N1, D), f(B, S2, 1, D), f(B, S1, N1, 4), f(B, S2, 1, 4)
+    qi, ki = f(B, S1, Ni, 8), f(B, S2, 1, 8)
+    w = np.abs(f(B, S1, Ni))
+    si = rng.randint(0, S2 + 3, (B, S1, 1, topK)).astype(np.int32)   # some past S2: clamped
+    smax = f(B, 1, S1, N1)
+    ssum = np.abs(f(B, 1, S1, N1)) + 1.0
+    return q, k, qr, kr, qi, ki, w, si, smax, ssum
+
+
+def test_kl_tnd_oracle_equal_lengths_is_bsnd():
+    from oracle.kl import kl_loss_bwd, kl_loss_bwd_tnd
+    B, S1, S2 = 2, 5, 48
+    q, k, qr, kr, qi, ki, w, si, smax, ssum = _kl_bsnd_problem(B, S1, S2)
+    a = kl_loss_bwd(q, k, qr, kr, qi, ki, w, si, smax, ssum, 0.3, compute_dtype=np.float64)
+    flat = lambda x, S: x.reshape(B * S, *x.shape[2:])  # noqa: E731
+    b = kl_loss_bwd_tnd(flat(q, S1), flat(k, S2), flat(qr, S1), flat(kr, S2), flat(qi, S1), flat(ki, S2),
+                        flat(w, S1), flat(si, S1), smax, ssum, 0.3, np.cumsum([S1] * B), np.cumsum([S2] * B),
+                        compute_dtype=np.float64)
+    for key in ("dQueryIndex", "dKeyIndex", "dW", "loss"):
+        assert np.array_equal(a[key].reshape(-1), b[key].reshape(-1)), key
+
+
+def test_kl_tnd_oracle_clamps_to_the_batch():
+    """A packed batch's out-of-range ids clamp to its own last key, which a
+    B = 1 problem of that batch alone reproduces."""
+    from oracle.kl import kl_loss_bwd, kl_loss_bwd_tnd
+    q, k, qr, kr, qi, ki, w, si, smax, ssum = _kl_bsnd_problem(1, 4, 30)
+    lq, lk = [0, 4], [18, 30]
+    # batch 1 of the packed problem is the B = 1 problem; batch 0 has keys only
+    kk = np.concatenate([np.ones((18, 1, 16), np.float32), k[0]], 0)
+    kkr = np.concatenate([np.ones((18, 1, 4), np.float32), kr[0]], 0)
+    kki = np.concatenate([np.ones((18, 1, 8), np.float32), ki[0]], 0)
+    t = kl_loss_bwd_tnd(q[0], kk, qr[0], kkr, qi[0], kki, w[0], si[0], smax, ssum, 0.3, np.cumsum(lq),
+                        np.cumsum(lk), compute_dtype=np.float64)
+    r = kl_loss_bwd(q, k, qr, kr, qi, ki, w, si, smax, ssum, 0.3, compute_dtype=np.float64)
+    assert np.array_equal(t["dKeyIndex"][18:], r["dKeyIndex"][0])
+    assert np.all(t["dKeyIndex"][:18] == 0)
+    assert np.array_equal(t["dQueryIndex"], r["dQueryIndex"][0]) and t["loss"][0] == r["loss"][0]
+
+
+def test_kl_paged_oracle_matches_bsnd_on_the_depaged_cache():
+    from oracle.kl import kl_loss_bwd, kl_loss_bwd_paged
+    B, S1, page, mb = 2, 5, 8, 6
+    S2 = page * mb
+    q, k, qr, kr, qi, ki, w, si, smax, ssum = _kl_bsnd_problem(B, S1, S2)
+    rng = np.random.RandomState(9)
+    perm = rng.permutation(B * mb + 3)[:B * mb].reshape(B, mb)          # disjoint pages, shuffled
+    nblk = B * mb + 3
+    caches = []
+    for x in (k, kr, ki):
+        c = rng.randn(nblk, page, 1, x.shape[-1]).astype(np.float32)   # unused pages hold noise
+        for b in range(B):
+            for i in range(mb):
+                c[perm[b, i]] = x[b, i * page:(i + 1) * page]
+        caches.append(c)
+    act_k = [S2, S2 - 5]
+    p = kl_loss_bwd_paged(q, caches[0], qr, caches[1], qi, caches[2], w, si, smax, ssum, 0.3, perm, act_k,
+                          compute_dtype=np.float64)
+    r = kl_loss_bwd(q, k, qr, kr, qi, ki, w, si, smax, ssum, 0.3, act_k=act_k, compute_dtype=np.float64)
+    for key in ("dQueryIndex", "dW", "loss"):
+        assert np.array_equal(p[key], r[key]), key
+    for b in range(B):
+        for i in range(mb):
+            assert np.array_equal(p["dKeyIndex"][perm[b, i]], r["dKeyIndex"][b, i * page:(i + 1) * page])
+    unused = sorted(set(range(nblk)) - set(perm.reshape(-1).tolist()))
+    assert unused and np.all(p["dKeyIndex"][unused] == 0)
