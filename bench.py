@@ -322,7 +322,41 @@ def long_legs(dev, steps):
                         "sparse_lightning_indexer_grad_kl_loss: B=1, S1=S2=4096, N1=128, D=512+64, Nidx1=64, "
                         "D_idx=128, topK=2048 causal, bf16 (fp32 weights), stats from the SFA forward",
                         n * (3 * 2 * NI * DI + 2 * N1 * (D + DR) + 2 * NI), ms, n)
+    del si, o, do
+    torch.cuda.empty_cache()
+    # dense warm-up stage at the same shape: every causal key, teacher stats of
+    # the dense causal forward [B, N2, S1, G]
+    dsmax, dssum = dense_stats(q, qr, k, kr, scale)
+
+    def dense():
+        return dsa.dense_loss_backward_triton(q, k, qi, ki, w, dsmax, dssum, scale_value=scale, query_rope=qr,
+                                              key_rope=kr)
+    ms = time_call(dense, steps, 1)
+    nd = S * (S + 1) // 2
+    out["dense_kl_bwd"] = leg("dense indexer KL-loss bwd TFLOP/s",
+                              "dense_loss_backward (warm-up stage, index LSE computed inside): B=1, S1=S2=4096, "
+                              "N1=128, N2=1, D=512+64, Nidx1=64, D_idx=128, all causal keys, bf16 (fp32 weights)",
+                              nd * (3 * 2 * NI * DI + 2 * N1 * (D + DR) + 2 * NI), ms, nd)
     return out
+
+
+def dense_stats(q, qr, k, kr, scale, rows=256):
+    """Softmax max / sum of the dense causal attention, [1, 1, S, N1] fp32."""
+    import torch
+    S = q.shape[1]
+    kk = torch.cat([k[0, :, 0], kr[0, :, 0]], -1).float()                     # [S, D+Dr]
+    smax = torch.empty(1, 1, S, q.shape[2], device=q.device)
+    ssum = torch.empty_like(smax)
+    ar = torch.arange(S, device=q.device)
+    for r0 in range(0, S, rows):
+        qq = torch.cat([q[0, r0:r0 + rows], qr[0, r0:r0 + rows]], -1).float()  # [r, N1, D+Dr]
+        sc = torch.matmul(qq, kk.T) * scale                                      # [r, N1, S]
+        sc.masked_fill_((ar[None, :] > ar[r0:r0 + rows, None])[:, None, :], float("-inf"))
+        m = sc.amax(-1)
+        smax[0, 0, r0:r0 + rows] = m
+        ssum[0, 0, r0:r0 + rows] = torch.exp(sc - m[..., None]).sum(-1)
+        del sc
+    return smax, ssum
 
 
 def measured_traffic(name="sfa_fwd_decode_traffic"):

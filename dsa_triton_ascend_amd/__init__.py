@@ -7,6 +7,9 @@ Public API, mirroring the reference's operator modules:
 * ``lightning_indexer_triton`` / ``LightningIndexerTriton``
 * ``sparse_lightning_indexer_grad_kl_loss_triton`` /
   ``SparseLightningIndexerGradKLLossTriton``
+* the dense warm-up stage: ``dense_lightning_indexer_softmax_lse_triton`` /
+  ``DenseLightningIndexerSoftmaxLseTriton`` and ``dense_loss_backward_triton``
+  / ``DenseLightningIndexerGradKLLossTriton`` (with their ``npu_`` aliases)
 
 and the autograd pairing for training (``autograd.py``):
 ``sparse_flash_attention_train`` / ``SparseFlashAttentionFunction`` and
@@ -31,6 +34,17 @@ from .lightning_indexer import (  # noqa: F401
 from .sparse_lightning_indexer_grad_kl_loss import (  # noqa: F401
     SparseLightningIndexerGradKLLossTriton,
     sparse_lightning_indexer_grad_kl_loss_triton,
+)
+
+from .dense_loss_backward import (  # noqa: F401
+    DenseLightningIndexerGradKLLossTriton,
+    DenseLightningIndexerSoftmaxLseTriton,
+    DenseLossBackwardTriton,
+    dense_lightning_indexer_grad_kl_loss_triton,
+    dense_lightning_indexer_softmax_lse_triton,
+    dense_loss_backward_triton,
+    npu_dense_lightning_indexer_grad_kl_loss_triton,
+    npu_dense_lightning_indexer_softmax_lse_triton,
 )
 
 sparse_flash_attention = sparse_flash_attention_triton

@@ -83,6 +83,24 @@ SIGNATURES = {
         _vp, _sz, _vp,                        # workspace, workspace_bytes, stream
     ]),
     "dsa_kl_bwd_ex_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
+    "dsa_dense_li_softmax_lse": (_c.c_int, [
+        _vp, _vp, _vp, _i32p, _i32p,          # query_index, key_index, weights, actual_seq_qlen, actual_seq_klen
+        _vp, _vp,                             # softmax_max_index, softmax_sum_index
+        _i64, _i64, _i64, _i64, _i64,         # batch, s1, s2, n_idx, d_idx
+        _i32, _i32, _vp,                      # dtype, weights_dtype, stream
+    ]),
+    "dsa_dense_kl_bwd": (_c.c_int, [
+        _vp, _vp, _vp, _vp,                   # query, key, query_rope, key_rope
+        _vp, _vp, _vp,                        # query_index, key_index, weights
+        _vp, _vp, _vp, _vp,                   # softmax_max, softmax_sum, softmax_max_index, softmax_sum_index
+        _i32p, _i32p,                         # actual_seq_qlen, actual_seq_klen
+        _vp, _vp, _vp, _vp,                   # d_query_index, d_key_index, d_weights, loss
+        _i64, _i64, _i64, _i64, _i64,         # batch, s1, s2, n1, n2
+        _i64, _i64, _i64, _i64,               # d, d_rope, n_idx, d_idx
+        _i32, _i32, _f32,                     # dtype, weights_dtype, scale_value
+        _vp, _sz, _vp,                        # workspace, workspace_bytes, stream
+    ]),
+    "dsa_dense_kl_bwd_workspace_size": (_sz, [_i64, _i64, _i64, _i64]),
     "dsa_li_fwd": (_c.c_int, [
         _vp, _vp, _vp, _i32p, _i32p,          # query, key, weights, actual_seq_q, actual_seq_k
         _i32p, _vp,                           # sparse_indices, sparse_values

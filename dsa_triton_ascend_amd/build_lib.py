@@ -23,6 +23,7 @@ SOURCES = [
     "sfa_bwd.hip",
     "li_fwd.hip",
     "kl_bwd.hip",
+    "dense_kl.hip",
 ]
 
 ARCH = os.environ.get("DSA_OFFLOAD_ARCH", "gfx950")

@@ -71,6 +71,19 @@ int sfa_bwd_run(const void* query, const void* query_rope, const void* key, cons
                 int64_t q_rows, int64_t kv_rows, int32_t sparse_block_size, int32_t sparse_mode,
                 int32_t layout, int32_t dtype, float scale_value, void* workspace, hipStream_t stream);
 
+// dense_kl.hip
+size_t dense_kl_workspace_bytes(int64_t batch, int64_t s1, int64_t s2, int64_t di);
+int dense_lse_run(const void* query_index, const void* key_index, const void* weights, const int32_t* act_q,
+                  const int32_t* act_k, float* max_index, float* sum_index, int64_t batch, int64_t s1,
+                  int64_t s2, int64_t nidx, int64_t di, int32_t dtype, int32_t w_dtype, hipStream_t stream);
+int dense_kl_run(const void* query, const void* key, const void* query_rope, const void* key_rope,
+                 const void* query_index, const void* key_index, const void* weights, const float* softmax_max,
+                 const float* softmax_sum, const float* max_index, const float* sum_index, const int32_t* act_q,
+                 const int32_t* act_k, void* d_query_index, void* d_key_index, void* d_weights, float* loss,
+                 int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t n2, int64_t d, int64_t d_rope,
+                 int64_t nidx, int64_t di, int32_t dtype, int32_t w_dtype, float scale_value, void* workspace,
+                 hipStream_t stream);
+
 // li_fwd.hip
 int li_scores_run(const void* query, const void* key, const void* weights, const int32_t* act_q,
                   const int32_t* act_k, float* scores, int64_t batch, int64_t s1, int64_t s2,
@@ -377,6 +390,77 @@ int dsa_kl_bwd_ex(const void* query, const void* key, const void* query_rope, co
                     d_key_index, d_weights, loss, batch, s1, s2, n1, d, d_rope, n_idx, sparse_count, q_rows,
                     kv_rows, max_blocks, page_size, layout_query, layout_key, dtype, weights_dtype, scale_value,
                     workspace, (hipStream_t)stream);
+}
+
+// shared validation of the dense index inputs (the reference's
+// _validate_dense_index_inputs / dtype checks, dense_loss_backward_triton.py:658-697)
+static int dense_check_index(const void* query_index, const void* key_index, const void* weights, int64_t batch,
+                             int64_t s1, int64_t s2, int64_t n_idx, int64_t d_idx, int32_t dtype,
+                             int32_t weights_dtype) {
+  DSA_CHECK_ARG(query_index && key_index && weights, "null index tensor pointer");
+  DSA_CHECK_SUPPORTED(d_idx == 128 || d_idx == 256 || d_idx == 512, "D_idx must be one of (128, 256, 512), got %lld",
+                      (long long)d_idx);
+  DSA_CHECK_SUPPORTED(n_idx >= 1 && n_idx <= 128, "Nidx1 must be in [1, 128], got %lld", (long long)n_idx);
+  DSA_CHECK_SUPPORTED(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_FP16, "index dtype must be bfloat16 or float16");
+  DSA_CHECK_SUPPORTED(weights_dtype == DSA_DTYPE_FP32 || weights_dtype == DSA_DTYPE_BF16 ||
+                          weights_dtype == DSA_DTYPE_FP16,
+                      "weights dtype must be float32, bfloat16 or float16");
+  DSA_CHECK_ARG(batch >= 1 && s1 >= 1 && s2 >= 1, "batch, S1 and S2 must be >= 1");
+  DSA_CHECK_ARG(batch * s1 < (1ll << 31) && batch * s2 < (1ll << 31) && s2 < (1ll << 30),
+                "B*S1, B*S2 and S2 must stay below 2^31");
+  return DSA_OK;
+}
+
+int dsa_dense_li_softmax_lse(const void* query_index, const void* key_index, const void* weights,
+                             const int32_t* actual_seq_qlen, const int32_t* actual_seq_klen,
+                             float* softmax_max_index, float* softmax_sum_index, int64_t batch, int64_t s1,
+                             int64_t s2, int64_t n_idx, int64_t d_idx, int32_t dtype, int32_t weights_dtype,
+                             void* stream) {
+  g_err[0] = '\0';
+  const int st = dense_check_index(query_index, key_index, weights, batch, s1, s2, n_idx, d_idx, dtype,
+                                   weights_dtype);
+  if (st != DSA_OK) return st;
+  DSA_CHECK_ARG(softmax_max_index && softmax_sum_index, "null output tensor pointer");
+  return dense_lse_run(query_index, key_index, weights, actual_seq_qlen, actual_seq_klen, softmax_max_index,
+                       softmax_sum_index, batch, s1, s2, n_idx, d_idx, dtype, weights_dtype, (hipStream_t)stream);
+}
+
+size_t dsa_dense_kl_bwd_workspace_size(int64_t batch, int64_t s1, int64_t s2, int64_t d_idx) {
+  if (batch <= 0 || s1 <= 0 || s2 <= 0 || !(d_idx == 128 || d_idx == 256 || d_idx == 512)) return 0;
+  return dense_kl_workspace_bytes(batch, s1, s2, d_idx);
+}
+
+int dsa_dense_kl_bwd(const void* query, const void* key, const void* query_rope, const void* key_rope,
+                     const void* query_index, const void* key_index, const void* weights,
+                     const float* softmax_max, const float* softmax_sum, const float* softmax_max_index,
+                     const float* softmax_sum_index, const int32_t* actual_seq_qlen,
+                     const int32_t* actual_seq_klen, void* d_query_index, void* d_key_index, void* d_weights,
+                     float* loss, int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t n2, int64_t d,
+                     int64_t d_rope, int64_t n_idx, int64_t d_idx, int32_t dtype, int32_t weights_dtype,
+                     float scale_value, void* workspace, size_t workspace_bytes, void* stream) {
+  g_err[0] = '\0';
+  int st = dense_check_index(query_index, key_index, weights, batch, s1, s2, n_idx, d_idx, dtype, weights_dtype);
+  if (st != DSA_OK) return st;
+  DSA_CHECK_ARG(query && key && softmax_max && softmax_sum, "null input tensor pointer");
+  DSA_CHECK_ARG(d_query_index && d_key_index && d_weights && loss, "null output tensor pointer");
+  DSA_CHECK_ARG((softmax_max_index == nullptr) == (softmax_sum_index == nullptr),
+                "softmax_max_index and softmax_sum_index must be both provided or both omitted");
+  DSA_CHECK_SUPPORTED(d == 128 || d == 256 || d == 512, "D must be one of (128, 256, 512), got %lld", (long long)d);
+  DSA_CHECK_SUPPORTED(d_rope == 0 || d_rope == 64, "rope dim must be 64 (or 0 for no rope), got %lld",
+                      (long long)d_rope);
+  DSA_CHECK_ARG(d_rope == 0 || (query_rope && key_rope), "null rope tensor pointer");
+  DSA_CHECK_ARG(n2 >= 1 && n1 >= 1 && n1 % n2 == 0, "query N1 must be divisible by key N2");
+  DSA_CHECK_SUPPORTED(n1 <= 128, "N1 must be <= 128, got %lld", (long long)n1);
+  const size_t need = dense_kl_workspace_bytes(batch, s1, s2, d_idx);
+  if (workspace == nullptr || workspace_bytes < need) {
+    set_error("workspace of %zu bytes required, %zu given", need, workspace_bytes);
+    return DSA_ERR_WORKSPACE;
+  }
+  return dense_kl_run(query, key, d_rope ? query_rope : nullptr, d_rope ? key_rope : nullptr, query_index,
+                      key_index, weights, softmax_max, softmax_sum, softmax_max_index, softmax_sum_index,
+                      actual_seq_qlen, actual_seq_klen, d_query_index, d_key_index, d_weights, loss, batch, s1, s2,
+                      n1, n2, d, d_rope, n_idx, d_idx, dtype, weights_dtype, scale_value, workspace,
+                      (hipStream_t)stream);
 }
 
 size_t dsa_li_fwd_workspace_size(int64_t q_rows, int64_t n2, int64_t s2) {

@@ -33,7 +33,7 @@
 //    not depend on the bucket order and the output is deterministic.
 //  * The loss is written per row and summed by one workgroup in a fixed
 //    order (the reference adds rows with an atomic).
-#include "common.h"
+#include "kl_common.h"
 
 namespace dsa {
 
@@ -77,30 +77,6 @@ constexpr int kKlWaves = 8;
 constexpr int kKlMaxNidx = 64;
 constexpr int kKlMaxTopk = 8192;
 constexpr int kKlDsRow = kKlMaxNidx + 8;  // padded LDS row of dS^T (elements)
-
-// x = hi + mid + lo exactly (bf16 parts of an fp32 value: 8 + 8 + 8 bits),
-// as the A operand of a 16x16x16 product whose k index is this lane's r
-struct Split3 {
-  s16x4 h, m, l;
-};
-__device__ __forceinline__ void split3_set(Split3& s, int r, float x) {
-  const bf16 h = (bf16)x;
-  const float r1 = x - (float)h;
-  const bf16 m = (bf16)r1;
-  const bf16 l = (bf16)(r1 - (float)m);
-  s.h[r] = __builtin_bit_cast(short, h);
-  s.m[r] = __builtin_bit_cast(short, m);
-  s.l[r] = __builtin_bit_cast(short, l);
-}
-// sum over k of A[row][k] (rows = MFMA rows of the A operand), all 16
-// output columns equal: B = ones
-__device__ __forceinline__ f32x4 split3_rowsum(const Split3& s) {
-  const short one = __builtin_bit_cast(short, (bf16)1.f);
-  const s16x4 ones = {one, one, one, one};
-  f32x4 c = Mfma16<bf16>::run(s.h, ones, (f32x4){0.f, 0.f, 0.f, 0.f});
-  c = Mfma16<bf16>::run(s.m, ones, c);
-  return Mfma16<bf16>::run(s.l, ones, c);
-}
 
 struct KlRow {
   int b, s1, n;
@@ -162,18 +138,6 @@ __device__ __forceinline__ int kl_token(const KlMap& m, const KlRow& r, const in
   const int blk = m.block_table[(int64_t)r.b * m.max_blocks + t / m.page_size];
   const int64_t phys = (int64_t)blk * m.page_size + t % m.page_size;
   return (blk < 0 || phys >= m.kv_rows) ? -1 : (int)phys;
-}
-
-__device__ __forceinline__ float load_w(const void* w, int64_t i, int dt) {
-  if (dt == DSA_DTYPE_FP32) return ((const float*)w)[i];
-  if (dt == DSA_DTYPE_BF16) return (float)((const bf16*)w)[i];
-  return (float)((const f16*)w)[i];
-}
-
-__device__ __forceinline__ void store_w(void* w, int64_t i, int dt, float v) {
-  if (dt == DSA_DTYPE_FP32) ((float*)w)[i] = v;
-  else if (dt == DSA_DTYPE_BF16) ((bf16*)w)[i] = (bf16)v;
-  else ((f16*)w)[i] = (f16)v;
 }
 
 template <int D, int DR, typename T>

@@ -180,6 +180,51 @@ int dsa_kl_bwd_ex(const void* query, const void* key, const void* query_rope, co
 size_t dsa_kl_bwd_ex_workspace_size(int64_t q_rows, int64_t kv_rows, int64_t sparse_count, int64_t d_idx);
 
 /*
+ * Dense lightning-indexer softmax LSE (the dense warm-up stage).  Replaces
+ * the reference core `_dense_index_stats_core` and its kernel
+ * `_dense_indexer_stats_kernel` (dense_loss_backward_triton.py:129-177,
+ * 405-432).  BSND: query_index [B,S1,Nidx1,d_idx], key_index [B,S2,1,d_idx],
+ * weights [B,S1,Nidx1] (weights_dtype), actual_seq_qlen / actual_seq_klen
+ * [B] per-batch lengths (NULL = full).  For a row (b, s1) with s1 < act_q
+ * over its visible keys t < min(max(act_k - act_q + s1 + 1, 0), S2):
+ * I[t] = sum_g w_g ReLU(qi_g . ki_t), softmax_max_index = max I and
+ * softmax_sum_index = sum exp(I - max) (fp32 [B*S1]); -inf / 0 for a row with
+ * no visible key.  d_idx in {128, 256, 512}, Nidx1 <= 128.  No workspace.
+ */
+int dsa_dense_li_softmax_lse(const void* query_index, const void* key_index, const void* weights,
+                             const int32_t* actual_seq_qlen, const int32_t* actual_seq_klen,
+                             float* softmax_max_index, float* softmax_sum_index, int64_t batch, int64_t s1,
+                             int64_t s2, int64_t n_idx, int64_t d_idx, int32_t dtype, int32_t weights_dtype,
+                             void* stream);
+
+/*
+ * Dense lightning-indexer KL-loss backward (the dense warm-up stage).
+ * Replaces `_dense_loss_backward_core` and `_dense_loss_backward_with_index_core`
+ * (dense_loss_backward_triton.py:435-655) with their kernels (129-397).
+ * query [B,S1,N1,D], key [B,S2,N2,D] (N1 % N2 == 0, GQA), query_rope /
+ * key_rope [..,64] or NULL with d_rope = 0, query_index / key_index /
+ * weights as dsa_dense_li_softmax_lse, softmax_max / softmax_sum [B,N2,S1,G]
+ * fp32 (G = N1/N2).  softmax_max_index / softmax_sum_index: the index LSE
+ * ([B*S1] fp32) as given, or both NULL to compute it.  Writes d_query_index,
+ * d_key_index (index dtype), d_weights (weights dtype) and loss[1] (sum over
+ * rows).  dKeyIndex is reduced without atomics, so every output is
+ * deterministic.  D in {128, 256, 512}, N1 <= 128.  The workspace
+ * (dsa_dense_kl_bwd_workspace_size) holds the [B*S1, S2] fp32 index-score /
+ * dI rows and the dKeyIndex partial sums.
+ */
+int dsa_dense_kl_bwd(const void* query, const void* key, const void* query_rope, const void* key_rope,
+                     const void* query_index, const void* key_index, const void* weights,
+                     const float* softmax_max, const float* softmax_sum, const float* softmax_max_index,
+                     const float* softmax_sum_index, const int32_t* actual_seq_qlen,
+                     const int32_t* actual_seq_klen, void* d_query_index, void* d_key_index, void* d_weights,
+                     float* loss, int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t n2, int64_t d,
+                     int64_t d_rope, int64_t n_idx, int64_t d_idx, int32_t dtype, int32_t weights_dtype,
+                     float scale_value, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of dsa_dense_kl_bwd. */
+size_t dsa_dense_kl_bwd_workspace_size(int64_t batch, int64_t s1, int64_t s2, int64_t d_idx);
+
+/*
  * Lightning indexer: scores + stable top-k.  Replaces the reference core
  * `_lightning_indexer_score_core` (lightning_indexer_triton.py:382-413) and the
  * top-k after it (`_stable_topk`, 339-357, called at 539), with the stable

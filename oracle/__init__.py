@@ -23,6 +23,9 @@ Modules and the reference code each one restates:
 * ``kl``         sparse lightning-indexer KL-loss backward
                  (sli_grad_kl_loss_numpy.py:16-152,
                   sparse_lightning_indexer_grad_kl_loss_triton.py:39-327)
+* ``dense_kl``   dense indexer softmax LSE and dense KL-loss backward
+                 (dense_loss_backward_triton.py:129-397,
+                  test_dense_loss_backward_triton.py:101-138)
 
 How each function is pinned (checks that are not a retyping of its formula)
 is listed in the test files ``tests/test_oracle_*.py``.  Every function here
