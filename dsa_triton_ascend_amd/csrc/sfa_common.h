@@ -60,14 +60,17 @@ __device__ __forceinline__ int sfa_load_id(const P& p, const int32_t* idx_row, i
   return idx_row[pos / p.bs];
 }
 
+// `tab` is the row's block-table row (PA_BSND), in global memory or staged
+// in LDS by the caller.
 template <typename P>
-__device__ __forceinline__ bool sfa_resolve_id(const P& p, const RowInfo& ri, int id, int pos, int* phys) {
+__device__ __forceinline__ bool sfa_resolve_id(const P& p, const RowInfo& ri, int id, int pos, int* phys,
+                                               const int32_t* tab) {
   if (id < 0) return false;
   int64_t tok = (int64_t)id * p.bs + (pos % p.bs);
   if (tok >= ri.threshold || tok >= ri.act_k) return false;
   if (p.layout_kv == DSA_LAYOUT_PA_BSND) {
     if (tok >= (int64_t)p.max_blocks * p.page_size) return false;
-    int blk = p.block_table[(int64_t)ri.b * p.max_blocks + tok / p.page_size];
+    int blk = tab[tok / p.page_size];
     int64_t r = (int64_t)blk * p.page_size + tok % p.page_size;
     *phys = (blk < 0 || r >= p.kv_rows) ? -1 : (int)r;
     return true;
@@ -82,7 +85,8 @@ __device__ __forceinline__ bool sfa_resolve_id(const P& p, const RowInfo& ri, in
 template <typename P>
 __device__ __forceinline__ bool sfa_resolve(const P& p, const RowInfo& ri, const int32_t* idx_row,
                                             int pos, int* phys) {
-  return sfa_resolve_id(p, ri, sfa_load_id(p, idx_row, pos), pos, phys);
+  const int32_t* tab = p.layout_kv == DSA_LAYOUT_PA_BSND ? p.block_table + (int64_t)ri.b * p.max_blocks : nullptr;
+  return sfa_resolve_id(p, ri, sfa_load_id(p, idx_row, pos), pos, phys, tab);
 }
 
 }  // namespace dsa

@@ -204,14 +204,34 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   if (q_early) load_q();
 
   // ---- compact attended positions into s_list (stable order) ----
+  // The first round's index entries are loaded first.  A PA_BSND row's
+  // block table is then staged in the unused tail of s_list (loaded while
+  // the index loads are in flight), so that resolving a page costs an LDS
+  // read instead of a second dependent global load.  Only the waves that
+  // resolve positions load it: the others have their Q loads in flight,
+  // ahead of anything they would issue now.
+  const int first_id = p0 + tid < p1 ? sfa_load_id(p, idx_row, p0 + tid) : -1;
+  const int32_t* tab = nullptr;
+  if (p.layout_kv == DSA_LAYOUT_PA_BSND) {
+    const int32_t* gtab = p.block_table + (int64_t)ri.b * p.max_blocks;
+    tab = gtab;
+    if ((p1 - p0) + p.max_blocks <= kSfaMaxList) {
+      int* s_tab = s_list + (kSfaMaxList + TILE - p.max_blocks);
+      const int nct = min(NTHR, ((p1 - p0 + 63) / 64) * 64);
+      if (tid < nct)
+        for (int i = tid; i < p.max_blocks; i += nct) s_tab[i] = gtab[i];
+      lds_barrier();
+      tab = s_tab;
+    }
+  }
   int n_valid = 0;
   for (int c0 = p0; c0 < p1; c0 += NTHR) {
     int pos = c0 + tid;
     int phys = 0;
     bool valid = false;
     // the index load does not wait for the row's lengths (act_q / act_k)
-    const int id = pos < p1 ? sfa_load_id(p, idx_row, pos) : -1;
-    if (ri.active && pos < p1) valid = sfa_resolve_id(p, ri, id, pos, &phys);
+    const int id = c0 == p0 ? first_id : (pos < p1 ? sfa_load_id(p, idx_row, pos) : -1);
+    if (ri.active && pos < p1) valid = sfa_resolve_id(p, ri, id, pos, &phys, tab);
     unsigned long long m = __ballot(valid);
     if (lane == 0) s_wcnt[wave] = __popcll(m);
     lds_barrier();
