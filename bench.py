@@ -310,6 +310,18 @@ def long_legs(dev, steps):
     ms = time_call(bwd, steps, 1)
     out["sfa_bwd"] = leg("SFA bwd TFLOP/s", "sfa_bwd: BSND B=1, S1=S2=4096, N1=128, D=512+64, topK=2048 "
                          "causal, sparse_mode 3, bf16", 2.0 * N1 * (3 * (D + DR) + 2 * D) * n, ms, n)
+    # the training path (autograd): the shared-latent gradient dk + dv in one output
+    from dsa_triton_ascend_amd.sparse_flash_attention import INT64_MAX
+    from dsa_triton_ascend_amd.sparse_flash_attention_grad import _sfa_grad
+
+    def bwd_merged():
+        return _sfa_grad(q, k, k, si, do, o, smax, ssum, scale, qr, kr, None, None, 1, "BSND", 3, INT64_MAX,
+                         INT64_MAX, False, merge_kv=True)
+    ms = time_call(bwd_merged, steps, 1)
+    out["sfa_bwd_merged"] = leg("SFA bwd TFLOP/s (training path, d_key = dk + dv)",
+                                "sfa_bwd as called by the autograd Function (MLA absorb: one key gradient dk + dv): "
+                                "BSND B=1, S1=S2=4096, N1=128, D=512+64, topK=2048 causal, sparse_mode 3, bf16",
+                                2.0 * N1 * (3 * (D + DR) + 2 * D) * n, ms, n)
     NI, DI = 64, 128
     qi, ki = rn(1, S, NI, DI), rn(1, S, 1, DI)
     w = torch.rand(1, S, NI, generator=g, device=dev)

@@ -394,7 +394,11 @@ __device__ __forceinline__ void bwd_dma16(unsigned lds_base, int voff, __amdgpu_
 }
 __device__ __forceinline__ void bwd_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-template <int D, typename T>
+// MERGE (the shared latent of MLA absorb, value = key[..., :D]): the dV
+// contribution of a token is added to its dK nope columns before the
+// atomics, so each (row, 64 heads, token) adds D + 64 values instead of
+// 2D + 64; dv is not written.
+template <int D, typename T, bool MERGE>
 __global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdParams p) {
   using E = Elem<T>;
   using V8 = typename E::v8;
@@ -409,6 +413,8 @@ __global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdP
   constexpr int NDN = TILE / TPI / kBwdWgWaves;  // nope DMAs per wave per tile
   constexpr int NCOL = 2 * D + DR;           // dK | dK_rope | dV columns
   constexpr int NCW = NCOL / 16 / kBwdWgWaves;   // column tiles per wave
+  constexpr int NNW = D / 16 / kBwdWgWaves;      // MERGE: nope column tiles per wave
+  constexpr int NXB = MERGE ? 2 * NNW + 1 : NCW; // B-operand column tiles per wave
   constexpr int TR = kBwdWgHeads + 8;        // padded [token][head] row
   static_assert(NCOL % (16 * kBwdWgWaves) == 0 && TILE % (TPI * kBwdWgWaves) == 0, "layout");
 
@@ -459,12 +465,20 @@ __global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdP
   } else {
     delta = 0.f;
   }
-  // B operands of the 64-head sums: column c = 16*(wave*NCW + i) + li of
-  // [Q nope | Q rope | dO], heads hbase + 32*ks + 8*lg + j
-  V8 xb[NCW][2];
+  // B operands of the 64-head sums: column c of [Q nope | Q rope | dO],
+  // heads hbase + 32*ks + 8*lg + j.  Tile i is column 16*(wave*NCW + i) + li;
+  // with MERGE, tiles i < NNW are Q nope columns 16*(wave*NNW + i) + li,
+  // tiles NNW + i the dO columns of the same index, and tile 2*NNW the Q
+  // rope columns 16*wave + li.
+  V8 xb[NXB][2];
 #pragma unroll
-  for (int i = 0; i < NCW; ++i) {
-    const int c = 16 * (wave * NCW + i) + li;
+  for (int i = 0; i < NXB; ++i) {
+    int c = 16 * (wave * NCW + i) + li;
+    if (MERGE) {
+      if (i < NNW) c = 16 * (wave * NNW + i) + li;
+      else if (i < 2 * NNW) c = D + DR + 16 * (wave * NNW + i - NNW) + li;
+      else c = D + 16 * wave + li;
+    }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -621,6 +635,35 @@ __global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdP
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) ph[tt][r] = s_list[t * TILE + tt * 16 + lg * 4 + r];
+      if (MERGE) {
+        // nope columns: dS^T.Q + P^T.dO in one accumulator; rope: dS^T.Q_rope
+#pragma unroll
+        for (int i = 0; i <= NNW; ++i) {
+          const bool rope = i == NNW;
+          const int c = rope ? 16 * wave + li : 16 * (wave * NNW + i) + li;
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+              const V8 ads = as_v8<V8>(*(const u32x4*)&s_t[0][tt * 16 + li][ks * 32 + lg * 8]);
+              acc = E::mfma(ads, xb[rope ? 2 * NNW : i][ks], acc);
+              if (!rope) {
+                const V8 ap = as_v8<V8>(*(const u32x4*)&s_t[1][tt * 16 + li][ks * 32 + lg * 8]);
+                acc = E::mfma(ap, xb[NNW + (rope ? 0 : i)][ks], acc);
+              }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int pr = ph[tt][r];
+              if (pr < 0) continue;
+              if (rope) atomicAdd(p.dkr + (int64_t)pr * DR + c, acc[r]);
+              else atomicAdd(p.dk + (int64_t)pr * D + c, acc[r]);
+            }
+          }
+        }
+        continue;
+      }
 #pragma unroll
       for (int i = 0; i < NCW; ++i) {
         const int ct = wave * NCW + i;
@@ -669,6 +712,11 @@ __global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdP
   }
 }
 
+__global__ __launch_bounds__(256) void bwd_fill_kernel(uint32_t* a, int64_t n, uint32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) a[i] = v;
+}
+
 // fp32 workspace -> output dtype
 template <typename T>
 __global__ __launch_bounds__(256) void cast_f32_kernel(const float* src, T* dst, int64_t n) {
@@ -692,11 +740,20 @@ size_t sfa_bwd_workspace_bytes(int64_t kv_rows, int64_t d) {
 
 // The workgroup kernel gathers with buffer loads (32-bit offsets): key
 // tensors of 2 GiB and more take the one-wave kernel.
+// The workgroup kernel (merged when `merge`) or, for key tensors of 2 GiB
+// and more, the one-wave kernel (never merged).  Returns whether the dK
+// workspace already holds dk + dv.
 template <int D, typename T>
-static hipError_t launch_sfa_bwd(const SfaBwdParams& p, hipStream_t stream) {
+static hipError_t launch_sfa_bwd(const SfaBwdParams& p, bool merge, bool* merged, hipStream_t stream) {
+  *merged = false;
   if ((int64_t)p.kv_rows * D * 2 < (1ll << 31)) {
-    hipLaunchKernelGGL((sfa_bwd_wg_kernel<D, T>), dim3((unsigned)p.rows, (unsigned)((p.n1 + kBwdWgHeads - 1) / kBwdWgHeads)),
-                       dim3(kBwdWgWaves * 64), 0, stream, p);
+    const dim3 grid((unsigned)p.rows, (unsigned)((p.n1 + kBwdWgHeads - 1) / kBwdWgHeads));
+    if (merge) {
+      hipLaunchKernelGGL((sfa_bwd_wg_kernel<D, T, true>), grid, dim3(kBwdWgWaves * 64), 0, stream, p);
+      *merged = true;
+    } else {
+      hipLaunchKernelGGL((sfa_bwd_wg_kernel<D, T, false>), grid, dim3(kBwdWgWaves * 64), 0, stream, p);
+    }
   } else {
     hipLaunchKernelGGL((sfa_bwd_kernel<D, T>), dim3((unsigned)p.rows, (unsigned)((p.n1 + 15) / 16)), dim3(64), 0,
                        stream, p);
@@ -776,13 +833,23 @@ int sfa_bwd_run(const void* query, const void* query_rope, const void* key, cons
   p.page_size = 1;
   p.scale = scale_value;
   p.scale_log2 = scale_value * kLog2e;
-  DSA_HIP(hipMemsetAsync(workspace, 0, sfa_bwd_workspace_bytes(kv_rows, d), stream));
+  // the fp32 accumulators start at zero (a fill kernel: no memset node when
+  // the caller captures the call in a graph)
+  const int64_t nacc = (int64_t)(sfa_bwd_workspace_bytes(kv_rows, d) / 4);
+  hipLaunchKernelGGL(bwd_fill_kernel, dim3((unsigned)((nacc + 255) / 256)), dim3(256), 0, stream, (uint32_t*)workspace,
+                     nacc, 0u);
+  DSA_HIP(hipGetLastError());
+  bool merged = false;
   if (q_rows > 0) {
     hipError_t e;
     const bool bf = dtype == DSA_DTYPE_BF16;
-    if (d == 128) e = bf ? launch_sfa_bwd<128, bf16>(p, stream) : launch_sfa_bwd<128, f16>(p, stream);
-    else if (d == 256) e = bf ? launch_sfa_bwd<256, bf16>(p, stream) : launch_sfa_bwd<256, f16>(p, stream);
-    else e = bf ? launch_sfa_bwd<512, bf16>(p, stream) : launch_sfa_bwd<512, f16>(p, stream);
+    const bool merge = d_value == nullptr;
+    if (d == 128) e = bf ? launch_sfa_bwd<128, bf16>(p, merge, &merged, stream)
+                         : launch_sfa_bwd<128, f16>(p, merge, &merged, stream);
+    else if (d == 256) e = bf ? launch_sfa_bwd<256, bf16>(p, merge, &merged, stream)
+                              : launch_sfa_bwd<256, f16>(p, merge, &merged, stream);
+    else e = bf ? launch_sfa_bwd<512, bf16>(p, merge, &merged, stream)
+                : launch_sfa_bwd<512, f16>(p, merge, &merged, stream);
     DSA_HIP(e);
   }
   const bool bf = dtype == DSA_DTYPE_BF16;
@@ -792,6 +859,8 @@ int sfa_bwd_run(const void* query, const void* query_rope, const void* key, cons
   if (d_value) {
     DSA_HIP(cast(p.dk, d_key, kv_rows * d));
     DSA_HIP(cast(p.dv, d_value, kv_rows * d));
+  } else if (merged) {
+    DSA_HIP(cast(p.dk, d_key, kv_rows * d));  // dk already holds dk + dv
   } else {
     // shared latent: d_key = dk + dv
     DSA_HIP(bf ? launch_cast_sum<bf16>(p.dk, p.dv, d_key, kv_rows * d, stream)
