@@ -700,9 +700,9 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
 // r_i, and its exact max t_i (log2 units); the merged output is
 // sum_i w_i O_i / l_i / sum_i w_i with w_i = 2^(r_i - M) l_i.
 // Lane s reads the record of split s, the weights are formed on the lanes
-// and broadcast with readlane, and each lane then reads its D/64 columns of
-// up to eight splits before using any of them, so a wave waits for about
-// two memory round trips instead of two per split.
+// and broadcast with readlane, and each lane reads its D/64 columns of the
+// splits.  With at most eight splits (every decode launch) all loads go out
+// together; above that, the columns of eight splits at a time.
 template <int D, typename T>
 __global__ __launch_bounds__(256) void sfa_combine_kernel(SfaFwdParams p) {
   using E = Elem<T>;
@@ -712,6 +712,46 @@ __global__ __launch_bounds__(256) void sfa_combine_kernel(SfaFwdParams p) {
   const int64_t rh = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (rh >= p.rows * p.n1) return;
   const int64_t sstride = p.rows * p.n1;  // (row, head) records per split
+  if (p.splits <= 8) {
+    // every load up front (lane s < splits: the record of split s; all
+    // lanes: their columns of every split), so the wave waits for one
+    // memory round trip
+    f32x4 ml = {-INFINITY, 0.f, -INFINITY, 0.f};
+    if (lane < p.splits) ml = *(const f32x4*)(p.part_ml + ((int64_t)lane * sstride + rh) * 4);
+    hvec v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (u < p.splits) v[u] = *(const hvec*)(p.part_o + ((int64_t)u * sstride + rh) * D + lane * PER);
+    const bool has = ml[1] > 0.f;
+    const float mref8 = wave_max(has ? ml[0] : -INFINITY);
+    const float mtrue8 = wave_max(has ? ml[2] : -INFINITY);
+    float acc8[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) acc8[e] = 0.f;
+    float L8 = 0.f;
+    if (mref8 != -INFINITY) {
+      const float w = has ? fast_exp2(ml[0] - mref8) * ml[1] : 0.f;
+      const float wsc = w * ml[3];
+      L8 = wave_sum(w);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (u >= p.splits) break;
+        const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wsc), u));
+        if (wu == 0.f) continue;  // split without attended tokens
+#pragma unroll
+        for (int e = 0; e < PER; ++e) acc8[e] += wu * (float)v[u][e];
+      }
+    }
+    const float inv8 = L8 > 0.f ? 1.f / L8 : 0.f;
+    T* op8 = (T*)p.out + rh * D + lane * PER;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) op8[j] = E::from_f32(acc8[j] * inv8);
+    if (p.return_lse && lane == 0) {
+      p.smax[rh] = L8 > 0.f ? mtrue8 * kLn2 : 0.f;
+      p.ssum[rh] = L8 > 0.f ? L8 * fast_exp2(mref8 - mtrue8) : 0.f;
+    }
+    return;
+  }
   float mref = -INFINITY, mtrue = -INFINITY;
   for (int s = lane; s < p.splits; s += 64) {
     const f32x4 ml = *(const f32x4*)(p.part_ml + ((int64_t)s * sstride + rh) * 4);
