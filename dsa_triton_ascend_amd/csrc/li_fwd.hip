@@ -812,23 +812,15 @@ __global__ __launch_bounds__(kTopkThreads) void li_topk_kernel(TopkParams p) {
     }
 
     // ---- 3. counting sort of the candidates by bin ----
-    // compact them (block scan of per-thread counts) into outb, then each
-    // takes a slot of its bin's range in cand
-    unsigned cmask = 0u;
+    // each candidate takes a slot of its bin's range in cand from the bin's
+    // cursor (the order inside a bin is arbitrary: step 4 ranks by key)
 #pragma unroll
-    for (int u = 0; u < kFastKpt; ++u)
-      cmask |= (kr[u] > kNegInfKey && digit(kr[u]) >= bstar) ? (1u << u) : 0u;
-    unsigned off[4] = {(unsigned)__popc(cmask), 0u, 0u, 0u};
-    block_scan4(off, wsum);
-    unsigned o = off[0];
-#pragma unroll
-    for (int u = 0; u < kFastKpt; ++u)
-      if ((cmask >> u) & 1u) outb[o++] = ((unsigned long long)(~kr[u]) << 32) | (unsigned)entry(u);
-    __syncthreads();
-    for (int q = tid; q < ncand; q += kTopkThreads) {
-      const unsigned long long cv = outb[q];
-      const unsigned slot = atomicAdd(&cursor[digit(~(unsigned)(cv >> 32))], 1u);
-      cand[slot] = cv;
+    for (int u = 0; u < kFastKpt; ++u) {
+      const unsigned d = digit(kr[u]);
+      if (kr[u] > kNegInfKey && d >= bstar) {
+        const unsigned slot = atomicAdd(&cursor[d], 1u);
+        cand[slot] = ((unsigned long long)(~kr[u]) << 32) | (unsigned)entry(u);
+      }
     }
     __syncthreads();
 
