@@ -351,3 +351,58 @@ def test_fwd_token_split_paged_decode():
     assert_close(out.float().cpu().numpy(), ref[0], RTOL, ATOL, "out")
     assert_close(smax.cpu().numpy(), ref[1], RTOL, ATOL, "smax")
     assert_close(ssum.cpu().numpy(), ref[2], RTOL, ATOL, "ssum")
+
+
+@pytest.mark.parametrize("combo", ["TND+PA_BSND", "TND+BSND", "BSND+TND"])
+def test_fwd_mixed_layouts(combo):
+    """Query and key layouts chosen independently, as the reference allows
+    (sparse_flash_attention_triton.py:540-597): a packed query over a paged
+    cache (chunked prefill on a paged KV cache), a packed query over a dense
+    per-batch key, and a dense query over a packed key."""
+    print(f"[sfa_fwd] mixed layouts {combo}", flush=True)
+    dsa = _api()
+    dtype = torch.bfloat16
+    lq_name, lk_name = combo.split("+")
+    N1, D, K, page = 32, 512, 40, 32
+    lens_q, lens_k = [5, 3], [200, 150]
+    B = 2
+    S1, S2 = max(lens_q), 224
+    q, k, qr, kr = sfa_inputs(B, S1, S2, N1, D, dtype, seed=21)
+    si = sparse_indices(B, S1, S2, K, 1, 3, lens_q, lens_k, seed=22)
+    rng = np.random.RandomState(23)
+    scale = 1.0 / np.sqrt(D + 64)
+    cq = np.cumsum(lens_q).tolist()
+    ck = np.cumsum(lens_k).tolist()
+    # query side
+    if lq_name == "TND":
+        qa = np.concatenate([q[b, :lens_q[b]] for b in range(B)])
+        qra = np.concatenate([qr[b, :lens_q[b]] for b in range(B)])
+        sia = np.concatenate([si[b, :lens_q[b]] for b in range(B)])
+        act_q = cq
+    else:
+        qa, qra, sia, act_q = q, qr, si, lens_q
+    # key side
+    bt = None
+    if lk_name == "PA_BSND":
+        ka, kra, bt = _paged(k, kr, page, rng)
+        act_k = lens_k
+    elif lk_name == "TND":
+        ka = np.concatenate([k[b, :lens_k[b]] for b in range(B)])
+        kra = np.concatenate([kr[b, :lens_k[b]] for b in range(B)])
+        act_k = ck
+    else:
+        ka, kra, act_k = k, kr, lens_k
+    kw = dict(scale_value=scale, actual_seq_lengths_query=act_q, actual_seq_lengths_kv=act_k,
+              layout_query=lq_name, layout_kv=lk_name, sparse_mode=3, return_softmax_lse=True)
+    out, smax, ssum = dsa.sparse_flash_attention_triton(
+        dev(qa, dtype), dev(ka, dtype), None, dev(sia, torch.int32), query_rope=dev(qra, dtype),
+        key_rope=dev(kra, dtype), block_table=None if bt is None else dev(bt, torch.int32),
+        **({"block_size": page} if bt is not None else {}), **kw)
+    kf = dev(ka, dtype).float().cpu().numpy()
+    krf = dev(kra, dtype).float().cpu().numpy()
+    ref = sparse_flash_attention(qa, kf, sia, scale, qra, krf, block_table=bt, actual_seq_lengths_query=act_q,
+                                 actual_seq_lengths_kv=act_k, layout_query=lq_name, layout_kv=lk_name,
+                                 sparse_mode=3, return_softmax_lse=True, dtype="float32")
+    assert_close(out.float().cpu().numpy(), ref[0], RTOL, ATOL, f"{combo} out")
+    assert_close(smax.cpu().numpy(), ref[1], RTOL, ATOL, f"{combo} smax")
+    assert_close(ssum.cpu().numpy(), ref[2], RTOL, ATOL, f"{combo} ssum")
