@@ -353,6 +353,46 @@ def test_fwd_token_split_paged_decode():
     assert_close(ssum.cpu().numpy(), ref[2], RTOL, ATOL, "ssum")
 
 
+def test_fwd_split_shapes_in_sequence():
+    """Split launches of different shapes one after another (workspaces
+    reused by the caching allocator hold the previous shape's partials).
+    The 8192-position row runs 32 splits: the merge path for more than
+    eight splits."""
+    seq = [(1, 2, 4096, 128, 2048, 0, 512), (2, 1, 2048, 16, 1024, 0, 512),
+           (1, 1, 8192, 128, 8192, 0, 512), (1, 4, 600, 64, 600, 3, 512),
+           (1, 2, 4096, 128, 2048, 0, 512), (1, 3, 1024, 32, 1000, 3, 256)]
+    dtype = torch.bfloat16
+    for i, (B, S1, S2, N1, K, mode, D) in enumerate(seq):
+        print(f"[sfa_fwd split sequence] step {i}: B={B} S1={S1} S2={S2} N1={N1} K={K} D={D}", flush=True)
+        q, k, qr, kr = sfa_inputs(B, S1, S2, N1, D, dtype, seed=70 + i)
+        si = sparse_indices(B, S1, S2, K, 1, mode, seed=80 + i)
+        scale = 1.0 / np.sqrt(D + 64)
+        out, smax, ssum = _run(q, k, qr, kr, si, dtype, scale, mode)
+        ref = sfa_fwd_bsnd(q, k, si, qr, kr, scale, [S1] * B, [S2] * B, 1, mode, True, "float32",
+                           positions="kernel")
+        assert_close(out, ref[0], RTOL, ATOL, "attention_out")
+        assert_close(smax, ref[1], RTOL, ATOL, "softmax_max")
+        assert_close(ssum, ref[2], RTOL, ATOL, "softmax_sum")
+
+
+def test_fwd_forced_split_many_rows():
+    """Index lists longer than one workgroup's list (2048 positions) force a
+    token split even when the rows fill the CUs."""
+    print("[sfa_fwd split] forced split, 1100 rows", flush=True)
+    dtype = torch.bfloat16
+    B, S1, S2, N1, K, D = 1, 1100, 4096, 1, 4096, 128
+    q, k, qr, kr = sfa_inputs(B, S1, S2, N1, D, dtype, seed=91)
+    si = sparse_indices(B, S1, S2, K, 1, 0, seed=92)
+    si[0, 7, 0, 3000:] = -1
+    scale = 1.0 / np.sqrt(D + 64)
+    out, smax, ssum = _run(q, k, qr, kr, si, dtype, scale, 0)
+    ref = sfa_fwd_bsnd(q, k, si, qr, kr, scale, [S1] * B, [S2] * B, 1, 0, True, "float32",
+                       positions="kernel")
+    assert_close(out, ref[0], RTOL, ATOL, "attention_out")
+    assert_close(smax, ref[1], RTOL, ATOL, "softmax_max")
+    assert_close(ssum, ref[2], RTOL, ATOL, "softmax_sum")
+
+
 @pytest.mark.parametrize("combo", ["TND+PA_BSND", "TND+BSND", "BSND+TND"])
 def test_fwd_mixed_layouts(combo):
     """Query and key layouts chosen independently, as the reference allows
