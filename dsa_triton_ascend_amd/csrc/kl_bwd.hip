@@ -16,8 +16,9 @@
 //
 // Design:
 //  * kl_bwd_row_kernel: one workgroup of 8 waves per query row.  Pass A
-//    streams tiles of 32 slots (K, K_rope, K_index rows gathered into LDS,
-//    the next tile's loads in flight during the current tile's MFMAs): each
+//    streams tiles of 32 slots (K, K_rope, K_index rows gathered straight
+//    into an LDS ring by LDS-DMA, the next tile's gather in flight during
+//    the current tile's MFMAs): each
 //    wave scores 16 heads of the teacher on MFMA (Q fragments resident in
 //    registers) and sums its heads' probabilities across lanes; waves 0-3
 //    score 16 index heads each.  I and p of the row stay in LDS.  Pass B is
@@ -52,6 +53,7 @@ struct KlMap {
 
 struct KlParams {
   KlMap m;
+  int32_t ring;  // pass A tile buffers in LDS (1 or 2)
   const void* q;
   const void* qr;
   const void* k;
@@ -140,6 +142,23 @@ __device__ __forceinline__ int kl_token(const KlMap& m, const KlRow& r, const in
   return (blk < 0 || phys >= m.kv_rows) ? -1 : (int)phys;
 }
 
+// Zero source row of the pass-A gather (slots past the row's end and
+// tokens of -1 pages).
+__device__ __attribute__((aligned(16))) unsigned char g_kl_zero_row[1024];
+
+// One 16-byte-per-lane DMA from global memory straight into LDS: lane L's
+// 16 bytes land at lds_base + 16*L (LDS address taken from M0).  Inline
+// asm, so that the compiler does not drain the DMAs before every LDS read;
+// the loop waits for them with an explicit vmcnt.
+__device__ __forceinline__ void kl_dma16(unsigned lds_base, const void* gaddr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(gaddr) : "memory");
+}
+
+// Bytes of one pass-A tile buffer: K, K_rope and K_index rows of 32 slots.
+template <int D, int DR>
+constexpr int kl_tile_bytes() { return kKlTile * (D * 2 + DR * 2 + kKlDi * 2); }
+
 template <int D, int DR, typename T>
 __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p) {
   using E = Elem<T>;
@@ -151,24 +170,31 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   constexpr int ROW = D * 2;            // K row bytes in LDS
   constexpr int IROW = DI * 2;          // K_index row bytes
   constexpr int CN = D / 8, CR = DR / 8, CI = DI / 8;  // 16-byte chunks per row
-  // gather assignment per tile: K chunks NJ_N per thread; the 256 rope
-  // chunks on threads 0-255; one K_index chunk per thread
-  constexpr int NJ_N = TILE * CN / NT;
-  static_assert(TILE * CN == NJ_N * NT && TILE * CI == NT && TILE * CR <= NT, "gather assignment");
+  // pass-A gather: every DMA moves 1 KB (64 lanes x 16 bytes) = TPK K rows,
+  // 8 rope rows or TPI K_index rows
+  constexpr int TPK = 64 / CN, TPI = 64 / CI;
+  constexpr int KD = TILE / TPK, RD = DR > 0 ? TILE / 8 : 0, ID = TILE / TPI;
+  static_assert(TPK * CN == 64 && TPI * CI == 64 && (DR == 0 || CR == 8), "gather assignment");
+  // pass-C gather: one K_index chunk per thread
+  static_assert(TILE * CI == NT, "pass C gather");
+  constexpr int BUF_K = TILE * ROW, BUF_R = TILE * DR * 2;
+  constexpr int BUF = kl_tile_bytes<D, DR>();
   constexpr bool kF16 = __is_same(T, f16);
 
-  __shared__ __attribute__((aligned(16))) unsigned char s_k[TILE * ROW];
-  __shared__ __attribute__((aligned(16))) unsigned char s_kr[DR > 0 ? TILE * DR * 2 : 16];
-  __shared__ __attribute__((aligned(16))) unsigned char s_ki[TILE * IROW];
-  __shared__ __attribute__((aligned(16))) float s_red[kKlWaves][TILE];
-  __shared__ __attribute__((aligned(16))) float s_redi[4][TILE];
+  // per-wave partial sums of a pass-A tile, double-buffered by tile parity
+  __shared__ __attribute__((aligned(16))) float s_red[2][kKlWaves][TILE];
+  __shared__ __attribute__((aligned(16))) float s_redi[2][4][TILE];
   __shared__ __attribute__((aligned(16))) T s_ds[2][TILE][kKlDsRow];  // dS^T hi / lo: [slot][g]
   __shared__ float s_misc[2 * kKlWaves + 4];
-  // dynamic: I (then dI) and p of the row, and its clamped token rows
-  extern __shared__ float s_dyn[];
-  float* s_I = s_dyn;
-  float* s_p = s_dyn + p.topk;
-  int* s_tok = (int*)(s_dyn + 2 * p.topk);
+  // dynamic: the pass-A tile ring (p.ring buffers of BUF bytes), then I
+  // (then dI) and p of the row, and its clamped token rows
+  extern __shared__ __attribute__((aligned(16))) unsigned char s_dynb[];
+  unsigned char* const ring = s_dynb;
+  float* s_I = (float*)(s_dynb + p.ring * BUF);
+  float* s_p = s_I + p.topk;
+  int* s_tok = (int*)(s_p + p.topk);
+  // pass C stages K_index tiles in buffer 0's index rows
+  unsigned char* const s_ki = ring + BUF_K + BUF_R;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -213,23 +239,28 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     m2r[r] = v ? p.smax[hr] * kLog2e : 0.f;
     invr[r] = v ? 1.f / (p.ssum[hr] + 1e-8f) : 0.f;  // 0 also masks heads >= N1
   }
-  // index heads: waves 0-3, g = 16*wave + li
-  const bool iwave = wave < 4 && wave * 16 < p.nidx;
-  const int g = wave * 16 + li;
-  const bool gv = iwave && g < p.nidx;
-  const int64_t grow = (int64_t)row * p.nidx + (gv ? g : 0);
+  // index heads 16*hg4 .. +15 (hg4 = wave mod 4), g = 16*hg4 + li.  Pass A
+  // scores them on waves w and w + 4, slots 0-15 and 16-31 of the tile;
+  // pass C runs them on waves 0-3 (iwave).
+  const int hg4 = wave & 3;
+  const bool ihg = hg4 * 16 < p.nidx;
+  const bool iwave = wave < 4 && ihg;
+  const int g = hg4 * 16 + li;
+  const bool gva = ihg && g < p.nidx;
+  const bool gv = iwave && gva;
+  const int64_t grow = (int64_t)row * p.nidx + (gva ? g : 0);
   V8 qif[DI / 32];
 #pragma unroll
   for (int ks = 0; ks < DI / 32; ++ks) {
     const u32x4 v = *(const u32x4*)((const T*)p.qi + grow * DI + ks * 32 + lg * 8);
-    qif[ks] = as_v8<V8>(gv ? v : z4);
+    qif[ks] = as_v8<V8>(gva ? v : z4);
   }
   const float wg = gv ? load_w(p.w, grow, p.w_dtype) : 0.f;
-  float wr[4];  // weights of index heads 16*wave + 4*lg + r (pass A layout)
+  float wr[4];  // weights of index heads 16*hg4 + 4*lg + r (pass A layout)
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int gg = wave * 16 + lg * 4 + r;
-    wr[r] = (iwave && gg < p.nidx) ? load_w(p.w, (int64_t)row * p.nidx + gg, p.w_dtype) : 0.f;
+    const int gg = hg4 * 16 + lg * 4 + r;
+    wr[r] = (ihg && gg < p.nidx) ? load_w(p.w, (int64_t)row * p.nidx + gg, p.w_dtype) : 0.f;
   }
   // B operand of c = dS^T . Qi for this wave's 16 columns: Qi[g 32*ks + 8*lg + j][16*wave + li]
   V8 qib[kKlMaxNidx / 32];
@@ -245,8 +276,8 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   }
   for (int e = tid; e < 2 * TILE * kKlDsRow; e += NT) (&s_ds[0][0][0])[e] = E::from_f32(0.f);
   // per-wave partial sums of a tile; waves without heads keep zeros
-  for (int e = tid; e < kKlWaves * TILE; e += NT) (&s_red[0][0])[e] = 0.f;
-  for (int e = tid; e < 4 * TILE; e += NT) (&s_redi[0][0])[e] = 0.f;
+  for (int e = tid; e < 2 * kKlWaves * TILE; e += NT) (&s_red[0][0][0])[e] = 0.f;
+  for (int e = tid; e < 2 * 4 * TILE; e += NT) (&s_redi[0][0][0])[e] = 0.f;
 
   const unsigned char* kb = (const unsigned char*)p.k;
   const unsigned char* krb = (const unsigned char*)p.kr;
@@ -256,53 +287,93 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   for (int k = tid; k < n; k += NT) s_tok[k] = kl_token(p.m, ri, p.idx, row, k);
   __syncthreads();
 
-  // per tile: K rows (NJ_N chunks per thread), rope rows (threads < 256),
-  // K_index rows (one chunk per thread); slots >= n and tokens of -1 pages
-  // read as zeros
   auto slot_tok = [&](int k) { return k < n ? s_tok[k] : -1; };
-  u32x4 pre_n[NJ_N], pre_r, pre_i;
-  auto load_a = [&](int t) {
+  // Tile t into ring buffer b: wave w issues K DMAs w, w+8, ..., rope DMA w
+  // (w < RD) and K_index DMA w.  A lane's 16 bytes land at its fixed slot
+  // of the buffer; it loads the source chunk that the XOR swizzle puts
+  // there (LDS chunk c of a row holds source chunk c ^ swz), so reads use
+  // the same addressing as a swizzled store would.
+  // The token ids of a tile are read from LDS first: the DMA asm is a
+  // compiler memory barrier, so a read placed between two DMAs would wait
+  // for its own LDS round trip.
+  constexpr int NKW = (KD + kKlWaves - 1) / kKlWaves, NIW = (ID + kKlWaves - 1) / kKlWaves;
+  auto issue_a = [&](int t, int b) {
+    const unsigned base = (unsigned)(uintptr_t)(ring + b * BUF);
+    int tk_k[NKW], tok_k[NKW], tk_i[NIW], tok_i[NIW], tk_r = 0, tok_r = -1;
 #pragma unroll
-    for (int j = 0; j < NJ_N; ++j) {
-      const int e = tid + j * NT;
-      const int tk = e / CN, ch = e - tk * CN;
-      const int tok = slot_tok(t * TILE + tk);
-      pre_n[j] = tok >= 0 ? *(const u32x4*)(kb + (int64_t)tok * ROW + ch * 16) : z4;
+    for (int u = 0; u < NKW; ++u) {
+      const int j = u * kKlWaves + wave;
+      tk_k[u] = j * TPK + lane / CN;
+      tok_k[u] = (KD % kKlWaves == 0 || j < KD) ? slot_tok(t * TILE + tk_k[u]) : -1;
     }
-    if (DR > 0) {
-      const int tk = tid / (CR > 0 ? CR : 1), ch = tid - tk * CR;
-      const int tok = tid < TILE * CR ? slot_tok(t * TILE + tk) : -1;
-      pre_r = tok >= 0 ? *(const u32x4*)(krb + (int64_t)tok * (DR * 2) + ch * 16) : z4;
+    if (DR > 0 && wave < RD) {
+      tk_r = wave * 8 + (lane >> 3);
+      tok_r = slot_tok(t * TILE + tk_r);
     }
-    {
-      const int tk = tid / CI, ch = tid - tk * CI;
-      const int tok = slot_tok(t * TILE + tk);
-      pre_i = tok >= 0 ? *(const u32x4*)(kib + (int64_t)tok * IROW + ch * 16) : z4;
-    }
-  };
-  auto store_a = [&]() {
 #pragma unroll
-    for (int j = 0; j < NJ_N; ++j) {
-      const int e = tid + j * NT;
-      const int tk = e / CN, ch = e - tk * CN;
-      *(u32x4*)(s_k + tk * ROW + ((ch ^ nope_swz(tk)) * 16)) = pre_n[j];
+    for (int u = 0; u < NIW; ++u) {
+      const int j = u * kKlWaves + wave;
+      tk_i[u] = j * TPI + lane / CI;
+      tok_i[u] = (ID % kKlWaves == 0 || j < ID) ? slot_tok(t * TILE + tk_i[u]) : -1;
     }
-    if (DR > 0 && tid < TILE * CR) {
-      const int tk = tid / (CR > 0 ? CR : 1), ch = tid - tk * CR;
-      *(u32x4*)(s_kr + tk * (DR * 2) + ((ch ^ rope_swz(tk)) * 16)) = pre_r;
+#pragma unroll
+    for (int u = 0; u < NKW; ++u) {
+      const int j = u * kKlWaves + wave;
+      if (KD % kKlWaves == 0 || j < KD) {
+        const int ch = (lane % CN) ^ nope_swz(tk_k[u]);
+        kl_dma16(base + j * 1024, tok_k[u] >= 0 ? (const void*)(kb + (int64_t)tok_k[u] * ROW + ch * 16)
+                                                : (const void*)(g_kl_zero_row + ch * 16));
+      }
     }
-    {
-      const int tk = tid / CI, ch = tid - tk * CI;
-      *(u32x4*)(s_ki + tk * IROW + ((ch ^ nope_swz(tk)) * 16)) = pre_i;
+    if (DR > 0 && wave < RD) {
+      const int ch = (lane & 7) ^ rope_swz(tk_r);
+      kl_dma16(base + BUF_K + wave * 1024, tok_r >= 0 ? (const void*)(krb + (int64_t)tok_r * (DR * 2) + ch * 16)
+                                                      : (const void*)(g_kl_zero_row + ch * 16));
+    }
+#pragma unroll
+    for (int u = 0; u < NIW; ++u) {
+      const int j = u * kKlWaves + wave;
+      if (ID % kKlWaves == 0 || j < ID) {
+        const int ch = (lane % CI) ^ nope_swz(tk_i[u]);
+        kl_dma16(base + BUF_K + BUF_R + j * 1024,
+                 tok_i[u] >= 0 ? (const void*)(kib + (int64_t)tok_i[u] * IROW + ch * 16)
+                               : (const void*)(g_kl_zero_row + ch * 16));
+      }
     }
   };
 
-  load_a(0);
+  // One barrier per tile.  With two buffers, tile t+1 is issued right
+  // after tile t's barrier into the buffer tile t-1 used (every wave is past
+  // it); with one, after a second barrier behind the tile's MFMAs.  The loop
+  // has no other global memory traffic, so vmcnt(0) waits for exactly this
+  // wave's share of the tile.  The per-slot sums of tile t-1 (complete at
+  // tile t's barrier) are reduced by wave 0 while the others start tile t;
+  // the partial-sum buffers alternate, and wave 0 has reduced tile t-2 from
+  // a buffer before any wave passes tile t's barrier to overwrite it.
+  auto reduce_a = [&](int t) {
+    if (tid < TILE) {
+      const int k = t * TILE + tid;
+      if (k < n) {
+        float ps = 0.f, is = 0.f;
+#pragma unroll
+        for (int w2 = 0; w2 < kKlWaves; ++w2) ps += s_red[t & 1][w2][tid];
+#pragma unroll
+        for (int w2 = 0; w2 < 4; ++w2) is += s_redi[t & 1][w2][tid];
+        s_p[k] = ps * (1.f / (float)p.n1);
+        s_I[k] = is;
+      }
+    }
+  };
+  issue_a(0, 0);
   for (int t = 0; t < nt; ++t) {
+    const int b = p.ring == 2 ? (t & 1) : 0;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
-    store_a();
-    lds_barrier();
-    if (t + 1 < nt) load_a(t + 1);
+    if (p.ring == 2 && t + 1 < nt) issue_a(t + 1, b ^ 1);
+    if (t > 0) reduce_a(t - 1);
+    const unsigned char* s_k = ring + b * BUF;
+    const unsigned char* s_kr = s_k + BUF_K;
+    const unsigned char* s_kia = s_k + BUF_K + BUF_R;
 
     // Scores as S[head][slot] = Q . K^T (heads on MFMA rows, C register r =
     // head 4*lg + r, column = slot li).  That C layout is the A layout of
@@ -312,16 +383,28 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     // cross-lane traffic).
     if (wave_heads) {
       f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+      // K fragments of step st = 2*ks + tt, read PF steps ahead of their
+      // MFMA; the scheduling barrier after each MFMA keeps the reads where
+      // they are (sunk next to their MFMAs, every MFMA would wait out a full
+      // LDS round trip)
+      constexpr int NS = 2 * KS, PF = 6;
+      auto a_read = [&](int st) -> u32x4 {
+        const int ks = st >> 1, tk = (st & 1) * 16 + li;
+        const unsigned char* a =
+            ks < KSN ? s_k + tk * ROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16)
+                     : s_kr + tk * (DR * 2) + ((((ks - KSN) * 4 + lg) ^ rope_swz(tk)) * 16);
+        return *(const u32x4*)a;
+      };
+      u32x4 fa[PF];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
+      for (int i = 0; i < PF; ++i) fa[i] = a_read(i);
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const int tk = tt * 16 + li;
-          const unsigned char* a =
-              ks < KSN ? s_k + tk * ROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16)
-                       : s_kr + tk * (DR * 2) + ((((ks - KSN) * 4 + lg) ^ rope_swz(tk)) * 16);
-          acc[tt] = E::mfma(qf[ks], as_v8<V8>(*(const u32x4*)a), acc[tt]);
-        }
+      for (int st = 0; st < NS; ++st) {
+        const V8 av = as_v8<V8>(fa[st % PF]);
+        if (st + PF < NS) fa[st % PF] = a_read(st + PF);
+        acc[st & 1] = E::mfma(qf[st >> 1], av, acc[st & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         Split3 sp;
@@ -329,43 +412,33 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
         for (int r = 0; r < 4; ++r) split3_set(sp, r, fast_exp2(acc[tt][r] * p.scale_log2 - m2r[r]) * invr[r]);
         // sum[r] = sum over the wave's heads for slot tt*16 + 4*lg + r
         const f32x4 sum = split3_rowsum(sp);
-        if (li == 0) *(f32x4*)&s_red[wave][tt * 16 + lg * 4] = sum;
+        if (li == 0) *(f32x4*)&s_red[t & 1][wave][tt * 16 + lg * 4] = sum;
       }
     }
-    // index scores I[slot] = sum_g w_g ReLU(qi_g . ki): waves 0-3, 16 index heads each
-    if (iwave) {
-      f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    // index scores I[slot] = sum_g w_g ReLU(qi_g . ki): index heads 16*hg4
+    // .. +15 for slots 16*tt .. +15 of the tile, tt = wave / 4
+    if (ihg) {
+      const int tt = wave >> 2;
+      const int tk = tt * 16 + li;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < DI / 32; ++ks)
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const int tk = tt * 16 + li;
-          const unsigned char* a = s_ki + tk * IROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16);
-          acc[tt] = E::mfma(qif[ks], as_v8<V8>(*(const u32x4*)a), acc[tt]);
-        }
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        Split3 sp;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) split3_set(sp, r, wr[r] * fmaxf(acc[tt][r], 0.f));
-        const f32x4 sum = split3_rowsum(sp);
-        if (li == 0) *(f32x4*)&s_redi[wave][tt * 16 + lg * 4] = sum;
+      for (int ks = 0; ks < DI / 32; ++ks) {
+        const unsigned char* a = s_kia + tk * IROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16);
+        acc = E::mfma(qif[ks], as_v8<V8>(*(const u32x4*)a), acc);
       }
+      Split3 sp;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) split3_set(sp, r, wr[r] * fmaxf(acc[r], 0.f));
+      const f32x4 sum = split3_rowsum(sp);
+      if (li == 0) *(f32x4*)&s_redi[t & 1][hg4][tt * 16 + lg * 4] = sum;
     }
-    lds_barrier();
-    if (tid < TILE) {
-      const int k = t * TILE + tid;
-      if (k < n) {
-        float ps = 0.f, is = 0.f;
-#pragma unroll
-        for (int w2 = 0; w2 < kKlWaves; ++w2) ps += s_red[w2][tid];
-#pragma unroll
-        for (int w2 = 0; w2 < 4; ++w2) is += s_redi[w2][tid];
-        s_p[k] = ps * (1.f / (float)p.n1);
-        s_I[k] = is;
-      }
+    if (p.ring == 1 && t + 1 < nt) {
+      lds_barrier();
+      issue_a(t + 1, 0);
     }
   }
+  lds_barrier();
+  reduce_a(nt - 1);
   lds_barrier();
 
   // ================= pass B: softmax(I), dI, KL =================
@@ -705,42 +778,48 @@ size_t kl_bwd_workspace_bytes(int64_t q_rows, int64_t kv_rows, int64_t topk) {
   return kl_ws_layout(q_rows, kv_rows, topk).total;
 }
 
-size_t kl_bwd_lds_bytes(int64_t topk) { return (size_t)3 * topk * sizeof(float); }
 int kl_bwd_max_topk() { return kKlMaxTopk; }
 int kl_bwd_max_nidx() { return kKlMaxNidx; }
 
-// the row kernel's dynamic LDS (I and p of a row) may exceed the default
-// dynamic limit: raise it once per instantiation
-template <int D, int DR, typename T>
-static hipError_t kl_row_lds_attr() {
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)kl_bwd_row_kernel<D, DR, T>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)(3 * kKlMaxTopk * 4));
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
-  return hipSuccess;
-}
+// The row kernel's dynamic LDS: the pass-A tile ring, then I, p and the
+// token rows of a row (3 x topK x 4 bytes).  Two tile buffers when they fit
+// beside the row's arrays and the static LDS, else one (top-k over about
+// 5000 at D = 512).
+constexpr int kKlLdsBytes = 160 * 1024;
 
 template <int D, int DR, typename T>
-static hipError_t run_kl_row(const KlParams& p, int rows, size_t dyn, hipStream_t stream) {
-  hipError_t e = kl_row_lds_attr<D, DR, T>();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((kl_bwd_row_kernel<D, DR, T>), dim3(rows), dim3(kKlWaves * 64), dyn, stream, p);
+static hipError_t run_kl_row(KlParams p, int rows, int64_t topk, hipStream_t stream) {
+  static int static_lds = -1, attr_dyn = 0;
+  const void* fn = (const void*)kl_bwd_row_kernel<D, DR, T>;
+  if (static_lds < 0) {
+    hipFuncAttributes fa;
+    hipError_t e = hipFuncGetAttributes(&fa, fn);
+    if (e != hipSuccess) return e;
+    static_lds = (int)fa.sharedSizeBytes;
+  }
+  const int buf = kl_tile_bytes<D, DR>();
+  const int rowb = (int)(3 * topk * sizeof(float));
+  p.ring = static_lds + 2 * buf + rowb <= kKlLdsBytes ? 2 : 1;
+  const int dyn = p.ring * buf + rowb;
+  if (dyn > attr_dyn) {
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
+    if (e != hipSuccess) return e;
+    attr_dyn = dyn;
+  }
+  hipLaunchKernelGGL((kl_bwd_row_kernel<D, DR, T>), dim3(rows), dim3(kKlWaves * 64), (size_t)dyn, stream, p);
   return hipGetLastError();
 }
 
 template <typename T>
-static hipError_t dispatch_kl_row(const KlParams& p, int rows, int d, int dr, size_t dyn, hipStream_t stream) {
+static hipError_t dispatch_kl_row(const KlParams& p, int rows, int d, int dr, int64_t topk, hipStream_t stream) {
   if (dr == 64) {
-    if (d == 128) return run_kl_row<128, 64, T>(p, rows, dyn, stream);
-    if (d == 256) return run_kl_row<256, 64, T>(p, rows, dyn, stream);
-    return run_kl_row<512, 64, T>(p, rows, dyn, stream);
+    if (d == 128) return run_kl_row<128, 64, T>(p, rows, topk, stream);
+    if (d == 256) return run_kl_row<256, 64, T>(p, rows, topk, stream);
+    return run_kl_row<512, 64, T>(p, rows, topk, stream);
   }
-  if (d == 128) return run_kl_row<128, 0, T>(p, rows, dyn, stream);
-  if (d == 256) return run_kl_row<256, 0, T>(p, rows, dyn, stream);
-  return run_kl_row<512, 0, T>(p, rows, dyn, stream);
+  if (d == 128) return run_kl_row<128, 0, T>(p, rows, topk, stream);
+  if (d == 256) return run_kl_row<256, 0, T>(p, rows, topk, stream);
+  return run_kl_row<512, 0, T>(p, rows, topk, stream);
 }
 
 int kl_bwd_run(const void* query, const void* key, const void* query_rope, const void* key_rope,
@@ -804,10 +883,9 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   const int64_t zn = (int64_t)((L.offs - L.cnt) / sizeof(int32_t));
   hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((zn + 255) / 256)), dim3(256), 0, stream, s.cnt, zn);
   DSA_HIP(hipGetLastError());
-  const size_t dyn = kl_bwd_lds_bytes(topk);
   const bool bf = dtype == DSA_DTYPE_BF16;
-  DSA_HIP(bf ? dispatch_kl_row<bf16>(p, (int)rows, (int)d, (int)d_rope, dyn, stream)
-             : dispatch_kl_row<f16>(p, (int)rows, (int)d, (int)d_rope, dyn, stream));
+  DSA_HIP(bf ? dispatch_kl_row<bf16>(p, (int)rows, (int)d, (int)d_rope, topk, stream)
+             : dispatch_kl_row<f16>(p, (int)rows, (int)d, (int)d_rope, topk, stream));
   const dim3 bgrid((unsigned)rows, (unsigned)((topk + 255) / 256));
   hipLaunchKernelGGL(kl_bucket_kernel<false>, bgrid, dim3(256), 0, stream, s);
   DSA_HIP(hipGetLastError());
