@@ -66,8 +66,11 @@ struct KlParams {
   const float* ssum;
   void* dqi;
   void* dw;
-  float* cbuf;       // [rows][topK][128] dKi contribution of each slot
+  // [rows][topK][128] dKi contribution c of each slot, stored as fp16
+  // c * 2^e_row, with e_row set from an a-priori bound of |c| over the row
+  _Float16* cbuf;
   float* rowmax;     // [rows] max |c| over the row's slots
+  float* rowscale;   // [rows] 2^-e_row
   float* loss_part;  // [rows]
   int32_t n1, nidx, topk, w_dtype;
   float scale_log2;  // scale * log2(e)
@@ -185,7 +188,9 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   __shared__ __attribute__((aligned(16))) float s_red[2][kKlWaves][TILE];
   __shared__ __attribute__((aligned(16))) float s_redi[2][4][TILE];
   __shared__ __attribute__((aligned(16))) T s_ds[2][TILE][kKlDsRow];  // dS^T hi / lo: [slot][g]
-  __shared__ float s_misc[2 * kKlWaves + 4];
+  // [0, 8) and [8, 16): per-wave pass-B sums / maxima; [16]: fp16 weight
+  // max; [17, 25): per-wave max |Qi|
+  __shared__ float s_misc[3 * kKlWaves + 4];
   // dynamic: the pass-A tile ring (p.ring buffers of BUF bytes), then I
   // (then dI) and p of the row, and its clamped token rows
   extern __shared__ __attribute__((aligned(16))) unsigned char s_dynb[];
@@ -193,8 +198,16 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   float* s_I = (float*)(s_dynb + p.ring * BUF);
   float* s_p = s_I + p.topk;
   int* s_tok = (int*)(s_p + p.topk);
-  // pass C stages K_index tiles in buffer 0's index rows
+  // pass C stages K_index tiles in buffer 0's index rows, and a tile's dKi
+  // contributions ([slot][128] fp16, 8 KB) in buffer 1, or with one buffer
+  // in buffer 0's K rows (one buffer only happens at D >= 256).  In a row,
+  // 32-byte block j of slot tk sits at block j ^ ((tk >> 2) & 3), so that
+  // the MFMA-layout writes of the four lane groups (slots 4*lg + r) fall in
+  // different banks.
   unsigned char* const s_ki = ring + BUF_K + BUF_R;
+  constexpr int CROW = DI * 2;
+  static_assert(TILE * CROW <= BUF && TILE * CROW <= BUF_K + BUF_R, "contribution staging");
+  unsigned char* const s_c = p.ring == 2 ? ring + BUF : ring;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -210,6 +223,7 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     if (tid == 0) {
       p.loss_part[row] = 0.f;
       p.rowmax[row] = 0.f;
+      p.rowscale[row] = 1.f;
     }
     return;
   }
@@ -508,6 +522,37 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     ds_unscale = ldexpf(1.f, -e);
   }
 
+  // Scale of the row's fp16 contributions: |c[slot][j]| = |sum_g dS[g][slot]
+  // Qi[g][j]| <= max|dI| * sum_g |w_g| * max|Qi|; with that bound below
+  // 2^(14 - e) the stored c * 2^e stays in fp16's normal range.
+  float c_scale = 1.f, c_unscale = 1.f;
+  {
+    float dm = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < kKlWaves; ++w2) dm = fmaxf(dm, s_misc[kKlWaves + w2]);
+    float ws = lane < p.nidx ? fabsf(load_w(p.w, (int64_t)row * p.nidx + lane, p.w_dtype)) : 0.f;
+    ws = wave_sum(ws);
+    float qm = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < kKlMaxNidx / 32; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qm = fmaxf(qm, fabsf(E::to_f32(qib[ks][j])));
+    qm = wave_max(qm);
+    lds_barrier();
+    if (lane == 0) s_misc[2 * kKlWaves + 1 + wave] = qm;
+    lds_barrier();
+#pragma unroll
+    for (int w2 = 0; w2 < kKlWaves; ++w2) qm = fmaxf(qm, s_misc[2 * kKlWaves + 1 + w2]);
+    const float bound = dm * ws * qm;
+    if (bound > 0.f && bound < INFINITY) {
+      int e;
+      frexpf(bound, &e);  // bound < 2^e
+      e = max(-100, min(100, 14 - e));
+      c_scale = ldexpf(1.f, e);
+      c_unscale = ldexpf(1.f, -e);
+    }
+  }
+
   // ================= pass C: dW, dQi, dKi contributions =================
   f32x4 acc_dqi[DI / 16];
 #pragma unroll
@@ -586,17 +631,26 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
           acc[tt] = E::mfma(ah, qib[ks], acc[tt]);
           acc[tt] = E::mfma(al, qib[ks], acc[tt]);
         }
+      // staged in LDS, then stored as whole 512-byte rows (16 bytes per
+      // lane): stored directly, each row would leave in 64-byte pieces from
+      // eight waves
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int k = t * TILE + tt * 16 + lg * 4 + r;
-          if (k < n) {
-            const float c = acc[tt][r] * ds_unscale;
-            cmax = fmaxf(cmax, fabsf(c));
-            p.cbuf[((int64_t)row * p.topk + k) * DI + wave * 16 + li] = c;
-          }
+          const int tk = tt * 16 + lg * 4 + r;
+          const float c = acc[tt][r] * ds_unscale;
+          if (t * TILE + tk < n) cmax = fmaxf(cmax, fabsf(c));
+          *(_Float16*)(s_c + tk * CROW + ((wave ^ ((tk >> 2) & 3)) * 16 + li) * 2) = (_Float16)(c * c_scale);
         }
+    }
+    lds_barrier();
+    static_assert(TILE * DI * 2 == NT * 16, "one 16-byte chunk per thread");
+    {
+      const int tk = tid / (DI / 8), ch = tid - tk * (DI / 8);
+      const int k = t * TILE + tk;
+      const u32x4 v = *(const u32x4*)(s_c + tk * CROW + (ch ^ (((tk >> 2) & 3) << 1)) * 16);
+      if (k < n) *(u32x4*)(p.cbuf + ((int64_t)row * p.topk + k) * DI + ch * 8) = v;
     }
   }
 
@@ -623,6 +677,7 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     float m = 0.f;
     for (int w2 = 0; w2 < kKlWaves; ++w2) m = fmaxf(m, s_misc[w2]);
     p.rowmax[row] = m;
+    p.rowscale[row] = c_unscale;
   }
 }
 
@@ -685,7 +740,8 @@ __global__ __launch_bounds__(1024) void kl_scan_kernel(const int32_t* cnt, int32
 
 // one wave per token: dKi[t] = sum of its slots' contributions, in int64 fixed point
 template <typename T>
-__global__ __launch_bounds__(256) void kl_reduce_kernel(const float* cbuf, const float* rowmax,
+__global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, const float* rowmax,
+                                                        const float* rowscale,
                                                         const int32_t* offs, const int32_t* list, T* dki,
                                                         int ntok, int topk) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -708,21 +764,30 @@ __global__ __launch_bounds__(256) void kl_reduce_kernel(const float* cbuf, const
     frexp((double)bm * (double)len, &ex);  // len * bm < 2^ex
     e = 62 - ex;
     const double sc = ldexp(1.0, e);
+    // a contribution is c16 * rowscale (exact in fp32: a power-of-two scale)
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     int i = 0;
     for (; i + 4 <= len; i += 4) {
-      float2 v[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = *(const float2*)(cbuf + (int64_t)list[o0 + i + u] * kKlDi + 2 * lane);
+      h2 v[4];
+      float rs[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        a0 += __double2ll_rn((double)v[u].x * sc);
-        a1 += __double2ll_rn((double)v[u].y * sc);
+        const int sl = list[o0 + i + u];
+        v[u] = *(const h2*)(cbuf + (int64_t)sl * kKlDi + 2 * lane);
+        rs[u] = rowscale[sl / topk];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        a0 += __double2ll_rn((double)((float)v[u].x * rs[u]) * sc);
+        a1 += __double2ll_rn((double)((float)v[u].y * rs[u]) * sc);
       }
     }
     for (; i < len; ++i) {
-      const float2 v = *(const float2*)(cbuf + (int64_t)list[o0 + i] * kKlDi + 2 * lane);
-      a0 += __double2ll_rn((double)v.x * sc);
-      a1 += __double2ll_rn((double)v.y * sc);
+      const int sl = list[o0 + i];
+      const h2 v = *(const h2*)(cbuf + (int64_t)sl * kKlDi + 2 * lane);
+      const float rs = rowscale[sl / topk];
+      a0 += __double2ll_rn((double)((float)v.x * rs) * sc);
+      a1 += __double2ll_rn((double)((float)v.y * rs) * sc);
     }
   }
   const double us = ldexp(1.0, -e);
@@ -750,15 +815,17 @@ __global__ __launch_bounds__(256) void kl_loss_kernel(const float* part, int row
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct KlWs {
-  size_t cbuf, rowmax, loss, cnt, offs, cur, list, total;
+  size_t cbuf, rowmax, rowscale, loss, cnt, offs, cur, list, total;
 };
 
 static KlWs kl_ws_layout(int64_t rows, int64_t tokens, int64_t topk) {
   KlWs w;
   size_t o = 0;
   w.cbuf = o;
-  o += align256((size_t)rows * topk * kKlDi * sizeof(float));
+  o += align256((size_t)rows * topk * kKlDi * sizeof(_Float16));
   w.rowmax = o;
+  o += align256((size_t)rows * sizeof(float));
+  w.rowscale = o;
   o += align256((size_t)rows * sizeof(float));
   w.loss = o;
   o += align256((size_t)rows * sizeof(float));
@@ -800,6 +867,9 @@ static hipError_t run_kl_row(KlParams p, int rows, int64_t topk, hipStream_t str
   const int buf = kl_tile_bytes<D, DR>();
   const int rowb = (int)(3 * topk * sizeof(float));
   p.ring = static_lds + 2 * buf + rowb <= kKlLdsBytes ? 2 : 1;
+  // one buffer stages pass C's contributions in its K rows: D >= 256 only
+  // (at D = 128 two buffers fit for every supported topK)
+  if (p.ring == 1 && D < 256) return hipErrorInvalidConfiguration;
   const int dyn = p.ring * buf + rowb;
   if (dyn > attr_dyn) {
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
@@ -862,8 +932,9 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   p.ssum = softmax_sum;
   p.dqi = d_query_index;
   p.dw = d_weights;
-  p.cbuf = (float*)(ws + L.cbuf);
+  p.cbuf = (_Float16*)(ws + L.cbuf);
   p.rowmax = (float*)(ws + L.rowmax);
+  p.rowscale = (float*)(ws + L.rowscale);
   p.loss_part = (float*)(ws + L.loss);
   p.n1 = (int32_t)n1;
   p.nidx = (int32_t)nidx;
@@ -895,10 +966,10 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   DSA_HIP(hipGetLastError());
   const dim3 rgrid((unsigned)((tokens + 3) / 4));
   if (bf)
-    hipLaunchKernelGGL(kl_reduce_kernel<bf16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowmax, s.offs, s.list,
+    hipLaunchKernelGGL(kl_reduce_kernel<bf16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowmax, p.rowscale, s.offs, s.list,
                        (bf16*)d_key_index, (int)tokens, (int)topk);
   else
-    hipLaunchKernelGGL(kl_reduce_kernel<f16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowmax, s.offs, s.list,
+    hipLaunchKernelGGL(kl_reduce_kernel<f16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowmax, p.rowscale, s.offs, s.list,
                        (f16*)d_key_index, (int)tokens, (int)topk);
   DSA_HIP(hipGetLastError());
   hipLaunchKernelGGL(kl_loss_kernel, dim3(1), dim3(256), 0, stream, p.loss_part, (int)rows, loss);
