@@ -70,7 +70,7 @@ struct KlParams {
   // c * 2^e_row, with e_row set from an a-priori bound of |c| over the row
   _Float16* cbuf;
   float* rowmax;     // [rows] max |c| over the row's slots
-  float* rowscale;   // [rows] 2^-e_row
+  int32_t* rowexp;   // [rows] e_row
   float* loss_part;  // [rows]
   int32_t n1, nidx, topk, w_dtype;
   float scale_log2;  // scale * log2(e)
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     if (tid == 0) {
       p.loss_part[row] = 0.f;
       p.rowmax[row] = 0.f;
-      p.rowscale[row] = 1.f;
+      p.rowexp[row] = 0;
     }
     return;
   }
@@ -525,7 +525,8 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   // Scale of the row's fp16 contributions: |c[slot][j]| = |sum_g dS[g][slot]
   // Qi[g][j]| <= max|dI| * sum_g |w_g| * max|Qi|; with that bound below
   // 2^(14 - e) the stored c * 2^e stays in fp16's normal range.
-  float c_scale = 1.f, c_unscale = 1.f;
+  float c_scale = 1.f;
+  int c_exp = 0;
   {
     float dm = 0.f;
 #pragma unroll
@@ -547,9 +548,8 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     if (bound > 0.f && bound < INFINITY) {
       int e;
       frexpf(bound, &e);  // bound < 2^e
-      e = max(-100, min(100, 14 - e));
-      c_scale = ldexpf(1.f, e);
-      c_unscale = ldexpf(1.f, -e);
+      c_exp = max(-100, min(100, 14 - e));
+      c_scale = ldexpf(1.f, c_exp);
     }
   }
 
@@ -677,7 +677,7 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     float m = 0.f;
     for (int w2 = 0; w2 < kKlWaves; ++w2) m = fmaxf(m, s_misc[w2]);
     p.rowmax[row] = m;
-    p.rowscale[row] = c_unscale;
+    p.rowexp[row] = c_exp;
   }
 }
 
@@ -687,10 +687,12 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
 struct KlScatter {
   KlMap m;
   const int32_t* idx;
-  int32_t* cnt;     // [tokens]
-  int32_t* offs;    // [tokens + 1]
-  int32_t* cur;     // [tokens]
-  int32_t* list;    // [rows * topK]
+  const float* rowmax;  // [rows]
+  int32_t* cnt;         // [tokens]
+  int32_t* offs;        // [tokens + 1]
+  int32_t* cur;         // [tokens]
+  uint32_t* tokmax;     // [tokens] largest row maximum among the token's slots (float bits)
+  int32_t* list;        // [rows * topK]
 };
 
 __global__ __launch_bounds__(256) void kl_zero_kernel(int32_t* a, int64_t n) {
@@ -711,6 +713,8 @@ __global__ __launch_bounds__(256) void kl_bucket_kernel(KlScatter s) {
   } else {
     const int pos = s.offs[t] + atomicAdd(&s.cur[t], 1);
     s.list[pos] = row * s.m.topk + k;
+    // non-negative floats order as their bit patterns
+    atomicMax(&s.tokmax[t], __float_as_uint(s.rowmax[row]));
   }
 }
 
@@ -738,61 +742,111 @@ __global__ __launch_bounds__(1024) void kl_scan_kernel(const int32_t* cnt, int32
   if (tid == 1023) offs[n] = s_sum[1023];
 }
 
-// one wave per token: dKi[t] = sum of its slots' contributions, in int64 fixed point
+// dKi[t] = sum of the token's slot contributions, in int64 fixed point with
+// the exponent fixed by the token's largest row maximum and slot count (no
+// partial sum can overflow).  A token's slots are split into up to
+// kKlReduceParts parts of at least kKlReduceChunk slots, one wave each: a
+// token with one part writes dKi directly; the parts of a longer token add
+// their partial sums into an int64 accumulator with integer atomics, which
+// kl_reduce_finish_kernel converts.  Integer addition is exact and
+// associative, so the result does not depend on the split or on the order.
+constexpr int kKlReduceParts = 16;
+constexpr int kKlReduceChunk = 256;
+
+__device__ __forceinline__ int kl_reduce_parts(int len) {
+  return max(1, min(kKlReduceParts, (len + kKlReduceChunk - 1) / kKlReduceChunk));
+}
+// fixed-point exponent: len * bm < 2^(62 - e)
+__device__ __forceinline__ int kl_fixed_exp(float bm, int len) {
+  int ex;
+  frexp((double)bm * (double)len, &ex);
+  return 62 - ex;
+}
+
 template <typename T>
-__global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, const float* rowmax,
-                                                        const float* rowscale,
-                                                        const int32_t* offs, const int32_t* list, T* dki,
-                                                        int ntok, int topk) {
+__global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, const int32_t* rowexp,
+                                                        const uint32_t* tokmax, const int32_t* offs,
+                                                        const int32_t* list, long long* acc, T* dki, int ntok,
+                                                        int topk) {
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int t = w / kKlReduceParts, part = w - t * kKlReduceParts;
+  const int lane = threadIdx.x & 63;
+  if (t >= ntok) return;
+  const int o0 = __builtin_amdgcn_readfirstlane(offs[t]);
+  const int len = __builtin_amdgcn_readfirstlane(offs[t + 1]) - o0;
+  const int np = kl_reduce_parts(len);
+  if (part >= np) return;
+  const float bm = __uint_as_float(tokmax[t]);
+  T* dst = dki + (int64_t)t * kKlDi + 2 * lane;
+  if (!(bm < INFINITY)) {  // non-finite contributions: no fixed-point scale exists
+    if (part == 0) {
+      dst[0] = Elem<T>::from_f32(NAN);
+      dst[1] = Elem<T>::from_f32(NAN);
+    }
+    return;
+  }
+  long long a0 = 0, a1 = 0;
+  int e = 0;
+  if (bm > 0.f) {
+    e = kl_fixed_exp(bm, len);
+    const int L = (len + np - 1) / np;
+    const int i1 = min(len, (part + 1) * L);
+    // A contribution is c16 * 2^-e_row; its fixed-point value is
+    // round(c16 * 2^(e - e_row)), exact through double (a branch-free
+    // conversion: an integer shift-and-round per element diverges and runs
+    // slower).  64 list entries and their row exponents come in with one
+    // load per lane and are broadcast with readlane; 16 contribution rows
+    // are in flight at a time.
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    constexpr int U = 16;
+    for (int base = part * L; base < i1; base += 64) {
+      const int cnt = min(64, i1 - base);
+      const int slv = lane < cnt ? list[o0 + base + lane] : 0;
+      const int kv = lane < cnt ? e - rowexp[slv / topk] : 0;
+      for (int u0 = 0; u0 < cnt; u0 += U) {
+        h2 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int sl = __builtin_amdgcn_readlane(slv, u0 + u);
+          v[u] = u0 + u < cnt ? *(const h2*)(cbuf + (int64_t)sl * kKlDi + 2 * lane) : (h2){0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const double sc = ldexp(1.0, __builtin_amdgcn_readlane(kv, u0 + u));
+          a0 += __double2ll_rn((double)v[u].x * sc);
+          a1 += __double2ll_rn((double)v[u].y * sc);
+        }
+      }
+    }
+  }
+  if (np == 1) {
+    const double us = ldexp(1.0, -e);
+    dst[0] = Elem<T>::from_f32((float)((double)a0 * us));
+    dst[1] = Elem<T>::from_f32((float)((double)a1 * us));
+  } else {
+    unsigned long long* ap = (unsigned long long*)acc + (int64_t)t * kKlDi + 2 * lane;
+    atomicAdd(ap, (unsigned long long)a0);
+    atomicAdd(ap + 1, (unsigned long long)a1);
+  }
+}
+
+// dKi of the tokens with more than one part, from their accumulators
+template <typename T>
+__global__ __launch_bounds__(256) void kl_reduce_finish_kernel(const uint32_t* tokmax, const int32_t* offs,
+                                                               const long long* acc, T* dki, int ntok) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (t >= ntok) return;
-  const int o0 = offs[t], len = offs[t + 1] - o0;
-  float bm = 0.f;
-  for (int i = lane; i < len; i += 64) bm = fmaxf(bm, rowmax[list[o0 + i] / topk]);
-  bm = wave_max(bm);
-  long long a0 = 0, a1 = 0;
-  int e = 0;
-  T* dst = dki + (int64_t)t * kKlDi + 2 * lane;
-  if (!(bm < INFINITY)) {  // non-finite contributions: no fixed-point scale exists
-    dst[0] = Elem<T>::from_f32(NAN);
-    dst[1] = Elem<T>::from_f32(NAN);
-    return;
-  }
-  if (bm > 0.f) {
-    int ex;
-    frexp((double)bm * (double)len, &ex);  // len * bm < 2^ex
-    e = 62 - ex;
-    const double sc = ldexp(1.0, e);
-    // a contribution is c16 * rowscale (exact in fp32: a power-of-two scale)
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    int i = 0;
-    for (; i + 4 <= len; i += 4) {
-      h2 v[4];
-      float rs[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int sl = list[o0 + i + u];
-        v[u] = *(const h2*)(cbuf + (int64_t)sl * kKlDi + 2 * lane);
-        rs[u] = rowscale[sl / topk];
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        a0 += __double2ll_rn((double)((float)v[u].x * rs[u]) * sc);
-        a1 += __double2ll_rn((double)((float)v[u].y * rs[u]) * sc);
-      }
-    }
-    for (; i < len; ++i) {
-      const int sl = list[o0 + i];
-      const h2 v = *(const h2*)(cbuf + (int64_t)sl * kKlDi + 2 * lane);
-      const float rs = rowscale[sl / topk];
-      a0 += __double2ll_rn((double)((float)v.x * rs) * sc);
-      a1 += __double2ll_rn((double)((float)v.y * rs) * sc);
-    }
-  }
+  const int len = offs[t + 1] - offs[t];
+  if (kl_reduce_parts(len) == 1) return;
+  const float bm = __uint_as_float(tokmax[t]);
+  if (!(bm < INFINITY)) return;
+  const int e = bm > 0.f ? kl_fixed_exp(bm, len) : 0;
   const double us = ldexp(1.0, -e);
-  dst[0] = Elem<T>::from_f32((float)((double)a0 * us));
-  dst[1] = Elem<T>::from_f32((float)((double)a1 * us));
+  const long long* ap = acc + (int64_t)t * kKlDi + 2 * lane;
+  T* dst = dki + (int64_t)t * kKlDi + 2 * lane;
+  dst[0] = Elem<T>::from_f32((float)((double)ap[0] * us));
+  dst[1] = Elem<T>::from_f32((float)((double)ap[1] * us));
 }
 
 // loss = sum of the per-row terms, in a fixed order (one workgroup)
@@ -815,7 +869,7 @@ __global__ __launch_bounds__(256) void kl_loss_kernel(const float* part, int row
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct KlWs {
-  size_t cbuf, rowmax, rowscale, loss, cnt, offs, cur, list, total;
+  size_t cbuf, rowmax, rowexp, loss, cnt, cur, tokmax, acc, offs, list, total;
 };
 
 static KlWs kl_ws_layout(int64_t rows, int64_t tokens, int64_t topk) {
@@ -825,14 +879,18 @@ static KlWs kl_ws_layout(int64_t rows, int64_t tokens, int64_t topk) {
   o += align256((size_t)rows * topk * kKlDi * sizeof(_Float16));
   w.rowmax = o;
   o += align256((size_t)rows * sizeof(float));
-  w.rowscale = o;
-  o += align256((size_t)rows * sizeof(float));
+  w.rowexp = o;
+  o += align256((size_t)rows * sizeof(int32_t));
   w.loss = o;
   o += align256((size_t)rows * sizeof(float));
   w.cnt = o;
   o += align256((size_t)tokens * sizeof(int32_t));
   w.cur = o;
   o += align256((size_t)tokens * sizeof(int32_t));
+  w.tokmax = o;
+  o += align256((size_t)tokens * sizeof(uint32_t));
+  w.acc = o;
+  o += align256((size_t)tokens * kKlDi * sizeof(long long));
   w.offs = o;
   o += align256((size_t)(tokens + 1) * sizeof(int32_t));
   w.list = o;
@@ -934,7 +992,7 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   p.dw = d_weights;
   p.cbuf = (_Float16*)(ws + L.cbuf);
   p.rowmax = (float*)(ws + L.rowmax);
-  p.rowscale = (float*)(ws + L.rowscale);
+  p.rowexp = (int32_t*)(ws + L.rowexp);
   p.loss_part = (float*)(ws + L.loss);
   p.n1 = (int32_t)n1;
   p.nidx = (int32_t)nidx;
@@ -948,9 +1006,13 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   s.cnt = (int32_t*)(ws + L.cnt);
   s.offs = (int32_t*)(ws + L.offs);
   s.cur = (int32_t*)(ws + L.cur);
+  s.tokmax = (uint32_t*)(ws + L.tokmax);
+  s.rowmax = p.rowmax;
   s.list = (int32_t*)(ws + L.list);
+  long long* acc = (long long*)(ws + L.acc);
 
-  // counters cleared by a kernel (no memset nodes when the caller captures)
+  // counters, token maxima and accumulators (cnt .. offs) cleared by a
+  // kernel (no memset nodes when the caller captures)
   const int64_t zn = (int64_t)((L.offs - L.cnt) / sizeof(int32_t));
   hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((zn + 255) / 256)), dim3(256), 0, stream, s.cnt, zn);
   DSA_HIP(hipGetLastError());
@@ -964,13 +1026,21 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   DSA_HIP(hipGetLastError());
   hipLaunchKernelGGL(kl_bucket_kernel<true>, bgrid, dim3(256), 0, stream, s);
   DSA_HIP(hipGetLastError());
-  const dim3 rgrid((unsigned)((tokens + 3) / 4));
-  if (bf)
-    hipLaunchKernelGGL(kl_reduce_kernel<bf16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowmax, p.rowscale, s.offs, s.list,
-                       (bf16*)d_key_index, (int)tokens, (int)topk);
-  else
-    hipLaunchKernelGGL(kl_reduce_kernel<f16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowmax, p.rowscale, s.offs, s.list,
-                       (f16*)d_key_index, (int)tokens, (int)topk);
+  const dim3 rgrid((unsigned)((tokens * kKlReduceParts + 3) / 4));
+  const dim3 fgrid((unsigned)((tokens + 3) / 4));
+  if (bf) {
+    hipLaunchKernelGGL(kl_reduce_kernel<bf16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowexp, s.tokmax, s.offs,
+                       s.list, acc, (bf16*)d_key_index, (int)tokens, (int)topk);
+    DSA_HIP(hipGetLastError());
+    hipLaunchKernelGGL(kl_reduce_finish_kernel<bf16>, fgrid, dim3(256), 0, stream, s.tokmax, s.offs, acc,
+                       (bf16*)d_key_index, (int)tokens);
+  } else {
+    hipLaunchKernelGGL(kl_reduce_kernel<f16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowexp, s.tokmax, s.offs,
+                       s.list, acc, (f16*)d_key_index, (int)tokens, (int)topk);
+    DSA_HIP(hipGetLastError());
+    hipLaunchKernelGGL(kl_reduce_finish_kernel<f16>, fgrid, dim3(256), 0, stream, s.tokmax, s.offs, acc,
+                       (f16*)d_key_index, (int)tokens);
+  }
   DSA_HIP(hipGetLastError());
   hipLaunchKernelGGL(kl_loss_kernel, dim3(1), dim3(256), 0, stream, p.loss_part, (int)rows, loss);
   DSA_HIP(hipGetLastError());
