@@ -201,13 +201,14 @@ def test_kl_topk_larger_than_window():
     _check(_run_gpu(c), _oracle(c), "topK>window")
 
 
-def test_kl_long_topk_single_tile_buffer():
-    """topK = 6144 at D = 512: the row's LDS arrays leave room for one pass-A
-    tile buffer only, so each tile's gather waits behind the previous
-    tile's MFMAs (two-buffer ring below about 5000 slots)."""
-    print("[kl_bwd] topK 6144, one tile buffer", flush=True)
-    c = _case(1, 4, 6200, 16, 512, 64, 6144, torch.bfloat16, "causal_random")
-    _check(_run_gpu(c), _oracle(c), "topK=6144")
+@pytest.mark.parametrize("topk", [3072, 6144])
+def test_kl_long_topk_smaller_tile_ring(topk):
+    """At D = 512 the pass-A tile ring shrinks with topK (the row's arrays
+    share the LDS): two buffers up to about 5000 slots (topK 3072 and every
+    other test), one above (topK 6144)."""
+    print(f"[kl_bwd] topK {topk}, smaller tile ring", flush=True)
+    c = _case(1, 4, topk + 56, 16, 512, 64, topk, torch.bfloat16, "causal_random")
+    _check(_run_gpu(c), _oracle(c), f"topK={topk}")
 
 
 def test_kl_deterministic():
