@@ -263,11 +263,17 @@ def time_call(fn, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
-def leg(metric, workload, flops, ms, n):
+def leg(metric, workload, flops, ms, n, hbm_bytes=None):
     tf = flops / (ms * 1e-3) / 1e12
-    return {"metric": metric, "value": round(tf, 2), "unit": "TFLOP/s", "higher_is_better": True,
-            "ms_per_step": round(ms, 4), "pct_of_bf16_peak": round(100.0 * tf / PEAK_BF16_TFLOPS, 3),
-            "algorithmic_flops": int(flops), "valid_pairs": n, "config": {"workload": workload}}
+    out = {"metric": metric, "value": round(tf, 2), "unit": "TFLOP/s", "higher_is_better": True,
+           "ms_per_step": round(ms, 4), "pct_of_bf16_peak": round(100.0 * tf / PEAK_BF16_TFLOPS, 3),
+           "algorithmic_flops": int(flops), "valid_pairs": n, "config": {"workload": workload}}
+    if hbm_bytes is not None:
+        # legs whose roofline is HBM: algorithmic bytes over the step time
+        gbs = hbm_bytes / (ms * 1e-3) / 1e9
+        out["hbm"] = {"algorithmic_bytes": int(hbm_bytes), "achieved_GBps": round(gbs, 1),
+                      "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2)}
+    return out
 
 
 def long_legs(dev, steps):
@@ -330,10 +336,15 @@ def long_legs(dev, steps):
         return dsa.sparse_lightning_indexer_grad_kl_loss_triton(q, k, qi, ki, w, si, smax, ssum, query_rope=qr,
                                                                 key_rope=kr, scale_value=scale)
     ms = time_call(kl, steps, 1)
+    # HBM-bound: every valid (row, slot) pair gathers a K, K_rope and
+    # K_index row; per row Q, Q_rope, Qi, weights, indices, statistics and
+    # dQi, dW; per key row dKi
+    kl_bytes = (n * (D + DR + DI) * 2 + S * (N1 * (D + DR) * 2 + NI * DI * 2 * 2 + NI * 4 * 2 + K * 4 + N1 * 8)
+                + S * DI * 2)
     out["kl_bwd"] = leg("indexer KL-loss bwd TFLOP/s",
                         "sparse_lightning_indexer_grad_kl_loss: B=1, S1=S2=4096, N1=128, D=512+64, Nidx1=64, "
                         "D_idx=128, topK=2048 causal, bf16 (fp32 weights), stats from the SFA forward",
-                        n * (3 * 2 * NI * DI + 2 * N1 * (D + DR) + 2 * NI), ms, n)
+                        n * (3 * 2 * NI * DI + 2 * N1 * (D + DR) + 2 * NI), ms, n, hbm_bytes=kl_bytes)
     del si, o, do
     torch.cuda.empty_cache()
     # dense warm-up stage at the same shape: every causal key, teacher stats of
