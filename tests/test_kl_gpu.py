@@ -211,6 +211,16 @@ def test_kl_long_topk_smaller_tile_ring(topk):
     _check(_run_gpu(c), _oracle(c), f"topK={topk}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_kl_many_contributions_per_token(dtype):
+    """600 rows over the same 64 tokens ("continuous": every row attends
+    tokens 0..63): each token receives 600 contributions, so its dKeyIndex
+    sum is split over three waves and finished from the int64 accumulator."""
+    print(f"[kl_bwd] 600 contributions per token, {dtype}", flush=True)
+    c = _case(1, 600, 64, 16, 128, 16, 64, dtype, "continuous")
+    _check(_run_gpu(c), _oracle(c), "600 per token")
+
+
 def test_kl_deterministic():
     """Two calls give bit-identical outputs (no atomics in the dKi reduction)."""
     print("[kl_bwd] determinism", flush=True)
