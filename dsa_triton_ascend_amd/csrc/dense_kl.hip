@@ -303,8 +303,12 @@ __global__ __launch_bounds__(kDkThreads, 1) void dense_teacher_kernel(DkParams p
   const int items = nt * p.n2;
   // item i: tile i / N2, key head i % N2; key row (b*S2 + t)*N2 + n2
   u32x4 pre_n[NJ_N], pre_r;
+  // the tile's index scores, read by the reducing threads one item ahead
+  // with the key rows (a load at the reduction would stall every tile)
+  float pre_i = 0.f, cur_i = 0.f;
   auto load_item = [&](int i) {
     const int t0 = (i / p.n2) * TILE, n2 = i - (i / p.n2) * p.n2;
+    if (tid < TILE && t0 + tid < ri.vis) pre_i = irow[t0 + tid];
 #pragma unroll
     for (int j = 0; j < NJ_N; ++j) {
       const int e = tid + j * NT;
@@ -340,6 +344,7 @@ __global__ __launch_bounds__(kDkThreads, 1) void dense_teacher_kernel(DkParams p
     const int t0 = (i / p.n2) * TILE, n2 = i - (i / p.n2) * p.n2;
     lds_barrier();
     store_item();
+    cur_i = pre_i;
     lds_barrier();
     if (i + 1 < items) load_item(i + 1);
     if (n2 >= n2_lo && n2 <= n2_hi) {
@@ -379,7 +384,7 @@ __global__ __launch_bounds__(kDkThreads, 1) void dense_teacher_kernel(DkParams p
 #pragma unroll
           for (int w2 = 0; w2 < 8; ++w2) ps += s_red[w2][tid];
           const float pk = ps * (1.f / (float)p.n1);
-          const float st = expf(irow[t] - imax) * inv_isum;
+          const float st = expf(cur_i - imax) * inv_isum;
           const float di = st - pk;
           const float pc = fmaxf(pk, 1e-8f), qc = fmaxf(st, 1e-8f);
           kl += pc * (logf(pc) - logf(qc));
