@@ -18,20 +18,23 @@
 //  * kl_bwd_row_kernel: one workgroup of 8 waves per query row.  Pass A
 //    streams tiles of 32 slots (K, K_rope, K_index rows gathered straight
 //    into an LDS ring by LDS-DMA, the next tile's gather in flight during
-//    the current tile's MFMAs): each
-//    wave scores 16 heads of the teacher on MFMA (Q fragments resident in
-//    registers) and sums its heads' probabilities across lanes; waves 0-3
-//    score 16 index heads each.  I and p of the row stay in LDS.  Pass B is
-//    the softmax/KL over the row.  Pass C re-streams K_index: the index
-//    scores are recomputed (cheaper than storing Nidx1 x topK ReLUs), dW and
-//    dQi accumulate in registers (dQi^T = Ki^T . dS^T through the
-//    transposing LDS read), and the per-slot dKi contributions
-//    c[k] = dS[:,k]^T . Qi are written to a workspace.
-//  * dKi without atomics: the slots are bucketed by target token (count,
-//    scan, fill), and one wave per token sums its contributions in int64
-//    fixed point, with the exponent fixed by the largest row maximum among
-//    the token's slots: integer addition is associative, so the result does
-//    not depend on the bucket order and the output is deterministic.
+//    the current tile's MFMAs): each wave scores 16 heads of the teacher on
+//    MFMA (Q fragments resident in registers) and sums its heads'
+//    probabilities on MFMA; waves w and w + 4 score index heads
+//    16*(w mod 4) .. +15 for the two halves of the tile.  I and p of the row
+//    stay in LDS.  Pass B is the softmax/KL over the row.  Pass C re-streams
+//    K_index: the index scores are recomputed (cheaper than storing
+//    Nidx1 x topK ReLUs), dW and dQi accumulate in registers (dQi^T =
+//    Ki^T . dS^T through the transposing LDS read), and the per-slot dKi
+//    contributions c[k] = dS[:,k]^T . Qi are written to a workspace as fp16
+//    scaled by a per-row power of two.
+//  * dKi without floating-point atomics: the slots are bucketed by target
+//    token (count, scan, fill), and a token's contributions are summed in
+//    int64 fixed point, with the exponent fixed by the largest row maximum
+//    among the token's slots and their count (long tokens split over up to
+//    16 waves whose partial sums meet in integer atomics): integer addition
+//    is exact and associative, so the result does not depend on the bucket
+//    order or the split and the output is deterministic.
 //  * The loss is written per row and summed by one workgroup in a fixed
 //    order (the reference adds rows with an atomic).
 #include "kl_common.h"
