@@ -128,8 +128,9 @@ size_t dsa_sfa_bwd_workspace_size(int64_t kv_rows, int64_t d);
  * index dtype), d_key_index (key index dtype), d_weights (weights dtype)
  * and loss[1] fp32 (sum over rows).  dKi is reduced without atomics in a
  * fixed-point sum, so every output is deterministic.  The workspace
- * (dsa_kl_bwd_workspace_size) holds rows * topK * d_idx fp32 slot
- * contributions and the token buckets.  query/key/rope/index tensors share
+ * (dsa_kl_bwd_workspace_size) holds rows * topK * d_idx fp16 slot
+ * contributions (scaled by a per-row power of two), the token buckets and
+ * kv_rows * d_idx int64 accumulators.  query/key/rope/index tensors share
  * one dtype (bf16 or fp16); D in {128, 256, 512}; d_idx = 128;
  * Nidx1 <= 64; N1 <= 128; topK <= 8192.
  */
