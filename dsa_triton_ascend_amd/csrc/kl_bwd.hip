@@ -693,8 +693,8 @@ struct KlScatter {
   const float* rowmax;  // [rows]
   int32_t* cnt;         // [tokens]
   int32_t* offs;        // [tokens + 1]
-  int32_t* cur;         // [tokens]
   uint32_t* tokmax;     // [tokens] largest row maximum among the token's slots (float bits)
+  int32_t* rank;        // [rows * topK] the slot's place among its token's slots
   int32_t* list;        // [rows * topK]
 };
 
@@ -711,13 +711,14 @@ __global__ __launch_bounds__(256) void kl_bucket_kernel(KlScatter s) {
   if (k >= r.n) return;
   const int t = kl_token(s.m, r, s.idx, row, k);
   if (t < 0) return;  // a -1 page: no gradient target
+  const int64_t slot = (int64_t)row * s.m.topk + k;
   if (!FILL) {
-    atomicAdd(&s.cnt[t], 1);
-  } else {
-    const int pos = s.offs[t] + atomicAdd(&s.cur[t], 1);
-    s.list[pos] = row * s.m.topk + k;
+    // the count's old value is the slot's place in the token's bucket
+    s.rank[slot] = atomicAdd(&s.cnt[t], 1);
     // non-negative floats order as their bit patterns
     atomicMax(&s.tokmax[t], __float_as_uint(s.rowmax[row]));
+  } else {
+    s.list[s.offs[t] + s.rank[slot]] = (int32_t)slot;
   }
 }
 
@@ -872,7 +873,7 @@ __global__ __launch_bounds__(256) void kl_loss_kernel(const float* part, int row
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct KlWs {
-  size_t cbuf, rowmax, rowexp, loss, cnt, cur, tokmax, acc, offs, list, total;
+  size_t cbuf, rowmax, rowexp, loss, cnt, tokmax, acc, offs, rank, list, total;
 };
 
 static KlWs kl_ws_layout(int64_t rows, int64_t tokens, int64_t topk) {
@@ -888,14 +889,14 @@ static KlWs kl_ws_layout(int64_t rows, int64_t tokens, int64_t topk) {
   o += align256((size_t)rows * sizeof(float));
   w.cnt = o;
   o += align256((size_t)tokens * sizeof(int32_t));
-  w.cur = o;
-  o += align256((size_t)tokens * sizeof(int32_t));
   w.tokmax = o;
   o += align256((size_t)tokens * sizeof(uint32_t));
   w.acc = o;
   o += align256((size_t)tokens * kKlDi * sizeof(long long));
   w.offs = o;
   o += align256((size_t)(tokens + 1) * sizeof(int32_t));
+  w.rank = o;
+  o += align256((size_t)rows * topk * sizeof(int32_t));
   w.list = o;
   o += align256((size_t)rows * topk * sizeof(int32_t));
   w.total = o;
@@ -1008,14 +1009,16 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   s.idx = sparse_indices;
   s.cnt = (int32_t*)(ws + L.cnt);
   s.offs = (int32_t*)(ws + L.offs);
-  s.cur = (int32_t*)(ws + L.cur);
   s.tokmax = (uint32_t*)(ws + L.tokmax);
+  s.rank = (int32_t*)(ws + L.rank);
   s.rowmax = p.rowmax;
   s.list = (int32_t*)(ws + L.list);
   long long* acc = (long long*)(ws + L.acc);
 
   // counters, token maxima and accumulators (cnt .. offs) cleared by a
-  // kernel (no memset nodes when the caller captures)
+  // kernel (no memset nodes when the caller captures).  The count pass
+  // records each slot's rank in its bucket and the token maxima; the fill
+  // pass then places the slots without atomics.
   const int64_t zn = (int64_t)((L.offs - L.cnt) / sizeof(int32_t));
   hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((zn + 255) / 256)), dim3(256), 0, stream, s.cnt, zn);
   DSA_HIP(hipGetLastError());
