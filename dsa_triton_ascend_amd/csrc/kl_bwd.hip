@@ -918,14 +918,15 @@ constexpr int kKlLdsBytes = 160 * 1024;
 
 template <int D, int DR, typename T>
 static hipError_t run_kl_row(KlParams p, int rows, int64_t topk, hipStream_t stream) {
-  static int static_lds = -1, attr_dyn = 0;
   const void* fn = (const void*)kl_bwd_row_kernel<D, DR, T>;
-  if (static_lds < 0) {
+  // the kernel's static LDS (a property of the code object; the local
+  // static's initialisation is thread-safe)
+  static const int static_lds = [] {
     hipFuncAttributes fa;
-    hipError_t e = hipFuncGetAttributes(&fa, fn);
-    if (e != hipSuccess) return e;
-    static_lds = (int)fa.sharedSizeBytes;
-  }
+    return hipFuncGetAttributes(&fa, (const void*)kl_bwd_row_kernel<D, DR, T>) == hipSuccess
+               ? (int)fa.sharedSizeBytes : -1;
+  }();
+  if (static_lds < 0) return hipErrorInvalidDeviceFunction;
   const int buf = kl_tile_bytes<D, DR>();
   const int rowb = (int)(3 * topk * sizeof(float));
   p.ring = static_lds + 2 * buf + rowb <= kKlLdsBytes ? 2 : 1;
@@ -933,11 +934,10 @@ static hipError_t run_kl_row(KlParams p, int rows, int64_t topk, hipStream_t str
   // (at D = 128 two buffers fit for every supported topK)
   if (p.ring == 1 && D < 256) return hipErrorInvalidConfiguration;
   const int dyn = p.ring * buf + rowb;
-  if (dyn > attr_dyn) {
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
-    if (e != hipSuccess) return e;
-    attr_dyn = dyn;
-  }
+  // raised on every call: a host-side setting, cheap next to the kernel, and
+  // right for whichever device is current and for concurrent callers
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL((kl_bwd_row_kernel<D, DR, T>), dim3(rows), dim3(kKlWaves * 64), (size_t)dyn, stream, p);
   return hipGetLastError();
 }

@@ -886,17 +886,14 @@ int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_
   p.k = (int32_t)k;
   p.val_dtype = val_dtype;
   p.sel_cap = (int32_t)pow2_at_least(k);
-  // dynamic LDS above 64 KB needs the per-function limit raised (once, to
-  // the full budget)
-  static bool attr_set[2] = {false, false};
+  // dynamic LDS above 64 KB needs the per-function limit raised (to the
+  // full budget; set on every call, which also covers every device and
+  // concurrent callers: a host-side setting, cheap next to the launch)
   const bool in_lds = li_topk_row_in_lds(s2, k);
   size_t lds = li_topk_fixed_bytes(k) + (in_lds ? (size_t)s2 * 4 : 0);  // general path
   if (lds < kFastLds) lds = kFastLds;
   const void* fn = in_lds ? (const void*)li_topk_kernel<true> : (const void*)li_topk_kernel<false>;
-  if (!attr_set[in_lds]) {
-    DSA_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kTopkLdsBudget));
-    attr_set[in_lds] = true;
-  }
+  DSA_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kTopkLdsBudget));
   if (in_lds)
     hipLaunchKernelGGL(li_topk_kernel<true>, dim3((unsigned)rows), dim3(kTopkThreads), lds, stream, p);
   else
