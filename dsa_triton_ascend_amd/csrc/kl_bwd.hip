@@ -749,7 +749,9 @@ __global__ __launch_bounds__(1024) void kl_scan_kernel(const int32_t* cnt, int32
 // dKi[t] = sum of the token's slot contributions, in int64 fixed point with
 // the exponent fixed by the token's largest row maximum and slot count (no
 // partial sum can overflow).  A token's slots are split into up to
-// kKlReduceParts parts of at least kKlReduceChunk slots, one wave each: a
+// `parts` (at most kKlReduceParts) parts of at least kKlReduceChunk slots,
+// one wave each; the host sets `parts` from the average slots per token, so
+// that sparsely hit tokens keep a grid of one wave per token: a
 // token with one part writes dKi directly; the parts of a longer token add
 // their partial sums into an int64 accumulator with integer atomics, which
 // kl_reduce_finish_kernel converts.  Integer addition is exact and
@@ -757,8 +759,8 @@ __global__ __launch_bounds__(1024) void kl_scan_kernel(const int32_t* cnt, int32
 constexpr int kKlReduceParts = 16;
 constexpr int kKlReduceChunk = 256;
 
-__device__ __forceinline__ int kl_reduce_parts(int len) {
-  return max(1, min(kKlReduceParts, (len + kKlReduceChunk - 1) / kKlReduceChunk));
+__device__ __forceinline__ int kl_reduce_parts(int len, int parts) {
+  return max(1, min(parts, (len + kKlReduceChunk - 1) / kKlReduceChunk));
 }
 // fixed-point exponent: len * bm < 2^(62 - e)
 __device__ __forceinline__ int kl_fixed_exp(float bm, int len) {
@@ -771,14 +773,14 @@ template <typename T>
 __global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, const int32_t* rowexp,
                                                         const uint32_t* tokmax, const int32_t* offs,
                                                         const int32_t* list, long long* acc, T* dki, int ntok,
-                                                        int topk) {
+                                                        int topk, int parts) {
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int t = w / kKlReduceParts, part = w - t * kKlReduceParts;
+  const int t = w / parts, part = w - t * parts;
   const int lane = threadIdx.x & 63;
   if (t >= ntok) return;
   const int o0 = __builtin_amdgcn_readfirstlane(offs[t]);
   const int len = __builtin_amdgcn_readfirstlane(offs[t + 1]) - o0;
-  const int np = kl_reduce_parts(len);
+  const int np = kl_reduce_parts(len, parts);
   if (part >= np) return;
   const float bm = __uint_as_float(tokmax[t]);
   T* dst = dki + (int64_t)t * kKlDi + 2 * lane;
@@ -837,12 +839,12 @@ __global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, co
 // dKi of the tokens with more than one part, from their accumulators
 template <typename T>
 __global__ __launch_bounds__(256) void kl_reduce_finish_kernel(const uint32_t* tokmax, const int32_t* offs,
-                                                               const long long* acc, T* dki, int ntok) {
+                                                               const long long* acc, T* dki, int ntok, int parts) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (t >= ntok) return;
   const int len = offs[t + 1] - offs[t];
-  if (kl_reduce_parts(len) == 1) return;
+  if (kl_reduce_parts(len, parts) == 1) return;
   const float bm = __uint_as_float(tokmax[t]);
   if (!(bm < INFINITY)) return;
   const int e = bm > 0.f ? kl_fixed_exp(bm, len) : 0;
@@ -1032,20 +1034,25 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   DSA_HIP(hipGetLastError());
   hipLaunchKernelGGL(kl_bucket_kernel<true>, bgrid, dim3(256), 0, stream, s);
   DSA_HIP(hipGetLastError());
-  const dim3 rgrid((unsigned)((tokens * kKlReduceParts + 3) / 4));
+  // parts per token: about avg_slots / 64, 1..kKlReduceParts (long causal
+  // rows give every early token thousands of slots; a long context with
+  // few slots per token keeps one wave per token)
+  const int64_t avg = tokens > 0 ? rows * topk / tokens : 0;
+  const int parts = (int)std::max<int64_t>(1, std::min<int64_t>(kKlReduceParts, (avg + 63) / 64));
+  const dim3 rgrid((unsigned)((tokens * parts + 3) / 4));
   const dim3 fgrid((unsigned)((tokens + 3) / 4));
   if (bf) {
     hipLaunchKernelGGL(kl_reduce_kernel<bf16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowexp, s.tokmax, s.offs,
-                       s.list, acc, (bf16*)d_key_index, (int)tokens, (int)topk);
+                       s.list, acc, (bf16*)d_key_index, (int)tokens, (int)topk, parts);
     DSA_HIP(hipGetLastError());
     hipLaunchKernelGGL(kl_reduce_finish_kernel<bf16>, fgrid, dim3(256), 0, stream, s.tokmax, s.offs, acc,
-                       (bf16*)d_key_index, (int)tokens);
+                       (bf16*)d_key_index, (int)tokens, parts);
   } else {
     hipLaunchKernelGGL(kl_reduce_kernel<f16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowexp, s.tokmax, s.offs,
-                       s.list, acc, (f16*)d_key_index, (int)tokens, (int)topk);
+                       s.list, acc, (f16*)d_key_index, (int)tokens, (int)topk, parts);
     DSA_HIP(hipGetLastError());
     hipLaunchKernelGGL(kl_reduce_finish_kernel<f16>, fgrid, dim3(256), 0, stream, s.tokmax, s.offs, acc,
-                       (f16*)d_key_index, (int)tokens);
+                       (f16*)d_key_index, (int)tokens, parts);
   }
   DSA_HIP(hipGetLastError());
   hipLaunchKernelGGL(kl_loss_kernel, dim3(1), dim3(256), 0, stream, p.loss_part, (int)rows, loss);
