@@ -1017,11 +1017,17 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   s.list = (int32_t*)(ws + L.list);
   long long* acc = (long long*)(ws + L.acc);
 
-  // counters, token maxima and accumulators (cnt .. offs) cleared by a
-  // kernel (no memset nodes when the caller captures).  The count pass
-  // records each slot's rank in its bucket and the token maxima; the fill
-  // pass then places the slots without atomics.
-  const int64_t zn = (int64_t)((L.offs - L.cnt) / sizeof(int32_t));
+  // parts per token of the dKi reduction: about avg_slots / 64,
+  // 1..kKlReduceParts (long causal rows give every early token thousands of
+  // slots; a long context with few slots per token keeps one wave per token)
+  const int64_t avg = tokens > 0 ? rows * topk / tokens : 0;
+  const int parts = (int)std::max<int64_t>(1, std::min<int64_t>(kKlReduceParts, (avg + 63) / 64));
+  // counters, token maxima and (when tokens are split) the accumulators,
+  // cnt .. acc or cnt .. offs, cleared by a kernel (no memset nodes when the
+  // caller captures).  The count pass records each slot's rank in its
+  // bucket and the token maxima; the fill pass then places the slots
+  // without atomics.
+  const int64_t zn = (int64_t)(((parts > 1 ? L.offs : L.acc) - L.cnt) / sizeof(int32_t));
   hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((zn + 255) / 256)), dim3(256), 0, stream, s.cnt, zn);
   DSA_HIP(hipGetLastError());
   const bool bf = dtype == DSA_DTYPE_BF16;
@@ -1034,11 +1040,6 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   DSA_HIP(hipGetLastError());
   hipLaunchKernelGGL(kl_bucket_kernel<true>, bgrid, dim3(256), 0, stream, s);
   DSA_HIP(hipGetLastError());
-  // parts per token: about avg_slots / 64, 1..kKlReduceParts (long causal
-  // rows give every early token thousands of slots; a long context with
-  // few slots per token keeps one wave per token)
-  const int64_t avg = tokens > 0 ? rows * topk / tokens : 0;
-  const int parts = (int)std::max<int64_t>(1, std::min<int64_t>(kKlReduceParts, (avg + 63) / 64));
   const dim3 rgrid((unsigned)((tokens * parts + 3) / 4));
   const dim3 fgrid((unsigned)((tokens + 3) / 4));
   if (bf) {
