@@ -5,6 +5,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+
 #include "common.h"
 
 namespace dsa {
@@ -24,16 +26,17 @@ int hip_fail(hipError_t e, const char* what) {
 }
 
 int device_cu_count() {
-  static int cached[64] = {0};
+  // per-device cache; concurrent first calls store the same value
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int cus = 0;
+  int cus = cached[dev].load(std::memory_order_relaxed);
+  if (!cus) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
       cus = 256;
-    cached[dev] = cus;
+    cached[dev].store(cus, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return cus;
 }
 
 // sfa_fwd.hip

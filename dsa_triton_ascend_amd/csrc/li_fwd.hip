@@ -907,14 +907,16 @@ int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_
 // round would leave most CUs idle while it runs).
 template <int D, typename T, int GT>
 static hipError_t launch_score(LiParams p, hipStream_t stream) {
-  static int occ = 0;
-  if (!occ) {
+  // Occupancy depends only on the kernel and the architecture (every device
+  // this library runs on is gfx950); the local static's initialisation is
+  // thread-safe.
+  static const int occ = [] {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, li_score_kernel<D, T, GT>, kLiThreads, 0) != hipSuccess ||
         n < 1)
       n = 1;
-    occ = n;
-  }
+    return n;
+  }();
   const int64_t rows = p.q_rows * p.n2;
   const int64_t target = (int64_t)device_cu_count() * occ;
   const int64_t per_row = rows >= target ? 1 : (target + rows - 1) / rows;

@@ -259,6 +259,8 @@ class DenseLightningIndexerSoftmaxLseTriton(torch.nn.Module):
             layout=self.layout, sparse_mode=self.sparse_mode, pre_tokens=self.pre_tokens,
             next_tokens=self.next_tokens)
 
+    construct = forward
+
 
 class DenseLossBackwardTriton(torch.nn.Module):
     """Module form (dense_loss_backward_triton.py:948-984)."""
@@ -281,6 +283,8 @@ class DenseLossBackwardTriton(torch.nn.Module):
             softmax_sum_index, effective_scale, query_rope=query_rope, key_rope=key_rope,
             actual_seq_qlen=actual_seq_qlen, actual_seq_klen=actual_seq_klen, layout=self.layout,
             sparse_mode=self.sparse_mode, pre_tokens=self.pre_tokens, next_tokens=self.next_tokens)
+
+    construct = forward
 
 
 class DenseLightningIndexerGradKLLossTriton(DenseLossBackwardTriton):

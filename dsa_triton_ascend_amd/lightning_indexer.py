@@ -212,18 +212,21 @@ def _lightning_indexer_paged(query, key, weights, actual_seq_lengths_query, actu
 
 
 class LightningIndexerTriton(torch.nn.Module):
-    """Module form (lightning_indexer_triton.py:416-459)."""
+    """Module form (lightning_indexer_triton.py:416-459).  The constructor
+    takes the reference's positional order (419-427): sparse_count,
+    sparse_mode, layout_query, layout_key, return_value, pre_tokens,
+    next_tokens."""
 
     def __init__(self, sparse_count=2048, sparse_mode=3, layout_query="BSND", layout_key="BSND",
-                 pre_tokens=INT64_MAX, next_tokens=INT64_MAX, return_value=False):
+                 return_value=False, pre_tokens=INT64_MAX, next_tokens=INT64_MAX):
         super().__init__()
         self.sparse_count = sparse_count
         self.sparse_mode = sparse_mode
         self.layout_query = layout_query
         self.layout_key = layout_key
+        self.return_value = return_value
         self.pre_tokens = pre_tokens
         self.next_tokens = next_tokens
-        self.return_value = return_value
 
     def forward(self, query, key, weights, actual_seq_lengths_query=None,
                 actual_seq_lengths_key=None, block_table=None):
@@ -231,6 +234,8 @@ class LightningIndexerTriton(torch.nn.Module):
             query, key, weights, actual_seq_lengths_query, actual_seq_lengths_key, block_table,
             self.layout_query, self.layout_key, self.sparse_count, self.sparse_mode,
             self.pre_tokens, self.next_tokens, self.return_value)
+
+    construct = forward
 
 
 def indexer_scores(query, key, weights, actual_seq_lengths_query=None, actual_seq_lengths_key=None,

@@ -35,6 +35,18 @@ def _seq_tensor(x, device):
     return torch.tensor(list(x), dtype=torch.int32, device=device)
 
 
+def _expect_shape(t, shape, name):
+    """Raise ValueError unless ``t`` has exactly ``shape``: the kernels index
+    every operand by these sizes, so a mismatch would read out of bounds."""
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+
+
+def _expect_numel(t, n, name):
+    if t.numel() != n:
+        raise ValueError(f"{name} must have {n} elements, got {t.numel()} (shape {tuple(t.shape)})")
+
+
 def _check_device(*tensors):
     dev = None
     for t in tensors:
@@ -97,7 +109,7 @@ def sparse_flash_attention_triton(
     is_tnd_q = layout_query == "TND"
     is_tnd_kv = layout_kv == "TND"
     is_pa = layout_kv == "PA_BSND"
-    device = _check_device(query, key, query_rope, key_rope, sparse_indices, block_table)
+    device = query.device
 
     # ---- shapes (reference 577-586) ----
     if is_tnd_q:
@@ -160,6 +172,14 @@ def sparse_flash_attention_triton(
     if sparse_indices.numel() != q_rows * K:
         raise ValueError(f"sparse_indices shape {tuple(sparse_indices.shape)} does not match "
                          f"{q_rows} query rows")
+    if key.dim() != (3 if is_tnd_kv else 4) or key.shape[-1] != D:
+        raise ValueError(f"key must be {'[T2,1,D]' if is_tnd_kv else '[B,S2,1,D]'} with D={D}, "
+                         f"got {tuple(key.shape)}")
+    _expect_shape(query_rope, tuple(query.shape[:-1]) + (D_ROPE,), "query_rope")
+    _expect_shape(key_rope, tuple(key.shape[:-1]) + (D_ROPE,), "key_rope")
+    if is_pa and (bt.dim() != 2 or bt.shape[0] < B):
+        raise ValueError(f"block_table must be [B, max_blocks] with B={B} rows, got {tuple(bt.shape)}")
+    _check_device(query, key, query_rope, key_rope, sparse_indices, block_table)
 
     q = query.contiguous()
     qr = query_rope.contiguous()

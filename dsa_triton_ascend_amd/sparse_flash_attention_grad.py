@@ -15,7 +15,8 @@ resolved in the kernel (no host unpacking).
 import torch
 
 from . import _lib
-from .sparse_flash_attention import INT64_MAX, _check_device, _seq_tensor, _VALID_D, _VALID_N1
+from .sparse_flash_attention import (INT64_MAX, _check_device, _expect_numel, _expect_shape, _seq_tensor,
+                                     _VALID_D, _VALID_N1)
 
 _D_ROPE = 64
 
@@ -69,8 +70,7 @@ def _sfa_grad(query, key, value, sparse_indices, d_out, out, softmax_max, softma
     if layout not in ("BSND", "TND"):
         raise ValueError(f"layout must be BSND or TND, got {layout}")
     is_tnd = layout == "TND"
-    device = _check_device(query, key, query_rope, key_rope, sparse_indices, d_out, out,
-                           softmax_max, softmax_sum)
+    device = query.device
 
     if is_tnd:
         if actual_seq_lengths_query is None or actual_seq_lengths_kv is None:
@@ -105,6 +105,19 @@ def _sfa_grad(query, key, value, sparse_indices, d_out, out, softmax_max, softma
         if t.dtype != query.dtype:
             raise ValueError(f"{nm} must have the query dtype")
     K = sparse_indices.shape[-1]
+    # every operand is indexed by these sizes in the kernel: check them before any launch
+    if key.shape[-1] != D:
+        raise ValueError(f"key head dim {key.shape[-1]} differs from the query's {D}")
+    _expect_numel(sparse_indices, q_rows * K, "sparse_indices")
+    _expect_numel(softmax_max, q_rows * N1, "softmax_max")
+    _expect_numel(softmax_sum, q_rows * N1, "softmax_sum")
+    _expect_shape(d_out, query.shape, "d_out")
+    _expect_shape(out, query.shape, "out")
+    _expect_shape(query_rope, tuple(query.shape[:-1]) + (D_ROPE,), "query_rope")
+    _expect_shape(key_rope, tuple(key.shape[:-1]) + (D_ROPE,), "key_rope")
+    if (act_k is not None and act_k.numel() != B) or (act_q is not None and act_q.numel() != B):
+        raise ValueError("actual sequence length arrays must have one entry per batch")
+    _check_device(query, key, query_rope, key_rope, sparse_indices, d_out, out, softmax_max, softmax_sum)
 
     dq = torch.empty_like(query)
     dqr = torch.empty_like(query_rope)
@@ -154,3 +167,5 @@ class SparseFlashAttentionGradTriton(torch.nn.Module):
             self.scale_value, query_rope, key_rope, actual_seq_lengths_query, actual_seq_lengths_kv,
             self.sparse_block_size, self.layout, self.sparse_mode, self.pre_tokens,
             self.next_tokens, self.deterministic)
+
+    construct = forward

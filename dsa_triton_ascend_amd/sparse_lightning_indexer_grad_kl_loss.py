@@ -201,3 +201,5 @@ class SparseLightningIndexerGradKLLossTriton(torch.nn.Module):
             actual_seq_klen=actual_seq_klen, scale_value=self.scale_value, layout=self.layout,
             sparse_mode=self.sparse_mode, pre_tokens=self.pre_tokens, next_tokens=self.next_tokens,
             deterministic=self.deterministic, block_table=block_table)
+
+    construct = forward
