@@ -25,6 +25,8 @@ DTYPE_FP32 = 2
 
 LAYOUT = {"BSND": 0, "TND": 1, "PA_BSND": 2}
 
+TEST_FORCE_GLOBAL_GATHER = 1
+
 _c = ctypes
 _vp = _c.c_void_p
 _i32p = _c.c_void_p
@@ -37,6 +39,7 @@ _sz = _c.c_size_t
 SIGNATURES = {
     "dsa_last_error": (_c.c_char_p, []),
     "dsa_abi_version": (_c.c_int, []),
+    "dsa_set_test_flags": (None, [_i32]),
     "dsa_sfa_fwd": (_c.c_int, [
         _vp, _vp, _vp, _vp, _i32p,           # query, query_rope, key, key_rope, sparse_indices
         _vp, _vp, _vp,                        # attention_out, softmax_max, softmax_sum

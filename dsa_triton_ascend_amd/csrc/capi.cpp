@@ -20,6 +20,9 @@ void set_error(const char* fmt, ...) {
   va_end(ap);
 }
 
+static std::atomic<int> g_test_flags{0};
+int test_flags() { return g_test_flags.load(std::memory_order_relaxed); }
+
 int hip_fail(hipError_t e, const char* what) {
   set_error("HIP error in %s: %s", what, hipGetErrorString(e));
   return DSA_ERR_HIP;
@@ -151,6 +154,8 @@ extern "C" {
 const char* dsa_last_error(void) { return g_err; }
 
 int dsa_abi_version(void) { return 1; }
+
+void dsa_set_test_flags(int32_t flags) { g_test_flags.store(flags, std::memory_order_relaxed); }
 
 size_t dsa_sfa_fwd_workspace_size(int64_t q_rows, int64_t n1, int64_t d, int64_t sparse_count,
                                   int32_t sparse_block_size) {

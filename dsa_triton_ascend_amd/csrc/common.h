@@ -133,6 +133,9 @@ void set_error(const char* fmt, ...);
 int hip_fail(hipError_t e, const char* what);
 // CUs of the current device (cached per device; 256 when it cannot be queried)
 int device_cu_count();
+// Test hooks set by dsa_set_test_flags (0 in normal use).
+constexpr int kTestForceGlobalGather = 1;  // gather with 64-bit addresses even below 2 GiB
+int test_flags();
 }  // namespace dsa
 
 #define DSA_CHECK_ARG(cond, ...)                                  \

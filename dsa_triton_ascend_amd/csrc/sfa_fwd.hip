@@ -101,7 +101,11 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
 // BUF: gather with buffer loads (32-bit offsets, key tensors under 2 GiB;
 // the hardware range check yields the zero rows); otherwise 64-bit global
 // addresses with an explicit zero row.
-template <int D, typename T, int HT, int NW, bool BUF>
+// CH: the split's position range may exceed kSfaMaxList and is compacted
+// and run in chunks.  A separate instantiation: the chunk loop around the
+// tile loop costs the D = 512 kernel registers it does not have (it spills),
+// so ranges that fit one list run the kernel without it.
+template <int D, typename T, int HT, int NW, bool BUF, bool CH>
 __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   using E = Elem<T>;
   using V8 = typename E::v8;
@@ -141,6 +145,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   // from LDS by GEMM1's last k-steps instead of held in registers
   __shared__ __attribute__((aligned(16))) unsigned char s_q[HEADS_PER_WG * QL * 64];
   __shared__ int s_wcnt[NW];
+  __shared__ RowInfo s_ri;  // the row's lengths, for compacting chunks after the first
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -159,6 +164,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   if (row >= p.rows) return;
 
   const RowInfo ri = sfa_row_info(p, (int)row);
+  if (tid == 0) s_ri = ri;
   const int32_t* idx_row = p.idx + row * p.K;
   const int total_pos = p.K * p.bs;
   const int p0 = split * p.pos_per_split;
@@ -204,12 +210,17 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   if (q_early) load_q();
 
   // ---- compact attended positions into s_list (stable order) ----
+  // The split's positions are taken in chunks of at most kSfaMaxList: a
+  // chunk is compacted into s_list and its tiles are run before the next
+  // chunk is compacted; the online-softmax state and the O accumulators
+  // carry over in registers, so a long range needs no extra split.
   // The first round's index entries are loaded first.  A PA_BSND row's
   // block table is then staged in the unused tail of s_list (loaded while
   // the index loads are in flight), so that resolving a page costs an LDS
   // read instead of a second dependent global load.  Only the waves that
   // resolve positions load it: the others have their Q loads in flight,
   // ahead of anything they would issue now.
+  const int n_chunks = p1 > p0 ? (CH ? (p1 - p0 + kSfaMaxList - 1) / kSfaMaxList : 1) : 0;
   const int first_id = p0 + tid < p1 ? sfa_load_id(p, idx_row, p0 + tid) : -1;
   const int32_t* tab = nullptr;
   if (p.layout_kv == DSA_LAYOUT_PA_BSND) {
@@ -224,33 +235,59 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
       tab = s_tab;
     }
   }
-  int n_valid = 0;
-  for (int c0 = p0; c0 < p1; c0 += NTHR) {
-    int pos = c0 + tid;
-    int phys = 0;
-    bool valid = false;
-    // the index load does not wait for the row's lengths (act_q / act_k)
-    const int id = c0 == p0 ? first_id : (pos < p1 ? sfa_load_id(p, idx_row, pos) : -1);
-    if (ri.active && pos < p1) valid = sfa_resolve_id(p, ri, id, pos, &phys, tab);
-    unsigned long long m = __ballot(valid);
-    if (lane == 0) s_wcnt[wave] = __popcll(m);
-    lds_barrier();
-    int off = n_valid;
-    int tot = 0;
+  int n_valid = 0, n_tiles = 0;
+  // Compacts chunk c (every wave takes part; the barriers also order the
+  // list's reuse after the previous chunk's tiles).  Chunk 0 resolves with
+  // the values at hand; later chunks (CH kernels only) re-derive the row's
+  // position, lengths and index pointer from blockIdx, the kernel arguments
+  // and s_ri instead of holding them in registers across the tile loop.
+  auto compact_range = [&](int cb, int ce, const RowInfo& rc, const int32_t* irow, const int32_t* tb,
+                           bool first) {
+    n_valid = 0;
+    for (int c0 = cb; c0 < ce; c0 += NTHR) {
+      int pos = c0 + tid;
+      int phys = 0;
+      bool valid = false;
+      // the index load does not wait for the row's lengths (act_q / act_k)
+      const int id = (first && c0 == cb) ? first_id : (pos < ce ? sfa_load_id(p, irow, pos) : -1);
+      if (rc.active && pos < ce) valid = sfa_resolve_id(p, rc, id, pos, &phys, tb);
+      unsigned long long m = __ballot(valid);
+      if (lane == 0) s_wcnt[wave] = __popcll(m);
+      lds_barrier();
+      int off = n_valid;
+      int tot = 0;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      int c = s_wcnt[w];
-      off += (w < wave) ? c : 0;
-      tot += c;
+      for (int w = 0; w < NW; ++w) {
+        const int cw = s_wcnt[w];
+        off += (w < wave) ? cw : 0;
+        tot += cw;
+      }
+      if (valid) s_list[off + __popcll(m & ((1ull << lane) - 1ull))] = phys;
+      n_valid += tot;
+      lds_barrier();
     }
-    if (valid) s_list[off + __popcll(m & ((1ull << lane) - 1ull))] = phys;
-    n_valid += tot;
+    // pad the list to a whole tile with -1 so tile loads index it unconditionally
+    if (tid < TILE) s_list[n_valid + tid] = -1;
     lds_barrier();
-  }
-  // pad the list to a whole tile with -1 so tile loads index it unconditionally
-  if (tid < TILE) s_list[n_valid + tid] = -1;
-  lds_barrier();
-  const int n_tiles = (n_valid + TILE - 1) / TILE;
+    n_tiles = (n_valid + TILE - 1) / TILE;
+  };
+  auto compact = [&](int c) {
+    if (c == 0) {
+      compact_range(p0, min(p1, p0 + kSfaMaxList), ri, idx_row, tab, true);
+      return;
+    }
+    int bl = blockIdx.x;
+    asm volatile("" : "+s"(bl));
+    const int jr2 = (bl >> 3) / hgroups;
+    const int64_t row2 = (int64_t)(bl & 7) * p.rows_per_xcd + jr2 / p.splits;
+    const int q0 = (jr2 % p.splits) * p.pos_per_split;
+    const int q1 = min(p.K * p.bs, q0 + p.pos_per_split);
+    const RowInfo rc = s_ri;
+    const int32_t* tb = p.layout_kv == DSA_LAYOUT_PA_BSND ? p.block_table + (int64_t)rc.b * p.max_blocks : nullptr;
+    const int cb = q0 + c * kSfaMaxList;
+    compact_range(cb, min(q1, cb + kSfaMaxList), rc, p.idx + row2 * p.K, tb, false);
+  };
+  if (n_chunks > 0) compact(0);
 
   // ---- tile gather: global -> LDS by DMA, swizzled rows ----
   // nope: DMA i of wave w covers tokens (i*NW + w)*TPI .. +TPI, lane L holds
@@ -364,7 +401,21 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
       wait_vmcnt<0>();
     };
     gather_only(false);
-    if (__syncthreads_or(0)) gather_only(true);
+    if constexpr (CH)
+      for (int c = 1; c < n_chunks; ++c) {
+        compact(c);
+        gather_only(true);
+      }
+    if (__syncthreads_or(0)) {
+      if constexpr (CH) {
+        for (int c = 0; c < (n_chunks > 0 ? n_chunks : 1); ++c) {
+          if (n_chunks > 1) compact(c);
+          gather_only(true);
+        }
+      } else {
+        gather_only(true);
+      }
+    }
     return;
   }
 
@@ -596,8 +647,13 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
     for (int ht = 0; ht < HT; ++ht) acc_o[dt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  if (kSplitP && n_valid >= kLoSplitMinTokens) run_tiles(false, LoOff{});
-  else run_tiles(false, LoOn{});
+  // chunk 0 is compacted and its first tiles are in flight; later chunks
+  // are compacted here and issue their own first tiles
+  for (int c = 0; c < (CH && n_chunks > 0 ? n_chunks : 1); ++c) {
+    if (CH && c > 0) compact(c);
+    if (kSplitP && n_valid >= kLoSplitMinTokens) run_tiles(c > 0, LoOff{});
+    else run_tiles(c > 0, LoOn{});
+  }
   if (__syncthreads_or(overflow ? 1 : 0)) {
     // rare: some head's score exceeded the reference by 2^kRefSlack; redo
     // the row with the exact maxima found by the first pass
@@ -610,7 +666,11 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
     for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int ht = 0; ht < HT; ++ht) acc_o[dt][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    run_tiles(true, LoOn{});  // rare second pass: always with the lo part
+    // rare second pass: always with the lo part
+    for (int c = 0; c < (CH && n_chunks > 0 ? n_chunks : 1); ++c) {
+      if (CH && n_chunks > 1) compact(c);
+      run_tiles(true, LoOn{});
+    }
   }
 
   // ---- epilogue ----
@@ -821,21 +881,22 @@ template <int D> struct SfaCfg {
 };
 constexpr int kSfaHeadsPerWg = 128;
 
-// Token splits: enough (row, split) workgroups to fill the CUs, at least
-// 256 positions per split, at most kSfaMaxList.  The workspace query and
-// the launch use the same count.
+// Token splits: when the (row, head group) units fill fewer than half the
+// CUs, enough splits to fill them, with at least 256 positions per split.
+// From half the CUs up one split per unit: two splits of half the work
+// would take the same two rounds on the CUs, plus the merge.  A split's
+// range has no length limit (it is compacted in chunks), so the split
+// workspace is below (cus + units) <= 1.5 * cus partial rows of N1 heads
+// (about 51 MB at 256 CUs, N1 = 128, D = 512).  The workspace query and the
+// launch use the same count.
 static int sfa_fwd_plan_splits(int64_t rows, int64_t n1, int64_t total_pos) {
   const int cus = device_cu_count();
   const int64_t units = rows * ((n1 + kSfaHeadsPerWg - 1) / kSfaHeadsPerWg);
-  int64_t splits = 1;
-  if (units < cus) {
-    const int64_t want = (cus + units - 1) / units;
-    const int64_t by_len = (total_pos + 255) / 256;
-    splits = want < by_len ? want : by_len;
-    if (splits < 1) splits = 1;
-  }
-  while ((total_pos + splits - 1) / splits > kSfaMaxList) ++splits;
-  return (int)splits;
+  if (2 * units > cus) return 1;
+  const int64_t want = (cus + units - 1) / units;
+  const int64_t by_len = (total_pos + 255) / 256;
+  const int64_t splits = want < by_len ? want : by_len;
+  return splits < 1 ? 1 : (int)splits;
 }
 
 int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
@@ -854,15 +915,19 @@ static hipError_t launch_sfa_fwd(SfaFwdParams& p, hipStream_t stream) {
   const int64_t rows_per_xcd = (p.rows + 7) / 8;
   p.rows_per_xcd = (int)rows_per_xcd;
   const int64_t blocks = 8 * rows_per_xcd * p.splits * ((p.n1 + kSfaHeadsPerWg - 1) / kSfaHeadsPerWg);
-  const bool buf = p.kv_rows * (int64_t)D * 2 < (1ll << 31);
+  const bool buf = p.kv_rows * (int64_t)D * 2 < (1ll << 31) && !(test_flags() & kTestForceGlobalGather);
   using C = SfaCfg<D>;
   static_assert(C::NW * C::HT * 16 == kSfaHeadsPerWg, "heads per workgroup");
-  if (buf)
-    hipLaunchKernelGGL((sfa_fwd_kernel<D, T, C::HT, C::NW, true>), dim3((unsigned)blocks),
-                       dim3(C::NW * 64), 0, stream, p);
+  const bool chunked = p.pos_per_split > kSfaMaxList;
+  const dim3 grid((unsigned)blocks), block(C::NW * 64);
+  if (buf && !chunked)
+    hipLaunchKernelGGL((sfa_fwd_kernel<D, T, C::HT, C::NW, true, false>), grid, block, 0, stream, p);
+  else if (buf)
+    hipLaunchKernelGGL((sfa_fwd_kernel<D, T, C::HT, C::NW, true, true>), grid, block, 0, stream, p);
+  else if (!chunked)
+    hipLaunchKernelGGL((sfa_fwd_kernel<D, T, C::HT, C::NW, false, false>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((sfa_fwd_kernel<D, T, C::HT, C::NW, false>), dim3((unsigned)blocks),
-                       dim3(C::NW * 64), 0, stream, p);
+    hipLaunchKernelGGL((sfa_fwd_kernel<D, T, C::HT, C::NW, false, true>), grid, block, 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) return e;
   const int64_t cblocks = (p.rows * p.n1 + 3) / 4;

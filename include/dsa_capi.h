@@ -56,6 +56,16 @@ const char* dsa_last_error(void);
 int dsa_abi_version(void);
 
 /*
+ * Test hook, no counterpart in the reference: flags that route calls through
+ * code paths normal sizes do not reach, so that tests can run them at small
+ * shapes.  Bit 0 (DSA_TEST_FORCE_GLOBAL_GATHER): the kernels gather key rows
+ * with 64-bit global addresses, the path key tensors of 2 GiB or more take,
+ * instead of 32-bit buffer offsets.  Process-wide; 0 in normal use.
+ */
+#define DSA_TEST_FORCE_GLOBAL_GATHER 1
+void dsa_set_test_flags(int32_t flags);
+
+/*
  * Sparse flash attention forward, MLA-absorb (value = key[..., :D]), MQA (N2 = 1).
  * Replaces the reference core `_sfa_core` (sparse_flash_attention_triton.py:445-477)
  * and the host-side layout normalisation around it (551-611): TND rows,

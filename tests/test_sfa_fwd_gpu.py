@@ -375,10 +375,10 @@ def test_fwd_split_shapes_in_sequence():
         assert_close(ssum, ref[2], RTOL, ATOL, "softmax_sum")
 
 
-def test_fwd_forced_split_many_rows():
-    """Index lists longer than one workgroup's list (2048 positions) force a
-    token split even when the rows fill the CUs."""
-    print("[sfa_fwd split] forced split, 1100 rows", flush=True)
+def test_fwd_long_lists_many_rows():
+    """Index lists longer than one workgroup's list (2048 positions) with
+    rows that fill the CUs: one split per row, compacted and run in chunks."""
+    print("[sfa_fwd chunks] 4096 positions, 1100 rows", flush=True)
     dtype = torch.bfloat16
     B, S1, S2, N1, K, D = 1, 1100, 4096, 1, 4096, 128
     q, k, qr, kr = sfa_inputs(B, S1, S2, N1, D, dtype, seed=91)
@@ -446,3 +446,84 @@ def test_fwd_mixed_layouts(combo):
     assert_close(out.float().cpu().numpy(), ref[0], RTOL, ATOL, f"{combo} out")
     assert_close(smax.cpu().numpy(), ref[1], RTOL, ATOL, f"{combo} smax")
     assert_close(ssum.cpu().numpy(), ref[2], RTOL, ATOL, f"{combo} ssum")
+
+
+# Block-wise indices expand to more positions than one compaction chunk
+# (2048): prefill-like row counts (one split per row) and few rows (token
+# splits whose ranges span several chunks).
+CHUNK_CASES = [
+    # B, S1, S2, N1, K (blocks), bs, mode, D
+    (1, 160, 8192, 16, 40, 128, 3, 128),
+    (1, 40, 16384, 16, 128, 128, 0, 128),
+    (2, 3, 8192, 32, 48, 128, 3, 512),
+]
+
+
+@pytest.mark.parametrize("B,S1,S2,N1,K,bs,mode,D", CHUNK_CASES)
+def test_fwd_block_indices_span_chunks(B, S1, S2, N1, K, bs, mode, D):
+    print(f"[sfa_fwd chunks] B={B} S1={S1} S2={S2} N1={N1} K={K} bs={bs} mode={mode} D={D}", flush=True)
+    dtype = torch.bfloat16
+    q, k, qr, kr = sfa_inputs(B, S1, S2, N1, D, dtype, seed=101)
+    si = sparse_indices(B, S1, S2, K, bs, mode, seed=102)
+    scale = 1.0 / np.sqrt(D + 64)
+    out, smax, ssum = _run(q, k, qr, kr, si, dtype, scale, mode, bs)
+    ref = sfa_fwd_bsnd(q, k, si, qr, kr, scale, [S1] * B, [S2] * B, bs, mode, True, "float32",
+                       positions="kernel")
+    assert_close(out, ref[0], RTOL, ATOL, "attention_out")
+    assert_close(smax, ref[1], RTOL, ATOL, "softmax_max")
+    assert_close(ssum, ref[2], RTOL, ATOL, "softmax_sum")
+
+
+def test_fwd_split_workspace_is_bounded():
+    """The split workspace stays below 1.5 CUs' worth of partial rows for any
+    index length (no split is forced by the list length)."""
+    from dsa_triton_ascend_amd import _lib
+    lib = _lib.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    bound = int(1.5 * cus) * 128 * (512 * 2 + 16)
+    for rows in (1, 7, 32, 100, 128, 129, 255, 256, 8192):
+        for k, bs in ((2048, 1), (2048, 128), (4096, 1), (64, 64)):
+            ws = lib.dsa_sfa_fwd_workspace_size(rows, 128, 512, k, bs)
+            assert ws <= bound, (rows, k, bs, ws)
+    assert lib.dsa_sfa_fwd_workspace_size(8192, 128, 512, 2048, 128) == 0
+
+
+GLOBAL_GATHER_CASES = [CASES[0], CASES[2], CASES[3], CASES[10]]
+
+
+@pytest.mark.parametrize("B,S1,S2,N1,K,bs,mode,D", GLOBAL_GATHER_CASES)
+def test_fwd_global_address_gather(B, S1, S2, N1, K, bs, mode, D):
+    """The gather path of key tensors of 2 GiB or more (64-bit global
+    addresses, explicit zero row) forced at small shapes."""
+    from dsa_triton_ascend_amd import _lib
+    print(f"[sfa_fwd global gather] B={B} S1={S1} S2={S2} N1={N1} K={K} bs={bs} D={D}", flush=True)
+    dtype = torch.bfloat16
+    q, k, qr, kr = sfa_inputs(B, S1, S2, N1, D, dtype)
+    si = sparse_indices(B, S1, S2, K, bs, mode)
+    scale = 1.0 / np.sqrt(D + 64)
+    lib = _lib.load()
+    lib.dsa_set_test_flags(_lib.TEST_FORCE_GLOBAL_GATHER)
+    try:
+        out, smax, ssum = _run(q, k, qr, kr, si, dtype, scale, mode, bs)
+    finally:
+        lib.dsa_set_test_flags(0)
+    ref = sfa_fwd_bsnd(q, k, si, qr, kr, scale, [S1] * B, [S2] * B, bs, mode, True, "float32",
+                       positions="kernel")
+    assert_close(out, ref[0], RTOL, ATOL, "attention_out")
+    assert_close(smax, ref[1], RTOL, ATOL, "softmax_max")
+    assert_close(ssum, ref[2], RTOL, ATOL, "softmax_sum")
+    # bit-identical to the buffer-offset path
+    out2, smax2, ssum2 = _run(q, k, qr, kr, si, dtype, scale, mode, bs)
+    np.testing.assert_array_equal(out, out2)
+    np.testing.assert_array_equal(ssum, ssum2)
+
+
+def test_fwd_global_address_gather_paged():
+    from dsa_triton_ascend_amd import _lib
+    print("[sfa_fwd global gather] paged with -1 pages", flush=True)
+    lib = _lib.load()
+    lib.dsa_set_test_flags(_lib.TEST_FORCE_GLOBAL_GATHER)
+    try:
+        test_fwd_paged_kv(True)
+    finally:
+        lib.dsa_set_test_flags(0)
