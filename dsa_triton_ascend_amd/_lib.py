@@ -51,6 +51,16 @@ SIGNATURES = {
         _vp, _sz, _vp,                        # workspace, workspace_bytes, stream
     ]),
     "dsa_sfa_fwd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32]),
+    "dsa_sfa_fwd_noalloc": (_c.c_int, [
+        _vp, _vp, _vp, _vp, _i32p,           # query, query_rope, key, key_rope, sparse_indices
+        _vp, _vp, _vp,                        # attention_out, softmax_max, softmax_sum
+        _i32p, _i32p, _i32p,                  # actual_seq_q, actual_seq_kv, block_table
+        _i64, _i64, _i64, _i64, _i64, _i64,   # batch, s1, s2, n1, d, d_rope
+        _i64, _i64, _i64, _i64, _i64,         # sparse_count, q_rows, kv_rows, max_blocks, page_size
+        _i32, _i32, _i32, _i32, _i32,         # sparse_block_size, sparse_mode, layout_q, layout_kv, dtype
+        _f32, _i32,                           # scale_value, return_lse
+        _vp,                                  # stream
+    ]),
     "dsa_sfa_bwd": (_c.c_int, [
         _vp, _vp, _vp, _vp, _i32p,           # query, query_rope, key, key_rope, sparse_indices
         _vp, _vp, _vp, _vp,                   # d_out, out, softmax_max, softmax_sum

@@ -46,6 +46,8 @@ int device_cu_count() {
 struct SfaFwdParams;
 int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos);
 size_t sfa_fwd_workspace_bytes(int64_t rows, int64_t n1, int64_t d, int64_t total_pos);
+size_t sfa_fwd_scratch_bytes();
+int sfa_fwd_scratch(void** ptr);
 int sfa_fwd_run(const void* query, const void* query_rope, const void* key, const void* key_rope,
                 const int32_t* sparse_indices, void* attention_out, float* softmax_max,
                 float* softmax_sum, const int32_t* actual_seq_q, const int32_t* actual_seq_kv,
@@ -147,32 +149,16 @@ static int li_check_scores(const void* query, const void* key, const void* weigh
 
 }  // namespace dsa
 
-using namespace dsa;
-
-extern "C" {
-
-const char* dsa_last_error(void) { return g_err; }
-
-int dsa_abi_version(void) { return 1; }
-
-void dsa_set_test_flags(int32_t flags) { g_test_flags.store(flags, std::memory_order_relaxed); }
-
-size_t dsa_sfa_fwd_workspace_size(int64_t q_rows, int64_t n1, int64_t d, int64_t sparse_count,
-                                  int32_t sparse_block_size) {
-  if (q_rows <= 0 || n1 <= 0 || d <= 0 || sparse_count <= 0 || sparse_block_size <= 0) return 0;
-  return sfa_fwd_workspace_bytes(q_rows, n1, d, sparse_count * (int64_t)sparse_block_size);
-}
-
-int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
-                const int32_t* sparse_indices, void* attention_out, float* softmax_max,
-                float* softmax_sum, const int32_t* actual_seq_q, const int32_t* actual_seq_kv,
-                const int32_t* block_table, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
-                int64_t d, int64_t d_rope, int64_t sparse_count, int64_t q_rows, int64_t kv_rows,
-                int64_t max_blocks, int64_t page_size, int32_t sparse_block_size,
-                int32_t sparse_mode, int32_t layout_query, int32_t layout_kv, int32_t dtype,
-                float scale_value, int32_t return_lse, void* workspace, size_t workspace_bytes,
-                void* stream) {
-  g_err[0] = '\0';
+namespace dsa {
+// argument checks shared by dsa_sfa_fwd and dsa_sfa_fwd_noalloc (HIP-free)
+static int sfa_fwd_check(const void* query, const void* query_rope, const void* key, const void* key_rope,
+                         const int32_t* sparse_indices, void* attention_out, float* softmax_max,
+                         float* softmax_sum, const int32_t* actual_seq_q, const int32_t* actual_seq_kv,
+                         const int32_t* block_table, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
+                         int64_t d, int64_t d_rope, int64_t sparse_count, int64_t q_rows, int64_t kv_rows,
+                         int64_t max_blocks, int64_t page_size, int32_t sparse_block_size,
+                         int32_t sparse_mode, int32_t layout_query, int32_t layout_kv, int32_t dtype,
+                         int32_t return_lse) {
   DSA_CHECK_ARG(query && query_rope && key && key_rope && sparse_indices && attention_out,
                 "null tensor pointer");
   DSA_CHECK_ARG(!return_lse || (softmax_max && softmax_sum),
@@ -215,6 +201,41 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, cons
     DSA_CHECK_ARG(s2 >= 1 && kv_rows == batch * s2, "kv_rows must equal B*S2 for BSND key");
   }
   DSA_CHECK_ARG(kv_rows >= 1 && kv_rows < (1ll << 31), "key must have between 1 and 2^31-1 rows");
+  return DSA_OK;
+}
+}  // namespace dsa
+
+using namespace dsa;
+
+extern "C" {
+
+const char* dsa_last_error(void) { return g_err; }
+
+int dsa_abi_version(void) { return 1; }
+
+void dsa_set_test_flags(int32_t flags) { g_test_flags.store(flags, std::memory_order_relaxed); }
+
+size_t dsa_sfa_fwd_workspace_size(int64_t q_rows, int64_t n1, int64_t d, int64_t sparse_count,
+                                  int32_t sparse_block_size) {
+  if (q_rows <= 0 || n1 <= 0 || d <= 0 || sparse_count <= 0 || sparse_block_size <= 0) return 0;
+  return sfa_fwd_workspace_bytes(q_rows, n1, d, sparse_count * (int64_t)sparse_block_size);
+}
+
+int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
+                const int32_t* sparse_indices, void* attention_out, float* softmax_max,
+                float* softmax_sum, const int32_t* actual_seq_q, const int32_t* actual_seq_kv,
+                const int32_t* block_table, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
+                int64_t d, int64_t d_rope, int64_t sparse_count, int64_t q_rows, int64_t kv_rows,
+                int64_t max_blocks, int64_t page_size, int32_t sparse_block_size,
+                int32_t sparse_mode, int32_t layout_query, int32_t layout_kv, int32_t dtype,
+                float scale_value, int32_t return_lse, void* workspace, size_t workspace_bytes,
+                void* stream) {
+  g_err[0] = '\0';
+  const int st = sfa_fwd_check(query, query_rope, key, key_rope, sparse_indices, attention_out, softmax_max, softmax_sum,
+                                 actual_seq_q, actual_seq_kv, block_table, batch, s1, s2, n1, d, d_rope,
+                                 sparse_count, q_rows, kv_rows, max_blocks, page_size, sparse_block_size,
+                                 sparse_mode, layout_query, layout_kv, dtype, return_lse);
+  if (st != DSA_OK) return st;
   const size_t need = sfa_fwd_workspace_bytes(q_rows, n1, d, sparse_count * (int64_t)sparse_block_size);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     set_error("workspace of %zu bytes required, %zu given", need, workspace_bytes);
@@ -225,6 +246,37 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, cons
                      sparse_count, q_rows, kv_rows, max_blocks, page_size, sparse_block_size,
                      sparse_mode, layout_query, layout_kv, dtype, scale_value, return_lse,
                      workspace, (hipStream_t)stream);
+}
+
+int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* key, const void* key_rope,
+                        const int32_t* sparse_indices, void* attention_out, float* softmax_max,
+                        float* softmax_sum, const int32_t* actual_seq_q, const int32_t* actual_seq_kv,
+                        const int32_t* block_table, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
+                        int64_t d, int64_t d_rope, int64_t sparse_count, int64_t q_rows, int64_t kv_rows,
+                        int64_t max_blocks, int64_t page_size, int32_t sparse_block_size,
+                        int32_t sparse_mode, int32_t layout_query, int32_t layout_kv, int32_t dtype,
+                        float scale_value, int32_t return_lse, void* stream) {
+  g_err[0] = '\0';
+  const int st = sfa_fwd_check(query, query_rope, key, key_rope, sparse_indices, attention_out, softmax_max, softmax_sum,
+                                 actual_seq_q, actual_seq_kv, block_table, batch, s1, s2, n1, d, d_rope,
+                                 sparse_count, q_rows, kv_rows, max_blocks, page_size, sparse_block_size,
+                                 sparse_mode, layout_query, layout_kv, dtype, return_lse);
+  if (st != DSA_OK) return st;
+  const size_t need = sfa_fwd_workspace_bytes(q_rows, n1, d, sparse_count * (int64_t)sparse_block_size);
+  void* ws = nullptr;
+  if (need > 0) {
+    DSA_CHECK_SUPPORTED(need <= sfa_fwd_scratch_bytes(),
+                        "these sizes need %zu bytes of split workspace, above the %zu-byte scratch of "
+                        "dsa_sfa_fwd_noalloc; call dsa_sfa_fwd with a workspace",
+                        need, sfa_fwd_scratch_bytes());
+    const int sst = sfa_fwd_scratch(&ws);
+    if (sst != DSA_OK) return sst;
+  }
+  return sfa_fwd_run(query, query_rope, key, key_rope, sparse_indices, attention_out, softmax_max,
+                     softmax_sum, actual_seq_q, actual_seq_kv, block_table, batch, s1, s2, n1, d,
+                     sparse_count, q_rows, kv_rows, max_blocks, page_size, sparse_block_size,
+                     sparse_mode, layout_query, layout_kv, dtype, scale_value, return_lse, ws,
+                     (hipStream_t)stream);
 }
 
 size_t dsa_sfa_bwd_workspace_size(int64_t kv_rows, int64_t d) {

@@ -28,6 +28,8 @@
 //  * When there are fewer rows than CUs the row's tokens are split across
 //    workgroups (all on one XCD) and a combine kernel merges the partial
 //    (O, max, sum) triples.
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -897,6 +899,52 @@ static int sfa_fwd_plan_splits(int64_t rows, int64_t n1, int64_t total_pos) {
   const int64_t by_len = (total_pos + 255) / 256;
   const int64_t splits = want < by_len ? want : by_len;
   return splits < 1 ? 1 : (int)splits;
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of dsa_sfa_fwd_noalloc: the split partials live in this
+// fixed-size device array instead of a caller's workspace, for callers that
+// cannot allocate (code under HIP graph capture, serving loops that forbid
+// hipMalloc).  Every GPU the library runs on holds its own copy until the
+// process ends.  64 MiB covers the split workspace of every shape on a
+// 256-CU device (at most 1.5 * CUs partial rows of N1 <= 128 heads: about
+// 51 MB at D = 512); larger needs are rejected.  Calls on one GPU share the
+// array: concurrent calls on one device race.  Every partial a launch reads
+// is written by the same launch, so nothing needs clearing between calls.
+// ---------------------------------------------------------------------------
+constexpr size_t kSfaScratchBytes = 64ull << 20;
+static __device__ __align__(256) unsigned char scratch[kSfaScratchBytes];
+
+// Device address of `scratch` per device, looked up once per device with
+// that device current.  The host-side name `scratch` is only a handle for
+// the lookup; kernels get the looked-up address.
+static std::atomic<void*> g_scratch_ptr[64];
+static std::mutex g_scratch_mu;
+
+size_t sfa_fwd_scratch_bytes() { return kSfaScratchBytes; }
+
+int sfa_fwd_scratch(void** ptr) {
+  int dev = -1;
+  DSA_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) {
+    set_error("device ordinal %d out of range for the scratch table", dev);
+    return DSA_ERR_UNSUPPORTED;
+  }
+  void* a = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!a) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    a = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!a) {
+      DSA_HIP(hipGetSymbolAddress(&a, HIP_SYMBOL(scratch)));
+      if (!a) {
+        set_error("hipGetSymbolAddress returned a null address for the scratch array");
+        return DSA_ERR_HIP;
+      }
+      g_scratch_ptr[dev].store(a, std::memory_order_release);
+    }
+  }
+  *ptr = a;
+  return DSA_OK;
 }
 
 int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {

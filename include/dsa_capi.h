@@ -94,6 +94,31 @@ size_t dsa_sfa_fwd_workspace_size(int64_t q_rows, int64_t n1, int64_t d,
                                   int64_t sparse_count, int32_t sparse_block_size);
 
 /*
+ * dsa_sfa_fwd without a workspace argument, and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops or harnesses
+ * that forbid hipMalloc).  Arguments and results are dsa_sfa_fwd's; the
+ * split partials go to a fixed 64 MiB device array inside the library (one
+ * per GPU, held until the process ends), whose address is looked up on the
+ * first call on each device.  Sizes whose split workspace
+ * (dsa_sfa_fwd_workspace_size) exceeds 64 MiB are rejected with
+ * DSA_ERR_UNSUPPORTED; on a 256-CU MI355X no supported shape needs more
+ * than about 51 MB.  The array is shared by every call on a GPU: calls that
+ * overlap on one device (concurrent streams or threads) race and must be
+ * serialised by the caller.
+ */
+int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* key,
+                        const void* key_rope, const int32_t* sparse_indices,
+                        void* attention_out, float* softmax_max, float* softmax_sum,
+                        const int32_t* actual_seq_q, const int32_t* actual_seq_kv,
+                        const int32_t* block_table, int64_t batch, int64_t s1, int64_t s2,
+                        int64_t n1, int64_t d, int64_t d_rope, int64_t sparse_count,
+                        int64_t q_rows, int64_t kv_rows, int64_t max_blocks,
+                        int64_t page_size, int32_t sparse_block_size, int32_t sparse_mode,
+                        int32_t layout_query, int32_t layout_kv, int32_t dtype,
+                        float scale_value, int32_t return_lse, void* stream);
+
+/*
  * Sparse flash attention backward, MLA-absorb, MQA.  Replaces the reference
  * core `_sfa_grad_core` (sparse_flash_attention_grad_triton.py:334-376) and
  * the layout handling around it (451-531): TND rows and block-wise indices

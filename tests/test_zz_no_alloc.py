@@ -1,0 +1,81 @@
+"""dsa_sfa_fwd_noalloc (the forward entry point that allocates nothing: its
+split partials live in the library's fixed device scratch array) against
+dsa_sfa_fwd with a caller workspace, through the C-ABI.
+
+Two calls in a row, the second with a smaller input, so the second runs on
+scratch that still holds the first call's partials.  Both shapes use token
+splits (fewer rows than CUs), so the scratch is read and written.  The same
+kernels run in both entry points, so the outputs must be bit-identical (a
+stronger bar than the rtol 2e-2 / atol 2e-3 tolerance of the forward).
+"""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(B, N1, D, K, ctx, page, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    bf = torch.bfloat16
+    nblk = B * ctx // page
+    t = dict(cache=torch.randn(nblk, page, 1, D, generator=g, device="cuda").to(bf),
+             cache_r=torch.randn(nblk, page, 1, 64, generator=g, device="cuda").to(bf),
+             q=torch.randn(B, 1, N1, D, generator=g, device="cuda").to(bf),
+             qr=torch.randn(B, 1, N1, 64, generator=g, device="cuda").to(bf),
+             bt=torch.randperm(nblk, generator=g, device="cuda").to(torch.int32).reshape(B, ctx // page))
+    si = torch.stack([torch.randperm(ctx, generator=g, device="cuda")[:K] for _ in range(B)])
+    si[0, K // 2:] = -1                     # one short row
+    t["si"] = si.to(torch.int32).reshape(B, 1, 1, K).contiguous()
+    t["act_k"] = torch.full((B,), ctx, dtype=torch.int32, device="cuda")
+    t["act_k"][-1] = ctx // 2
+    return t
+
+
+def _call(lib, L, t, B, N1, D, K, ctx, page, noalloc):
+    out = torch.full((B, 1, N1, D), float("nan"), dtype=torch.bfloat16, device="cuda")
+    smax = torch.full((B, 1, 1, N1), float("nan"), device="cuda")
+    ssum = torch.full((B, 1, 1, N1), float("nan"), device="cuda")
+    nblk = t["cache"].shape[0]
+    args = [t["q"].data_ptr(), t["qr"].data_ptr(), t["cache"].data_ptr(), t["cache_r"].data_ptr(),
+            t["si"].data_ptr(), out.data_ptr(), smax.data_ptr(), ssum.data_ptr(), None, t["act_k"].data_ptr(),
+            t["bt"].data_ptr(), B, 1, ctx, N1, D, 64, K, B, nblk * page, ctx // page, page, 1, 0,
+            L.LAYOUT["BSND"], L.LAYOUT["PA_BSND"], L.DTYPE_BF16, 1.0 / np.sqrt(D + 64), 1]
+    stream = L.stream_handle(torch.device("cuda:0"))
+    if noalloc:
+        st = lib.dsa_sfa_fwd_noalloc(*args, stream)
+        L.check(st, "dsa_sfa_fwd_noalloc")
+    else:
+        ws_bytes = lib.dsa_sfa_fwd_workspace_size(B, N1, D, K, 1)
+        assert ws_bytes > 0, "the shape must use token splits"
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+        st = lib.dsa_sfa_fwd(*args, ws.data_ptr(), ws_bytes, stream)
+        L.check(st, "dsa_sfa_fwd")
+    torch.cuda.synchronize()
+    return out, smax, ssum
+
+
+@pytest.mark.parametrize("shapes", [
+    # (B, N1, D, K, ctx, page): the second call is smaller than the first
+    ((32, 128, 512, 2048, 4096, 64), (4, 64, 256, 512, 1024, 32)),
+])
+def test_noalloc_matches_workspace_entry_point(shapes):
+    from dsa_triton_ascend_amd import _lib as L
+    lib = L.load()
+    for i, (B, N1, D, K, ctx, page) in enumerate(shapes):
+        print(f"[noalloc] call {i}: B={B} N1={N1} D={D} K={K} ctx={ctx} page={page}", flush=True)
+        t = _inputs(B, N1, D, K, ctx, page, seed=100 + i)
+        got = _call(lib, L, t, B, N1, D, K, ctx, page, noalloc=True)
+        exp = _call(lib, L, t, B, N1, D, K, ctx, page, noalloc=False)
+        for name, a, b in zip(("attention_out", "softmax_max", "softmax_sum"), got, exp):
+            assert torch.equal(a, b), f"call {i}: {name} differs from dsa_sfa_fwd"
+        assert not torch.isnan(got[0]).any()
+
+
+def test_noalloc_validates_like_dsa_sfa_fwd():
+    from dsa_triton_ascend_amd import _lib as L
+    lib = L.load()
+    stream = L.stream_handle(torch.device("cuda:0"))
+    st = lib.dsa_sfa_fwd_noalloc(1, 1, 1, 1, 1, 1, None, None, None, None, None, 1, 4, 256, 8, 96, 64, 64, 4,
+                                 256, 0, 0, 1, 0, 0, 0, 0, 0.1, 0, stream)
+    assert st == L.DSA_ERR_UNSUPPORTED and b"D must be" in lib.dsa_last_error()
