@@ -26,6 +26,7 @@ DTYPE_FP32 = 2
 LAYOUT = {"BSND": 0, "TND": 1, "PA_BSND": 2}
 
 TEST_FORCE_GLOBAL_GATHER = 1
+TEST_SMALL_BWD_CHUNKS = 2
 
 _c = ctypes
 _vp = _c.c_void_p
@@ -72,7 +73,7 @@ SIGNATURES = {
         _f32,                                 # scale_value
         _vp, _sz, _vp,                        # workspace, workspace_bytes, stream
     ]),
-    "dsa_sfa_bwd_workspace_size": (_sz, [_i64, _i64]),
+    "dsa_sfa_bwd_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i32, _i32]),
     "dsa_kl_bwd": (_c.c_int, [
         _vp, _vp, _vp, _vp,                   # query, key, query_rope, key_rope
         _vp, _vp, _vp, _i32p,                 # query_index, key_index, weights, sparse_indices

@@ -58,7 +58,8 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
                 float scale_value, int32_t return_lse, void* workspace, hipStream_t stream);
 
 // sfa_bwd.hip
-size_t sfa_bwd_workspace_bytes(int64_t kv_rows, int64_t d);
+size_t sfa_bwd_workspace_bytes(int64_t q_rows, int64_t kv_rows, int64_t n1, int64_t d, int64_t total_pos,
+                               bool merge);
 // kl_bwd.hip
 size_t kl_bwd_workspace_bytes(int64_t q_rows, int64_t kv_rows, int64_t topk);
 int kl_bwd_max_topk();
@@ -211,7 +212,7 @@ extern "C" {
 
 const char* dsa_last_error(void) { return g_err; }
 
-int dsa_abi_version(void) { return 1; }
+int dsa_abi_version(void) { return 2; }
 
 void dsa_set_test_flags(int32_t flags) { g_test_flags.store(flags, std::memory_order_relaxed); }
 
@@ -279,9 +280,10 @@ int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* k
                      (hipStream_t)stream);
 }
 
-size_t dsa_sfa_bwd_workspace_size(int64_t kv_rows, int64_t d) {
-  if (kv_rows <= 0 || d <= 0) return 0;
-  return sfa_bwd_workspace_bytes(kv_rows, d);
+size_t dsa_sfa_bwd_workspace_size(int64_t q_rows, int64_t kv_rows, int64_t n1, int64_t d, int64_t sparse_count,
+                                  int32_t sparse_block_size, int32_t merge_kv) {
+  if (q_rows < 0 || kv_rows <= 0 || n1 <= 0 || d <= 0 || sparse_count <= 0 || sparse_block_size <= 0) return 0;
+  return sfa_bwd_workspace_bytes(q_rows, kv_rows, n1, d, sparse_count * (int64_t)sparse_block_size, merge_kv != 0);
 }
 
 int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
@@ -319,7 +321,8 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
     DSA_CHECK_ARG(s2 >= 1 && kv_rows == batch * s2, "kv_rows must equal B*S2 for BSND");
   }
   DSA_CHECK_ARG(q_rows < (1ll << 31) && kv_rows >= 1 && kv_rows < (1ll << 31), "row counts out of range");
-  const size_t need = sfa_bwd_workspace_bytes(kv_rows, d);
+  const size_t need = sfa_bwd_workspace_bytes(q_rows, kv_rows, n1, d, sparse_count * (int64_t)sparse_block_size,
+                                             d_value == nullptr);
   if (workspace == nullptr || workspace_bytes < need) {
     set_error("workspace of %zu bytes required, %zu given", need, workspace_bytes);
     return DSA_ERR_WORKSPACE;

@@ -135,6 +135,7 @@ int hip_fail(hipError_t e, const char* what);
 int device_cu_count();
 // Test hooks set by dsa_set_test_flags (0 in normal use).
 constexpr int kTestForceGlobalGather = 1;  // gather with 64-bit addresses even below 2 GiB
+constexpr int kTestSmallBwdChunks = 2;     // backward rows in chunks of a 64 KiB workspace budget
 int test_flags();
 }  // namespace dsa
 

@@ -7,30 +7,36 @@
 //   s     = (q_nope.k_nope + q_rope.k_rope) * scale
 //   P     = exp(s - softmax_max) / softmax_sum   (sum <= 0 taken as 1, 233-234)
 //   delta = sum_d dO * O                          (237)
-//   dS    = P * (dO.v - delta) * scale            (262-267)
+//   dS    = P * (dP - delta) * scale, dP = dO.v   (262-267)
 //   dq += dS k_nope,  dq_rope += dS k_rope        (271-272)
 //   dk += dS^T q_nope, dk_rope += dS^T q_rope, dv += P^T dO   (277-300)
-// dq / dq_rope are owned per (row, head) and stored in the query dtype; dk,
-// dk_rope and dv are scatter-added in fp32 (many rows select one key row;
-// the order of the fp32 additions is not fixed, as in the reference, which
-// rejects deterministic=True) and cast to the key dtype afterwards.
+// The reference scatters dk / dk_rope / dv with fp32 atomics, so its results
+// depend on the order of the additions (and it rejects deterministic=True).
+// Here every output is deterministic and no floating-point atomics are used:
 //
-// Design (one wave = one query row x 16 heads; 1 wave per SIMD, so the wave
-// has the whole 512-register file):
-//  * Q (nope + rope) and dO fragments of the 16 heads sit in registers as
-//    MFMA B operands; so do their transposes Q^T / dO^T (4 heads x 1 column
-//    per lane), the B operands of the dK / dV products, built once through
-//    LDS.  Per-head statistics (max in log2 units, 1/sum, delta) are
-//    lane-local, one head per lane column.
-//  * Tiles of 32 attended tokens are gathered into LDS (swizzled 16-byte
-//    chunks, the forward's layout).  S^T = K.Q^T and dP^T = K_nope.dO^T share
-//    the K fragment reads; P^T and dS^T come out lane-local.
-//  * dq^T += K^T.dS^T and dq_rope^T += Kr^T.dS^T read K^T through the
-//    transposing LDS load (ds_read_b64_tr_b16), as the forward's P.V.
-//  * dS and P go through a 1 KB LDS transpose into the A operand of
-//    v_mfma_f32_16x16x16 (tokens x 16 heads); dK/dK_rope = dS^T.Q and
-//    dV = P^T.dO come out as 16 tokens x 16 columns tiles whose fp32 values
-//    are added to the workspaces with global atomics.
+//  A. sfa_bwd_dq_kernel: one workgroup per (query row, 64 heads), 4 waves of
+//     16 heads.  Tiles of 32 attended tokens are gathered into LDS by
+//     LDS-DMA; S^T = K.Q^T and dP^T = V.dO^T share the K fragment reads; P
+//     and dS are lane-local; dq^T += K^T.dS^T through the transposing LDS
+//     read.  dS and P of the tile are stored ([row][slot][dS | P][head]) for
+//     kernel B, and the row's compacted token list is recorded together with
+//     each slot's rank in its token's bucket (an integer count).
+//  B. sfa_bwd_rec_kernel: one workgroup per query row, all heads (8 waves).
+//     Each wave owns a slice of the output columns [dK | dK_rope | dV] (or
+//     [dK + dV | dK_rope] for the shared latent) and holds Q^T / dO^T for all
+//     heads of its slice as MFMA A operands; per tile it reads dS / P from
+//     LDS and produces, per attended token, the head-summed contribution
+//     ("record") of its columns.  Records go to the token's bucket as fp16
+//     scaled by a power of two per (record, slice), so the stored values
+//     keep 11 bits relative to the slice's largest entry.
+//  C. sfa_bwd_reduce_kernel: one wave per (key token, slice) sums the
+//     token's records in int64 fixed point (exact and associative, so the
+//     bucket order does not matter) and writes the key gradients.
+// Rows are processed in chunks whose workspace stays within a budget; the
+// chunks' sums are added in chunk order in fp32.
+#include <atomic>
+#include <type_traits>
+
 #include "sfa_common.h"
 
 namespace dsa {
@@ -50,385 +56,104 @@ struct SfaBwdParams {
   const int32_t* block_table;  // unused (no paged layout in the backward)
   void* dq;
   void* dqr;
-  float* dk;
-  float* dkr;
-  float* dv;
+  // outputs of the key side (kernel C)
+  void* dk;
+  void* dkr;
+  void* dv;  // nullptr: dk receives dk + dv
   int64_t rows, kv_rows;
+  int64_t row0;    // first row of the chunk
+  int32_t nrows;   // rows of the chunk
   int32_t batch, s1, s2, n1, K, bs, mode, layout_q, layout_kv, max_blocks, page_size;
+  int32_t hp;      // heads padded to a multiple of 32 (dS / P row stride)
+  int32_t kposp;   // index positions per row, padded to a multiple of 32
+  int32_t nc;      // record columns: 2D + 64, or D + 64 when merged
   float scale, scale_log2;
+  // workspace
+  int32_t* cnt;    // [kv_rows] slots per token in this chunk
+  int32_t* offs;   // [kv_rows + 1] bucket offsets
+  int32_t* list;   // [nrows, kposp] physical token of each compacted slot
+  int32_t* rank;   // [nrows, kposp] the slot's place in its token's bucket
+  int32_t* nval;   // [nrows] compacted slots per row
+  void* dsp;       // [nrows, kposp, 2, hp] dS and P (T; fp16 scaled by 2^kF16Shift)
+  _Float16* rec;   // [slots, nc] records in bucket order
+  int16_t* rexp;   // [slots, kRecSlices] exponent of each record slice
+  float* acc;      // [kv_rows, nc] running fp32 sums over chunks
 };
 
 constexpr int kBwdTile = 32;
-constexpr int kBwdList = 2048;  // attended positions resolved per compaction round
-
-
-template <typename T>
-__device__ __forceinline__ short to_bits(float x) {
-  return __builtin_bit_cast(short, Elem<T>::from_f32(x));
-}
-
-template <int D, typename T>
-__global__ __launch_bounds__(64, 1) void sfa_bwd_kernel(SfaBwdParams p) {
-  using E = Elem<T>;
-  using V8 = typename E::v8;
-  constexpr int DR = 64;
-  constexpr int DC = D + DR;         // columns of dK + dK_rope
-  constexpr int KS = DC / 32;        // k-steps of S
-  constexpr int KSN = D / 32;        // of which nope
-  constexpr int NDT = D / 16;        // d-tiles of dq / dv
-  constexpr int NCT = DC / 16;       // column tiles of dk + dk_rope
-  constexpr int TILE = kBwdTile;
-  constexpr int ROW = D * 2;         // nope row bytes in LDS
-  constexpr int QST = DC + 16;       // staging row (elements), padded
-  static_assert(D >= 128 && TILE == 32, "layout");
-
-  __shared__ __attribute__((aligned(16))) unsigned char s_k[TILE * ROW];
-  __shared__ __attribute__((aligned(16))) unsigned char s_kr[TILE * DR * 2];
-  __shared__ int s_list[kBwdList + TILE];
-  // dS and P as [token][head], each as a hi and a lo part (bf16 I/O)
-  __shared__ __attribute__((aligned(16))) T s_tr[4][TILE][16];
-
-  const int lane = threadIdx.x;
-  const int li = lane & 15, lg = lane >> 4;
-  const int row = blockIdx.x;
-  const int head0 = blockIdx.y * 16;
-  const RowInfo ri = sfa_row_info(p, row);
-  const int64_t total_pos = (int64_t)p.K * p.bs;
-  const int32_t* idx_row = p.idx + (int64_t)row * p.K;
-
-  // ---- per-lane head (head0 + li): fragments and statistics ----
-  const int head = head0 + li;
-  const bool hv = head < p.n1;
-  const int64_t hrow = (int64_t)row * p.n1 + (hv ? head : 0);
-  V8 qf[KS], dof[KSN];
-  const u32x4 z4 = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    u32x4 v;
-    if (ks < KSN) v = *(const u32x4*)((const T*)p.q + hrow * D + ks * 32 + lg * 8);
-    else v = *(const u32x4*)((const T*)p.qr + hrow * DR + (ks - KSN) * 32 + lg * 8);
-    qf[ks] = as_v8<V8>(hv ? v : z4);
-  }
-  float delta = 0.f;
-#pragma unroll
-  for (int ks = 0; ks < KSN; ++ks) {
-    const u32x4 v = *(const u32x4*)((const T*)p.dout + hrow * D + ks * 32 + lg * 8);
-    const u32x4 o = *(const u32x4*)((const T*)p.out + hrow * D + ks * 32 + lg * 8);
-    dof[ks] = as_v8<V8>(hv ? v : z4);
-    const V8 dv8 = as_v8<V8>(v), ov8 = as_v8<V8>(o);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) delta += E::to_f32(dv8[j]) * E::to_f32(ov8[j]);
-  }
-  delta = xgroup_sum(delta);  // lanes li, li+16, li+32, li+48 cover all D columns
-  float m2 = 0.f, inv = 0.f;
-  if (hv) {
-    const float sm = p.smax[hrow], ss = p.ssum[hrow];
-    m2 = sm * kLog2e;
-    inv = 1.f / (ss > 0.f ? ss : 1.f);
-  } else {
-    delta = 0.f;
-  }
-
-  // transposed fragments (B operands of the 16x16x16 products):
-  // qT[c] = Q[heads 4*lg + j][column c*16 + li], dT[c] = dO[...] likewise,
-  // built through LDS (rows of 16 heads, padded to QST elements)
-  s16x4 qT[NCT], dT[NDT];
-  {
-    T* st = (T*)s_k;  // 16 x QST elements fit in the tile buffer
-    static_assert(16 * QST * 2 <= TILE * ROW, "staging fits");
-    for (int e = lane; e < 16 * DC; e += 64) {
-      const int h = e / DC, c = e - h * DC;
-      const int hh = head0 + h;
-      T v = E::from_f32(0.f);
-      if (hh < p.n1) {
-        const int64_t r = (int64_t)row * p.n1 + hh;
-        v = c < D ? ((const T*)p.q)[r * D + c] : ((const T*)p.qr)[r * DR + (c - D)];
-      }
-      st[h * QST + c] = v;
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int c = 0; c < NCT; ++c) {
-      s16x4 f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) f[j] = __builtin_bit_cast(short, st[(4 * lg + j) * QST + c * 16 + li]);
-      qT[c] = f;
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    for (int e = lane; e < 16 * D; e += 64) {
-      const int h = e / D, c = e - h * D;
-      const int hh = head0 + h;
-      T v = E::from_f32(0.f);
-      if (hh < p.n1) v = ((const T*)p.dout)[((int64_t)row * p.n1 + hh) * D + c];
-      st[h * QST + c] = v;
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int c = 0; c < NDT; ++c) {
-      s16x4 f;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) f[j] = __builtin_bit_cast(short, st[(4 * lg + j) * QST + c * 16 + li]);
-      dT[c] = f;
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-  }
-
-  f32x4 acc_dq[NDT], acc_dqr[DR / 16];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) acc_dq[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int dt = 0; dt < DR / 16; ++dt) acc_dqr[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-  // per-lane LDS offsets (tile rows are D*2 / 128 bytes; chunk swizzles as
-  // in the forward)
-  auto a1_off = [&](int ks, int tt) -> int {
-    const int tk = tt * 16 + li;
-    if (ks < KSN) return tk * ROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16);
-    return tk * (DR * 2) + ((((ks - KSN) * 4 + lg) ^ rope_swz(tk)) * 16);
-  };
-
-  for (int64_t c0 = 0; c0 < total_pos; c0 += kBwdList) {
-    // ---- compact this range of positions into s_list ----
-    const int64_t c1 = min(total_pos, c0 + (int64_t)kBwdList);
-    int n_valid = 0;
-    for (int64_t b0 = c0; b0 < c1; b0 += 64) {
-      const int64_t pos = b0 + lane;
-      int phys = 0;
-      bool valid = false;
-      if (ri.active && pos < c1) valid = sfa_resolve(p, ri, idx_row, (int)pos, &phys);
-      const unsigned long long m = __ballot(valid);
-      if (valid) s_list[n_valid + __popcll(m & ((1ull << lane) - 1ull))] = phys;
-      n_valid += __popcll(m);
-    }
-    if (lane < TILE) s_list[n_valid + lane] = -1;
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
-    const int n_tiles = (n_valid + TILE - 1) / TILE;
-
-    for (int t = 0; t < n_tiles; ++t) {
-      // ---- gather the tile (16-byte chunks, swizzled) ----
-      constexpr int CPR = D / 8;  // nope chunks per row
-#pragma unroll 4
-      for (int e = lane; e < TILE * CPR; e += 64) {
-        const int tk = e / CPR, ch = e - tk * CPR;
-        const int ph = s_list[t * TILE + tk];
-        u32x4 v = z4;
-        if (ph >= 0) v = *(const u32x4*)((const unsigned char*)p.k + (int64_t)ph * (D * 2) + ch * 16);
-        *(u32x4*)(s_k + tk * ROW + ((ch ^ nope_swz(tk)) * 16)) = v;
-      }
-#pragma unroll
-      for (int e = lane; e < TILE * 8; e += 64) {
-        const int tk = e >> 3, ch = e & 7;
-        const int ph = s_list[t * TILE + tk];
-        u32x4 v = z4;
-        if (ph >= 0) v = *(const u32x4*)((const unsigned char*)p.kr + (int64_t)ph * (DR * 2) + ch * 16);
-        *(u32x4*)(s_kr + tk * (DR * 2) + ((ch ^ rope_swz(tk)) * 16)) = v;
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-      __builtin_amdgcn_wave_barrier();
-
-      // ---- S^T = K.Q^T and dP^T = K_nope.dO^T (shared K fragments) ----
-      f32x4 acc_s[2], acc_p[2];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        acc_s[tt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-        acc_p[tt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-      }
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const unsigned char* base = ks < KSN ? s_k : s_kr;
-          const V8 av = as_v8<V8>(*(const u32x4*)(base + a1_off(ks, tt)));
-          acc_s[tt] = E::mfma(av, qf[ks], acc_s[tt]);
-          if (ks < KSN) acc_p[tt] = E::mfma(av, dof[ks], acc_p[tt]);
-        }
-
-      // ---- P^T, dS^T (token tt*16 + 4*lg + r, head li) ----
-      // dS^T as the B operand of K^T.dS^T (token k = 8*lg + j).  For bf16 I/O
-      // dS (and P below) are split into bf16 hi + lo parts, so the products
-      // carry ~16 bits of them: a single bf16 rounding (2^-9 relative per
-      // term) exceeds the fp32-golden tolerance on rows with few tokens.
-      constexpr bool kSplit = __is_same(T, bf16);
-      V8 dsf, dsf_lo;
-      float pv[8], dsv[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int tt = j >> 2, r = j & 3;
-        const int tok = t * TILE + tt * 16 + lg * 4 + r;
-        const bool tv = tok < n_valid;
-        const float pp = tv ? fast_exp2(acc_s[tt][r] * p.scale_log2 - m2) * inv : 0.f;
-        const float ds = pp * (acc_p[tt][r] - delta) * p.scale;
-        pv[j] = pp;
-        dsv[j] = ds;
-        dsf[j] = E::from_f32(ds);
-        dsf_lo[j] = E::from_f32(ds - E::to_f32(dsf[j]));
-      }
-
-      // ---- dq^T += K^T.dS^T, dq_rope^T += Kr^T.dS^T ----
-      // K^T fragment (16 d x 32 tokens) through the transposing read: row
-      // r1 = 4*lg + li/4 (and r1 + 16), chunk 2*dt + (li&3)/2, half li&1
-      {
-        const int r1 = lg * 4 + (li >> 2);
-        const int hb = (li & 3) >> 1;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          const int ch = 2 * dt + hb;
-          const unsigned char* p1 = s_k + r1 * ROW + ((ch ^ nope_swz(r1)) * 16) + (li & 1) * 8;
-          const unsigned char* p2 = s_k + (r1 + 16) * ROW + ((ch ^ nope_swz(r1 + 16)) * 16) + (li & 1) * 8;
-          const i16x4 w1 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1));
-          const i16x4 w2 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p2));
-          const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
-          acc_dq[dt] = E::mfma(__builtin_bit_cast(V8, w), dsf, acc_dq[dt]);
-          if (kSplit) acc_dq[dt] = E::mfma(__builtin_bit_cast(V8, w), dsf_lo, acc_dq[dt]);
-        }
-#pragma unroll
-        for (int dt = 0; dt < DR / 16; ++dt) {
-          const int ch = 2 * dt + hb;
-          const unsigned char* p1 = s_kr + r1 * (DR * 2) + ((ch ^ rope_swz(r1)) * 16) + (li & 1) * 8;
-          const unsigned char* p2 = s_kr + (r1 + 16) * (DR * 2) + ((ch ^ rope_swz(r1 + 16)) * 16) + (li & 1) * 8;
-          const i16x4 w1 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1));
-          const i16x4 w2 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p2));
-          const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
-          acc_dqr[dt] = E::mfma(__builtin_bit_cast(V8, w), dsf, acc_dqr[dt]);
-          if (kSplit) acc_dqr[dt] = E::mfma(__builtin_bit_cast(V8, w), dsf_lo, acc_dqr[dt]);
-        }
-      }
-
-      // ---- dS, P -> [token][head] in LDS, then 16x16x16 A fragments ----
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int tk = (j >> 2) * 16 + lg * 4 + (j & 3);
-        const T dh = E::from_f32(dsv[j]), ph = E::from_f32(pv[j]);
-        s_tr[0][tk][li] = dh;
-        s_tr[1][tk][li] = ph;
-        s_tr[2][tk][li] = E::from_f32(dsv[j] - E::to_f32(dh));
-        s_tr[3][tk][li] = E::from_f32(pv[j] - E::to_f32(ph));
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        // A[token tt*16 + li][heads 4*lg ..]: 8 bytes
-        const s16x4 a_ds = *(const s16x4*)&s_tr[0][tt * 16 + li][4 * lg];
-        const s16x4 a_p = *(const s16x4*)&s_tr[1][tt * 16 + li][4 * lg];
-        const s16x4 a_ds_lo = *(const s16x4*)&s_tr[2][tt * 16 + li][4 * lg];
-        const s16x4 a_p_lo = *(const s16x4*)&s_tr[3][tt * 16 + li][4 * lg];
-        // token rows of this lane's C entries: tt*16 + 4*lg + r
-        int ph[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) ph[r] = s_list[t * TILE + tt * 16 + lg * 4 + r];
-#pragma unroll
-        for (int c = 0; c < NCT; ++c) {
-          f32x4 cd = Mfma16<T>::run(a_ds, qT[c], (f32x4){0.f, 0.f, 0.f, 0.f});
-          if (kSplit) cd = Mfma16<T>::run(a_ds_lo, qT[c], cd);
-          const int col = c * 16 + li;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            if (ph[r] < 0) continue;
-            if (col < D) atomicAdd(p.dk + (int64_t)ph[r] * D + col, cd[r]);
-            else atomicAdd(p.dkr + (int64_t)ph[r] * DR + (col - D), cd[r]);
-          }
-        }
-#pragma unroll
-        for (int c = 0; c < NDT; ++c) {
-          f32x4 cv = Mfma16<T>::run(a_p, dT[c], (f32x4){0.f, 0.f, 0.f, 0.f});
-          if (kSplit) cv = Mfma16<T>::run(a_p_lo, dT[c], cv);
-          const int col = c * 16 + li;
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (ph[r] >= 0) atomicAdd(p.dv + (int64_t)ph[r] * D + col, cv[r]);
-        }
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-      __builtin_amdgcn_wave_barrier();
-    }
-  }
-
-  // ---- dq, dq_rope (head li, columns 16*dt + 4*lg + r) ----
-  if (hv) {
-    typedef T T4 __attribute__((ext_vector_type(4)));
-    T* dqp = (T*)p.dq + hrow * D;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const T4 o = {E::from_f32(acc_dq[dt][0]), E::from_f32(acc_dq[dt][1]), E::from_f32(acc_dq[dt][2]),
-                    E::from_f32(acc_dq[dt][3])};
-      *(T4*)(dqp + dt * 16 + lg * 4) = o;
-    }
-    T* dqrp = (T*)p.dqr + hrow * DR;
-#pragma unroll
-    for (int dt = 0; dt < DR / 16; ++dt) {
-      const T4 o = {E::from_f32(acc_dqr[dt][0]), E::from_f32(acc_dqr[dt][1]), E::from_f32(acc_dqr[dt][2]),
-                    E::from_f32(acc_dqr[dt][3])};
-      *(T4*)(dqrp + dt * 16 + lg * 4) = o;
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Workgroup kernel: 4 waves x 16 heads = 64 heads of one query row.
-//
-// Per tile of 32 attended tokens (LDS ring of two buffers, filled by LDS DMA
-// right after the previous tile's barrier, so a tile's gather overlaps the
-// previous tile's products):
-//  * each wave: S^T, dP^T, P, dS and dq / dq_rope for its 16 heads, as the
-//    one-wave kernel above;
-//  * dS and P of the 64 heads go to LDS as [token][head] (bf16 / fp16);
-//  * each wave then owns a quarter of the 2D + 64 output columns (dK, dK_rope,
-//    dV) and sums them over all 64 heads on MFMA: A = dS^T or P^T [16 tokens
-//    x 32 heads] from LDS, B = Q / Q_rope / dO [32 heads x 16 columns]
-//    resident in registers for the row; the sums go to the fp32 workspaces.
-// The 64-head sum cuts the scatter payload by 4 against one wave per 16
-// heads.  One wave per SIMD: each wave has the whole 512-register file.
-// ---------------------------------------------------------------------------
-constexpr int kBwdWgWaves = 4;
-constexpr int kBwdWgHeads = 64;
+constexpr int kBwdList = 2048;  // positions resolved per compaction round
+constexpr int kBwdWaves = 4;    // kernel A
+constexpr int kBwdHeads = 64;   // heads per kernel-A workgroup
+constexpr int kRecSlices = 8;   // column slices (one per kernel-B wave)
+// fp16 dS / P are stored scaled by 2^8: dS is typically ~1e-5, inside
+// fp16's subnormal range, and P <= 1 stays below 256.  bf16 has fp32's
+// exponent range and is stored as is.
+constexpr int kF16Shift = 8;
+// a slice exponent that marks non-finite contributions
+constexpr int kRecNonFinite = 0x7fff;
 
 __device__ __forceinline__ void bwd_dma16(unsigned lds_base, int voff, __amdgpu_buffer_rsrc_t rsrc) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :: "s"(lds_base), "v"(voff), "s"(rsrc) : "memory");
 }
+__device__ __forceinline__ void bwd_dma16_glb(unsigned lds_base, const void* gaddr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(lds_base), "v"(gaddr) : "memory");
+}
 __device__ __forceinline__ void bwd_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// MERGE (the shared latent of MLA absorb, value = key[..., :D]): the dV
-// contribution of a token is added to its dK nope columns before the
-// atomics, so each (row, 64 heads, token) adds D + 64 values instead of
-// 2D + 64; dv is not written.
-template <int D, typename T, bool MERGE>
-__global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdParams p) {
+__device__ __attribute__((aligned(16))) unsigned char g_bwd_zero_row[1024];
+
+// Column slices of a record.  Unmerged: slices 0-3 split the dK | dK_rope
+// tiles ((D + 64) / 16), slices 4-7 the dV tiles (D / 16); merged: the
+// eight slices split the (D + 64) / 16 tiles of dK + dV | dK_rope.
+template <int D, bool MERGE>
+struct RecSlices {
+  static constexpr int NK = (D + 64) / 16, NV = D / 16;
+  static constexpr int MT = MERGE ? (NK + 7) / 8 : (NK / 4 > NV / 4 ? NK / 4 : NV / 4);
+  static_assert(MERGE || (NK % 4 == 0 && NV % 4 == 0), "slices");
+  // first column tile of slice s and its tile count
+  static __host__ __device__ constexpr int t0(int s) {
+    return MERGE ? s * NK / 8 : (s < 4 ? s * (NK / 4) : NK + (s - 4) * (NV / 4));
+  }
+  static __host__ __device__ constexpr int n(int s) {
+    return MERGE ? (s + 1) * NK / 8 - s * NK / 8 : (s < 4 ? NK / 4 : NV / 4);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// A. dq, dq_rope; dS / P; token list and bucket ranks
+// ---------------------------------------------------------------------------
+template <int D, typename T, bool BUF>
+__global__ __launch_bounds__(kBwdWaves * 64, 1) void sfa_bwd_dq_kernel(SfaBwdParams p) {
   using E = Elem<T>;
   using V8 = typename E::v8;
   constexpr int DR = 64;
-  constexpr int DC = D + DR;
-  constexpr int KS = DC / 32, KSN = D / 32;
+  constexpr int KS = (D + DR) / 32, KSN = D / 32;
   constexpr int NDT = D / 16;
   constexpr int TILE = kBwdTile;
-  constexpr int NT = kBwdWgWaves * 64;
+  constexpr int NT = kBwdWaves * 64;
   constexpr int ROW = D * 2;
-  constexpr int TPI = 1024 / ROW;            // nope rows per DMA (1 KB per DMA)
-  constexpr int NDN = TILE / TPI / kBwdWgWaves;  // nope DMAs per wave per tile
-  constexpr int NCOL = 2 * D + DR;           // dK | dK_rope | dV columns
-  constexpr int NCW = NCOL / 16 / kBwdWgWaves;   // column tiles per wave
-  constexpr int NNW = D / 16 / kBwdWgWaves;      // MERGE: nope column tiles per wave
-  constexpr int NXB = MERGE ? 2 * NNW + 1 : NCW; // B-operand column tiles per wave
-  constexpr int TR = kBwdWgHeads + 8;        // padded [token][head] row
-  static_assert(NCOL % (16 * kBwdWgWaves) == 0 && TILE % (TPI * kBwdWgWaves) == 0, "layout");
+  constexpr int TPI = 1024 / ROW;                // nope rows per DMA (1 KB per DMA)
+  constexpr int NDN = TILE / TPI / kBwdWaves;    // nope DMAs per wave per tile
+  constexpr int TR = kBwdHeads + 8;              // padded [token][head] row
+  constexpr float kDsMul = __is_same(T, f16) ? (float)(1 << kF16Shift) : 1.f;
+  static_assert(TILE % (TPI * kBwdWaves) == 0, "layout");
 
-  __shared__ __attribute__((aligned(1024))) unsigned char s_k[2][TILE * ROW];
-  __shared__ __attribute__((aligned(1024))) unsigned char s_kr[2][TILE * DR * 2];
+  constexpr int NBUF = 3;  // tile ring: tile t+2 is in flight while tile t runs
+  __shared__ __attribute__((aligned(1024))) unsigned char s_k[NBUF][TILE * ROW];
+  __shared__ __attribute__((aligned(1024))) unsigned char s_kr[NBUF][TILE * DR * 2];
   __shared__ int s_list[kBwdList + TILE];
   __shared__ __attribute__((aligned(16))) T s_t[2][TILE][TR];  // dS, P of the 64 heads
-  __shared__ int s_wcnt[kBwdWgWaves];
+  __shared__ int s_wcnt[kBwdWaves];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const int row = blockIdx.x;
-  const int hbase = blockIdx.y * kBwdWgHeads;
+  const int rowl = blockIdx.x;
+  const int row = (int)(p.row0 + rowl);
+  const int hg = blockIdx.y;
+  const int hbase = hg * kBwdHeads;
   const RowInfo ri = sfa_row_info(p, row);
   const int64_t total_pos = (int64_t)p.K * p.bs;
   const int32_t* idx_row = p.idx + (int64_t)row * p.K;
@@ -456,7 +181,7 @@ __global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdP
 #pragma unroll
     for (int j = 0; j < 8; ++j) delta += E::to_f32(dv8[j]) * E::to_f32(ov8[j]);
   }
-  delta = xgroup_sum(delta);
+  delta = xgroup_sum(delta);  // lanes li, li+16, li+32, li+48 cover all D columns
   float m2 = 0.f, inv = 0.f;
   if (hv) {
     m2 = p.smax[hrow] * kLog2e;
@@ -465,35 +190,6 @@ __global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdP
   } else {
     delta = 0.f;
   }
-  // B operands of the 64-head sums: column c of [Q nope | Q rope | dO],
-  // heads hbase + 32*ks + 8*lg + j.  Tile i is column 16*(wave*NCW + i) + li;
-  // with MERGE, tiles i < NNW are Q nope columns 16*(wave*NNW + i) + li,
-  // tiles NNW + i the dO columns of the same index, and tile 2*NNW the Q
-  // rope columns 16*wave + li.
-  V8 xb[NXB][2];
-#pragma unroll
-  for (int i = 0; i < NXB; ++i) {
-    int c = 16 * (wave * NCW + i) + li;
-    if (MERGE) {
-      if (i < NNW) c = 16 * (wave * NNW + i) + li;
-      else if (i < 2 * NNW) c = D + DR + 16 * (wave * NNW + i - NNW) + li;
-      else c = D + 16 * wave + li;
-    }
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int h = hbase + ks * 32 + lg * 8 + j;
-        T v = E::from_f32(0.f);
-        if (h < p.n1) {
-          const int64_t r = (int64_t)row * p.n1 + h;
-          if (c < D) v = ((const T*)p.q)[r * D + c];
-          else if (c < D + DR) v = ((const T*)p.qr)[r * DR + (c - D)];
-          else v = ((const T*)p.dout)[r * D + (c - D - DR)];
-        }
-        xb[i][ks][j] = v;
-      }
-  }
   f32x4 acc_dq[NDT], acc_dqr[DR / 16];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) acc_dq[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -501,33 +197,54 @@ __global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdP
   for (int dt = 0; dt < DR / 16; ++dt) acc_dqr[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   // ---- tile DMA: wave w loads nope rows (j*4 + w)*TPI .. +TPI (lane L ->
-  // row + L/CPT, source chunk (L%CPT) ^ nope_swz) and rope rows 8w .. 8w+7 ----
+  // row + L/CPT, source chunk (L%CPT) ^ nope_swz) and rope rows 8w .. 8w+7.
+  // BUF: 32-bit buffer offsets (key tensors under 2 GiB; the range check
+  // yields zero rows), otherwise 64-bit addresses and an explicit zero row.
   constexpr int CPT = 64 / TPI;  // chunks per row covered by one DMA
-  const __amdgpu_buffer_rsrc_t rk =
-      __builtin_amdgcn_make_buffer_rsrc((void*)p.k, (short)0, (int)(p.kv_rows * D * 2), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rr =
-      __builtin_amdgcn_make_buffer_rsrc((void*)p.kr, (short)0, (int)(p.kv_rows * DR * 2), 0x00020000);
+  __amdgpu_buffer_rsrc_t rk, rr;
+  if constexpr (BUF) {
+    rk = __builtin_amdgcn_make_buffer_rsrc((void*)p.k, (short)0, (int)(p.kv_rows * D * 2), 0x00020000);
+    rr = __builtin_amdgcn_make_buffer_rsrc((void*)p.kr, (short)0, (int)(p.kv_rows * DR * 2), 0x00020000);
+  }
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   auto issue_tile = [&](int t, int b) {
     int ph[NDN + 1];
 #pragma unroll
-    for (int j = 0; j < NDN; ++j) ph[j] = s_list[t * TILE + (j * kBwdWgWaves + wave_s) * TPI + lane / CPT];
+    for (int j = 0; j < NDN; ++j) ph[j] = s_list[t * TILE + (j * kBwdWaves + wave_s) * TPI + lane / CPT];
     ph[NDN] = s_list[t * TILE + wave_s * 8 + (lane >> 3)];
 #pragma unroll
     for (int j = 0; j < NDN; ++j) {
-      const int tk = (j * kBwdWgWaves + wave_s) * TPI + lane / CPT;
+      const int tk = (j * kBwdWaves + wave_s) * TPI + lane / CPT;
       const int ch = (lane % CPT) ^ nope_swz(tk);
-      const unsigned dst = (unsigned)(uintptr_t)&s_k[b][(j * kBwdWgWaves + wave_s) * TPI * ROW];
-      bwd_dma16(dst, ph[j] >= 0 ? ph[j] * ROW + ch * 16 : (int)0x80000000, rk);
+      const unsigned dst = (unsigned)(uintptr_t)&s_k[b][(j * kBwdWaves + wave_s) * TPI * ROW];
+      if constexpr (BUF) {
+        bwd_dma16(dst, ph[j] >= 0 ? ph[j] * ROW + ch * 16 : (int)0x80000000, rk);
+      } else {
+        bwd_dma16_glb(dst, ph[j] >= 0 ? (const void*)((const unsigned char*)p.k + (int64_t)ph[j] * ROW + ch * 16)
+                                      : (const void*)(g_bwd_zero_row + ch * 16));
+      }
     }
     {
       const int tk = wave_s * 8 + (lane >> 3);
       const int ch = (lane & 7) ^ rope_swz(tk);
       const unsigned dst = (unsigned)(uintptr_t)&s_kr[b][wave_s * 8 * DR * 2];
-      bwd_dma16(dst, ph[NDN] >= 0 ? ph[NDN] * (DR * 2) + ch * 16 : (int)0x80000000, rr);
+      if constexpr (BUF) {
+        bwd_dma16(dst, ph[NDN] >= 0 ? ph[NDN] * (DR * 2) + ch * 16 : (int)0x80000000, rr);
+      } else {
+        bwd_dma16_glb(dst, ph[NDN] >= 0
+                               ? (const void*)((const unsigned char*)p.kr + (int64_t)ph[NDN] * (DR * 2) + ch * 16)
+                               : (const void*)(g_bwd_zero_row + ch * 16));
+      }
     }
   };
 
+  // dS / P rows of this workgroup's heads in the slot's [dS | P] row
+  const int nh = min(kBwdHeads, p.hp - hbase);  // 32 or 64 heads stored
+  T* dsp_row = (T*)p.dsp + (int64_t)rowl * p.kposp * 2 * p.hp + hbase;
+  int32_t* list_row = p.list + (int64_t)rowl * p.kposp;
+  int32_t* rank_row = p.rank + (int64_t)rowl * p.kposp;
+
+  int jbase = 0;  // slots compacted by earlier rounds
   for (int64_t c0 = 0; c0 < total_pos; c0 += kBwdList) {
     // ---- compact this range of positions into s_list (stable order) ----
     const int64_t c1 = min(total_pos, c0 + (int64_t)kBwdList);
@@ -542,12 +259,21 @@ __global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdP
       lds_barrier();
       int off = n_valid, tot = 0;
 #pragma unroll
-      for (int w = 0; w < kBwdWgWaves; ++w) {
+      for (int w = 0; w < kBwdWaves; ++w) {
         const int c = s_wcnt[w];
         off += w < wave ? c : 0;
         tot += c;
       }
-      if (valid) s_list[off + __popcll(m & ((1ull << lane) - 1ull))] = phys;
+      if (valid) {
+        const int j = off + __popcll(m & ((1ull << lane) - 1ull));
+        s_list[j] = phys;
+        if (hg == 0) {
+          // the token list and, from the token's count, the slot's place in
+          // its bucket (integer counts: their order does not matter)
+          list_row[jbase + j] = phys;
+          rank_row[jbase + j] = atomicAdd(&p.cnt[phys], 1);
+        }
+      }
       n_valid += tot;
       lds_barrier();
     }
@@ -555,12 +281,20 @@ __global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdP
     lds_barrier();
     const int n_tiles = (n_valid + TILE - 1) / TILE;
     if (n_tiles > 0) issue_tile(0, 0);
+    if (n_tiles > 1) issue_tile(1, 1);
+    // P.V-style split of dS into bf16 hi + lo for the dq product only while
+    // the range has few tokens (as the forward splits P): over longer ranges
+    // one rounding of dS averages out.
+    const bool lo = n_valid < 256;
 
     for (int t = 0; t < n_tiles; ++t) {
-      const int b = t & 1;
-      bwd_wait_all();  // this tile's DMA (and everything older) has landed
+      const int b = t % NBUF;
+      // tile t's DMA has landed.  Issued per wave in the order DMA(t),
+      // stores(t-1), DMA(t+1): with tile t+1's NDN + 1 DMAs allowed in
+      // flight, loads returning in order, DMA(t) is complete.
+      if (t + 1 < n_tiles) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(NDN + 1) : "memory");
+      else bwd_wait_all();
       lds_barrier();
-      if (t + 1 < n_tiles) issue_tile(t + 1, b ^ 1);
       const unsigned char* kt = s_k[b];
       const unsigned char* krt = s_kr[b];
 
@@ -571,17 +305,30 @@ __global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdP
         acc_s[tt] = (f32x4){0.f, 0.f, 0.f, 0.f};
         acc_p[tt] = (f32x4){0.f, 0.f, 0.f, 0.f};
       }
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const int tk = tt * 16 + li;
+      // K fragments are read PF steps ahead of their MFMAs; the scheduling
+      // barrier keeps the reads there (sunk next to their MFMAs, each MFMA
+      // would wait out a full LDS round trip with no other wave to run)
+      {
+        constexpr int NS = 2 * KS, PF = 6;
+        auto kread = [&](int st) -> u32x4 {
+          const int ks = st >> 1, tk = (st & 1) * 16 + li;
           const unsigned char* a = ks < KSN ? kt + tk * ROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16)
                                             : krt + tk * (DR * 2) + ((((ks - KSN) * 4 + lg) ^ rope_swz(tk)) * 16);
-          const V8 av = as_v8<V8>(*(const u32x4*)a);
+          return *(const u32x4*)a;
+        };
+        u32x4 fa[PF];
+#pragma unroll
+        for (int i = 0; i < PF; ++i) fa[i] = kread(i);
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+          const int ks = st >> 1, tt = st & 1;
+          const V8 av = as_v8<V8>(fa[st % PF]);
+          if (st + PF < NS) fa[st % PF] = kread(st + PF);
           acc_s[tt] = E::mfma(av, qf[ks], acc_s[tt]);
           if (ks < KSN) acc_p[tt] = E::mfma(av, dof[ks], acc_p[tt]);
+          __builtin_amdgcn_sched_barrier(0);
         }
+      }
 
       // ---- P^T, dS^T (token tt*16 + 4*lg + r, head li) ----
       constexpr bool kSplit = __is_same(T, bf16);
@@ -596,101 +343,67 @@ __global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdP
         const T dh = E::from_f32(ds);
         dsf[j] = dh;
         dsl[j] = E::from_f32(ds - E::to_f32(dh));
-        s_t[0][tk][wave * 16 + li] = dh;
-        s_t[1][tk][wave * 16 + li] = E::from_f32(pp);
+        s_t[0][tk][wave * 16 + li] = kDsMul == 1.f ? dh : E::from_f32(ds * kDsMul);
+        s_t[1][tk][wave * 16 + li] = E::from_f32(pp * kDsMul);
       }
+      lds_barrier();  // dS / P of the 64 heads in LDS
+      // ---- dS / P rows out (16 bytes per thread: 8 heads of one slot) ----
+      {
+        const int cpr = nh / 8;  // chunks per (slot, dS | P) row: 4 or 8
+        for (int e = tid; e < TILE * 2 * cpr; e += NT) {
+          const int tk = e / (2 * cpr), rem = e - tk * 2 * cpr, which = rem / cpr, c = rem - which * cpr;
+          const int j = t * TILE + tk;
+          if (j < n_valid)
+            *(u32x4*)(dsp_row + ((int64_t)(jbase + j) * 2 + which) * p.hp + c * 8) =
+                *(const u32x4*)&s_t[which][tk][c * 8];
+        }
+      }
+      // tile t+2 into the buffer tile t-1 used (every wave is past tile t's
+      // first barrier, so past tile t-1)
+      if (t + 2 < n_tiles) issue_tile(t + 2, (t + 2) % NBUF);
 
       // ---- dq^T += K^T.dS^T, dq_rope^T += Kr^T.dS^T (transposing reads) ----
       {
         const int r1 = lg * 4 + (li >> 2);
         const int hb = (li & 3) >> 1;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          const int ch = 2 * dt + hb;
-          const unsigned char* p1 = kt + r1 * ROW + ((ch ^ nope_swz(r1)) * 16) + (li & 1) * 8;
-          const unsigned char* p2 = kt + (r1 + 16) * ROW + ((ch ^ nope_swz(r1 + 16)) * 16) + (li & 1) * 8;
+        // K^T fragment of d-tile dt (nope tiles, then the rope tiles)
+        constexpr int NQ = NDT + DR / 16, PF = 4;
+        auto tread = [&](int dt) -> V8 {
+          const unsigned char *p1, *p2;
+          if (dt < NDT) {
+            const int ch = 2 * dt + hb;
+            p1 = kt + r1 * ROW + ((ch ^ nope_swz(r1)) * 16) + (li & 1) * 8;
+            p2 = kt + (r1 + 16) * ROW + ((ch ^ nope_swz(r1 + 16)) * 16) + (li & 1) * 8;
+          } else {
+            const int ch = 2 * (dt - NDT) + hb;
+            p1 = krt + r1 * (DR * 2) + ((ch ^ rope_swz(r1)) * 16) + (li & 1) * 8;
+            p2 = krt + (r1 + 16) * (DR * 2) + ((ch ^ rope_swz(r1 + 16)) * 16) + (li & 1) * 8;
+          }
           const i16x4 w1 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1));
           const i16x4 w2 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p2));
           const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
-          acc_dq[dt] = E::mfma(__builtin_bit_cast(V8, w), dsf, acc_dq[dt]);
-          if (kSplit) acc_dq[dt] = E::mfma(__builtin_bit_cast(V8, w), dsl, acc_dq[dt]);
-        }
+          return __builtin_bit_cast(V8, w);
+        };
+        V8 fk[PF];
 #pragma unroll
-        for (int dt = 0; dt < DR / 16; ++dt) {
-          const int ch = 2 * dt + hb;
-          const unsigned char* p1 = krt + r1 * (DR * 2) + ((ch ^ rope_swz(r1)) * 16) + (li & 1) * 8;
-          const unsigned char* p2 = krt + (r1 + 16) * (DR * 2) + ((ch ^ rope_swz(r1 + 16)) * 16) + (li & 1) * 8;
-          const i16x4 w1 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1));
-          const i16x4 w2 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p2));
-          const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
-          acc_dqr[dt] = E::mfma(__builtin_bit_cast(V8, w), dsf, acc_dqr[dt]);
-          if (kSplit) acc_dqr[dt] = E::mfma(__builtin_bit_cast(V8, w), dsl, acc_dqr[dt]);
-        }
-      }
-      lds_barrier();  // dS / P of all 64 heads in LDS
-
-      // ---- dK | dK_rope | dV columns of this wave, summed over 64 heads ----
-      int ph[2][4];
+        for (int i = 0; i < PF; ++i) fk[i] = tread(i);
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) ph[tt][r] = s_list[t * TILE + tt * 16 + lg * 4 + r];
-      if (MERGE) {
-        // nope columns: dS^T.Q + P^T.dO in one accumulator; rope: dS^T.Q_rope
-#pragma unroll
-        for (int i = 0; i <= NNW; ++i) {
-          const bool rope = i == NNW;
-          const int c = rope ? 16 * wave + li : 16 * (wave * NNW + i) + li;
-#pragma unroll
-          for (int tt = 0; tt < 2; ++tt) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-              const V8 ads = as_v8<V8>(*(const u32x4*)&s_t[0][tt * 16 + li][ks * 32 + lg * 8]);
-              acc = E::mfma(ads, xb[rope ? 2 * NNW : i][ks], acc);
-              if (!rope) {
-                const V8 ap = as_v8<V8>(*(const u32x4*)&s_t[1][tt * 16 + li][ks * 32 + lg * 8]);
-                acc = E::mfma(ap, xb[NNW + (rope ? 0 : i)][ks], acc);
-              }
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const int pr = ph[tt][r];
-              if (pr < 0) continue;
-              if (rope) atomicAdd(p.dkr + (int64_t)pr * DR + c, acc[r]);
-              else atomicAdd(p.dk + (int64_t)pr * D + c, acc[r]);
-            }
-          }
-        }
-        continue;
-      }
-#pragma unroll
-      for (int i = 0; i < NCW; ++i) {
-        const int ct = wave * NCW + i;
-        const int sel = ct < (D + DR) / 16 ? 0 : 1;  // dS for dK / dK_rope, P for dV
-        const int c = 16 * ct + li;
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            const V8 a = as_v8<V8>(*(const u32x4*)&s_t[sel][tt * 16 + li][ks * 32 + lg * 8]);
-            acc = E::mfma(a, xb[i][ks], acc);
-          }
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int pr = ph[tt][r];
-            if (pr < 0) continue;
-            if (c < D) atomicAdd(p.dk + (int64_t)pr * D + c, acc[r]);
-            else if (c < D + DR) atomicAdd(p.dkr + (int64_t)pr * DR + (c - D), acc[r]);
-            else atomicAdd(p.dv + (int64_t)pr * D + (c - D - DR), acc[r]);
-          }
+        for (int dt = 0; dt < NQ; ++dt) {
+          const V8 w = fk[dt % PF];
+          if (dt + PF < NQ) fk[dt % PF] = tread(dt + PF);
+          f32x4& acc = dt < NDT ? acc_dq[dt] : acc_dqr[dt - NDT];
+          acc = E::mfma(w, dsf, acc);
+          if (kSplit && lo) acc = E::mfma(w, dsl, acc);
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
+      // s_t is rewritten by the next tile only after its first barrier
     }
     bwd_wait_all();
     lds_barrier();  // s_list is rebuilt for the next range
+    jbase += n_valid;
   }
+  if (hg == 0 && tid == 0) p.nval[rowl] = jbase;
 
   // ---- dq, dq_rope (head li, columns 16*dt + 4*lg + r) ----
   if (hv) {
@@ -712,84 +425,419 @@ __global__ __launch_bounds__(kBwdWgWaves * 64, 1) void sfa_bwd_wg_kernel(SfaBwdP
   }
 }
 
-__global__ __launch_bounds__(256) void bwd_fill_kernel(uint32_t* a, int64_t n, uint32_t v) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i < n) a[i] = v;
+// ---------------------------------------------------------------------------
+// B. records: per attended token, the head-summed dK | dK_rope | dV columns
+// ---------------------------------------------------------------------------
+// rec^T[col][token] = sum_h X[h][col] * Y[h][token] on v_mfma_f32_16x16x32:
+// A = X^T (lane: column li, heads 8*lg..) resident for the row, B = dS or P
+// (lane: token li, heads 8*lg..) from LDS; C register r = column 4*lg + r of
+// token li, so a lane stores 4 consecutive fp16 values of one record.
+// Waves of the record kernel: eight (two per SIMD, 256 registers each), or
+// four when a wave's resident operands need more (D = 512 with 128 heads:
+// each wave then takes two slices, one after the other, with 512 registers).
+template <int D, typename T, bool MERGE, int HP>
+__global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) {
+  using E = Elem<T>;
+  using V8 = typename E::v8;
+  using SL = RecSlices<D, MERGE>;
+  constexpr int DR = 64;
+  constexpr int MT = SL::MT;
+  constexpr int NW = 8;
+  constexpr int KH = HP / 32;          // k-steps over heads
+  constexpr int TILE = kBwdTile;
+  constexpr int ROWB = 2 * HP * 2;     // bytes of a slot's [dS | P] row
+  constexpr int CH = ROWB / 16;        // 16-byte chunks per slot row
+  constexpr int TB = TILE * ROWB;      // tile bytes
+  constexpr int NDMA = TB / 1024;      // 1 KB DMAs per tile
+  constexpr int SPD = 1024 / ROWB;     // slots per DMA
+  constexpr int SWM = CH < 16 ? CH - 1 : 15;  // chunk swizzle mask
+  constexpr int XC = 2 * D + DR;       // staged columns: Q nope | Q rope | dO
+  constexpr int XROW = XC + 16;        // padded staged row (elements)
+  static_assert(NDMA >= 1 && NDMA <= 2 * NW && kRecSlices == NW, "tile DMAs / slices");
+  constexpr int NBUF = 3;              // tile ring: tile t+2 is in flight while tile t runs
+  constexpr int NPOS = 2048;           // record positions resolved per refill (64 tiles)
+  __shared__ __attribute__((aligned(1024))) unsigned char s_ds[NBUF][TB];
+  __shared__ __attribute__((aligned(16))) T s_x[32 * XROW];  // 32 heads of [Q | Q rope | dO]
+  __shared__ int s_pos[NPOS];          // bucket position of each slot of 64 tiles
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const int rowl = blockIdx.x;
+  const int64_t row = p.row0 + rowl;
+  const int nv = p.nval[rowl];
+  const int n_tiles = (nv + TILE - 1) / TILE;
+
+  // ---- this wave's column slice and its A operands X^T (X = [Q | Q rope |
+  // dO] of all heads): 32 heads at a time are staged row-major in LDS and
+  // read back transposed (ds_read_b64_tr_b16: lane li gets column li of a
+  // 4-row block).  Operand slot j of lane group lg holds head
+  // 32*ks + 16*(j >> 2) + 4*lg + (j & 3); the dS / P reads below use the
+  // same order. ----
+  const int sl = wave_s;
+  const int ct0 = SL::t0(sl), nct = SL::n(sl);
+  const bool vslice = !MERGE && sl >= 4;  // dV columns (P^T . dO)
+  V8 xa[MT][KH];                          // Q nope / Q rope / dO columns
+  V8 xo[MERGE ? MT : 1][KH];              // merged nope columns: dO
+  constexpr int CPR = XC / 8;             // 16-byte chunks per staged row
+  for (int ks = 0; ks < KH; ++ks) {
+    for (int e = tid; e < 32 * CPR; e += NW * 64) {
+      const int hh = e / CPR, c = (e - hh * CPR) * 8;
+      const int h = ks * 32 + hh;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (h < p.n1) {
+        const int64_t r = row * p.n1 + h;
+        if (c < D) v = *(const u32x4*)((const T*)p.q + r * D + c);
+        else if (c < D + DR) v = *(const u32x4*)((const T*)p.qr + r * DR + (c - D));
+        else v = *(const u32x4*)((const T*)p.dout + r * D + (c - D - DR));
+      }
+      *(u32x4*)&s_x[hh * XROW + c] = v;
+    }
+    lds_barrier();
+    const int r1 = lg * 4 + (li >> 2);
+    auto xread = [&](int col0) -> V8 {
+      const T* a1 = &s_x[r1 * XROW + col0 + 4 * (li & 3)];
+      const i16x4 w1 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)a1));
+      const i16x4 w2 =
+          __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(a1 + 16 * XROW)));
+      const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
+      return __builtin_bit_cast(V8, w);
+    };
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int ct = ct0 + (i < nct ? i : 0);
+      xa[i][ks] = xread(ct * 16);
+      if constexpr (MERGE) xo[i][ks] = xread(D + DR + (ct * 16 < D ? ct * 16 : 0));
+    }
+    lds_barrier();  // s_x is restaged for the next 32 heads
+  }
+
+  // ---- tile DMA: the tile's slot rows are contiguous in dS / P; slot s of
+  // the tile lands with its 16-byte chunk c at chunk c ^ (s & SWM) ----
+  const unsigned char* src_row = (const unsigned char*)p.dsp + (int64_t)rowl * p.kposp * ROWB;
+  auto issue_tile = [&](int t, int b) {
+    for (int d = wave_s; d < NDMA; d += NW) {
+      const int s = d * SPD + lane / CH;       // slot within the tile
+      const int c = (lane % CH) ^ (s & SWM);   // source chunk for this LDS chunk
+      const unsigned dst = (unsigned)(uintptr_t)&s_ds[b][d * 1024];
+      bwd_dma16_glb(dst, src_row + ((int64_t)t * TILE + s) * ROWB + c * 16);
+    }
+  };
+  // B operand of token tt*16 + li for k-step ks of dS (which 0) or P (1):
+  // heads 32*ks + 4*lg .. +3 and 32*ks + 16 + 4*lg .. +3 (8 bytes each)
+  auto b_read = [&](int b, int tt, int ks, int which) -> V8 {
+    const int s = tt * 16 + li;
+    const int c = which * (HP / 8) + ks * 4 + (lg >> 1);
+    const unsigned char* rb = &s_ds[b][s * ROWB + (lg & 1) * 8];
+    const i16x4 w1 = *(const i16x4*)(rb + ((c ^ (s & SWM)) * 16));
+    const i16x4 w2 = *(const i16x4*)(rb + (((c + 2) ^ (s & SWM)) * 16));
+    const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
+    return __builtin_bit_cast(V8, w);
+  };
+
+  const int32_t* list_row = p.list + (int64_t)rowl * p.kposp;
+  const int32_t* rank_row = p.rank + (int64_t)rowl * p.kposp;
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  // record staging: 16 rows (tokens) of the slice per wave, in s_x (free
+  // after the operands are read)
+  constexpr int SROW = MT * 16 + 8;
+  static_assert(NW * 16 * SROW <= 32 * XROW, "staging fits");
+  _Float16* stg = (_Float16*)s_x + wave_s * 16 * SROW;
+  // DMAs this wave issues per tile (0, 1 or 2)
+  const int ndw = wave_s < NDMA ? (NDMA - wave_s + NW - 1) / NW : 0;
+  if (n_tiles > 0) issue_tile(0, 0);
+  if (n_tiles > 1) issue_tile(1, 1);
+  for (int t = 0; t < n_tiles; ++t) {
+    const int b = t % NBUF;
+    // tile t's DMA has landed: per wave the order is DMA(t), stores(t-1),
+    // DMA(t+1), and loads return in order, so the last ndw may be in flight
+    if (t + 1 < n_tiles && ndw >= 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    else if (t + 1 < n_tiles && ndw == 1) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+    else bwd_wait_all();
+    lds_barrier();
+    if ((t % (NPOS / TILE)) == 0) {
+      // bucket positions of the next 64 tiles' slots (every wave is past
+      // the reads of the previous ones)
+      for (int e = tid; e < NPOS; e += NW * 64) {
+        const int j = t * TILE + e;
+        s_pos[e] = j < nv ? p.offs[list_row[j]] + rank_row[j] : 0;
+      }
+      lds_barrier();
+    }
+    // one 16-token half at a time: the two halves' accumulators are not
+    // live together
+#pragma unroll 1
+    for (int tt = 0; tt < 2; ++tt) {
+      const int j = t * TILE + tt * 16 + li;
+      const int64_t pos = s_pos[(j - (t / (NPOS / TILE)) * NPOS)];
+      f32x4 acc[MT];
+#pragma unroll
+      for (int i = 0; i < MT; ++i) acc[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      // k-steps outer: each B fragment (dS or P of 32 heads) is read right
+      // before the MT products that use it
+#pragma unroll
+      for (int ks = 0; ks < KH; ++ks) {
+        const V8 bf = b_read(b, tt, ks, vslice ? 1 : 0);
+        V8 bq;
+        if constexpr (MERGE) bq = b_read(b, tt, ks, 1);
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+          if (i < nct) {
+            acc[i] = E::mfma(xa[i][ks], bf, acc[i]);
+            if constexpr (MERGE)
+              if ((ct0 + i) * 16 < D) acc[i] = E::mfma(xo[i][ks], bq, acc[i]);
+          }
+      }
+      // the slice's largest magnitude for token li (lanes li, li+16, li+32, li+48)
+      float mx = 0.f;
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, fabsf(acc[i][r]));
+      mx = xgroup_max(mx);
+      // stored value = acc * 2^-e with 2^e > max |acc| (|stored| < 1)
+      int e = 0;
+      if (!(mx < INFINITY)) e = kRecNonFinite;
+      else if (mx > 0.f) (void)frexpf(mx, &e);
+      const float sc = e == kRecNonFinite ? 1.f : ldexpf(1.f, -e);
+      // the 16 tokens' slices go through this wave's LDS staging rows, so
+      // that the stores are whole 16-byte pieces of each record's slice
+      _Float16* srow = stg + li * SROW;
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+        if (i < nct) {
+          const h4 v = {(_Float16)(acc[i][0] * sc), (_Float16)(acc[i][1] * sc), (_Float16)(acc[i][2] * sc),
+                        (_Float16)(acc[i][3] * sc)};
+          *(h4*)(srow + i * 16 + lg * 4) = v;
+        }
+      __builtin_amdgcn_wave_barrier();
+      const int cpr2 = nct * 2;  // 16-byte pieces per record slice
+      for (int q = lane; q < 16 * cpr2; q += 64) {
+        const int tk = q / cpr2, cc = q - tk * cpr2;
+        const int j2 = t * TILE + tt * 16 + tk;
+        if (j2 < nv) {
+          const int64_t pos2 = s_pos[j2 - (t / (NPOS / TILE)) * NPOS];
+          *(u32x4*)(p.rec + pos2 * p.nc + ct0 * 16 + cc * 8) = *(const u32x4*)(stg + tk * SROW + cc * 8);
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      // the exponent of the true value (fp16 dS / P carry 2^kF16Shift)
+      if (j < nv && lg == 0)
+        p.rexp[pos * kRecSlices + sl] =
+            (int16_t)(e == kRecNonFinite ? e : e - (__is_same(T, f16) ? kF16Shift : 0));
+    }
+    // tile t+2 into the buffer tile t-1 used (every wave is past tile t's
+    // barrier), after this tile's stores
+    if (t + 2 < n_tiles) issue_tile(t + 2, (t + 2) % NBUF);
+  }
 }
 
-// fp32 workspace -> output dtype
-template <typename T>
-__global__ __launch_bounds__(256) void cast_f32_kernel(const float* src, T* dst, int64_t n) {
-  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-  if (i + 3 < n) {
-    const float4 v = *(const float4*)(src + i);
-    typedef T T4 __attribute__((ext_vector_type(4)));
-    const T4 o = {Elem<T>::from_f32(v.x), Elem<T>::from_f32(v.y), Elem<T>::from_f32(v.z), Elem<T>::from_f32(v.w)};
-    *(T4*)(dst + i) = o;
-  } else {
-    for (int64_t j = i; j < n; ++j) dst[j] = Elem<T>::from_f32(src[j]);
+// ---------------------------------------------------------------------------
+// C. per key token: the sum of its records, one wave per column slice
+// ---------------------------------------------------------------------------
+// Records of token t are rec[offs[t] .. offs[t+1]); a slice value is
+// fp16 * 2^e.  They are summed in int64 fixed point with 2^-F resolution,
+// F chosen from the largest slice exponent and the record count so that no
+// partial sum overflows; integer addition is exact and associative.  A lane
+// reads 16 bytes (8 columns) of a record, so one load instruction covers
+// 64 / (width / 8) records of the slice; the lanes holding the same columns
+// are summed through LDS at the end.  The chunk's sum is added to the
+// running fp32 sum (FIRST: none yet); FINAL writes the key gradients in the
+// key dtype.
+template <typename T, int D, bool MERGE, bool FIRST, bool FINAL>
+__global__ __launch_bounds__(kRecSlices * 64) void sfa_bwd_reduce_kernel(SfaBwdParams p) {
+  using SL = RecSlices<D, MERGE>;
+  constexpr int DR = 64;
+  constexpr int U = 4;  // loads in flight per lane
+  __shared__ long long s_red[kRecSlices][64][8];
+  const int lane = threadIdx.x & 63;
+  const int s = threadIdx.x >> 6;  // slice
+  const int64_t t = blockIdx.x;
+  const int c0 = SL::t0(s) * 16, width = SL::n(s) * 16;  // <= 160 columns
+  const int cps = width / 8;                 // 16-byte chunks per record slice
+  const int rpi = 64 / cps;                  // records per load instruction
+  const int u = lane / cps, ch = lane - u * cps;
+  const bool act = u < rpi;
+  const int o0 = __builtin_amdgcn_readfirstlane(p.offs[t]);
+  const int len = __builtin_amdgcn_readfirstlane(p.offs[t + 1]) - o0;
+  // pass 1: the largest slice exponent
+  int emax = -100000;
+  for (int i = lane; i < len; i += 64) emax = max(emax, (int)p.rexp[(int64_t)(o0 + i) * kRecSlices + s]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) emax = max(emax, __shfl_xor(emax, o));
+  const bool nonfinite = emax == kRecNonFinite;
+  int lb = 0;
+  while ((1 << lb) < len) ++lb;
+  const int F = 61 - emax - lb;  // |sum| < len * 2^emax <= 2^(emax + lb)
+  // pass 2
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  long long a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (len > 0 && !nonfinite && act) {
+    const _Float16* src = p.rec + (int64_t)o0 * p.nc + c0 + ch * 8;
+    const int16_t* ex = p.rexp + (int64_t)o0 * kRecSlices + s;
+    for (int base = 0; base < len; base += rpi * U) {
+      h8 v[U];
+      int ev[U];
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        const int r = base + k * rpi + u;
+        const bool ok = r < len;
+        v[k] = ok ? *(const h8*)(src + (int64_t)r * p.nc) : (h8){0, 0, 0, 0, 0, 0, 0, 0};
+        ev[k] = ok ? (int)ex[(int64_t)r * kRecSlices] : 0;
+      }
+#pragma unroll
+      for (int k = 0; k < U; ++k) {
+        const double sc = ldexp(1.0, ev[k] + F);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] += __double2ll_rn((double)v[k][e] * sc);
+      }
+    }
   }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s_red[s][lane][e] = a[e];
+  __syncthreads();
+  if (lane >= cps) return;
+  long long sum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int k = 0; k < rpi; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sum[e] += s_red[s][k * cps + ch][e];
+  const double us = ldexp(1.0, -F);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int c = c0 + ch * 8 + e;  // record column
+    float v = len == 0 ? 0.f : (nonfinite ? NAN : (float)((double)sum[e] * us));
+    float* ap = p.acc + t * p.nc + c;
+    if (!FIRST) v += *ap;
+    if (!FINAL) {
+      *ap = v;
+      continue;
+    }
+    const T o = Elem<T>::from_f32(v);
+    if (c < D) ((T*)p.dk)[t * D + c] = o;
+    else if (c < D + DR) ((T*)p.dkr)[t * DR + (c - D)] = o;
+    else ((T*)p.dv)[t * D + (c - D - DR)] = o;
+  }
+}
+
+__global__ __launch_bounds__(256) void bwd_zero_kernel(int32_t* a, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) a[i] = 0;
+}
+
+// exclusive scan of cnt[0..n) into offs[0..n] (one workgroup)
+__global__ __launch_bounds__(1024) void bwd_scan_kernel(const int32_t* cnt, int32_t* offs, int64_t n) {
+  __shared__ int32_t s_sum[1024];
+  const int tid = threadIdx.x;
+  const int64_t per = (n + 1023) / 1024;
+  const int64_t lo = min(n, tid * per), hi = min(n, lo + per);
+  int32_t s = 0;
+  for (int64_t i = lo; i < hi; ++i) s += cnt[i];
+  s_sum[tid] = s;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    const int32_t v = tid >= o ? s_sum[tid - o] : 0;
+    __syncthreads();
+    s_sum[tid] += v;
+    __syncthreads();
+  }
+  int32_t run = tid > 0 ? s_sum[tid - 1] : 0;
+  for (int64_t i = lo; i < hi; ++i) {
+    offs[i] = run;
+    run += cnt[i];
+  }
+  if (tid == 1023) offs[n] = s_sum[1023];
 }
 
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-size_t sfa_bwd_workspace_bytes(int64_t kv_rows, int64_t d) {
-  return (size_t)kv_rows * (size_t)(d + 64 + d) * sizeof(float);
+// Rows per chunk: the per-row workspace of a chunk stays within this budget
+// (a whole S = 4096, topK = 2048, N1 = 128, D = 512 problem fits one chunk).
+constexpr size_t kBwdChunkBudget = 24ull << 30;
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct BwdPlan {
+  int64_t hp, kposp, nc, chunk_rows, nchunks;
+  size_t cnt, offs, acc, list, rank, nval, dsp, rec, rexp, total;
+};
+
+static BwdPlan bwd_plan(int64_t q_rows, int64_t kv_rows, int64_t n1, int64_t d, int64_t total_pos, bool merge,
+                        int esz) {
+  BwdPlan L;
+  L.hp = ((n1 + 31) / 32) * 32;
+  L.kposp = ((total_pos + 31) / 32) * 32;
+  L.nc = merge ? d + 64 : 2 * d + 64;
+  const size_t per_row = (size_t)L.kposp * (2 * sizeof(int32_t) + 2 * L.hp * esz + L.nc * sizeof(_Float16) +
+                                            kRecSlices * sizeof(int16_t)) + sizeof(int32_t);
+  const size_t budget = (test_flags() & kTestSmallBwdChunks) ? ((size_t)1 << 16) : kBwdChunkBudget;
+  int64_t cr = (int64_t)(budget / per_row);
+  if (cr < 1) cr = 1;
+  // equal chunks
+  L.nchunks = q_rows > 0 ? (q_rows + cr - 1) / cr : 1;
+  L.chunk_rows = q_rows > 0 ? (q_rows + L.nchunks - 1) / L.nchunks : 1;
+  size_t o = 0;
+  L.cnt = o;
+  o += align256((size_t)kv_rows * sizeof(int32_t));
+  L.offs = o;
+  o += align256((size_t)(kv_rows + 1) * sizeof(int32_t));
+  L.acc = o;
+  if (L.nchunks > 1) o += align256((size_t)kv_rows * L.nc * sizeof(float));
+  L.nval = o;
+  o += align256((size_t)L.chunk_rows * sizeof(int32_t));
+  L.list = o;
+  o += align256((size_t)L.chunk_rows * L.kposp * sizeof(int32_t));
+  L.rank = o;
+  o += align256((size_t)L.chunk_rows * L.kposp * sizeof(int32_t));
+  L.dsp = o;
+  o += align256((size_t)L.chunk_rows * L.kposp * 2 * L.hp * esz);
+  L.rec = o;
+  o += align256((size_t)L.chunk_rows * L.kposp * L.nc * sizeof(_Float16));
+  L.rexp = o;
+  o += align256((size_t)L.chunk_rows * L.kposp * kRecSlices * sizeof(int16_t));
+  L.total = o;
+  return L;
 }
 
-// The workgroup kernel gathers with buffer loads (32-bit offsets): key
-// tensors of 2 GiB and more take the one-wave kernel.
-// The workgroup kernel (merged when `merge`) or, for key tensors of 2 GiB
-// and more, the one-wave kernel (never merged).  Returns whether the dK
-// workspace already holds dk + dv.
+size_t sfa_bwd_workspace_bytes(int64_t q_rows, int64_t kv_rows, int64_t n1, int64_t d, int64_t total_pos,
+                               bool merge) {
+  return bwd_plan(q_rows, kv_rows, n1, d, total_pos, merge, 2).total;
+}
+
+template <int D, typename T, bool MERGE>
+static hipError_t run_bwd_chunks(SfaBwdParams p, const BwdPlan& L, hipStream_t stream) {
+  const bool buf = (int64_t)p.kv_rows * D * 2 < (1ll << 31) && !(test_flags() & kTestForceGlobalGather);
+  const int64_t zb = (p.kv_rows + 255) / 256;
+  for (int64_t c = 0; c < L.nchunks; ++c) {
+    p.row0 = c * L.chunk_rows;
+    const int64_t nr = min(L.chunk_rows, p.rows - p.row0);
+    if (nr <= 0) break;
+    p.nrows = (int32_t)nr;
+    hipLaunchKernelGGL(bwd_zero_kernel, dim3((unsigned)zb), dim3(256), 0, stream, p.cnt, p.kv_rows);
+    const dim3 ga((unsigned)nr, (unsigned)((p.n1 + kBwdHeads - 1) / kBwdHeads));
+    if (buf) hipLaunchKernelGGL((sfa_bwd_dq_kernel<D, T, true>), ga, dim3(kBwdWaves * 64), 0, stream, p);
+    else hipLaunchKernelGGL((sfa_bwd_dq_kernel<D, T, false>), ga, dim3(kBwdWaves * 64), 0, stream, p);
+    hipLaunchKernelGGL(bwd_scan_kernel, dim3(1), dim3(1024), 0, stream, p.cnt, p.offs, p.kv_rows);
+    const dim3 gb((unsigned)nr);
+    if (p.hp == 32) hipLaunchKernelGGL((sfa_bwd_rec_kernel<D, T, MERGE, 32>), gb, dim3(512), 0, stream, p);
+    else if (p.hp == 64) hipLaunchKernelGGL((sfa_bwd_rec_kernel<D, T, MERGE, 64>), gb, dim3(512), 0, stream, p);
+    else hipLaunchKernelGGL((sfa_bwd_rec_kernel<D, T, MERGE, 128>), gb, dim3(512), 0, stream, p);
+    const dim3 gc((unsigned)p.kv_rows);
+    const bool first = c == 0, final = c == L.nchunks - 1;
+    if (first && final) hipLaunchKernelGGL((sfa_bwd_reduce_kernel<T, D, MERGE, true, true>), gc, dim3(512), 0, stream, p);
+    else if (first) hipLaunchKernelGGL((sfa_bwd_reduce_kernel<T, D, MERGE, true, false>), gc, dim3(512), 0, stream, p);
+    else if (final) hipLaunchKernelGGL((sfa_bwd_reduce_kernel<T, D, MERGE, false, true>), gc, dim3(512), 0, stream, p);
+    else hipLaunchKernelGGL((sfa_bwd_reduce_kernel<T, D, MERGE, false, false>), gc, dim3(512), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 template <int D, typename T>
-static hipError_t launch_sfa_bwd(const SfaBwdParams& p, bool merge, bool* merged, hipStream_t stream) {
-  *merged = false;
-  if ((int64_t)p.kv_rows * D * 2 < (1ll << 31)) {
-    const dim3 grid((unsigned)p.rows, (unsigned)((p.n1 + kBwdWgHeads - 1) / kBwdWgHeads));
-    if (merge) {
-      hipLaunchKernelGGL((sfa_bwd_wg_kernel<D, T, true>), grid, dim3(kBwdWgWaves * 64), 0, stream, p);
-      *merged = true;
-    } else {
-      hipLaunchKernelGGL((sfa_bwd_wg_kernel<D, T, false>), grid, dim3(kBwdWgWaves * 64), 0, stream, p);
-    }
-  } else {
-    hipLaunchKernelGGL((sfa_bwd_kernel<D, T>), dim3((unsigned)p.rows, (unsigned)((p.n1 + 15) / 16)), dim3(64), 0,
-                       stream, p);
-  }
-  return hipGetLastError();
-}
-
-// d_key = dk + dv (fp32 workspaces summed before the cast)
-template <typename T>
-__global__ __launch_bounds__(256) void cast_sum_f32_kernel(const float* a, const float* b, T* dst, int64_t n) {
-  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-  if (i + 3 < n) {
-    const float4 x = *(const float4*)(a + i), y = *(const float4*)(b + i);
-    typedef T T4 __attribute__((ext_vector_type(4)));
-    const T4 o = {Elem<T>::from_f32(x.x + y.x), Elem<T>::from_f32(x.y + y.y), Elem<T>::from_f32(x.z + y.z),
-                  Elem<T>::from_f32(x.w + y.w)};
-    *(T4*)(dst + i) = o;
-  } else {
-    for (int64_t j = i; j < n; ++j) dst[j] = Elem<T>::from_f32(a[j] + b[j]);
-  }
-}
-
-template <typename T>
-static hipError_t launch_cast_sum(const float* a, const float* b, void* dst, int64_t n, hipStream_t stream) {
-  if (n <= 0) return hipSuccess;
-  const int64_t blocks = (n + 1023) / 1024;
-  hipLaunchKernelGGL((cast_sum_f32_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, stream, a, b, (T*)dst, n);
-  return hipGetLastError();
-}
-
-template <typename T>
-static hipError_t launch_cast(const float* src, void* dst, int64_t n, hipStream_t stream) {
-  if (n <= 0) return hipSuccess;
-  const int64_t blocks = (n + 1023) / 1024;
-  hipLaunchKernelGGL((cast_f32_kernel<T>), dim3((unsigned)blocks), dim3(256), 0, stream, src, (T*)dst, n);
-  return hipGetLastError();
+static hipError_t run_bwd_d(const SfaBwdParams& p, const BwdPlan& L, bool merge, hipStream_t stream) {
+  return merge ? run_bwd_chunks<D, T, true>(p, L, stream) : run_bwd_chunks<D, T, false>(p, L, stream);
 }
 
 int sfa_bwd_run(const void* query, const void* query_rope, const void* key, const void* key_rope,
@@ -799,6 +847,9 @@ int sfa_bwd_run(const void* query, const void* query_rope, const void* key, cons
                 int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t d, int64_t sparse_count,
                 int64_t q_rows, int64_t kv_rows, int32_t sparse_block_size, int32_t sparse_mode,
                 int32_t layout, int32_t dtype, float scale_value, void* workspace, hipStream_t stream) {
+  const bool merge = d_value == nullptr;
+  const BwdPlan L = bwd_plan(q_rows, kv_rows, n1, d, sparse_count * (int64_t)sparse_block_size, merge, 2);
+  unsigned char* ws = (unsigned char*)workspace;
   SfaBwdParams p;
   p.q = query;
   p.qr = query_rope;
@@ -814,12 +865,13 @@ int sfa_bwd_run(const void* query, const void* query_rope, const void* key, cons
   p.block_table = nullptr;
   p.dq = d_query;
   p.dqr = d_query_rope;
-  float* ws = (float*)workspace;
-  p.dk = ws;
-  p.dkr = ws + kv_rows * d;
-  p.dv = ws + kv_rows * (d + 64);
+  p.dk = d_key;
+  p.dkr = d_key_rope;
+  p.dv = d_value;
   p.rows = q_rows;
   p.kv_rows = kv_rows;
+  p.row0 = 0;
+  p.nrows = 0;
   p.batch = (int32_t)batch;
   p.s1 = (int32_t)s1;
   p.s2 = (int32_t)s2;
@@ -831,42 +883,54 @@ int sfa_bwd_run(const void* query, const void* query_rope, const void* key, cons
   p.layout_kv = layout;
   p.max_blocks = 0;
   p.page_size = 1;
+  p.hp = (int32_t)L.hp;
+  p.kposp = (int32_t)L.kposp;
+  p.nc = (int32_t)L.nc;
   p.scale = scale_value;
   p.scale_log2 = scale_value * kLog2e;
-  // the fp32 accumulators start at zero (a fill kernel: no memset node when
-  // the caller captures the call in a graph)
-  const int64_t nacc = (int64_t)(sfa_bwd_workspace_bytes(kv_rows, d) / 4);
-  hipLaunchKernelGGL(bwd_fill_kernel, dim3((unsigned)((nacc + 255) / 256)), dim3(256), 0, stream, (uint32_t*)workspace,
-                     nacc, 0u);
-  DSA_HIP(hipGetLastError());
-  bool merged = false;
-  if (q_rows > 0) {
-    hipError_t e;
-    const bool bf = dtype == DSA_DTYPE_BF16;
-    const bool merge = d_value == nullptr;
-    if (d == 128) e = bf ? launch_sfa_bwd<128, bf16>(p, merge, &merged, stream)
-                         : launch_sfa_bwd<128, f16>(p, merge, &merged, stream);
-    else if (d == 256) e = bf ? launch_sfa_bwd<256, bf16>(p, merge, &merged, stream)
-                              : launch_sfa_bwd<256, f16>(p, merge, &merged, stream);
-    else e = bf ? launch_sfa_bwd<512, bf16>(p, merge, &merged, stream)
-                : launch_sfa_bwd<512, f16>(p, merge, &merged, stream);
-    DSA_HIP(e);
+  p.cnt = (int32_t*)(ws + L.cnt);
+  p.offs = (int32_t*)(ws + L.offs);
+  p.acc = (float*)(ws + L.acc);
+  p.nval = (int32_t*)(ws + L.nval);
+  p.list = (int32_t*)(ws + L.list);
+  p.rank = (int32_t*)(ws + L.rank);
+  p.dsp = (void*)(ws + L.dsp);
+  p.rec = (_Float16*)(ws + L.rec);
+  p.rexp = (int16_t*)(ws + L.rexp);
+  if (q_rows == 0) {
+    // no query rows: every key gradient is zero (the reduce kernel writes
+    // zeros for tokens without records)
+    const int64_t zb = (kv_rows + 1 + 255) / 256;
+    hipLaunchKernelGGL(bwd_zero_kernel, dim3((unsigned)zb), dim3(256), 0, stream, p.offs, kv_rows + 1);
+    DSA_HIP(hipGetLastError());
   }
+  hipError_t e;
   const bool bf = dtype == DSA_DTYPE_BF16;
-  auto cast = [&](const float* src, void* dst, int64_t n) {
-    return bf ? launch_cast<bf16>(src, dst, n, stream) : launch_cast<f16>(src, dst, n, stream);
-  };
-  if (d_value) {
-    DSA_HIP(cast(p.dk, d_key, kv_rows * d));
-    DSA_HIP(cast(p.dv, d_value, kv_rows * d));
-  } else if (merged) {
-    DSA_HIP(cast(p.dk, d_key, kv_rows * d));  // dk already holds dk + dv
+  if (q_rows == 0) {
+    const dim3 gc((unsigned)kv_rows);
+    auto zero_out = [&](auto tag) {
+      using T = decltype(tag);
+      if (d == 128) {
+        if (merge) hipLaunchKernelGGL((sfa_bwd_reduce_kernel<T, 128, true, true, true>), gc, dim3(512), 0, stream, p);
+        else hipLaunchKernelGGL((sfa_bwd_reduce_kernel<T, 128, false, true, true>), gc, dim3(512), 0, stream, p);
+      } else if (d == 256) {
+        if (merge) hipLaunchKernelGGL((sfa_bwd_reduce_kernel<T, 256, true, true, true>), gc, dim3(512), 0, stream, p);
+        else hipLaunchKernelGGL((sfa_bwd_reduce_kernel<T, 256, false, true, true>), gc, dim3(512), 0, stream, p);
+      } else {
+        if (merge) hipLaunchKernelGGL((sfa_bwd_reduce_kernel<T, 512, true, true, true>), gc, dim3(512), 0, stream, p);
+        else hipLaunchKernelGGL((sfa_bwd_reduce_kernel<T, 512, false, true, true>), gc, dim3(512), 0, stream, p);
+      }
+      return hipGetLastError();
+    };
+    e = bf ? zero_out(bf16{}) : zero_out(f16{});
+  } else if (d == 128) {
+    e = bf ? run_bwd_d<128, bf16>(p, L, merge, stream) : run_bwd_d<128, f16>(p, L, merge, stream);
+  } else if (d == 256) {
+    e = bf ? run_bwd_d<256, bf16>(p, L, merge, stream) : run_bwd_d<256, f16>(p, L, merge, stream);
   } else {
-    // shared latent: d_key = dk + dv
-    DSA_HIP(bf ? launch_cast_sum<bf16>(p.dk, p.dv, d_key, kv_rows * d, stream)
-               : launch_cast_sum<f16>(p.dk, p.dv, d_key, kv_rows * d, stream));
+    e = bf ? run_bwd_d<512, bf16>(p, L, merge, stream) : run_bwd_d<512, f16>(p, L, merge, stream);
   }
-  DSA_HIP(cast(p.dkr, d_key_rope, kv_rows * 64));
+  DSA_HIP(e);
   return DSA_OK;
 }
 

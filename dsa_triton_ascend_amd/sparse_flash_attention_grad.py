@@ -63,6 +63,8 @@ def _sfa_grad(query, key, value, sparse_indices, d_out, out, softmax_max, softma
     if query_rope is None or key_rope is None:
         raise ValueError("query_rope and key_rope are required (no empty rope)")
     if deterministic:
+        # the reference rejects it (sparse_flash_attention_grad_triton.py:434-435); kept for
+        # parity, although every output here is deterministic
         raise ValueError("deterministic=True is not supported (scatter-add path)")
     if sparse_block_size < 1 or (sparse_block_size & (sparse_block_size - 1)) != 0 \
             or sparse_block_size > 128:
@@ -127,7 +129,7 @@ def _sfa_grad(query, key, value, sparse_indices, d_out, out, softmax_max, softma
         raise ValueError("value dtype must equal the key dtype")
     dv = None if merge_kv else torch.empty(key.shape, dtype=key.dtype, device=device)
     lib = _lib.load()
-    ws_bytes = lib.dsa_sfa_bwd_workspace_size(kv_rows, D)
+    ws_bytes = lib.dsa_sfa_bwd_workspace_size(q_rows, kv_rows, N1, D, K, sparse_block_size, 1 if merge_kv else 0)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
     c = [t.contiguous() for t in (query, query_rope, key, key_rope, d_out, out)]
     si = sparse_indices.to(torch.int32).contiguous()

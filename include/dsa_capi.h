@@ -63,6 +63,10 @@ int dsa_abi_version(void);
  * instead of 32-bit buffer offsets.  Process-wide; 0 in normal use.
  */
 #define DSA_TEST_FORCE_GLOBAL_GATHER 1
+/* Bit 1: dsa_sfa_bwd plans its row chunks for a 64 KiB workspace budget (so
+ * that small problems run several chunks); set it around both the
+ * workspace query and the call. */
+#define DSA_TEST_SMALL_BWD_CHUNKS 2
 void dsa_set_test_flags(int32_t flags);
 
 /*
@@ -132,9 +136,13 @@ int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* k
  * d_value may be NULL: d_key then receives dk + dv, summed in fp32 before
  * the cast (MLA absorb, value = key[..., :D]: the gradient of the shared
  * latent, which the reference's bprop recipe forms as dk + dv, 30-71).
- * The dK / dV scatter-add uses fp32 atomics: results may differ in the last
- * bits between runs, as the reference's (deterministic mode is rejected by
- * the reference API, 434-435).  The workspace holds the fp32 accumulators.
+ * Every output is deterministic (bit-identical between runs): the dK / dV
+ * contributions of each (query row, token) are summed over all heads and
+ * reduced per key token in integer fixed point, where the reference
+ * scatter-adds with fp32 atomics (277-300) and rejects deterministic mode
+ * (434-435).  The workspace (dsa_sfa_bwd_workspace_size) holds the
+ * per-slot dS / P, the per-token records and their buckets; rows are
+ * processed in chunks that keep it within about 24 GiB.
  */
 int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
                 const int32_t* sparse_indices, const void* d_out, const void* out,
@@ -145,8 +153,10 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
                 int32_t sparse_block_size, int32_t sparse_mode, int32_t layout, int32_t dtype,
                 float scale_value, void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes of dsa_sfa_bwd: kv_rows * (2*d + 64) fp32. */
-size_t dsa_sfa_bwd_workspace_size(int64_t kv_rows, int64_t d);
+/* Workspace bytes of dsa_sfa_bwd for these sizes; merge_kv != 0 when
+ * d_value will be NULL (dk + dv in one output). */
+size_t dsa_sfa_bwd_workspace_size(int64_t q_rows, int64_t kv_rows, int64_t n1, int64_t d,
+                                  int64_t sparse_count, int32_t sparse_block_size, int32_t merge_kv);
 
 /*
  * Sparse lightning-indexer KL-loss backward.  Replaces the reference core
