@@ -21,6 +21,8 @@ import os
 import sys
 import time
 
+INT64_MAX = 9223372036854775807  # pre_tokens / next_tokens: no band
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
@@ -94,7 +96,7 @@ def time_decode(sets, steps, warmup):
         st = lib.dsa_sfa_fwd(
             s["q"].data_ptr(), s["qr"].data_ptr(), s["cache"].data_ptr(), s["cache_r"].data_ptr(),
             s["si"].data_ptr(), out.data_ptr(), None, None, None, act_k.data_ptr(), s["bt"].data_ptr(),
-            B, 1, CTX, N1, D, DR, K, B, nblk * PAGE, CTX // PAGE, PAGE, 1, 0,
+            B, 1, CTX, N1, D, DR, K, B, nblk * PAGE, CTX // PAGE, PAGE, 1, 0, INT64_MAX, INT64_MAX,
             _lib.LAYOUT["BSND"], _lib.LAYOUT["PA_BSND"], _lib.DTYPE_BF16, scale, 0,
             ws.data_ptr(), ws_bytes, stream)
         if st != 0:

@@ -47,7 +47,8 @@ SIGNATURES = {
         _i32p, _i32p, _i32p,                  # actual_seq_q, actual_seq_kv, block_table
         _i64, _i64, _i64, _i64, _i64, _i64,   # batch, s1, s2, n1, d, d_rope
         _i64, _i64, _i64, _i64, _i64,         # sparse_count, q_rows, kv_rows, max_blocks, page_size
-        _i32, _i32, _i32, _i32, _i32,         # sparse_block_size, sparse_mode, layout_q, layout_kv, dtype
+        _i32, _i32, _i64, _i64,               # sparse_block_size, sparse_mode, pre_tokens, next_tokens
+        _i32, _i32, _i32,                     # layout_q, layout_kv, dtype
         _f32, _i32,                           # scale_value, return_lse
         _vp, _sz, _vp,                        # workspace, workspace_bytes, stream
     ]),
@@ -58,7 +59,8 @@ SIGNATURES = {
         _i32p, _i32p, _i32p,                  # actual_seq_q, actual_seq_kv, block_table
         _i64, _i64, _i64, _i64, _i64, _i64,   # batch, s1, s2, n1, d, d_rope
         _i64, _i64, _i64, _i64, _i64,         # sparse_count, q_rows, kv_rows, max_blocks, page_size
-        _i32, _i32, _i32, _i32, _i32,         # sparse_block_size, sparse_mode, layout_q, layout_kv, dtype
+        _i32, _i32, _i64, _i64,               # sparse_block_size, sparse_mode, pre_tokens, next_tokens
+        _i32, _i32, _i32,                     # layout_q, layout_kv, dtype
         _f32, _i32,                           # scale_value, return_lse
         _vp,                                  # stream
     ]),
@@ -69,7 +71,8 @@ SIGNATURES = {
         _vp, _vp, _vp, _vp, _vp,              # d_query, d_query_rope, d_key, d_key_rope, d_value
         _i64, _i64, _i64, _i64, _i64, _i64,   # batch, s1, s2, n1, d, d_rope
         _i64, _i64, _i64,                     # sparse_count, q_rows, kv_rows
-        _i32, _i32, _i32, _i32,               # sparse_block_size, sparse_mode, layout, dtype
+        _i32, _i32, _i64, _i64,               # sparse_block_size, sparse_mode, pre_tokens, next_tokens
+        _i32, _i32,                           # layout, dtype
         _f32,                                 # scale_value
         _vp, _sz, _vp,                        # workspace, workspace_bytes, stream
     ]),

@@ -42,37 +42,38 @@ class SparseFlashAttentionFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, query, key, query_rope, key_rope, sparse_indices, scale_value,
                 actual_seq_lengths_query, actual_seq_lengths_kv, sparse_block_size, layout,
-                sparse_mode):
+                sparse_mode, pre_tokens, next_tokens):
         out, smax, ssum = sparse_flash_attention_triton(
             query, key, None, sparse_indices, scale_value=scale_value,
             actual_seq_lengths_query=actual_seq_lengths_query,
             actual_seq_lengths_kv=actual_seq_lengths_kv, query_rope=query_rope, key_rope=key_rope,
             sparse_block_size=sparse_block_size, layout_query=layout, layout_kv=layout,
-            sparse_mode=sparse_mode, return_softmax_lse=True)
+            sparse_mode=sparse_mode, pre_tokens=pre_tokens, next_tokens=next_tokens,
+            return_softmax_lse=True)
         ctx.save_for_backward(query, key, query_rope, key_rope, sparse_indices, out, smax, ssum)
         ctx.args = (scale_value, actual_seq_lengths_query, actual_seq_lengths_kv, sparse_block_size,
-                    layout, sparse_mode)
+                    layout, sparse_mode, pre_tokens, next_tokens)
         ctx.mark_non_differentiable(smax, ssum)
         return out, smax, ssum
 
     @staticmethod
     def backward(ctx, d_out, d_smax, d_ssum):
         query, key, query_rope, key_rope, sparse_indices, out, smax, ssum = ctx.saved_tensors
-        scale_value, act_q, act_k, bs, layout, mode = ctx.args
+        scale_value, act_q, act_k, bs, layout, mode, pre, nxt = ctx.args
         if d_out is None:
-            return (None,) * 11
+            return (None,) * 13
         # shared latent: d_key = dk (QK path) + dv (PV path), summed in fp32
         dq, d_key, _, dqr, dkr = _sfa_grad(
             query, key, key, sparse_indices, d_out.contiguous(), out, smax, ssum, scale_value,
-            query_rope, key_rope, act_q, act_k, bs, layout, mode, INT64_MAX, INT64_MAX, False,
+            query_rope, key_rope, act_q, act_k, bs, layout, mode, pre, nxt, False,
             merge_kv=True)
-        return dq, d_key, dqr, dkr, None, None, None, None, None, None, None
+        return dq, d_key, dqr, dkr, None, None, None, None, None, None, None, None, None
 
 
 def sparse_flash_attention_train(query, key, sparse_indices, scale_value=1.0, query_rope=None,
                                  key_rope=None, actual_seq_lengths_query=None,
                                  actual_seq_lengths_kv=None, sparse_block_size=1, layout="BSND",
-                                 sparse_mode=3):
+                                 sparse_mode=3, pre_tokens=INT64_MAX, next_tokens=INT64_MAX):
     """Differentiable SFA forward for training (BSND or TND; the backward has
     no paged-KV form, as in the reference).  Returns
     ``(attention_out, softmax_max, softmax_sum)``."""
@@ -80,7 +81,7 @@ def sparse_flash_attention_train(query, key, sparse_indices, scale_value=1.0, qu
         raise ValueError(f"layout must be BSND or TND for training, got {layout}")
     return SparseFlashAttentionFunction.apply(
         query, key, query_rope, key_rope, sparse_indices, scale_value, actual_seq_lengths_query,
-        actual_seq_lengths_kv, sparse_block_size, layout, sparse_mode)
+        actual_seq_lengths_kv, sparse_block_size, layout, sparse_mode, pre_tokens, next_tokens)
 
 
 class SparseLightningIndexerKLLossFunction(torch.autograd.Function):

@@ -54,8 +54,9 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
                 const int32_t* block_table, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
                 int64_t d, int64_t sparse_count, int64_t q_rows, int64_t kv_rows,
                 int64_t max_blocks, int64_t page_size, int32_t sparse_block_size,
-                int32_t sparse_mode, int32_t layout_query, int32_t layout_kv, int32_t dtype,
-                float scale_value, int32_t return_lse, void* workspace, hipStream_t stream);
+                int32_t sparse_mode, int64_t pre_tokens, int64_t next_tokens, int32_t layout_query,
+                int32_t layout_kv, int32_t dtype, float scale_value, int32_t return_lse, void* workspace,
+                hipStream_t stream);
 
 // sfa_bwd.hip
 size_t sfa_bwd_workspace_bytes(int64_t q_rows, int64_t kv_rows, int64_t n1, int64_t d, int64_t total_pos,
@@ -78,7 +79,8 @@ int sfa_bwd_run(const void* query, const void* query_rope, const void* key, cons
                 void* d_query, void* d_query_rope, void* d_key, void* d_key_rope, void* d_value,
                 int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t d, int64_t sparse_count,
                 int64_t q_rows, int64_t kv_rows, int32_t sparse_block_size, int32_t sparse_mode,
-                int32_t layout, int32_t dtype, float scale_value, void* workspace, hipStream_t stream);
+                int64_t pre_tokens, int64_t next_tokens, int32_t layout, int32_t dtype, float scale_value,
+                void* workspace, hipStream_t stream);
 
 // dense_kl.hip
 size_t dense_kl_workspace_bytes(int64_t batch, int64_t s1, int64_t s2, int64_t di);
@@ -212,7 +214,7 @@ extern "C" {
 
 const char* dsa_last_error(void) { return g_err; }
 
-int dsa_abi_version(void) { return 2; }
+int dsa_abi_version(void) { return 3; }
 
 void dsa_set_test_flags(int32_t flags) { g_test_flags.store(flags, std::memory_order_relaxed); }
 
@@ -228,9 +230,9 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, cons
                 const int32_t* block_table, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
                 int64_t d, int64_t d_rope, int64_t sparse_count, int64_t q_rows, int64_t kv_rows,
                 int64_t max_blocks, int64_t page_size, int32_t sparse_block_size,
-                int32_t sparse_mode, int32_t layout_query, int32_t layout_kv, int32_t dtype,
-                float scale_value, int32_t return_lse, void* workspace, size_t workspace_bytes,
-                void* stream) {
+                int32_t sparse_mode, int64_t pre_tokens, int64_t next_tokens, int32_t layout_query,
+                int32_t layout_kv, int32_t dtype, float scale_value, int32_t return_lse, void* workspace,
+                size_t workspace_bytes, void* stream) {
   g_err[0] = '\0';
   const int st = sfa_fwd_check(query, query_rope, key, key_rope, sparse_indices, attention_out, softmax_max, softmax_sum,
                                  actual_seq_q, actual_seq_kv, block_table, batch, s1, s2, n1, d, d_rope,
@@ -245,7 +247,7 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, cons
   return sfa_fwd_run(query, query_rope, key, key_rope, sparse_indices, attention_out, softmax_max,
                      softmax_sum, actual_seq_q, actual_seq_kv, block_table, batch, s1, s2, n1, d,
                      sparse_count, q_rows, kv_rows, max_blocks, page_size, sparse_block_size,
-                     sparse_mode, layout_query, layout_kv, dtype, scale_value, return_lse,
+                     sparse_mode, pre_tokens, next_tokens, layout_query, layout_kv, dtype, scale_value, return_lse,
                      workspace, (hipStream_t)stream);
 }
 
@@ -255,8 +257,9 @@ int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* k
                         const int32_t* block_table, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
                         int64_t d, int64_t d_rope, int64_t sparse_count, int64_t q_rows, int64_t kv_rows,
                         int64_t max_blocks, int64_t page_size, int32_t sparse_block_size,
-                        int32_t sparse_mode, int32_t layout_query, int32_t layout_kv, int32_t dtype,
-                        float scale_value, int32_t return_lse, void* stream) {
+                        int32_t sparse_mode, int64_t pre_tokens, int64_t next_tokens, int32_t layout_query,
+                        int32_t layout_kv, int32_t dtype, float scale_value, int32_t return_lse,
+                        void* stream) {
   g_err[0] = '\0';
   const int st = sfa_fwd_check(query, query_rope, key, key_rope, sparse_indices, attention_out, softmax_max, softmax_sum,
                                  actual_seq_q, actual_seq_kv, block_table, batch, s1, s2, n1, d, d_rope,
@@ -276,7 +279,7 @@ int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* k
   return sfa_fwd_run(query, query_rope, key, key_rope, sparse_indices, attention_out, softmax_max,
                      softmax_sum, actual_seq_q, actual_seq_kv, block_table, batch, s1, s2, n1, d,
                      sparse_count, q_rows, kv_rows, max_blocks, page_size, sparse_block_size,
-                     sparse_mode, layout_query, layout_kv, dtype, scale_value, return_lse, ws,
+                     sparse_mode, pre_tokens, next_tokens, layout_query, layout_kv, dtype, scale_value, return_lse, ws,
                      (hipStream_t)stream);
 }
 
@@ -292,8 +295,8 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
                 void* d_query, void* d_query_rope, void* d_key, void* d_key_rope, void* d_value,
                 int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t d, int64_t d_rope,
                 int64_t sparse_count, int64_t q_rows, int64_t kv_rows, int32_t sparse_block_size,
-                int32_t sparse_mode, int32_t layout, int32_t dtype, float scale_value, void* workspace,
-                size_t workspace_bytes, void* stream) {
+                int32_t sparse_mode, int64_t pre_tokens, int64_t next_tokens, int32_t layout, int32_t dtype,
+                float scale_value, void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = '\0';
   DSA_CHECK_ARG(query && query_rope && key && key_rope && sparse_indices && d_out && out && softmax_max &&
                     softmax_sum,
@@ -329,7 +332,7 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
   }
   return sfa_bwd_run(query, query_rope, key, key_rope, sparse_indices, d_out, out, softmax_max, softmax_sum,
                      actual_seq_q, actual_seq_kv, d_query, d_query_rope, d_key, d_key_rope, d_value, batch, s1,
-                     s2, n1, d, sparse_count, q_rows, kv_rows, sparse_block_size, sparse_mode, layout, dtype,
+                     s2, n1, d, sparse_count, q_rows, kv_rows, sparse_block_size, sparse_mode, pre_tokens, next_tokens, layout, dtype,
                      scale_value, workspace, (hipStream_t)stream);
 }
 

@@ -64,6 +64,7 @@ struct SfaBwdParams {
   int64_t row0;    // first row of the chunk
   int32_t nrows;   // rows of the chunk
   int32_t batch, s1, s2, n1, K, bs, mode, layout_q, layout_kv, max_blocks, page_size;
+  int64_t band_pre, band_next;  // pre_tokens / next_tokens clamped to +-kBandOpen
   int32_t hp;      // heads padded to a multiple of 32 (dS / P row stride)
   int32_t kposp;   // index positions per row, padded to a multiple of 32
   int32_t nc;      // record columns: 2D + 64, or D + 64 when merged
@@ -846,7 +847,8 @@ int sfa_bwd_run(const void* query, const void* query_rope, const void* key, cons
                 void* d_query, void* d_query_rope, void* d_key, void* d_key_rope, void* d_value,
                 int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t d, int64_t sparse_count,
                 int64_t q_rows, int64_t kv_rows, int32_t sparse_block_size, int32_t sparse_mode,
-                int32_t layout, int32_t dtype, float scale_value, void* workspace, hipStream_t stream) {
+                int64_t pre_tokens, int64_t next_tokens, int32_t layout, int32_t dtype, float scale_value,
+                void* workspace, hipStream_t stream) {
   const bool merge = d_value == nullptr;
   const BwdPlan L = bwd_plan(q_rows, kv_rows, n1, d, sparse_count * (int64_t)sparse_block_size, merge, 2);
   unsigned char* ws = (unsigned char*)workspace;
@@ -879,6 +881,8 @@ int sfa_bwd_run(const void* query, const void* query_rope, const void* key, cons
   p.K = (int32_t)sparse_count;
   p.bs = sparse_block_size;
   p.mode = sparse_mode;
+  p.band_pre = band_clamp(pre_tokens);
+  p.band_next = band_clamp(next_tokens);
   p.layout_q = layout;
   p.layout_kv = layout;
   p.max_blocks = 0;

@@ -5,14 +5,31 @@
 // handling the reference does on the host (TND cumulative lengths, PA_BSND
 // block_table, block-wise ids; sparse_flash_attention_triton.py:345-421).
 // The parameter structs of both kernels carry the fields used here.
+//
+// Band mask: the reference accepts only pre_tokens = next_tokens = INT64_MAX
+// (sparse_flash_attention_triton.py:531-532).  Other values select the band
+// of the Ascend FlashAttention operators: token t of a row is visible iff
+// diag - pre_tokens <= t <= diag + next_tokens, with diag = s1 in mode 0 and
+// act_k - act_q + s1 in mode 3.  The host clamps both to +-kBandOpen, which
+// keeps the sums below in int64 range and makes INT64_MAX an open side
+// (|diag| < 2^32 and tokens lie in [0, 2^31)).
 #pragma once
 
 #include "common.h"
 
 namespace dsa {
 
+constexpr int64_t kBandOpen = 1ll << 40;
+
+__host__ __device__ inline int64_t band_clamp(int64_t v) {
+  return v > kBandOpen ? kBandOpen : (v < -kBandOpen ? -kBandOpen : v);
+}
+
 struct RowInfo {
-  int b, s1, act_q, act_k, threshold;
+  int b, s1, act_q, act_k;
+  // tokens lo <= t < hi are attended: hi = min(act_k, causal threshold,
+  // next_tokens bound), lo = the pre_tokens bound (0 without a band)
+  int lo, hi;
   int64_t kv_base;
   bool active;
 };
@@ -44,8 +61,16 @@ __device__ __forceinline__ RowInfo sfa_row_info(const P& p, int row) {
     ri.kv_base = (int64_t)ri.b * p.s2;  // unused for PA_BSND
     ri.act_k = p.act_k ? p.act_k[ri.b] : p.s2;
   }
-  ri.threshold = p.mode == 0 ? ri.act_k : ri.act_k - ri.act_q + ri.s1 + 1;
-  ri.active = (ri.s1 < ri.act_q) && (ri.threshold > 0);
+  const int64_t thr = p.mode == 0 ? ri.act_k : (int64_t)ri.act_k - ri.act_q + ri.s1 + 1;
+  const int64_t diag = p.mode == 0 ? (int64_t)ri.s1 : (int64_t)ri.act_k - ri.act_q + ri.s1;
+  // band_pre / band_next are clamped to +-kBandOpen on the host
+  const int64_t hi = min(min(thr, (int64_t)ri.act_k), diag + p.band_next + 1);
+  const int64_t lo = diag - p.band_pre;
+  ri.hi = (int)max(hi, (int64_t)0);
+  ri.lo = (int)min(max(lo, (int64_t)0), (int64_t)0x7fffffff);
+  // a row with no visible token resolves nothing (its outputs stay zero,
+  // like a row of -1 ids)
+  ri.active = (ri.s1 < ri.act_q) && (ri.hi > ri.lo);
   return ri;
 }
 
@@ -67,7 +92,7 @@ __device__ __forceinline__ bool sfa_resolve_id(const P& p, const RowInfo& ri, in
                                                const int32_t* tab) {
   if (id < 0) return false;
   int64_t tok = (int64_t)id * p.bs + (pos % p.bs);
-  if (tok >= ri.threshold || tok >= ri.act_k) return false;
+  if (tok >= ri.hi || tok < ri.lo) return false;
   if (p.layout_kv == DSA_LAYOUT_PA_BSND) {
     if (tok >= (int64_t)p.max_blocks * p.page_size) return false;
     int blk = tab[tok / p.page_size];

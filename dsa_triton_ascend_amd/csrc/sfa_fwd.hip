@@ -60,6 +60,7 @@ struct SfaFwdParams {
   int32_t batch, s1, s2, n1, K;
   int32_t bs;  // sparse_block_size
   int32_t mode, layout_q, layout_kv;
+  int64_t band_pre, band_next;  // pre_tokens / next_tokens clamped to +-kBandOpen
   int32_t max_blocks, page_size;
   int32_t splits, rows_per_xcd, pos_per_split;
   float scale_log2;
@@ -989,8 +990,9 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
                 const int32_t* block_table, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
                 int64_t d, int64_t sparse_count, int64_t q_rows, int64_t kv_rows,
                 int64_t max_blocks, int64_t page_size, int32_t sparse_block_size,
-                int32_t sparse_mode, int32_t layout_query, int32_t layout_kv, int32_t dtype,
-                float scale_value, int32_t return_lse, void* workspace, hipStream_t stream) {
+                int32_t sparse_mode, int64_t pre_tokens, int64_t next_tokens, int32_t layout_query,
+                int32_t layout_kv, int32_t dtype, float scale_value, int32_t return_lse, void* workspace,
+                hipStream_t stream) {
   SfaFwdParams p;
   p.q = query;
   p.qr = query_rope;
@@ -1012,6 +1014,8 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
   p.K = (int32_t)sparse_count;
   p.bs = sparse_block_size;
   p.mode = sparse_mode;
+  p.band_pre = band_clamp(pre_tokens);
+  p.band_next = band_clamp(next_tokens);
   p.layout_q = layout_query;
   p.layout_kv = layout_kv;
   p.max_blocks = (int32_t)max_blocks;

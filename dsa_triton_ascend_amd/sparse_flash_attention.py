@@ -11,6 +11,11 @@ expansion, lines 551-611) is done inside the kernel instead: no host loops,
 no device->host synchronisation.
 
 Deliberate differences, all on inputs the reference does not handle:
+* ``pre_tokens`` / ``next_tokens`` other than INT64_MAX (rejected by the
+  reference, lines 531-532) select a band: token t of query row s1 is
+  visible iff diag - pre_tokens <= t <= diag + next_tokens, with diag = s1
+  in sparse_mode 0 and act_kv - act_q + s1 in sparse_mode 3 (the band of the
+  Ascend FlashAttention operators; INT64_MAX leaves a side open);
 * a block_table entry outside [0, blocks) reads as a zero row like -1
   (the reference would raise while slicing);
 * ``block_size`` must equal key.shape[1] when given (the reference mixes the
@@ -45,6 +50,22 @@ def _expect_shape(t, shape, name):
 def _expect_numel(t, n, name):
     if t.numel() != n:
         raise ValueError(f"{name} must have {n} elements, got {t.numel()} (shape {tuple(t.shape)})")
+
+
+def _band_args(pre_tokens, next_tokens):
+    """pre_tokens / next_tokens as Python ints in int64 range (the C-ABI
+    takes int64_t; ctypes would wrap larger values silently)."""
+    out = []
+    for name, v in (("pre_tokens", pre_tokens), ("next_tokens", next_tokens)):
+        if isinstance(v, torch.Tensor):
+            v = v.item()
+        if isinstance(v, bool) or int(v) != v:
+            raise ValueError(f"{name} must be an integer, got {v!r}")
+        v = int(v)
+        if not -INT64_MAX - 1 <= v <= INT64_MAX:
+            raise ValueError(f"{name} must fit in int64, got {v}")
+        out.append(v)
+    return tuple(out)
 
 
 def _check_device(*tensors):
@@ -92,8 +113,7 @@ def sparse_flash_attention_triton(
     """
     if attention_mode != 2:
         raise ValueError("Only attention_mode=2 (MLA-absorb) is supported")
-    if pre_tokens != INT64_MAX or next_tokens != INT64_MAX:
-        raise ValueError("pre_tokens/next_tokens only support default INT64_MAX")
+    pre_tokens, next_tokens = _band_args(pre_tokens, next_tokens)
     if sparse_mode not in (0, 3):
         raise ValueError("Only sparse_mode 0 (full) / 3 (rightDownCausal) supported")
     if query_rope is None or key_rope is None:
@@ -208,7 +228,8 @@ def sparse_flash_attention_triton(
         _lib.ptr(ssum) if return_softmax_lse else None,
         _lib.ptr(act_q), _lib.ptr(act_k), _lib.ptr(bt),
         B, S1, S2, N1, D, D_ROPE, K, q_rows, kv_rows, max_blocks, page,
-        sparse_block_size, sparse_mode, _lib.LAYOUT[layout_query], _lib.LAYOUT[layout_kv],
+        sparse_block_size, sparse_mode, pre_tokens, next_tokens, _lib.LAYOUT[layout_query],
+        _lib.LAYOUT[layout_kv],
         _lib.dtype_code(query.dtype), float(scale_value), 1 if return_softmax_lse else 0,
         _lib.ptr(ws), ws_bytes, _lib.stream_handle(device))
     _lib.check(status, "dsa_sfa_fwd")
@@ -243,13 +264,14 @@ class SparseFlashAttentionTriton(torch.nn.Module):
             # training: the forward/backward pair as one autograd op (the
             # reference's P.Morph bprop recipe, sparse_flash_attention_grad_triton.py:30-71)
             from .autograd import sparse_flash_attention_train
-            if self.pre_tokens != INT64_MAX or self.next_tokens != INT64_MAX or self.attention_mode != 2:
-                raise ValueError("pre_tokens/next_tokens only support default and attention_mode must be 2")
+            if self.attention_mode != 2:
+                raise ValueError("Only attention_mode=2 (MLA-absorb) is supported")
             out, smax, ssum = sparse_flash_attention_train(
                 query, key, sparse_indices, scale_value=self.scale_value, query_rope=query_rope,
                 key_rope=key_rope, actual_seq_lengths_query=actual_seq_lengths_query,
                 actual_seq_lengths_kv=actual_seq_lengths_kv, sparse_block_size=self.sparse_block_size,
-                layout=self.layout_query, sparse_mode=self.sparse_mode)
+                layout=self.layout_query, sparse_mode=self.sparse_mode, pre_tokens=self.pre_tokens,
+                next_tokens=self.next_tokens)
             if not self.return_softmax_lse:
                 smax, ssum = torch.zeros_like(smax), torch.zeros_like(ssum)
             return out, smax, ssum

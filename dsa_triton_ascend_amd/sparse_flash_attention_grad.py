@@ -4,19 +4,22 @@ the HIP library.
 Drop-in for ``sparse_flash_attention_grad_triton`` /
 ``SparseFlashAttentionGradTriton`` (sparse_flash_attention_grad_triton.py:
 382-586): same argument names and defaults (``layout="BSND"``,
-``sparse_mode=3``), the same guards (ValueError for non-default
-pre/next_tokens, sparse modes other than 0/3, missing rope,
-``deterministic=True``, a block size that is not a power of two <= 128, D,
+``sparse_mode=3``), the same guards (ValueError for sparse modes other than
+0/3, missing rope, ``deterministic=True``, a block size that is not a power of two <= 128, D,
 rope width, N2 != 1, N1 not a power of two <= 128) and the same return tuple
 ``(d_query, d_key, d_value, d_query_rope, d_key_rope)`` with the shapes and
 dtypes of the corresponding inputs.  TND rows and block-wise indices are
-resolved in the kernel (no host unpacking).
+resolved in the kernel (no host unpacking).  ``pre_tokens`` /
+``next_tokens`` other than INT64_MAX, which the reference rejects (lines
+428-429), select the same band as the forward: token t of query row s1 is
+visible iff diag - pre_tokens <= t <= diag + next_tokens, diag = s1 in
+sparse_mode 0 and act_kv - act_q + s1 in sparse_mode 3.
 """
 import torch
 
 from . import _lib
-from .sparse_flash_attention import (INT64_MAX, _check_device, _expect_numel, _expect_shape, _seq_tensor,
-                                     _VALID_D, _VALID_N1)
+from .sparse_flash_attention import (INT64_MAX, _band_args, _check_device, _expect_numel, _expect_shape,
+                                     _seq_tensor, _VALID_D, _VALID_N1)
 
 _D_ROPE = 64
 
@@ -56,8 +59,7 @@ def _sfa_grad(query, key, value, sparse_indices, d_out, out, softmax_max, softma
     """Body of the backward.  With ``merge_kv`` the key gradient is dk + dv,
     summed in fp32 before the cast (the shared-latent gradient), and d_value
     is None."""
-    if pre_tokens != INT64_MAX or next_tokens != INT64_MAX:
-        raise ValueError("pre_tokens/next_tokens only support default INT64_MAX")
+    pre_tokens, next_tokens = _band_args(pre_tokens, next_tokens)
     if sparse_mode not in (0, 3):
         raise ValueError("Only sparse_mode 0 (full) / 3 (rightDownCausal) supported")
     if query_rope is None or key_rope is None:
@@ -141,7 +143,7 @@ def _sfa_grad(query, key, value, sparse_indices, d_out, out, softmax_max, softma
         _lib.ptr(act_q), _lib.ptr(act_k),
         dq.data_ptr(), dqr.data_ptr(), dk.data_ptr(), dkr.data_ptr(), _lib.ptr(dv),
         B, S1, S2, N1, D, D_ROPE, K, q_rows, kv_rows, sparse_block_size, sparse_mode,
-        _lib.LAYOUT[layout], _lib.dtype_code(query.dtype), float(scale_value),
+        pre_tokens, next_tokens, _lib.LAYOUT[layout], _lib.dtype_code(query.dtype), float(scale_value),
         ws.data_ptr(), ws_bytes, _lib.stream_handle(device))
     _lib.check(st, "sparse_flash_attention_grad")
     return dq, dk, dv, dqr, dkr

@@ -77,6 +77,12 @@ void dsa_set_test_flags(int32_t flags);
  * are handled inside the kernel.
  *   D in {128, 256, 512}, d_rope = 64, 1 <= N1 <= 128, dtype BF16 or FP16,
  *   sparse_mode 0 (full) or 3 (rightDownCausal).
+ * pre_tokens / next_tokens (the reference's arguments of those names, which
+ * it accepts only at their default INT64_MAX, 531-532) select a band: token
+ * t of query row s1 is visible iff diag - pre_tokens <= t <= diag +
+ * next_tokens, diag = s1 in mode 0 and act_kv - act_q + s1 in mode 3 (the
+ * band of the Ascend FlashAttention operators).  INT64_MAX on a side leaves
+ * it open; negative values are allowed.
  * Writes attention_out [R, N1, D]; when return_lse != 0 also softmax_max /
  * softmax_sum [R, N1] (entries of rows without a visible token are 0; the
  * caller pre-zeroes them when return_lse == 0).
@@ -89,6 +95,7 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key,
                 int64_t n1, int64_t d, int64_t d_rope, int64_t sparse_count,
                 int64_t q_rows, int64_t kv_rows, int64_t max_blocks,
                 int64_t page_size, int32_t sparse_block_size, int32_t sparse_mode,
+                int64_t pre_tokens, int64_t next_tokens,
                 int32_t layout_query, int32_t layout_kv, int32_t dtype,
                 float scale_value, int32_t return_lse, void* workspace,
                 size_t workspace_bytes, void* stream);
@@ -119,6 +126,7 @@ int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* k
                         int64_t n1, int64_t d, int64_t d_rope, int64_t sparse_count,
                         int64_t q_rows, int64_t kv_rows, int64_t max_blocks,
                         int64_t page_size, int32_t sparse_block_size, int32_t sparse_mode,
+                        int64_t pre_tokens, int64_t next_tokens,
                         int32_t layout_query, int32_t layout_kv, int32_t dtype,
                         float scale_value, int32_t return_lse, void* stream);
 
@@ -127,7 +135,9 @@ int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* k
  * core `_sfa_grad_core` (sparse_flash_attention_grad_triton.py:334-376) and
  * the layout handling around it (451-531): TND rows and block-wise indices
  * are resolved in the kernel.  layout applies to query and key alike (BSND
- * or TND), as in the reference.  Inputs as dsa_sfa_fwd plus d_out and out
+ * or TND), as in the reference.  pre_tokens / next_tokens select the same
+ * band as in dsa_sfa_fwd (the reference rejects values other than INT64_MAX,
+ * 428-429).  Inputs as dsa_sfa_fwd plus d_out and out
  * [R, N1, D] and the forward's softmax_max / softmax_sum [R, N1] fp32
  * (natural-log units).  Writes d_query [R, N1, D], d_query_rope [R, N1, 64]
  * in the query dtype and d_key / d_value [KV, D], d_key_rope [KV, 64] in the
@@ -150,8 +160,9 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
                 const int32_t* actual_seq_kv, void* d_query, void* d_query_rope, void* d_key,
                 void* d_key_rope, void* d_value, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
                 int64_t d, int64_t d_rope, int64_t sparse_count, int64_t q_rows, int64_t kv_rows,
-                int32_t sparse_block_size, int32_t sparse_mode, int32_t layout, int32_t dtype,
-                float scale_value, void* workspace, size_t workspace_bytes, void* stream);
+                int32_t sparse_block_size, int32_t sparse_mode, int64_t pre_tokens,
+                int64_t next_tokens, int32_t layout, int32_t dtype, float scale_value,
+                void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes of dsa_sfa_bwd for these sizes; merge_kv != 0 when
  * d_value will be NULL (dk + dv in one output). */

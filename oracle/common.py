@@ -59,13 +59,39 @@ def row_threshold(sparse_mode, act_q, act_k, s1):
     return act_k if sparse_mode == 0 else act_k - act_q + s1 + 1
 
 
-def gather_positions(idx_row, block_size, threshold, act_k):
+def band_bounds(sparse_mode, act_q, act_k, s1, pre_tokens=INT64_MAX, next_tokens=INT64_MAX):
+    """(lo, threshold) of query row ``s1``: tokens lo <= t < threshold are visible.
+
+    ``threshold`` starts from ``row_threshold``.  The reference accepts only
+    the default pre_tokens = next_tokens = INT64_MAX
+    (sparse_flash_attention_triton.py:531-532,
+    sparse_flash_attention_grad_triton.py:428-429).  Other values are read as
+    the band of the Ascend FlashAttention operators: token t is visible iff
+    diag - pre_tokens <= t <= diag + next_tokens, where diag = s1 in mode 0
+    (aligned at the top left) and diag = act_k - act_q + s1 in mode 3 (aligned
+    at the bottom right, so next_tokens >= 0 leaves the causal bound as it
+    is).  INT64_MAX on either side means that side is open.  Python integers
+    make the sums exact (no saturation is needed here).
+    """
+    thr = row_threshold(sparse_mode, act_q, act_k, s1)
+    diag = s1 if sparse_mode == 0 else act_k - act_q + s1
+    lo = 0
+    if pre_tokens != INT64_MAX:
+        lo = max(0, diag - int(pre_tokens))
+    if next_tokens != INT64_MAX:
+        thr = min(thr, diag + int(next_tokens) + 1)
+    return lo, thr
+
+
+def gather_positions(idx_row, block_size, threshold, act_k, band_lo=0):
     """Token positions a row attends to, following the golden's scan.
 
     Restates sparse_flash_attention_numpy.py:38-60: only the first
     ceil(threshold / block_size) entries are scanned, a -1 entry ends the
     scan, each block id expands to [id*bs, id*bs+bs) clipped to act_k and to
     the threshold.  Duplicated ids contribute their positions twice.
+    Positions below ``band_lo`` (the band's lower edge, ``band_bounds``)
+    are dropped.
     """
     count = min(len(idx_row), math.ceil(threshold / block_size))
     out = []
@@ -77,16 +103,17 @@ def gather_positions(idx_row, block_size, threshold, act_k):
         hi = min(lo + block_size, act_k)
         if lo >= threshold:
             continue
-        out.extend(range(lo, min(hi, threshold)))
+        out.extend(range(max(lo, band_lo), min(hi, threshold)))
     return out
 
 
-def kernel_positions(idx_row, block_size, threshold, act_k):
+def kernel_positions(idx_row, block_size, threshold, act_k, band_lo=0):
     """Token positions under per-entry masking (the device kernels' rule).
 
     Block ids are expanded to token ids first (sparse_flash_attention_triton.py
     :406-421); each token is kept iff tok != -1, tok < threshold and
-    tok < act_k (sparse_flash_attention_triton.py:270-272).  Agrees with
+    tok < act_k (sparse_flash_attention_triton.py:270-272), and tok >=
+    ``band_lo`` (the band's lower edge, ``band_bounds``).  Agrees with
     ``gather_positions`` on front-valid rows.
     """
     out = []
@@ -95,7 +122,7 @@ def kernel_positions(idx_row, block_size, threshold, act_k):
         if blk == -1:
             continue
         for t in range(blk * block_size, blk * block_size + block_size):
-            if 0 <= t < threshold and t < act_k:
+            if max(0, band_lo) <= t < threshold and t < act_k:
                 out.append(t)
     return out
 

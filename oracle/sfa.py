@@ -20,14 +20,15 @@ fp32 dot product.
 """
 import numpy as np
 
-from .common import (BF16, expand_block_indices, gather_positions,
-                     kernel_positions, round_to, row_threshold,
+from .common import (BF16, INT64_MAX, band_bounds, expand_block_indices, gather_positions,
+                     kernel_positions, round_to,
                      cumsum_to_lengths, tnd_to_bsnd, bsnd_to_tnd, pa_to_bsnd)
 
 
 def sfa_fwd_bsnd(q, k, sparse_indices, q_rope, k_rope, scale, act_q, act_k,
                  sparse_block_size=1, sparse_mode=3, return_lse=True,
-                 dtype=BF16, positions="golden", rows=None, compute_dtype=np.float32):
+                 dtype=BF16, positions="golden", rows=None, compute_dtype=np.float32,
+                 pre_tokens=INT64_MAX, next_tokens=INT64_MAX):
     """SFA forward on BSND arrays; inputs are fp32 arrays of dtype-rounded values.
 
     Args follow sparse_flash_attention_numpy.py:63-101.  ``positions`` picks
@@ -37,6 +38,7 @@ def sfa_fwd_bsnd(q, k, sparse_indices, q_rope, k_rope, scale, act_q, act_k,
     list of (b, s1) pairs (other rows stay zero), used for sampled parity at
     full sizes.  ``compute_dtype=np.float64`` evaluates without any dtype
     rounding (used for finite differences and fp64 cross-checks).
+    ``pre_tokens`` / ``next_tokens`` add the band mask of ``band_bounds``.
 
     Returns (out [B,S1,N1,D], softmax_max [B,1,S1,N1], softmax_sum [B,1,S1,N1]).
     """
@@ -60,10 +62,10 @@ def sfa_fwd_bsnd(q, k, sparse_indices, q_rope, k_rope, scale, act_q, act_k,
             continue
         if sparse_mode != 0 and s1 < aq - ak:
             continue
-        thr = row_threshold(sparse_mode, aq, ak, s1)
+        lo, thr = band_bounds(sparse_mode, aq, ak, s1, pre_tokens, next_tokens)
         if thr <= 0:
             continue
-        pos = pos_fn(sparse_indices[b, s1, 0, :], sparse_block_size, thr, ak)
+        pos = pos_fn(sparse_indices[b, s1, 0, :], sparse_block_size, thr, ak, lo)
         if not pos:
             continue
         pos = np.asarray(pos, np.int64)
@@ -90,7 +92,7 @@ def sparse_flash_attention(query, key, sparse_indices, scale_value, query_rope,
                            actual_seq_lengths_kv=None, sparse_block_size=1,
                            layout_query="BSND", layout_kv="BSND", sparse_mode=0,
                            return_softmax_lse=False, dtype=BF16,
-                           positions="kernel"):
+                           positions="kernel", pre_tokens=INT64_MAX, next_tokens=INT64_MAX):
     """Oracle of the public forward API (sparse_flash_attention_triton.py:483-641).
 
     Normalises TND / PA_BSND to dense BSND the way the reference's host code
@@ -137,7 +139,8 @@ def sparse_flash_attention(query, key, sparse_indices, scale_value, query_rope,
     out, smax, ssum = sfa_fwd_bsnd(q, k, si_tok, qr, kr, scale_value, act_q, act_k,
                                    sparse_block_size=1, sparse_mode=sparse_mode,
                                    return_lse=return_softmax_lse, dtype=dtype,
-                                   positions=positions)
+                                   positions=positions, pre_tokens=pre_tokens,
+                                   next_tokens=next_tokens)
     if is_tnd_q:
         out = bsnd_to_tnd(out, lq)
         smax = bsnd_to_tnd(smax.transpose(0, 2, 1, 3), lq).transpose(1, 0, 2)

@@ -13,18 +13,21 @@ Heads are evaluated together as matrix products.
 """
 import numpy as np
 
-from .common import BF16, gather_positions, kernel_positions, round_to, row_threshold
+from .common import BF16, INT64_MAX, band_bounds, gather_positions, kernel_positions, round_to
 
 
 def sfa_bwd_bsnd(q, k, sparse_indices, d_out, out, softmax_max, softmax_sum,
                  q_rope, k_rope, scale, act_q, act_k, sparse_block_size=1,
                  sparse_mode=3, dtype=BF16, positions="golden", rows=None,
-                 guard_sum=False, compute_dtype=np.float32):
+                 guard_sum=False, compute_dtype=np.float32, pre_tokens=INT64_MAX,
+                 next_tokens=INT64_MAX):
     """Returns (d_query, d_key, d_value, d_query_rope, d_key_rope), fp32 arrays.
 
     ``guard_sum`` replaces a non-positive softmax_sum by 1, as the device
     kernel does (sparse_flash_attention_grad_triton.py:233-234); the golden
     divides unguarded, which only differs for rows with no valid token.
+    ``pre_tokens`` / ``next_tokens`` add the band mask of ``band_bounds``
+    (the forward oracle's rule).
     """
     ct = compute_dtype
     q = np.asarray(q, ct)
@@ -53,10 +56,10 @@ def sfa_bwd_bsnd(q, k, sparse_indices, d_out, out, softmax_max, softmax_sum,
             continue
         if sparse_mode != 0 and s1 < aq - ak:
             continue
-        thr = row_threshold(sparse_mode, aq, ak, s1)
+        lo, thr = band_bounds(sparse_mode, aq, ak, s1, pre_tokens, next_tokens)
         if thr <= 0:
             continue
-        pos = pos_fn(sparse_indices[b, s1, 0, :], sparse_block_size, thr, ak)
+        pos = pos_fn(sparse_indices[b, s1, 0, :], sparse_block_size, thr, ak, lo)
         if not pos:
             continue
         pos = np.asarray(pos, np.int64)

@@ -51,7 +51,8 @@ def _sfa_args(**kw):
     a = dict(query=1, query_rope=1, key=1, key_rope=1, sparse_indices=1, attention_out=1,
              softmax_max=1, softmax_sum=1, actual_seq_q=None, actual_seq_kv=None, block_table=None,
              batch=1, s1=4, s2=256, n1=8, d=128, d_rope=64, sparse_count=64, q_rows=4, kv_rows=256,
-             max_blocks=0, page_size=0, sparse_block_size=1, sparse_mode=0, layout_query=0,
+             max_blocks=0, page_size=0, sparse_block_size=1, sparse_mode=0,
+             pre_tokens=9223372036854775807, next_tokens=9223372036854775807, layout_query=0,
              layout_kv=0, dtype=0, scale=0.1, return_lse=1, workspace=None, workspace_bytes=0,
              stream=None)
     a.update(kw)

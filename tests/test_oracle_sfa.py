@@ -9,6 +9,10 @@ What pins what:
   does for the golden), and the delta identity dO.O = sum_p P.dP.
 * layout helpers: PA == de-paged BSND, TND == per-sequence BSND,
   block-wise == expanded token-wise.
+* band mask (pre_tokens / next_tokens, which the reference rejects): an fp64
+  brute force that tests each key position's offset from the diagonal, open
+  sides == no band, the diagonal-only closed form, empty bands, and finite
+  differences of the banded forward for the banded backward.
 """
 import glob
 import math
@@ -377,3 +381,134 @@ def test_bwd_delta_identity():
         P = np.exp(sc - mx[0, 0, s1][:, None]) / sm[0, 0, s1][:, None]
         dP = do[0, s1] @ k[0, pos, 0].T
         np.testing.assert_allclose((P * dP).sum(1), (do[0, s1] * out[0, s1]).sum(1), rtol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# band mask (pre_tokens / next_tokens)
+# ---------------------------------------------------------------------------
+INT64_MAX = 9223372036854775807
+
+
+def _brute_band_fwd(q, k, qr, kr, si, scale, aq, ak, mode, pre, nxt):
+    """fp64 brute force over every key position with an explicit visibility
+    test: t is kept once per index entry naming it, iff t < act_k, t is at or
+    before the causal diagonal (mode 3) and its offset from the band's
+    diagonal lies in [-pre, next]."""
+    B, S1, N1, D = q.shape
+    S2 = k.shape[1]
+    out = np.zeros((B, S1, N1, D))
+    mx = np.zeros((B, 1, S1, N1))
+    sm = np.zeros((B, 1, S1, N1))
+    for b in range(B):
+        for s1 in range(aq[b]):
+            diag = s1 if mode == 0 else ak[b] - aq[b] + s1
+            toks = []
+            for t in range(S2):
+                mult = sum(1 for e in si[b, s1, 0] if int(e) == t)
+                off = t - diag
+                causal_ok = mode == 0 or t <= ak[b] - aq[b] + s1
+                if mult and t < ak[b] and causal_ok and -pre <= off <= nxt:
+                    toks.extend([t] * mult)
+            if not toks:
+                continue
+            sc = np.array([(q[b, s1] @ k[b, t, 0] + qr[b, s1] @ kr[b, t, 0]) * scale for t in toks]).T
+            m = sc.max(axis=1, keepdims=True)
+            e = np.exp(sc - m)
+            z = e.sum(axis=1, keepdims=True)
+            out[b, s1] = (e / z) @ k[b, toks, 0]
+            mx[b, 0, s1] = m[:, 0]
+            sm[b, 0, s1] = z[:, 0]
+    return out, mx, sm
+
+
+def _band_case(seed, mode, S1=5, S2=14, K=9):
+    rng = np.random.RandomState(seed)
+    B, N1, D, Dr = 2, 2, 8, 4
+    q = rng.randn(B, S1, N1, D); k = rng.randn(B, S2, 1, D)
+    qr = rng.randn(B, S1, N1, Dr); kr = rng.randn(B, S2, 1, Dr)
+    si = rng.randint(-1, S2, size=(B, S1, 1, K)).astype(np.int32)
+    aq, ak = [S1, S1 - 2], [S2, S2 - 3]
+    return q, k, qr, kr, si, aq, ak
+
+
+@pytest.mark.parametrize("mode", [0, 3])
+@pytest.mark.parametrize("pre,nxt", [(0, 0), (2, 1), (3, INT64_MAX), (INT64_MAX, 2), (1, -1), (-2, 4),
+                                     (INT64_MAX, -3), (6, 0), (0, 9)])
+def test_band_oracle_matches_brute_force(mode, pre, nxt):
+    q, k, qr, kr, si, aq, ak = _band_case(11 + mode, mode)
+    got = sfa_fwd_bsnd(q, k, si, qr, kr, 0.3, aq, ak, sparse_mode=mode, positions="kernel",
+                       compute_dtype=np.float64, pre_tokens=pre, next_tokens=nxt)
+    exp = _brute_band_fwd(q, k, qr, kr, si, 0.3, aq, ak, mode, pre, nxt)
+    for g, e in zip(got, exp):
+        np.testing.assert_allclose(g, e, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("mode", [0, 3])
+def test_band_open_sides_equal_no_band(mode):
+    q, k, qr, kr, si, aq, ak = _band_case(21, mode)
+    base = sfa_fwd_bsnd(q, k, si, qr, kr, 0.3, aq, ak, sparse_mode=mode, positions="kernel",
+                        compute_dtype=np.float64)
+    wide = sfa_fwd_bsnd(q, k, si, qr, kr, 0.3, aq, ak, sparse_mode=mode, positions="kernel",
+                        compute_dtype=np.float64, pre_tokens=10**6, next_tokens=10**6)
+    for a, b in zip(base, wide):
+        np.testing.assert_array_equal(a, b)
+    if mode == 3:
+        # bottom-right band: next_tokens >= 0 adds nothing to the causal bound
+        nz = sfa_fwd_bsnd(q, k, si, qr, kr, 0.3, aq, ak, sparse_mode=3, positions="kernel",
+                          compute_dtype=np.float64, next_tokens=0)
+        for a, b in zip(base, nz):
+            np.testing.assert_array_equal(a, b)
+
+
+def test_band_diagonal_only_closed_form():
+    """pre = next = 0 keeps exactly the diagonal token: out = v[diag], sum 1."""
+    rng = np.random.RandomState(31)
+    B, S1, S2, N1, D, Dr = 1, 4, 10, 3, 8, 4
+    q = rng.randn(B, S1, N1, D); k = rng.randn(B, S2, 1, D)
+    qr = rng.randn(B, S1, N1, Dr); kr = rng.randn(B, S2, 1, Dr)
+    si = np.tile(np.arange(S2, dtype=np.int32), (B, S1, 1, 1))
+    for mode, diag in ((0, lambda s: s), (3, lambda s: S2 - S1 + s)):
+        out, mx, sm = sfa_fwd_bsnd(q, k, si, qr, kr, 0.5, [S1], [S2], sparse_mode=mode, positions="kernel",
+                                   compute_dtype=np.float64, pre_tokens=0, next_tokens=0)
+        for s1 in range(S1):
+            t = diag(s1)
+            np.testing.assert_allclose(out[0, s1], np.broadcast_to(k[0, t, 0], (N1, D)), rtol=1e-13)
+            np.testing.assert_allclose(sm[0, 0, s1], 1.0)
+            np.testing.assert_allclose(mx[0, 0, s1], 0.5 * (q[0, s1] @ k[0, t, 0] + qr[0, s1] @ kr[0, t, 0]))
+
+
+def test_band_empty_rows_are_zero():
+    """A band that lies wholly outside [0, act_k) leaves output and stats zero."""
+    q, k, qr, kr, si, aq, ak = _band_case(41, 0)
+    out, mx, sm = sfa_fwd_bsnd(q, k, si, qr, kr, 0.3, aq, ak, sparse_mode=0, positions="kernel",
+                               compute_dtype=np.float64, pre_tokens=-100, next_tokens=INT64_MAX)
+    assert not out.any() and not mx.any() and not sm.any()
+
+
+@pytest.mark.parametrize("mode", [0, 3])
+def test_band_bwd_matches_finite_differences(mode):
+    rng = np.random.RandomState(51)
+    B, S1, S2, N1, D, Dr, K = 1, 4, 9, 2, 8, 4, 7
+    qn = rng.randn(B, S1, N1, D) * 0.3; kn = rng.randn(B, S2, 1, D) * 0.3
+    qr = rng.randn(B, S1, N1, Dr) * 0.3; kr = rng.randn(B, S2, 1, Dr) * 0.3
+    do = rng.randn(B, S1, N1, D)
+    si = np.stack([rng.permutation(S2)[:K] for _ in range(S1)]).astype(np.int32).reshape(B, S1, 1, K)
+    sc, aq, ak, pre, nxt = 1 / np.sqrt(D + Dr), [S1], [S2], 2, 1
+    kw = dict(sparse_mode=mode, positions="kernel", compute_dtype=np.float64, pre_tokens=pre, next_tokens=nxt)
+
+    def loss(qn_, kn_, qr_, kr_):
+        return float(np.sum(sfa_fwd_bsnd(qn_, kn_, si, qr_, kr_, sc, aq, ak, **kw)[0] * do))
+
+    out, mx, sm = sfa_fwd_bsnd(qn, kn, si, qr, kr, sc, aq, ak, **kw)
+    dq, dk, dv, dqr, dkr = sfa_bwd_bsnd(qn, kn, si, do, out, mx, sm, qr, kr, sc, aq, ak, **kw)
+    assert np.abs(dk).sum() > 0
+    eps = 1e-6
+    args = [qn, kn, qr, kr]
+    for ai, (arr, g) in enumerate(zip(args, [dq, dk + dv, dqr, dkr])):
+        for idx in list(np.ndindex(arr.shape))[::max(1, arr.size // 12)]:
+            a = [x.copy() for x in args]
+            a[ai][idx] += eps
+            lp = loss(*a)
+            a[ai][idx] -= 2 * eps
+            lm = loss(*a)
+            assert abs((lp - lm) / (2 * eps) - g[idx]) < 1e-7, (ai, idx)

@@ -12,6 +12,8 @@ import numpy as np
 import pytest
 import torch
 
+INT64_MAX = 9223372036854775807  # pre_tokens / next_tokens: no band
+
 pytestmark = pytest.mark.gpu
 
 
@@ -40,7 +42,7 @@ def _call(lib, L, t, B, N1, D, K, ctx, page, noalloc):
     args = [t["q"].data_ptr(), t["qr"].data_ptr(), t["cache"].data_ptr(), t["cache_r"].data_ptr(),
             t["si"].data_ptr(), out.data_ptr(), smax.data_ptr(), ssum.data_ptr(), None, t["act_k"].data_ptr(),
             t["bt"].data_ptr(), B, 1, ctx, N1, D, 64, K, B, nblk * page, ctx // page, page, 1, 0,
-            L.LAYOUT["BSND"], L.LAYOUT["PA_BSND"], L.DTYPE_BF16, 1.0 / np.sqrt(D + 64), 1]
+            INT64_MAX, INT64_MAX, L.LAYOUT["BSND"], L.LAYOUT["PA_BSND"], L.DTYPE_BF16, 1.0 / np.sqrt(D + 64), 1]
     stream = L.stream_handle(torch.device("cuda:0"))
     if noalloc:
         st = lib.dsa_sfa_fwd_noalloc(*args, stream)
@@ -77,5 +79,5 @@ def test_noalloc_validates_like_dsa_sfa_fwd():
     lib = L.load()
     stream = L.stream_handle(torch.device("cuda:0"))
     st = lib.dsa_sfa_fwd_noalloc(1, 1, 1, 1, 1, 1, None, None, None, None, None, 1, 4, 256, 8, 96, 64, 64, 4,
-                                 256, 0, 0, 1, 0, 0, 0, 0, 0.1, 0, stream)
+                                 256, 0, 0, 1, 0, INT64_MAX, INT64_MAX, 0, 0, 0, 0.1, 0, stream)
     assert st == L.DSA_ERR_UNSUPPORTED and b"D must be" in lib.dsa_last_error()
