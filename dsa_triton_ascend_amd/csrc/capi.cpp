@@ -108,6 +108,21 @@ constexpr int64_t kLiMaxK = 4096;
 
 static bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
+// Overflow-safe products for argument checks: false when either factor is
+// negative or a * b does not fit in int64.
+static bool mul_eq(int64_t a, int64_t b, int64_t want) {
+  int64_t r;
+  return a >= 0 && b >= 0 && !__builtin_mul_overflow(a, b, &r) && r == want;
+}
+static bool mul_lt(int64_t a, int64_t b, int64_t lim) {
+  int64_t r;
+  return a >= 0 && b >= 0 && !__builtin_mul_overflow(a, b, &r) && r < lim;
+}
+static bool mul_le(int64_t a, int64_t b, int64_t lim) {
+  int64_t r;
+  return a >= 0 && b >= 0 && !__builtin_mul_overflow(a, b, &r) && r <= lim;
+}
+
 // shared validation of the indexer score inputs
 static int li_check_scores(const void* query, const void* key, const void* weights,
                            const int32_t* act_q, const int32_t* act_k, int64_t batch, int64_t s1,
@@ -142,11 +157,11 @@ static int li_check_scores(const void* query, const void* key, const void* weigh
     DSA_CHECK_ARG(act_q && act_k, "TND layout requires cumulative actual_seq_lengths_query and _key");
     DSA_CHECK_ARG(q_rows >= 1, "TND query must have at least one row");
   } else {
-    DSA_CHECK_ARG(s1 >= 1 && q_rows == batch * s1, "q_rows must equal B*S1 for BSND query");
+    DSA_CHECK_ARG(s1 >= 1 && mul_eq(batch, s1, q_rows), "q_rows must equal B*S1 for BSND query");
   }
-  if (layout_k == DSA_LAYOUT_BSND) DSA_CHECK_ARG(k_rows == batch * s2, "k_rows must equal B*S2 for BSND key");
+  if (layout_k == DSA_LAYOUT_BSND) DSA_CHECK_ARG(mul_eq(batch, s2, k_rows), "k_rows must equal B*S2 for BSND key");
   DSA_CHECK_ARG(k_rows >= 1 && k_rows < (1ll << 31), "key must have between 1 and 2^31-1 rows");
-  DSA_CHECK_ARG(q_rows * n2 < (1ll << 31), "too many query rows");
+  DSA_CHECK_ARG(mul_lt(q_rows, n2, 1ll << 31), "too many query rows");
   return DSA_OK;
 }
 
@@ -183,14 +198,14 @@ static int sfa_fwd_check(const void* query, const void* query_rope, const void* 
                       "layout_kv must be BSND, TND or PA_BSND");
   DSA_CHECK_ARG(batch >= 1 && batch <= (1 << 24), "batch must be >= 1, got %lld", (long long)batch);
   DSA_CHECK_ARG(sparse_count >= 1, "sparse_count must be >= 1");
-  DSA_CHECK_ARG(sparse_count * (int64_t)sparse_block_size <= (1ll << 30),
+  DSA_CHECK_ARG(mul_le(sparse_count, sparse_block_size, 1ll << 30),
                 "sparse_count * sparse_block_size too large");
   if (layout_query == DSA_LAYOUT_TND) {
     DSA_CHECK_ARG(actual_seq_q, "TND query layout requires cumulative actual_seq_lengths_query");
     DSA_CHECK_ARG(q_rows >= 1, "TND query must have at least one row");
   } else {
     DSA_CHECK_ARG(s1 >= 1, "S1 must be >= 1");
-    DSA_CHECK_ARG(q_rows == batch * s1, "q_rows must equal B*S1 for BSND query");
+    DSA_CHECK_ARG(mul_eq(batch, s1, q_rows), "q_rows must equal B*S1 for BSND query");
   }
   DSA_CHECK_ARG(q_rows < (1ll << 31), "too many query rows");
   if (layout_kv == DSA_LAYOUT_TND) {
@@ -201,7 +216,7 @@ static int sfa_fwd_check(const void* query, const void* query_rope, const void* 
     DSA_CHECK_ARG(page_size >= 1 && max_blocks >= 1, "PA_BSND requires block_size and block_table columns");
     DSA_CHECK_ARG(kv_rows % page_size == 0, "paged key rows must be a multiple of block_size");
   } else {
-    DSA_CHECK_ARG(s2 >= 1 && kv_rows == batch * s2, "kv_rows must equal B*S2 for BSND key");
+    DSA_CHECK_ARG(s2 >= 1 && mul_eq(batch, s2, kv_rows), "kv_rows must equal B*S2 for BSND key");
   }
   DSA_CHECK_ARG(kv_rows >= 1 && kv_rows < (1ll << 31), "key must have between 1 and 2^31-1 rows");
   return DSA_OK;
@@ -220,7 +235,10 @@ void dsa_set_test_flags(int32_t flags) { g_test_flags.store(flags, std::memory_o
 
 size_t dsa_sfa_fwd_workspace_size(int64_t q_rows, int64_t n1, int64_t d, int64_t sparse_count,
                                   int32_t sparse_block_size) {
-  if (q_rows <= 0 || n1 <= 0 || d <= 0 || sparse_count <= 0 || sparse_block_size <= 0) return 0;
+  // sizes the entry point rejects need no workspace
+  if (q_rows <= 0 || q_rows >= (1ll << 31) || n1 <= 0 || n1 > 128 || d <= 0 || d > 512 || sparse_count <= 0 ||
+      sparse_block_size <= 0 || !mul_le(sparse_count, sparse_block_size, 1ll << 30))
+    return 0;
   return sfa_fwd_workspace_bytes(q_rows, n1, d, sparse_count * (int64_t)sparse_block_size);
 }
 
@@ -285,7 +303,10 @@ int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* k
 
 size_t dsa_sfa_bwd_workspace_size(int64_t q_rows, int64_t kv_rows, int64_t n1, int64_t d, int64_t sparse_count,
                                   int32_t sparse_block_size, int32_t merge_kv) {
-  if (q_rows < 0 || kv_rows <= 0 || n1 <= 0 || d <= 0 || sparse_count <= 0 || sparse_block_size <= 0) return 0;
+  if (q_rows < 0 || q_rows >= (1ll << 31) || kv_rows <= 0 || kv_rows >= (1ll << 31) || n1 <= 0 || n1 > 128 ||
+      d <= 0 || d > 512 || sparse_count <= 0 || sparse_block_size <= 0 ||
+      !mul_le(sparse_count, sparse_block_size, 1ll << 30))
+    return 0;
   return sfa_bwd_workspace_bytes(q_rows, kv_rows, n1, d, sparse_count * (int64_t)sparse_block_size, merge_kv != 0);
 }
 
@@ -314,14 +335,14 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
                       "query/key dtype must be bfloat16 or float16");
   DSA_CHECK_SUPPORTED(layout == DSA_LAYOUT_BSND || layout == DSA_LAYOUT_TND, "layout must be BSND or TND");
   DSA_CHECK_ARG(batch >= 1 && batch <= (1 << 24), "batch must be >= 1");
-  DSA_CHECK_ARG(sparse_count >= 1 && sparse_count * (int64_t)sparse_block_size <= (1ll << 30),
+  DSA_CHECK_ARG(sparse_count >= 1 && mul_le(sparse_count, sparse_block_size, 1ll << 30),
                 "sparse_count out of range");
   if (layout == DSA_LAYOUT_TND) {
     DSA_CHECK_ARG(actual_seq_q && actual_seq_kv, "TND layout requires cumulative actual sequence lengths");
     DSA_CHECK_ARG(q_rows >= 1, "TND query must have at least one row");
   } else {
-    DSA_CHECK_ARG(s1 >= 1 && q_rows == batch * s1, "q_rows must equal B*S1 for BSND");
-    DSA_CHECK_ARG(s2 >= 1 && kv_rows == batch * s2, "kv_rows must equal B*S2 for BSND");
+    DSA_CHECK_ARG(s1 >= 1 && mul_eq(batch, s1, q_rows), "q_rows must equal B*S1 for BSND");
+    DSA_CHECK_ARG(s2 >= 1 && mul_eq(batch, s2, kv_rows), "kv_rows must equal B*S2 for BSND");
   }
   DSA_CHECK_ARG(q_rows < (1ll << 31) && kv_rows >= 1 && kv_rows < (1ll << 31), "row counts out of range");
   const size_t need = sfa_bwd_workspace_bytes(q_rows, kv_rows, n1, d, sparse_count * (int64_t)sparse_block_size,
@@ -337,12 +358,16 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
 }
 
 size_t dsa_kl_bwd_workspace_size(int64_t batch, int64_t s1, int64_t s2, int64_t sparse_count, int64_t d_idx) {
-  if (batch <= 0 || s1 <= 0 || s2 <= 0 || sparse_count <= 0 || d_idx != 128) return 0;
+  if (batch <= 0 || !mul_lt(batch, s1, 1ll << 31) || !mul_lt(batch, s2, 1ll << 31) || s1 <= 0 || s2 <= 0 ||
+      sparse_count <= 0 || sparse_count > kl_bwd_max_topk() || d_idx != 128)
+    return 0;
   return kl_bwd_workspace_bytes(batch * s1, batch * s2, sparse_count);
 }
 
 size_t dsa_kl_bwd_ex_workspace_size(int64_t q_rows, int64_t kv_rows, int64_t sparse_count, int64_t d_idx) {
-  if (q_rows <= 0 || kv_rows <= 0 || sparse_count <= 0 || d_idx != 128) return 0;
+  if (q_rows <= 0 || q_rows >= (1ll << 31) || kv_rows <= 0 || kv_rows >= (1ll << 31) || sparse_count <= 0 ||
+      sparse_count > kl_bwd_max_topk() || d_idx != 128)
+    return 0;
   return kl_bwd_workspace_bytes(q_rows, kv_rows, sparse_count);
 }
 
@@ -383,12 +408,12 @@ static int kl_check(const void* query, const void* key, const void* query_rope, 
   DSA_CHECK_ARG(!(layout_q == DSA_LAYOUT_BSND && layout_k == DSA_LAYOUT_TND), "a TND key needs a TND query");
   DSA_CHECK_ARG(batch >= 1 && batch <= (1 << 24), "batch must be in [1, 2^24]");
   DSA_CHECK_ARG(q_rows >= 1 && kv_rows >= 1, "the query and the key need at least one row");
-  DSA_CHECK_ARG(q_rows * sparse_count < (1ll << 31) && kv_rows < (1ll << 31),
+  DSA_CHECK_ARG(mul_lt(q_rows, sparse_count, 1ll << 31) && kv_rows < (1ll << 31),
                 "rows x topK and the key rows must stay below 2^31");
   if (layout_q == DSA_LAYOUT_TND) {
     DSA_CHECK_ARG(act_q, "TND query requires cumulative actual_seq_qlen");
   } else {
-    DSA_CHECK_ARG(s1 >= 1 && q_rows == batch * s1, "q_rows must equal B*S1 for a BSND query");
+    DSA_CHECK_ARG(s1 >= 1 && mul_eq(batch, s1, q_rows), "q_rows must equal B*S1 for a BSND query");
   }
   if (layout_k == DSA_LAYOUT_TND) {
     DSA_CHECK_ARG(act_k, "TND key requires cumulative actual_seq_klen");
@@ -396,11 +421,11 @@ static int kl_check(const void* query, const void* key, const void* query_rope, 
     DSA_CHECK_ARG(block_table, "PA_BSND key requires a block_table");
     DSA_CHECK_ARG(act_k, "PA_BSND key requires actual_seq_klen (per-batch lengths)");
     DSA_CHECK_ARG(page_size >= 1 && page_size <= (1 << 20), "page (block) size must be in [1, 2^20]");
-    DSA_CHECK_ARG(max_blocks >= 1 && max_blocks * page_size < (1ll << 31),
+    DSA_CHECK_ARG(max_blocks >= 1 && mul_lt(max_blocks, page_size, 1ll << 31),
                   "max_blocks * page size must be in [1, 2^31)");
     DSA_CHECK_ARG(kv_rows % page_size == 0, "the paged key rows must be a whole number of pages");
   } else {
-    DSA_CHECK_ARG(s2 >= 1 && kv_rows == batch * s2, "kv_rows must equal B*S2 for a BSND key");
+    DSA_CHECK_ARG(s2 >= 1 && mul_eq(batch, s2, kv_rows), "kv_rows must equal B*S2 for a BSND key");
   }
   const size_t need = kl_bwd_workspace_bytes(q_rows, kv_rows, sparse_count);
   if (workspace == nullptr || workspace_bytes < need) {
@@ -419,7 +444,8 @@ int dsa_kl_bwd(const void* query, const void* key, const void* query_rope, const
                int32_t dtype, int32_t weights_dtype, float scale_value, void* workspace,
                size_t workspace_bytes, void* stream) {
   g_err[0] = '\0';
-  DSA_CHECK_ARG(batch >= 1 && s1 >= 1 && s2 >= 1, "batch, S1 and S2 must be >= 1");
+  DSA_CHECK_ARG(batch >= 1 && batch <= (1 << 24) && s1 >= 1 && s1 < (1ll << 31) && s2 >= 1 && s2 < (1ll << 31),
+                "batch must be in [1, 2^24], S1 and S2 in [1, 2^31)");
   const int st = kl_check(query, key, query_rope, key_rope, query_index, key_index, weights, sparse_indices,
                           softmax_max, softmax_sum, actual_seq_qlen, actual_seq_klen, nullptr, d_query_index,
                           d_key_index, d_weights, loss, batch, s1, s2, n1, d, d_rope, n_idx, d_idx, sparse_count,
@@ -443,7 +469,11 @@ int dsa_kl_bwd_ex(const void* query, const void* key, const void* query_rope, co
                   int32_t layout_query, int32_t layout_key, int32_t dtype, int32_t weights_dtype,
                   float scale_value, void* workspace, size_t workspace_bytes, void* stream) {
   g_err[0] = '\0';
-  if (layout_key == DSA_LAYOUT_PA_BSND) s2 = max_blocks * page_size;
+  if (layout_key == DSA_LAYOUT_PA_BSND) {
+    DSA_CHECK_ARG(max_blocks >= 1 && page_size >= 1 && mul_lt(max_blocks, page_size, 1ll << 31),
+                  "max_blocks * page size must be in [1, 2^31)");
+    s2 = max_blocks * page_size;
+  }
   const int st = kl_check(query, key, query_rope, key_rope, query_index, key_index, weights, sparse_indices,
                           softmax_max, softmax_sum, actual_seq_qlen, actual_seq_klen, block_table, d_query_index,
                           d_key_index, d_weights, loss, batch, s1, s2, n1, d, d_rope, n_idx, d_idx, sparse_count,
@@ -471,8 +501,9 @@ static int dense_check_index(const void* query_index, const void* key_index, con
   DSA_CHECK_SUPPORTED(weights_dtype == DSA_DTYPE_FP32 || weights_dtype == DSA_DTYPE_BF16 ||
                           weights_dtype == DSA_DTYPE_FP16,
                       "weights dtype must be float32, bfloat16 or float16");
-  DSA_CHECK_ARG(batch >= 1 && s1 >= 1 && s2 >= 1, "batch, S1 and S2 must be >= 1");
-  DSA_CHECK_ARG(batch * s1 < (1ll << 31) && batch * s2 < (1ll << 31) && s2 < (1ll << 30),
+  DSA_CHECK_ARG(batch >= 1 && batch <= (1 << 24) && s1 >= 1 && s1 < (1ll << 31) && s2 >= 1 && s2 < (1ll << 31),
+                "batch must be in [1, 2^24], S1 and S2 in [1, 2^31)");
+  DSA_CHECK_ARG(mul_lt(batch, s1, 1ll << 31) && mul_lt(batch, s2, 1ll << 31) && s2 < (1ll << 30),
                 "B*S1, B*S2 and S2 must stay below 2^31");
   return DSA_OK;
 }
@@ -492,7 +523,9 @@ int dsa_dense_li_softmax_lse(const void* query_index, const void* key_index, con
 }
 
 size_t dsa_dense_kl_bwd_workspace_size(int64_t batch, int64_t s1, int64_t s2, int64_t d_idx) {
-  if (batch <= 0 || s1 <= 0 || s2 <= 0 || !(d_idx == 128 || d_idx == 256 || d_idx == 512)) return 0;
+  if (batch <= 0 || s1 <= 0 || s2 <= 0 || !mul_lt(batch, s1, 1ll << 31) || !mul_lt(batch, s2, 1ll << 31) ||
+      !(d_idx == 128 || d_idx == 256 || d_idx == 512))
+    return 0;
   return dense_kl_workspace_bytes(batch, s1, s2, d_idx);
 }
 
@@ -530,7 +563,8 @@ int dsa_dense_kl_bwd(const void* query, const void* key, const void* query_rope,
 }
 
 size_t dsa_li_fwd_workspace_size(int64_t q_rows, int64_t n2, int64_t s2) {
-  if (q_rows <= 0 || n2 <= 0 || s2 <= 0) return 0;
+  if (q_rows <= 0 || q_rows >= (1ll << 31) || n2 <= 0 || n2 > (1 << 16) || s2 <= 0 || s2 > 65535ll * 1024)
+    return 0;
   return (size_t)q_rows * n2 * s2 * sizeof(float);
 }
 
@@ -595,8 +629,8 @@ static int li_check_paged(const int32_t* block_table, int64_t num_blocks, int64_
   DSA_CHECK_ARG(block_table, "PA_BSND key requires a block_table");
   DSA_CHECK_ARG(page_size >= 1 && page_size <= (1 << 20), "page (block) size must be in [1, 2^20]");
   DSA_CHECK_ARG(num_blocks >= 1 && max_blocks >= 1, "the cache and the block table need at least one block");
-  DSA_CHECK_ARG(max_blocks * page_size <= 65535ll * 1024, "max_blocks * page size must be <= 67107840");
-  DSA_CHECK_ARG(num_blocks * page_size < (1ll << 31), "the key cache must have fewer than 2^31 rows");
+  DSA_CHECK_ARG(mul_le(max_blocks, page_size, 65535ll * 1024), "max_blocks * page size must be <= 67107840");
+  DSA_CHECK_ARG(mul_lt(num_blocks, page_size, 1ll << 31), "the key cache must have fewer than 2^31 rows");
   return DSA_OK;
 }
 
