@@ -104,7 +104,7 @@ int li_scores_run(const void* query, const void* key, const void* weights, const
                   int64_t max_blocks = 0, int64_t page_size = 1);
 int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_t* indices,
                 void* values, int32_t val_dtype, hipStream_t stream);
-constexpr int64_t kLiMaxK = 4096;
+constexpr int64_t kLiMaxK = 16384;  // the top-k sorts up to 16384 entries (LDS and per-wave registers)
 
 static bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
@@ -130,16 +130,18 @@ static int li_check_scores(const void* query, const void* key, const void* weigh
                            int64_t k_rows, int32_t sparse_mode, int32_t layout_q,
                            int32_t layout_k, int32_t dtype, int32_t w_dtype, bool allow_pa = false) {
   DSA_CHECK_ARG(query && key && weights, "null tensor pointer");
-  DSA_CHECK_SUPPORTED(d == 64 || d == 128 || d == 256, "head dim D must be one of (64, 128, 256), got %lld",
-                      (long long)d);
+  DSA_CHECK_SUPPORTED(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_FP16 || dtype == DSA_DTYPE_FP32,
+                      "query/key dtype must be bfloat16, float16 or float32");
+  // 16-byte rows: a multiple of 8 elements (16-bit types) or of 4 (fp32)
+  DSA_CHECK_SUPPORTED(d >= 1 && d <= 256 && d % (dtype == DSA_DTYPE_FP32 ? 4 : 8) == 0,
+                      "head dim D must be a multiple of %d in [%d, 256], got %lld", dtype == DSA_DTYPE_FP32 ? 4 : 8,
+                      dtype == DSA_DTYPE_FP32 ? 4 : 8, (long long)d);
   DSA_CHECK_ARG(n2 >= 1 && n1 >= 1, "N1 and N2 must be >= 1");
   DSA_CHECK_ARG(n1 % n2 == 0, "N1(%lld) must be divisible by N2(%lld)", (long long)n1, (long long)n2);
   DSA_CHECK_SUPPORTED(n1 / n2 <= 128, "N1/N2 (query heads per key head) must be <= 128, got %lld",
                       (long long)(n1 / n2));
   DSA_CHECK_SUPPORTED(sparse_mode == 0 || sparse_mode == 3,
                       "Only sparse_mode 0 (full) / 3 (rightDownCausal) supported");
-  DSA_CHECK_SUPPORTED(dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_FP16,
-                      "query/key dtype must be bfloat16 or float16");
   DSA_CHECK_SUPPORTED(w_dtype == DSA_DTYPE_BF16 || w_dtype == DSA_DTYPE_FP16 || w_dtype == DSA_DTYPE_FP32,
                       "weights dtype must be bfloat16, float16 or float32");
   DSA_CHECK_SUPPORTED(layout_q == DSA_LAYOUT_BSND || layout_q == DSA_LAYOUT_TND,

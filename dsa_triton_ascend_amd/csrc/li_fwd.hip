@@ -44,6 +44,7 @@ struct LiParams {
   float* scores;       // [q_rows * n2, s2] (row stride s2)
   int64_t q_rows, k_rows;
   int32_t batch, s1, s2, n1, n2, g;
+  int32_t d;           // head dim (the row stride of q and k)
   int32_t mode, layout_q, layout_k, w_dtype;
   int32_t chunk;       // keys per workgroup
   // PA_BSND key cache [blocks, page, N2, D]: key s2 of batch b is row
@@ -111,13 +112,57 @@ __device__ __forceinline__ float li_load_w(const LiParams& p, int64_t idx) {
 // collect in LDS and leave in coalesced 16-byte stores at the end.  At the
 // decode shape the kernel streams K at about 4.9 TB/s, close to what a
 // plain streaming read reaches on the MI355X (about 5.5 TB/s measured).
+// PAD: the head dim p.d is below D (a multiple of 8); the 8-element chunks
+// at or past p.d load as zeros, so the MFMAs see zero-padded rows of D.
 constexpr int kLiMaxChunk = 8192;  // keys per workgroup (LDS score buffer)
 
-template <int D, typename T, int GT>
+// Scores of the chunk [c0, c1) from s_sc to the row, in coalesced 16-byte
+// stores where the destination is 16-byte aligned; keys in -1 (or
+// out-of-range) pages of a paged cache are zero rows, score 0 while visible.
+__device__ __forceinline__ void li_store_chunk(const LiParams& p, const LiRow& ri, const int32_t* btab, float* s_sc,
+                                               float* srow, int c0, int c1) {
+  const int n = c1 - c0;
+  if (p.layout_k == DSA_LAYOUT_PA_BSND) {
+    const int64_t nblk = p.k_rows / p.page_size;
+    for (int j = threadIdx.x; j < n; j += kLiThreads) {
+      const int key = c0 + j;
+      if (key < ri.lim) {
+        const int blk = btab[key / p.page_size];
+        if (blk < 0 || blk >= nblk) s_sc[j] = 0.f;
+      }
+    }
+    __syncthreads();
+  }
+  float* dst = srow + c0;
+  const int head = (int)(((16 - ((uintptr_t)dst & 15)) & 15) >> 2);  // scalars before 16-byte alignment
+  const int h = head < n ? head : n;
+  for (int j = threadIdx.x; j < h; j += kLiThreads) dst[j] = s_sc[j];
+  const int n4 = (n - h) >> 2;
+  for (int j = threadIdx.x; j < n4; j += kLiThreads) {
+    const float4 v = make_float4(s_sc[h + 4 * j], s_sc[h + 4 * j + 1], s_sc[h + 4 * j + 2], s_sc[h + 4 * j + 3]);
+    *(float4*)(dst + h + 4 * j) = v;
+  }
+  for (int j = h + 4 * n4 + threadIdx.x; j < n; j += kLiThreads) dst[j] = s_sc[j];
+}
+
+// Physical key row of visible key `key` of a row (clamped into the tensor).
+__device__ __forceinline__ int64_t li_key_row(const LiParams& p, const LiRow& ri, const int32_t* btab, int key) {
+  int64_t krow = ri.k_base + key;
+  if (p.layout_k == DSA_LAYOUT_PA_BSND) {
+    // a -1 or out-of-range page reads row 0; its scores are set to zero
+    // when the chunk is stored (a zero key row, as de-paging leaves it)
+    const int blk = btab[key / p.page_size];
+    krow = (int64_t)(blk < 0 ? 0 : blk) * p.page_size + key % p.page_size;
+  }
+  return krow < p.k_rows ? krow : p.k_rows - 1;  // inconsistent cumulative lengths stay in bounds
+}
+
+template <int D, typename T, int GT, bool PAD>
 __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
   using E = Elem<T>;
   using V8 = typename E::v8;
   constexpr int KS = D / 32;
+  const int dstride = PAD ? p.d : D;
   __shared__ __attribute__((aligned(16))) float s_sc[kLiMaxChunk];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -144,8 +189,9 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
     const int64_t qrow = (int64_t)row * p.n1 + kh * p.g + (gv ? g : 0);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const u32x4 v = *(const u32x4*)((const T*)p.q + qrow * D + ks * 32 + lg * 8);
+      const bool dv = !PAD || ks * 32 + lg * 8 < p.d;
       const u32x4 z = {0u, 0u, 0u, 0u};
+      const u32x4 v = dv ? *(const u32x4*)((const T*)p.q + qrow * dstride + (dv ? ks * 32 + lg * 8 : 0)) : z;
       qf[ht][ks] = as_v8<V8>(gv ? v : z);
     }
   }
@@ -179,17 +225,13 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
   auto kload = [&](int grp, u32x4 (&kf)[KS]) {
     int key = c0 + grp * 16 + li;
     key = key < lastvis ? key : lastvis;  // stays in the batch's rows; masked below
-    int64_t krow = ri.k_base + key;
-    if (paged) {
-      // a -1 or out-of-range page reads row 0; its scores are set to zero
-      // after the loop (a zero key row, as de-paging leaves it)
-      const int blk = btab[key / p.page_size];
-      krow = (int64_t)(blk < 0 ? 0 : blk) * p.page_size + key % p.page_size;
-    }
-    krow = krow < p.k_rows ? krow : p.k_rows - 1;  // inconsistent cumulative lengths stay in bounds
-    const T* kp = (const T*)p.k + (krow * p.n2 + kh) * D + lg * 8;
+    const int64_t krow = li_key_row(p, ri, btab, key);
+    const T* kp = (const T*)p.k + (krow * p.n2 + kh) * dstride + lg * 8;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kf[ks] = *(const u32x4*)(kp + ks * 32);
+    for (int ks = 0; ks < KS; ++ks) {
+      if (!PAD || ks * 32 + lg * 8 < p.d) kf[ks] = *(const u32x4*)(kp + ks * 32);
+      else kf[ks] = (u32x4){0u, 0u, 0u, 0u};
+    }
   };
   constexpr int NP = 4;
   u32x4 kf[NP][KS];
@@ -223,37 +265,113 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
     }
   }
   __syncthreads();
-  const int n = c1 - c0;
-  if (paged) {
-    // keys in -1 (or out-of-range) pages are zero rows: score 0 while visible
-    const int64_t nblk = p.k_rows / p.page_size;
-    for (int j = threadIdx.x; j < n; j += kLiThreads) {
-      const int key = c0 + j;
-      if (key < ri.lim) {
-        const int blk = btab[key / p.page_size];
-        if (blk < 0 || blk >= nblk) s_sc[j] = 0.f;
+  li_store_chunk(p, ri, btab, s_sc, srow, c0, c1);
+}
+
+// fp32 query / key (and weights): the products run on v_mfma_f32_16x16x4f32
+// in full fp32.  A lane loads 16 bytes (4 consecutive d) of a Q row and of a
+// K row, as the 16-bit kernel does, and feeds them to four MFMAs, element t
+// to the t-th: MFMA t of 16-column block c takes d = 16c + 4*lg + t from the
+// lanes of group lg, for the A and the B operand alike, so every d of the
+// block is summed once.  The G heads run in passes of 16 (Q of one head
+// tile stays in registers); each pass streams the chunk's keys again and
+// adds its heads' ReLU-weighted sums to the key's score.  PAD as above, for
+// a head dim p.d (a multiple of 4) below D.
+template <int D, bool PAD>
+__global__ __launch_bounds__(kLiThreads) void li_score_f32_kernel(LiParams p) {
+  constexpr int KC = D / 16;  // 16-column blocks
+  const int dstride = PAD ? p.d : D;
+  __shared__ __attribute__((aligned(16))) float s_sc[kLiMaxChunk];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int rn = blockIdx.x;
+  const int row = rn / p.n2;
+  const int kh = rn - row * p.n2;
+  const LiRow ri = li_row_info(p, row);
+  const int c0 = blockIdx.y * p.chunk;
+  const int c1 = min(p.s2, c0 + p.chunk);
+  float* srow = p.scores + (int64_t)rn * p.s2;
+  if (c0 >= ri.lim) {
+    for (int j = c0 + threadIdx.x; j < c1; j += kLiThreads) srow[j] = -INFINITY;
+    return;
+  }
+  const int ngroups = (c1 - c0 + 15) >> 4;
+  const int lastvis = ri.lim - 1;
+  const int32_t* btab = p.layout_k == DSA_LAYOUT_PA_BSND ? p.block_table + (int64_t)ri.b * p.max_blocks : nullptr;
+  const int64_t wbase = (int64_t)row * p.n1 + kh * p.g;
+  const int npass = (p.g + 15) >> 4;
+  for (int pass = 0; pass < npass; ++pass) {
+    const int g0 = pass * 16;
+    f32x4 qf[KC];
+    {
+      const int g = g0 + li;
+      const bool gv = g < p.g;
+      const float* qp = (const float*)p.q + (wbase + (gv ? g : 0)) * dstride + lg * 4;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const bool dv = gv && (!PAD || c * 16 + lg * 4 < p.d);
+        qf[c] = dv ? *(const f32x4*)(qp + c * 16) : (f32x4){0.f, 0.f, 0.f, 0.f};
       }
     }
-    __syncthreads();
+    float wv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int gg = g0 + lg * 4 + r;
+      wv[r] = gg < p.g ? li_load_w(p, wbase + gg) : 0.f;
+    }
+    auto kload = [&](int grp, f32x4 (&kf)[KC]) {
+      int key = c0 + grp * 16 + li;
+      key = key < lastvis ? key : lastvis;
+      const int64_t krow = li_key_row(p, ri, btab, key);
+      const float* kp = (const float*)p.k + (krow * p.n2 + kh) * dstride + lg * 4;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        if (!PAD || c * 16 + lg * 4 < p.d) kf[c] = *(const f32x4*)(kp + c * 16);
+        else kf[c] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      }
+    };
+    constexpr int NP = 2;
+    f32x4 kf[NP][KC];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) kload(min(wave + 4 * i, ngroups - 1), kf[i]);
+    for (int grp = wave; grp < ngroups; grp += 4 * NP) {
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        const int gi = grp + 4 * i;
+        if (gi < ngroups) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < KC; ++c)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[c][t], kf[i][c][t], acc, 0, 0, 0);
+          float s = 0.f;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s += fmaxf(acc[r], 0.f) * wv[r];
+          s = xgroup_sum(s);
+          const int key = c0 + gi * 16 + li;
+          // the same lane owns this key in every pass: no barrier needed
+          if (lg == 0 && key < c1) {
+            const int j = gi * 16 + li;
+            const float prev = pass ? s_sc[j] : 0.f;
+            s_sc[j] = pass + 1 < npass ? prev + s : (key < ri.lim ? prev + s : -INFINITY);
+          }
+        }
+        kload(min(gi + 4 * NP, ngroups - 1), kf[i]);
+      }
+    }
   }
-  // coalesced stores of the chunk's scores (16 bytes per lane where the
-  // destination is 16-byte aligned)
-  float* dst = srow + c0;
-  const int head = (int)(((16 - ((uintptr_t)dst & 15)) & 15) >> 2);  // scalars before 16-byte alignment
-  const int h = head < n ? head : n;
-  for (int j = threadIdx.x; j < h; j += kLiThreads) dst[j] = s_sc[j];
-  const int n4 = (n - h) >> 2;
-  for (int j = threadIdx.x; j < n4; j += kLiThreads) {
-    const float4 v = make_float4(s_sc[h + 4 * j], s_sc[h + 4 * j + 1], s_sc[h + 4 * j + 2], s_sc[h + 4 * j + 3]);
-    *(float4*)(dst + h + 4 * j) = v;
-  }
-  for (int j = h + 4 * n4 + threadIdx.x; j < n; j += kLiThreads) dst[j] = s_sc[j];
+  __syncthreads();
+  li_store_chunk(p, ri, btab, s_sc, srow, c0, c1);
 }
 
 // ---------------------------------------------------------------------------
 // top-k kernel
 // ---------------------------------------------------------------------------
 constexpr int kTopkThreads = 1024;
+// 128-entry blocks of the selection sort held in registers per wave: 16
+// waves x 8 blocks x 128 = 16384 entries, the largest K
+constexpr int kSortBlocksPerWave = 8;
 constexpr int kTopkLdsBudget = 160 * 1024;  // LDS per workgroup on gfx950
 
 // order-preserving map fp32 -> uint32 (larger score -> larger key); -0.0
@@ -505,8 +623,9 @@ __device__ void topk_row_generic(const TopkParams& p, const int64_t row, unsigne
 
   // bitonic sort ascending of sel[0, npow).  Stages with stride >= 128 go
   // through LDS (one barrier each); the stages with stride < 128 run in
-  // registers: wave w holds 128-entry blocks w and w + 16 (two entries per
-  // lane, index base + lane and base + 64 + lane) and exchanges partners with
+  // registers: wave w holds 128-entry blocks w, w + 16, w + 32, ... (two
+  // entries per lane, index base + lane and base + 64 + lane; up to
+  // kSortBlocksPerWave blocks, 16384 entries) and exchanges partners with
   // lane shuffles, so most of the 66 stages of a 2048-entry sort need no
   // barrier.
   auto lds_stage = [&](int size, int stride) {
@@ -523,11 +642,11 @@ __device__ void topk_row_generic(const TopkParams& p, const int64_t row, unsigne
     for (int size = 2; size <= npow; size <<= 1)
       for (int stride = size >> 1; stride > 0; stride >>= 1) lds_stage(size, stride);
   } else {
-    const int nblk = npow >> 7;  // <= 32
-    unsigned long long x[2][2];
+    const int nblk = npow >> 7;  // <= 16 * kSortBlocksPerWave
+    unsigned long long x[kSortBlocksPerWave][2];
     auto load_blocks = [&]() {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < kSortBlocksPerWave; ++h) {
         const int blk = wave + 16 * h;
         if (blk < nblk) {
           x[h][0] = sel[blk * 128 + lane];
@@ -537,7 +656,7 @@ __device__ void topk_row_generic(const TopkParams& p, const int64_t row, unsigne
     };
     auto store_blocks = [&]() {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < kSortBlocksPerWave; ++h) {
         const int blk = wave + 16 * h;
         if (blk < nblk) {
           sel[blk * 128 + lane] = x[h][0];
@@ -547,7 +666,7 @@ __device__ void topk_row_generic(const TopkParams& p, const int64_t row, unsigne
     };
     auto reg_stages = [&](int size, int smax) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < kSortBlocksPerWave; ++h) {
         const int blk = wave + 16 * h;
         if (blk >= nblk) continue;
         const int base = blk * 128;
@@ -905,18 +1024,7 @@ int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_
 // Keys per workgroup: enough chunks per row that the grid fills every CU
 // with as many workgroups as fit at once, in one round (a partial second
 // round would leave most CUs idle while it runs).
-template <int D, typename T, int GT>
-static hipError_t launch_score(LiParams p, hipStream_t stream) {
-  // Occupancy depends only on the kernel and the architecture (every device
-  // this library runs on is gfx950); the local static's initialisation is
-  // thread-safe.
-  static const int occ = [] {
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, li_score_kernel<D, T, GT>, kLiThreads, 0) != hipSuccess ||
-        n < 1)
-      n = 1;
-    return n;
-  }();
+static hipError_t launch_score_kernel(const void* fn, int occ, LiParams p, hipStream_t stream) {
   const int64_t rows = p.q_rows * p.n2;
   const int64_t target = (int64_t)device_cu_count() * occ;
   const int64_t per_row = rows >= target ? 1 : (target + rows - 1) / rows;
@@ -925,23 +1033,60 @@ static hipError_t launch_score(LiParams p, hipStream_t stream) {
   chunk = chunk < 64 ? 64 : chunk;
   p.chunk = (int32_t)(chunk > kLiMaxChunk ? kLiMaxChunk : chunk);
   const unsigned chunks = (unsigned)((p.s2 + p.chunk - 1) / p.chunk);
-  hipLaunchKernelGGL((li_score_kernel<D, T, GT>), dim3((unsigned)rows, chunks), dim3(kLiThreads), 0, stream, p);
-  return hipGetLastError();
+  void* args[] = {&p};
+  return hipLaunchKernel(fn, dim3((unsigned)rows, chunks), dim3(kLiThreads), args, 0, stream);
 }
 
-template <int D, typename T>
+// Occupancy depends only on the kernel and the architecture (every device
+// this library runs on is gfx950); the local static's initialisation is
+// thread-safe.
+template <typename F>
+static int score_occupancy(F fn) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kLiThreads, 0) != hipSuccess || n < 1) n = 1;
+  return n;
+}
+
+template <int D, typename T, int GT, bool PAD>
+static hipError_t launch_score(const LiParams& p, hipStream_t stream) {
+  static const int occ = score_occupancy(li_score_kernel<D, T, GT, PAD>);
+  return launch_score_kernel((const void*)li_score_kernel<D, T, GT, PAD>, occ, p, stream);
+}
+
+template <int D, typename T, bool PAD>
 static hipError_t launch_score_g(const LiParams& p, hipStream_t stream) {
-  if (p.g <= 16) return launch_score<D, T, 1>(p, stream);
-  if (p.g <= 32) return launch_score<D, T, 2>(p, stream);
-  if (p.g <= 64) return launch_score<D, T, 4>(p, stream);
-  return launch_score<D, T, 8>(p, stream);
+  if (p.g <= 16) return launch_score<D, T, 1, PAD>(p, stream);
+  if (p.g <= 32) return launch_score<D, T, 2, PAD>(p, stream);
+  if (p.g <= 64) return launch_score<D, T, 4, PAD>(p, stream);
+  return launch_score<D, T, 8, PAD>(p, stream);
 }
 
+template <int D, bool PAD>
+static hipError_t launch_score_f32(const LiParams& p, hipStream_t stream) {
+  static const int occ = score_occupancy(li_score_f32_kernel<D, PAD>);
+  return launch_score_kernel((const void*)li_score_f32_kernel<D, PAD>, occ, p, stream);
+}
+
+// Head dims 64 / 128 / 256 run exact kernels; any other supported head dim
+// (a multiple of 8 up to 256; of 4 for fp32) runs the next larger one with
+// zero-padded rows.
 template <typename T>
 static hipError_t launch_score_d(const LiParams& p, int64_t d, hipStream_t stream) {
-  if (d == 64) return launch_score_g<64, T>(p, stream);
-  if (d == 128) return launch_score_g<128, T>(p, stream);
-  return launch_score_g<256, T>(p, stream);
+  if constexpr (__is_same(T, float)) {
+    if (d == 64) return launch_score_f32<64, false>(p, stream);
+    if (d == 128) return launch_score_f32<128, false>(p, stream);
+    if (d == 256) return launch_score_f32<256, false>(p, stream);
+    if (d < 64) return launch_score_f32<64, true>(p, stream);
+    if (d < 128) return launch_score_f32<128, true>(p, stream);
+    return launch_score_f32<256, true>(p, stream);
+  } else {
+    if (d == 64) return launch_score_g<64, T, false>(p, stream);
+    if (d == 128) return launch_score_g<128, T, false>(p, stream);
+    if (d == 256) return launch_score_g<256, T, false>(p, stream);
+    if (d < 64) return launch_score_g<64, T, true>(p, stream);
+    if (d < 128) return launch_score_g<128, T, true>(p, stream);
+    return launch_score_g<256, T, true>(p, stream);
+  }
 }
 
 int li_scores_run(const void* query, const void* key, const void* weights, const int32_t* act_q,
@@ -974,8 +1119,10 @@ int li_scores_run(const void* query, const void* key, const void* weights, const
   p.max_blocks = (int32_t)max_blocks;
   p.page_size = (int32_t)(page_size > 0 ? page_size : 1);
   p.chunk = kLiChunk;
-  hipError_t e = dtype == DSA_DTYPE_BF16 ? launch_score_d<bf16>(p, d, stream)
-                                         : launch_score_d<f16>(p, d, stream);
+  p.d = (int32_t)d;
+  hipError_t e = dtype == DSA_DTYPE_BF16   ? launch_score_d<bf16>(p, d, stream)
+                 : dtype == DSA_DTYPE_FP16 ? launch_score_d<f16>(p, d, stream)
+                                           : launch_score_d<float>(p, d, stream);
   DSA_HIP(e);
   return DSA_OK;
 }

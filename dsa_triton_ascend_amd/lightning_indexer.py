@@ -16,17 +16,37 @@ Extension: ``layout_key="PA_BSND"`` with a ``block_table`` runs the indexer
 over a paged key cache (``_lightning_indexer_paged``); the reference rejects
 a block_table, and still does here with any other key layout.
 
+Inputs: query / key in bfloat16, float16 or float32 (one dtype; fp32 runs
+full-fp32 products), any head dim up to 256 whose rows are a whole number of
+16 bytes (a multiple of 8 elements, or of 4 in fp32), N1 divisible by N2.
+
 Deliberate differences, on inputs the reference does not handle:
 * ``sparse_count`` larger than the key length pads with -1 (the reference's
   reshape fails, lines 341 vs 540);
-* ``sparse_count`` is limited to 4096.
+* ``sparse_count`` is limited to 16384 (the top-k sorts in LDS).
 """
 import torch
 
 from . import _lib
 from .sparse_flash_attention import INT64_MAX, _check_device, _seq_tensor
 
-_VALID_D = (64, 128, 256)
+_MAX_K = 16384
+_MAX_D = 256
+
+
+def _check_dtypes_and_dim(query, key, D):
+    if query.dtype not in (torch.bfloat16, torch.float16, torch.float32) or key.dtype != query.dtype:
+        raise ValueError("query and key must share one dtype: bfloat16, float16 or float32")
+    step = 4 if query.dtype == torch.float32 else 8
+    if D < step or D > _MAX_D or D % step:
+        raise ValueError(f"head dim must be a multiple of {step} in [{step}, {_MAX_D}], got {D}")
+
+
+def _check_k(sparse_count):
+    K = int(sparse_count)
+    if K < 1 or K > _MAX_K:
+        raise ValueError(f"sparse_count must be in [1, {_MAX_K}]")
+    return K
 
 
 def _weights_code(dt):
@@ -70,8 +90,8 @@ def lightning_indexer_triton(
                                         block_table, layout_query, sparse_count, sparse_mode, return_value)
     if sparse_mode not in (0, 3):
         raise ValueError("Only sparse_mode 0 (full) / 3 (rightDownCausal) supported")
-    if query.dtype not in (torch.bfloat16, torch.float16) or key.dtype != query.dtype:
-        raise ValueError("query and key must both be bfloat16 or both float16")
+    if query.dtype not in (torch.bfloat16, torch.float16, torch.float32) or key.dtype != query.dtype:
+        raise ValueError("query and key must share one dtype: bfloat16, float16 or float32")
     device = _check_device(query, key, weights)
     is_tnd = layout_query == "TND"
     if not is_tnd and layout_key == "TND":
@@ -113,13 +133,10 @@ def lightning_indexer_triton(
         raise ValueError("query and key head dims differ")
     if N1 % N2 != 0:
         raise ValueError(f"N1({N1}) must be divisible by N2({N2})")
-    if D not in _VALID_D:
-        raise ValueError(f"head dim must be one of {_VALID_D}, got {D}")
+    _check_dtypes_and_dim(query, key, D)
     if tuple(weights.shape) != w_shape:
         raise ValueError(f"weights must have shape {w_shape}, got {tuple(weights.shape)}")
-    K = int(sparse_count)
-    if K < 1 or K > 4096:
-        raise ValueError("sparse_count must be in [1, 4096]")
+    K = _check_k(sparse_count)
 
     out_shape = (q_rows, N2, K) if is_tnd else (B, S1, N2, K)
     indices = torch.empty(out_shape, dtype=torch.int32, device=device)
@@ -157,8 +174,6 @@ def _lightning_indexer_paged(query, key, weights, actual_seq_lengths_query, actu
         raise ValueError("PA_BSND key layout requires actual_seq_lengths_key")
     if sparse_mode not in (0, 3):
         raise ValueError("Only sparse_mode 0 (full) / 3 (rightDownCausal) supported")
-    if query.dtype not in (torch.bfloat16, torch.float16) or key.dtype != query.dtype:
-        raise ValueError("query and key must both be bfloat16 or both float16")
     if key.dim() != 4 or block_table.dim() != 2:
         raise ValueError("PA_BSND key must be [blocks, page, N2, D] and block_table [B, max_blocks]")
     device = _check_device(query, key, weights, block_table)
@@ -184,13 +199,10 @@ def _lightning_indexer_paged(query, key, weights, actual_seq_lengths_query, actu
         raise ValueError("query and key head dims differ")
     if N1 % N2 != 0:
         raise ValueError(f"N1({N1}) must be divisible by N2({N2})")
-    if D not in _VALID_D:
-        raise ValueError(f"head dim must be one of {_VALID_D}, got {D}")
+    _check_dtypes_and_dim(query, key, D)
     if tuple(weights.shape) != w_shape:
         raise ValueError(f"weights must have shape {w_shape}, got {tuple(weights.shape)}")
-    K = int(sparse_count)
-    if K < 1 or K > 4096:
-        raise ValueError("sparse_count must be in [1, 4096]")
+    K = _check_k(sparse_count)
     indices = torch.empty(out_shape, dtype=torch.int32, device=device)
     values = torch.zeros(out_shape, dtype=query.dtype, device=device)
     if q_rows == 0:

@@ -289,14 +289,15 @@ size_t dsa_dense_kl_bwd_workspace_size(int64_t batch, int64_t s1, int64_t s2, in
  * ascending on ties, -inf entries and padding reported as index -1.
  *   query [R1, N1, D] (R1 = B*S1 BSND or T1 TND), key [R2, N2, D] (R2 = B*S2
  *   BSND or T2 TND), weights [R1, N1] (weights_dtype BF16 / FP16 / FP32),
- *   D in {64, 128, 256}, N1 % N2 == 0, N1/N2 <= 128, dtype BF16 or FP16,
+ *   D up to 256 with 16-byte rows (a multiple of 8; of 4 for FP32), N1 % N2
+ *   == 0, N1/N2 <= 128, dtype BF16, FP16 or FP32 (FP32 products in full fp32),
  *   sparse_mode 0 or 3.  With a TND query both length arrays are cumulative
  *   (as the reference converts both, 500-506); a TND key needs a TND query.
  *   For a TND key, s2 is the largest per-batch key length (the width of the
  *   score rows).
  * Writes sparse_indices [R1, N2, K] int32 and, when return_value != 0,
  * sparse_values [R1, N2, K] in the query dtype (-inf where the index is -1).
- * The workspace holds the fp32 scores [R1*N2, s2].  K <= 4096.
+ * The workspace holds the fp32 scores [R1*N2, s2].  K <= 16384.
  */
 int dsa_li_fwd(const void* query, const void* key, const void* weights,
                const int32_t* actual_seq_q, const int32_t* actual_seq_k,
@@ -324,7 +325,7 @@ int dsa_li_scores(const void* query, const void* key, const void* weights,
  * Stable top-k of fp32 score rows (the second stage of dsa_li_fwd; replaces
  * `_stable_topk`, lightning_indexer_triton.py:339-357): scores [rows, s2] ->
  * indices [rows, K] int32 and, if values != NULL, values [rows, K] fp32.
- * Bit-exact on given scores; K <= 4096; K > s2 pads with -1 / -inf.
+ * Bit-exact on given scores; K <= 16384; K > s2 pads with -1 / -inf.
  */
 int dsa_li_topk_from_scores(const float* scores, int64_t rows, int64_t s2, int64_t sparse_count,
                             int32_t* indices, float* values, void* stream);

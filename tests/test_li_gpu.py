@@ -30,9 +30,12 @@ def _api():
 
 
 def _inputs(B, S1, S2, N1, N2, D, dtype, wdtype=torch.float32, seed=42):
+    """fp16-representable q / k for 16-bit dtypes; full fp32 values for fp32
+    (so that its products are not exact in fp32)."""
     rng = np.random.RandomState(seed)
-    q = to_dtype_np(rng.randn(B, S1, N1, D).astype(np.float16).astype(np.float32), dtype)
-    k = to_dtype_np(rng.randn(B, S2, N2, D).astype(np.float16).astype(np.float32), dtype)
+    via16 = (lambda x: x) if dtype == torch.float32 else (lambda x: x.astype(np.float16).astype(np.float32))
+    q = to_dtype_np(via16(rng.randn(B, S1, N1, D).astype(np.float32)), dtype)
+    k = to_dtype_np(via16(rng.randn(B, S2, N2, D).astype(np.float32)), dtype)
     w = to_dtype_np(rng.rand(B, S1, N1).astype(np.float32), wdtype)
     return q, k, w
 
@@ -52,6 +55,8 @@ def _topk_gpu(scores_np, k):
     (4096, 2048, "ties"), (16384, 2048, "random"), (20000, 2048, "ties"), (32768, 2048, "random"),
     (32768, 4096, "mixed"), (5000, 1, "ties"), (2049, 2048, "masked_tail"), (3000, 100, "equal"),
     (32768, 2048, "narrow"), (32767, 2048, "random"), (40001, 2048, "ties"), (8191, 4096, "random"),
+    # K above 4096: the general selection with a 16384-entry LDS sort
+    (32768, 8192, "random"), (20000, 16384, "ties"), (40001, 8192, "mixed"), (12000, 16384, "k_gt_s2"),
 ])
 def test_topk_bit_exact(S2, k, kind):
     print(f"[li topk] S2={S2} k={k} {kind}", flush=True)
@@ -105,6 +110,16 @@ def _score_tol(q, k, w, N2):
     (2, 3, 257, 8, 1, 256, 0, torch.bfloat16, torch.float16),
     (1, 4, 2100, 128, 1, 128, 3, torch.bfloat16, torch.float32),
     (1, 2, 333, 24, 1, 128, 0, torch.float16, torch.float32),
+    # head dims other than 64 / 128 / 256 (zero-padded rows), odd N1, G = 3
+    (1, 4, 256, 7, 1, 96, 0, torch.bfloat16, torch.bfloat16),
+    (2, 3, 300, 12, 4, 256, 3, torch.float16, torch.float16),
+    (1, 3, 290, 8, 1, 40, 3, torch.bfloat16, torch.float32),
+    # fp32 query / key / weights: full-fp32 products
+    (1, 3, 500, 16, 2, 64, 3, torch.float32, torch.float32),
+    (1, 4, 256, 7, 1, 96, 3, torch.float32, torch.float32),
+    (2, 2, 400, 64, 1, 128, 0, torch.float32, torch.float32),
+    (1, 2, 300, 40, 1, 256, 3, torch.float32, torch.float32),
+    (1, 3, 200, 8, 1, 20, 0, torch.float32, torch.float32),
 ])
 def test_scores_match_oracle(B, S1, S2, N1, N2, D, mode, dtype, wdtype):
     print(f"[li scores] B={B} S1={S1} S2={S2} N1={N1} N2={N2} D={D} mode={mode} {dtype}", flush=True)
@@ -146,11 +161,12 @@ def _check_topk_with_ties(idx_g, sc_rows, k, score_tol_rows, what):
     assert flips <= max(4, idx_g.size // 500)
 
 
-def _full_case(B, S1, S2, N1, N2, D, k, mode, dtype, rows=None, act_q=None, act_k=None, seed=42):
+def _full_case(B, S1, S2, N1, N2, D, k, mode, dtype, rows=None, act_q=None, act_k=None, seed=42,
+               wdtype=torch.float32):
     dsa = _api()
-    q, k_, w = _inputs(B, S1, S2, N1, N2, D, dtype, seed=seed)
+    q, k_, w = _inputs(B, S1, S2, N1, N2, D, dtype, wdtype, seed=seed)
     idx, val = dsa.lightning_indexer_triton(
-        dev(q, dtype), dev(k_, dtype), dev(w, torch.float32), act_q, act_k,
+        dev(q, dtype), dev(k_, dtype), dev(w, wdtype), act_q, act_k,
         sparse_count=k, sparse_mode=mode, return_value=True)
     torch.cuda.synchronize()
     idx = idx.cpu().numpy()
@@ -187,6 +203,22 @@ def test_indexer_small_mode3_hidden_rows():
     for s in range(9):
         vis = min(max(20 - 9 + s + 1, 0), 20)
         assert (idx[1, s, 0, :min(vis, 16)] >= 0).all() and (idx[1, s, 0, min(vis, 16):] == -1).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["fp16", "fp32"])
+@pytest.mark.parametrize("mode", [0, 3])
+@pytest.mark.parametrize("B", [1, 2, 3])
+@pytest.mark.parametrize("S1,S2,N1,N2,D,k", [
+    (1, 128, 8, 1, 128, 32), (4, 256, 7, 1, 96, 32), (8, 128, 16, 2, 64, 64), (3, 256, 12, 4, 256, 32),
+])
+def test_indexer_reference_small_grid(S1, S2, N1, N2, D, k, B, mode, dtype):
+    """The small shapes of the reference's test_basic grid (test_li_triton.py:42-57):
+    odd N1, D = 96, GQA groups, fp16 and fp32 inputs with weights of the same
+    dtype, against the oracle."""
+    print(f"[li full] reference grid S1={S1} S2={S2} N1={N1} N2={N2} D={D} k={k} B={B} mode={mode} {dtype}",
+          flush=True)
+    idx = _full_case(B, S1, S2, N1, N2, D, k, mode, dtype, wdtype=dtype, seed=7 + B)
+    assert idx.shape == (B, S1, N2, k) and ((idx >= 0) & (idx < S2)).any()
 
 
 def test_indexer_gqa_fp16_mode0():
