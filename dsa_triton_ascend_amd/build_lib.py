@@ -23,6 +23,7 @@ SOURCES = [
     "sfa_bwd.hip",
     "li_fwd.hip",
     "kl_bwd.hip",
+    "kl_generic.hip",
     "dense_kl.hip",
 ]
 

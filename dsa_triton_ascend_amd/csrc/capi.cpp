@@ -62,15 +62,18 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
 size_t sfa_bwd_workspace_bytes(int64_t q_rows, int64_t kv_rows, int64_t n1, int64_t d, int64_t total_pos,
                                bool merge);
 // kl_bwd.hip
-size_t kl_bwd_workspace_bytes(int64_t q_rows, int64_t kv_rows, int64_t topk);
+size_t kl_bwd_workspace_bytes(int64_t q_rows, int64_t kv_rows, int64_t topk, int64_t d_idx);
 int kl_bwd_max_topk();
 int kl_bwd_max_nidx();
+int kl_bwd_max_didx();
+// index head dims of the KL backward: 16-byte rows up to kl_bwd_max_didx()
+static bool kl_didx_ok(int64_t d_idx) { return d_idx >= 8 && d_idx <= kl_bwd_max_didx() && d_idx % 8 == 0; }
 int kl_bwd_run(const void* query, const void* key, const void* query_rope, const void* key_rope,
                const void* query_index, const void* key_index, const void* weights, const int32_t* sparse_indices,
                const float* softmax_max, const float* softmax_sum, const int32_t* act_q, const int32_t* act_k,
                const int32_t* block_table, void* d_query_index, void* d_key_index, void* d_weights, float* loss,
                int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t d, int64_t d_rope, int64_t nidx,
-               int64_t topk, int64_t q_rows, int64_t kv_rows, int64_t max_blocks, int64_t page_size,
+               int64_t d_idx, int64_t topk, int64_t q_rows, int64_t kv_rows, int64_t max_blocks, int64_t page_size,
                int32_t layout_q, int32_t layout_k, int32_t dtype, int32_t w_dtype, float scale_value,
                void* workspace, hipStream_t stream);
 int sfa_bwd_run(const void* query, const void* query_rope, const void* key, const void* key_rope,
@@ -361,16 +364,16 @@ int dsa_sfa_bwd(const void* query, const void* query_rope, const void* key, cons
 
 size_t dsa_kl_bwd_workspace_size(int64_t batch, int64_t s1, int64_t s2, int64_t sparse_count, int64_t d_idx) {
   if (batch <= 0 || !mul_lt(batch, s1, 1ll << 31) || !mul_lt(batch, s2, 1ll << 31) || s1 <= 0 || s2 <= 0 ||
-      sparse_count <= 0 || sparse_count > kl_bwd_max_topk() || d_idx != 128)
+      sparse_count <= 0 || sparse_count > kl_bwd_max_topk() || !kl_didx_ok(d_idx))
     return 0;
-  return kl_bwd_workspace_bytes(batch * s1, batch * s2, sparse_count);
+  return kl_bwd_workspace_bytes(batch * s1, batch * s2, sparse_count, d_idx);
 }
 
 size_t dsa_kl_bwd_ex_workspace_size(int64_t q_rows, int64_t kv_rows, int64_t sparse_count, int64_t d_idx) {
   if (q_rows <= 0 || q_rows >= (1ll << 31) || kv_rows <= 0 || kv_rows >= (1ll << 31) || sparse_count <= 0 ||
-      sparse_count > kl_bwd_max_topk() || d_idx != 128)
+      sparse_count > kl_bwd_max_topk() || !kl_didx_ok(d_idx))
     return 0;
-  return kl_bwd_workspace_bytes(q_rows, kv_rows, sparse_count);
+  return kl_bwd_workspace_bytes(q_rows, kv_rows, sparse_count, d_idx);
 }
 
 // Validation shared by dsa_kl_bwd and dsa_kl_bwd_ex.  For a TND side s1 / s2
@@ -393,7 +396,8 @@ static int kl_check(const void* query, const void* key, const void* query_rope, 
   DSA_CHECK_SUPPORTED(d_rope == 0 || d_rope == 64, "rope dim must be 64 (or 0 for no rope), got %lld",
                       (long long)d_rope);
   DSA_CHECK_ARG(d_rope == 0 || (query_rope && key_rope), "null rope tensor pointer");
-  DSA_CHECK_SUPPORTED(d_idx == 128, "index head dim must be 128, got %lld", (long long)d_idx);
+  DSA_CHECK_SUPPORTED(kl_didx_ok(d_idx), "index head dim must be a multiple of 8 in [8, %d], got %lld",
+                      kl_bwd_max_didx(), (long long)d_idx);
   DSA_CHECK_SUPPORTED(n_idx >= 1 && n_idx <= kl_bwd_max_nidx(), "Nidx1 must be in [1, %d], got %lld",
                       kl_bwd_max_nidx(), (long long)n_idx);
   DSA_CHECK_SUPPORTED(n1 >= 1 && n1 <= 128, "N1 must be in [1, 128], got %lld", (long long)n1);
@@ -429,7 +433,7 @@ static int kl_check(const void* query, const void* key, const void* query_rope, 
   } else {
     DSA_CHECK_ARG(s2 >= 1 && mul_eq(batch, s2, kv_rows), "kv_rows must equal B*S2 for a BSND key");
   }
-  const size_t need = kl_bwd_workspace_bytes(q_rows, kv_rows, sparse_count);
+  const size_t need = kl_bwd_workspace_bytes(q_rows, kv_rows, sparse_count, d_idx);
   if (workspace == nullptr || workspace_bytes < need) {
     set_error("workspace of %zu bytes required, %zu given", need, workspace_bytes);
     return DSA_ERR_WORKSPACE;
@@ -457,7 +461,7 @@ int dsa_kl_bwd(const void* query, const void* key, const void* query_rope, const
   return kl_bwd_run(query, key, d_rope ? query_rope : nullptr, d_rope ? key_rope : nullptr, query_index,
                     key_index, weights, sparse_indices, softmax_max, softmax_sum, actual_seq_qlen,
                     actual_seq_klen, nullptr, d_query_index, d_key_index, d_weights, loss, batch, s1, s2, n1, d,
-                    d_rope, n_idx, sparse_count, batch * s1, batch * s2, 0, 1, DSA_LAYOUT_BSND,
+                    d_rope, n_idx, d_idx, sparse_count, batch * s1, batch * s2, 0, 1, DSA_LAYOUT_BSND,
                     DSA_LAYOUT_BSND, dtype, weights_dtype, scale_value, workspace, (hipStream_t)stream);
 }
 
@@ -485,7 +489,7 @@ int dsa_kl_bwd_ex(const void* query, const void* key, const void* query_rope, co
   return kl_bwd_run(query, key, d_rope ? query_rope : nullptr, d_rope ? key_rope : nullptr, query_index,
                     key_index, weights, sparse_indices, softmax_max, softmax_sum, actual_seq_qlen,
                     actual_seq_klen, layout_key == DSA_LAYOUT_PA_BSND ? block_table : nullptr, d_query_index,
-                    d_key_index, d_weights, loss, batch, s1, s2, n1, d, d_rope, n_idx, sparse_count, q_rows,
+                    d_key_index, d_weights, loss, batch, s1, s2, n1, d, d_rope, n_idx, d_idx, sparse_count, q_rows,
                     kv_rows, max_blocks, page_size, layout_query, layout_key, dtype, weights_dtype, scale_value,
                     workspace, (hipStream_t)stream);
 }

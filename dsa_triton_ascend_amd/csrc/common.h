@@ -136,6 +136,7 @@ int device_cu_count();
 // Test hooks set by dsa_set_test_flags (0 in normal use).
 constexpr int kTestForceGlobalGather = 1;  // gather with 64-bit addresses even below 2 GiB
 constexpr int kTestSmallBwdChunks = 2;     // backward rows in chunks of a 64 KiB workspace budget
+constexpr int kTestKlGeneric = 4;          // the KL backward takes its generic path at every shape
 int test_flags();
 }  // namespace dsa
 

@@ -37,22 +37,9 @@
 //    order or the split and the output is deterministic.
 //  * The loss is written per row and summed by one workgroup in a fixed
 //    order (the reference adds rows with an atomic).
-#include "kl_common.h"
+#include "kl_generic.h"
 
 namespace dsa {
-
-// Query-row and key-row addressing of one call.  Query rows are b*S1 + s1
-// (BSND) or packed with cumulative lengths (TND); key rows are b*S2 + t
-// (BSND), packed (TND) or pages of a cache through a block table (PA_BSND).
-// Length arrays are cumulative for a TND side, per-batch lengths otherwise.
-struct KlMap {
-  const int32_t* act_q;
-  const int32_t* act_k;
-  const int32_t* block_table;  // [batch, max_blocks] (PA_BSND key)
-  int64_t kv_rows;             // key rows in memory
-  int32_t batch, s1, s2, rows, topk, max_blocks, page_size;
-  int32_t layout_q, layout_k;
-};
 
 struct KlParams {
   KlMap m;
@@ -85,68 +72,6 @@ constexpr int kKlWaves = 8;
 constexpr int kKlMaxNidx = 64;
 constexpr int kKlMaxTopk = 8192;
 constexpr int kKlDsRow = kKlMaxNidx + 8;  // padded LDS row of dS^T (elements)
-
-struct KlRow {
-  int b, s1, n;
-  int klen;       // clamp bound of the row's token ids (S2, or the packed / paged length)
-  int64_t kbase;  // first key row of the row's batch (BSND / TND)
-  bool active;
-};
-
-// A row's batch, position and slot count n = min(topK, max(act_k - act_q +
-// s1 + 1, 0)) (kernel line 107); inactive rows (s1 >= act_q) have n = 0.
-__device__ __forceinline__ KlRow kl_row_info(const KlMap& m, int row) {
-  KlRow r;
-  int aq, ak;
-  if (m.layout_q == DSA_LAYOUT_TND) {
-    int lo = 0, hi = m.batch - 1;  // first b with cu[b] > row
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (m.act_q[mid] > row) hi = mid; else lo = mid + 1;
-    }
-    r.b = lo;
-    const int start = lo ? m.act_q[lo - 1] : 0;
-    r.s1 = row - start;
-    aq = m.act_q[lo] - start;
-  } else {
-    r.b = row / m.s1;
-    r.s1 = row - r.b * m.s1;
-    aq = m.act_q ? m.act_q[r.b] : m.s1;
-  }
-  if (m.layout_k == DSA_LAYOUT_TND) {
-    const int start = r.b ? m.act_k[r.b - 1] : 0;
-    r.kbase = start;
-    ak = m.act_k[r.b] - start;
-    r.klen = ak;
-  } else if (m.layout_k == DSA_LAYOUT_PA_BSND) {
-    r.kbase = 0;
-    r.klen = m.max_blocks * m.page_size;
-    ak = m.act_k ? m.act_k[r.b] : r.klen;
-  } else {
-    r.kbase = (int64_t)r.b * m.s2;
-    r.klen = m.s2;
-    ak = m.act_k ? m.act_k[r.b] : m.s2;
-  }
-  r.active = r.s1 < aq;
-  r.n = r.active ? min(m.topk, max(ak - aq + r.s1 + 1, 0)) : 0;
-  return r;
-}
-
-// Key row of slot k: the token id clamped to [0, klen) with no -1 test (lines
-// 58, 63, 300), then translated through the block table for a paged cache.
-// -1 marks a token in a -1 (or out-of-range) page: it reads as a zero key
-// row and receives no gradient.  Key rows past the end of the key tensor
-// (cumulative lengths larger than it) are treated the same way.
-__device__ __forceinline__ int kl_token(const KlMap& m, const KlRow& r, const int32_t* idx, int row, int k) {
-  const int t = min(max(idx[(int64_t)row * m.topk + k], 0), r.klen - 1);
-  if (m.layout_k != DSA_LAYOUT_PA_BSND) {
-    const int64_t g = r.kbase + t;
-    return g < m.kv_rows ? (int)g : -1;
-  }
-  const int blk = m.block_table[(int64_t)r.b * m.max_blocks + t / m.page_size];
-  const int64_t phys = (int64_t)blk * m.page_size + t % m.page_size;
-  return (blk < 0 || phys >= m.kv_rows) ? -1 : (int)phys;
-}
 
 // Zero source row of the pass-A gather (slots past the row's end and
 // tokens of -1 pages).
@@ -769,11 +694,13 @@ __device__ __forceinline__ int kl_fixed_exp(float bm, int len) {
   return 62 - ex;
 }
 
+// di: contribution columns (the index head dim), a multiple of 8; a wave
+// covers 128 columns per sweep (two per lane).
 template <typename T>
 __global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, const int32_t* rowexp,
                                                         const uint32_t* tokmax, const int32_t* offs,
                                                         const int32_t* list, long long* acc, T* dki, int ntok,
-                                                        int topk, int parts) {
+                                                        int topk, int parts, int di) {
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int t = w / parts, part = w - t * parts;
   const int lane = threadIdx.x & 63;
@@ -783,63 +710,68 @@ __global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, co
   const int np = kl_reduce_parts(len, parts);
   if (part >= np) return;
   const float bm = __uint_as_float(tokmax[t]);
-  T* dst = dki + (int64_t)t * kKlDi + 2 * lane;
-  if (!(bm < INFINITY)) {  // non-finite contributions: no fixed-point scale exists
-    if (part == 0) {
-      dst[0] = Elem<T>::from_f32(NAN);
-      dst[1] = Elem<T>::from_f32(NAN);
+  for (int col = 2 * lane; col < ((di + 127) & ~127); col += 128) {
+    const bool cv = col < di;
+    T* dst = dki + (int64_t)t * di + col;
+    if (!(bm < INFINITY)) {  // non-finite contributions: no fixed-point scale exists
+      if (part == 0 && cv) {
+        dst[0] = Elem<T>::from_f32(NAN);
+        dst[1] = Elem<T>::from_f32(NAN);
+      }
+      continue;
     }
-    return;
-  }
-  long long a0 = 0, a1 = 0;
-  int e = 0;
-  if (bm > 0.f) {
-    e = kl_fixed_exp(bm, len);
-    const int L = (len + np - 1) / np;
-    const int i1 = min(len, (part + 1) * L);
-    // A contribution is c16 * 2^-e_row; its fixed-point value is
-    // round(c16 * 2^(e - e_row)), exact through double (a branch-free
-    // conversion: an integer shift-and-round per element diverges and runs
-    // slower).  64 list entries and their row exponents come in with one
-    // load per lane and are broadcast with readlane; 16 contribution rows
-    // are in flight at a time.
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    constexpr int U = 16;
-    for (int base = part * L; base < i1; base += 64) {
-      const int cnt = min(64, i1 - base);
-      const int slv = lane < cnt ? list[o0 + base + lane] : 0;
-      const int kv = lane < cnt ? e - rowexp[slv / topk] : 0;
-      for (int u0 = 0; u0 < cnt; u0 += U) {
-        h2 v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int sl = __builtin_amdgcn_readlane(slv, u0 + u);
-          v[u] = u0 + u < cnt ? *(const h2*)(cbuf + (int64_t)sl * kKlDi + 2 * lane) : (h2){0, 0};
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const double sc = ldexp(1.0, __builtin_amdgcn_readlane(kv, u0 + u));
-          a0 += __double2ll_rn((double)v[u].x * sc);
-          a1 += __double2ll_rn((double)v[u].y * sc);
+    long long a0 = 0, a1 = 0;
+    int e = 0;
+    if (bm > 0.f) {
+      e = kl_fixed_exp(bm, len);
+      const int L = (len + np - 1) / np;
+      const int i1 = min(len, (part + 1) * L);
+      // A contribution is c16 * 2^-e_row; its fixed-point value is
+      // round(c16 * 2^(e - e_row)), exact through double (a branch-free
+      // conversion: an integer shift-and-round per element diverges and runs
+      // slower).  64 list entries and their row exponents come in with one
+      // load per lane and are broadcast with readlane; 16 contribution rows
+      // are in flight at a time.
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      constexpr int U = 16;
+      for (int base = part * L; base < i1; base += 64) {
+        const int cnt = min(64, i1 - base);
+        const int slv = lane < cnt ? list[o0 + base + lane] : 0;
+        const int kv = lane < cnt ? e - rowexp[slv / topk] : 0;
+        for (int u0 = 0; u0 < cnt; u0 += U) {
+          h2 v[U];
+  #pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int sl = __builtin_amdgcn_readlane(slv, u0 + u);
+            v[u] = (u0 + u < cnt && cv) ? *(const h2*)(cbuf + (int64_t)sl * di + col) : (h2){0, 0};
+          }
+  #pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const double sc = ldexp(1.0, __builtin_amdgcn_readlane(kv, u0 + u));
+            a0 += __double2ll_rn((double)v[u].x * sc);
+            a1 += __double2ll_rn((double)v[u].y * sc);
+          }
         }
       }
     }
-  }
-  if (np == 1) {
-    const double us = ldexp(1.0, -e);
-    dst[0] = Elem<T>::from_f32((float)((double)a0 * us));
-    dst[1] = Elem<T>::from_f32((float)((double)a1 * us));
-  } else {
-    unsigned long long* ap = (unsigned long long*)acc + (int64_t)t * kKlDi + 2 * lane;
-    atomicAdd(ap, (unsigned long long)a0);
-    atomicAdd(ap + 1, (unsigned long long)a1);
+    if (!cv) continue;
+    if (np == 1) {
+      const double us = ldexp(1.0, -e);
+      dst[0] = Elem<T>::from_f32((float)((double)a0 * us));
+      dst[1] = Elem<T>::from_f32((float)((double)a1 * us));
+    } else {
+      unsigned long long* ap = (unsigned long long*)acc + (int64_t)t * di + col;
+      atomicAdd(ap, (unsigned long long)a0);
+      atomicAdd(ap + 1, (unsigned long long)a1);
+    }
   }
 }
 
 // dKi of the tokens with more than one part, from their accumulators
 template <typename T>
 __global__ __launch_bounds__(256) void kl_reduce_finish_kernel(const uint32_t* tokmax, const int32_t* offs,
-                                                               const long long* acc, T* dki, int ntok, int parts) {
+                                                               const long long* acc, T* dki, int ntok, int parts,
+                                                               int di) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (t >= ntok) return;
@@ -849,10 +781,12 @@ __global__ __launch_bounds__(256) void kl_reduce_finish_kernel(const uint32_t* t
   if (!(bm < INFINITY)) return;
   const int e = bm > 0.f ? kl_fixed_exp(bm, len) : 0;
   const double us = ldexp(1.0, -e);
-  const long long* ap = acc + (int64_t)t * kKlDi + 2 * lane;
-  T* dst = dki + (int64_t)t * kKlDi + 2 * lane;
-  dst[0] = Elem<T>::from_f32((float)((double)ap[0] * us));
-  dst[1] = Elem<T>::from_f32((float)((double)ap[1] * us));
+  for (int col = 2 * lane; col < di; col += 128) {
+    const long long* ap = acc + (int64_t)t * di + col;
+    T* dst = dki + (int64_t)t * di + col;
+    dst[0] = Elem<T>::from_f32((float)((double)ap[0] * us));
+    dst[1] = Elem<T>::from_f32((float)((double)ap[1] * us));
+  }
 }
 
 // loss = sum of the per-row terms, in a fixed order (one workgroup)
@@ -875,14 +809,16 @@ __global__ __launch_bounds__(256) void kl_loss_kernel(const float* part, int row
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct KlWs {
-  size_t cbuf, rowmax, rowexp, loss, cnt, tokmax, acc, offs, rank, list, total;
+  size_t cbuf, rowmax, rowexp, loss, cnt, tokmax, acc, offs, rank, list, pi, total;
 };
 
-static KlWs kl_ws_layout(int64_t rows, int64_t tokens, int64_t topk) {
+// pi (the generic path's per-slot p / I) is laid out for every call: the
+// workspace query does not know Nidx1, which also selects the generic path
+static KlWs kl_ws_layout(int64_t rows, int64_t tokens, int64_t topk, int64_t di) {
   KlWs w;
   size_t o = 0;
   w.cbuf = o;
-  o += align256((size_t)rows * topk * kKlDi * sizeof(_Float16));
+  o += align256((size_t)rows * topk * di * sizeof(_Float16));
   w.rowmax = o;
   o += align256((size_t)rows * sizeof(float));
   w.rowexp = o;
@@ -894,23 +830,28 @@ static KlWs kl_ws_layout(int64_t rows, int64_t tokens, int64_t topk) {
   w.tokmax = o;
   o += align256((size_t)tokens * sizeof(uint32_t));
   w.acc = o;
-  o += align256((size_t)tokens * kKlDi * sizeof(long long));
+  o += align256((size_t)tokens * di * sizeof(long long));
   w.offs = o;
   o += align256((size_t)(tokens + 1) * sizeof(int32_t));
   w.rank = o;
   o += align256((size_t)rows * topk * sizeof(int32_t));
   w.list = o;
   o += align256((size_t)rows * topk * sizeof(int32_t));
+  w.pi = o;
+  o += align256((size_t)rows * topk * 2 * sizeof(float));
   w.total = o;
   return w;
 }
 
-size_t kl_bwd_workspace_bytes(int64_t q_rows, int64_t kv_rows, int64_t topk) {
-  return kl_ws_layout(q_rows, kv_rows, topk).total;
+size_t kl_bwd_workspace_bytes(int64_t q_rows, int64_t kv_rows, int64_t topk, int64_t d_idx) {
+  return kl_ws_layout(q_rows, kv_rows, topk, d_idx).total;
 }
 
-int kl_bwd_max_topk() { return kKlMaxTopk; }
-int kl_bwd_max_nidx() { return kKlMaxNidx; }
+// limits of the whole operator (the generic path's); the fused row kernel
+// takes d_idx = 128, Nidx1 <= kKlMaxNidx and topK <= kKlMaxTopk
+int kl_bwd_max_topk() { return 1 << 20; }
+int kl_bwd_max_nidx() { return kGenMaxNidx; }
+int kl_bwd_max_didx() { return kGenMaxDi; }
 
 // The row kernel's dynamic LDS: the pass-A tile ring, then I, p and the
 // token rows of a row (3 x topK x 4 bytes).  Two tile buffers when they fit
@@ -961,11 +902,11 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
                const float* softmax_max, const float* softmax_sum, const int32_t* act_q, const int32_t* act_k,
                const int32_t* block_table, void* d_query_index, void* d_key_index, void* d_weights, float* loss,
                int64_t batch, int64_t s1, int64_t s2, int64_t n1, int64_t d, int64_t d_rope, int64_t nidx,
-               int64_t topk, int64_t q_rows, int64_t kv_rows, int64_t max_blocks, int64_t page_size,
-               int32_t layout_q, int32_t layout_k, int32_t dtype, int32_t w_dtype, float scale_value,
-               void* workspace, hipStream_t stream) {
+               int64_t d_idx, int64_t topk, int64_t q_rows, int64_t kv_rows, int64_t max_blocks,
+               int64_t page_size, int32_t layout_q, int32_t layout_k, int32_t dtype, int32_t w_dtype,
+               float scale_value, void* workspace, hipStream_t stream) {
   const int64_t rows = q_rows, tokens = kv_rows;
-  const KlWs L = kl_ws_layout(rows, tokens, topk);
+  const KlWs L = kl_ws_layout(rows, tokens, topk, d_idx);
   unsigned char* ws = (unsigned char*)workspace;
   KlMap m;
   m.act_q = act_q;
@@ -1031,8 +972,43 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((zn + 255) / 256)), dim3(256), 0, stream, s.cnt, zn);
   DSA_HIP(hipGetLastError());
   const bool bf = dtype == DSA_DTYPE_BF16;
-  DSA_HIP(bf ? dispatch_kl_row<bf16>(p, (int)rows, (int)d, (int)d_rope, topk, stream)
-             : dispatch_kl_row<f16>(p, (int)rows, (int)d, (int)d_rope, topk, stream));
+  // the fused row kernel where it applies (d_idx = 128, Nidx1 <= 64, topK
+  // <= 8192, and its LDS fits: it returns hipErrorInvalidConfiguration
+  // before launching otherwise), else the generic path
+  hipError_t e = hipErrorInvalidConfiguration;
+  if (d_idx == kKlDi && nidx <= kKlMaxNidx && topk <= kKlMaxTopk && !(test_flags() & kTestKlGeneric))
+    e = bf ? dispatch_kl_row<bf16>(p, (int)rows, (int)d, (int)d_rope, topk, stream)
+           : dispatch_kl_row<f16>(p, (int)rows, (int)d, (int)d_rope, topk, stream);
+  if (e == hipErrorInvalidConfiguration) {
+    KlGenParams g;
+    g.m = m;
+    g.q = query;
+    g.qr = query_rope;
+    g.k = key;
+    g.kr = key_rope;
+    g.qi = query_index;
+    g.ki = key_index;
+    g.w = weights;
+    g.idx = sparse_indices;
+    g.smax = softmax_max;
+    g.ssum = softmax_sum;
+    g.dqi = d_query_index;
+    g.dw = d_weights;
+    g.cbuf = p.cbuf;
+    g.rowmax = p.rowmax;
+    g.rowexp = p.rowexp;
+    g.loss_part = p.loss_part;
+    g.pi = (float*)(ws + L.pi);
+    g.n1 = (int32_t)n1;
+    g.nidx = (int32_t)nidx;
+    g.di = (int32_t)d_idx;
+    g.dip = (int32_t)((d_idx + 31) / 32 * 32);
+    g.topk = (int32_t)topk;
+    g.w_dtype = w_dtype;
+    g.scale_log2 = scale_value * kLog2e;
+    e = kl_gen_run(g, (int)rows, (int)d, (int)d_rope, bf, stream);
+  }
+  DSA_HIP(e);
   const dim3 bgrid((unsigned)rows, (unsigned)((topk + 255) / 256));
   hipLaunchKernelGGL(kl_bucket_kernel<false>, bgrid, dim3(256), 0, stream, s);
   DSA_HIP(hipGetLastError());
@@ -1044,16 +1020,16 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   const dim3 fgrid((unsigned)((tokens + 3) / 4));
   if (bf) {
     hipLaunchKernelGGL(kl_reduce_kernel<bf16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowexp, s.tokmax, s.offs,
-                       s.list, acc, (bf16*)d_key_index, (int)tokens, (int)topk, parts);
+                       s.list, acc, (bf16*)d_key_index, (int)tokens, (int)topk, parts, (int)d_idx);
     DSA_HIP(hipGetLastError());
     hipLaunchKernelGGL(kl_reduce_finish_kernel<bf16>, fgrid, dim3(256), 0, stream, s.tokmax, s.offs, acc,
-                       (bf16*)d_key_index, (int)tokens, parts);
+                       (bf16*)d_key_index, (int)tokens, parts, (int)d_idx);
   } else {
     hipLaunchKernelGGL(kl_reduce_kernel<f16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowexp, s.tokmax, s.offs,
-                       s.list, acc, (f16*)d_key_index, (int)tokens, (int)topk, parts);
+                       s.list, acc, (f16*)d_key_index, (int)tokens, (int)topk, parts, (int)d_idx);
     DSA_HIP(hipGetLastError());
     hipLaunchKernelGGL(kl_reduce_finish_kernel<f16>, fgrid, dim3(256), 0, stream, s.tokmax, s.offs, acc,
-                       (f16*)d_key_index, (int)tokens, parts);
+                       (f16*)d_key_index, (int)tokens, parts, (int)d_idx);
   }
   DSA_HIP(hipGetLastError());
   hipLaunchKernelGGL(kl_loss_kernel, dim3(1), dim3(256), 0, stream, p.loss_part, (int)rows, loss);

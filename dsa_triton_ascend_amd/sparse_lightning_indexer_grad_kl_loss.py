@@ -13,10 +13,15 @@ and loss a [1] fp32 tensor (the sum over all query rows).  pre_tokens,
 next_tokens and deterministic are accepted and ignored, as in the
 reference; every output of this implementation is deterministic.
 
+Index shapes: D_idx any multiple of 8 up to 256, Nidx1 up to 128, any topK
+(rows x topK < 2^31); the reference loops over any D_idx and Nidx1
+(119-136, 219-262).  D_idx = 128, Nidx1 <= 64 and topK <= 8192 run the
+fused row kernel, other shapes a generic path with the same outputs.
+
 Extensions over the reference, which accepts BSND only (534-535):
 
 * ``layout="TND"``: packed rows, query [T1, N1, D], key [T2, 1, D],
-  query_index [T1, Nidx1, 128], key_index [T2, 1, 128], weights [T1, Nidx1],
+  query_index [T1, Nidx1, D_idx], key_index [T2, 1, D_idx], weights [T1, Nidx1],
   sparse_indices [T1, 1, topK], softmax statistics with T1 * N1 entries
   ([1, T1, N1] from the TND forward), and cumulative ``actual_seq_qlen`` /
   ``actual_seq_klen`` (required), as the TND forward takes them.  Token ids
@@ -33,8 +38,8 @@ from . import _lib
 from .sparse_flash_attention import INT64_MAX, _check_device, _seq_tensor, _VALID_D
 
 _D_ROPE = 64
-_D_IDX = 128
-_MAX_NIDX = 64
+_MAX_D_IDX = 256
+_MAX_NIDX = 128
 _MAX_N1 = 128
 
 
@@ -113,8 +118,8 @@ def sparse_lightning_indexer_grad_kl_loss_triton(
     topK = sparse_indices.shape[-1]
     if D not in _VALID_D:
         raise ValueError(f"D must be one of {_VALID_D}, got {D}")
-    if D_idx != _D_IDX:
-        raise ValueError(f"index head dim must be {_D_IDX}, got {D_idx}")
+    if D_idx < 8 or D_idx > _MAX_D_IDX or D_idx % 8:
+        raise ValueError(f"index head dim must be a multiple of 8 in [8, {_MAX_D_IDX}], got {D_idx}")
     if not 1 <= Nidx1 <= _MAX_NIDX:
         raise ValueError(f"Nidx1 must be in [1, {_MAX_NIDX}], got {Nidx1}")
     if not 1 <= N1 <= _MAX_N1:

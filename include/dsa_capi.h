@@ -67,6 +67,9 @@ int dsa_abi_version(void);
  * that small problems run several chunks); set it around both the
  * workspace query and the call. */
 #define DSA_TEST_SMALL_BWD_CHUNKS 2
+/* Bit 2: dsa_kl_bwd / dsa_kl_bwd_ex take their generic path (the one for
+ * index shapes outside the fused row kernel) at every shape. */
+#define DSA_TEST_KL_GENERIC 4
 void dsa_set_test_flags(int32_t flags);
 
 /*
@@ -187,8 +190,10 @@ size_t dsa_sfa_bwd_workspace_size(int64_t q_rows, int64_t kv_rows, int64_t n1, i
  * (dsa_kl_bwd_workspace_size) holds rows * topK * d_idx fp16 slot
  * contributions (scaled by a per-row power of two), the token buckets and
  * kv_rows * d_idx int64 accumulators.  query/key/rope/index tensors share
- * one dtype (bf16 or fp16); D in {128, 256, 512}; d_idx = 128;
- * Nidx1 <= 64; N1 <= 128; topK <= 8192.
+ * one dtype (bf16 or fp16); D in {128, 256, 512}; N1 <= 128; d_idx a
+ * multiple of 8 up to 256; Nidx1 <= 128; topK up to 2^20 with rows * topK
+ * < 2^31.  d_idx = 128, Nidx1 <= 64 and topK <= 8192 run one fused row
+ * kernel; other shapes a generic path with the same outputs.
  */
 int dsa_kl_bwd(const void* query, const void* key, const void* query_rope, const void* key_rope,
                const void* query_index, const void* key_index, const void* weights,

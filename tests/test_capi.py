@@ -107,7 +107,8 @@ def _kl_ex_args(**kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(d=96), 2), (dict(n_idx=65), 2), (dict(sparse_count=8193), 2), (dict(layout_query=2), 2),
+    (dict(d=96), 2), (dict(n_idx=129), 2), (dict(d_idx=260), 2), (dict(d_idx=100), 2),
+    (dict(sparse_count=(1 << 20) + 1), 2), (dict(layout_query=2), 2),
     (dict(layout_key=5), 2), (dict(weights_dtype=7), 2),
     (dict(query=None), 1), (dict(loss=None), 1), (dict(q_rows=5), 1), (dict(kv_rows=63), 1),
     (dict(layout_query=1), 1),                                 # TND query without cumulative lengths
@@ -131,4 +132,7 @@ def test_kl_workspace_sizes_agree():
     _, lib = _lib()
     assert lib.dsa_kl_bwd_ex_workspace_size(2 * 7, 2 * 80, 48, 128) == lib.dsa_kl_bwd_workspace_size(2, 7, 80, 48, 128)
     assert lib.dsa_kl_bwd_ex_workspace_size(0, 80, 48, 128) == 0
-    assert lib.dsa_kl_bwd_ex_workspace_size(7, 80, 48, 64) == 0
+    assert lib.dsa_kl_bwd_ex_workspace_size(7, 80, 48, 100) == 0      # d_idx not a multiple of 8
+    assert lib.dsa_kl_bwd_ex_workspace_size(7, 80, 48, 264) == 0      # d_idx above 256
+    # the contribution buffer and the accumulators scale with d_idx
+    assert lib.dsa_kl_bwd_ex_workspace_size(7, 80, 48, 64) < lib.dsa_kl_bwd_ex_workspace_size(7, 80, 48, 128)

@@ -107,12 +107,12 @@ def _gpu_stats(q, k, qr, kr, scale):
 
 
 def _case(B, S1, S2, N1, D, Ni, topK, dtype, pattern="causal_random", rope=True, w_dtype=torch.float32,
-          act_q=None, act_k=None, seed=42, gpu_stats=False):
+          act_q=None, act_k=None, seed=42, gpu_stats=False, Di=128):
     rng = np.random.RandomState(seed)
     f = lambda *s: to_dtype_np(rng.randn(*s).astype(np.float16).astype(np.float32), dtype)  # noqa: E731
     q, k = f(B, S1, N1, D), f(B, S2, 1, D)
     qr, kr = (f(B, S1, N1, 64), f(B, S2, 1, 64)) if rope else (None, None)
-    qi, ki = f(B, S1, Ni, 128), f(B, S2, 1, 128)
+    qi, ki = f(B, S1, Ni, Di), f(B, S2, 1, Di)
     w = to_dtype_np(np.abs(rng.randn(B, S1, Ni)).astype(np.float32), w_dtype)
     si = _indices(B, S1, S2, topK, pattern, rng)
     aq = [S1] * B if act_q is None else list(act_q)
@@ -245,6 +245,70 @@ def test_kl_large_rows_sampled():
         e = exp["dW"][0, s1]
         assert_close(got[2][0, s1], e, 1e-3, 1e-5 * float(np.abs(e).max()) + ATOL_DW, f"row {s1} dW")
     assert np.isfinite(got[1]).all() and float(got[3][0]) >= 0.0
+
+
+# ---------------------------------------------------------------------------
+# the generic path: index shapes outside the fused row kernel (d_idx != 128,
+# Nidx1 > 64, topK > 8192), which the reference's loops take
+# (sparse_lightning_indexer_grad_kl_loss_triton.py:119-136, 219-262)
+# ---------------------------------------------------------------------------
+GEN_CASES = [
+    # B, S1, S2, N1, D, Nidx1, D_idx, topK, pattern
+    (1, 6, 96, 16, 128, 96, 64, 48, "causal_random"),
+    (1, 5, 80, 32, 512, 128, 256, 40, "random"),
+    (2, 7, 80, 16, 256, 24, 96, 48, "causal_continuous"),
+    (1, 4, 64, 8, 128, 8, 40, 32, "repeated"),
+    (1, 9, 120, 64, 512, 72, 128, 64, "continuous"),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("case", GEN_CASES, ids=[f"s{c[1]}k{c[2]}n{c[3]}d{c[4]}i{c[5]}di{c[6]}K{c[7]}{c[8]}"
+                                                 for c in GEN_CASES])
+def test_kl_generic_index_shapes(case, dtype):
+    B, S1, S2, N1, D, Ni, Di, topK, pattern = case
+    print(f"[kl_bwd generic] {case} {dtype}", flush=True)
+    c = _case(B, S1, S2, N1, D, Ni, topK, dtype, pattern, Di=Di)
+    _check(_run_gpu(c), _oracle(c), f"generic {case}")
+
+
+def test_kl_generic_topk_above_fused_limit():
+    """topK = 9000 (> 8192, the fused kernel's limit), no rope, bf16 weights, act lengths."""
+    print("[kl_bwd generic] topK 9000", flush=True)
+    c = _case(2, 3, 9100, 16, 128, 16, 9000, torch.bfloat16, "causal_random", rope=False,
+              w_dtype=torch.bfloat16, act_q=[3, 2], act_k=[9100, 5000])
+    _check(_run_gpu(c), _oracle(c), "topK 9000", torch.bfloat16)
+
+
+def _with_flags(flags, fn):
+    from dsa_triton_ascend_amd import _lib
+    lib = _lib.load()
+    lib.dsa_set_test_flags(flags)
+    try:
+        return fn()
+    finally:
+        lib.dsa_set_test_flags(0)
+
+
+@pytest.mark.parametrize("case", [CASES[0], CASES[4], CASES[5]], ids=["n32d512", "b2n64", "s33n128"])
+def test_kl_generic_path_at_fused_shapes(case):
+    """The generic path forced at shapes the fused kernel takes: both match
+    the oracle and each other (to the tolerance: their fp32 sums differ in
+    order and the generic path keeps dS in fp32), and the generic path is
+    bit-identical between two runs."""
+    from dsa_triton_ascend_amd import _lib
+    B, S1, S2, N1, D, Ni, topK, pattern = case
+    print(f"[kl_bwd generic forced] {case}", flush=True)
+    c = _case(B, S1, S2, N1, D, Ni, topK, torch.bfloat16, pattern)
+    fused = _run_gpu(c)
+    gen = _with_flags(_lib.TEST_KL_GENERIC, lambda: _run_gpu(c))
+    gen2 = _with_flags(_lib.TEST_KL_GENERIC, lambda: _run_gpu(c))
+    exp = _oracle(c)
+    _check(gen, exp, "generic (forced)")
+    for name, a, b in zip(("dQueryIndex", "dKeyIndex", "dW", "loss"), gen, fused):
+        assert_close(a, b, 1e-2, 2e-3 * float(np.abs(b).max()) + 1e-5, f"generic vs fused {name}")
+    for a, b in zip(gen, gen2):
+        assert np.array_equal(a, b)
 
 
 def test_kl_guards():
