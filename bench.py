@@ -40,6 +40,8 @@ def parse():
     ap.add_argument("--long-steps", type=int, default=3,
                     help="timed steps of the prefill / backward legs (each step is milliseconds)")
     ap.add_argument("--no-long", action="store_true", help="skip the prefill / backward legs")
+    ap.add_argument("--legs", default="prefill,bwd,bwd_merged,kl,dense",
+                    help="comma list of the long legs to run (prefill, bwd, bwd_merged, kl, dense)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain copy kernel of known size (for PMC calibration)")
     return ap.parse_args()
@@ -278,7 +280,7 @@ def leg(metric, workload, flops, ms, n, hbm_bytes=None):
     return out
 
 
-def long_legs(dev, steps):
+def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense")):
     import torch
     import dsa_triton_ascend_amd as dsa
     out = {}
@@ -297,10 +299,11 @@ def long_legs(dev, steps):
                                                  actual_seq_lengths_kv=cu, query_rope=qr, key_rope=kr,
                                                  layout_query="TND", layout_kv="TND", sparse_mode=3,
                                                  return_softmax_lse=True)
-    ms = time_call(fwd_tnd, steps, 1)
-    out["sfa_fwd_prefill"] = leg("SFA fwd TFLOP/s (prefill)",
-                                 "sfa_fwd prefill: TND one sequence T=8192, N1=128, D=512+64, topK=2048 "
-                                 "causal, sparse_mode 3, stats returned", 2.0 * N1 * (2 * D + DR) * n, ms, n)
+    if "prefill" in legs:
+        ms = time_call(fwd_tnd, steps, 1)
+        out["sfa_fwd_prefill"] = leg("SFA fwd TFLOP/s (prefill)",
+                                   "sfa_fwd prefill: TND one sequence T=8192, N1=128, D=512+64, topK=2048 "
+                                   "causal, sparse_mode 3, stats returned", 2.0 * N1 * (2 * D + DR) * n, ms, n)
     del q, qr, k, kr, idx, si
     torch.cuda.empty_cache()
     # cfg5a / cfg5b: backward pair at S=4096
@@ -315,9 +318,10 @@ def long_legs(dev, steps):
     def bwd():
         return dsa.sparse_flash_attention_grad_triton(q, k, k, si, do, o, smax, ssum, scale_value=scale,
                                                       query_rope=qr, key_rope=kr, sparse_mode=3)
-    ms = time_call(bwd, steps, 1)
-    out["sfa_bwd"] = leg("SFA bwd TFLOP/s", "sfa_bwd: BSND B=1, S1=S2=4096, N1=128, D=512+64, topK=2048 "
-                         "causal, sparse_mode 3, bf16", 2.0 * N1 * (3 * (D + DR) + 2 * D) * n, ms, n)
+    if "bwd" in legs:
+        ms = time_call(bwd, steps, 1)
+        out["sfa_bwd"] = leg("SFA bwd TFLOP/s", "sfa_bwd: BSND B=1, S1=S2=4096, N1=128, D=512+64, topK=2048 "
+                           "causal, sparse_mode 3, bf16", 2.0 * N1 * (3 * (D + DR) + 2 * D) * n, ms, n)
     # the training path (autograd): the shared-latent gradient dk + dv in one output
     from dsa_triton_ascend_amd.sparse_flash_attention import INT64_MAX
     from dsa_triton_ascend_amd.sparse_flash_attention_grad import _sfa_grad
@@ -325,11 +329,12 @@ def long_legs(dev, steps):
     def bwd_merged():
         return _sfa_grad(q, k, k, si, do, o, smax, ssum, scale, qr, kr, None, None, 1, "BSND", 3, INT64_MAX,
                          INT64_MAX, False, merge_kv=True)
-    ms = time_call(bwd_merged, steps, 1)
-    out["sfa_bwd_merged"] = leg("SFA bwd TFLOP/s (training path, d_key = dk + dv)",
-                                "sfa_bwd as called by the autograd Function (MLA absorb: one key gradient dk + dv): "
-                                "BSND B=1, S1=S2=4096, N1=128, D=512+64, topK=2048 causal, sparse_mode 3, bf16",
-                                2.0 * N1 * (3 * (D + DR) + 2 * D) * n, ms, n)
+    if "bwd_merged" in legs:
+        ms = time_call(bwd_merged, steps, 1)
+        out["sfa_bwd_merged"] = leg("SFA bwd TFLOP/s (training path, d_key = dk + dv)",
+                                  "sfa_bwd as called by the autograd Function (MLA absorb: one key gradient dk + dv): "
+                                  "BSND B=1, S1=S2=4096, N1=128, D=512+64, topK=2048 causal, sparse_mode 3, bf16",
+                                  2.0 * N1 * (3 * (D + DR) + 2 * D) * n, ms, n)
     NI, DI = 64, 128
     qi, ki = rn(1, S, NI, DI), rn(1, S, 1, DI)
     w = torch.rand(1, S, NI, generator=g, device=dev)
@@ -337,20 +342,24 @@ def long_legs(dev, steps):
     def kl():
         return dsa.sparse_lightning_indexer_grad_kl_loss_triton(q, k, qi, ki, w, si, smax, ssum, query_rope=qr,
                                                                 key_rope=kr, scale_value=scale)
-    ms = time_call(kl, steps, 1)
+    if "kl" in legs:
+        ms = time_call(kl, steps, 1)
     # HBM-bound: every valid (row, slot) pair gathers a K, K_rope and
     # K_index row; per row Q, Q_rope, Qi, weights, indices, statistics and
     # dQi, dW; per key row dKi
     kl_bytes = (n * (D + DR + DI) * 2 + S * (N1 * (D + DR) * 2 + NI * DI * 2 * 2 + NI * 4 * 2 + K * 4 + N1 * 8)
                 + S * DI * 2)
-    out["kl_bwd"] = leg("indexer KL-loss bwd TFLOP/s",
-                        "sparse_lightning_indexer_grad_kl_loss: B=1, S1=S2=4096, N1=128, D=512+64, Nidx1=64, "
-                        "D_idx=128, topK=2048 causal, bf16 (fp32 weights), stats from the SFA forward",
-                        n * (3 * 2 * NI * DI + 2 * N1 * (D + DR) + 2 * NI), ms, n, hbm_bytes=kl_bytes)
+    if "kl" in legs:
+        out["kl_bwd"] = leg("indexer KL-loss bwd TFLOP/s",
+                          "sparse_lightning_indexer_grad_kl_loss: B=1, S1=S2=4096, N1=128, D=512+64, Nidx1=64, "
+                          "D_idx=128, topK=2048 causal, bf16 (fp32 weights), stats from the SFA forward",
+                          n * (3 * 2 * NI * DI + 2 * N1 * (D + DR) + 2 * NI), ms, n, hbm_bytes=kl_bytes)
     del si, o, do
     torch.cuda.empty_cache()
     # dense warm-up stage at the same shape: every causal key, teacher stats of
     # the dense causal forward [B, N2, S1, G]
+    if "dense" not in legs:
+        return out
     dsmax, dssum = dense_stats(q, qr, k, kr, scale)
 
     def dense():
@@ -473,7 +482,7 @@ def main():
     del li_sets
     torch.cuda.empty_cache()
     if not args.no_long:
-        result.update(long_legs(dev, args.long_steps))
+        result.update(long_legs(dev, args.long_steps, tuple(args.legs.split(","))))
         torch.cuda.empty_cache()
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_decode(make_decode_sets(1, dev))
