@@ -37,7 +37,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--sets", type=int, default=6)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--long-steps", type=int, default=3,
+    ap.add_argument("--long-steps", type=int, default=10,
                     help="timed steps of the prefill / backward legs (each step is milliseconds)")
     ap.add_argument("--no-long", action="store_true", help="skip the prefill / backward legs")
     ap.add_argument("--legs", default="prefill,bwd,bwd_merged,kl,dense",
@@ -94,13 +94,13 @@ def time_decode(sets, steps, warmup):
     scale = 1.0 / math.sqrt(D + DR)
     nblk = B * CTX // PAGE
 
-    def step(s):
+    def step(s, strm=stream):
         st = lib.dsa_sfa_fwd(
             s["q"].data_ptr(), s["qr"].data_ptr(), s["cache"].data_ptr(), s["cache_r"].data_ptr(),
             s["si"].data_ptr(), out.data_ptr(), None, None, None, act_k.data_ptr(), s["bt"].data_ptr(),
             B, 1, CTX, N1, D, DR, K, B, nblk * PAGE, CTX // PAGE, PAGE, 1, 0, INT64_MAX, INT64_MAX,
             _lib.LAYOUT["BSND"], _lib.LAYOUT["PA_BSND"], _lib.DTYPE_BF16, scale, 0,
-            ws.data_ptr(), ws_bytes, stream)
+            ws.data_ptr(), ws_bytes, strm)
         if st != 0:
             _lib.check(st, "dsa_sfa_fwd")
 
@@ -126,7 +126,30 @@ def time_decode(sets, steps, warmup):
         e1.synchronize()
         per.append(e0.elapsed_time(e1))
     per.sort()
-    return total_ms / steps, per
+    # the same step captured once in a HIP graph (both kernels) and replayed:
+    # K replays back to back, no host launch work between them
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step(sets[0], torch.cuda.current_stream().cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step(sets[0], torch.cuda.current_stream().cuda_stream)
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    g0 = torch.cuda.Event(enable_timing=True)
+    g1 = torch.cuda.Event(enable_timing=True)
+    g0.record()
+    for _ in range(steps):
+        graph.replay()
+    g1.record()
+    torch.cuda.synchronize()
+    graph_ms = g0.elapsed_time(g1) / steps
+    del graph
+    return total_ms / steps, per, graph_ms
 
 
 def cpu_baseline_decode(sets):
@@ -267,17 +290,17 @@ def time_call(fn, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
-def leg(metric, workload, flops, ms, n, hbm_bytes=None):
+def leg(metric, workload, flops, ms, n):
+    """A secondary leg: algorithmic flops over the step time.  These legs are
+    MFMA-bound by their arithmetic intensity (the gathered rows they re-read
+    are served from L2 / MALL), so their roofline is the bf16 MFMA peak; the
+    measured HBM bytes of each kernel are in profiles/."""
     tf = flops / (ms * 1e-3) / 1e12
-    out = {"metric": metric, "value": round(tf, 2), "unit": "TFLOP/s", "higher_is_better": True,
-           "ms_per_step": round(ms, 4), "pct_of_bf16_peak": round(100.0 * tf / PEAK_BF16_TFLOPS, 3),
-           "algorithmic_flops": int(flops), "valid_pairs": n, "config": {"workload": workload}}
-    if hbm_bytes is not None:
-        # legs whose roofline is HBM: algorithmic bytes over the step time
-        gbs = hbm_bytes / (ms * 1e-3) / 1e9
-        out["hbm"] = {"algorithmic_bytes": int(hbm_bytes), "achieved_GBps": round(gbs, 1),
-                      "pct_of_peak": round(100.0 * gbs / PEAK_HBM_GBS, 2)}
-    return out
+    return {"metric": metric, "value": round(tf, 2), "unit": "TFLOP/s", "higher_is_better": True,
+            "ms_per_step": round(ms, 4), "pct_of_bf16_peak": round(100.0 * tf / PEAK_BF16_TFLOPS, 3),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tf / PEAK_BF16_TFLOPS, 4)},
+            "algorithmic_flops": int(flops), "valid_pairs": n, "config": {"workload": workload}}
 
 
 def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense")):
@@ -300,7 +323,7 @@ def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense")):
                                                  layout_query="TND", layout_kv="TND", sparse_mode=3,
                                                  return_softmax_lse=True)
     if "prefill" in legs:
-        ms = time_call(fwd_tnd, steps, 1)
+        ms = time_call(fwd_tnd, steps, 2)
         out["sfa_fwd_prefill"] = leg("SFA fwd TFLOP/s (prefill)",
                                    "sfa_fwd prefill: TND one sequence T=8192, N1=128, D=512+64, topK=2048 "
                                    "causal, sparse_mode 3, stats returned", 2.0 * N1 * (2 * D + DR) * n, ms, n)
@@ -319,7 +342,7 @@ def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense")):
         return dsa.sparse_flash_attention_grad_triton(q, k, k, si, do, o, smax, ssum, scale_value=scale,
                                                       query_rope=qr, key_rope=kr, sparse_mode=3)
     if "bwd" in legs:
-        ms = time_call(bwd, steps, 1)
+        ms = time_call(bwd, steps, 2)
         out["sfa_bwd"] = leg("SFA bwd TFLOP/s", "sfa_bwd: BSND B=1, S1=S2=4096, N1=128, D=512+64, topK=2048 "
                            "causal, sparse_mode 3, bf16", 2.0 * N1 * (3 * (D + DR) + 2 * D) * n, ms, n)
     # the training path (autograd): the shared-latent gradient dk + dv in one output
@@ -330,7 +353,7 @@ def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense")):
         return _sfa_grad(q, k, k, si, do, o, smax, ssum, scale, qr, kr, None, None, 1, "BSND", 3, INT64_MAX,
                          INT64_MAX, False, merge_kv=True)
     if "bwd_merged" in legs:
-        ms = time_call(bwd_merged, steps, 1)
+        ms = time_call(bwd_merged, steps, 2)
         out["sfa_bwd_merged"] = leg("SFA bwd TFLOP/s (training path, d_key = dk + dv)",
                                   "sfa_bwd as called by the autograd Function (MLA absorb: one key gradient dk + dv): "
                                   "BSND B=1, S1=S2=4096, N1=128, D=512+64, topK=2048 causal, sparse_mode 3, bf16",
@@ -343,17 +366,12 @@ def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense")):
         return dsa.sparse_lightning_indexer_grad_kl_loss_triton(q, k, qi, ki, w, si, smax, ssum, query_rope=qr,
                                                                 key_rope=kr, scale_value=scale)
     if "kl" in legs:
-        ms = time_call(kl, steps, 1)
-    # HBM-bound: every valid (row, slot) pair gathers a K, K_rope and
-    # K_index row; per row Q, Q_rope, Qi, weights, indices, statistics and
-    # dQi, dW; per key row dKi
-    kl_bytes = (n * (D + DR + DI) * 2 + S * (N1 * (D + DR) * 2 + NI * DI * 2 * 2 + NI * 4 * 2 + K * 4 + N1 * 8)
-                + S * DI * 2)
+        ms = time_call(kl, steps, 2)
     if "kl" in legs:
         out["kl_bwd"] = leg("indexer KL-loss bwd TFLOP/s",
                           "sparse_lightning_indexer_grad_kl_loss: B=1, S1=S2=4096, N1=128, D=512+64, Nidx1=64, "
                           "D_idx=128, topK=2048 causal, bf16 (fp32 weights), stats from the SFA forward",
-                          n * (3 * 2 * NI * DI + 2 * N1 * (D + DR) + 2 * NI), ms, n, hbm_bytes=kl_bytes)
+                          n * (3 * 2 * NI * DI + 2 * N1 * (D + DR) + 2 * NI), ms, n)
     del si, o, do
     torch.cuda.empty_cache()
     # dense warm-up stage at the same shape: every causal key, teacher stats of
@@ -365,7 +383,7 @@ def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense")):
     def dense():
         return dsa.dense_loss_backward_triton(q, k, qi, ki, w, dsmax, dssum, scale_value=scale, query_rope=qr,
                                               key_rope=kr)
-    ms = time_call(dense, steps, 1)
+    ms = time_call(dense, steps, 2)
     nd = S * (S + 1) // 2
     out["dense_kl_bwd"] = leg("dense indexer KL-loss bwd TFLOP/s",
                               "dense_loss_backward (warm-up stage, index LSE computed inside): B=1, S1=S2=4096, "
@@ -415,7 +433,7 @@ def main():
     torch.cuda.set_device(dev)
     sets = make_decode_sets(args.sets, dev)
     torch.cuda.synchronize()
-    ms, per = time_decode(sets, args.steps, args.warmup)
+    ms, per, graph_ms = time_decode(sets, args.steps, args.warmup)
     n_valid = B * K
     flops, nbytes = decode_algorithmic(n_valid)
     tflops = flops / (ms * 1e-3) / 1e12
@@ -441,6 +459,8 @@ def main():
         "pct_of_attainable_roofline": round(100.0 * tflops / attainable, 2),
         "per_step_ms": {"median": round(per[len(per) // 2], 5), "p20": round(per[len(per) // 5], 5),
                         "p80": round(per[4 * len(per) // 5], 5)},
+        "hip_graph": {"ms_per_step": round(graph_ms, 5), "value": round(flops / (graph_ms * 1e-3) / 1e12, 2),
+                      "note": "the step captured once in a HIP graph and replayed K times (input set 0)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                      "traffic": measured_traffic(),

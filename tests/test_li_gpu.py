@@ -235,10 +235,11 @@ def test_indexer_cfg2_sampled_rows():
     _full_case(2, 4096, 4096, 64, 1, 128, 2048, 3, torch.bfloat16, rows=rows)
 
 
-def test_indexer_decode_32k_sampled_rows():
-    """Decode at 32K context (S1=1, S2=32768, N1=64, D=128, k=2048, mode 3), B=4."""
-    print("[li full] decode 32k", flush=True)
-    _full_case(4, 1, 32768, 64, 1, 128, 2048, 3, torch.bfloat16)
+def test_indexer_decode_32k_bench_batch():
+    """Decode at 32K context with the bench batch (B=32, S1=1, S2=32768,
+    N1=64, D=128, k=2048, mode 3): every row against the oracle."""
+    print("[li full] decode 32k, B=32", flush=True)
+    _full_case(32, 1, 32768, 64, 1, 128, 2048, 3, torch.bfloat16)
 
 
 def test_indexer_tnd_matches_bsnd():
