@@ -28,6 +28,7 @@ LAYOUT = {"BSND": 0, "TND": 1, "PA_BSND": 2}
 TEST_FORCE_GLOBAL_GATHER = 1
 TEST_SMALL_BWD_CHUNKS = 2
 TEST_KL_GENERIC = 4
+TEST_FWD_WIDE = 8
 
 _c = ctypes
 _vp = _c.c_void_p

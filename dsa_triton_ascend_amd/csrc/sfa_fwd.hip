@@ -364,7 +364,6 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
 #pragma unroll
     for (int j = 0; j < NDMA; ++j) dma_issue(j, ph[j], b);
   };
-
   // Barrier sequence, identical for every wave: per tile one barrier, then
   // one vote barrier, and (only if the vote is set) a second pass of tiles.
   // Tile t is waited for (vmcnt) before its barrier and tile t+2 is issued
@@ -758,6 +757,552 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// D = 512 kernel for launches with token splits (few query rows): 64 heads
+// per workgroup, 8 waves, and the two products divided among the waves in
+// different ways, so that each LDS fragment is read by fewer waves.
+//  * S^T = K . Q^T: wave w takes head tile w % 4 (16 heads) and token half
+//    w / 4 (16 of the tile's 32 tokens): 18 MFMAs per tile, and each K
+//    fragment is read by two waves instead of eight.
+//  * The softmax numerators P^T of the 64 heads go through LDS, 64 bytes per
+//    head (bf16 hi and, for short ranges, lo parts).
+//  * O^T += V^T . P^T: wave w owns columns 64w .. 64w + 63 of all 64 heads
+//    (64 accumulator registers); each V^T fragment is read by one wave and
+//    serves four head tiles.
+//  Per token and head the LDS reads drop by about 25 % against the 128-head
+//  kernel, and the split partials halve (4 splits of 64 heads instead of 8
+//  of 128 at B = 32: 17 instead of 34 MB written and read back).  The price
+//  is a second gather of every KV row, by the row's other head group: both
+//  run on one XCD, so HBM reads stay the same (L2 serves the second), but
+//  each CU's gather path, whose DMA issue is the loop's limiter, carries
+//  twice the bytes.  Net at the decode shape: about 2 us (4 %) faster.
+//  The token halves of a head share one reference max, taken from the first
+//  tile's two half maxima through one LDS exchange.
+// ---------------------------------------------------------------------------
+constexpr int kSfaDsHeads = 64;
+
+template <int D, typename T, bool BUF, bool CH>
+__global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
+  using E = Elem<T>;
+  using V8 = typename E::v8;
+  constexpr bool kSplitP = __is_same(T, bf16);
+  constexpr int NW = 8;
+  constexpr int NTHR = NW * 64;
+  constexpr int HG = kSfaDsHeads;
+  constexpr int HGT = HG / 16;       // head tiles of the workgroup
+  constexpr int DR = 64;
+  constexpr int KS = (D + DR) / 32;  // GEMM1 k-steps
+  constexpr int KSN = D / 32;
+  constexpr int NDW = D / NW / 16;   // GEMM2 d-tiles per wave
+  constexpr int TILE = kSfaTile;
+  constexpr int NOPE_BYTES = TILE * D * 2;
+  constexpr int BUF_BYTES = NOPE_BYTES + TILE * DR * 2;
+  constexpr int NBUF = 3;
+  constexpr int CPT = D / 8;
+  constexpr int TPI = 64 / CPT;
+  constexpr int NI = TILE / TPI / 4;
+  constexpr int ROPE0 = NBUF * NOPE_BYTES;
+  auto nope_off = [](int tk, int b) { return ((tk / TPI) * NBUF + b) * 1024 + (tk % TPI) * (D * 2); };
+  auto rope_off = [](int tk, int b) { return ROPE0 + ((tk >> 3) * NBUF + b) * 1024 + (tk & 7) * (DR * 2); };
+  static_assert(D == 512 && TPI == 1 && NI == 8 && NDW == 4, "D = 512 layout");
+  constexpr int QL = 4;
+  constexpr int KQR = KS - QL;
+  constexpr int PROW = TILE * 2;  // bytes of one head's P^T row
+  constexpr int NP = kSplitP ? 2 : 1;
+
+  __shared__ __attribute__((aligned(16))) unsigned char smem[NBUF * BUF_BYTES];
+  __shared__ int s_list[kSfaMaxList + kSfaTile];
+  __shared__ __attribute__((aligned(16))) unsigned char s_q[HG * QL * 64];
+  // P^T of the tile: row h (64 bytes) holds head h's 32 numerators, token
+  // 16*tt + 4*g + r in slot 8*g + 4*tt + r, 16-byte chunk g stored at
+  // g ^ ((h >> 2) & 3); the lo parts follow the hi parts
+  __shared__ __attribute__((aligned(16))) unsigned char s_p[NP * HG * PROW];
+  __shared__ float s_mx[2][HG];    // token halves' maxima: first tile, then exact
+  __shared__ float s_lsum[2][HG];  // token halves' sums
+  __shared__ float s_mref[HG];
+  __shared__ float s_am[NW][HG];   // max |O| of each wave's columns
+  __shared__ float s_mul[HG];
+  __shared__ int s_wcnt[NW];
+  __shared__ RowInfo s_ri;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+
+  const int hgroups = (p.n1 + HG - 1) / HG;
+  const int bid = blockIdx.x;
+  const int jj = bid >> 3;
+  const int hg = jj % hgroups;
+  const int jr = jj / hgroups;
+  const int64_t row = (int64_t)(bid & 7) * p.rows_per_xcd + jr / p.splits;
+  const int split = jr % p.splits;
+  if (row >= p.rows) return;
+
+  const RowInfo ri = sfa_row_info(p, (int)row);
+  if (tid == 0) s_ri = ri;
+  const int32_t* idx_row = p.idx + row * p.K;
+  const int total_pos = p.K * p.bs;
+  const int p0 = split * p.pos_per_split;
+  const int p1 = min(total_pos, p0 + p.pos_per_split);
+
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const int hq = wave_s & 3;   // GEMM1 head tile
+  const int th = wave_s >> 2;  // GEMM1 token half
+  const int head1 = hg * HG + hq * 16;
+
+  // ---- Q fragments of the GEMM1 head tile (both token halves hold them) ----
+  V8 qf[KQR];
+  u32x4 qlv[QL];
+  const u32x4 z4 = {0u, 0u, 0u, 0u};
+  auto q_chunk = [&](int64_t hsafe, int ks) -> u32x4 {
+    if (ks < KSN) return *(const u32x4*)((const T*)p.q + hsafe * D + ks * 32 + lg * 8);
+    return *(const u32x4*)((const T*)p.qr + hsafe * DR + (ks - KSN) * 32 + lg * 8);
+  };
+  auto load_q = [&]() {
+    const int head = head1 + li;
+    const bool hv = head < p.n1;
+    const int64_t hsafe = row * p.n1 + (hv ? head : 0);
+    if (th == 0) {
+#pragma unroll
+      for (int m = 0; m < QL; ++m) qlv[m] = hv ? q_chunk(hsafe, KQR + m) : z4;
+    }
+#pragma unroll
+    for (int ks = 0; ks < KQR; ++ks) qf[ks] = as_v8<V8>(hv ? q_chunk(hsafe, ks) : z4);
+  };
+  const bool q_early = (int64_t)wave * 64 >= (int64_t)(p1 - p0);
+  if (q_early) load_q();
+
+  // ---- compaction of the split's positions (as in sfa_fwd_kernel) ----
+  const int n_chunks = p1 > p0 ? (CH ? (p1 - p0 + kSfaMaxList - 1) / kSfaMaxList : 1) : 0;
+  const int first_id = p0 + tid < p1 ? sfa_load_id(p, idx_row, p0 + tid) : -1;
+  const int32_t* tab = nullptr;
+  if (p.layout_kv == DSA_LAYOUT_PA_BSND) {
+    const int32_t* gtab = p.block_table + (int64_t)ri.b * p.max_blocks;
+    tab = gtab;
+    if ((p1 - p0) + p.max_blocks <= kSfaMaxList) {
+      int* s_tab = s_list + (kSfaMaxList + TILE - p.max_blocks);
+      const int nct = min(NTHR, ((p1 - p0 + 63) / 64) * 64);
+      if (tid < nct)
+        for (int i = tid; i < p.max_blocks; i += nct) s_tab[i] = gtab[i];
+      lds_barrier();
+      tab = s_tab;
+    }
+  }
+  int n_valid = 0, n_tiles = 0;
+  auto compact_range = [&](int cb, int ce, const RowInfo& rc, const int32_t* irow, const int32_t* tb,
+                           bool first) {
+    n_valid = 0;
+    for (int c0 = cb; c0 < ce; c0 += NTHR) {
+      int pos = c0 + tid;
+      int phys = 0;
+      bool valid = false;
+      const int id = (first && c0 == cb) ? first_id : (pos < ce ? sfa_load_id(p, irow, pos) : -1);
+      if (rc.active && pos < ce) valid = sfa_resolve_id(p, rc, id, pos, &phys, tb);
+      unsigned long long m = __ballot(valid);
+      if (lane == 0) s_wcnt[wave] = __popcll(m);
+      lds_barrier();
+      int off = n_valid;
+      int tot = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const int cw = s_wcnt[w];
+        off += (w < wave) ? cw : 0;
+        tot += cw;
+      }
+      if (valid) s_list[off + __popcll(m & ((1ull << lane) - 1ull))] = phys;
+      n_valid += tot;
+      lds_barrier();
+    }
+    if (tid < TILE) s_list[n_valid + tid] = -1;
+    lds_barrier();
+    n_tiles = (n_valid + TILE - 1) / TILE;
+  };
+  auto compact = [&](int c) {
+    if (c == 0) {
+      compact_range(p0, min(p1, p0 + kSfaMaxList), ri, idx_row, tab, true);
+      return;
+    }
+    int bl = blockIdx.x;
+    asm volatile("" : "+s"(bl));
+    const int jr2 = (bl >> 3) / hgroups;
+    const int64_t row2 = (int64_t)(bl & 7) * p.rows_per_xcd + jr2 / p.splits;
+    const int q0 = (jr2 % p.splits) * p.pos_per_split;
+    const int q1 = min(p.K * p.bs, q0 + p.pos_per_split);
+    const RowInfo rc = s_ri;
+    const int32_t* tb = p.layout_kv == DSA_LAYOUT_PA_BSND ? p.block_table + (int64_t)rc.b * p.max_blocks : nullptr;
+    const int cb = q0 + c * kSfaMaxList;
+    compact_range(cb, min(q1, cb + kSfaMaxList), rc, p.idx + row2 * p.K, tb, false);
+  };
+  if (n_chunks > 0) compact(0);
+
+  // ---- tile gather by LDS-DMA, spread over all eight waves ----
+  // Nope DMA j < NIW of wave w loads the 1 KB row of token j*8 + w; waves
+  // 0..3 also load the rope rows of tokens 8w .. 8w+7 (one DMA).  An LDS-DMA
+  // of 1 KB occupies the CU's address unit for about 16 cycles, and a wave
+  // that issues into a full queue stalls: issued by four waves, the tile's 36
+  // DMAs held those waves back in every tile.
+  constexpr int NIW = TILE / NW;
+  const unsigned smem_base = (unsigned)(uintptr_t)smem;
+  const bool rope_wave = wave_s < 4;
+  __amdgpu_buffer_rsrc_t rsrc_k, rsrc_r;
+  if constexpr (BUF) {
+    rsrc_k = __builtin_amdgcn_make_buffer_rsrc((void*)p.k, (short)0, (int)(p.kv_rows * D * 2), 0x00020000);
+    rsrc_r = __builtin_amdgcn_make_buffer_rsrc((void*)p.kr, (short)0, (int)(p.kv_rows * DR * 2), 0x00020000);
+  }
+  constexpr int NDMA = NIW + 1;  // DMA slots per wave (the last one: rope, waves 0..3)
+  auto dma_phys = [&](int t, bool live, int j) -> int {
+    int v;
+    if (j < NIW) v = __builtin_amdgcn_readfirstlane(s_list[t * TILE + j * NW + wave_s]);
+    else v = rope_wave ? s_list[t * TILE + wave_s * 8 + (lane >> 3)] : -1;
+    return live ? v : -1;
+  };
+  auto dma_issue = [&](int j, int phys, int b) {
+    if (j < NIW) {
+      const int tk = j * NW + wave_s;
+      const int ch = lane ^ nope_swz(tk);
+      const unsigned dst = smem_base + nope_off(tk, b);
+      if constexpr (BUF) {
+        dma_buf16(dst, phys >= 0 ? phys * (D * 2) + ch * 16 : (int)0x80000000, rsrc_k);
+      } else {
+        const void* src = phys >= 0 ? (const void*)((const unsigned char*)p.k + (int64_t)phys * (D * 2) + ch * 16)
+                                    : (const void*)(g_sfa_zero_row + ch * 16);
+        dma_glb16(dst, src);
+      }
+    } else if (rope_wave) {
+      const int tk = wave_s * 8 + (lane >> 3);
+      const int ch = (lane & 7) ^ rope_swz(tk);
+      const unsigned dst = smem_base + rope_off(wave_s * 8, b);
+      if constexpr (BUF) {
+        dma_buf16(dst, phys >= 0 ? phys * (DR * 2) + ch * 16 : (int)0x80000000, rsrc_r);
+      } else {
+        const void* src = phys >= 0 ? (const void*)((const unsigned char*)p.kr + (int64_t)phys * (DR * 2) + ch * 16)
+                                    : (const void*)(g_sfa_zero_row + ch * 16);
+        dma_glb16(dst, src);
+      }
+    }
+  };
+  auto issue_tile = [&](int t, int b) {
+    int ph[NDMA];
+#pragma unroll
+    for (int j = 0; j < NDMA; ++j) ph[j] = dma_phys(t, true, j);
+#pragma unroll
+    for (int j = 0; j < NDMA; ++j) dma_issue(j, ph[j], b);
+  };
+  auto gather_loop_prologue = [&]() {
+    if (n_tiles > 0) issue_tile(0, 0);
+    if (n_tiles > 1) issue_tile(1, 1);
+  };
+  // a wave's DMAs of tile t+1 are its last NIW (+1) loads
+  auto tile_sync = [&](int t) {
+    if (t + 1 >= n_tiles) wait_vmcnt<0>();
+    else if (rope_wave) wait_vmcnt<NIW + 1>();
+    else wait_vmcnt<NIW>();
+    lds_barrier();
+  };
+  auto next_buf = [](int b) { return b == 0 ? NBUF - 1 : b - 1; };
+  gather_loop_prologue();
+
+  if (!q_early) load_q();
+  auto ql_base = [&](int ln) {
+    const int l = ln & 15, g = ln >> 4;
+    return (hq * 16 + l) * (QL * 64) + ((g ^ nope_swz(l)) * 16);
+  };
+  if (th == 0) {
+    const int qb = ql_base(lane);
+#pragma unroll
+    for (int m = 0; m < QL; ++m) *(u32x4*)(s_q + (qb ^ (m << 6))) = qlv[m];
+  }
+
+  f32x4 acc_o[NDW][HGT];
+  // reference max (log2 units) shared by the token halves, fixed by the
+  // first tile; exact max of this half; lane-partial sum of 2^(s - m_ref)
+  float m_ref = -INFINITY, m_true = -INFINITY, l_run = 0.f;
+  bool overflow = false;
+  bool need_ref = true;
+
+  auto fresh_lane = []() {
+    int ln = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    asm volatile("" : "+v"(ln));
+    return ln;
+  };
+  auto g1_base = [&](int ln) { const int l = ln & 15, g = ln >> 4; return nope_off(l, 0) + ((g ^ nope_swz(l)) * 16); };
+  auto g1r_base = [&](int ln) { const int l = ln & 15, g = ln >> 4; return rope_off(l, 0) + ((g ^ rope_swz(l)) * 16); };
+  constexpr int G1_TT = nope_off(16, 0) - nope_off(0, 0);
+  constexpr int G1R_TT = rope_off(16, 0) - rope_off(0, 0);
+  auto g2_base = [&](int ln) {
+    const int l = ln & 15, g = ln >> 4;
+    const int r1 = g * 4 + (l >> 2);
+    const int h = (l & 3) >> 1;
+    return nope_off(r1, 0) + ((h ^ nope_swz(r1)) * 16) + (l & 1) * 8;
+  };
+  constexpr int G2_ROW16 = (16 / TPI) * NBUF * 1024;
+  // P^T chunk of lane ln in head tile 0 (B operand of GEMM2)
+  auto p_base = [&](int ln) {
+    const int l = ln & 15, g = ln >> 4;
+    return l * PROW + ((g ^ ((l >> 2) & 3)) * 16);
+  };
+  auto a1 = [&](int g1b, int g1rb, int b, int ks) -> u32x4 {
+    if (ks < KSN) return *(const u32x4*)(smem + ((g1b ^ ((ks & 3) << 6)) + th * G1_TT + b * 1024 + (ks >> 2) * 256));
+    return *(const u32x4*)(smem + ((g1rb ^ ((ks - KSN) << 6)) + th * G1R_TT + b * 1024));
+  };
+  auto a2 = [&](int g2b, int b, int dt) -> V8 {
+    const unsigned char* pp = smem + ((g2b ^ ((dt & 7) << 5)) + b * 1024 + (dt >> 3) * 256);
+    const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)pp);
+    const bf16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(pp + G2_ROW16));
+    const i16x4 w1 = __builtin_bit_cast(i16x4, v1);
+    const i16x4 w2 = __builtin_bit_cast(i16x4, v2);
+    const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
+    return __builtin_bit_cast(V8, w);
+  };
+  auto dma_plan = [&](int tn, int (&dph)[NDMA]) {
+    const bool live = tn < n_tiles;
+#pragma unroll
+    for (int j = 0; j < NDMA; ++j) dph[j] = dma_phys(live ? tn : 0, live, j);
+  };
+
+  // ---- GEMM1: S^T [16 tokens x 16 heads] of this wave's half and head tile ----
+  // two accumulators (even / odd k-steps) so consecutive MFMAs are
+  // independent; no scheduling barriers (the compiler's interleaving of the
+  // fragment reads measured faster here than the fixed prefetch order)
+  auto gemm1 = [&](int b, f32x4& s_out) {
+    const int ln = fresh_lane();
+    const int g1b = g1_base(ln), g1rb = g1r_base(ln), qlb = ql_base(ln);
+    V8 ql[QL];
+    auto ql_read = [&](int m) { ql[m] = as_v8<V8>(*(const u32x4*)(s_q + (qlb ^ (m << 6)))); };
+    constexpr int PF = 6;
+    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    u32x4 fa[PF];
+#pragma unroll
+    for (int i = 0; i < PF; ++i) fa[i] = a1(g1b, g1rb, b, i);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 2 >= KQR && ks + 2 < KS) ql_read(ks + 2 - KQR);
+      const V8 av = as_v8<V8>(fa[ks % PF]);
+      if (ks + PF < KS) fa[ks % PF] = a1(g1b, g1rb, b, ks + PF);
+      acc[ks & 1] = E::mfma(av, ks < KQR ? qf[ks < KQR ? ks : 0] : ql[ks < KQR ? 0 : ks - KQR], acc[ks & 1]);
+    }
+    s_out = acc[0] + acc[1];
+  };
+
+  // ---- softmax numerators of this wave's 16 tokens x 16 heads -> s_p ----
+  const int pw_off = (hq * 16 + li) * PROW + ((lg ^ ((li >> 2) & 3)) * 16) + th * 8;
+  auto softmax_p = [&](int t, const f32x4& s, auto with_lo) {
+    constexpr bool kLo = kSplitP && decltype(with_lo)::value;
+    float v[4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tok = t * TILE + th * 16 + lg * 4 + r;
+      const float x = tok < n_valid ? s[r] * p.scale_log2 : -INFINITY;
+      v[r] = x;
+      tmax = fmaxf(tmax, x);
+    }
+    tmax = xgroup_max(tmax);
+    m_true = fmaxf(m_true, tmax);
+    if (need_ref) {
+      // the first tile of the pass: both halves take the max of the two
+      if (lg == 0) s_mx[th][hq * 16 + li] = tmax;
+      lds_barrier();
+      m_ref = fmaxf(s_mx[0][hq * 16 + li], s_mx[1][hq * 16 + li]);
+      // no finite score in the first tile (non-finite inputs): the first
+      // pass contributes nothing and the row is redone with the exact max
+      overflow |= m_ref == -INFINITY;
+      need_ref = false;
+    }
+    overflow |= tmax > m_ref + kRefSlack;
+    typedef T T4 __attribute__((ext_vector_type(4)));
+    T4 hi, lo;
+    float lsum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float e = m_ref == -INFINITY ? 0.f : fast_exp2(v[r] - m_ref);
+      lsum += e;
+      hi[r] = E::from_f32(e);
+      lo[r] = E::from_f32(e - E::to_f32(hi[r]));
+    }
+    l_run += lsum;
+    *(T4*)(s_p + pw_off) = hi;
+    if constexpr (kLo) *(T4*)(s_p + HG * PROW + pw_off) = lo;
+  };
+
+  // ---- GEMM2: O^T [64 columns x 64 heads] += V^T . P^T ----
+  // This wave's DMAs of tile tn (into buffer bn) go out between the MFMAs:
+  // every wave stalls on its DMA issue for a while (the CU's gather path is
+  // shared), and here the other wave of the SIMD has MFMAs to run meanwhile.
+  auto gemm2 = [&](int b, auto with_lo, int tn, int bn) {
+    constexpr bool kLo = kSplitP && decltype(with_lo)::value;
+    int dph[NDMA];
+    dma_plan(tn, dph);
+    const int ln = fresh_lane();
+    const int g2b = g2_base(ln), pb = p_base(ln);
+    V8 va[NDW];
+#pragma unroll
+    for (int j = 0; j < NDW; ++j) va[j] = a2(g2b, b, wave_s * NDW + j);
+    V8 ph[HGT], pl[HGT];
+#pragma unroll
+    for (int ht = 0; ht < HGT; ++ht) {
+      ph[ht] = as_v8<V8>(*(const u32x4*)(s_p + pb + ht * 16 * PROW));
+      if constexpr (kLo) pl[ht] = as_v8<V8>(*(const u32x4*)(s_p + HG * PROW + pb + ht * 16 * PROW));
+    }
+#pragma unroll
+    for (int ht = 0; ht < HGT; ++ht)
+#pragma unroll
+      for (int j = 0; j < NDW; ++j) {
+        acc_o[j][ht] = E::mfma(va[j], ph[ht], acc_o[j][ht]);
+        if constexpr (kLo) acc_o[j][ht] = E::mfma(va[j], pl[ht], acc_o[j][ht]);
+        constexpr int kStep = HGT * NDW / NDMA;
+        const int st = ht * NDW + j;
+        if (st % kStep == 0 && st / kStep < NDMA) dma_issue(st / kStep, dph[st / kStep], bn);
+      }
+  };
+
+  // Tile t: wait for its loads, barrier, GEMM1, softmax numerators to LDS,
+  // barrier, GEMM2 (with the DMAs of tile t+2 into the buffer tile t-1
+  // used).  The next tile's first barrier orders the P^T reads before the
+  // next writes.
+  auto run_tiles = [&](bool prologue, auto with_lo) {
+    if (prologue) gather_loop_prologue();
+    for (int t0 = 0; t0 < n_tiles; t0 += NBUF)
+#pragma unroll
+      for (int b = 0; b < NBUF; ++b) {
+        const int t = t0 + b;
+        if (t >= n_tiles) break;
+        tile_sync(t);
+        f32x4 sc;
+        gemm1(b, sc);
+        softmax_p(t, sc, with_lo);
+        lds_barrier();
+        gemm2(b, with_lo, t + 2, next_buf(b));
+      }
+    wait_vmcnt<0>();
+  };
+  using LoOn = std::integral_constant<bool, true>;
+  using LoOff = std::integral_constant<bool, false>;
+
+#pragma unroll
+  for (int j = 0; j < NDW; ++j)
+#pragma unroll
+    for (int ht = 0; ht < HGT; ++ht) acc_o[j][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < (CH && n_chunks > 0 ? n_chunks : 1); ++c) {
+    if (CH && c > 0) compact(c);
+    if (kSplitP && n_valid >= kLoSplitMinTokens) run_tiles(c > 0, LoOff{});
+    else run_tiles(c > 0, LoOn{});
+  }
+  // exact maxima of the two halves; the vote barrier orders them
+  if (lg == 0) s_mx[th][hq * 16 + li] = m_true;
+  if (__syncthreads_or(overflow ? 1 : 0)) {
+    m_ref = fmaxf(s_mx[0][hq * 16 + li], s_mx[1][hq * 16 + li]);
+    l_run = 0.f;
+    need_ref = false;
+#pragma unroll
+    for (int j = 0; j < NDW; ++j)
+#pragma unroll
+      for (int ht = 0; ht < HGT; ++ht) acc_o[j][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < (CH && n_chunks > 0 ? n_chunks : 1); ++c) {
+      if (CH && n_chunks > 1) compact(c);
+      run_tiles(true, LoOn{});
+    }
+  }
+
+  // ---- epilogue ----
+  // per head: total sum (two halves), statistics, and for split partials
+  // the fp16 scale 2^ex >= max |O / l| over all columns (eight waves)
+  {
+    const float lw = xgroup_sum(l_run);
+    if (lg == 0) {
+      s_lsum[th][hq * 16 + li] = lw;
+      if (th == 0) s_mref[hq * 16 + li] = m_ref;
+    }
+    if (p.splits > 1) {
+#pragma unroll
+      for (int ht = 0; ht < HGT; ++ht) {
+        float a = 0.f;
+#pragma unroll
+        for (int j = 0; j < NDW; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) a = fmaxf(a, fabsf(acc_o[j][ht][r]));
+        a = xgroup_max(a);
+        if (lg == 0) s_am[wave][ht * 16 + li] = a;
+      }
+    }
+  }
+  lds_barrier();
+  if (tid < HG) {
+    const int h = tid;
+    const int head = hg * HG + h;
+    const float l_tot = s_lsum[0][h] + s_lsum[1][h];
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    const float mt = fmaxf(s_mx[0][h], s_mx[1][h]);
+    const float mr = s_mref[h];
+    int ex = 0;
+    if (p.splits > 1) {
+      float a = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) a = fmaxf(a, s_am[w][h]);
+      a *= inv;
+      if (a > 0.f) (void)frexpf(a, &ex);
+    }
+    s_mul[h] = ldexpf(inv, -ex);
+    if (head < p.n1) {
+      const int64_t orow = row * p.n1 + head;
+      if (p.splits == 1) {
+        if (p.return_lse) {
+          const bool any = l_tot > 0.f;
+          p.smax[orow] = any ? mt * kLn2 : 0.f;
+          p.ssum[orow] = any ? l_tot * fast_exp2(mr - mt) : 0.f;
+        }
+      } else {
+        const int64_t prow = (int64_t)split * p.rows * p.n1 + orow;
+        const f32x4 ml = {mr, l_tot, mt, ldexpf(1.f, ex)};
+        *(f32x4*)(p.part_ml + prow * 4) = ml;
+      }
+    }
+  }
+  lds_barrier();
+  // O rows staged in the (idle) tile ring as [head][D] in the output type
+  // (or fp16 partials), then stored as whole rows, 16 bytes per lane
+  constexpr int SROW = D * 2 + 16;
+  static_assert(HG * SROW <= NBUF * BUF_BYTES, "epilogue staging");
+  typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
+  typedef T T4o __attribute__((ext_vector_type(4)));
+  const bool to_out = p.splits == 1;
+#pragma unroll
+  for (int ht = 0; ht < HGT; ++ht) {
+    const float mul = s_mul[ht * 16 + li];
+#pragma unroll
+    for (int j = 0; j < NDW; ++j) {
+      const f32x4 v = acc_o[j][ht] * mul;
+      u16x4 w;
+      if (to_out) {
+        const T4o o = {E::from_f32(v[0]), E::from_f32(v[1]), E::from_f32(v[2]), E::from_f32(v[3])};
+        w = __builtin_bit_cast(u16x4, o);
+      } else {
+        const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+        w = __builtin_bit_cast(u16x4, o);
+      }
+      *(u16x4*)(smem + (ht * 16 + li) * SROW + (wave * (NDW * 16) + j * 16 + lg * 4) * 2) = w;
+    }
+  }
+  lds_barrier();
+  constexpr int CPR = D * 2 / 16;
+  static_assert(HG * CPR % NTHR == 0, "store loop");
+#pragma unroll
+  for (int i = 0; i < HG * CPR / NTHR; ++i) {
+    const int c = i * NTHR + tid;
+    const int r = c / CPR, col = c % CPR;
+    const u32x4 val = *(const u32x4*)(smem + r * SROW + col * 16);
+    const int head = hg * HG + r;
+    if (head < p.n1) {
+      const int64_t orow = row * p.n1 + head;
+      unsigned char* dst = to_out ? (unsigned char*)p.out + orow * (D * 2)
+                                  : (unsigned char*)(p.part_o + ((int64_t)split * p.rows * p.n1 + orow) * D);
+      *(u32x4*)(dst + col * 16) = val;
+    }
+  }
+}
+
 // Merge per-split partials: one wave per (row, head).  Partial i holds
 // O_i / l_i (as scale_i * stored value), l_i relative to its reference max
 // r_i, and its exact max t_i (log2 units); the merged output is
@@ -892,9 +1437,13 @@ constexpr int kSfaHeadsPerWg = 128;
 // workspace is below (cus + units) <= 1.5 * cus partial rows of N1 heads
 // (about 51 MB at 256 CUs, N1 = 128, D = 512).  The workspace query and the
 // launch use the same count.
-static int sfa_fwd_plan_splits(int64_t rows, int64_t n1, int64_t total_pos) {
+//
+// Heads per workgroup: D = 512 launches that split tokens with 64-head
+// workgroups run sfa_fwd_ds_kernel (64 heads); everything else runs
+// sfa_fwd_kernel with 128 heads, which gathers each KV row once per row.
+static int sfa_fwd_plan_splits(int64_t rows, int64_t n1, int64_t total_pos, int heads_per_wg) {
   const int cus = device_cu_count();
-  const int64_t units = rows * ((n1 + kSfaHeadsPerWg - 1) / kSfaHeadsPerWg);
+  const int64_t units = rows * ((n1 + heads_per_wg - 1) / heads_per_wg);
   if (2 * units > cus) return 1;
   const int64_t want = (cus + units - 1) / units;
   const int64_t by_len = (total_pos + 255) / 256;
@@ -948,9 +1497,14 @@ int sfa_fwd_scratch(void** ptr) {
   return DSA_OK;
 }
 
+static int sfa_fwd_heads_per_wg(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
+  if (d == 512 && !(test_flags() & kTestFwdWide) && sfa_fwd_plan_splits(rows, n1, total_pos, kSfaDsHeads) > 1)
+    return kSfaDsHeads;
+  return kSfaHeadsPerWg;
+}
+
 int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
-  (void)d;
-  return sfa_fwd_plan_splits(rows, n1, total_pos);
+  return sfa_fwd_plan_splits(rows, n1, total_pos, sfa_fwd_heads_per_wg(rows, n1, d, total_pos));
 }
 
 size_t sfa_fwd_workspace_bytes(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
@@ -960,16 +1514,29 @@ size_t sfa_fwd_workspace_bytes(int64_t rows, int64_t n1, int64_t d, int64_t tota
 }
 
 template <int D, typename T>
-static hipError_t launch_sfa_fwd(SfaFwdParams& p, hipStream_t stream) {
+static hipError_t launch_sfa_fwd(SfaFwdParams& p, int heads_per_wg, hipStream_t stream) {
   const int64_t rows_per_xcd = (p.rows + 7) / 8;
   p.rows_per_xcd = (int)rows_per_xcd;
-  const int64_t blocks = 8 * rows_per_xcd * p.splits * ((p.n1 + kSfaHeadsPerWg - 1) / kSfaHeadsPerWg);
+  const int64_t blocks = 8 * rows_per_xcd * p.splits * ((p.n1 + heads_per_wg - 1) / heads_per_wg);
   const bool buf = p.kv_rows * (int64_t)D * 2 < (1ll << 31) && !(test_flags() & kTestForceGlobalGather);
   using C = SfaCfg<D>;
   static_assert(C::NW * C::HT * 16 == kSfaHeadsPerWg, "heads per workgroup");
   const bool chunked = p.pos_per_split > kSfaMaxList;
   const dim3 grid((unsigned)blocks), block(C::NW * 64);
-  if (buf && !chunked)
+  if constexpr (D == 512) {
+    if (heads_per_wg == kSfaDsHeads) {
+      if (buf && !chunked)
+        hipLaunchKernelGGL((sfa_fwd_ds_kernel<D, T, true, false>), grid, dim3(512), 0, stream, p);
+      else if (buf)
+        hipLaunchKernelGGL((sfa_fwd_ds_kernel<D, T, true, true>), grid, dim3(512), 0, stream, p);
+      else if (!chunked)
+        hipLaunchKernelGGL((sfa_fwd_ds_kernel<D, T, false, false>), grid, dim3(512), 0, stream, p);
+      else
+        hipLaunchKernelGGL((sfa_fwd_ds_kernel<D, T, false, true>), grid, dim3(512), 0, stream, p);
+    }
+  }
+  if (heads_per_wg == kSfaDsHeads) {
+  } else if (buf && !chunked)
     hipLaunchKernelGGL((sfa_fwd_kernel<D, T, C::HT, C::NW, true, false>), grid, block, 0, stream, p);
   else if (buf)
     hipLaunchKernelGGL((sfa_fwd_kernel<D, T, C::HT, C::NW, true, true>), grid, block, 0, stream, p);
@@ -1021,7 +1588,8 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
   p.max_blocks = (int32_t)max_blocks;
   p.page_size = (int32_t)page_size;
   const int64_t total_pos = sparse_count * (int64_t)sparse_block_size;
-  p.splits = sfa_fwd_plan_splits(q_rows, n1, total_pos);
+  const int hpw = sfa_fwd_heads_per_wg(q_rows, n1, d, total_pos);
+  p.splits = sfa_fwd_plan_splits(q_rows, n1, total_pos, hpw);
   p.pos_per_split = (int32_t)((total_pos + p.splits - 1) / p.splits);
   p.part_o = nullptr;
   p.part_ml = nullptr;
@@ -1034,13 +1602,13 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
   p.rows_per_xcd = 0;
   hipError_t e;
   if (dtype == DSA_DTYPE_BF16) {
-    e = d == 512 ? launch_sfa_fwd<512, bf16>(p, stream)
-      : d == 256 ? launch_sfa_fwd<256, bf16>(p, stream)
-                 : launch_sfa_fwd<128, bf16>(p, stream);
+    e = d == 512 ? launch_sfa_fwd<512, bf16>(p, hpw, stream)
+      : d == 256 ? launch_sfa_fwd<256, bf16>(p, hpw, stream)
+                 : launch_sfa_fwd<128, bf16>(p, hpw, stream);
   } else {
-    e = d == 512 ? launch_sfa_fwd<512, f16>(p, stream)
-      : d == 256 ? launch_sfa_fwd<256, f16>(p, stream)
-                 : launch_sfa_fwd<128, f16>(p, stream);
+    e = d == 512 ? launch_sfa_fwd<512, f16>(p, hpw, stream)
+      : d == 256 ? launch_sfa_fwd<256, f16>(p, hpw, stream)
+                 : launch_sfa_fwd<128, f16>(p, hpw, stream);
   }
   if (e != hipSuccess) return hip_fail(e, "sfa_fwd launch");
   return DSA_OK;

@@ -302,10 +302,10 @@ def test_fwd_repeat_runs_bitwise_identical():
 
 
 # Few rows with long index lists: the token-split path.  At D = 512 it runs
-# the paired 64-head kernel (two waves per 16 heads, P exchanged through
-# LDS, half of D per wave) and the combine kernel; N1 < 64 leaves pairs
-# without heads, short causal rows take the bf16 lo part of P, fp16 the
-# single-part path.
+# the 64-head kernel (S = K.Q^T by head tile and token half, P^T through
+# LDS, O^T by column slice) and the combine kernel; N1 < 64 leaves head
+# tiles without heads, short causal rows take the bf16 lo part of P, fp16
+# the single-part path.
 SPLIT_CASES = [
     # B, S1, S2, N1, K, mode, D
     (1, 2, 4096, 128, 2048, 0, 512),
@@ -326,6 +326,30 @@ def test_fwd_token_split_rows(B, S1, S2, N1, K, mode, D, dtype):
         si[0, 0, 0, K // 3:] = -1   # one short row inside a long batch
     scale = 1.0 / np.sqrt(D + 64)
     out, smax, ssum = _run(q, k, qr, kr, si, dtype, scale, mode)
+    ref = sfa_fwd_bsnd(q, k, si, qr, kr, scale, [S1] * B, [S2] * B, 1, mode, True, "float32",
+                       positions="kernel")
+    assert_close(out, ref[0], RTOL, ATOL, "attention_out")
+    assert_close(smax, ref[1], RTOL, ATOL, "softmax_max")
+    assert_close(ssum, ref[2], RTOL, ATOL, "softmax_sum")
+
+
+@pytest.mark.parametrize("flag", ["TEST_FORCE_GLOBAL_GATHER", "TEST_FWD_WIDE"])
+@pytest.mark.parametrize("B,S1,S2,N1,K,mode,D", [SPLIT_CASES[0], SPLIT_CASES[3]])
+def test_fwd_token_split_variants(B, S1, S2, N1, K, mode, D, flag):
+    """The D = 512 split launch through its other paths: the 64-bit global
+    gather of the 64-head kernel, and the 128-head kernel (test flags)."""
+    from dsa_triton_ascend_amd import _lib
+    print(f"[sfa_fwd split {flag}] B={B} S1={S1} S2={S2} N1={N1} K={K} mode={mode}", flush=True)
+    dtype = torch.bfloat16
+    q, k, qr, kr = sfa_inputs(B, S1, S2, N1, D, dtype, seed=52)
+    si = sparse_indices(B, S1, S2, K, 1, mode, seed=54)
+    scale = 1.0 / np.sqrt(D + 64)
+    lib = _lib.load()
+    lib.dsa_set_test_flags(getattr(_lib, flag))
+    try:
+        out, smax, ssum = _run(q, k, qr, kr, si, dtype, scale, mode)
+    finally:
+        lib.dsa_set_test_flags(0)
     ref = sfa_fwd_bsnd(q, k, si, qr, kr, scale, [S1] * B, [S2] * B, 1, mode, True, "float32",
                        positions="kernel")
     assert_close(out, ref[0], RTOL, ATOL, "attention_out")
