@@ -123,10 +123,11 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   constexpr int NBUF = 3;                    // DMA ring: tiles t+1, t+2 in flight during t
   constexpr int CPT = D / 8;                 // 16-byte chunks per nope row
   constexpr int TPI = 64 / CPT;              // nope tokens per wave-wide DMA (1 KB)
-  // Four waves issue the tile loads (all of them with NW = 4, waves 4..7
-  // with NW = 8): NI nope DMAs (1 KB each) plus one rope DMA (8 tokens x
-  // 128 B) per issuing wave per tile.
-  constexpr int NI = TILE / TPI / 4;
+  // Every wave issues NI nope DMAs (1 KB each) per tile, and waves 0..3
+  // one rope DMA (8 tokens x 128 B) each.  An LDS-DMA holds its wave at
+  // issue while the CU's gather path is busy; spread over all waves, the
+  // SIMD's other wave runs MFMAs meanwhile.
+  constexpr int NI = TILE / TPI / NW;
   constexpr int NTHR = NW * 64;
   // LDS layout: the NBUF tile buffers are interleaved in 1 KB blocks (one
   // DMA each) so that a buffer index only adds a small immediate to a read
@@ -299,32 +300,32 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   // rope: wave w < 4 covers tokens 8w .. 8w+7, lane L -> token 8w + L/8.
   const unsigned smem_base = (unsigned)(uintptr_t)smem;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-  const bool issuer = NW == 4 || wave_s >= 4;
-  const int wiss = wave_s & 3;  // index among the issuing waves
-  // wave-uniform DMA destinations: nope block (j*4 + wiss), rope block wiss
-  const unsigned smem_wave = smem_base + nope_off(wiss * TPI, 0);
+  const bool rope_wave = wave_s < 4;
+  const int wiss = wave_s & 3;  // rope block of waves 0..3
+  // wave-uniform DMA destinations: nope block (j*NW + wave), rope block wiss
+  const unsigned smem_wave = smem_base + nope_off(wave_s * TPI, 0);
   const unsigned smem_rope_wave = smem_base + rope_off(wiss * 8, 0) - rope_off(0, 0);
   __amdgpu_buffer_rsrc_t rsrc_k, rsrc_r;
   if constexpr (BUF) {
     rsrc_k = __builtin_amdgcn_make_buffer_rsrc((void*)p.k, (short)0, (int)(p.kv_rows * D * 2), 0x00020000);
     rsrc_r = __builtin_amdgcn_make_buffer_rsrc((void*)p.kr, (short)0, (int)(p.kv_rows * DR * 2), 0x00020000);
   }
-  // DMA j < NI of an issuing wave loads nope block (j*4 + wiss); DMA NI
-  // loads rope block wiss.  A tile past the end (phys = -1 everywhere) loads
-  // zeros and touches no memory.  With one token per nope DMA (D = 512) the
-  // row id is wave-uniform and kept in a scalar register.
-  constexpr int NDMA = NI + 1;
+  // DMA j < NI of a wave loads nope block (j*NW + wave); DMA NI (waves
+  // 0..3) loads rope block wiss.  A tile past the end (phys = -1
+  // everywhere) loads zeros and touches no memory.  With one token per nope
+  // DMA (D = 512) the row id is wave-uniform and kept in a scalar register.
+  constexpr int NDMA = NI + 1;  // DMA slots per wave (the last: rope, waves 0..3)
   auto dma_phys = [&](int t, bool live, int j) -> int {
-    const int tk = j < NI ? (j * 4 + wiss) * TPI + lane / CPT : wiss * 8 + (lane >> 3);
+    const int tk = j < NI ? (j * NW + wave_s) * TPI + lane / CPT : wiss * 8 + (lane >> 3);
     int v = s_list[t * TILE + tk];  // -1 past n_valid / for -1 pages
     if (TPI == 1 && j < NI) v = __builtin_amdgcn_readfirstlane(v);
-    return live ? v : -1;
+    return live && (j < NI || rope_wave) ? v : -1;
   };
   auto dma_issue = [&](int j, int phys, int b) {
     if (j < NI) {
-      const int tk = (j * 4 + wiss) * TPI + lane / CPT;
+      const int tk = (j * NW + wave_s) * TPI + lane / CPT;
       const int ch = (lane % CPT) ^ nope_swz(tk);
-      const unsigned dst = smem_wave + nope_off(j * 4 * TPI, b);
+      const unsigned dst = smem_wave + nope_off(j * NW * TPI, b);
       if constexpr (BUF) {
         dma_buf16(dst, phys >= 0 ? phys * (D * 2) + ch * 16 : (int)0x80000000, rsrc_k);
       } else {
@@ -332,7 +333,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
                                     : (const void*)(g_sfa_zero_row + ch * 16);
         dma_glb16(dst, src);
       }
-    } else {
+    } else if (rope_wave) {
       const int tk = wiss * 8 + (lane >> 3);
       const int ch = (lane & 7) ^ rope_swz(tk);
       const unsigned dst = smem_rope_wave + rope_off(0, b);
@@ -368,16 +369,16 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   // one vote barrier, and (only if the vote is set) a second pass of tiles.
   // Tile t is waited for (vmcnt) before its barrier and tile t+2 is issued
   // after it, into the buffer tile t-1 used (all waves are past it).  Each
-  // issuing wave issues NDMA loads per tile (zeros past the end), so the
-  // vmcnt counts hold; the other waves have none outstanding.
+  // wave issues its NI (+1) loads per tile (zeros past the end), so the
+  // vmcnt counts hold.
   auto gather_loop_prologue = [&]() {
-    if (!issuer) return;
     if (n_tiles > 0) issue_tile(0, 0);
     if (n_tiles > 1) issue_tile(1, 1);
   };
   auto tile_sync = [&](int t) {
     if (t + 1 >= n_tiles) wait_vmcnt<0>();
-    else wait_vmcnt<NDMA>();
+    else if (rope_wave) wait_vmcnt<NI + 1>();
+    else wait_vmcnt<NI>();
     lds_barrier();
   };
   auto next_buf = [](int b) { return b == 0 ? NBUF - 1 : b - 1; };
@@ -398,7 +399,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
           const int t = t0 + b;
           if (t >= n_tiles) break;
           tile_sync(t);
-          if (issuer) issue_tile_or_zero(t + 2, next_buf(b));
+          issue_tile_or_zero(t + 2, next_buf(b));
         }
       wait_vmcnt<0>();
     };
@@ -515,8 +516,9 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
   };
 
   // ---- GEMM1 of tile t (buffer b): S^T[32 tok x HT*16 heads] ----
-  // With DMA, this wave's loads of tile tn into buffer bn go out one every
-  // four steps, so that the address unit drains while the MFMAs run.
+  // With DMA, this wave's loads of tile tn into buffer bn go out evenly
+  // spaced over the steps, so that the address unit drains while the MFMAs
+  // run.
   auto gemm1 = [&](int t, int b, f32x4 (&acc_s)[2][HT], auto with_dma, int tn, int bn) {
     const int ln = fresh_lane();
     const int g1b = g1_base(ln), g1rb = g1r_base(ln), qlb = ql_base(ln);
@@ -530,7 +532,8 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
     constexpr bool kDma = decltype(with_dma)::value;
     int dph[NDMA];
     if constexpr (kDma) dma_plan(tn, dph);
-    static_assert(2 + 4 * (NDMA - 1) < NS1, "DMA slots inside GEMM1");
+    constexpr int DSTEP = NS1 / NDMA;  // GEMM1 steps per DMA slot
+    static_assert(DSTEP >= 2, "DMA slots inside GEMM1");
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -550,7 +553,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
       for (int ht = 0; ht < HT; ++ht)
         acc_s[tt][ht] = E::mfma(av, ks < KQR ? qf[ht][ks < KQR ? ks : 0] : ql[ht][ks < KQR ? 0 : ks - KQR], acc_s[tt][ht]);
       if constexpr (kDma)
-        if ((st & 3) == 2 && (st >> 2) < NDMA) dma_issue(st >> 2, dph[st >> 2], bn);
+        if (st % DSTEP == 2 && st / DSTEP < NDMA) dma_issue(st / DSTEP, dph[st / DSTEP], bn);
       // keeps the prefetched fragment reads where they are: without it the
       // scheduler sinks each read next to its MFMA to save registers, and
       // every MFMA then waits out a full LDS round trip
@@ -618,11 +621,10 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
     }
   };
 
-  using DmaOff = std::integral_constant<bool, false>;
   using DmaSpread = std::integral_constant<bool, true>;
 
-  // Tile t: wait for its loads, barrier, GEMM1 (the issuing waves load tile
-  // t+2 into the buffer tile t-1 used, one DMA every four steps: every
+  // Tile t: wait for its loads, barrier, GEMM1 (every wave loads its share
+  // of tile t+2 into the buffer tile t-1 used, spaced over the steps: every
   // workgroup runs the same schedule, and bursts would queue at the memory
   // system), softmax, GEMM2.  (A two-group ping-pong schedule, GEMM1 of one
   // group beside softmax + GEMM2 of the other, measured slower here: the
@@ -636,8 +638,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
         if (t >= n_tiles) break;
         tile_sync(t);
         f32x4 sc[2][HT];
-        if (issuer) gemm1(t, b, sc, DmaSpread{}, t + 2, next_buf(b));
-        else gemm1(t, b, sc, DmaOff{}, 0, 0);
+        gemm1(t, b, sc, DmaSpread{}, t + 2, next_buf(b));
         sm_gemm2(t, b, sc, with_lo);
       }
     wait_vmcnt<0>();  // tail loads of tiles past the end
