@@ -1021,12 +1021,14 @@ int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_
   return DSA_OK;
 }
 
-// Keys per workgroup: enough chunks per row that the grid fills every CU
-// with as many workgroups as fit at once, in one round (a partial second
-// round would leave most CUs idle while it runs).
-static hipError_t launch_score_kernel(const void* fn, int occ, LiParams p, hipStream_t stream) {
+// Keys per workgroup: enough chunks per row that the grid puts one
+// workgroup on every CU, in one round.  Two resident workgroups per CU
+// measured slower: they start together, but one streams ahead while the
+// other waits behind it, so the grid ran as two serial rounds with a long
+// tail (decode step 72.5 -> 66.6 us with one per CU).
+static hipError_t launch_score_kernel(const void* fn, LiParams p, hipStream_t stream) {
   const int64_t rows = p.q_rows * p.n2;
-  const int64_t target = (int64_t)device_cu_count() * occ;
+  const int64_t target = (int64_t)device_cu_count();
   const int64_t per_row = rows >= target ? 1 : (target + rows - 1) / rows;
   int64_t chunk = (p.s2 + per_row - 1) / per_row;
   chunk = ((chunk + 63) / 64) * 64;
@@ -1037,20 +1039,9 @@ static hipError_t launch_score_kernel(const void* fn, int occ, LiParams p, hipSt
   return hipLaunchKernel(fn, dim3((unsigned)rows, chunks), dim3(kLiThreads), args, 0, stream);
 }
 
-// Occupancy depends only on the kernel and the architecture (every device
-// this library runs on is gfx950); the local static's initialisation is
-// thread-safe.
-template <typename F>
-static int score_occupancy(F fn) {
-  int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kLiThreads, 0) != hipSuccess || n < 1) n = 1;
-  return n;
-}
-
 template <int D, typename T, int GT, bool PAD>
 static hipError_t launch_score(const LiParams& p, hipStream_t stream) {
-  static const int occ = score_occupancy(li_score_kernel<D, T, GT, PAD>);
-  return launch_score_kernel((const void*)li_score_kernel<D, T, GT, PAD>, occ, p, stream);
+  return launch_score_kernel((const void*)li_score_kernel<D, T, GT, PAD>, p, stream);
 }
 
 template <int D, typename T, bool PAD>
@@ -1063,8 +1054,7 @@ static hipError_t launch_score_g(const LiParams& p, hipStream_t stream) {
 
 template <int D, bool PAD>
 static hipError_t launch_score_f32(const LiParams& p, hipStream_t stream) {
-  static const int occ = score_occupancy(li_score_f32_kernel<D, PAD>);
-  return launch_score_kernel((const void*)li_score_f32_kernel<D, PAD>, occ, p, stream);
+  return launch_score_kernel((const void*)li_score_f32_kernel<D, PAD>, p, stream);
 }
 
 // Head dims 64 / 128 / 256 run exact kernels; any other supported head dim
