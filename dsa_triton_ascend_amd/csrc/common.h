@@ -137,7 +137,7 @@ int device_cu_count();
 constexpr int kTestForceGlobalGather = 1;  // gather with 64-bit addresses even below 2 GiB
 constexpr int kTestSmallBwdChunks = 2;     // backward rows in chunks of a 64 KiB workspace budget
 constexpr int kTestKlGeneric = 4;          // the KL backward takes its generic path at every shape
-constexpr int kTestFwdWide = 8;            // D = 512 split forwards keep the 128-head workgroup
+constexpr int kTestFwdWide = 8;            // D = 512 forwards run sfa_fwd_kernel (no column split)
 int test_flags();
 }  // namespace dsa
 

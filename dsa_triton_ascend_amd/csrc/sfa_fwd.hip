@@ -759,38 +759,43 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// D = 512 kernel for launches with token splits (few query rows): 64 heads
-// per workgroup, 8 waves, and the two products divided among the waves in
+// D = 512 kernel with O^T split by column slice: HG (64 or 128) heads per
+// workgroup, 8 waves, and the two products divided among the waves in
 // different ways, so that each LDS fragment is read by fewer waves.
-//  * S^T = K . Q^T: wave w takes head tile w % 4 (16 heads) and token half
-//    w / 4 (16 of the tile's 32 tokens): 18 MFMAs per tile, and each K
-//    fragment is read by two waves instead of eight.
-//  * The softmax numerators P^T of the 64 heads go through LDS, 64 bytes per
-//    head (bf16 hi and, for short ranges, lo parts).
-//  * O^T += V^T . P^T: wave w owns columns 64w .. 64w + 63 of all 64 heads
-//    (64 accumulator registers); each V^T fragment is read by one wave and
-//    serves four head tiles.
-//  Per token and head the LDS reads drop by about 25 % against the 128-head
-//  kernel, and the split partials halve (4 splits of 64 heads instead of 8
-//  of 128 at B = 32: 17 instead of 34 MB written and read back).  The price
-//  is a second gather of every KV row, by the row's other head group: both
-//  run on one XCD, so HBM reads stay the same (L2 serves the second), but
-//  each CU's gather path, whose DMA issue is the loop's limiter, carries
-//  twice the bytes.  Net at the decode shape: about 2 us (4 %) faster.
-//  The token halves of a head share one reference max, taken from the first
-//  tile's two half maxima through one LDS exchange.
+//  * S^T = K . Q^T: wave w takes head tile w % (HG/16) (16 heads); with 64
+//    heads also token half w / 4 (16 of the tile's 32 tokens, 18 MFMAs per
+//    tile; each K fragment read by two waves instead of eight), with 128
+//    heads all 32 tokens (36 MFMAs, as in sfa_fwd_kernel).
+//  * The softmax numerators P^T of the HG heads go through LDS, 64 bytes
+//    per head (bf16 hi and, for short ranges, lo parts: at 64 heads in a
+//    second buffer, at 128 heads through the same buffer after the hi part).
+//  * O^T += V^T . P^T: wave w owns columns 64w .. 64w + 63 of all HG heads
+//    (HG accumulator registers); each V^T fragment is read by one wave and
+//    serves HG/16 head tiles (sfa_fwd_kernel reads every V^T fragment in
+//    each of its 8 waves).
+// 64 heads is the decode (token-split) configuration: per token and head
+// the LDS reads drop by about 25 % against sfa_fwd_kernel, and the split
+// partials halve (4 splits of 64 heads instead of 8 of 128 at B = 32: 17
+// instead of 34 MB written and read back).  The price is a second gather of
+// every KV row, by the row's other head group: both run on one XCD, so HBM
+// reads stay the same (L2 serves the second), but each CU's gather path,
+// whose DMA issue is the loop's limiter, carries twice the bytes.  The
+// token halves of a head share one reference max, taken from the first
+// tile's two half maxima through one LDS exchange.  128 heads is the
+// configuration of every other D = 512 launch (prefill).
 // ---------------------------------------------------------------------------
 constexpr int kSfaDsHeads = 64;
 
-template <int D, typename T, bool BUF, bool CH>
+template <int D, typename T, int HG, bool BUF, bool CH>
 __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
   using E = Elem<T>;
   using V8 = typename E::v8;
   constexpr bool kSplitP = __is_same(T, bf16);
   constexpr int NW = 8;
   constexpr int NTHR = NW * 64;
-  constexpr int HG = kSfaDsHeads;
   constexpr int HGT = HG / 16;       // head tiles of the workgroup
+  constexpr int TG = NW / HGT;       // token groups of GEMM1 (2 or 1)
+  constexpr int NTT = 2 / TG;        // 16-token sub-tiles per GEMM1 wave
   constexpr int DR = 64;
   constexpr int KS = (D + DR) / 32;  // GEMM1 k-steps
   constexpr int KSN = D / 32;
@@ -805,11 +810,13 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
   constexpr int ROPE0 = NBUF * NOPE_BYTES;
   auto nope_off = [](int tk, int b) { return ((tk / TPI) * NBUF + b) * 1024 + (tk % TPI) * (D * 2); };
   auto rope_off = [](int tk, int b) { return ROPE0 + ((tk >> 3) * NBUF + b) * 1024 + (tk & 7) * (DR * 2); };
-  static_assert(D == 512 && TPI == 1 && NI == 8 && NDW == 4, "D = 512 layout");
+  static_assert(D == 512 && TPI == 1 && NI == 8 && NDW == 4 && (HG == 64 || HG == 128), "D = 512 layout");
   constexpr int QL = 4;
   constexpr int KQR = KS - QL;
   constexpr int PROW = TILE * 2;  // bytes of one head's P^T row
-  constexpr int NP = kSplitP ? 2 : 1;
+  // P buffers: hi and lo at 64 heads; at 128 heads one (the LDS is full),
+  // the lo part goes through it after the hi part
+  constexpr int NPB = (kSplitP && HG == 64) ? 2 : 1;
 
   __shared__ __attribute__((aligned(16))) unsigned char smem[NBUF * BUF_BYTES];
   __shared__ int s_list[kSfaMaxList + kSfaTile];
@@ -817,12 +824,19 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
   // P^T of the tile: row h (64 bytes) holds head h's 32 numerators, token
   // 16*tt + 4*g + r in slot 8*g + 4*tt + r, 16-byte chunk g stored at
   // g ^ ((h >> 2) & 3); the lo parts follow the hi parts
-  __shared__ __attribute__((aligned(16))) unsigned char s_p[NP * HG * PROW];
-  __shared__ float s_mx[2][HG];    // token halves' maxima: first tile, then exact
-  __shared__ float s_lsum[2][HG];  // token halves' sums
-  __shared__ float s_mref[HG];
-  __shared__ float s_am[NW][HG];   // max |O| of each wave's columns
-  __shared__ float s_mul[HG];
+  __shared__ __attribute__((aligned(16))) unsigned char s_p[NPB * HG * PROW];
+  // per-head statistics: token groups' maxima (at 64 heads: first tile,
+  // then exact) and sums, reference maxima, each wave's max |O|, output
+  // scales.  At 128 heads they live in s_p, which is idle after the tiles
+  // (and no maxima are exchanged during them).
+  constexpr int NSTAT = 2 * TG * HG + HG + NW * HG + HG;
+  static_assert(HG == 64 || NSTAT * 4 <= NPB * HG * PROW, "statistics in the P buffer");
+  __shared__ float s_stat_own[HG == 64 ? NSTAT : 1];
+  float* const s_mx = HG == 64 ? s_stat_own : (float*)s_p;  // [TG][HG]
+  float* const s_lsum = s_mx + TG * HG;                      // [TG][HG]
+  float* const s_mref = s_lsum + TG * HG;                    // [HG]
+  float* const s_am = s_mref + HG;                           // [NW][HG]
+  float* const s_mul = s_am + NW * HG;                       // [HG]
   __shared__ int s_wcnt[NW];
   __shared__ RowInfo s_ri;
 
@@ -849,8 +863,8 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
   const int p1 = min(total_pos, p0 + p.pos_per_split);
 
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-  const int hq = wave_s & 3;   // GEMM1 head tile
-  const int th = wave_s >> 2;  // GEMM1 token half
+  const int hq = wave_s % HGT;  // GEMM1 head tile
+  const int th = wave_s / HGT;  // GEMM1 token half (64 heads), 0 (128 heads)
   const int head1 = hg * HG + hq * 16;
 
   // ---- Q fragments of the GEMM1 head tile (both token halves hold them) ----
@@ -1044,9 +1058,9 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
     const int l = ln & 15, g = ln >> 4;
     return l * PROW + ((g ^ ((l >> 2) & 3)) * 16);
   };
-  auto a1 = [&](int g1b, int g1rb, int b, int ks) -> u32x4 {
-    if (ks < KSN) return *(const u32x4*)(smem + ((g1b ^ ((ks & 3) << 6)) + th * G1_TT + b * 1024 + (ks >> 2) * 256));
-    return *(const u32x4*)(smem + ((g1rb ^ ((ks - KSN) << 6)) + th * G1R_TT + b * 1024));
+  auto a1 = [&](int g1b, int g1rb, int b, int ks, int tt) -> u32x4 {
+    if (ks < KSN) return *(const u32x4*)(smem + ((g1b ^ ((ks & 3) << 6)) + tt * G1_TT + b * 1024 + (ks >> 2) * 256));
+    return *(const u32x4*)(smem + ((g1rb ^ ((ks - KSN) << 6)) + tt * G1R_TT + b * 1024));
   };
   auto a2 = [&](int g2b, int b, int dt) -> V8 {
     const unsigned char* pp = smem + ((g2b ^ ((dt & 7) << 5)) + b * 1024 + (dt >> 3) * 256);
@@ -1063,107 +1077,150 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
     for (int j = 0; j < NDMA; ++j) dph[j] = dma_phys(live ? tn : 0, live, j);
   };
 
-  // ---- GEMM1: S^T [16 tokens x 16 heads] of this wave's half and head tile ----
-  // two accumulators (even / odd k-steps) so consecutive MFMAs are
-  // independent; no scheduling barriers (the compiler's interleaving of the
-  // fragment reads measured faster here than the fixed prefetch order)
-  auto gemm1 = [&](int b, f32x4& s_out) {
+  // ---- GEMM1: S^T [16 NTT tokens x 16 heads] of this wave's head tile ----
+  // Two accumulators so consecutive MFMAs are independent: the two token
+  // sub-tiles (128 heads) or even / odd k-steps (64 heads).  Step st is
+  // k-step st / NTT of sub-tile st % NTT.  No scheduling barriers (the
+  // compiler's interleaving of the fragment reads measured faster than the
+  // fixed prefetch order at 64 heads).
+  auto gemm1 = [&](int b, f32x4 (&s_out)[NTT]) {
     const int ln = fresh_lane();
     const int g1b = g1_base(ln), g1rb = g1r_base(ln), qlb = ql_base(ln);
     V8 ql[QL];
     auto ql_read = [&](int m) { ql[m] = as_v8<V8>(*(const u32x4*)(s_q + (qlb ^ (m << 6)))); };
-    constexpr int PF = 6;
+    constexpr int NS = KS * NTT;
+    constexpr int PF = NTT == 1 ? 6 : 4;
+    auto a1s = [&](int st) { return a1(g1b, g1rb, b, st / NTT, NTT == 1 ? th : st % NTT); };
     f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     u32x4 fa[PF];
 #pragma unroll
-    for (int i = 0; i < PF; ++i) fa[i] = a1(g1b, g1rb, b, i);
+    for (int i = 0; i < PF; ++i) fa[i] = a1s(i);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      if (ks + 2 >= KQR && ks + 2 < KS) ql_read(ks + 2 - KQR);
-      const V8 av = as_v8<V8>(fa[ks % PF]);
-      if (ks + PF < KS) fa[ks % PF] = a1(g1b, g1rb, b, ks + PF);
-      acc[ks & 1] = E::mfma(av, ks < KQR ? qf[ks < KQR ? ks : 0] : ql[ks < KQR ? 0 : ks - KQR], acc[ks & 1]);
+    for (int st = 0; st < NS; ++st) {
+      const int ks = st / NTT;
+      if (st % NTT == 0 && ks + 2 >= KQR && ks + 2 < KS) ql_read(ks + 2 - KQR);
+      const V8 av = as_v8<V8>(fa[st % PF]);
+      if (st + PF < NS) fa[st % PF] = a1s(st + PF);
+      acc[st & 1] = E::mfma(av, ks < KQR ? qf[ks < KQR ? ks : 0] : ql[ks < KQR ? 0 : ks - KQR], acc[st & 1]);
+      if constexpr (NTT == 2) __builtin_amdgcn_sched_barrier(0);
     }
-    s_out = acc[0] + acc[1];
+    if constexpr (NTT == 1) s_out[0] = acc[0] + acc[1];
+    else { s_out[0] = acc[0]; s_out[1] = acc[1]; }
   };
 
-  // ---- softmax numerators of this wave's 16 tokens x 16 heads -> s_p ----
-  const int pw_off = (hq * 16 + li) * PROW + ((lg ^ ((li >> 2) & 3)) * 16) + th * 8;
-  auto softmax_p = [&](int t, const f32x4& s, auto with_lo) {
+  // ---- softmax numerators of this wave's 16 NTT tokens x 16 heads -> s_p ----
+  // token 16*tt + 4*lg + r of head 16*hq + li goes to slot 8*lg + 4*tt + r
+  typedef T T4 __attribute__((ext_vector_type(4)));
+  const int pw_off = (hq * 16 + li) * PROW + ((lg ^ ((li >> 2) & 3)) * 16);
+  auto softmax_p = [&](int t, const f32x4 (&s)[NTT], auto with_lo, T4 (&lo_out)[NTT]) {
     constexpr bool kLo = kSplitP && decltype(with_lo)::value;
-    float v[4];
+    float v[NTT][4];
     float tmax = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tok = t * TILE + th * 16 + lg * 4 + r;
-      const float x = tok < n_valid ? s[r] * p.scale_log2 : -INFINITY;
-      v[r] = x;
-      tmax = fmaxf(tmax, x);
-    }
+    for (int u = 0; u < NTT; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tt = NTT == 1 ? th : u;
+        const int tok = t * TILE + tt * 16 + lg * 4 + r;
+        const float x = tok < n_valid ? s[u][r] * p.scale_log2 : -INFINITY;
+        v[u][r] = x;
+        tmax = fmaxf(tmax, x);
+      }
     tmax = xgroup_max(tmax);
     m_true = fmaxf(m_true, tmax);
-    if (need_ref) {
-      // the first tile of the pass: both halves take the max of the two
-      if (lg == 0) s_mx[th][hq * 16 + li] = tmax;
-      lds_barrier();
-      m_ref = fmaxf(s_mx[0][hq * 16 + li], s_mx[1][hq * 16 + li]);
-      // no finite score in the first tile (non-finite inputs): the first
-      // pass contributes nothing and the row is redone with the exact max
-      overflow |= m_ref == -INFINITY;
-      need_ref = false;
+    if constexpr (TG == 2) {
+      if (need_ref) {
+        // the first tile of the pass: both halves take the max of the two
+        if (lg == 0) s_mx[th * HG + hq * 16 + li] = tmax;
+        lds_barrier();
+        m_ref = fmaxf(s_mx[hq * 16 + li], s_mx[HG + hq * 16 + li]);
+        // no finite score in the first tile (non-finite inputs): the first
+        // pass contributes nothing and the row is redone with the exact max
+        overflow |= m_ref == -INFINITY;
+        need_ref = false;
+      }
+    } else {
+      // the wave sees all of its heads' tokens: the reference max is the
+      // first tile's with a visible score
+      if (m_ref == -INFINITY) m_ref = tmax;
     }
     overflow |= tmax > m_ref + kRefSlack;
-    typedef T T4 __attribute__((ext_vector_type(4)));
-    T4 hi, lo;
     float lsum = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float e = m_ref == -INFINITY ? 0.f : fast_exp2(v[r] - m_ref);
-      lsum += e;
-      hi[r] = E::from_f32(e);
-      lo[r] = E::from_f32(e - E::to_f32(hi[r]));
+    for (int u = 0; u < NTT; ++u) {
+      T4 hi, lo;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float e = m_ref == -INFINITY ? 0.f : fast_exp2(v[u][r] - m_ref);
+        lsum += e;
+        hi[r] = E::from_f32(e);
+        lo[r] = E::from_f32(e - E::to_f32(hi[r]));
+      }
+      const int tt = NTT == 1 ? th : u;
+      *(T4*)(s_p + pw_off + tt * 8) = hi;
+      if constexpr (kLo) {
+        if constexpr (NPB == 2) *(T4*)(s_p + HG * PROW + pw_off + tt * 8) = lo;
+        else lo_out[u] = lo;
+      }
     }
     l_run += lsum;
-    *(T4*)(s_p + pw_off) = hi;
-    if constexpr (kLo) *(T4*)(s_p + HG * PROW + pw_off) = lo;
+  };
+  auto write_lo = [&](const T4 (&lo)[NTT]) {
+#pragma unroll
+    for (int u = 0; u < NTT; ++u) *(T4*)(s_p + pw_off + (NTT == 1 ? th : u) * 8) = lo[u];
   };
 
-  // ---- GEMM2: O^T [64 columns x 64 heads] += V^T . P^T ----
-  // This wave's DMAs of tile tn (into buffer bn) go out between the MFMAs:
-  // every wave stalls on its DMA issue for a while (the CU's gather path is
-  // shared), and here the other wave of the SIMD has MFMAs to run meanwhile.
-  auto gemm2 = [&](int b, auto with_lo, int tn, int bn) {
-    constexpr bool kLo = kSplitP && decltype(with_lo)::value;
+  // ---- GEMM2: O^T [64 columns x HG heads] += V^T . P^T ----
+  // With DMA, this wave's DMAs of tile tn (into buffer bn) go out between
+  // the MFMAs: every wave stalls on its DMA issue for a while (the CU's
+  // gather path is shared), and here the other wave of the SIMD has MFMAs
+  // to run meanwhile.  TWO: the lo part of P sits in the second buffer and
+  // is multiplied in the same pass.
+  V8 va[NDW];
+  auto gemm2 = [&](int b, auto two, auto with_dma, int tn, int bn) {
+    constexpr bool kTwo = decltype(two)::value;
+    constexpr bool kDma = decltype(with_dma)::value;
     int dph[NDMA];
-    dma_plan(tn, dph);
+    if constexpr (kDma) dma_plan(tn, dph);
     const int ln = fresh_lane();
-    const int g2b = g2_base(ln), pb = p_base(ln);
-    V8 va[NDW];
+    const int pb = p_base(ln);
+    if constexpr (kDma) {
+      // the hi pass reads the wave's V^T fragments (kept for a lo pass)
+      const int g2b = g2_base(ln);
 #pragma unroll
-    for (int j = 0; j < NDW; ++j) va[j] = a2(g2b, b, wave_s * NDW + j);
-    V8 ph[HGT], pl[HGT];
+      for (int j = 0; j < NDW; ++j) va[j] = a2(g2b, b, wave_s * NDW + j);
+    }
+    auto pread = [&](int ht, int part) { return as_v8<V8>(*(const u32x4*)(s_p + part * HG * PROW + pb + ht * 16 * PROW)); };
+    V8 ph = pread(0, 0), pl = kTwo ? pread(0, 1) : ph;
 #pragma unroll
     for (int ht = 0; ht < HGT; ++ht) {
-      ph[ht] = as_v8<V8>(*(const u32x4*)(s_p + pb + ht * 16 * PROW));
-      if constexpr (kLo) pl[ht] = as_v8<V8>(*(const u32x4*)(s_p + HG * PROW + pb + ht * 16 * PROW));
-    }
-#pragma unroll
-    for (int ht = 0; ht < HGT; ++ht)
+      const V8 ch = ph, cl = pl;
+      if (ht + 1 < HGT) {
+        ph = pread(ht + 1, 0);
+        if constexpr (kTwo) pl = pread(ht + 1, 1);
+      }
 #pragma unroll
       for (int j = 0; j < NDW; ++j) {
-        acc_o[j][ht] = E::mfma(va[j], ph[ht], acc_o[j][ht]);
-        if constexpr (kLo) acc_o[j][ht] = E::mfma(va[j], pl[ht], acc_o[j][ht]);
-        constexpr int kStep = HGT * NDW / NDMA;
-        const int st = ht * NDW + j;
-        if (st % kStep == 0 && st / kStep < NDMA) dma_issue(st / kStep, dph[st / kStep], bn);
+        acc_o[j][ht] = E::mfma(va[j], ch, acc_o[j][ht]);
+        if constexpr (kTwo) acc_o[j][ht] = E::mfma(va[j], cl, acc_o[j][ht]);
+        if constexpr (kDma) {
+          constexpr int kStep = HGT * NDW / NDMA;
+          const int st = ht * NDW + j;
+          if (st % kStep == 0 && st / kStep < NDMA) dma_issue(st / kStep, dph[st / kStep], bn);
+        }
       }
+    }
   };
 
   // Tile t: wait for its loads, barrier, GEMM1, softmax numerators to LDS,
   // barrier, GEMM2 (with the DMAs of tile t+2 into the buffer tile t-1
-  // used).  The next tile's first barrier orders the P^T reads before the
-  // next writes.
+  // used); with one P buffer and the lo part, a barrier, the lo part into
+  // the buffer, a barrier and its GEMM2.  The next tile's first barrier
+  // orders the P^T reads before the next writes.
+  using On = std::integral_constant<bool, true>;
+  using Off = std::integral_constant<bool, false>;
   auto run_tiles = [&](bool prologue, auto with_lo) {
+    constexpr bool kLo = kSplitP && decltype(with_lo)::value;
     if (prologue) gather_loop_prologue();
     for (int t0 = 0; t0 < n_tiles; t0 += NBUF)
 #pragma unroll
@@ -1171,16 +1228,27 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
         const int t = t0 + b;
         if (t >= n_tiles) break;
         tile_sync(t);
-        f32x4 sc;
+        f32x4 sc[NTT];
+        T4 lo[NTT];
         gemm1(b, sc);
-        softmax_p(t, sc, with_lo);
+        softmax_p(t, sc, with_lo, lo);
         lds_barrier();
-        gemm2(b, with_lo, t + 2, next_buf(b));
+        if constexpr (kLo && NPB == 2) {
+          gemm2(b, On{}, On{}, t + 2, next_buf(b));
+        } else {
+          gemm2(b, Off{}, On{}, t + 2, next_buf(b));
+          if constexpr (kLo) {
+            lds_barrier();
+            write_lo(lo);
+            lds_barrier();
+            gemm2(b, Off{}, Off{}, 0, 0);
+          }
+        }
       }
     wait_vmcnt<0>();
   };
-  using LoOn = std::integral_constant<bool, true>;
-  using LoOff = std::integral_constant<bool, false>;
+  using LoOn = On;
+  using LoOff = Off;
 
 #pragma unroll
   for (int j = 0; j < NDW; ++j)
@@ -1191,10 +1259,12 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
     if (kSplitP && n_valid >= kLoSplitMinTokens) run_tiles(c > 0, LoOff{});
     else run_tiles(c > 0, LoOn{});
   }
-  // exact maxima of the two halves; the vote barrier orders them
-  if (lg == 0) s_mx[th][hq * 16 + li] = m_true;
+  // exact maxima of the two halves (64 heads); the vote barrier orders them
+  if constexpr (TG == 2)
+    if (lg == 0) s_mx[th * HG + hq * 16 + li] = m_true;
   if (__syncthreads_or(overflow ? 1 : 0)) {
-    m_ref = fmaxf(s_mx[0][hq * 16 + li], s_mx[1][hq * 16 + li]);
+    if constexpr (TG == 2) m_ref = fmaxf(s_mx[hq * 16 + li], s_mx[HG + hq * 16 + li]);
+    else m_ref = m_true;
     l_run = 0.f;
     need_ref = false;
 #pragma unroll
@@ -1208,13 +1278,16 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
   }
 
   // ---- epilogue ----
-  // per head: total sum (two halves), statistics, and for split partials
-  // the fp16 scale 2^ex >= max |O / l| over all columns (eight waves)
+  // per head: total sum (token groups), statistics, and for split partials
+  // the fp16 scale 2^ex >= max |O / l| over all columns (eight waves).  At
+  // 128 heads the statistics overwrite s_p: every wave is past its last
+  // GEMM2 (the vote barrier above).
   {
     const float lw = xgroup_sum(l_run);
     if (lg == 0) {
-      s_lsum[th][hq * 16 + li] = lw;
+      s_lsum[th * HG + hq * 16 + li] = lw;
       if (th == 0) s_mref[hq * 16 + li] = m_ref;
+      if constexpr (TG == 1) s_mx[hq * 16 + li] = m_true;
     }
     if (p.splits > 1) {
 #pragma unroll
@@ -1225,7 +1298,7 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) a = fmaxf(a, fabsf(acc_o[j][ht][r]));
         a = xgroup_max(a);
-        if (lg == 0) s_am[wave][ht * 16 + li] = a;
+        if (lg == 0) s_am[wave * HG + ht * 16 + li] = a;
       }
     }
   }
@@ -1233,15 +1306,15 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
   if (tid < HG) {
     const int h = tid;
     const int head = hg * HG + h;
-    const float l_tot = s_lsum[0][h] + s_lsum[1][h];
+    const float l_tot = TG == 2 ? s_lsum[h] + s_lsum[HG + h] : s_lsum[h];
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    const float mt = fmaxf(s_mx[0][h], s_mx[1][h]);
+    const float mt = TG == 2 ? fmaxf(s_mx[h], s_mx[HG + h]) : s_mx[h];
     const float mr = s_mref[h];
     int ex = 0;
     if (p.splits > 1) {
       float a = 0.f;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) a = fmaxf(a, s_am[w][h]);
+      for (int w = 0; w < NW; ++w) a = fmaxf(a, s_am[w * HG + h]);
       a *= inv;
       if (a > 0.f) (void)frexpf(a, &ex);
     }
@@ -1263,43 +1336,51 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
   }
   lds_barrier();
   // O rows staged in the (idle) tile ring as [head][D] in the output type
-  // (or fp16 partials), then stored as whole rows, 16 bytes per lane
+  // (or fp16 partials), 64 heads at a time, then stored as whole rows, 16
+  // bytes per lane
   constexpr int SROW = D * 2 + 16;
-  static_assert(HG * SROW <= NBUF * BUF_BYTES, "epilogue staging");
+  constexpr int SH = 64;  // heads per staging round
+  static_assert(SH * SROW <= NBUF * BUF_BYTES, "epilogue staging");
   typedef unsigned short u16x4 __attribute__((ext_vector_type(4)));
-  typedef T T4o __attribute__((ext_vector_type(4)));
   const bool to_out = p.splits == 1;
+  float mulv[HGT];
 #pragma unroll
-  for (int ht = 0; ht < HGT; ++ht) {
-    const float mul = s_mul[ht * 16 + li];
+  for (int ht = 0; ht < HGT; ++ht) mulv[ht] = s_mul[ht * 16 + li];
 #pragma unroll
-    for (int j = 0; j < NDW; ++j) {
-      const f32x4 v = acc_o[j][ht] * mul;
-      u16x4 w;
-      if (to_out) {
-        const T4o o = {E::from_f32(v[0]), E::from_f32(v[1]), E::from_f32(v[2]), E::from_f32(v[3])};
-        w = __builtin_bit_cast(u16x4, o);
-      } else {
-        const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
-        w = __builtin_bit_cast(u16x4, o);
+  for (int hh = 0; hh < HG / SH; ++hh) {
+    if (hh > 0) lds_barrier();  // the previous round's rows are stored
+#pragma unroll
+    for (int hl = 0; hl < SH / 16; ++hl) {
+      const int ht = hh * (SH / 16) + hl;
+#pragma unroll
+      for (int j = 0; j < NDW; ++j) {
+        const f32x4 v = acc_o[j][ht] * mulv[ht];
+        u16x4 w;
+        if (to_out) {
+          const T4 o = {E::from_f32(v[0]), E::from_f32(v[1]), E::from_f32(v[2]), E::from_f32(v[3])};
+          w = __builtin_bit_cast(u16x4, o);
+        } else {
+          const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+          w = __builtin_bit_cast(u16x4, o);
+        }
+        *(u16x4*)(smem + (hl * 16 + li) * SROW + (wave * (NDW * 16) + j * 16 + lg * 4) * 2) = w;
       }
-      *(u16x4*)(smem + (ht * 16 + li) * SROW + (wave * (NDW * 16) + j * 16 + lg * 4) * 2) = w;
     }
-  }
-  lds_barrier();
-  constexpr int CPR = D * 2 / 16;
-  static_assert(HG * CPR % NTHR == 0, "store loop");
+    lds_barrier();
+    constexpr int CPR = D * 2 / 16;
+    static_assert(SH * CPR % NTHR == 0, "store loop");
 #pragma unroll
-  for (int i = 0; i < HG * CPR / NTHR; ++i) {
-    const int c = i * NTHR + tid;
-    const int r = c / CPR, col = c % CPR;
-    const u32x4 val = *(const u32x4*)(smem + r * SROW + col * 16);
-    const int head = hg * HG + r;
-    if (head < p.n1) {
-      const int64_t orow = row * p.n1 + head;
-      unsigned char* dst = to_out ? (unsigned char*)p.out + orow * (D * 2)
-                                  : (unsigned char*)(p.part_o + ((int64_t)split * p.rows * p.n1 + orow) * D);
-      *(u32x4*)(dst + col * 16) = val;
+    for (int i = 0; i < SH * CPR / NTHR; ++i) {
+      const int c = i * NTHR + tid;
+      const int r = c / CPR, col = c % CPR;
+      const u32x4 val = *(const u32x4*)(smem + r * SROW + col * 16);
+      const int head = hg * HG + hh * SH + r;
+      if (head < p.n1) {
+        const int64_t orow = row * p.n1 + head;
+        unsigned char* dst = to_out ? (unsigned char*)p.out + orow * (D * 2)
+                                    : (unsigned char*)(p.part_o + ((int64_t)split * p.rows * p.n1 + orow) * D);
+        *(u32x4*)(dst + col * 16) = val;
+      }
     }
   }
 }
@@ -1439,9 +1520,11 @@ constexpr int kSfaHeadsPerWg = 128;
 // (about 51 MB at 256 CUs, N1 = 128, D = 512).  The workspace query and the
 // launch use the same count.
 //
-// Heads per workgroup: D = 512 launches that split tokens with 64-head
-// workgroups run sfa_fwd_ds_kernel (64 heads); everything else runs
-// sfa_fwd_kernel with 128 heads, which gathers each KV row once per row.
+// Kernel choice: D = 512 launches that split tokens with 64-head workgroups
+// run sfa_fwd_ds_kernel with 64 heads (decode: 44.8 us against 46.6 with
+// 128 heads and twice the splits); other D = 512 launches run it with 128
+// heads (each KV row gathered once per row; prefill 4.64 ms against 4.77
+// for sfa_fwd_kernel); D < 512 runs sfa_fwd_kernel (128 heads).
 static int sfa_fwd_plan_splits(int64_t rows, int64_t n1, int64_t total_pos, int heads_per_wg) {
   const int cus = device_cu_count();
   const int64_t units = rows * ((n1 + heads_per_wg - 1) / heads_per_wg);
@@ -1498,10 +1581,14 @@ int sfa_fwd_scratch(void** ptr) {
   return DSA_OK;
 }
 
+enum SfaFwdKind { kFwdWide, kFwdDs64, kFwdDs128 };
+static SfaFwdKind sfa_fwd_kind(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
+  if (d != 512 || (test_flags() & kTestFwdWide)) return kFwdWide;
+  if (sfa_fwd_plan_splits(rows, n1, total_pos, kSfaDsHeads) > 1) return kFwdDs64;
+  return kFwdDs128;
+}
 static int sfa_fwd_heads_per_wg(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
-  if (d == 512 && !(test_flags() & kTestFwdWide) && sfa_fwd_plan_splits(rows, n1, total_pos, kSfaDsHeads) > 1)
-    return kSfaDsHeads;
-  return kSfaHeadsPerWg;
+  return sfa_fwd_kind(rows, n1, d, total_pos) == kFwdDs64 ? kSfaDsHeads : kSfaHeadsPerWg;
 }
 
 int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
@@ -1515,7 +1602,8 @@ size_t sfa_fwd_workspace_bytes(int64_t rows, int64_t n1, int64_t d, int64_t tota
 }
 
 template <int D, typename T>
-static hipError_t launch_sfa_fwd(SfaFwdParams& p, int heads_per_wg, hipStream_t stream) {
+static hipError_t launch_sfa_fwd(SfaFwdParams& p, SfaFwdKind kind, hipStream_t stream) {
+  const int heads_per_wg = kind == kFwdDs64 ? kSfaDsHeads : kSfaHeadsPerWg;
   const int64_t rows_per_xcd = (p.rows + 7) / 8;
   p.rows_per_xcd = (int)rows_per_xcd;
   const int64_t blocks = 8 * rows_per_xcd * p.splits * ((p.n1 + heads_per_wg - 1) / heads_per_wg);
@@ -1524,19 +1612,23 @@ static hipError_t launch_sfa_fwd(SfaFwdParams& p, int heads_per_wg, hipStream_t 
   static_assert(C::NW * C::HT * 16 == kSfaHeadsPerWg, "heads per workgroup");
   const bool chunked = p.pos_per_split > kSfaMaxList;
   const dim3 grid((unsigned)blocks), block(C::NW * 64);
-  if constexpr (D == 512) {
-    if (heads_per_wg == kSfaDsHeads) {
+  auto launch_ds = [&](auto hg) {
+    constexpr int HG = decltype(hg)::value;
+    if constexpr (D == 512) {
       if (buf && !chunked)
-        hipLaunchKernelGGL((sfa_fwd_ds_kernel<D, T, true, false>), grid, dim3(512), 0, stream, p);
+        hipLaunchKernelGGL((sfa_fwd_ds_kernel<D, T, HG, true, false>), grid, dim3(512), 0, stream, p);
       else if (buf)
-        hipLaunchKernelGGL((sfa_fwd_ds_kernel<D, T, true, true>), grid, dim3(512), 0, stream, p);
+        hipLaunchKernelGGL((sfa_fwd_ds_kernel<D, T, HG, true, true>), grid, dim3(512), 0, stream, p);
       else if (!chunked)
-        hipLaunchKernelGGL((sfa_fwd_ds_kernel<D, T, false, false>), grid, dim3(512), 0, stream, p);
+        hipLaunchKernelGGL((sfa_fwd_ds_kernel<D, T, HG, false, false>), grid, dim3(512), 0, stream, p);
       else
-        hipLaunchKernelGGL((sfa_fwd_ds_kernel<D, T, false, true>), grid, dim3(512), 0, stream, p);
+        hipLaunchKernelGGL((sfa_fwd_ds_kernel<D, T, HG, false, true>), grid, dim3(512), 0, stream, p);
     }
-  }
-  if (heads_per_wg == kSfaDsHeads) {
+  };
+  if (kind == kFwdDs64) {
+    launch_ds(std::integral_constant<int, 64>{});
+  } else if (kind == kFwdDs128) {
+    launch_ds(std::integral_constant<int, 128>{});
   } else if (buf && !chunked)
     hipLaunchKernelGGL((sfa_fwd_kernel<D, T, C::HT, C::NW, true, false>), grid, block, 0, stream, p);
   else if (buf)
@@ -1589,8 +1681,8 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
   p.max_blocks = (int32_t)max_blocks;
   p.page_size = (int32_t)page_size;
   const int64_t total_pos = sparse_count * (int64_t)sparse_block_size;
-  const int hpw = sfa_fwd_heads_per_wg(q_rows, n1, d, total_pos);
-  p.splits = sfa_fwd_plan_splits(q_rows, n1, total_pos, hpw);
+  const SfaFwdKind kind = sfa_fwd_kind(q_rows, n1, d, total_pos);
+  p.splits = sfa_fwd_plan_splits(q_rows, n1, total_pos, kind == kFwdDs64 ? kSfaDsHeads : kSfaHeadsPerWg);
   p.pos_per_split = (int32_t)((total_pos + p.splits - 1) / p.splits);
   p.part_o = nullptr;
   p.part_ml = nullptr;
@@ -1603,13 +1695,13 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
   p.rows_per_xcd = 0;
   hipError_t e;
   if (dtype == DSA_DTYPE_BF16) {
-    e = d == 512 ? launch_sfa_fwd<512, bf16>(p, hpw, stream)
-      : d == 256 ? launch_sfa_fwd<256, bf16>(p, hpw, stream)
-                 : launch_sfa_fwd<128, bf16>(p, hpw, stream);
+    e = d == 512 ? launch_sfa_fwd<512, bf16>(p, kind, stream)
+      : d == 256 ? launch_sfa_fwd<256, bf16>(p, kind, stream)
+                 : launch_sfa_fwd<128, bf16>(p, kind, stream);
   } else {
-    e = d == 512 ? launch_sfa_fwd<512, f16>(p, hpw, stream)
-      : d == 256 ? launch_sfa_fwd<256, f16>(p, hpw, stream)
-                 : launch_sfa_fwd<128, f16>(p, hpw, stream);
+    e = d == 512 ? launch_sfa_fwd<512, f16>(p, kind, stream)
+      : d == 256 ? launch_sfa_fwd<256, f16>(p, kind, stream)
+                 : launch_sfa_fwd<128, f16>(p, kind, stream);
   }
   if (e != hipSuccess) return hip_fail(e, "sfa_fwd launch");
   return DSA_OK;

@@ -70,9 +70,9 @@ int dsa_abi_version(void);
 /* Bit 2: dsa_kl_bwd / dsa_kl_bwd_ex take their generic path (the one for
  * index shapes outside the fused row kernel) at every shape. */
 #define DSA_TEST_KL_GENERIC 4
-/* Bit 3: D = 512 forwards that split tokens keep the 128-head workgroup
- * kernel instead of the 64-head one; set it around both the workspace query
- * and the call. */
+/* Bit 3: D = 512 forwards run the 128-head workgroup kernel without the
+ * column-split P.V product (the D < 512 kernel) instead of the column-split
+ * kernels; set it around both the workspace query and the call. */
 #define DSA_TEST_FWD_WIDE 8
 void dsa_set_test_flags(int32_t flags);
 

@@ -334,10 +334,11 @@ def test_fwd_token_split_rows(B, S1, S2, N1, K, mode, D, dtype):
 
 
 @pytest.mark.parametrize("flag", ["TEST_FORCE_GLOBAL_GATHER", "TEST_FWD_WIDE"])
-@pytest.mark.parametrize("B,S1,S2,N1,K,mode,D", [SPLIT_CASES[0], SPLIT_CASES[3]])
-def test_fwd_token_split_variants(B, S1, S2, N1, K, mode, D, flag):
-    """The D = 512 split launch through its other paths: the 64-bit global
-    gather of the 64-head kernel, and the 128-head kernel (test flags)."""
+@pytest.mark.parametrize("B,S1,S2,N1,K,mode,D", [SPLIT_CASES[0], SPLIT_CASES[3], (1, 300, 512, 128, 64, 3, 512)])
+def test_fwd_d512_variants(B, S1, S2, N1, K, mode, D, flag):
+    """D = 512 launches (token splits and, 300 rows, none) through their
+    other paths: the 64-bit global gather of the column-split kernels, and
+    the 128-head kernel without the column split (test flags)."""
     from dsa_triton_ascend_amd import _lib
     print(f"[sfa_fwd split {flag}] B={B} S1={S1} S2={S2} N1={N1} K={K} mode={mode}", flush=True)
     dtype = torch.bfloat16
