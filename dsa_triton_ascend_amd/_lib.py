@@ -43,6 +43,7 @@ SIGNATURES = {
     "dsa_last_error": (_c.c_char_p, []),
     "dsa_abi_version": (_c.c_int, []),
     "dsa_set_test_flags": (None, [_i32]),
+    "dsa_calib_stream_read": (_c.c_int, [_vp, _sz, _i32, _vp, _vp]),
     "dsa_sfa_fwd": (_c.c_int, [
         _vp, _vp, _vp, _vp, _i32p,           # query, query_rope, key, key_rope, sparse_indices
         _vp, _vp, _vp,                        # attention_out, softmax_max, softmax_sum

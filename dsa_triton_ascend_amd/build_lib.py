@@ -25,6 +25,7 @@ SOURCES = [
     "kl_bwd.hip",
     "kl_generic.hip",
     "dense_kl.hip",
+    "calib.hip",
 ]
 
 ARCH = os.environ.get("DSA_OFFLOAD_ARCH", "gfx950")

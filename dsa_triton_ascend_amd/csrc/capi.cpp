@@ -108,6 +108,8 @@ int li_scores_run(const void* query, const void* key, const void* weights, const
 int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_t* indices,
                 void* values, int32_t val_dtype, hipStream_t stream);
 constexpr int64_t kLiMaxK = 16384;  // the top-k sorts up to 16384 entries (LDS and per-wave registers)
+// calib.hip
+int calib_stream_read_run(const void* buf, size_t bytes, int nontemporal, unsigned* sink, hipStream_t stream);
 
 static bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 
@@ -690,6 +692,14 @@ int dsa_li_fwd_paged(const void* query, const void* key_cache, const void* weigh
   if (st != DSA_OK) return st;
   return li_topk_run(scores, q_rows * n2, s2, sparse_count, sparse_indices,
                      return_value ? sparse_values : nullptr, dtype, (hipStream_t)stream);
+}
+
+int dsa_calib_stream_read(const void* buffer, size_t bytes, int32_t nontemporal, uint32_t* sink, void* stream) {
+  g_err[0] = '\0';
+  DSA_CHECK_ARG(buffer, "null buffer pointer");
+  DSA_CHECK_ARG(bytes >= 16 && bytes % 16 == 0, "bytes must be a positive multiple of 16, got %zu", bytes);
+  DSA_CHECK_ARG(((uintptr_t)buffer & 15) == 0, "buffer must be 16-byte aligned");
+  return calib_stream_read_run(buffer, bytes, nontemporal, sink, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -77,6 +77,17 @@ int dsa_abi_version(void);
 void dsa_set_test_flags(int32_t flags);
 
 /*
+ * Calibration hook, no counterpart in the reference: one launch of a
+ * streaming-read kernel over `bytes` bytes of `buffer` (16-byte aligned,
+ * a multiple of 16), each byte read once with plain or, when `nontemporal`
+ * is set, non-temporal 16-byte loads.  Timed by the caller (events around
+ * the launch on `stream`), it gives the read rate that HBM-bound kernels of
+ * this library can reach on the device.  `sink` may be NULL (a word the
+ * kernel writes only to keep its loads).  Status codes as below.
+ */
+int dsa_calib_stream_read(const void* buffer, size_t bytes, int32_t nontemporal, uint32_t* sink, void* stream);
+
+/*
  * Sparse flash attention forward, MLA-absorb (value = key[..., :D]), MQA (N2 = 1).
  * Replaces the reference core `_sfa_core` (sparse_flash_attention_triton.py:445-477)
  * and the host-side layout normalisation around it (551-611): TND rows,

@@ -224,6 +224,12 @@ int main() {
                                                   v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7], v[8], I32(v, 9),
                                                   I32(v, 10), I32(v, 11), I32(v, 12), nullptr);
                      }});
+  entries.push_back({"dsa_calib_stream_read",
+                     {1 << 20, 0},
+                     2, {1},
+                     [](const Ptrs& p, const Ints& v) {
+                       return dsa_calib_stream_read(P(p, 0), (size_t)v[0], I32(v, 1), (uint32_t*)P(p, 1), nullptr);
+                     }});
   for (const Entry& e : entries) sweep(e);
 
   sweep_size("dsa_sfa_fwd_workspace_size", {32, 128, 512, 2048, 1}, [](const Ints& v) {

@@ -136,3 +136,15 @@ def test_kl_workspace_sizes_agree():
     assert lib.dsa_kl_bwd_ex_workspace_size(7, 80, 48, 264) == 0      # d_idx above 256
     # the contribution buffer and the accumulators scale with d_idx
     assert lib.dsa_kl_bwd_ex_workspace_size(7, 80, 48, 64) < lib.dsa_kl_bwd_ex_workspace_size(7, 80, 48, 128)
+
+
+@pytest.mark.parametrize("args,code", [
+    ((None, 1 << 20, 0, None, None), 1),      # no buffer
+    ((0x10000, 8, 0, None, None), 1),         # under 16 bytes
+    ((0x10000, 1000, 0, None, None), 1),      # not a multiple of 16
+    ((0x10008, 1 << 20, 1, None, None), 1),   # misaligned
+])
+def test_calib_stream_read_rejects_bad_arguments(args, code):
+    _, lib = _lib()
+    assert lib.dsa_calib_stream_read(*args) == code
+    assert lib.dsa_last_error().decode()
