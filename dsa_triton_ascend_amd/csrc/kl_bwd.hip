@@ -43,7 +43,8 @@ namespace dsa {
 
 struct KlParams {
   KlMap m;
-  int32_t ring;  // pass A tile buffers in LDS (1 or 2)
+  int32_t ring;   // pass A tile buffers in LDS (1 or 2)
+  int32_t ringb;  // bytes of the LDS ring region: max(ring tile buffers, pass C's)
   const void* q;
   const void* qr;
   const void* k;
@@ -72,6 +73,12 @@ constexpr int kKlWaves = 8;
 constexpr int kKlMaxNidx = 64;
 constexpr int kKlMaxTopk = 8192;
 constexpr int kKlDsRow = kKlMaxNidx + 8;  // padded LDS row of dS^T (elements)
+// Pass C's use of the ring region: three K_index tile buffers (32 rows of
+// 128 bf16/fp16) and the dS^T hi / lo tiles of two consecutive tiles.
+constexpr int kKlPcKiBytes = kKlTile * kKlDi * 2;
+constexpr int kKlPcDsBytes = 2 * kKlTile * kKlDsRow * 2;
+constexpr int kKlPcBufs = 3;
+constexpr int kKlPcBytes = kKlPcBufs * kKlPcKiBytes + 2 * kKlPcDsBytes;
 
 // Zero source row of the pass-A gather (slots past the row's end and
 // tokens of -1 pages).
@@ -115,27 +122,17 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   // per-wave partial sums of a pass-A tile, double-buffered by tile parity
   __shared__ __attribute__((aligned(16))) float s_red[2][kKlWaves][TILE];
   __shared__ __attribute__((aligned(16))) float s_redi[2][4][TILE];
-  __shared__ __attribute__((aligned(16))) T s_ds[2][TILE][kKlDsRow];  // dS^T hi / lo: [slot][g]
   // [0, 8) and [8, 16): per-wave pass-B sums / maxima; [16]: fp16 weight
   // max; [17, 25): per-wave max |Qi|
   __shared__ float s_misc[3 * kKlWaves + 4];
-  // dynamic: the pass-A tile ring (p.ring buffers of BUF bytes), then I
-  // (then dI) and p of the row, and its clamped token rows
+  // dynamic: the ring region (pass A's p.ring tile buffers of BUF bytes;
+  // pass C's K_index tiles and dS^T tiles), then I (then dI) and p of the
+  // row, and its clamped token rows
   extern __shared__ __attribute__((aligned(16))) unsigned char s_dynb[];
   unsigned char* const ring = s_dynb;
-  float* s_I = (float*)(s_dynb + p.ring * BUF);
+  float* s_I = (float*)(s_dynb + p.ringb);
   float* s_p = s_I + p.topk;
   int* s_tok = (int*)(s_p + p.topk);
-  // pass C stages K_index tiles in buffer 0's index rows, and a tile's dKi
-  // contributions ([slot][128] fp16, 8 KB) in buffer 1, or with one buffer
-  // in buffer 0's K rows (one buffer only happens at D >= 256).  In a row,
-  // 32-byte block j of slot tk sits at block j ^ ((tk >> 2) & 3), so that
-  // the MFMA-layout writes of the four lane groups (slots 4*lg + r) fall in
-  // different banks.
-  unsigned char* const s_ki = ring + BUF_K + BUF_R;
-  constexpr int CROW = DI * 2;
-  static_assert(TILE * CROW <= BUF && TILE * CROW <= BUF_K + BUF_R, "contribution staging");
-  unsigned char* const s_c = p.ring == 2 ? ring + BUF : ring;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -204,19 +201,21 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     const int gg = hg4 * 16 + lg * 4 + r;
     wr[r] = (ihg && gg < p.nidx) ? load_w(p.w, (int64_t)row * p.nidx + gg, p.w_dtype) : 0.f;
   }
-  // B operand of c = dS^T . Qi for this wave's 16 columns: Qi[g 32*ks + 8*lg + j][16*wave + li]
-  V8 qib[kKlMaxNidx / 32];
+  // A operand of c^T = Qi^T . dS for the 32 columns 32*(wave & 3) + 16*ct
+  // + li that pass C gives waves 4-7: Qi[g 32*ks + 8*lg + j][column]
+  V8 qib[2][kKlMaxNidx / 32];
 #pragma unroll
-  for (int ks = 0; ks < kKlMaxNidx / 32; ++ks) {
+  for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int gg = ks * 32 + lg * 8 + j;
-      T v = E::from_f32(0.f);
-      if (gg < p.nidx) v = ((const T*)p.qi)[((int64_t)row * p.nidx + gg) * DI + wave * 16 + li];
-      qib[ks][j] = v;
+    for (int ks = 0; ks < kKlMaxNidx / 32; ++ks) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int gg = ks * 32 + lg * 8 + j;
+        T v = E::from_f32(0.f);
+        if (gg < p.nidx) v = ((const T*)p.qi)[((int64_t)row * p.nidx + gg) * DI + (wave & 3) * 32 + ct * 16 + li];
+        qib[ct][ks][j] = v;
+      }
     }
-  }
-  for (int e = tid; e < 2 * TILE * kKlDsRow; e += NT) (&s_ds[0][0][0])[e] = E::from_f32(0.f);
   // per-wave partial sums of a tile; waves without heads keep zeros
   for (int e = tid; e < 2 * kKlWaves * TILE; e += NT) (&s_red[0][0][0])[e] = 0.f;
   for (int e = tid; e < 2 * 4 * TILE; e += NT) (&s_redi[0][0][0])[e] = 0.f;
@@ -229,7 +228,12 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   for (int k = tid; k < n; k += NT) s_tok[k] = kl_token(p.m, ri, p.idx, row, k);
   __syncthreads();
 
-  auto slot_tok = [&](int k) { return k < n ? s_tok[k] : -1; };
+  // unconditional LDS reads (index clamped into the row) and a select: a
+  // read under a lane condition is masked on its own and waited for alone
+  auto slot_tok = [&](int k) {
+    const int v = s_tok[k < n ? k : n - 1];
+    return k < n ? v : -1;
+  };
   // Tile t into ring buffer b: wave w issues K DMAs w, w+8, ..., rope DMA w
   // (w < RD) and K_index DMA w.  A lane's 16 bytes land at its fixed slot
   // of the buffer; it loads the source chunk that the XOR swizzle puts
@@ -463,9 +467,11 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     ws = wave_sum(ws);
     float qm = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < kKlMaxNidx / 32; ++ks)
+    for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) qm = fmaxf(qm, fabsf(E::to_f32(qib[ks][j])));
+      for (int ks = 0; ks < kKlMaxNidx / 32; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qm = fmaxf(qm, fabsf(E::to_f32(qib[ct][ks][j])));
     qm = wave_max(qm);
     lds_barrier();
     if (lane == 0) s_misc[2 * kKlWaves + 1 + wave] = qm;
@@ -482,27 +488,58 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   }
 
   // ================= pass C: dW, dQi, dKi contributions =================
+  // Software-pipelined over the tiles with one barrier per tile.  In step t,
+  // waves 0-3 recompute tile t's index scores from its K_index tile, form
+  // dS (hi / lo) into the dS^T tile of parity t & 1, and accumulate dW and
+  // dQi; waves 4-7 turn tile t-1's dS^T tile into the slots' dKi
+  // contributions and store them.  Waves 0-3 gather the K_index tiles by
+  // LDS-DMA into three buffers, two tiles ahead; they issue no other global
+  // memory operation in the loop, so their vmcnt counts exactly these DMAs
+  // (two per wave and tile).  The buffer that tile t+2 is issued into held
+  // tile t-1, which every wave finished before step t's barrier; the dS^T
+  // tile of parity t & 1 held tile t-2, whose contributions were finished
+  // before the same barrier.
+  static_assert(ID == 8 && kKlTile * DI * 2 == 8 * 1024, "two K_index DMAs per wave of waves 0-3");
+  unsigned char* const pc_ki = ring;
+  T* const pc_ds = (T*)(ring + kKlPcBufs * kKlPcKiBytes);  // [parity][hi / lo][slot][kKlDsRow]
+  // columns g >= Nidx1 of the dS^T tiles stay zero (waves without index
+  // heads never write theirs); the K rows of pass A no longer need the space
+  for (int e = tid; e < 2 * kKlPcDsBytes / 8; e += NT) ((uint2*)pc_ds)[e] = make_uint2(0u, 0u);
   f32x4 acc_dqi[DI / 16];
 #pragma unroll
   for (int dt = 0; dt < DI / 16; ++dt) acc_dqi[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
   float dw_acc = 0.f, cmax = 0.f;
-  u32x4 prei;
-  auto load_c = [&](int t) {
-    const int tk = tid / CI, ch = tid - tk * CI;
-    const int tok = slot_tok(t * TILE + tk);
-    prei = tok >= 0 ? *(const u32x4*)(kib + (int64_t)tok * IROW + ch * 16) : z4;
+  const bool dma_wave = wave < 4;
+  auto issue_c = [&](int t) {
+    const unsigned base = (unsigned)(uintptr_t)(pc_ki + (t % kKlPcBufs) * kKlPcKiBytes);
+    int tk[2], tok[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      tk[u] = (u * 4 + wave) * TPI + lane / CI;
+      tok[u] = slot_tok(t * TILE + tk[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int ch = (lane % CI) ^ nope_swz(tk[u]);
+      kl_dma16(base + (u * 4 + wave) * 1024, tok[u] >= 0 ? (const void*)(kib + (int64_t)tok[u] * IROW + ch * 16)
+                                                         : (const void*)(g_kl_zero_row + ch * 16));
+    }
   };
-  load_c(0);
-  for (int t = 0; t < nt; ++t) {
-    lds_barrier();
-    {
-      const int tk = tid / CI, ch = tid - tk * CI;
-      *(u32x4*)(s_ki + tk * IROW + ((ch ^ nope_swz(tk)) * 16)) = prei;
+  if (dma_wave) {
+    issue_c(0);
+    if (nt > 1) issue_c(1);
+  }
+  for (int t = 0; t <= nt; ++t) {
+    if (dma_wave && t < nt) {
+      if (t + 1 < nt) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
     lds_barrier();
-    if (t + 1 < nt) load_c(t + 1);
-
-    if (iwave) {
+    if (dma_wave && t + 2 < nt) issue_c(t + 2);
+    if (iwave && t < nt) {
+      const unsigned char* s_ki = pc_ki + (t % kKlPcBufs) * kKlPcKiBytes;
+      T* const dsh = pc_ds + (t & 1) * 2 * TILE * kKlDsRow;
+      T* const dsl_ = dsh + TILE * kKlDsRow;
       f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
       for (int ks = 0; ks < DI / 32; ++ks)
@@ -512,7 +549,14 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
           const unsigned char* a = s_ki + tk * IROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16);
           acc[tt] = E::mfma(as_v8<V8>(*(const u32x4*)a), qif[ks], acc[tt]);
         }
-      // dS^T (slot 8*lg + j maps to slot (j>>2)*16 + 4*lg + (j&3)) as B operand
+      // dS^T (slot 8*lg + j maps to slot (j>>2)*16 + 4*lg + (j&3)) as B
+      // operand; the slots' dI read together (unconditional, clamped)
+      float dis[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int k = t * TILE + (j >> 2) * 16 + lg * 4 + (j & 3);
+        dis[j] = s_I[k < n ? k : n - 1];
+      }
       V8 dsf, dsl;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -520,15 +564,15 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
         const int tk = tt * 16 + lg * 4 + r;
         const int k = t * TILE + tk;
         const float relu = fmaxf(acc[tt][r], 0.f);
-        const float di = (k < n && gv) ? s_I[k] : 0.f;
+        const float di = (k < n && gv) ? dis[j] : 0.f;
         dw_acc += di * relu;
         const float ds = relu > 0.f ? di * wg * ds_scale : 0.f;
         const T hi = E::from_f32(ds);
         const T lo = E::from_f32(ds - E::to_f32(hi));
         dsf[j] = hi;
         dsl[j] = lo;
-        s_ds[0][tk][g] = hi;
-        s_ds[1][tk][g] = lo;
+        dsh[tk * kKlDsRow + g] = hi;
+        dsl_[tk * kKlDsRow + g] = lo;
       }
       // dQi^T[d][g] += Ki^T[d][slot] . dS^T[slot][g]; Ki^T fragment through
       // the transposing read: rows 4*lg + li/4 (+16), chunk 2*dt + (li&3)/2
@@ -546,39 +590,44 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
         acc_dqi[dt] = E::mfma(__builtin_bit_cast(V8, wv), dsl, acc_dqi[dt]);
       }
     }
-    lds_barrier();
-    // c[slot][16*wave + li] = sum_g dS^T[slot][g] Qi[g][16*wave + li]
-    {
-      f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    if (!dma_wave && t > 0) {
+      // c^T[d][slot] = sum_g Qi^T[d][g] dS^T[slot][g] for tile t-1: C
+      // register r of a lane is column d = 32*(wave & 3) + 16*ct + 4*lg + r
+      // of slot 16*tt + li, so a lane stores 4 consecutive fp16 values
+      const int tp = t - 1;
+      const T* const dsh = pc_ds + (tp & 1) * 2 * TILE * kKlDsRow;
+      const T* const dsl_ = dsh + TILE * kKlDsRow;
+      f32x4 acc[2][2] = {{{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}, {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}};
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int ks = 0; ks < kKlMaxNidx / 32; ++ks) {
-          const V8 ah = as_v8<V8>(*(const u32x4*)&s_ds[0][tt * 16 + li][ks * 32 + lg * 8]);
-          const V8 al = as_v8<V8>(*(const u32x4*)&s_ds[1][tt * 16 + li][ks * 32 + lg * 8]);
-          acc[tt] = E::mfma(ah, qib[ks], acc[tt]);
-          acc[tt] = E::mfma(al, qib[ks], acc[tt]);
-        }
-      // staged in LDS, then stored as whole 512-byte rows (16 bytes per
-      // lane): stored directly, each row would leave in 64-byte pieces from
-      // eight waves
+          const V8 bh = as_v8<V8>(*(const u32x4*)&dsh[(tt * 16 + li) * kKlDsRow + ks * 32 + lg * 8]);
+          const V8 bl = as_v8<V8>(*(const u32x4*)&dsl_[(tt * 16 + li) * kKlDsRow + ks * 32 + lg * 8]);
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int tk = tt * 16 + lg * 4 + r;
-          const float c = acc[tt][r] * ds_unscale;
-          if (t * TILE + tk < n) cmax = fmaxf(cmax, fabsf(c));
-          *(_Float16*)(s_c + tk * CROW + ((wave ^ ((tk >> 2) & 3)) * 16 + li) * 2) = (_Float16)(c * c_scale);
+          for (int ct = 0; ct < 2; ++ct) {
+            acc[tt][ct] = E::mfma(qib[ct][ks], bh, acc[tt][ct]);
+            acc[tt][ct] = E::mfma(qib[ct][ks], bl, acc[tt][ct]);
+          }
         }
-    }
-    lds_barrier();
-    static_assert(TILE * DI * 2 == NT * 16, "one 16-byte chunk per thread");
-    {
-      const int tk = tid / (DI / 8), ch = tid - tk * (DI / 8);
-      const int k = t * TILE + tk;
-      const u32x4 v = *(const u32x4*)(s_c + tk * CROW + (ch ^ (((tk >> 2) & 3) << 1)) * 16);
-      if (k < n) *(u32x4*)(p.cbuf + ((int64_t)row * p.topk + k) * DI + ch * 8) = v;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        const int k = tp * TILE + tt * 16 + li;
+        if (k < n) {
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct) {
+            _Float16 h[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float c = acc[tt][ct][r] * ds_unscale;
+              cmax = fmaxf(cmax, fabsf(c));
+              h[r] = (_Float16)(c * c_scale);
+            }
+            *(uint2*)(p.cbuf + ((int64_t)row * p.topk + k) * DI + (wave & 3) * 32 + ct * 16 + lg * 4) =
+                __builtin_bit_cast(uint2, h);
+          }
+        }
+      }
     }
   }
 
@@ -872,11 +921,10 @@ static hipError_t run_kl_row(KlParams p, int rows, int64_t topk, hipStream_t str
   if (static_lds < 0) return hipErrorInvalidDeviceFunction;
   const int buf = kl_tile_bytes<D, DR>();
   const int rowb = (int)(3 * topk * sizeof(float));
-  p.ring = static_lds + 2 * buf + rowb <= kKlLdsBytes ? 2 : 1;
-  // one buffer stages pass C's contributions in its K rows: D >= 256 only
-  // (at D = 128 two buffers fit for every supported topK)
-  if (p.ring == 1 && D < 256) return hipErrorInvalidConfiguration;
-  const int dyn = p.ring * buf + rowb;
+  p.ring = static_lds + std::max(2 * buf, kKlPcBytes) + rowb <= kKlLdsBytes ? 2 : 1;
+  p.ringb = std::max(p.ring * buf, kKlPcBytes);
+  const int dyn = p.ringb + rowb;
+  if (static_lds + dyn > kKlLdsBytes) return hipErrorInvalidConfiguration;
   // raised on every call: a host-side setting, cheap next to the kernel, and
   // right for whichever device is current and for concurrent callers
   hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);

@@ -180,6 +180,23 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
     return;
   }
 
+  // weight of head ht*16 + 4*lg + r (the C-layout rows of this lane),
+  // loaded first, as raw bits under one width branch, and converted only
+  // after the first key groups are issued: loads issued before the branch,
+  // or a conversion inside it, make the compiler wait for them there
+  uint32_t wraw[GT][4];
+  const int64_t wbase = (int64_t)row * p.n1 + kh * p.g;
+  auto load_w = [&](auto* wp) {
+#pragma unroll
+    for (int ht = 0; ht < GT; ++ht)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int gg = ht * 16 + lg * 4 + r;
+        wraw[ht][r] = wp[wbase + (gg < p.g ? gg : 0)];  // unconditional: no branch per load
+      }
+  };
+  if (p.w_dtype == DSA_DTYPE_FP32) load_w((const uint32_t*)p.w);
+  else load_w((const uint16_t*)p.w);
   // Q fragments (A operand): lane -> head ht*16 + li, d = ks*32 + 8*lg ..
   V8 qf[GT][KS];
 #pragma unroll
@@ -195,23 +212,6 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
       qf[ht][ks] = as_v8<V8>(gv ? v : z);
     }
   }
-  // weight of head ht*16 + 4*lg + r (the C-layout rows of this lane); one
-  // dtype branch around all loads so that they are in flight together
-  float wv[GT][4];
-  const int64_t wbase = (int64_t)row * p.n1 + kh * p.g;
-  auto load_w = [&](auto* wp) {
-#pragma unroll
-    for (int ht = 0; ht < GT; ++ht)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int gg = ht * 16 + lg * 4 + r;
-        const float x = (float)wp[wbase + (gg < p.g ? gg : 0)];  // unconditional: no branch per load
-        wv[ht][r] = gg < p.g ? x : 0.f;
-      }
-  };
-  if (p.w_dtype == DSA_DTYPE_FP32) load_w((const float*)p.w);
-  else if (p.w_dtype == DSA_DTYPE_BF16) load_w((const bf16*)p.w);
-  else load_w((const f16*)p.w);
 
   // key groups of 16: wave w takes groups w, w+4, ...; K fragment of group
   // kg (B operand): lane -> key kg*16 + li, d = ks*32 + 8*lg ..
@@ -237,6 +237,17 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
   u32x4 kf[NP][KS];
 #pragma unroll
   for (int i = 0; i < NP; ++i) kload(min(wave + 4 * i, ngroups - 1), kf[i]);
+  float wv[GT][4];
+#pragma unroll
+  for (int ht = 0; ht < GT; ++ht)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t b = wraw[ht][r];
+      const float x = p.w_dtype == DSA_DTYPE_FP32 ? __uint_as_float(b)
+                      : p.w_dtype == DSA_DTYPE_BF16 ? __uint_as_float(b << 16)
+                                                    : (float)__builtin_bit_cast(f16, (uint16_t)b);
+      wv[ht][r] = ht * 16 + lg * 4 + r < p.g ? x : 0.f;
+    }
   auto process = [&](int gi, const u32x4 (&kf)[KS]) {
     f32x4 acc[GT];
 #pragma unroll
