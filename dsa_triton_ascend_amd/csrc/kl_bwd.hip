@@ -23,11 +23,12 @@
 //    probabilities on MFMA; waves w and w + 4 score index heads
 //    16*(w mod 4) .. +15 for the two halves of the tile.  I and p of the row
 //    stay in LDS.  Pass B is the softmax/KL over the row.  Pass C re-streams
-//    K_index: the index scores are recomputed (cheaper than storing
-//    Nidx1 x topK ReLUs), dW and dQi accumulate in registers (dQi^T =
-//    Ki^T . dS^T through the transposing LDS read), and the per-slot dKi
-//    contributions c[k] = dS[:,k]^T . Qi are written to a workspace as fp16
-//    scaled by a per-row power of two.
+//    K_index by LDS-DMA, pipelined over the tiles: waves 0-3 recompute a
+//    tile's index scores (cheaper than storing Nidx1 x topK ReLUs), form
+//    dS, and accumulate dW and dQi in registers (dQi^T = Ki^T . dS^T
+//    through the transposing LDS read), while waves 4-7 turn the previous
+//    tile's dS into the per-slot dKi contributions c[k] = dS[:,k]^T . Qi,
+//    written to a workspace as fp16 scaled by a per-row power of two.
 //  * dKi without floating-point atomics: the slots are bucketed by target
 //    token (count, scan, fill), and a token's contributions are summed in
 //    int64 fixed point, with the exponent fixed by the largest row maximum
