@@ -244,49 +244,61 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   // compiler memory barrier, so a read placed between two DMAs would wait
   // for its own LDS round trip.
   constexpr int NKW = (KD + kKlWaves - 1) / kKlWaves, NIW = (ID + kKlWaves - 1) / kKlWaves;
-  auto issue_a = [&](int t, int b) {
+  constexpr int NDA = NKW + 1 + NIW;  // DMA positions of a wave: K, rope, K_index
+  // the slots a lane gathers: K DMA u row, rope row, K_index DMA v row
+  auto tk_k = [&](int u) { return (u * kKlWaves + wave) * TPK + lane / CN; };
+  auto tk_r = [&]() { return wave * 8 + (lane >> 3); };
+  auto tk_i = [&](int v) { return (v * kKlWaves + wave) * TPI + lane / CI; };
+  struct TokA {
+    int tok_k[NKW], tok_i[NIW], tok_r;
+  };
+  auto tokens_a = [&](int t) {
+    TokA x;
+    x.tok_r = -1;
+#pragma unroll
+    for (int u = 0; u < NKW; ++u) {
+      const int j = u * kKlWaves + wave;
+      x.tok_k[u] = (KD % kKlWaves == 0 || j < KD) ? slot_tok(t * TILE + tk_k(u)) : -1;
+    }
+    if (DR > 0 && wave < RD) x.tok_r = slot_tok(t * TILE + tk_r());
+#pragma unroll
+    for (int v = 0; v < NIW; ++v) {
+      const int j = v * kKlWaves + wave;
+      x.tok_i[v] = (ID % kKlWaves == 0 || j < ID) ? slot_tok(t * TILE + tk_i(v)) : -1;
+    }
+    return x;
+  };
+  // DMA position u of this wave (u < NKW: K DMA u; NKW: rope; then K_index)
+  auto fire_a = [&](const TokA& x, int b, int u) {
     const unsigned base = (unsigned)(uintptr_t)(ring + b * BUF);
-    int tk_k[NKW], tok_k[NKW], tk_i[NIW], tok_i[NIW], tk_r = 0, tok_r = -1;
-#pragma unroll
-    for (int u = 0; u < NKW; ++u) {
-      const int j = u * kKlWaves + wave;
-      tk_k[u] = j * TPK + lane / CN;
-      tok_k[u] = (KD % kKlWaves == 0 || j < KD) ? slot_tok(t * TILE + tk_k[u]) : -1;
-    }
-    if (DR > 0 && wave < RD) {
-      tk_r = wave * 8 + (lane >> 3);
-      tok_r = slot_tok(t * TILE + tk_r);
-    }
-#pragma unroll
-    for (int u = 0; u < NIW; ++u) {
-      const int j = u * kKlWaves + wave;
-      tk_i[u] = j * TPI + lane / CI;
-      tok_i[u] = (ID % kKlWaves == 0 || j < ID) ? slot_tok(t * TILE + tk_i[u]) : -1;
-    }
-#pragma unroll
-    for (int u = 0; u < NKW; ++u) {
+    if (u < NKW) {
       const int j = u * kKlWaves + wave;
       if (KD % kKlWaves == 0 || j < KD) {
-        const int ch = (lane % CN) ^ nope_swz(tk_k[u]);
-        kl_dma16(base + j * 1024, tok_k[u] >= 0 ? (const void*)(kb + (int64_t)tok_k[u] * ROW + ch * 16)
-                                                : (const void*)(g_kl_zero_row + ch * 16));
+        const int ch = (lane % CN) ^ nope_swz(tk_k(u));
+        kl_dma16(base + j * 1024, x.tok_k[u] >= 0 ? (const void*)(kb + (int64_t)x.tok_k[u] * ROW + ch * 16)
+                                                  : (const void*)(g_kl_zero_row + ch * 16));
       }
-    }
-    if (DR > 0 && wave < RD) {
-      const int ch = (lane & 7) ^ rope_swz(tk_r);
-      kl_dma16(base + BUF_K + wave * 1024, tok_r >= 0 ? (const void*)(krb + (int64_t)tok_r * (DR * 2) + ch * 16)
-                                                      : (const void*)(g_kl_zero_row + ch * 16));
-    }
-#pragma unroll
-    for (int u = 0; u < NIW; ++u) {
-      const int j = u * kKlWaves + wave;
+    } else if (u == NKW) {
+      if (DR > 0 && wave < RD) {
+        const int ch = (lane & 7) ^ rope_swz(tk_r());
+        kl_dma16(base + BUF_K + wave * 1024, x.tok_r >= 0 ? (const void*)(krb + (int64_t)x.tok_r * (DR * 2) + ch * 16)
+                                                          : (const void*)(g_kl_zero_row + ch * 16));
+      }
+    } else {
+      const int v = u - NKW - 1;
+      const int j = v * kKlWaves + wave;
       if (ID % kKlWaves == 0 || j < ID) {
-        const int ch = (lane % CI) ^ nope_swz(tk_i[u]);
+        const int ch = (lane % CI) ^ nope_swz(tk_i(v));
         kl_dma16(base + BUF_K + BUF_R + j * 1024,
-                 tok_i[u] >= 0 ? (const void*)(kib + (int64_t)tok_i[u] * IROW + ch * 16)
-                               : (const void*)(g_kl_zero_row + ch * 16));
+                 x.tok_i[v] >= 0 ? (const void*)(kib + (int64_t)x.tok_i[v] * IROW + ch * 16)
+                                 : (const void*)(g_kl_zero_row + ch * 16));
       }
     }
+  };
+  auto issue_a = [&](int t, int b) {
+    const TokA x = tokens_a(t);
+#pragma unroll
+    for (int u = 0; u < NDA; ++u) fire_a(x, b, u);
   };
 
   // One barrier per tile.  With two buffers, tile t+1 is issued right
@@ -316,7 +328,17 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     const int b = p.ring == 2 ? (t & 1) : 0;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
-    if (p.ring == 2 && t + 1 < nt) issue_a(t + 1, b ^ 1);
+    // with two buffers the next tile's DMAs are spread over the teacher
+    // MFMAs (one every DSTEP steps): a wave stalls at each DMA it issues
+    // while the CU's gather path is busy, and spread out the stalls overlap
+    // the other wave's MFMAs on the SIMD
+    const bool pre = p.ring == 2 && t + 1 < nt;
+    TokA nx;
+    if (pre) nx = tokens_a(t + 1);
+    if (pre && !wave_heads) {
+#pragma unroll
+      for (int u = 0; u < NDA; ++u) fire_a(nx, b ^ 1, u);
+    }
     if (t > 0) reduce_a(t - 1);
     const unsigned char* s_k = ring + b * BUF;
     const unsigned char* s_kr = s_k + BUF_K;
@@ -334,7 +356,8 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
       // MFMA; the scheduling barrier after each MFMA keeps the reads where
       // they are (sunk next to their MFMAs, every MFMA would wait out a full
       // LDS round trip)
-      constexpr int NS = 2 * KS, PF = 6;
+      constexpr int NS = 2 * KS, PF = 4, DSTEP = NS / NDA;
+      static_assert(DSTEP >= 1, "DMA spacing");
       auto a_read = [&](int st) -> u32x4 {
         const int ks = st >> 1, tk = (st & 1) * 16 + li;
         const unsigned char* a =
@@ -351,6 +374,10 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
         if (st + PF < NS) fa[st % PF] = a_read(st + PF);
         acc[st & 1] = E::mfma(qf[st >> 1], av, acc[st & 1]);
         __builtin_amdgcn_sched_barrier(0);
+        if (pre && st % DSTEP == DSTEP - 1 && st / DSTEP < NDA) {
+          fire_a(nx, b ^ 1, st / DSTEP);
+          __builtin_amdgcn_sched_barrier(0);
+        }
       }
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
