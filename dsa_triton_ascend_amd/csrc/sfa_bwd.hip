@@ -613,13 +613,27 @@ __global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) 
           *(h4*)(srow + i * 16 + lg * 4) = v;
         }
       __builtin_amdgcn_wave_barrier();
-      const int cpr2 = nct * 2;  // 16-byte pieces per record slice
-      for (int q = lane; q < 16 * cpr2; q += 64) {
-        const int tk = q / cpr2, cc = q - tk * cpr2;
+      // four lanes per token: lane (tk, sub) stores pieces sub, sub+4, ...
+      // of token tk's slice; the token's position and all of the lane's
+      // staged pieces are read first, then the stores go out together
+      {
+        const int cpr2 = nct * 2;  // 16-byte pieces per record slice
+        const int tk = lane >> 2, sub = lane & 3;
         const int j2 = t * TILE + tt * 16 + tk;
+        const int64_t pos2 = s_pos[j2 - (t / (NPOS / TILE)) * NPOS];
+        constexpr int MAXP = (2 * MT + 3) / 4;  // pieces per lane, at most
+        u32x4 pv[MAXP];
+#pragma unroll
+        for (int it = 0; it < MAXP; ++it) {
+          const int cc = it * 4 + sub;
+          pv[it] = *(const u32x4*)(stg + tk * SROW + (cc < cpr2 ? cc : 0) * 8);
+        }
         if (j2 < nv) {
-          const int64_t pos2 = s_pos[j2 - (t / (NPOS / TILE)) * NPOS];
-          *(u32x4*)(p.rec + pos2 * p.nc + ct0 * 16 + cc * 8) = *(const u32x4*)(stg + tk * SROW + cc * 8);
+#pragma unroll
+          for (int it = 0; it < MAXP; ++it) {
+            const int cc = it * 4 + sub;
+            if (cc < cpr2) *(u32x4*)(p.rec + pos2 * p.nc + ct0 * 16 + cc * 8) = pv[it];
+          }
         }
       }
       __builtin_amdgcn_wave_barrier();
