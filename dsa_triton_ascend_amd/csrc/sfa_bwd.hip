@@ -348,16 +348,28 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void sfa_bwd_dq_kernel(SfaBwdPar
         s_t[1][tk][wave * 16 + li] = E::from_f32(pp * kDsMul);
       }
       lds_barrier();  // dS / P of the 64 heads in LDS
-      // ---- dS / P rows out (16 bytes per thread: 8 heads of one slot) ----
+      // ---- dS / P rows out (16 bytes per thread: 8 heads of one slot); all
+      // of a thread's LDS reads go out before its stores ----
       {
         const int cpr = nh / 8;  // chunks per (slot, dS | P) row: 4 or 8
-        for (int e = tid; e < TILE * 2 * cpr; e += NT) {
-          const int tk = e / (2 * cpr), rem = e - tk * 2 * cpr, which = rem / cpr, c = rem - which * cpr;
+        constexpr int NE = (TILE * 2 * (kBwdHeads / 8) + NT - 1) / NT;
+        u32x4 v[NE];
+        int64_t off[NE];
+        bool ok[NE];
+#pragma unroll
+        for (int i = 0; i < NE; ++i) {
+          const int e = tid + i * NT;
+          const bool in = e < TILE * 2 * cpr;
+          const int ee = in ? e : 0;
+          const int tk = ee / (2 * cpr), rem = ee - tk * 2 * cpr, which = rem / cpr, c = rem - which * cpr;
           const int j = t * TILE + tk;
-          if (j < n_valid)
-            *(u32x4*)(dsp_row + ((int64_t)(jbase + j) * 2 + which) * p.hp + c * 8) =
-                *(const u32x4*)&s_t[which][tk][c * 8];
+          ok[i] = in && j < n_valid;
+          off[i] = ((int64_t)(jbase + j) * 2 + which) * p.hp + c * 8;
+          v[i] = *(const u32x4*)&s_t[which][tk][c * 8];
         }
+#pragma unroll
+        for (int i = 0; i < NE; ++i)
+          if (ok[i]) *(u32x4*)(dsp_row + off[i]) = v[i];
       }
       // tile t+2 into the buffer tile t-1 used (every wave is past tile t's
       // first barrier, so past tile t-1)
@@ -368,7 +380,7 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void sfa_bwd_dq_kernel(SfaBwdPar
         const int r1 = lg * 4 + (li >> 2);
         const int hb = (li & 3) >> 1;
         // K^T fragment of d-tile dt (nope tiles, then the rope tiles)
-        constexpr int NQ = NDT + DR / 16, PF = 4;
+        constexpr int NQ = NDT + DR / 16, PF = 8;
         auto tread = [&](int dt) -> V8 {
           const unsigned char *p1, *p2;
           if (dt < NDT) {
