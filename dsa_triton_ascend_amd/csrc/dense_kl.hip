@@ -349,16 +349,27 @@ __global__ __launch_bounds__(kDkThreads, 1) void dense_teacher_kernel(DkParams p
     if (i + 1 < items) load_item(i + 1);
     if (n2 >= n2_lo && n2 <= n2_hi) {
       f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+      // K fragments of step st = 2*ks + tt, read PF steps ahead of their
+      // MFMA; the scheduling barrier after each MFMA keeps the reads there
+      // (sunk next to their MFMAs, every MFMA waits out an LDS round trip)
+      constexpr int NS = 2 * KS, PF = 4;
+      auto kread = [&](int st) -> u32x4 {
+        const int ks = st >> 1, tk = (st & 1) * 16 + li;
+        const unsigned char* a =
+            ks < KSN ? s_k + tk * ROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16)
+                     : s_kr + tk * (DR * 2) + ((((ks - KSN) * 4 + lg) ^ rope_swz(tk)) * 16);
+        return *(const u32x4*)a;
+      };
+      u32x4 fa[PF];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
+      for (int i = 0; i < PF; ++i) fa[i] = kread(i);
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const int tk = tt * 16 + li;
-          const unsigned char* a =
-              ks < KSN ? s_k + tk * ROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16)
-                       : s_kr + tk * (DR * 2) + ((((ks - KSN) * 4 + lg) ^ rope_swz(tk)) * 16);
-          acc[tt] = E::mfma(qf[ks], as_v8<V8>(*(const u32x4*)a), acc[tt]);
-        }
+      for (int st = 0; st < NS; ++st) {
+        const V8 bv = as_v8<V8>(fa[st % PF]);
+        if (st + PF < NS) fa[st % PF] = kread(st + PF);
+        acc[st & 1] = E::mfma(qf[st >> 1], bv, acc[st & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
         Split3 sp;
