@@ -110,8 +110,9 @@ __device__ __forceinline__ float li_load_w(const LiParams& p, int64_t idx) {
 
 // D = head dim, GT = head tiles of 16 (G <= 16*GT).  The chunk's scores
 // collect in LDS and leave in coalesced 16-byte stores at the end.  At the
-// decode shape the kernel streams K at about 4.9 TB/s, close to what a
-// plain streaming read reaches on the MI355X (about 5.5 TB/s measured).
+// decode shape one workgroup per CU streams K at about 6.7 TB/s in its
+// steady state (about 5.5 TB/s over the whole launch, with the start-up
+// and the tail); a plain streaming read of 1 GiB reaches 6.2-6.45 TB/s.
 // PAD: the head dim p.d is below D (a multiple of 8); the 8-element chunks
 // at or past p.d load as zeros, so the MFMAs see zero-padded rows of D.
 constexpr int kLiMaxChunk = 8192;  // keys per workgroup (LDS score buffer)
