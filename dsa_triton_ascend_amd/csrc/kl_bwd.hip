@@ -25,10 +25,10 @@
 //    stay in LDS.  Pass B is the softmax/KL over the row.  Pass C re-streams
 //    K_index by LDS-DMA, pipelined over the tiles: waves 0-3 recompute a
 //    tile's index scores (cheaper than storing Nidx1 x topK ReLUs), form
-//    dS, and accumulate dW and dQi in registers (dQi^T = Ki^T . dS^T
-//    through the transposing LDS read), while waves 4-7 turn the previous
-//    tile's dS into the per-slot dKi contributions c[k] = dS[:,k]^T . Qi,
-//    written to a workspace as fp16 scaled by a per-row power of two.
+//    dS and accumulate dW, while waves 4-7 take the previous tile: dQi
+//    (dQi^T = Ki^T . dS^T through the transposing LDS read) in registers,
+//    and the per-slot dKi contributions c[k] = dS[:,k]^T . Qi, written to a
+//    workspace as fp16 scaled by a per-row power of two.
 //  * dKi without floating-point atomics: the slots are bucketed by target
 //    token (count, scan, fill), and a token's contributions are summed in
 //    int64 fixed point, with the exponent fixed by the largest row maximum
@@ -74,11 +74,11 @@ constexpr int kKlWaves = 8;
 constexpr int kKlMaxNidx = 64;
 constexpr int kKlMaxTopk = 8192;
 constexpr int kKlDsRow = kKlMaxNidx + 8;  // padded LDS row of dS^T (elements)
-// Pass C's use of the ring region: three K_index tile buffers (32 rows of
+// Pass C's use of the ring region: four K_index tile buffers (32 rows of
 // 128 bf16/fp16) and the dS^T hi / lo tiles of two consecutive tiles.
 constexpr int kKlPcKiBytes = kKlTile * kKlDi * 2;
 constexpr int kKlPcDsBytes = 2 * kKlTile * kKlDsRow * 2;
-constexpr int kKlPcBufs = 3;
+constexpr int kKlPcBufs = 4;
 constexpr int kKlPcBytes = kKlPcBufs * kKlPcKiBytes + 2 * kKlPcDsBytes;
 
 // Zero source row of the pass-A gather (slots past the row's end and
@@ -518,15 +518,16 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   // ================= pass C: dW, dQi, dKi contributions =================
   // Software-pipelined over the tiles with one barrier per tile.  In step t,
   // waves 0-3 recompute tile t's index scores from its K_index tile, form
-  // dS (hi / lo) into the dS^T tile of parity t & 1, and accumulate dW and
-  // dQi; waves 4-7 turn tile t-1's dS^T tile into the slots' dKi
-  // contributions and store them.  Waves 0-3 gather the K_index tiles by
-  // LDS-DMA into three buffers, two tiles ahead; they issue no other global
-  // memory operation in the loop, so their vmcnt counts exactly these DMAs
-  // (two per wave and tile).  The buffer that tile t+2 is issued into held
-  // tile t-1, which every wave finished before step t's barrier; the dS^T
-  // tile of parity t & 1 held tile t-2, whose contributions were finished
-  // before the same barrier.
+  // dS (hi / lo) into the dS^T tile of parity t & 1, and accumulate dW;
+  // waves 4-7 take tile t-1: its dQi product (K_index and dS^T tiles through
+  // the transposing read) and the slots' dKi contributions, which they
+  // store.  Waves w and w + 4 own the same 16 index heads.  Waves 0-3
+  // gather the K_index tiles by LDS-DMA into four buffers, two tiles ahead;
+  // they issue no other global memory operation in the loop, so their vmcnt
+  // counts exactly these DMAs (two per wave and tile).  The buffer that tile
+  // t+2 is issued into held tile t-2, which waves 0-3 read in step t-2 and
+  // waves 4-7 in step t-1, both before step t's barrier; the dS^T tile of
+  // parity t & 1 held tile t-2, likewise finished before that barrier.
   static_assert(ID == 8 && kKlTile * DI * 2 == 8 * 1024, "two K_index DMAs per wave of waves 0-3");
   unsigned char* const pc_ki = ring;
   T* const pc_ds = (T*)(ring + kKlPcBufs * kKlPcKiBytes);  // [parity][hi / lo][slot][kKlDsRow]
@@ -577,15 +578,14 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
           const unsigned char* a = s_ki + tk * IROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16);
           acc[tt] = E::mfma(as_v8<V8>(*(const u32x4*)a), qif[ks], acc[tt]);
         }
-      // dS^T (slot 8*lg + j maps to slot (j>>2)*16 + 4*lg + (j&3)) as B
-      // operand; the slots' dI read together (unconditional, clamped)
+      // dS^T of slots 16*tt + 4*lg + r, head g; the slots' dI read together
+      // (unconditional, clamped)
       float dis[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int k = t * TILE + (j >> 2) * 16 + lg * 4 + (j & 3);
         dis[j] = s_I[k < n ? k : n - 1];
       }
-      V8 dsf, dsl;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int tt = j >> 2, r = j & 3;
@@ -597,25 +597,8 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
         const float ds = relu > 0.f ? di * wg * ds_scale : 0.f;
         const T hi = E::from_f32(ds);
         const T lo = E::from_f32(ds - E::to_f32(hi));
-        dsf[j] = hi;
-        dsl[j] = lo;
         dsh[tk * kKlDsRow + g] = hi;
         dsl_[tk * kKlDsRow + g] = lo;
-      }
-      // dQi^T[d][g] += Ki^T[d][slot] . dS^T[slot][g]; Ki^T fragment through
-      // the transposing read: rows 4*lg + li/4 (+16), chunk 2*dt + (li&3)/2
-      const int r1 = lg * 4 + (li >> 2);
-      const int hb = (li & 3) >> 1;
-#pragma unroll
-      for (int dt = 0; dt < DI / 16; ++dt) {
-        const int ch = 2 * dt + hb;
-        const unsigned char* p1 = s_ki + r1 * IROW + ((ch ^ nope_swz(r1)) * 16) + (li & 1) * 8;
-        const unsigned char* p2 = s_ki + (r1 + 16) * IROW + ((ch ^ nope_swz(r1 + 16)) * 16) + (li & 1) * 8;
-        const i16x4 w1 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1));
-        const i16x4 w2 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p2));
-        const i16x8 wv = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
-        acc_dqi[dt] = E::mfma(__builtin_bit_cast(V8, wv), dsf, acc_dqi[dt]);
-        acc_dqi[dt] = E::mfma(__builtin_bit_cast(V8, wv), dsl, acc_dqi[dt]);
       }
     }
     if (!dma_wave && t > 0) {
@@ -625,6 +608,34 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
       const int tp = t - 1;
       const T* const dsh = pc_ds + (tp & 1) * 2 * TILE * kKlDsRow;
       const T* const dsl_ = dsh + TILE * kKlDsRow;
+      if (ihg) {
+        // dQi^T[d][g] += Ki^T[d][slot] . dS^T[slot][g] for this wave's 16
+        // heads.  Both operands come through the transposing read: rows
+        // 4*lg + li/4 (+16), 16-byte chunk 2*dt + (li&3)/2 (+8 bytes for odd
+        // li) of a [slot][column] tile gives k-slot 8*lg + j as slot
+        // (j>>2)*16 + 4*lg + (j&3) in either operand.
+        const unsigned char* s_ki = pc_ki + (tp % kKlPcBufs) * kKlPcKiBytes;
+        const int r1 = lg * 4 + (li >> 2);
+        const int hb = (li & 3) >> 1;
+        auto tr8 = [&](const unsigned char* q1, const unsigned char* q2) -> V8 {
+          const i16x4 w1 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)q1));
+          const i16x4 w2 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)q2));
+          const i16x8 wv = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
+          return __builtin_bit_cast(V8, wv);
+        };
+        constexpr int DSR = kKlDsRow * 2;  // bytes of a dS^T row
+        const int dso = (2 * hg4 + hb) * 16 + (li & 1) * 8;
+        const V8 dsf = tr8((const unsigned char*)dsh + r1 * DSR + dso, (const unsigned char*)dsh + (r1 + 16) * DSR + dso);
+        const V8 dsl = tr8((const unsigned char*)dsl_ + r1 * DSR + dso, (const unsigned char*)dsl_ + (r1 + 16) * DSR + dso);
+#pragma unroll
+        for (int dt = 0; dt < DI / 16; ++dt) {
+          const int ch = 2 * dt + hb;
+          const V8 kt = tr8(s_ki + r1 * IROW + ((ch ^ nope_swz(r1)) * 16) + (li & 1) * 8,
+                            s_ki + (r1 + 16) * IROW + ((ch ^ nope_swz(r1 + 16)) * 16) + (li & 1) * 8);
+          acc_dqi[dt] = E::mfma(kt, dsf, acc_dqi[dt]);
+          acc_dqi[dt] = E::mfma(kt, dsl, acc_dqi[dt]);
+        }
+      }
       f32x4 acc[2][2] = {{{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}, {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}};
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
@@ -659,19 +670,19 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     }
   }
 
-  // ---- epilogue: dW, dQi, row maximum of |c| ----
+  // ---- epilogue: dW (waves 0-3), dQi (waves 4-7), row maximum of |c| ----
   if (iwave) {
     const float dwv = xgroup_sum(dw_acc);
     if (lg == 0 && gv) store_w(p.dw, grow, p.w_dtype, dwv);
-    if (gv) {
-      typedef T T4 __attribute__((ext_vector_type(4)));
-      T* dst = (T*)p.dqi + grow * DI;
+  }
+  if (!dma_wave && gva) {
+    typedef T T4 __attribute__((ext_vector_type(4)));
+    T* dst = (T*)p.dqi + grow * DI;
 #pragma unroll
-      for (int dt = 0; dt < DI / 16; ++dt) {
-        const T4 o = {E::from_f32(acc_dqi[dt][0] * ds_unscale), E::from_f32(acc_dqi[dt][1] * ds_unscale),
-                      E::from_f32(acc_dqi[dt][2] * ds_unscale), E::from_f32(acc_dqi[dt][3] * ds_unscale)};
-        *(T4*)(dst + dt * 16 + lg * 4) = o;
-      }
+    for (int dt = 0; dt < DI / 16; ++dt) {
+      const T4 o = {E::from_f32(acc_dqi[dt][0] * ds_unscale), E::from_f32(acc_dqi[dt][1] * ds_unscale),
+                    E::from_f32(acc_dqi[dt][2] * ds_unscale), E::from_f32(acc_dqi[dt][3] * ds_unscale)};
+      *(T4*)(dst + dt * 16 + lg * 4) = o;
     }
   }
   cmax = wave_max(cmax);
