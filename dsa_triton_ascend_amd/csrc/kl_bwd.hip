@@ -537,7 +537,7 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   f32x4 acc_dqi[DI / 16];
 #pragma unroll
   for (int dt = 0; dt < DI / 16; ++dt) acc_dqi[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  float dw_acc = 0.f, cmax = 0.f;
+  float dw_acc = 0.f, cmax = 0.f, cnan = 0.f;
   const bool dma_wave = wave < 4;
   auto issue_c = [&](int t) {
     const unsigned base = (unsigned)(uintptr_t)(pc_ki + (t % kKlPcBufs) * kKlPcKiBytes);
@@ -660,6 +660,7 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
             for (int r = 0; r < 4; ++r) {
               const float c = acc[tt][ct][r] * ds_unscale;
               cmax = fmaxf(cmax, fabsf(c));
+              cnan = fmaf(c, 0.f, cnan);  // NaN once any contribution is not finite
               h[r] = (_Float16)(c * c_scale);
             }
             *(uint2*)(p.cbuf + ((int64_t)row * p.topk + k) * DI + (wave & 3) * 32 + ct * 16 + lg * 4) =
@@ -685,6 +686,9 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
       *(T4*)(dst + dt * 16 + lg * 4) = o;
     }
   }
+  // a non-finite contribution makes the row maximum infinite, which turns
+  // its tokens' dKi into NaN in the reduction
+  cmax = cnan == 0.f ? cmax : INFINITY;
   cmax = wave_max(cmax);
   lds_barrier();
   if (lane == 0) s_misc[wave] = cmax;
@@ -815,11 +819,11 @@ __global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, co
       const int L = (len + np - 1) / np;
       const int i1 = min(len, (part + 1) * L);
       // A contribution is c16 * 2^-e_row; its fixed-point value is
-      // round(c16 * 2^(e - e_row)), exact through double (a branch-free
-      // conversion: an integer shift-and-round per element diverges and runs
-      // slower).  64 list entries and their row exponents come in with one
-      // load per lane and are broadcast with readlane; 16 contribution rows
-      // are in flight at a time.
+      // round(c16 * 2^(e - e_row)), exact through double (an integer
+      // shift-and-round per element measured slower, with branches and
+      // branch-free).  64 list entries and their row exponents come in with
+      // one load per lane and are broadcast with readlane; 16 contribution
+      // rows are in flight at a time.
       typedef _Float16 h2 __attribute__((ext_vector_type(2)));
       constexpr int U = 16;
       for (int base = part * L; base < i1; base += 64) {

@@ -362,7 +362,8 @@ __global__ __launch_bounds__(kGenThreads) void kl_gen_row_kernel(KlGenParams p) 
             H8 h;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-              cmax = fmaxf(cmax, fabsf(a[e]));
+              // non-finite: an infinite row maximum (NaN dKi for its tokens)
+              cmax = a[e] - a[e] == 0.f ? fmaxf(cmax, fabsf(a[e])) : INFINITY;
               h[e] = (_Float16)(a[e] * c_scale);
             }
             *(H8*)(p.cbuf + ((int64_t)row * p.topk + k) * di + c * 8) = h;

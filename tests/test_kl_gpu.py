@@ -311,6 +311,33 @@ def test_kl_generic_path_at_fused_shapes(case):
         assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("generic", [False, True], ids=["fused", "generic"])
+def test_kl_nan_weight_poisons_exactly_its_tokens(generic):
+    """A NaN weight in one query row makes that row's dS NaN, so the dKi of
+    exactly the tokens the row attends is NaN (as in the reference, whose
+    fp32 atomics add the NaN in); every other dKi entry stays finite and
+    matches the clean run.  The reduction sums in fixed point, where NaN has
+    no representation: a non-finite contribution marks its row maximum
+    infinite, which the reduction turns into NaN for the row's tokens."""
+    from dsa_triton_ascend_amd import _lib
+    print(f"[kl_bwd] NaN weight generic={generic}", flush=True)
+    c = _case(1, 24, 96, 32, 128, 16, 48, torch.bfloat16, "causal_random")
+    run = (lambda: _with_flags(_lib.TEST_KL_GENERIC, lambda: _run_gpu(c))) if generic else (lambda: _run_gpu(c))
+    clean = run()
+    s = 20
+    c["w"] = c["w"].copy()
+    c["w"][0, s, 3] = np.nan
+    got = run()
+    dki, dki0 = got[1][0, :, 0], clean[1][0, :, 0]
+    S2 = c["k"].shape[1]
+    n = min(48, S2 - 24 + s + 1)
+    hit = np.zeros(S2, bool)
+    hit[np.clip(c["si"][0, s, 0, :n], 0, S2 - 1)] = True
+    assert np.isnan(dki[hit]).all(), "tokens attended by the NaN row must be NaN"
+    assert np.isfinite(dki[~hit]).all(), "tokens not attended by the NaN row must stay finite"
+    np.testing.assert_array_equal(dki[~hit], dki0[~hit])
+
+
 def test_kl_guards():
     import dsa_triton_ascend_amd as dsa
     z = lambda *s: torch.zeros(*s, dtype=torch.bfloat16, device="cuda")  # noqa: E731
