@@ -537,7 +537,7 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   f32x4 acc_dqi[DI / 16];
 #pragma unroll
   for (int dt = 0; dt < DI / 16; ++dt) acc_dqi[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  float dw_acc = 0.f, cmax = 0.f, cnan = 0.f;
+  float dw_acc = 0.f, cmax = 0.f;
   const bool dma_wave = wave < 4;
   auto issue_c = [&](int t) {
     const unsigned base = (unsigned)(uintptr_t)(pc_ki + (t % kKlPcBufs) * kKlPcKiBytes);
@@ -659,8 +659,7 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const float c = acc[tt][ct][r] * ds_unscale;
-              cmax = fmaxf(cmax, fabsf(c));
-              cnan = fmaf(c, 0.f, cnan);  // NaN once any contribution is not finite
+              cmax = __builtin_elementwise_maximum(cmax, fabsf(c));  // NaN-propagating
               h[r] = (_Float16)(c * c_scale);
             }
             *(uint2*)(p.cbuf + ((int64_t)row * p.topk + k) * DI + (wave & 3) * 32 + ct * 16 + lg * 4) =
@@ -686,9 +685,9 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
       *(T4*)(dst + dt * 16 + lg * 4) = o;
     }
   }
-  // a non-finite contribution makes the row maximum infinite, which turns
-  // its tokens' dKi into NaN in the reduction
-  cmax = cnan == 0.f ? cmax : INFINITY;
+  // a non-finite contribution (NaN kept by the maximum above) makes the row
+  // maximum infinite, which turns its tokens' dKi into NaN in the reduction
+  cmax = cmax < INFINITY ? cmax : INFINITY;
   cmax = wave_max(cmax);
   lds_barrier();
   if (lane == 0) s_misc[wave] = cmax;

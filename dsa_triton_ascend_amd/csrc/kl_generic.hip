@@ -362,8 +362,7 @@ __global__ __launch_bounds__(kGenThreads) void kl_gen_row_kernel(KlGenParams p) 
             H8 h;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-              // non-finite: an infinite row maximum (NaN dKi for its tokens)
-              cmax = a[e] - a[e] == 0.f ? fmaxf(cmax, fabsf(a[e])) : INFINITY;
+              cmax = __builtin_elementwise_maximum(cmax, fabsf(a[e]));  // NaN-propagating
               h[e] = (_Float16)(a[e] * c_scale);
             }
             *(H8*)(p.cbuf + ((int64_t)row * p.topk + k) * di + c * 8) = h;
@@ -412,7 +411,9 @@ __global__ __launch_bounds__(kGenThreads) void kl_gen_row_kernel(KlGenParams p) 
     for (int s = 0; s < TL; ++s) a += s_ds[s * DSR + g];
     store_w(p.dw, (int64_t)row * ni + g, p.w_dtype, a);
   }
-  cmax = block_max4(cmax, s_red);
+  // a non-finite contribution (NaN kept above) makes the row maximum
+  // infinite: NaN dKi for the row's tokens in the reduction
+  cmax = block_max4(cmax < INFINITY ? cmax : INFINITY, s_red);
   if (tid == 0) {
     p.loss_part[row] = kl;
     p.rowmax[row] = cmax;

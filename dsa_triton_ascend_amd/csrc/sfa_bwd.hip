@@ -603,11 +603,14 @@ __global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) 
           }
       }
       // the slice's largest magnitude for token li (lanes li, li+16, li+32, li+48)
+      // (a NaN-propagating maximum, so that a NaN value is flagged too; a
+      // non-finite lane reads as infinite in the cross-lane reduction)
       float mx = 0.f;
 #pragma unroll
       for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, fabsf(acc[i][r]));
+        for (int r = 0; r < 4; ++r) mx = __builtin_elementwise_maximum(mx, fabsf(acc[i][r]));
+      mx = mx < INFINITY ? mx : INFINITY;
       mx = xgroup_max(mx);
       // stored value = acc * 2^-e with 2^e > max |acc| (|stored| < 1)
       int e = 0;

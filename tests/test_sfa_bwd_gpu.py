@@ -198,6 +198,55 @@ def _with_flags(flags, fn):
         lib.dsa_set_test_flags(0)
 
 
+@pytest.mark.parametrize("merge", [False, True], ids=["dk_dv", "merged"])
+def test_bwd_nan_in_one_row_reaches_exactly_its_tokens(merge):
+    """A NaN in one query row's d_out (one head, one column) makes that
+    row's dS NaN for the head, so the key gradients of exactly the tokens
+    the row attends carry NaN: all dK / dK_rope columns (as in the
+    reference), and at least the d_out column in dV.  The records are summed
+    in fixed point, which has no NaN: a record slice holding a non-finite
+    value is flagged and its token's slice is written as NaN.  Every other
+    token's gradients stay finite and equal to a clean run's."""
+    from dsa_triton_ascend_amd.sparse_flash_attention import INT64_MAX
+    from dsa_triton_ascend_amd.sparse_flash_attention_grad import _sfa_grad
+    print(f"[sfa_bwd] NaN row merge={merge}", flush=True)
+    dtype = torch.bfloat16
+    q, k, qr, kr, si, do, out, smax, ssum, scale, mode, bs = _random_case(CASES[5], dtype, seed=5)
+
+    def run(d_out):
+        res = _sfa_grad(dev(q, dtype), dev(k, dtype), dev(k, dtype), dev(si, torch.int32), dev(d_out, dtype),
+                        dev(out, dtype), dev(smax, torch.float32), dev(ssum, torch.float32), scale, dev(qr, dtype),
+                        dev(kr, dtype), None, None, bs, "BSND", mode, INT64_MAX, INT64_MAX, False, merge_kv=merge)
+        torch.cuda.synchronize()
+        return [None if r is None else r.float().cpu().numpy() for r in res]
+    clean = run(do)
+    s, h = 30, 3
+    bad = do.copy()
+    bad[0, s, h, 0] = np.nan
+    got = run(bad)
+    S2 = k.shape[1]
+    n = min(si.shape[-1], S2 - q.shape[1] + s + 1)   # mode 3: the row's visible slots
+    toks = si[0, s, 0, :n]
+    hit = np.zeros(S2, bool)
+    hit[toks[(toks >= 0) & (toks < S2)]] = True
+    dk, dk0 = got[1][0, :, 0], clean[1][0, :, 0]
+    assert np.isnan(dk[hit]).all(), "dK of the tokens the NaN row attends"
+    assert np.isfinite(dk[~hit]).all()
+    np.testing.assert_array_equal(dk[~hit], dk0[~hit])
+    dkr = got[4][0, :, 0]
+    assert np.isnan(dkr[hit]).all() and np.isfinite(dkr[~hit]).all()
+    np.testing.assert_array_equal(dkr[~hit], clean[4][0, :, 0][~hit])
+    if not merge:
+        dv = got[2][0, :, 0]
+        assert np.isnan(dv[hit, 0]).all(), "dV's d_out column of the tokens the NaN row attends"
+        assert np.isfinite(dv[~hit]).all()
+        np.testing.assert_array_equal(dv[~hit], clean[2][0, :, 0][~hit])
+    dq = got[0][0]
+    assert np.isnan(dq[s, h]).all()
+    rows = np.arange(q.shape[1]) != s
+    np.testing.assert_array_equal(dq[rows], clean[0][0][rows])
+
+
 @pytest.mark.parametrize("case", [CASES[1], CASES[3], CASES[5]], ids=["b2s9", "d256bs2", "s40"])
 @pytest.mark.parametrize("merge", [False, True], ids=["dk_dv", "merged"])
 def test_bwd_row_chunks_match_one_chunk(case, merge):
