@@ -40,6 +40,12 @@ template <> struct Elem<bf16> {
   static __device__ __forceinline__ f32x4 mfma(v8 a, v8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
+  // 32x32 output, k = 16: A lane l holds row l%32, k 8*(l/32) .. +7; B lane
+  // l holds k 8*(l/32) .. +7 of column l%32; C register r of lane l is row
+  // 8*(r/4) + 4*(l/32) + r%4, column l%32
+  static __device__ __forceinline__ f32x16 mfma32(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
 };
 
 template <> struct Elem<f16> {
@@ -48,6 +54,9 @@ template <> struct Elem<f16> {
   static __device__ __forceinline__ f16 from_f32(float x) { return (f16)x; }
   static __device__ __forceinline__ f32x4 mfma(v8 a, v8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x16 mfma32(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
 };
 

@@ -18,11 +18,13 @@
 //  * kl_bwd_row_kernel: one workgroup of 8 waves per query row.  Pass A
 //    streams tiles of 32 slots (K, K_rope, K_index rows gathered straight
 //    into an LDS ring by LDS-DMA, the next tile's gather in flight during
-//    the current tile's MFMAs): each wave scores 16 heads of the teacher on
-//    MFMA (Q fragments resident in registers) and sums its heads'
-//    probabilities on MFMA; waves w and w + 4 score index heads
-//    16*(w mod 4) .. +15 for the two halves of the tile.  I and p of the row
-//    stay in LDS.  Pass B is the softmax/KL over the row.  Pass C re-streams
+//    the current tile's MFMAs).  Waves 0-3 compute: each scores 32 heads of
+//    the teacher on the 32x32x16 MFMA (Q fragments resident in registers,
+//    log2 of each head's softmax denominator in LDS) and sums their
+//    probabilities per slot, then scores index heads 16*w .. +15 over the
+//    tile.  Waves 4-7 issue the next tile's gather and reduce the previous
+//    tile's partial sums into p and I.  I and p of the row stay in LDS.
+//    Pass B is the softmax/KL over the row.  Pass C re-streams
 //    K_index by LDS-DMA, pipelined over the tiles: waves 0-3 recompute a
 //    tile's index scores (cheaper than storing Nidx1 x topK ReLUs), form
 //    dS and accumulate dW, while waves 4-7 take the previous tile: dQi
@@ -72,7 +74,9 @@ constexpr int kKlTile = 32;
 constexpr int kKlDi = 128;
 constexpr int kKlWaves = 8;
 constexpr int kKlMaxNidx = 64;
-constexpr int kKlMaxTopk = 8192;
+// the row's I, p and token arrays (12 bytes per slot) share the LDS with
+// the static arrays (about 21 KB) and the ring region (at most 50 KB)
+constexpr int kKlMaxTopk = 7168;
 constexpr int kKlDsRow = kKlMaxNidx + 8;  // padded LDS row of dS^T (elements)
 // Pass C's use of the ring region: four K_index tile buffers (32 rows of
 // 128 bf16/fp16) and the dS^T hi / lo tiles of two consecutive tiles.
@@ -126,6 +130,11 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   // [0, 8) and [8, 16): per-wave pass-B sums / maxima; [16]: fp16 weight
   // max; [17, 25): per-wave max |Qi|
   __shared__ float s_misc[3 * kKlWaves + 4];
+  __shared__ __attribute__((aligned(16))) float s_m2p[128];  // pass A: per-head offset of the teacher exponent
+  // the row's index queries (kKlMaxNidx heads, rows padded by 16 bytes so
+  // that 16 heads' 16-byte reads hit distinct banks; heads >= Nidx1 zero)
+  constexpr int QIR = DI + 8;
+  __shared__ __attribute__((aligned(16))) T s_qi[kKlMaxNidx * QIR];
   // dynamic: the ring region (pass A's p.ring tile buffers of BUF bytes;
   // pass C's K_index tiles and dS^T tiles), then I (then dI) and p of the
   // row, and its clamped token rows
@@ -157,31 +166,39 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   const u32x4 z4 = {0u, 0u, 0u, 0u};
 
   // ---- resident fragments ----
-  const int head = wave * 16 + li;
-  const bool hv = head < p.n1;
-  const bool wave_heads = wave * 16 < p.n1;
-  const int64_t hrow = (int64_t)row * p.n1 + (hv ? head : 0);
-  V8 qf[KS];
+  // pass A teacher: waves 0-3 take heads 32*wave .. +31 on
+  // v_mfma_f32_32x32x16 (A operand: head 32*wave + lane%32, k-step ks = d
+  // 16*ks + 8*(lane/32) .. +7, nope k-steps then rope)
+  constexpr int KS16 = (D + DR) / 16, KSN16 = D / 16;
+  const bool twave = wave < 4;
+  const bool wave_heads = twave && wave * 32 < p.n1;
+  const int thead = wave * 32 + (lane & 31);
+  const bool thv = twave && thead < p.n1;
+  const int64_t throw_ = (int64_t)row * p.n1 + (thv ? thead : 0);
+  V8 qf[KS16];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    u32x4 v;
-    if (ks < KSN) v = *(const u32x4*)((const T*)p.q + hrow * D + ks * 32 + lg * 8);
-    else v = *(const u32x4*)((const T*)p.qr + hrow * DR + (ks - KSN) * 32 + lg * 8);
-    qf[ks] = as_v8<V8>(hv ? v : z4);
+  for (int ks = 0; ks < KS16; ++ks) {
+    const int d8 = (lane >> 5) * 8;
+    u32x4 v = z4;
+    if (thv) {
+      if (ks < KSN16) v = *(const u32x4*)((const T*)p.q + throw_ * D + ks * 16 + d8);
+      else v = *(const u32x4*)((const T*)p.qr + throw_ * DR + (ks - KSN16) * 16 + d8);
+    }
+    qf[ks] = as_v8<V8>(v);
   }
-  // pass A scores heads on MFMA rows: this lane's heads are 16*wave + 4*lg + r
-  float m2r[4], invr[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int h = wave * 16 + lg * 4 + r;
+  // C register r of the 32x32 product is head 32*wave + 8*(r/4) + 4*(lane/32)
+  // + r%4 (column: slot lane%32).  p = exp2(s*scale*log2e - m2 - log2(l +
+  // 1e-8)): the max and the normalisation fold into one offset; +inf masks
+  // heads >= N1
+  // (kept in LDS, s_m2p[head], and read per tile)
+  for (int h = tid; h < 128; h += NT) {
     const bool v = h < p.n1;
     const int64_t hr = (int64_t)row * p.n1 + (v ? h : 0);
-    m2r[r] = v ? p.smax[hr] * kLog2e : 0.f;
-    invr[r] = v ? 1.f / (p.ssum[hr] + 1e-8f) : 0.f;  // 0 also masks heads >= N1
+    s_m2p[h] = v ? p.smax[hr] * kLog2e + __log2f(p.ssum[hr] + 1e-8f) : INFINITY;
   }
   // index heads 16*hg4 .. +15 (hg4 = wave mod 4), g = 16*hg4 + li.  Pass A
-  // scores them on waves w and w + 4, slots 0-15 and 16-31 of the tile;
-  // pass C runs them on waves 0-3 (iwave).
+  // scores them on wave hg4 (both halves of the tile); pass C on waves hg4
+  // (scores, dS, dW) and 4 + hg4 (dQi, contributions).
   const int hg4 = wave & 3;
   const bool ihg = hg4 * 16 < p.nidx;
   const bool iwave = wave < 4 && ihg;
@@ -189,12 +206,14 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
   const bool gva = ihg && g < p.nidx;
   const bool gv = iwave && gva;
   const int64_t grow = (int64_t)row * p.nidx + (gva ? g : 0);
-  V8 qif[DI / 32];
-#pragma unroll
-  for (int ks = 0; ks < DI / 32; ++ks) {
-    const u32x4 v = *(const u32x4*)((const T*)p.qi + grow * DI + ks * 32 + lg * 8);
-    qif[ks] = as_v8<V8>(gva ? v : z4);
+  // index Q fragments (A operand of the index scores: head g, d 32*ks +
+  // 8*lg ..) from the row's index queries staged in LDS
+  for (int e = tid; e < kKlMaxNidx * (DI / 8); e += NT) {
+    const int gg = e / (DI / 8), c = e - gg * (DI / 8);
+    const u32x4 v = gg < p.nidx ? *(const u32x4*)((const T*)p.qi + ((int64_t)row * p.nidx + gg) * DI + c * 8) : z4;
+    *(u32x4*)&s_qi[gg * QIR + c * 8] = v;
   }
+  auto qif_load = [&](int ks) -> V8 { return as_v8<V8>(*(const u32x4*)&s_qi[g * QIR + ks * 32 + lg * 8]); };
   const float wg = gv ? load_w(p.w, grow, p.w_dtype) : 0.f;
   float wr[4];  // weights of index heads 16*hg4 + 4*lg + r (pass A layout)
 #pragma unroll
@@ -202,21 +221,6 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     const int gg = hg4 * 16 + lg * 4 + r;
     wr[r] = (ihg && gg < p.nidx) ? load_w(p.w, (int64_t)row * p.nidx + gg, p.w_dtype) : 0.f;
   }
-  // A operand of c^T = Qi^T . dS for the 32 columns 32*(wave & 3) + 16*ct
-  // + li that pass C gives waves 4-7: Qi[g 32*ks + 8*lg + j][column]
-  V8 qib[2][kKlMaxNidx / 32];
-#pragma unroll
-  for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-    for (int ks = 0; ks < kKlMaxNidx / 32; ++ks) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int gg = ks * 32 + lg * 8 + j;
-        T v = E::from_f32(0.f);
-        if (gg < p.nidx) v = ((const T*)p.qi)[((int64_t)row * p.nidx + gg) * DI + (wave & 3) * 32 + ct * 16 + li];
-        qib[ct][ks][j] = v;
-      }
-    }
   // per-wave partial sums of a tile; waves without heads keep zeros
   for (int e = tid; e < 2 * kKlWaves * TILE; e += NT) (&s_red[0][0][0])[e] = 0.f;
   for (int e = tid; e < 2 * 4 * TILE; e += NT) (&s_redi[0][0][0])[e] = 0.f;
@@ -235,186 +239,201 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     const int v = s_tok[k < n ? k : n - 1];
     return k < n ? v : -1;
   };
-  // Tile t into ring buffer b: wave w issues K DMAs w, w+8, ..., rope DMA w
-  // (w < RD) and K_index DMA w.  A lane's 16 bytes land at its fixed slot
-  // of the buffer; it loads the source chunk that the XOR swizzle puts
-  // there (LDS chunk c of a row holds source chunk c ^ swz), so reads use
-  // the same addressing as a swizzled store would.
-  // The token ids of a tile are read from LDS first: the DMA asm is a
-  // compiler memory barrier, so a read placed between two DMAs would wait
-  // for its own LDS round trip.
-  constexpr int NKW = (KD + kKlWaves - 1) / kKlWaves, NIW = (ID + kKlWaves - 1) / kKlWaves;
-  constexpr int NDA = NKW + 1 + NIW;  // DMA positions of a wave: K, rope, K_index
-  // the slots a lane gathers: K DMA u row, rope row, K_index DMA v row
-  auto tk_k = [&](int u) { return (u * kKlWaves + wave) * TPK + lane / CN; };
-  auto tk_r = [&]() { return wave * 8 + (lane >> 3); };
-  auto tk_i = [&](int v) { return (v * kKlWaves + wave) * TPI + lane / CI; };
-  struct TokA {
-    int tok_k[NKW], tok_i[NIW], tok_r;
-  };
-  auto tokens_a = [&](int t) {
-    TokA x;
-    x.tok_r = -1;
+  // Tile t into ring buffer b, gathered by waves 4-7 (iw = wave - 4): K
+  // DMAs iw, iw+4, ..., rope DMA iw (iw < RD) and K_index DMAs iw, iw+4.  A
+  // lane's 16 bytes land at its fixed slot of the buffer; it loads the
+  // source chunk that the XOR swizzle puts there (LDS chunk c of a row holds
+  // source chunk c ^ swz), so reads use the same addressing as a swizzled
+  // store would.  A wave stalls at each DMA it issues while the CU's load
+  // path is busy; on waves 4-7 those stalls leave the teacher waves 0-3 of
+  // the same SIMDs running their MFMAs.  The token ids of a tile are read
+  // from LDS first: the DMA asm is a compiler memory barrier, so a read
+  // placed between two DMAs would wait for its own LDS round trip.
+  constexpr int NIS = 4;
+  static_assert(RD <= NIS, "one rope DMA per issuing wave");
+  const int iw = wave - NIS;
+  const bool a_issuer = iw >= 0;
+  constexpr int NKW = (KD + NIS - 1) / NIS, NIW = (ID + NIS - 1) / NIS;
+  auto issue_a = [&](int t, int b) {
+    const unsigned base = (unsigned)(uintptr_t)(ring + b * BUF);
+    int tk_k[NKW], tok_k[NKW], tk_i[NIW], tok_i[NIW], tk_r = 0, tok_r = -1;
 #pragma unroll
     for (int u = 0; u < NKW; ++u) {
-      const int j = u * kKlWaves + wave;
-      x.tok_k[u] = (KD % kKlWaves == 0 || j < KD) ? slot_tok(t * TILE + tk_k(u)) : -1;
+      const int j = u * NIS + iw;
+      tk_k[u] = j * TPK + lane / CN;
+      tok_k[u] = (KD % NIS == 0 || j < KD) ? slot_tok(t * TILE + tk_k[u]) : -1;
     }
-    if (DR > 0 && wave < RD) x.tok_r = slot_tok(t * TILE + tk_r());
+    if (DR > 0 && iw < RD) {
+      tk_r = iw * 8 + (lane >> 3);
+      tok_r = slot_tok(t * TILE + tk_r);
+    }
 #pragma unroll
-    for (int v = 0; v < NIW; ++v) {
-      const int j = v * kKlWaves + wave;
-      x.tok_i[v] = (ID % kKlWaves == 0 || j < ID) ? slot_tok(t * TILE + tk_i(v)) : -1;
+    for (int u = 0; u < NIW; ++u) {
+      const int j = u * NIS + iw;
+      tk_i[u] = j * TPI + lane / CI;
+      tok_i[u] = (ID % NIS == 0 || j < ID) ? slot_tok(t * TILE + tk_i[u]) : -1;
     }
-    return x;
-  };
-  // DMA position u of this wave (u < NKW: K DMA u; NKW: rope; then K_index)
-  auto fire_a = [&](const TokA& x, int b, int u) {
-    const unsigned base = (unsigned)(uintptr_t)(ring + b * BUF);
-    if (u < NKW) {
-      const int j = u * kKlWaves + wave;
-      if (KD % kKlWaves == 0 || j < KD) {
-        const int ch = (lane % CN) ^ nope_swz(tk_k(u));
-        kl_dma16(base + j * 1024, x.tok_k[u] >= 0 ? (const void*)(kb + (int64_t)x.tok_k[u] * ROW + ch * 16)
-                                                  : (const void*)(g_kl_zero_row + ch * 16));
+#pragma unroll
+    for (int u = 0; u < NKW; ++u) {
+      const int j = u * NIS + iw;
+      if (KD % NIS == 0 || j < KD) {
+        const int ch = (lane % CN) ^ nope_swz(tk_k[u]);
+        kl_dma16(base + j * 1024, tok_k[u] >= 0 ? (const void*)(kb + (int64_t)tok_k[u] * ROW + ch * 16)
+                                                : (const void*)(g_kl_zero_row + ch * 16));
       }
-    } else if (u == NKW) {
-      if (DR > 0 && wave < RD) {
-        const int ch = (lane & 7) ^ rope_swz(tk_r());
-        kl_dma16(base + BUF_K + wave * 1024, x.tok_r >= 0 ? (const void*)(krb + (int64_t)x.tok_r * (DR * 2) + ch * 16)
-                                                          : (const void*)(g_kl_zero_row + ch * 16));
-      }
-    } else {
-      const int v = u - NKW - 1;
-      const int j = v * kKlWaves + wave;
-      if (ID % kKlWaves == 0 || j < ID) {
-        const int ch = (lane % CI) ^ nope_swz(tk_i(v));
+    }
+    if (DR > 0 && iw < RD) {
+      const int ch = (lane & 7) ^ rope_swz(tk_r);
+      kl_dma16(base + BUF_K + iw * 1024, tok_r >= 0 ? (const void*)(krb + (int64_t)tok_r * (DR * 2) + ch * 16)
+                                                    : (const void*)(g_kl_zero_row + ch * 16));
+    }
+#pragma unroll
+    for (int u = 0; u < NIW; ++u) {
+      const int j = u * NIS + iw;
+      if (ID % NIS == 0 || j < ID) {
+        const int ch = (lane % CI) ^ nope_swz(tk_i[u]);
         kl_dma16(base + BUF_K + BUF_R + j * 1024,
-                 x.tok_i[v] >= 0 ? (const void*)(kib + (int64_t)x.tok_i[v] * IROW + ch * 16)
-                                 : (const void*)(g_kl_zero_row + ch * 16));
+                 tok_i[u] >= 0 ? (const void*)(kib + (int64_t)tok_i[u] * IROW + ch * 16)
+                               : (const void*)(g_kl_zero_row + ch * 16));
       }
     }
-  };
-  auto issue_a = [&](int t, int b) {
-    const TokA x = tokens_a(t);
-#pragma unroll
-    for (int u = 0; u < NDA; ++u) fire_a(x, b, u);
   };
 
   // One barrier per tile.  With two buffers, tile t+1 is issued right
   // after tile t's barrier into the buffer tile t-1 used (every wave is past
   // it); with one, after a second barrier behind the tile's MFMAs.  The loop
-  // has no other global memory traffic, so vmcnt(0) waits for exactly this
-  // wave's share of the tile.  The per-slot sums of tile t-1 (complete at
-  // tile t's barrier) are reduced by wave 0 while the others start tile t;
-  // the partial-sum buffers alternate, and wave 0 has reduced tile t-2 from
-  // a buffer before any wave passes tile t's barrier to overwrite it.
+  // has no other global memory traffic, so vmcnt(0) waits for exactly the
+  // issuing wave's share of the tile.  The per-slot sums of tile t-1
+  // (complete at tile t's barrier) are reduced by wave 4 while the others
+  // start tile t; the partial-sum buffers alternate, and wave 4 has reduced
+  // tile t-2 from a buffer before any wave passes tile t's barrier to
+  // overwrite it.
   auto reduce_a = [&](int t) {
-    if (tid < TILE) {
-      const int k = t * TILE + tid;
+    const int q = tid - NIS * 64;
+    if (q >= 0 && q < TILE) {
+      const int k = t * TILE + q;
       if (k < n) {
         float ps = 0.f, is = 0.f;
 #pragma unroll
-        for (int w2 = 0; w2 < kKlWaves; ++w2) ps += s_red[t & 1][w2][tid];
+        for (int w2 = 0; w2 < 4; ++w2) ps += s_red[t & 1][w2][q];
 #pragma unroll
-        for (int w2 = 0; w2 < 4; ++w2) is += s_redi[t & 1][w2][tid];
+        for (int w2 = 0; w2 < 4; ++w2) is += s_redi[t & 1][w2][q];
         s_p[k] = ps * (1.f / (float)p.n1);
         s_I[k] = is;
       }
     }
   };
-  issue_a(0, 0);
+  if (a_issuer) issue_a(0, 0);
   for (int t = 0; t < nt; ++t) {
     const int b = p.ring == 2 ? (t & 1) : 0;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     lds_barrier();
-    // with two buffers the next tile's DMAs are spread over the teacher
-    // MFMAs (one every DSTEP steps): a wave stalls at each DMA it issues
-    // while the CU's gather path is busy, and spread out the stalls overlap
-    // the other wave's MFMAs on the SIMD
-    const bool pre = p.ring == 2 && t + 1 < nt;
-    TokA nx;
-    if (pre) nx = tokens_a(t + 1);
-    if (pre && !wave_heads) {
-#pragma unroll
-      for (int u = 0; u < NDA; ++u) fire_a(nx, b ^ 1, u);
-    }
+    if (a_issuer && p.ring == 2 && t + 1 < nt) issue_a(t + 1, b ^ 1);
     if (t > 0) reduce_a(t - 1);
     const unsigned char* s_k = ring + b * BUF;
     const unsigned char* s_kr = s_k + BUF_K;
     const unsigned char* s_kia = s_k + BUF_K + BUF_R;
 
-    // Scores as S[head][slot] = Q . K^T (heads on MFMA rows, C register r =
-    // head 4*lg + r, column = slot li).  That C layout is the A layout of
-    // v_mfma_16x16x16 ([slot][head], k = 4*lg + j), so the sum over the
-    // wave's 16 heads is one more product with a ones matrix, run on an
-    // exact three-part bf16 split of the fp32 terms (fp32-level sums without
-    // cross-lane traffic).
+    // Teacher scores S[head][slot] = Q . K^T for the wave's 32 heads on
+    // v_mfma_f32_32x32x16: B operand K[slot lane%32][d 16*ks + 8*(lane/32)
+    // .. +7], one 16-byte LDS read per lane and k-step.  A lane's 16 results
+    // are 16 heads of slot lane%32; their probabilities sum in the lane and
+    // then with lane lane^32 (the other 16 heads).
     if (wave_heads) {
-      f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-      // K fragments of step st = 2*ks + tt, read PF steps ahead of their
-      // MFMA; the scheduling barrier after each MFMA keeps the reads where
-      // they are (sunk next to their MFMAs, every MFMA would wait out a full
-      // LDS round trip)
-      constexpr int NS = 2 * KS, PF = 4, DSTEP = NS / NDA;
-      static_assert(DSTEP >= 1, "DMA spacing");
-      auto a_read = [&](int st) -> u32x4 {
-        const int ks = st >> 1, tk = (st & 1) * 16 + li;
+      f32x16 acc = {};
+      // K fragments read PF k-steps ahead of their MFMA; the scheduling
+      // barrier after each MFMA keeps the reads there (one wave per SIMD
+      // runs these MFMAs: nothing else hides an LDS round trip)
+      constexpr int PF = 4;
+      // chunk 2*ks + hf of slot sl sits at (2*ks + hf) ^ swz(sl); with the
+      // swizzle below 16 that is 16*(ks/8) + ((2*(ks%8)) ^ (hf ^ swz)): eight
+      // lane offsets plus an immediate (nope), four for the rope rows
+      const int sl = lane & 31, hf = lane >> 5;
+      const int xn = hf ^ nope_swz(sl), xr = hf ^ rope_swz(sl);
+      auto a_read = [&](int ks) -> u32x4 {
         const unsigned char* a =
-            ks < KSN ? s_k + tk * ROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16)
-                     : s_kr + tk * (DR * 2) + ((((ks - KSN) * 4 + lg) ^ rope_swz(tk)) * 16);
+            ks < KSN16 ? s_k + sl * ROW + (ks >> 3) * 256 + (((2 * (ks & 7)) ^ xn) * 16)
+                       : s_kr + sl * (DR * 2) + (((2 * (ks - KSN16)) ^ xr) * 16);
         return *(const u32x4*)a;
       };
       u32x4 fa[PF];
 #pragma unroll
       for (int i = 0; i < PF; ++i) fa[i] = a_read(i);
 #pragma unroll
-      for (int st = 0; st < NS; ++st) {
-        const V8 av = as_v8<V8>(fa[st % PF]);
-        if (st + PF < NS) fa[st % PF] = a_read(st + PF);
-        acc[st & 1] = E::mfma(qf[st >> 1], av, acc[st & 1]);
+      for (int ks = 0; ks < KS16; ++ks) {
+        const V8 bv = as_v8<V8>(fa[ks % PF]);
+        if (ks + PF < KS16) fa[ks % PF] = a_read(ks + PF);
+        acc = E::mfma32(qf[ks], bv, acc);
         __builtin_amdgcn_sched_barrier(0);
-        if (pre && st % DSTEP == DSTEP - 1 && st / DSTEP < NDA) {
-          fire_a(nx, b ^ 1, st / DSTEP);
-          __builtin_amdgcn_sched_barrier(0);
-        }
       }
+      float ps = 0.f;
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        const f32x4 mo = *(const f32x4*)&s_m2p[wave * 32 + 8 * r4 + 4 * hf];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ps += fast_exp2(acc[4 * r4 + r] * p.scale_log2 - mo[r]);
+      }
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ps), __float_as_uint(ps), false, false);
+      ps = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      if (lane < 32) s_red[t & 1][wave][lane] = ps;
+    }
+    // index scores I[slot] = sum_g w_g ReLU(qi_g . ki) on wave hg4 (after
+    // its teacher scores; waves 4-7 are busy with the gather): index heads
+    // 16*hg4 .. +15 for both halves of the tile
+    if (twave && ihg) {
+      // all twelve LDS reads first (query fragments, both halves' key
+      // fragments), so their round trips overlap
+      V8 qf_i[DI / 32];
+      u32x4 kfi[2][DI / 32];
+#pragma unroll
+      for (int ks = 0; ks < DI / 32; ++ks) qf_i[ks] = qif_load(ks);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int ks = 0; ks < DI / 32; ++ks) {
+          const int tk = tt * 16 + li;
+          kfi[tt][ks] = *(const u32x4*)(s_kia + tk * IROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16));
+        }
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < DI / 32; ++ks) acc = E::mfma(qf_i[ks], as_v8<V8>(kfi[tt][ks]), acc);
         Split3 sp;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) split3_set(sp, r, fast_exp2(acc[tt][r] * p.scale_log2 - m2r[r]) * invr[r]);
-        // sum[r] = sum over the wave's heads for slot tt*16 + 4*lg + r
+        for (int r = 0; r < 4; ++r) split3_set(sp, r, wr[r] * fmaxf(acc[r], 0.f));
         const f32x4 sum = split3_rowsum(sp);
-        if (li == 0) *(f32x4*)&s_red[t & 1][wave][tt * 16 + lg * 4] = sum;
+        if (li == 0) *(f32x4*)&s_redi[t & 1][hg4][tt * 16 + lg * 4] = sum;
       }
-    }
-    // index scores I[slot] = sum_g w_g ReLU(qi_g . ki): index heads 16*hg4
-    // .. +15 for slots 16*tt .. +15 of the tile, tt = wave / 4
-    if (ihg) {
-      const int tt = wave >> 2;
-      const int tk = tt * 16 + li;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < DI / 32; ++ks) {
-        const unsigned char* a = s_kia + tk * IROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16);
-        acc = E::mfma(qif[ks], as_v8<V8>(*(const u32x4*)a), acc);
-      }
-      Split3 sp;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) split3_set(sp, r, wr[r] * fmaxf(acc[r], 0.f));
-      const f32x4 sum = split3_rowsum(sp);
-      if (li == 0) *(f32x4*)&s_redi[t & 1][hg4][tt * 16 + lg * 4] = sum;
     }
     if (p.ring == 1 && t + 1 < nt) {
       lds_barrier();
-      issue_a(t + 1, 0);
+      if (a_issuer) issue_a(t + 1, 0);
     }
   }
   lds_barrier();
   reduce_a(nt - 1);
   lds_barrier();
 
+  // (loaded after pass A, where they would only hold registers)
+  V8 qif[DI / 32];
+#pragma unroll
+  for (int ks = 0; ks < DI / 32; ++ks) qif[ks] = qif_load(ks);
+  // A operand of c^T = Qi^T . dS for the 32 columns 32*(wave & 3) + 16*ct
+  // + li that pass C gives waves 4-7: Qi[g 32*ks + 8*lg + j][column]
+  V8 qib[2][kKlMaxNidx / 32];
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+    for (int ks = 0; ks < kKlMaxNidx / 32; ++ks) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int gg = ks * 32 + lg * 8 + j;
+        T v = E::from_f32(0.f);
+        if (gg < p.nidx) v = ((const T*)p.qi)[((int64_t)row * p.nidx + gg) * DI + (wave & 3) * 32 + ct * 16 + li];
+        qib[ct][ks][j] = v;
+      }
+    }
   // ================= pass B: softmax(I), dI, KL =================
   float mx = -INFINITY;
   for (int k = tid; k < n; k += NT) mx = fmaxf(mx, s_I[k]);

@@ -15,7 +15,7 @@ reference; every output of this implementation is deterministic.
 
 Index shapes: D_idx any multiple of 8 up to 256, Nidx1 up to 128, any topK
 (rows x topK < 2^31); the reference loops over any D_idx and Nidx1
-(119-136, 219-262).  D_idx = 128, Nidx1 <= 64 and topK <= 8192 run the
+(119-136, 219-262).  D_idx = 128, Nidx1 <= 64 and topK <= 7168 run the
 fused row kernel, other shapes a generic path with the same outputs.
 
 Extensions over the reference, which accepts BSND only (534-535):

@@ -207,7 +207,7 @@ size_t dsa_sfa_bwd_workspace_size(int64_t q_rows, int64_t kv_rows, int64_t n1, i
  * kv_rows * d_idx int64 accumulators.  query/key/rope/index tensors share
  * one dtype (bf16 or fp16); D in {128, 256, 512}; N1 <= 128; d_idx a
  * multiple of 8 up to 256; Nidx1 <= 128; topK up to 2^20 with rows * topK
- * < 2^31.  d_idx = 128, Nidx1 <= 64 and topK <= 8192 run one fused row
+ * < 2^31.  d_idx = 128, Nidx1 <= 64 and topK <= 7168 run one fused row
  * kernel; other shapes a generic path with the same outputs.
  */
 int dsa_kl_bwd(const void* query, const void* key, const void* query_rope, const void* key_rope,

@@ -249,7 +249,7 @@ def test_kl_large_rows_sampled():
 
 # ---------------------------------------------------------------------------
 # the generic path: index shapes outside the fused row kernel (d_idx != 128,
-# Nidx1 > 64, topK > 8192), which the reference's loops take
+# Nidx1 > 64, topK > 7168), which the reference's loops take
 # (sparse_lightning_indexer_grad_kl_loss_triton.py:119-136, 219-262)
 # ---------------------------------------------------------------------------
 GEN_CASES = [
@@ -273,7 +273,7 @@ def test_kl_generic_index_shapes(case, dtype):
 
 
 def test_kl_generic_topk_above_fused_limit():
-    """topK = 9000 (> 8192, the fused kernel's limit), no rope, bf16 weights, act lengths."""
+    """topK = 9000 (> 7168, the fused kernel's limit), no rope, bf16 weights, act lengths."""
     print("[kl_bwd generic] topK 9000", flush=True)
     c = _case(2, 3, 9100, 16, 128, 16, 9000, torch.bfloat16, "causal_random", rope=False,
               w_dtype=torch.bfloat16, act_q=[3, 2], act_k=[9100, 5000])
