@@ -234,19 +234,27 @@ __global__ __launch_bounds__(kDkThreads, 1) void dense_teacher_kernel(DkParams p
   using V8 = typename E::v8;
   constexpr int TILE = kDkTile;
   constexpr int NT = kDkThreads;
-  constexpr int KSN = D / 32, KSR = DR / 32, KS = KSN + KSR;
+  constexpr int KS16 = (D + DR) / 16, KSN16 = D / 16;
   constexpr int ROW = D * 2;
   constexpr int CN = D / 8, CR = DR / 8;
-  constexpr int NJ_N = TILE * CN / NT;
-  static_assert(TILE * CN == NJ_N * NT && TILE * CR <= NT, "tile assignment");
-  __shared__ __attribute__((aligned(16))) unsigned char s_k[TILE * ROW];
-  __shared__ __attribute__((aligned(16))) unsigned char s_kr[DR > 0 ? TILE * DR * 2 : 16];
-  __shared__ __attribute__((aligned(16))) float s_red[8][TILE];
+  constexpr int NF = NT / 2;  // feed threads (waves 4-7)
+  constexpr int NJ_N = TILE * CN / NF;
+  static_assert(TILE * CN == NJ_N * NF && TILE * CR <= NF, "tile assignment");
+  __shared__ __attribute__((aligned(16))) unsigned char s_k[2][TILE * ROW];
+  __shared__ __attribute__((aligned(16))) unsigned char s_kr[2][DR > 0 ? TILE * DR * 2 : 16];
+  __shared__ __attribute__((aligned(16))) float s_red[2][4][TILE];
+  __shared__ __attribute__((aligned(16))) float s_m2p[128];
+  __shared__ __attribute__((aligned(16))) int s_kvh[128];
+  // Q rope rows of the 128 heads (A operands of the last k-steps, read
+  // just before use: resident they would not fit beside the nope part);
+  // 144-byte rows keep a wave's 16-byte reads bank-conflict free
+  constexpr int QRR = DR + 8;
+  __shared__ __attribute__((aligned(16))) T s_qr[DR > 0 ? 128 * QRR : 8];
   __shared__ float s_wm[8];
+  __shared__ float s_kl, s_dmax;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int li = lane & 15, lg = lane >> 4;
   const int rows = p.batch * p.s1;
   const int row = rows - 1 - (int)blockIdx.x;  // long causal rows first
   const DkRow ri = dk_row(p, row);
@@ -265,34 +273,40 @@ __global__ __launch_bounds__(kDkThreads, 1) void dense_teacher_kernel(DkParams p
   const float inv_isum = 1.f / fmaxf(isum, 1e-8f);
   const u32x4 z4 = {0u, 0u, 0u, 0u};
 
-  // resident Q fragments: this lane's head 16*wave + li
-  const int head = wave * 16 + li;
-  const bool hv = head < p.n1;
-  const bool wave_heads = wave * 16 < p.n1;
-  const int64_t hrow = (int64_t)row * p.n1 + (hv ? head : 0);
-  V8 qf[KS];
+  // Waves 0-3 compute: wave w scores heads 32*w .. +31 on
+  // v_mfma_f32_32x32x16 (A operand: head 32*w + lane%32, k-step ks = d
+  // 16*ks + 8*(lane/32) .. +7, nope k-steps then rope; Q resident).  Waves
+  // 4-7 feed: they load the next tile into registers and write it into the
+  // two-buffer LDS ring, and wave 4 reduces the previous tile's partial sums
+  // into dI.  One barrier per item.
+  const bool cwave = wave < 4;
+  const bool wave_heads = cwave && wave * 32 < p.n1;
+  const int thead = wave * 32 + (lane & 31);
+  const bool thv = cwave && thead < p.n1;
+  const int64_t hrow = (int64_t)row * p.n1 + (thv ? thead : 0);
+  V8 qf[KSN16];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    u32x4 v;
-    if (ks < KSN) v = *(const u32x4*)((const T*)p.q + hrow * D + ks * 32 + lg * 8);
-    else v = *(const u32x4*)((const T*)p.qr + hrow * DR + (ks - KSN) * 32 + lg * 8);
-    qf[ks] = as_v8<V8>(hv ? v : z4);
+  for (int ks = 0; ks < KSN16; ++ks)
+    qf[ks] = as_v8<V8>(thv ? *(const u32x4*)((const T*)p.q + hrow * D + ks * 16 + (lane >> 5) * 8) : z4);
+  for (int e = tid; e < (DR > 0 ? 128 * (DR / 8) : 0); e += NT) {
+    const int h = e / (DR / 8), c = e - h * (DR / 8);
+    const int64_t hr = (int64_t)row * p.n1 + (h < p.n1 ? h : 0);
+    *(u32x4*)&s_qr[h * QRR + c * 8] = h < p.n1 ? *(const u32x4*)((const T*)p.qr + hr * DR + c * 8) : z4;
   }
-  // C-layout rows: heads 16*wave + 4*lg + r, their key head and statistics
-  float m2r[4], invr[4];
-  int kvh[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int h = wave * 16 + lg * 4 + r;
+  // per head: p = exp2(s*scale*log2e - m2 - log2(l + 1e-8)) (the max and the
+  // normalisation folded into one offset; +inf masks heads >= N1) and the
+  // key head, -1 past N1.  C register r of the 32x32 product is head 32*w +
+  // 8*(r/4) + 4*(lane/32) + r%4, column (key) lane%32.
+  for (int h = tid; h < 128; h += NT) {
     const bool v = h < p.n1;
     const int n2 = v ? h / p.g : 0, gg = v ? h - n2 * p.g : 0;
     const int64_t si = (((int64_t)ri.b * p.n2 + n2) * p.s1 + ri.s1) * p.g + gg;
-    m2r[r] = v ? p.smax[si] * kLog2e : 0.f;
-    invr[r] = v ? 1.f / (p.ssum[si] + 1e-8f) : 0.f;
-    kvh[r] = v ? n2 : -1;
+    s_m2p[h] = v ? p.smax[si] * kLog2e + __log2f(p.ssum[si] + 1e-8f) : INFINITY;
+    s_kvh[h] = v ? n2 : -1;
   }
-  const int n2_lo = wave_heads ? (wave * 16) / p.g : 0;
-  const int n2_hi = wave_heads ? (min(wave * 16 + 15, p.n1 - 1)) / p.g : -1;
+  for (int e = tid; e < 2 * 4 * TILE; e += NT) (&s_red[0][0][0])[e] = 0.f;
+  const int n2_lo = wave_heads ? (wave * 32) / p.g : 0;
+  const int n2_hi = wave_heads ? (min(wave * 32 + 31, p.n1 - 1)) / p.g : -1;
   // row maximum of |w| (fp16 dS scale)
   float wm = 0.f;
   for (int gg = tid; gg < p.nidx; gg += NT) wm = fmaxf(wm, fabsf(load_w(p.w, (int64_t)row * p.nidx + gg, p.w_dtype)));
@@ -302,120 +316,158 @@ __global__ __launch_bounds__(kDkThreads, 1) void dense_teacher_kernel(DkParams p
   const int nt = (ri.vis + TILE - 1) / TILE;
   const int items = nt * p.n2;
   // item i: tile i / N2, key head i % N2; key row (b*S2 + t)*N2 + n2
-  u32x4 pre_n[NJ_N], pre_r;
-  // the tile's index scores, read by the reducing threads one item ahead
-  // with the key rows (a load at the reduction would stall every tile)
-  float pre_i = 0.f, cur_i = 0.f;
+  const int f = tid - NF;  // feed thread index (>= 0 on waves 4-7)
+  // feed thread f loads 16-byte chunk ch0 of keys tk0 + TKS*j (nope) and
+  // chunk chr of key tkr (rope)
+  constexpr int TKS = NF / CN;
+  static_assert(NF % CN == 0 && (DR == 0 || NF == TILE * CR), "feed assignment");
+  const int fs = f >= 0 ? f : 0;
+  const int tk0 = fs / CN, ch0 = fs - tk0 * CN;
+  const int tkr = fs / (CR > 0 ? CR : 1), chr = fs - tkr * CR;
+  u32x4 pre_n[NJ_N], pre_r = z4;
+  // keys past the row's end load its last visible key instead: their
+  // scores are never reduced, and every load stays unconditional (a load
+  // under a lane branch makes the compiler wait for all earlier loads)
+  const int64_t rb = (int64_t)ri.b * p.s2;
   auto load_item = [&](int i) {
     const int t0 = (i / p.n2) * TILE, n2 = i - (i / p.n2) * p.n2;
-    if (tid < TILE && t0 + tid < ri.vis) pre_i = irow[t0 + tid];
 #pragma unroll
     for (int j = 0; j < NJ_N; ++j) {
-      const int e = tid + j * NT;
-      const int tk = e / CN, ch = e - tk * CN;
-      const int t = t0 + tk;
-      const int64_t kr = ((int64_t)ri.b * p.s2 + t) * p.n2 + n2;
-      pre_n[j] = t < ri.vis ? *(const u32x4*)(kb + kr * ROW + ch * 16) : z4;
+      const int t = min(t0 + tk0 + j * TKS, ri.vis - 1);
+      pre_n[j] = *(const u32x4*)(kb + ((rb + t) * p.n2 + n2) * ROW + ch0 * 16);
     }
     if (DR > 0) {
-      const int tk = tid / (CR > 0 ? CR : 1), ch = tid - tk * CR;
-      const int t = t0 + tk;
-      const int64_t kr = ((int64_t)ri.b * p.s2 + t) * p.n2 + n2;
-      pre_r = (tid < TILE * CR && t < ri.vis) ? *(const u32x4*)(krb + kr * (DR * 2) + ch * 16) : z4;
+      const int t = min(t0 + tkr, ri.vis - 1);
+      pre_r = *(const u32x4*)(krb + ((rb + t) * p.n2 + n2) * (DR * 2) + chr * 16);
     }
   };
-  auto store_item = [&]() {
+  auto store_item = [&](int b) {
 #pragma unroll
     for (int j = 0; j < NJ_N; ++j) {
-      const int e = tid + j * NT;
-      const int tk = e / CN, ch = e - tk * CN;
-      *(u32x4*)(s_k + tk * ROW + ((ch ^ nope_swz(tk)) * 16)) = pre_n[j];
+      const int tk = tk0 + j * TKS;
+      *(u32x4*)(s_k[b] + tk * ROW + ((ch0 ^ nope_swz(tk)) * 16)) = pre_n[j];
     }
-    if (DR > 0 && tid < TILE * CR) {
-      const int tk = tid / (CR > 0 ? CR : 1), ch = tid - tk * CR;
-      *(u32x4*)(s_kr + tk * (DR * 2) + ((ch ^ rope_swz(tk)) * 16)) = pre_r;
+    if (DR > 0) *(u32x4*)(s_kr[b] + tkr * (DR * 2) + ((chr ^ rope_swz(tkr)) * 16)) = pre_r;
+  };
+  // wave 4, lanes < TILE: the student of a tile (its index scores), loaded
+  // one item ahead of the reduction, which turns them into dI in place
+  const int q = tid - NF;
+  const bool red_lane = q >= 0 && q < TILE;
+  float kl = 0.f, dmax = 0.f, pre_i = 0.f, cur_i = 0.f;
+  auto reduce_item = [&](int i) {
+    const int t = (i / p.n2) * TILE + q;
+    if (red_lane && t < ri.vis) {
+      float ps = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) ps += s_red[i & 1][w2][q];
+      const float pk = ps * (1.f / (float)p.n1);
+      const float st = expf(cur_i - imax) * inv_isum;
+      const float di = st - pk;
+      const float pc = fmaxf(pk, 1e-8f), qc = fmaxf(st, 1e-8f);
+      kl += pc * (logf(pc) - logf(qc));
+      dmax = fmaxf(dmax, fabsf(di));
+      irow[t] = di;
     }
   };
 
-  f32x4 psum[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  float kl = 0.f, dmax = 0.f;
-  load_item(0);
+  if (!cwave) {
+    load_item(0);
+    store_item(0);
+    pre_i = irow[min(q & (TILE - 1), ri.vis - 1)];
+    if (items > 1) load_item(1);
+  }
+  float ps_acc = 0.f;
   for (int i = 0; i < items; ++i) {
-    const int t0 = (i / p.n2) * TILE, n2 = i - (i / p.n2) * p.n2;
+    const int n2 = i - (i / p.n2) * p.n2;
+    const int b = i & 1;
     lds_barrier();
-    store_item();
-    cur_i = pre_i;
-    lds_barrier();
-    if (i + 1 < items) load_item(i + 1);
-    if (n2 >= n2_lo && n2 <= n2_hi) {
-      f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-      // K fragments of step st = 2*ks + tt, read PF steps ahead of their
-      // MFMA; the scheduling barrier after each MFMA keeps the reads there
-      // (sunk next to their MFMAs, every MFMA waits out an LDS round trip)
-      constexpr int NS = 2 * KS, PF = 4;
-      auto kread = [&](int st) -> u32x4 {
-        const int ks = st >> 1, tk = (st & 1) * 16 + li;
-        const unsigned char* a =
-            ks < KSN ? s_k + tk * ROW + (((ks * 4 + lg) ^ nope_swz(tk)) * 16)
-                     : s_kr + tk * (DR * 2) + ((((ks - KSN) * 4 + lg) ^ rope_swz(tk)) * 16);
-        return *(const u32x4*)a;
-      };
-      u32x4 fa[PF];
-#pragma unroll
-      for (int i = 0; i < PF; ++i) fa[i] = kread(i);
-#pragma unroll
-      for (int st = 0; st < NS; ++st) {
-        const V8 bv = as_v8<V8>(fa[st % PF]);
-        if (st + PF < NS) fa[st % PF] = kread(st + PF);
-        acc[st & 1] = E::mfma(qf[st >> 1], bv, acc[st & 1]);
-        __builtin_amdgcn_sched_barrier(0);
+    if (!cwave) {
+      // item i+1 into the buffer item i-1 used (every wave is past it)
+      if (i + 1 < items) store_item(b ^ 1);
+      // the previous item's tile, when that was its last key head
+      if (i > 0 && n2 == 0) {
+        cur_i = pre_i;
+        reduce_item(i - 1);
       }
+      // (every feed lane loads, clamped, so that the load is unconditional)
+      if (n2 == 0) pre_i = irow[min((i / p.n2) * TILE + (q & (TILE - 1)), ri.vis - 1)];
+      if (i + 2 < items) load_item(i + 2);
+    } else {
+      if (n2 >= n2_lo && n2 <= n2_hi) {
+        // S[head][key] on the 32x32x16 MFMA: B operand K[key lane%32][d
+        // 16*ks + 8*(lane/32) .. +7].  K fragments read PF k-steps ahead
+        // of their MFMA; the scheduling barrier after each MFMA keeps the
+        // reads there (one wave per SIMD runs these MFMAs: nothing else
+        // hides an LDS round trip).  Chunk 2*ks + hf of key sl sits at
+        // (2*ks + hf) ^ swz(sl) = 16*(ks/8) + ((2*(ks%8)) ^ (hf ^ swz)).
+        const unsigned char* sk = s_k[b];
+        const unsigned char* skr = s_kr[b];
+        const int sl = lane & 31, hf = lane >> 5;
+        const int xn = hf ^ nope_swz(sl), xr = hf ^ rope_swz(sl);
+        auto a_read = [&](int ks) -> u32x4 {
+          const unsigned char* a = ks < KSN16 ? sk + sl * ROW + (ks >> 3) * 256 + (((2 * (ks & 7)) ^ xn) * 16)
+                                              : skr + sl * (DR * 2) + (((2 * (ks - KSN16)) ^ xr) * 16);
+          return *(const u32x4*)a;
+        };
+        constexpr int PF = 4, KSR16 = KS16 - KSN16;
+        f32x16 acc = {};
+        u32x4 fa[PF];
+        V8 qrf[KSR16 > 0 ? KSR16 : 1];
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        Split3 sp;
+        for (int j = 0; j < PF; ++j) fa[j] = a_read(j);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float pr = kvh[r] == n2 ? fast_exp2(acc[tt][r] * p.scale_log2 - m2r[r]) * invr[r] : 0.f;
-          split3_set(sp, r, pr);
+        for (int ks = 0; ks < KS16; ++ks) {
+          if (KSR16 > 0 && ks + 2 >= KSN16 && ks + 2 < KS16) {
+            const int u = ks + 2 - KSN16;
+            qrf[u] = *(const V8*)&s_qr[thead * QRR + u * 16 + hf * 8];
+          }
+          const V8 bv = as_v8<V8>(fa[ks % PF]);
+          if (ks + PF < KS16) fa[ks % PF] = a_read(ks + PF);
+          acc = E::mfma32(ks < KSN16 ? qf[ks < KSN16 ? ks : 0] : qrf[ks < KSN16 ? 0 : ks - KSN16], bv, acc);
+          __builtin_amdgcn_sched_barrier(0);
         }
-        psum[tt] += split3_rowsum(sp);
-      }
-    }
-    if (n2 == p.n2 - 1) {
-      if (li == 0) {
-        *(f32x4*)&s_red[wave][lg * 4] = psum[0];
-        *(f32x4*)&s_red[wave][16 + lg * 4] = psum[1];
-      }
-      psum[0] = psum[1] = (f32x4){0.f, 0.f, 0.f, 0.f};
-      lds_barrier();
-      if (tid < TILE) {
-        const int t = t0 + tid;
-        if (t < ri.vis) {
-          float ps = 0.f;
+        // the lane's 16 heads of key lane%32 (heads of other key heads
+        // masked), then the other 16 from lane lane^32
+        float ps = 0.f;
 #pragma unroll
-          for (int w2 = 0; w2 < 8; ++w2) ps += s_red[w2][tid];
-          const float pk = ps * (1.f / (float)p.n1);
-          const float st = expf(cur_i - imax) * inv_isum;
-          const float di = st - pk;
-          const float pc = fmaxf(pk, 1e-8f), qc = fmaxf(st, 1e-8f);
-          kl += pc * (logf(pc) - logf(qc));
-          dmax = fmaxf(dmax, fabsf(di));
-          irow[t] = di;
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int h0 = wave * 32 + 8 * r4 + 4 * hf;
+          const f32x4 mo = *(const f32x4*)&s_m2p[h0];
+          const i32x4 kv = *(const i32x4*)&s_kvh[h0];
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            ps += kv[r] == n2 ? fast_exp2(acc[4 * r4 + r] * p.scale_log2 - mo[r]) : 0.f;
         }
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ps), __float_as_uint(ps), false, false);
+        ps_acc += __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      }
+      if (n2 == p.n2 - 1) {
+        // both halves of the wave hold the sums: no lane branch
+        s_red[b][wave][lane & 31] = ps_acc;
+        ps_acc = 0.f;
       }
     }
   }
-  // loss and max |dI| live in wave 0 (threads < TILE); max |w| in waves 0-1
+  lds_barrier();
+  if (!cwave) {
+    cur_i = pre_i;
+    reduce_item(items - 1);
+  }
+  // loss and max |dI| live in wave 4 (lanes < TILE); max |w| in waves 0-1
   kl = wave_sum(kl);
   dmax = wave_max(dmax);
   wm = wave_max(wm);
   if (lane == 0) s_wm[wave] = wm;
+  if (tid == NF) {
+    s_kl = kl;
+    s_dmax = dmax;
+  }
   lds_barrier();
   if (tid == 0) {
     float w_all = 0.f;
     for (int w2 = 0; w2 < 8; ++w2) w_all = fmaxf(w_all, s_wm[w2]);
-    p.loss_part[row] = kl;
-    p.dexp[row] = dk_scale_exp(dmax * w_all);
+    p.loss_part[row] = s_kl;
+    p.dexp[row] = dk_scale_exp(s_dmax * w_all);
   }
 }
 
