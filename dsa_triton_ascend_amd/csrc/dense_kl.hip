@@ -23,11 +23,13 @@
 //    ReLU head-sum as an exact three-part bf16 product with a ones matrix.
 //    Writes I to a row-major fp32 buffer [rows, S2] and the row's LSE
 //    (online per thread, merged at the end).
-//  * dense_teacher_kernel: one workgroup per query row streams K / K_rope;
-//    the heads sit on MFMA rows with Q resident in registers (one gathered
-//    key row serves every head).  For GQA the key heads are visited in turn
-//    and rows of other key heads are masked.  p, then dI = student - p
-//    against the index LSE, overwriting I in place; per-row loss.
+//  * dense_teacher_kernel: one workgroup per query row streams K / K_rope
+//    through a two-buffer LDS ring.  Waves 0-3 score 32 heads each on the
+//    32x32x16 MFMA (Q resident, one key row serves every head); waves 4-7
+//    stage the next tile and reduce the previous one: p, then dI = student
+//    - p against the index LSE, overwriting I in place; per-row loss.  For
+//    GQA the key heads are visited in turn and heads of other key heads
+//    are masked.
 //  * dense_index_grad_kernel: one workgroup per row: index scores again,
 //    dW in registers, dQi^T = Ki^T . dS^T through the transposing LDS read.
 //  * dense_dki_kernel: key-major.  A workgroup owns 128 keys (16 per wave,
