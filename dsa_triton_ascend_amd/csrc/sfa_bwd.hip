@@ -145,7 +145,8 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void sfa_bwd_dq_kernel(SfaBwdPar
   __shared__ __attribute__((aligned(1024))) unsigned char s_k[NBUF][TILE * ROW];
   __shared__ __attribute__((aligned(1024))) unsigned char s_kr[NBUF][TILE * DR * 2];
   __shared__ int s_list[kBwdList + TILE];
-  __shared__ __attribute__((aligned(16))) T s_t[2][TILE][TR];  // dS, P of the 64 heads
+  // dS, P and (bf16, short ranges) the lo part of dS of the 64 heads
+  __shared__ __attribute__((aligned(16))) T s_t[3][TILE][TR];
   __shared__ int s_wcnt[kBwdWaves];
 
   const int tid = threadIdx.x;
@@ -191,11 +192,16 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void sfa_bwd_dq_kernel(SfaBwdPar
   } else {
     delta = 0.f;
   }
-  f32x4 acc_dq[NDT], acc_dqr[DR / 16];
+  // dq^T of this wave's column slice (d-tiles dt0 .. dt0 + NQW - 1 of the
+  // D + 64 columns, nope tiles then rope) for the workgroup's four head tiles
+  constexpr int NQ = NDT + DR / 16, NQW = NQ / kBwdWaves;
+  static_assert(NQ % kBwdWaves == 0, "column slices");
+  const int dt0 = __builtin_amdgcn_readfirstlane(wave) * NQW;
+  f32x4 acc_dq[NQW][4];
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) acc_dq[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < NQW; ++q)
 #pragma unroll
-  for (int dt = 0; dt < DR / 16; ++dt) acc_dqr[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int ht = 0; ht < 4; ++ht) acc_dq[q][ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   // ---- tile DMA: wave w loads nope rows (j*4 + w)*TPI .. +TPI (lane L ->
   // row + L/CPT, source chunk (L%CPT) ^ nope_swz) and rope rows 8w .. 8w+7.
@@ -333,7 +339,6 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void sfa_bwd_dq_kernel(SfaBwdPar
 
       // ---- P^T, dS^T (token tt*16 + 4*lg + r, head li) ----
       constexpr bool kSplit = __is_same(T, bf16);
-      V8 dsf, dsl;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int tt = j >> 2, r = j & 3;
@@ -341,11 +346,10 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void sfa_bwd_dq_kernel(SfaBwdPar
         const bool tv = t * TILE + tk < n_valid;
         const float pp = tv ? fast_exp2(acc_s[tt][r] * p.scale_log2 - m2) * inv : 0.f;
         const float ds = pp * (acc_p[tt][r] - delta) * p.scale;
-        const T dh = E::from_f32(ds);
-        dsf[j] = dh;
-        dsl[j] = E::from_f32(ds - E::to_f32(dh));
-        s_t[0][tk][wave * 16 + li] = kDsMul == 1.f ? dh : E::from_f32(ds * kDsMul);
+        const T dh = E::from_f32(ds * kDsMul);
+        s_t[0][tk][wave * 16 + li] = dh;
         s_t[1][tk][wave * 16 + li] = E::from_f32(pp * kDsMul);
+        if (kSplit && lo) s_t[2][tk][wave * 16 + li] = E::from_f32(ds - E::to_f32(dh));
       }
       lds_barrier();  // dS / P of the 64 heads in LDS
       // ---- dS / P rows out (16 bytes per thread: 8 heads of one slot); all
@@ -375,39 +379,65 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void sfa_bwd_dq_kernel(SfaBwdPar
       // first barrier, so past tile t-1)
       if (t + 2 < n_tiles) issue_tile(t + 2, (t + 2) % NBUF);
 
-      // ---- dq^T += K^T.dS^T, dq_rope^T += Kr^T.dS^T (transposing reads) ----
+      // ---- dq^T += K^T.dS^T over this wave's column slice ----
+      // Both operands through the transposing read: rows 4*lg + li/4 (+16),
+      // 16-byte chunk 2*c + (li&3)/2 (+8 bytes for odd li) of a [token][col]
+      // tile give k-index 8*lg + j as token 16*(j>>2) + 4*lg + (j&3), column
+      // 16*c + li.  dS^T of all four head tiles is read once per tile, so
+      // each K^T fragment feeds four MFMAs (the wave's 16 heads alone read
+      // the whole K tile transposed for one MFMA per fragment).  fp16 dS is
+      // carried as dS * 2^8 (the workspace value); dq is scaled back at the end.
       {
         const int r1 = lg * 4 + (li >> 2);
         const int hb = (li & 3) >> 1;
-        // K^T fragment of d-tile dt (nope tiles, then the rope tiles)
-        constexpr int NQ = NDT + DR / 16, PF = 8;
-        auto tread = [&](int dt) -> V8 {
-          const unsigned char *p1, *p2;
-          if (dt < NDT) {
-            const int ch = 2 * dt + hb;
-            p1 = kt + r1 * ROW + ((ch ^ nope_swz(r1)) * 16) + (li & 1) * 8;
-            p2 = kt + (r1 + 16) * ROW + ((ch ^ nope_swz(r1 + 16)) * 16) + (li & 1) * 8;
-          } else {
-            const int ch = 2 * (dt - NDT) + hb;
-            p1 = krt + r1 * (DR * 2) + ((ch ^ rope_swz(r1)) * 16) + (li & 1) * 8;
-            p2 = krt + (r1 + 16) * (DR * 2) + ((ch ^ rope_swz(r1 + 16)) * 16) + (li & 1) * 8;
-          }
+        auto tr8 = [&](const unsigned char* p1, const unsigned char* p2) -> V8 {
           const i16x4 w1 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p1));
           const i16x4 w2 = __builtin_bit_cast(i16x4, __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p2));
           const i16x8 w = {w1[0], w1[1], w1[2], w1[3], w2[0], w2[1], w2[2], w2[3]};
           return __builtin_bit_cast(V8, w);
         };
-        V8 fk[PF];
+        // K^T fragment of d-tile dt (nope tiles, then the rope tiles)
+        auto tread = [&](int dt) -> V8 {
+          const bool nope = dt < NDT;
+          const int ch = 2 * (nope ? dt : dt - NDT) + hb;
+          const unsigned char* p1 = nope ? kt + r1 * ROW + ((ch ^ nope_swz(r1)) * 16)
+                                         : krt + r1 * (DR * 2) + ((ch ^ rope_swz(r1)) * 16);
+          const unsigned char* p2 = nope ? kt + (r1 + 16) * ROW + ((ch ^ nope_swz(r1 + 16)) * 16)
+                                         : krt + (r1 + 16) * (DR * 2) + ((ch ^ rope_swz(r1 + 16)) * 16);
+          return tr8(p1 + (li & 1) * 8, p2 + (li & 1) * 8);
+        };
+        auto sread = [&](int plane, int ht) -> V8 {
+          const unsigned char* b0 = (const unsigned char*)&s_t[plane][0][0] + (2 * ht + hb) * 16 + (li & 1) * 8;
+          return tr8(b0 + r1 * (TR * 2), b0 + (r1 + 16) * (TR * 2));
+        };
+        constexpr int PF = 4;
+        V8 fk[PF], dsb[4];
 #pragma unroll
-        for (int i = 0; i < PF; ++i) fk[i] = tread(i);
+        for (int i = 0; i < PF; ++i) fk[i] = tread(dt0 + i);
 #pragma unroll
-        for (int dt = 0; dt < NQ; ++dt) {
-          const V8 w = fk[dt % PF];
-          if (dt + PF < NQ) fk[dt % PF] = tread(dt + PF);
-          f32x4& acc = dt < NDT ? acc_dq[dt] : acc_dqr[dt - NDT];
-          acc = E::mfma(w, dsf, acc);
-          if (kSplit && lo) acc = E::mfma(w, dsl, acc);
+        for (int ht = 0; ht < 4; ++ht) dsb[ht] = sread(0, ht);
+#pragma unroll
+        for (int q = 0; q < NQW; ++q) {
+          const V8 w = fk[q % PF];
+          if (q + PF < NQW) fk[q % PF] = tread(dt0 + q + PF);
+#pragma unroll
+          for (int ht = 0; ht < 4; ++ht) acc_dq[q][ht] = E::mfma(w, dsb[ht], acc_dq[q][ht]);
           __builtin_amdgcn_sched_barrier(0);
+        }
+        if (kSplit && lo) {
+          // the lo part of dS (short ranges), a second pass over the slice
+#pragma unroll
+          for (int ht = 0; ht < 4; ++ht) dsb[ht] = sread(2, ht);
+#pragma unroll
+          for (int i = 0; i < PF; ++i) fk[i] = tread(dt0 + i);
+#pragma unroll
+          for (int q = 0; q < NQW; ++q) {
+            const V8 w = fk[q % PF];
+            if (q + PF < NQW) fk[q % PF] = tread(dt0 + q + PF);
+#pragma unroll
+            for (int ht = 0; ht < 4; ++ht) acc_dq[q][ht] = E::mfma(w, dsb[ht], acc_dq[q][ht]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
       }
       // s_t is rewritten by the next tile only after its first barrier
@@ -418,22 +448,25 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void sfa_bwd_dq_kernel(SfaBwdPar
   }
   if (hg == 0 && tid == 0) p.nval[rowl] = jbase;
 
-  // ---- dq, dq_rope (head li, columns 16*dt + 4*lg + r) ----
-  if (hv) {
+  // ---- dq, dq_rope: C register r of (q, ht) is column 16*(dt0 + q) +
+  // 4*lg + r of head hbase + 16*ht + li ----
+  {
     typedef T T4 __attribute__((ext_vector_type(4)));
-    T* dqp = (T*)p.dq + hrow * D;
+    const float mul = 1.f / kDsMul;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const T4 o = {E::from_f32(acc_dq[dt][0]), E::from_f32(acc_dq[dt][1]), E::from_f32(acc_dq[dt][2]),
-                    E::from_f32(acc_dq[dt][3])};
-      *(T4*)(dqp + dt * 16 + lg * 4) = o;
-    }
-    T* dqrp = (T*)p.dqr + hrow * DR;
+    for (int ht = 0; ht < 4; ++ht) {
+      const int hh = hbase + ht * 16 + li;
+      if (hh < p.n1) {
+        const int64_t hr = (int64_t)row * p.n1 + hh;
 #pragma unroll
-    for (int dt = 0; dt < DR / 16; ++dt) {
-      const T4 o = {E::from_f32(acc_dqr[dt][0]), E::from_f32(acc_dqr[dt][1]), E::from_f32(acc_dqr[dt][2]),
-                    E::from_f32(acc_dqr[dt][3])};
-      *(T4*)(dqrp + dt * 16 + lg * 4) = o;
+        for (int q = 0; q < NQW; ++q) {
+          const int dt = dt0 + q;
+          const f32x4 a = acc_dq[q][ht] * mul;
+          const T4 o = {E::from_f32(a[0]), E::from_f32(a[1]), E::from_f32(a[2]), E::from_f32(a[3])};
+          T* dst = dt < NDT ? (T*)p.dq + hr * D + dt * 16 : (T*)p.dqr + hr * DR + (dt - NDT) * 16;
+          *(T4*)(dst + lg * 4) = o;
+        }
+      }
     }
   }
 }
