@@ -17,8 +17,10 @@
 //  A. sfa_bwd_dq_kernel: one workgroup per (query row, 64 heads), 4 waves of
 //     16 heads.  Tiles of 32 attended tokens are gathered into LDS by
 //     LDS-DMA; S^T = K.Q^T and dP^T = V.dO^T share the K fragment reads; P
-//     and dS are lane-local; dq^T += K^T.dS^T through the transposing LDS
-//     read.  dS and P of the tile are stored ([row][slot][dS | P][head]) for
+//     and dS are lane-local and go through an LDS tile; dq^T += K^T.dS^T is
+//     split by column slice (each wave all 64 heads over a quarter of the
+//     columns, both operands through the transposing LDS read).  dS and P
+//     of the tile are stored ([row][slot][dS | P][head]) for
 //     kernel B, and the row's compacted token list is recorded together with
 //     each slot's rank in its token's bucket (an integer count).
 //  B. sfa_bwd_rec_kernel: one workgroup per query row, all heads (8 waves).
