@@ -596,11 +596,26 @@ __global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) 
   const int ndw = wave_s < NDMA ? (NDMA - wave_s + NW - 1) / NW : 0;
   if (n_tiles > 0) issue_tile(0, 0);
   if (n_tiles > 1) issue_tile(1, 1);
+  // Store instructions a wave issues per 16-token half of a full tile: one
+  // per 16-byte piece index it < ceil(pieces / 4) (some lanes may idle in
+  // the last) plus the exponent store; the smallest slice bounds them all.
+  constexpr int kHalfStores = [] {
+    int m = 1 << 30;
+    for (int s2 = 0; s2 < NW; ++s2) m = (SL::n(s2) + 1) / 2 < m ? (SL::n(s2) + 1) / 2 : m;
+    return m + 1;
+  }();
   for (int t = 0; t < n_tiles; ++t) {
     const int b = t % NBUF;
-    // tile t's DMA has landed: per wave the order is DMA(t), stores(t-1),
-    // DMA(t+1), and loads return in order, so the last ndw may be in flight
-    if (t + 1 < n_tiles && ndw >= 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    // tile t's DMA has landed: per wave the issue order is DMA(t),
+    // stores(t-1) (two halves), DMA(t+1), and vector memory operations,
+    // loads and stores alike, retire in order on this counter, so the
+    // second half's stores of the previous (full) tile and DMA(t+1) may
+    // stay in flight (waiting for them too held every tile behind the
+    // previous tile's store acknowledgements)
+    if (t > 0 && t + 1 < n_tiles && ndw >= 2) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kHalfStores + 2) : "memory");
+    else if (t > 0 && t + 1 < n_tiles && ndw == 1) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kHalfStores + 1) : "memory");
+    else if (t > 0 && t + 1 < n_tiles) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kHalfStores) : "memory");
+    else if (t + 1 < n_tiles && ndw >= 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
     else if (t + 1 < n_tiles && ndw == 1) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
     else bwd_wait_all();
     lds_barrier();
