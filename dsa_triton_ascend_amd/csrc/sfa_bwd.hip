@@ -609,12 +609,12 @@ __global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) 
     // tile t's DMA has landed: per wave the issue order is DMA(t),
     // stores(t-1) (two halves), DMA(t+1), and vector memory operations,
     // loads and stores alike, retire in order on this counter, so the
-    // second half's stores of the previous (full) tile and DMA(t+1) may
-    // stay in flight (waiting for them too held every tile behind the
-    // previous tile's store acknowledgements)
-    if (t > 0 && t + 1 < n_tiles && ndw >= 2) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kHalfStores + 2) : "memory");
-    else if (t > 0 && t + 1 < n_tiles && ndw == 1) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kHalfStores + 1) : "memory");
-    else if (t > 0 && t + 1 < n_tiles) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(kHalfStores) : "memory");
+    // previous (full) tile's stores and DMA(t+1) may stay in flight (waiting
+    // for them too held every tile behind the previous tile's store
+    // acknowledgements)
+    if (t > 0 && t + 1 < n_tiles && ndw >= 2) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * kHalfStores + 2) : "memory");
+    else if (t > 0 && t + 1 < n_tiles && ndw == 1) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * kHalfStores + 1) : "memory");
+    else if (t > 0 && t + 1 < n_tiles) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * kHalfStores) : "memory");
     else if (t + 1 < n_tiles && ndw >= 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
     else if (t + 1 < n_tiles && ndw == 1) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
     else bwd_wait_all();
