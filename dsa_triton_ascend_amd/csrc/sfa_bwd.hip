@@ -299,9 +299,13 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void sfa_bwd_dq_kernel(SfaBwdPar
     for (int t = 0; t < n_tiles; ++t) {
       const int b = t % NBUF;
       // tile t's DMA has landed.  Issued per wave in the order DMA(t),
-      // stores(t-1), DMA(t+1): with tile t+1's NDN + 1 DMAs allowed in
-      // flight, loads returning in order, DMA(t) is complete.
-      if (t + 1 < n_tiles) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(NDN + 1) : "memory");
+      // stores(t-1), DMA(t+1), and vector memory operations, loads and
+      // stores alike, retire in order on this counter: with tile t+1's
+      // NDN + 1 DMAs and (after a full tile t-1) its first dS / P row store
+      // allowed in flight, DMA(t) is complete without waiting for the
+      // stores' acknowledgements.
+      if (t > 0 && t + 1 < n_tiles) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(NDN + 2) : "memory");
+      else if (t + 1 < n_tiles) asm volatile("s_waitcnt vmcnt(%0)" :: "n"(NDN + 1) : "memory");
       else bwd_wait_all();
       lds_barrier();
       const unsigned char* kt = s_k[b];
