@@ -681,31 +681,39 @@ __global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) 
                         (_Float16)(acc[i][3] * sc)};
           *(h4*)(srow + i * 16 + lg * 4) = v;
         }
-      __builtin_amdgcn_wave_barrier();
-      // four lanes per token: lane (tk, sub) stores pieces sub, sub+4, ...
-      // of token tk's slice; the token's position and all of the lane's
-      // staged pieces are read first, then the stores go out together
+      lds_barrier();  // every slice of the half's 16 tokens is staged
+      // whole records: wave w stores tokens 2w (lanes 0-31) and 2w + 1
+      // (lanes 32-63) of the half.  A record is its slices' column tiles in
+      // order; 16-byte piece gp is half gp & 1 of column tile gp / 2, read
+      // from that tile's slice staging.  A record row (17 or 9 whole 128-byte
+      // lines) goes out as full-line writes, where per-slice pieces wrote 64
+      // bytes of 16 different records per instruction.
       {
-        const int cpr2 = nct * 2;  // 16-byte pieces per record slice
-        const int tk = lane >> 2, sub = lane & 3;
+        constexpr int PPR = 2 * (MERGE ? SL::NK : SL::NK + SL::NV);  // pieces per record
+        constexpr int NIT = (PPR + 31) / 32;
+        const int tk = wave_s * 2 + (lane >> 5);
         const int j2 = t * TILE + tt * 16 + tk;
         const int64_t pos2 = s_pos[j2 - (t / (NPOS / TILE)) * NPOS];
-        constexpr int MAXP = (2 * MT + 3) / 4;  // pieces per lane, at most
-        u32x4 pv[MAXP];
+        u32x4 pv[NIT];
 #pragma unroll
-        for (int it = 0; it < MAXP; ++it) {
-          const int cc = it * 4 + sub;
-          pv[it] = *(const u32x4*)(stg + tk * SROW + (cc < cpr2 ? cc : 0) * 8);
+        for (int it = 0; it < NIT; ++it) {
+          const int gp = it * 32 + (lane & 31);
+          const int ct = (gp < PPR ? gp : 0) >> 1;
+          int s2 = 0;
+#pragma unroll
+          for (int u = 1; u < NW; ++u) s2 += ct >= SL::t0(u) ? 1 : 0;
+          pv[it] = *(const u32x4*)((const _Float16*)s_x + (s2 * 16 + tk) * SROW + (ct - SL::t0(s2)) * 16 +
+                                   (gp & 1) * 8);
         }
         if (j2 < nv) {
 #pragma unroll
-          for (int it = 0; it < MAXP; ++it) {
-            const int cc = it * 4 + sub;
-            if (cc < cpr2) *(u32x4*)(p.rec + pos2 * p.nc + ct0 * 16 + cc * 8) = pv[it];
+          for (int it = 0; it < NIT; ++it) {
+            const int gp = it * 32 + (lane & 31);
+            if (gp < PPR) *(u32x4*)(p.rec + pos2 * p.nc + gp * 8) = pv[it];
           }
         }
       }
-      __builtin_amdgcn_wave_barrier();
+      lds_barrier();  // the staging is rewritten by the next half
       // the exponent of the true value (fp16 dS / P carry 2^kF16Shift)
       if (j < nv && lg == 0)
         p.rexp[pos * kRecSlices + sl] =
