@@ -671,8 +671,8 @@ __global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) 
       if (!(mx < INFINITY)) e = kRecNonFinite;
       else if (mx > 0.f) (void)frexpf(mx, &e);
       const float sc = e == kRecNonFinite ? 1.f : ldexpf(1.f, -e);
-      // the 16 tokens' slices go through this wave's LDS staging rows, so
-      // that the stores are whole 16-byte pieces of each record's slice
+      // the 16 tokens' slices go to this wave's LDS staging rows; the
+      // records are stored whole from there, below
       _Float16* srow = stg + li * SROW;
 #pragma unroll
       for (int i = 0; i < MT; ++i)
