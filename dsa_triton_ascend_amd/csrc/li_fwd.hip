@@ -158,7 +158,10 @@ __device__ __forceinline__ int64_t li_key_row(const LiParams& p, const LiRow& ri
   return krow < p.k_rows ? krow : p.k_rows - 1;  // inconsistent cumulative lengths stay in bounds
 }
 
-template <int D, typename T, int GT, bool PAD>
+// NT: non-temporal key loads, for launches where no other query row reads
+// the same keys (one query row per batch, as at decode): the keys then have
+// no reuse to keep in the caches.
+template <int D, typename T, int GT, bool PAD, bool NT>
 __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
   using E = Elem<T>;
   using V8 = typename E::v8;
@@ -230,7 +233,10 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
     const T* kp = (const T*)p.k + (krow * p.n2 + kh) * dstride + lg * 8;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      if (!PAD || ks * 32 + lg * 8 < p.d) kf[ks] = *(const u32x4*)(kp + ks * 32);
+      if (!PAD || ks * 32 + lg * 8 < p.d) {
+        if constexpr (NT) kf[ks] = __builtin_nontemporal_load((const u32x4*)(kp + ks * 32));
+        else kf[ks] = *(const u32x4*)(kp + ks * 32);
+      }
       else kf[ks] = (u32x4){0u, 0u, 0u, 0u};
     }
   };
@@ -1053,7 +1059,10 @@ static hipError_t launch_score_kernel(const void* fn, LiParams p, hipStream_t st
 
 template <int D, typename T, int GT, bool PAD>
 static hipError_t launch_score(const LiParams& p, hipStream_t stream) {
-  return launch_score_kernel((const void*)li_score_kernel<D, T, GT, PAD>, p, stream);
+  // one query row per batch: no key is read twice (exact head dims only)
+  if (!PAD && p.q_rows == p.batch)
+    return launch_score_kernel((const void*)li_score_kernel<D, T, GT, false, true>, p, stream);
+  return launch_score_kernel((const void*)li_score_kernel<D, T, GT, PAD, false>, p, stream);
 }
 
 template <int D, typename T, bool PAD>
