@@ -709,7 +709,9 @@ __global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) 
 #pragma unroll
           for (int it = 0; it < NIT; ++it) {
             const int gp = it * 32 + (lane & 31);
-            if (gp < PPR) *(u32x4*)(p.rec + pos2 * p.nc + gp * 8) = pv[it];
+            // non-temporal: the records are read back only by the reduction
+            // kernel, gigabytes later
+            if (gp < PPR) __builtin_nontemporal_store(pv[it], (u32x4*)(p.rec + pos2 * p.nc + gp * 8));
           }
         }
       }
