@@ -1405,13 +1405,13 @@ __global__ __launch_bounds__(256) void sfa_combine_kernel(SfaFwdParams p) {
   if (p.splits <= 8) {
     // every load up front (lane s < splits: the record of split s; all
     // lanes: their columns of every split), so the wave waits for one
-    // memory round trip
+    // memory round trip; the partials are read once (non-temporal)
     f32x4 ml = {-INFINITY, 0.f, -INFINITY, 0.f};
     if (lane < p.splits) ml = *(const f32x4*)(p.part_ml + ((int64_t)lane * sstride + rh) * 4);
     hvec v[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u)
-      if (u < p.splits) v[u] = *(const hvec*)(p.part_o + ((int64_t)u * sstride + rh) * D + lane * PER);
+      if (u < p.splits) v[u] = __builtin_nontemporal_load((const hvec*)(p.part_o + ((int64_t)u * sstride + rh) * D + lane * PER));
     const bool has = ml[1] > 0.f;
     const float mref8 = wave_max(has ? ml[0] : -INFINITY);
     const float mtrue8 = wave_max(has ? ml[2] : -INFINITY);
