@@ -11,8 +11,19 @@ six independent input sets (KV cache, block table, indices, queries) are
 rotated so the 256 MiB Infinity Cache cannot serve the ~75 MB each step
 reads.  Timing: HIP events on the launch stream around exactly K steps,
 with device synchronisation on both sides.  The roofline object is for the
-dominant kernel (sfa_fwd_kernel).  The CPU baseline is the numpy oracle
-(tests-only port of the reference golden) on the host.
+step's dominant kernel, sfa_fwd_ds_kernel (64 heads per workgroup, four
+token splits), together with the sfa_combine_kernel that merges its splits.
+
+Beside the headline, each leg of the operator set is timed the same way:
+the lightning indexer at 32K context (decode, secondary metric) and at the
+cfg2 prefill shape, the SFA prefill forward, the SFA backward (reference API
+and training path), the sparse KL-loss backward and the dense warm-up stage.
+Each leg carries a CPU baseline: the numpy oracle (a tests-only restatement
+of the reference goldens) on the host cores, over the whole batch or a
+seeded row sample extrapolated by the valid (row, token) pairs, with the KV
+gather inside the timed region.  The indexer legs also report the tie-flip
+count of the GPU top-k against the oracle's top-k of the oracle's fp32
+scores.
 """
 import argparse
 import json
@@ -36,7 +47,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--sets", type=int, default=6)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--cpu-s", type=float, default=3.0,
+                    help="seconds of host work per CPU baseline leg (the decode headline takes twice this)")
     ap.add_argument("--long-steps", type=int, default=10,
                     help="timed steps of the prefill / backward legs (each step is milliseconds)")
     ap.add_argument("--no-long", action="store_true", help="skip the prefill / backward legs")
@@ -82,6 +95,7 @@ def decode_algorithmic(n_valid):
 
 
 SETTLE_MS = 200.0
+GRAPH_STEPS = 12  # steps per graph in the multi-step graph measurement
 
 
 def settle(step, ms=SETTLE_MS):
@@ -146,77 +160,128 @@ def time_decode(sets, steps, warmup):
         e1.synchronize()
         per.append(e0.elapsed_time(e1))
     per.sort()
-    # the same step captured once in a HIP graph (both kernels) and replayed:
-    # K replays back to back, no host launch work between them
+    # the step captured in HIP graphs and replayed, K steps back to back: a
+    # graph of one step (input set 0, replayed K times), and a graph of G
+    # consecutive steps over the rotating input sets (replayed K / G times),
+    # as a serving loop captures a whole decode step of many layers.  The
+    # difference between the two is the cost of launching a graph, paid once
+    # per replay, not per kernel.
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
         for _ in range(2):
             step(sets[0], torch.cuda.current_stream().cuda_stream)
     torch.cuda.current_stream().wait_stream(side)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        step(sets[0], torch.cuda.current_stream().cuda_stream)
-    for _ in range(warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    g0 = torch.cuda.Event(enable_timing=True)
-    g1 = torch.cuda.Event(enable_timing=True)
-    g0.record()
-    for _ in range(steps):
-        graph.replay()
-    g1.record()
-    torch.cuda.synchronize()
-    graph_ms = g0.elapsed_time(g1) / steps
-    del graph
+
+    def graph_time(nsteps_in_graph):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(nsteps_in_graph):
+                step(sets[i % len(sets)], torch.cuda.current_stream().cuda_stream)
+        reps = max(1, steps // nsteps_in_graph)
+        for _ in range(max(2, warmup // nsteps_in_graph)):
+            graph.replay()
+        torch.cuda.synchronize()
+        g0 = torch.cuda.Event(enable_timing=True)
+        g1 = torch.cuda.Event(enable_timing=True)
+        g0.record()
+        for _ in range(reps):
+            graph.replay()
+        g1.record()
+        torch.cuda.synchronize()
+        del graph
+        return g0.elapsed_time(g1) / (reps * nsteps_in_graph)
+    graph_ms = {1: graph_time(1), GRAPH_STEPS: graph_time(GRAPH_STEPS)}
     return total_ms / steps, per, graph_ms
 
 
-def cpu_baseline_decode(sets):
-    """numpy oracle over the full decode batch of one input set (host cores)."""
-    import numpy as np
+def cpu_threads():
+    """BLAS threads numpy runs on (the CPU baselines' core count)."""
     try:
         from threadpoolctl import threadpool_info
-        cores = max(int(i.get("num_threads", 1)) for i in threadpool_info()) if threadpool_info() else 1
+        info = threadpool_info()
+        if info:
+            return max(int(i.get("num_threads", 1)) for i in info)
     except Exception:
-        cores = len(os.sched_getaffinity(0))
+        pass
+    return len(os.sched_getaffinity(0))
+
+
+def bf16_host(t):
+    """A bf16 device tensor as an fp32 numpy array on the host (exact)."""
+    return t.float().cpu().numpy()
+
+
+def timed_reps(fn, min_s):
+    """Runs fn() until at least min_s seconds have passed; (reps, seconds)."""
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s:
+            return reps, dt
+
+
+ORACLE_NOTE = ("head-vectorised numpy oracle: one [N1 x P] matrix product per query row "
+               "where the reference golden loops over heads")
+
+
+def cpu_baseline_decode(sets, min_s=8.0):
+    """numpy oracle over the full decode batch of one input set (host cores).
+    Each row's selected rows are de-paged and gathered from the host copy of
+    the paged cache inside the timed region, as the reference's host code
+    de-pages before its golden runs (sparse_flash_attention_triton.py:382-403)."""
+    import numpy as np
     from oracle.sfa import sfa_fwd_bsnd
     s = sets[0]
     si = s["si"].cpu().numpy()
     bt = s["bt"].cpu().numpy()
-    cache = s["cache"].reshape(-1, D)
-    cache_r = s["cache_r"].reshape(-1, DR)
-    q = s["q"].float().cpu().numpy()
-    qr = s["qr"].float().cpu().numpy()
-    rows = list(range(B))
-    # gather each row's selected KV (the reference de-pages on the host too)
-    ks, krs = [], []
-    for b in rows:
-        toks = si[b, 0, 0]
-        phys = bt[b, toks // PAGE].astype(np.int64) * PAGE + toks % PAGE
-        import torch
-        pt = torch.from_numpy(phys).to(cache.device)
-        ks.append(cache[pt].float().cpu().numpy())
-        krs.append(cache_r[pt].float().cpu().numpy())
+    cache = bf16_host(s["cache"]).reshape(-1, D)
+    cache_r = bf16_host(s["cache_r"]).reshape(-1, DR)
+    q = bf16_host(s["q"])
+    qr = bf16_host(s["qr"])
     idx = np.arange(K, dtype=np.int32).reshape(1, 1, 1, K)
     scale = 1.0 / math.sqrt(D + DR)
-    # the whole batch, repeated until at least ~10 s of host work is timed
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        for b in rows:
-            sfa_fwd_bsnd(q[b:b + 1], ks[b][None, :, None, :], idx, qr[b:b + 1],
-                         krs[b][None, :, None, :], scale, [1], [K], 1, 0, True, "bfloat16",
+
+    def batch():
+        for b in range(B):
+            toks = si[b, 0, 0]
+            phys = bt[b, toks // PAGE].astype(np.int64) * PAGE + toks % PAGE
+            sfa_fwd_bsnd(q[b:b + 1], cache[phys][None, :, None, :], idx, qr[b:b + 1],
+                         cache_r[phys][None, :, None, :], scale, [1], [K], 1, 0, True, "bfloat16",
                          positions="kernel")
-        reps += 1
-        dt = time.perf_counter() - t0
-        if dt >= 10.0:
-            break
+    reps, dt = timed_reps(batch, min_s)
     flops, _ = decode_algorithmic(B * K)
-    return {"value": reps * flops / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"numpy oracle (port of sparse_flash_attention_numpy.py) over the full "
-                      f"decode batch of one input set ({B} rows x {K} tokens x {N1} heads), "
-                      f"repeated {reps} times, {dt:.1f} s"}
+    del cache, cache_r
+    return {"value": reps * flops / dt / 1e12, "unit": "TFLOP/s", "cores": cpu_threads(), "kind": "port",
+            "ms_per_step": round(dt / reps * 1e3, 2),
+            "sample": f"the full decode batch of one input set ({B} rows x {K} tokens x {N1} heads), "
+                      f"paged gather inside the timed region, repeated {reps} times, {dt:.1f} s; "
+                      + ORACLE_NOTE}
+
+
+def sample_rows(S, n, seed):
+    """n distinct query rows of [0, S) spread over the causal range (seeded)."""
+    import numpy as np
+    rng = np.random.RandomState(seed)
+    return np.sort(rng.choice(S, size=min(n, S), replace=False))
+
+
+def extrapolated(leg_name, flops_full, n_full, n_sample, reps, dt, rows, total_rows, unit="TFLOP/s",
+                 note="KV gather inside the timed region; " + ORACLE_NOTE):
+    """A CPU baseline timed on a row sample, scaled to the whole step by the
+    valid (row, token) pairs: t_full = t_sample * n_full / n_sample."""
+    t_sample = dt / reps
+    t_full = t_sample * n_full / max(n_sample, 1)
+    which = ("every query row" if rows == total_rows else
+             f"{rows} of {total_rows} query rows (seeded, spread over the causal range)")
+    scaled = "" if n_sample == n_full else " and extrapolated by valid pairs"
+    return {"value": flops_full / t_full / 1e12, "unit": unit, "cores": cpu_threads(), "kind": "port",
+            "ms_per_step": round(t_full * 1e3, 1),
+            "sample": f"{leg_name}: {which}, {n_sample} of {n_full} valid pairs, timed {reps}x in {dt:.1f} s"
+                      f"{scaled}; {note}"}
 
 
 # ---------------------------------------------------------------------------
@@ -246,36 +311,160 @@ def li_algorithmic():
     return flops, nbytes
 
 
-def time_li(sets, steps, warmup):
-    import torch
+def li_step_fn(q, k, w, idx, rows_b, s1, s2, n1, d, kk, mode):
+    """One dsa_li_fwd call (score + top-k) over BSND q / k / w into idx."""
     from dsa_triton_ascend_amd import _lib
     lib = _lib.load()
-    dev = sets[0]["q"].device
-    idx = torch.empty(LI_B, 1, 1, LI_K, dtype=torch.int32, device=dev)
-    ws_bytes = lib.dsa_li_fwd_workspace_size(LI_B, 1, LI_S2)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    dev = q.device
+    ws_bytes = lib.dsa_li_fwd_workspace_size(rows_b * s1, 1, s2)
+    ws = torch_empty_u8(ws_bytes, dev)
     stream = _lib.stream_handle(dev)
 
-    def step(s):
-        st = lib.dsa_li_fwd(s["q"].data_ptr(), s["k"].data_ptr(), s["w"].data_ptr(), None, None,
-                            idx.data_ptr(), None, LI_B, 1, LI_S2, LI_N1, 1, LI_D, LI_K, LI_B,
-                            LI_B * LI_S2, 3, _lib.LAYOUT["BSND"], _lib.LAYOUT["BSND"], _lib.DTYPE_BF16,
-                            _lib.DTYPE_FP32, 0, ws.data_ptr(), ws_bytes, stream)
+    def step(qq=q, kk_=k, ww=w):
+        st = lib.dsa_li_fwd(qq.data_ptr(), kk_.data_ptr(), ww.data_ptr(), None, None, idx.data_ptr(), None,
+                            rows_b, s1, s2, n1, 1, d, kk, rows_b * s1, rows_b * s2, mode,
+                            _lib.LAYOUT["BSND"], _lib.LAYOUT["BSND"], _lib.DTYPE_BF16, _lib.DTYPE_FP32, 0,
+                            ws.data_ptr(), ws_bytes, stream)
         if st != 0:
             _lib.check(st, "dsa_li_fwd")
+    return step
 
-    settle(lambda i: step(sets[i % len(sets)]))
+
+def torch_empty_u8(n, dev):
+    import torch
+    return torch.empty(max(int(n), 1), dtype=torch.uint8, device=dev)
+
+
+def time_li(sets, steps, warmup):
+    """Decode indexer step time (ms) over rotating input sets, and the
+    indices of one more step on set 0 (for the tie-flip count)."""
+    import torch
+    dev = sets[0]["q"].device
+    idx = torch.empty(LI_B, 1, 1, LI_K, dtype=torch.int32, device=dev)
+    fns = [li_step_fn(s["q"], s["k"], s["w"], idx, LI_B, 1, LI_S2, LI_N1, LI_D, LI_K, 3) for s in sets]
+    settle(lambda i: fns[i % len(fns)]())
     for i in range(warmup):
-        step(sets[i % len(sets)])
+        fns[i % len(fns)]()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
     for i in range(steps):
-        step(sets[i % len(sets)])
+        fns[i % len(fns)]()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    ms = start.elapsed_time(end) / steps
+    fns[0]()
+    torch.cuda.synchronize()
+    return ms, idx.cpu().numpy().reshape(LI_B, LI_K)
+
+
+# cfg2: the indexer at the reference harness's prefill shape
+# (perf_li_triton.py:39-44), B = 2, S1 = S2 = 4096, N1 = 64, D = 128, k = 2048,
+# sparse_mode 3, bf16 q / k, fp32 weights
+LIP_B, LIP_S, LIP_N1, LIP_D, LIP_K = 2, 4096, 64, 128, 2048
+
+
+def make_li_prefill_sets(nsets, device):
+    import torch
+    g = torch.Generator(device=device).manual_seed(2468)
+    return [{"q": torch.randn(LIP_B, LIP_S, LIP_N1, LIP_D, generator=g, device=device).to(torch.bfloat16),
+             "k": torch.randn(LIP_B, LIP_S, 1, LIP_D, generator=g, device=device).to(torch.bfloat16),
+             "w": torch.rand(LIP_B, LIP_S, LIP_N1, generator=g, device=device)} for _ in range(nsets)]
+
+
+def li_prefill_algorithmic():
+    """Causal pairs, flops and HBM bytes (q, k, w in; indices out) of one
+    cfg2 step."""
+    pairs = LIP_B * LIP_S * (LIP_S + 1) // 2
+    flops = 2.0 * LIP_N1 * LIP_D * pairs
+    nbytes = (LIP_B * LIP_S * LIP_N1 * (LIP_D * 2 + 4) + LIP_B * LIP_S * LIP_D * 2
+              + LIP_B * LIP_S * LIP_K * 4)
+    return pairs, flops, nbytes
+
+
+def time_li_prefill(sets, steps, warmup):
+    import torch
+    dev = sets[0]["q"].device
+    idx = torch.empty(LIP_B, LIP_S, 1, LIP_K, dtype=torch.int32, device=dev)
+    fns = [li_step_fn(s["q"], s["k"], s["w"], idx, LIP_B, LIP_S, LIP_S, LIP_N1, LIP_D, LIP_K, 3) for s in sets]
+    settle(lambda i: fns[i % len(fns)]())
+    for i in range(warmup):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        fns[i % len(fns)]()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    fns[0]()
+    torch.cuda.synchronize()
+    return ms, idx
+
+
+def np_rows(idx, rows):
+    """idx [B, S1, 1, k] on the device -> the listed (b, s1) rows, [R, k] numpy."""
+    h = idx.cpu().numpy()
+    return __import__("numpy").stack([h[b, s, 0] for b, s in rows])
+
+
+def tie_flips(idx_gpu, scores, kk):
+    """Entries where the GPU's top-k indices differ from the oracle's stable
+    top-k of the oracle's fp32 scores (rows x kk), and the largest relative
+    score gap between the two indices at such an entry (a near-tie is a
+    gap of a few fp32 ulps of reassociation)."""
+    import numpy as np
+    from oracle.indexer import stable_topk
+    ie, _ = stable_topk(scores, kk)
+    diff = idx_gpu != ie
+    n = int(diff.sum())
+    gap = 0.0
+    if n:
+        r, c = np.nonzero(diff)
+        a, b = idx_gpu[r, c], ie[r, c]
+        ok = (a >= 0) & (b >= 0)
+        sa = np.where(ok, scores[r, np.maximum(a, 0)], np.nan)
+        sb = np.where(ok, scores[r, np.maximum(b, 0)], np.nan)
+        rel = np.abs(sa - sb) / np.maximum(np.abs(sb), 1e-30)
+        gap = float(np.nanmax(rel)) if ok.any() else float("inf")
+        if not ok.all():
+            gap = float("inf")  # a -1 against a valid index: not a tie
+    return {"entries_differing": n, "entries": int(idx_gpu.size), "rows": int(idx_gpu.shape[0]),
+            "max_rel_score_gap": gap,
+            "note": "GPU indices against np.lexsort((index, -score)) of the oracle's fp32 scores"}
+
+
+def cpu_li(q, k, w, rows, s2, kk, idx_gpu_rows, min_s, what, flops_full, pairs_full, total_rows):
+    """Oracle indexer (scores + stable top-k) over the given (b, s1) rows on the
+    host, timed, each row as its own problem over its visible keys (mode 3,
+    full lengths: keys [0, s1 + S2 - S1]); plus the tie-flip count of the
+    GPU's indices on those rows."""
+    import numpy as np
+    from oracle.indexer import indexer_scores, stable_topk, visible_limit
+    S1_ = q.shape[1]
+    lims = [visible_limit(3, S1_, s2, s1, s2) for _, s1 in rows]
+
+    def run():
+        out = []
+        for (b, s1), lim in zip(rows, lims):
+            sc = indexer_scores(q[b:b + 1, s1:s1 + 1], k[b:b + 1, :lim], w[b:b + 1, s1:s1 + 1], [1], [lim], 0)
+            out.append(sc[0, 0, 0])
+            stable_topk(sc[0, 0], kk)
+        return out
+    scs = run()
+    reps, dt = timed_reps(run, min_s)
+    base = extrapolated(what, flops_full, pairs_full, sum(lims), reps, dt, len(rows), total_rows,
+                        note="numpy restatement of the score kernel (one [N1 x S2] product per query row, "
+                             "ReLU, weights, head sum) and np.lexsort stable top-k; the reference has no CPU "
+                             "golden of the indexer")
+    # tie flips on the full-width rows (-inf past each row's visible keys)
+    sel = np.full((len(rows), s2), -np.inf, np.float32)
+    for i, sc in enumerate(scs):
+        sel[i, :sc.shape[0]] = sc
+    return base, tie_flips(idx_gpu_rows, sel, kk)
 
 
 # ---------------------------------------------------------------------------
@@ -324,7 +513,10 @@ def leg(metric, workload, flops, ms, n):
             "algorithmic_flops": int(flops), "valid_pairs": n, "config": {"workload": workload}}
 
 
-def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense")):
+def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense"), cpu_s=0.0):
+    """The prefill forward and the backward legs; with cpu_s > 0 each also
+    gets a CPU baseline (oracle on a seeded row sample, about cpu_s seconds)."""
+    import numpy as np
     import torch
     import dsa_triton_ascend_amd as dsa
     out = {}
@@ -345,9 +537,12 @@ def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense")):
                                                  return_softmax_lse=True)
     if "prefill" in legs:
         ms = time_call(fwd_tnd, steps, 2)
+        flops = 2.0 * N1 * (2 * D + DR) * n
         out["sfa_fwd_prefill"] = leg("SFA fwd TFLOP/s (prefill)",
-                                   "sfa_fwd prefill: TND one sequence T=8192, N1=128, D=512+64, topK=2048 "
-                                   "causal, sparse_mode 3, stats returned", 2.0 * N1 * (2 * D + DR) * n, ms, n)
+                                     "sfa_fwd prefill: TND one sequence T=8192, N1=128, D=512+64, topK=2048 "
+                                     "causal, sparse_mode 3, stats returned", flops, ms, n)
+        if cpu_s > 0:
+            out["sfa_fwd_prefill"]["cpu_baseline"] = cpu_fwd_rows(q, qr, k, kr, si, scale, T, flops, n, cpu_s)
     del q, qr, k, kr, idx, si
     torch.cuda.empty_cache()
     # cfg5a / cfg5b: backward pair at S=4096
@@ -358,6 +553,7 @@ def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense")):
     si = idx.reshape(1, S, 1, K).contiguous()
     o, smax, ssum = dsa.sparse_flash_attention_triton(q, k, k, si, scale_value=scale, query_rope=qr, key_rope=kr,
                                                       sparse_mode=3, return_softmax_lse=True)
+    bwd_flops = 2.0 * N1 * (3 * (D + DR) + 2 * D) * n
 
     def bwd():
         return dsa.sparse_flash_attention_grad_triton(q, k, k, si, do, o, smax, ssum, scale_value=scale,
@@ -365,7 +561,10 @@ def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense")):
     if "bwd" in legs:
         ms = time_call(bwd, steps, 2)
         out["sfa_bwd"] = leg("SFA bwd TFLOP/s", "sfa_bwd: BSND B=1, S1=S2=4096, N1=128, D=512+64, topK=2048 "
-                           "causal, sparse_mode 3, bf16", 2.0 * N1 * (3 * (D + DR) + 2 * D) * n, ms, n)
+                             "causal, sparse_mode 3, bf16", bwd_flops, ms, n)
+        if cpu_s > 0:
+            out["sfa_bwd"]["cpu_baseline"] = cpu_bwd_rows(q, qr, k, kr, si, do, o, smax, ssum, scale, S,
+                                                          bwd_flops, n, cpu_s)
     # the training path (autograd): the shared-latent gradient dk + dv in one output
     from dsa_triton_ascend_amd.sparse_flash_attention import INT64_MAX
     from dsa_triton_ascend_amd.sparse_flash_attention_grad import _sfa_grad
@@ -376,23 +575,26 @@ def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense")):
     if "bwd_merged" in legs:
         ms = time_call(bwd_merged, steps, 2)
         out["sfa_bwd_merged"] = leg("SFA bwd TFLOP/s (training path, d_key = dk + dv)",
-                                  "sfa_bwd as called by the autograd Function (MLA absorb: one key gradient dk + dv): "
-                                  "BSND B=1, S1=S2=4096, N1=128, D=512+64, topK=2048 causal, sparse_mode 3, bf16",
-                                  2.0 * N1 * (3 * (D + DR) + 2 * D) * n, ms, n)
+                                    "sfa_bwd as called by the autograd Function (MLA absorb: one key gradient "
+                                    "dk + dv): BSND B=1, S1=S2=4096, N1=128, D=512+64, topK=2048 causal, "
+                                    "sparse_mode 3, bf16", bwd_flops, ms, n)
     NI, DI = 64, 128
     qi, ki = rn(1, S, NI, DI), rn(1, S, 1, DI)
     w = torch.rand(1, S, NI, generator=g, device=dev)
+    kl_flops = n * (3 * 2 * NI * DI + 2 * N1 * (D + DR) + 2 * NI)
 
     def kl():
         return dsa.sparse_lightning_indexer_grad_kl_loss_triton(q, k, qi, ki, w, si, smax, ssum, query_rope=qr,
                                                                 key_rope=kr, scale_value=scale)
     if "kl" in legs:
         ms = time_call(kl, steps, 2)
-    if "kl" in legs:
         out["kl_bwd"] = leg("indexer KL-loss bwd TFLOP/s",
-                          "sparse_lightning_indexer_grad_kl_loss: B=1, S1=S2=4096, N1=128, D=512+64, Nidx1=64, "
-                          "D_idx=128, topK=2048 causal, bf16 (fp32 weights), stats from the SFA forward",
-                          n * (3 * 2 * NI * DI + 2 * N1 * (D + DR) + 2 * NI), ms, n)
+                            "sparse_lightning_indexer_grad_kl_loss: B=1, S1=S2=4096, N1=128, D=512+64, Nidx1=64, "
+                            "D_idx=128, topK=2048 causal, bf16 (fp32 weights), stats from the SFA forward",
+                            kl_flops, ms, n)
+        if cpu_s > 0:
+            out["kl_bwd"]["cpu_baseline"] = cpu_kl_rows(q, qr, k, kr, qi, ki, w, si, smax, ssum, scale, S,
+                                                        kl_flops, n, cpu_s)
     del si, o, do
     torch.cuda.empty_cache()
     # dense warm-up stage at the same shape: every causal key, teacher stats of
@@ -406,11 +608,123 @@ def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense")):
                                               key_rope=kr)
     ms = time_call(dense, steps, 2)
     nd = S * (S + 1) // 2
+    dense_flops = nd * (3 * 2 * NI * DI + 2 * N1 * (D + DR) + 2 * NI)
     out["dense_kl_bwd"] = leg("dense indexer KL-loss bwd TFLOP/s",
                               "dense_loss_backward (warm-up stage, index LSE computed inside): B=1, S1=S2=4096, "
                               "N1=128, N2=1, D=512+64, Nidx1=64, D_idx=128, all causal keys, bf16 (fp32 weights)",
-                              nd * (3 * 2 * NI * DI + 2 * N1 * (D + DR) + 2 * NI), ms, nd)
+                              dense_flops, ms, nd)
+    if cpu_s > 0:
+        out["dense_kl_bwd"]["cpu_baseline"] = cpu_dense_rows(q, qr, k, kr, qi, ki, w, dsmax, dssum, scale, S,
+                                                             dense_flops, nd, cpu_s)
     return out
+
+
+CPU_SAMPLE_ROWS = 48
+
+
+def _rows_host(t, rows):
+    """Rows `rows` of dim 1 of a [1, S, ...] (or dim 0 of a [T, ...]) device
+    tensor, as fp32 numpy (only those rows cross to the host)."""
+    import torch
+    ri = torch.as_tensor(rows, device=t.device, dtype=torch.long)
+    return t.index_select(1 if t.dim() == 4 else 0, ri).float().cpu().numpy()
+
+
+def cpu_fwd_rows(q, qr, k, kr, si, scale, T, flops, n, min_s):
+    """Prefill forward oracle on a row sample: the sampled rows as one BSND
+    problem over the whole key sequence, sparse_mode 0 (every causal index
+    row of this workload is already within [0, s1], so mode 0 keeps exactly
+    the positions mode 3 keeps)."""
+    import numpy as np
+    from oracle.sfa import sfa_fwd_bsnd
+    rows = sample_rows(T, CPU_SAMPLE_ROWS, 11)
+    qs, qrs = _rows_host(q, rows)[None], _rows_host(qr, rows)[None]           # [1, R, N1, *]
+    sis = si.index_select(0, __import__("torch").as_tensor(rows, device=si.device)).cpu().numpy()[None]
+    kh, krh = k.float().cpu().numpy()[None], kr.float().cpu().numpy()[None]   # [1, T, 1, *]
+    R = len(rows)
+    n_s = int((sis >= 0).sum())
+
+    def run():
+        sfa_fwd_bsnd(qs, kh, sis, qrs, krh, scale, [R], [T], 1, 0, True, "bfloat16", positions="kernel")
+    reps, dt = timed_reps(run, min_s)
+    return extrapolated("sfa_fwd prefill", flops, n, n_s, reps, dt, R, T)
+
+
+def cpu_bwd_rows(q, qr, k, kr, si, do, o, smax, ssum, scale, S, flops, n, min_s):
+    """SFA backward oracle (reference API: dq, dk, dv, dq_rope, dk_rope) on a
+    row sample, as one problem over the whole key sequence (mode 0, as in
+    cpu_fwd_rows)."""
+    import torch
+    from oracle.sfa_grad import sfa_bwd_bsnd
+    rows = sample_rows(S, CPU_SAMPLE_ROWS, 12)
+    ri = torch.as_tensor(rows, device=q.device)
+    qs, qrs, dos, os_ = (_rows_host(t, rows) for t in (q, qr, do, o))
+    sis = si.index_select(1, ri).cpu().numpy()
+    sm = smax.index_select(2, ri).cpu().numpy()
+    ss = ssum.index_select(2, ri).cpu().numpy()
+    kh, krh = k.float().cpu().numpy(), kr.float().cpu().numpy()
+    R = len(rows)
+    n_s = int((sis >= 0).sum())
+
+    def run():
+        sfa_bwd_bsnd(qs, kh, sis, dos, os_, sm, ss, qrs, krh, scale, [R], [S], 1, 0, "bfloat16",
+                     positions="kernel", guard_sum=True)
+    reps, dt = timed_reps(run, min_s)
+    return extrapolated("sfa_bwd", flops, n, n_s, reps, dt, R, S)
+
+
+def cpu_kl_rows(q, qr, k, kr, qi, ki, w, si, smax, ssum, scale, S, flops, n, min_s):
+    """KL-loss backward oracle on a row sample of the full problem (only the
+    sampled rows of q / q_rope / q_index / weights cross to the host; the
+    others stay untouched zero pages)."""
+    import numpy as np
+    import torch
+    from oracle.kl import kl_loss_bwd
+    rows = sample_rows(S, CPU_SAMPLE_ROWS, 13)
+
+    def sparse_rows(t):
+        h = np.zeros(tuple(t.shape), np.float32)
+        h[0, rows] = _rows_host(t, rows)[0]
+        return h
+    qh, qrh, qih = sparse_rows(q), sparse_rows(qr), sparse_rows(qi)
+    wh = np.zeros(tuple(w.shape), np.float32)
+    wh[0, rows] = w[0, torch.as_tensor(rows, device=w.device)].cpu().numpy()
+    kh, krh, kih = k.float().cpu().numpy(), kr.float().cpu().numpy(), ki.float().cpu().numpy()
+    sih = si.cpu().numpy()
+    smh, ssh = smax.cpu().numpy(), ssum.cpu().numpy()
+    sel = [(0, int(s)) for s in rows]
+    n_s = int(sum(min(K, s + 1) for _, s in sel))
+
+    def run():
+        kl_loss_bwd(qh, kh, qrh, krh, qih, kih, wh, sih, smh, ssh, scale, rows=sel)
+    reps, dt = timed_reps(run, min_s)
+    return extrapolated("sparse KL-loss bwd", flops, n, n_s, reps, dt, len(rows), S)
+
+
+def cpu_dense_rows(q, qr, k, kr, qi, ki, w, dsmax, dssum, scale, S, flops, n, min_s):
+    """Dense KL-loss backward oracle (fp32) on a row sample, each row as its
+    own problem over its visible keys [0, s1] (the index LSE computed inside,
+    as in the timed GPU call)."""
+    import numpy as np
+    import torch
+    from oracle.dense_kl import dense_kl_bwd
+    rows = sample_rows(S, CPU_SAMPLE_ROWS // 4, 14)
+    ri = torch.as_tensor(rows, device=q.device)
+    qs, qrs, qis = (_rows_host(t, rows) for t in (q, qr, qi))
+    ws = w.index_select(1, ri).cpu().numpy()
+    sm = dsmax.index_select(2, ri).cpu().numpy()
+    ss = dssum.index_select(2, ri).cpu().numpy()
+    kh, krh, kih = k.float().cpu().numpy(), kr.float().cpu().numpy(), ki.float().cpu().numpy()
+    n_s = int(sum(int(s) + 1 for s in rows))
+
+    def run():
+        for i, s in enumerate(rows):
+            L = int(s) + 1
+            dense_kl_bwd(qs[:, i:i + 1], kh[:, :L], qrs[:, i:i + 1], krh[:, :L], qis[:, i:i + 1], kih[:, :L],
+                         ws[:, i:i + 1], sm[:, :, i:i + 1], ss[:, :, i:i + 1], scale, act_q=[1], act_k=[L],
+                         compute_dtype=np.float32)
+    reps, dt = timed_reps(run, min_s)
+    return extrapolated("dense KL-loss bwd", flops, n, n_s, reps, dt, len(rows), S)
 
 
 def dense_stats(q, qr, k, kr, scale, rows=256):
@@ -486,8 +800,23 @@ def main():
     stream_read = stream_read_rate(dev)  # the device's streaming-read rate, fresh memory
     li_sets = make_li_sets(max(2, min(args.sets, 4)), dev)
     n_li_sets = len(li_sets)
-    li_ms = time_li(li_sets, args.steps, args.warmup)
+    li_ms, li_idx = time_li(li_sets, args.steps, args.warmup)
+    li_host = None
+    if not args.no_cpu:
+        s0 = li_sets[0]
+        li_host = (bf16_host(s0["q"]), bf16_host(s0["k"]), s0["w"].cpu().numpy())
     del li_sets
+    torch.cuda.empty_cache()
+    # cfg2: the indexer at the prefill shape
+    lip_sets = make_li_prefill_sets(2, dev)
+    lip_ms, lip_idx = time_li_prefill(lip_sets, max(args.long_steps * 2, 10), 3)
+    lip_host = None
+    if not args.no_cpu:
+        s0 = lip_sets[0]
+        lip_rows = [(int(b), int(s)) for b in range(LIP_B) for s in sample_rows(LIP_S, 24, 21 + b)]
+        lip_host = (bf16_host(s0["q"]), bf16_host(s0["k"]), s0["w"].cpu().numpy(), lip_rows,
+                    np_rows(lip_idx, lip_rows))
+    del lip_sets, lip_idx
     torch.cuda.empty_cache()
     sets = make_decode_sets(args.sets, dev)
     torch.cuda.synchronize()
@@ -518,8 +847,13 @@ def main():
         "pct_of_attainable_roofline": round(100.0 * tflops / attainable, 2),
         "per_step_ms": {"median": round(per[len(per) // 2], 5), "p20": round(per[len(per) // 5], 5),
                         "p80": round(per[4 * len(per) // 5], 5)},
-        "hip_graph": {"ms_per_step": round(graph_ms, 5), "value": round(flops / (graph_ms * 1e-3) / 1e12, 2),
-                      "note": "the step captured once in a HIP graph and replayed K times (input set 0)"},
+        "hip_graph": {"ms_per_step": round(graph_ms[1], 5),
+                      "value": round(flops / (graph_ms[1] * 1e-3) / 1e12, 2),
+                      "note": "the step captured once in a HIP graph and replayed K times (input set 0)",
+                      f"ms_per_step_{GRAPH_STEPS}_per_graph": round(graph_ms[GRAPH_STEPS], 5),
+                      f"note_{GRAPH_STEPS}_per_graph": f"{GRAPH_STEPS} consecutive steps (rotating input sets) "
+                                                       f"captured in one graph, replayed K / {GRAPH_STEPS} times; "
+                                                       f"per step"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
                      "traffic": measured_traffic(),
@@ -558,11 +892,44 @@ def main():
                      "algorithmic_bytes_per_launch": int(li_bytes),
                      "algorithmic_flops_per_launch": int(li_flops)},
     }
+    lip_pairs, lip_flops, lip_bytes = li_prefill_algorithmic()
+    lip_tf = lip_flops / (lip_ms * 1e-3) / 1e12
+    result["lightning_indexer_prefill"] = {
+        "metric": "lightning_indexer TFLOP/s and us/query (cfg2 prefill)",
+        "value": round(lip_tf, 2), "unit": "TFLOP/s", "higher_is_better": True,
+        "us_per_query": round(lip_ms * 1e3 / (LIP_B * LIP_S), 5),
+        "ms_per_step": round(lip_ms, 5),
+        "config": {"workload": "lightning_indexer cfg2: BSND, B=2, S1=S2=4096, N1=64, N2=1, D=128, k=2048, "
+                               "sparse_mode 3, bf16 q/k, fp32 weights", "input_sets": 2},
+        "roofline": {"bound": "mfma", "achieved": round(lip_tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(lip_tf / PEAK_BF16_TFLOPS, 4),
+                     "kernel": "li_score_kernel + li_topk_kernel (one step)",
+                     "algorithmic_flops_per_launch": int(lip_flops), "causal_pairs": int(lip_pairs),
+                     "algorithmic_bytes_per_launch": int(lip_bytes)},
+    }
     if not args.no_long:
-        result.update(long_legs(dev, args.long_steps, tuple(args.legs.split(","))))
+        result.update(long_legs(dev, args.long_steps, tuple(args.legs.split(",")),
+                                cpu_s=0.0 if args.no_cpu else args.cpu_s))
         torch.cuda.empty_cache()
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline_decode(make_decode_sets(1, dev))
+        result["cpu_baseline"] = cpu_baseline_decode(make_decode_sets(1, dev), args.cpu_s * 2)
+        # the indexer legs: oracle scores + stable top-k, and the tie flips of
+        # the GPU's indices against them
+        q_, k_, w_ = li_host
+        rows = [(b, 0) for b in range(LI_B)]
+        base, flips = cpu_li(q_, k_, w_, rows, LI_S2, LI_K, li_idx, args.cpu_s, "lightning_indexer decode",
+                             li_flops, LI_B * LI_S2, LI_B)
+        base["value_us_per_query"] = round(base["ms_per_step"] * 1e3 / LI_B, 2)
+        result["lightning_indexer"]["cpu_baseline"] = base
+        result["lightning_indexer"]["tie_flips"] = flips
+        del li_host, q_, k_, w_
+        q_, k_, w_, rows, idx_rows = lip_host
+        base, flips = cpu_li(q_, k_, w_, rows, LIP_S, LIP_K, idx_rows, args.cpu_s,
+                             "lightning_indexer cfg2", lip_flops, lip_pairs, LIP_B * LIP_S)
+        base["value_us_per_query"] = round(base["ms_per_step"] * 1e3 / (LIP_B * LIP_S), 2)
+        result["lightning_indexer_prefill"]["cpu_baseline"] = base
+        result["lightning_indexer_prefill"]["tie_flips"] = flips
+        del lip_host, q_, k_, w_
     print(json.dumps(result), flush=True)
 
 

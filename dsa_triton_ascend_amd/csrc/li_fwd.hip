@@ -21,11 +21,16 @@
 // over registers and head tiles, then a 4-lane butterfly.
 //
 // Top-k kernel: one workgroup (1024 threads) per row.  Scores map to
-// order-preserving uint32 keys; four 8-bit radix passes find the K-th
-// largest key T among the finite scores and how many entries equal to T are
-// taken (the lowest indices: an ordered block scan, no atomics), the
-// selected (key, index) pairs are bitonic-sorted in LDS on the composite
-// (~key << 32 | index), which is exactly score descending / index ascending.
+// order-preserving uint32 keys.  Rows of up to 32768 scores take the fast
+// selection (li_topk_kernel below): a 4096-bin histogram of the 12 key bits
+// under the common prefix of the row's finite keys finds the bin holding
+// the K-th largest key; the candidates in that bin and above are counting-
+// sorted by bin, and each one's final position is its bin start plus its
+// rank within the bin by the composite (~key << 32 | index), which is
+// exactly score descending / index ascending.  Wider rows, more than 4096
+// candidates, or a crowded bin take the general selection: a radix select
+// of the K-th largest key, an ordered selection of the ties, and a bitonic
+// sort of the selected composites in LDS.
 #include <type_traits>
 
 #include "common.h"

@@ -94,6 +94,12 @@ constexpr int kRecSlices = 8;   // column slices (one per kernel-B wave)
 constexpr int kF16Shift = 8;
 // a slice exponent that marks non-finite contributions
 constexpr int kRecNonFinite = 0x7fff;
+// Smallest slice exponent: a slice whose largest magnitude is below
+// 2^kRecMinExp (a bf16 product of tiny P and d_out, or an all-zero slice)
+// is stored with this exponent, so its scale 2^-e stays finite (2^120) and
+// its stored values stay below 1; an all-zero slice then cannot raise the
+// token's largest exponent and cost the fixed-point sum its resolution.
+constexpr int kRecMinExp = -120;
 
 __device__ __forceinline__ void bwd_dma16(unsigned lds_base, int voff, __amdgpu_buffer_rsrc_t rsrc) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
@@ -600,14 +606,17 @@ __global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) 
   const int ndw = wave_s < NDMA ? (NDMA - wave_s + NW - 1) / NW : 0;
   if (n_tiles > 0) issue_tile(0, 0);
   if (n_tiles > 1) issue_tile(1, 1);
-  // Store instructions a wave issues per 16-token half of a full tile: one
-  // per 16-byte piece index it < ceil(pieces / 4) (some lanes may idle in
-  // the last) plus the exponent store; the smallest slice bounds them all.
-  constexpr int kHalfStores = [] {
-    int m = 1 << 30;
-    for (int s2 = 0; s2 < NW; ++s2) m = (SL::n(s2) + 1) / 2 < m ? (SL::n(s2) + 1) / 2 : m;
-    return m + 1;
-  }();
+  // Vector-memory stores a wave issues per 16-token half of a full tile
+  // (every token of the half valid): the whole-record loop below, one
+  // 16-byte store per iteration it < kRecIters (two records per wave, 32
+  // lanes each; lane 0 is active in every iteration, so none is skipped),
+  // then the one exponent store (lanes of group 0).  The tile wait below
+  // counts on exactly these: a store fewer per half would let it pass
+  // before the tile's DMA has landed.
+  constexpr int kRecPieces = 2 * (MERGE ? SL::NK : SL::NK + SL::NV);  // 16-byte pieces per record
+  constexpr int kRecIters = (kRecPieces + 31) / 32;
+  static_assert(kRecPieces > (kRecIters - 1) * 32, "lane 0 stores in every record iteration");
+  constexpr int kHalfStores = kRecIters + 1;
   for (int t = 0; t < n_tiles; ++t) {
     const int b = t % NBUF;
     // tile t's DMA has landed: per wave the issue order is DMA(t),
@@ -666,10 +675,12 @@ __global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) 
         for (int r = 0; r < 4; ++r) mx = __builtin_elementwise_maximum(mx, fabsf(acc[i][r]));
       mx = mx < INFINITY ? mx : INFINITY;
       mx = xgroup_max(mx);
-      // stored value = acc * 2^-e with 2^e > max |acc| (|stored| < 1)
-      int e = 0;
+      // stored value = acc * 2^-e with 2^e > max |acc| (|stored| < 1); e is
+      // at least kRecMinExp (an all-zero slice gets it too)
+      int e = kRecMinExp;
       if (!(mx < INFINITY)) e = kRecNonFinite;
       else if (mx > 0.f) (void)frexpf(mx, &e);
+      if (e < kRecMinExp) e = kRecMinExp;
       const float sc = e == kRecNonFinite ? 1.f : ldexpf(1.f, -e);
       // the 16 tokens' slices go to this wave's LDS staging rows; the
       // records are stored whole from there, below
@@ -689,8 +700,8 @@ __global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) 
       // lines) goes out as full-line writes, where per-slice pieces wrote 64
       // bytes of 16 different records per instruction.
       {
-        constexpr int PPR = 2 * (MERGE ? SL::NK : SL::NK + SL::NV);  // pieces per record
-        constexpr int NIT = (PPR + 31) / 32;
+        constexpr int PPR = kRecPieces;
+        constexpr int NIT = kRecIters;  // the store count kHalfStores is derived from
         const int tk = wave_s * 2 + (lane >> 5);
         const int j2 = t * TILE + tt * 16 + tk;
         const int64_t pos2 = s_pos[j2 - (t / (NPOS / TILE)) * NPOS];

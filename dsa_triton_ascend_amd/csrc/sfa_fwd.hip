@@ -78,6 +78,11 @@ constexpr int kSfaMaxList = 2048;
 // lengths, while for a handful of tokens it is not.
 constexpr int kLoSplitMinTokens = 256;
 constexpr float kRefSlack = 64.f;  // log2 units
+// Smallest exponent of a split partial's scale 2^e: a partial whose largest
+// |O / l| is below 2^kPartMinExp (tiny values) keeps the scale 2^-120, so
+// the stored multiplier inv * 2^-e (inv <= 1: l counts the reference-max
+// token) stays finite and the stored values stay below 1.
+constexpr int kPartMinExp = -120;
 
 // Zero row for padding slots of the 64-bit gather path (the buffer path
 // gets zeros from the hardware range check instead).
@@ -694,6 +699,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
         for (int r = 0; r < 4; ++r) a = fmaxf(a, fabsf(acc_o[dt][ht][r]));
       a = xgroup_max(a) * inv;
       if (a > 0.f) (void)frexpf(a, &ex);  // a < 2^ex
+      ex = ex < kPartMinExp ? kPartMinExp : ex;
     }
     mul[ht] = ldexpf(inv, -ex);
     if (head < p.n1 && lg == 0) {
@@ -1317,6 +1323,7 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
       for (int w = 0; w < NW; ++w) a = fmaxf(a, s_am[w * HG + h]);
       a *= inv;
       if (a > 0.f) (void)frexpf(a, &ex);
+      ex = ex < kPartMinExp ? kPartMinExp : ex;
     }
     s_mul[h] = ldexpf(inv, -ex);
     if (head < p.n1) {

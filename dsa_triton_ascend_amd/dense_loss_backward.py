@@ -31,111 +31,115 @@ SUPPORTED_NIDX1 = (32, 64, 128)
 _MAX_N1 = 128
 
 
-def _check_in(name, value, supported):
-    if value not in supported:
-        raise ValueError(f"{name} must be one of {supported}, got {value}")
+# Guards.  Each public entry point runs an ordered list of rules, the first
+# that fires raising its exception: the order of the checks and the exception
+# types follow the reference's validators (dense_loss_backward_triton.py:
+# 658-753), which is what a caller can observe; shape reads sit behind the
+# rank checks that make them valid.  A rule is (fires, exception type,
+# message); messages are callables so that they format lazily.
+def _raise_first(rules):
+    for fires, exc, msg in rules:
+        if fires():
+            raise exc(msg() if callable(msg) else msg)
 
 
-def _validate_dense_index_inputs(query_index, key_index, weights, layout, sparse_mode,
-                                 pre_tokens=INT64_MAX, next_tokens=INT64_MAX):
-    """dense_loss_backward_triton.py:658-682."""
-    if layout != "BSND":
-        raise ValueError("Only BSND layout is supported")
-    if sparse_mode != 3:
-        raise ValueError("Only sparse_mode=3 (rightDownCausal) is supported")
-    if pre_tokens != INT64_MAX or next_tokens != INT64_MAX:
-        raise ValueError("pre_tokens/next_tokens only support the official default value")
-    if query_index.dim() != 4 or key_index.dim() != 4:
-        raise ValueError("query_index and key_index must be 4D BSND tensors")
-    if weights.dim() != 3:
-        raise ValueError("weights must be [B, S1, Nidx1]")
-    B, S1, Nidx1, D_idx = query_index.shape
-    if key_index.shape[0] != B or key_index.shape[2] != 1:
-        raise ValueError("key_index must be [B, S2, 1, D_idx]")
-    if tuple(weights.shape) != (B, S1, Nidx1):
-        raise ValueError("weights must be [B, S1, Nidx1]")
-    if key_index.shape[3] != D_idx:
-        raise ValueError("query_index and key_index must share D_idx")
-    _check_in("Nidx1", Nidx1, SUPPORTED_NIDX1)
-    _check_in("D_idx", D_idx, SUPPORTED_D)
+def _index_rules(qi, ki, w, layout, sparse_mode, pre_tokens, next_tokens):
+    """Layout, mode and band arguments, then the index tensors' ranks and
+    shapes (reference 658-682)."""
+    dims = lambda: tuple(qi.shape)  # noqa: E731  [B, S1, Nidx1, D_idx]
+    return [
+        (lambda: layout != "BSND", ValueError, "Only BSND layout is supported"),
+        (lambda: sparse_mode != 3, ValueError, "Only sparse_mode=3 (rightDownCausal) is supported"),
+        (lambda: pre_tokens != INT64_MAX or next_tokens != INT64_MAX, ValueError,
+         "pre_tokens/next_tokens only support the official default value"),
+        (lambda: qi.dim() != 4 or ki.dim() != 4, ValueError, "query_index and key_index must be 4D BSND tensors"),
+        (lambda: w.dim() != 3, ValueError, "weights must be [B, S1, Nidx1]"),
+        (lambda: ki.shape[0] != dims()[0] or ki.shape[2] != 1, ValueError, "key_index must be [B, S2, 1, D_idx]"),
+        (lambda: tuple(w.shape) != dims()[:3], ValueError, "weights must be [B, S1, Nidx1]"),
+        (lambda: ki.shape[3] != dims()[3], ValueError, "query_index and key_index must share D_idx"),
+        (lambda: dims()[2] not in SUPPORTED_NIDX1, ValueError,
+         lambda: f"Nidx1 must be one of {SUPPORTED_NIDX1}, got {dims()[2]}"),
+        (lambda: dims()[3] not in SUPPORTED_D, ValueError,
+         lambda: f"D_idx must be one of {SUPPORTED_D}, got {dims()[3]}"),
+    ]
 
 
-def _validate_index_dtypes(query_index, key_index, weights):
-    if query_index.dtype not in (torch.float16, torch.bfloat16):
-        raise TypeError(f"query_index dtype must be float16 or bfloat16, got {query_index.dtype}")
-    if key_index.dtype != query_index.dtype:
-        raise TypeError("query_index and key_index must share dtype")
-    if weights.dtype not in (query_index.dtype, torch.float32):
-        raise TypeError("weights dtype must match the index dtype or be float32")
+def _index_dtype_rules(qi, ki, w):
+    """dtypes of the LSE's inputs."""
+    half = (torch.float16, torch.bfloat16)
+    return [
+        (lambda: qi.dtype not in half, TypeError,
+         lambda: f"query_index dtype must be float16 or bfloat16, got {qi.dtype}"),
+        (lambda: ki.dtype != qi.dtype, TypeError, "query_index and key_index must share dtype"),
+        (lambda: w.dtype not in (qi.dtype, torch.float32), TypeError,
+         "weights dtype must match the index dtype or be float32"),
+    ]
 
 
-def _validate_dense_dtypes(query, key, query_index, key_index, weights, softmax_max, softmax_sum):
-    """dense_loss_backward_triton.py:685-697."""
-    data_dtype = query.dtype
-    if data_dtype not in (torch.float16, torch.bfloat16):
-        raise TypeError(f"query dtype must be float16 or bfloat16, got {data_dtype}")
-    if key.dtype != data_dtype or query_index.dtype != data_dtype or key_index.dtype != data_dtype:
-        raise TypeError("query, key, query_index, and key_index must share dtype")
-    if weights.dtype != data_dtype and weights.dtype != torch.float32:
-        raise TypeError("weights dtype must match query dtype or be float32")
-    if softmax_max.dtype != torch.float32 or softmax_sum.dtype != torch.float32:
-        raise TypeError("softmax_max and softmax_sum must be float32")
+def _backward_rules(q, k, qi, ki, w, smax, ssum, qr, kr):
+    """dtypes (reference 685-697), then the attention tensors' shapes against
+    the index tensors and the statistics (720-743), then the optional rope
+    pair (700-717)."""
+    dt = q.dtype
+    shp = lambda: tuple(q.shape)  # noqa: E731  [B, S1, N1, D]
+    n2 = lambda: k.shape[2]  # noqa: E731
+    stat_shape = lambda: (shp()[0], n2(), shp()[1], shp()[2] // n2())  # noqa: E731
+    return [
+        (lambda: dt not in (torch.float16, torch.bfloat16), TypeError,
+         lambda: f"query dtype must be float16 or bfloat16, got {dt}"),
+        (lambda: any(t.dtype != dt for t in (k, qi, ki)), TypeError,
+         "query, key, query_index, and key_index must share dtype"),
+        (lambda: w.dtype not in (dt, torch.float32), TypeError, "weights dtype must match query dtype or be float32"),
+        (lambda: smax.dtype != torch.float32 or ssum.dtype != torch.float32, TypeError,
+         "softmax_max and softmax_sum must be float32"),
+        (lambda: k.shape[0] != shp()[0] or k.shape[3] != shp()[3], ValueError, "key must be [B, S2, N2, D_attn]"),
+        (lambda: n2() <= 0 or shp()[2] % n2() != 0, ValueError, "query N1 must be divisible by key N2"),
+        (lambda: tuple(qi.shape[:2]) != shp()[:2], ValueError, "query_index must share B and S1 with query"),
+        (lambda: ki.shape[1] != k.shape[1], ValueError, "key_index S2 must match key S2"),
+        (lambda: tuple(smax.shape) != stat_shape() or tuple(ssum.shape) != stat_shape(), ValueError,
+         lambda: f"softmax_max and softmax_sum must be [B, N2, S1, G], got {tuple(smax.shape)}"),
+        (lambda: shp()[3] not in SUPPORTED_D, ValueError,
+         lambda: f"D_attn must be one of {SUPPORTED_D}, got {shp()[3]}"),
+        (lambda: shp()[2] > _MAX_N1, ValueError, lambda: f"N1 must be <= {_MAX_N1}, got {shp()[2]}"),
+        (lambda: (qr is None) != (kr is None), ValueError,
+         "query_rope and key_rope must be both provided or both omitted"),
+    ]
 
 
-def _validate_rope_inputs(query, key, query_rope, key_rope):
-    """dense_loss_backward_triton.py:700-717."""
-    if (query_rope is None) != (key_rope is None):
-        raise ValueError("query_rope and key_rope must be both provided or both omitted")
-    if query_rope is None:
+def _rope_rules(q, k, qr, kr):
+    """The rope pair, when given."""
+    return [
+        (lambda: qr.dim() != 4 or kr.dim() != 4, ValueError, "query_rope and key_rope must be 4D BSND tensors"),
+        (lambda: qr.shape[:3] != q.shape[:3], ValueError, "query_rope must share [B, S1, N1] with query"),
+        (lambda: kr.shape[:3] != k.shape[:3], ValueError, "key_rope must share [B, S2, N2] with key"),
+        (lambda: qr.shape[3] != kr.shape[3], ValueError, "query_rope and key_rope must share Drope"),
+        (lambda: qr.shape[3] != 64, ValueError, "Only Drope=64 is supported for query_rope/key_rope"),
+        (lambda: qr.dtype != q.dtype or kr.dtype != k.dtype, TypeError,
+         "query_rope/key_rope dtype must match query/key dtype"),
+    ]
+
+
+def _guard_lse(qi, ki, w, layout, sparse_mode, pre_tokens, next_tokens):
+    _raise_first(_index_rules(qi, ki, w, layout, sparse_mode, pre_tokens, next_tokens)
+                 + _index_dtype_rules(qi, ki, w))
+
+
+def _guard_backward(q, k, qi, ki, w, smax, ssum, layout, sparse_mode, qr, kr, pre_tokens, next_tokens):
+    """Returns the rope width (0 without rope)."""
+    _raise_first([(lambda: q.dim() != 4 or k.dim() != 4, ValueError, "query and key must be 4D BSND tensors")])
+    _raise_first(_index_rules(qi, ki, w, layout, sparse_mode, pre_tokens, next_tokens)
+                 + _backward_rules(q, k, qi, ki, w, smax, ssum, qr, kr))
+    if qr is None:
         return 0
-    if query_rope.dim() != 4 or key_rope.dim() != 4:
-        raise ValueError("query_rope and key_rope must be 4D BSND tensors")
-    if query_rope.shape[:3] != query.shape[:3]:
-        raise ValueError("query_rope must share [B, S1, N1] with query")
-    if key_rope.shape[:3] != key.shape[:3]:
-        raise ValueError("key_rope must share [B, S2, N2] with key")
-    if query_rope.shape[3] != key_rope.shape[3]:
-        raise ValueError("query_rope and key_rope must share Drope")
-    if query_rope.shape[3] != 64:
-        raise ValueError("Only Drope=64 is supported for query_rope/key_rope")
-    if query_rope.dtype != query.dtype or key_rope.dtype != key.dtype:
-        raise TypeError("query_rope/key_rope dtype must match query/key dtype")
-    return query_rope.shape[3]
+    _raise_first(_rope_rules(q, k, qr, kr))
+    return qr.shape[3]
 
 
-def _validate_dense_inputs(query, key, query_index, key_index, weights, softmax_max, softmax_sum, layout,
-                           sparse_mode, query_rope=None, key_rope=None, pre_tokens=INT64_MAX,
-                           next_tokens=INT64_MAX):
-    """dense_loss_backward_triton.py:720-743."""
-    if query.dim() != 4 or key.dim() != 4:
-        raise ValueError("query and key must be 4D BSND tensors")
-    _validate_dense_index_inputs(query_index, key_index, weights, layout, sparse_mode,
-                                 pre_tokens=pre_tokens, next_tokens=next_tokens)
-    _validate_dense_dtypes(query, key, query_index, key_index, weights, softmax_max, softmax_sum)
-    B, S1, N1, D = query.shape
-    if key.shape[0] != B or key.shape[3] != D:
-        raise ValueError("key must be [B, S2, N2, D_attn]")
-    N2 = key.shape[2]
-    if N2 <= 0 or N1 % N2 != 0:
-        raise ValueError("query N1 must be divisible by key N2")
-    if query_index.shape[0] != B or query_index.shape[1] != S1:
-        raise ValueError("query_index must share B and S1 with query")
-    if key_index.shape[1] != key.shape[1]:
-        raise ValueError("key_index S2 must match key S2")
-    softmax_shape = (B, N2, S1, N1 // N2)
-    if tuple(softmax_max.shape) != softmax_shape or tuple(softmax_sum.shape) != softmax_shape:
-        raise ValueError(f"softmax_max and softmax_sum must be [B, N2, S1, G], got {tuple(softmax_max.shape)}")
-    _check_in("D_attn", D, SUPPORTED_D)
-    if N1 > _MAX_N1:
-        raise ValueError(f"N1 must be <= {_MAX_N1}, got {N1}")
-    return _validate_rope_inputs(query, key, query_rope, key_rope)
-
-
-def _reshape_dense_index_stat(stat, B, S1, name):
-    """dense_loss_backward_triton.py:746-753."""
-    if tuple(stat.shape) in ((B, S1), (B * S1,), (B, 1, S1), (B, 1, S1, 1)):
-        return stat.reshape(B * S1).contiguous()
-    raise ValueError(f"{name} must have shape [B,S1], [B*S1], [B,1,S1], or [B,1,S1,1], got {tuple(stat.shape)}")
+# shapes accepted for a per-row index statistic (reference 746-753)
+def _row_stat(stat, B, S1, name):
+    if tuple(stat.shape) not in ((B, S1), (B * S1,), (B, 1, S1), (B, 1, S1, 1)):
+        raise ValueError(f"{name} must have shape [B,S1], [B*S1], [B,1,S1], or [B,1,S1,1], got {tuple(stat.shape)}")
+    return stat.reshape(B * S1).contiguous()
 
 
 def npu_dense_lightning_indexer_softmax_lse_triton(query_index, key_index, weights, actual_seq_qlen=None,
@@ -143,9 +147,7 @@ def npu_dense_lightning_indexer_softmax_lse_triton(query_index, key_index, weigh
                                                    pre_tokens=INT64_MAX, next_tokens=INT64_MAX):
     """Dense indexer softmax LSE (dense_loss_backward_triton.py:812-838):
     ``(softmax_max_index, softmax_sum_index)``, each [B, 1, S1] fp32."""
-    _validate_dense_index_inputs(query_index, key_index, weights, layout, sparse_mode,
-                                 pre_tokens=pre_tokens, next_tokens=next_tokens)
-    _validate_index_dtypes(query_index, key_index, weights)
+    _guard_lse(query_index, key_index, weights, layout, sparse_mode, pre_tokens, next_tokens)
     device = _check_device(query_index, key_index, weights)
     B, S1, Nidx1, D_idx = query_index.shape
     S2 = key_index.shape[1]
@@ -178,9 +180,8 @@ def dense_loss_backward_triton(query, key, query_index, key_index, weights, soft
                                layout="BSND", sparse_mode=3, pre_tokens=INT64_MAX, next_tokens=INT64_MAX):
     """Dense KL-loss backward (dense_loss_backward_triton.py:756-809):
     ``(dQueryIndex, dKeyIndex, dWeights, loss)``."""
-    d_rope = _validate_dense_inputs(query, key, query_index, key_index, weights, softmax_max, softmax_sum,
-                                    layout, sparse_mode, query_rope=query_rope, key_rope=key_rope,
-                                    pre_tokens=pre_tokens, next_tokens=next_tokens)
+    d_rope = _guard_backward(query, key, query_index, key_index, weights, softmax_max, softmax_sum, layout,
+                             sparse_mode, query_rope, key_rope, pre_tokens, next_tokens)
     if (softmax_max_index is None) != (softmax_sum_index is None):
         raise ValueError("softmax_max_index and softmax_sum_index must be both provided or both omitted")
     device = _check_device(query, key, query_index, key_index, weights, softmax_max, softmax_sum,
@@ -192,8 +193,8 @@ def dense_loss_backward_triton(query, key, query_index, key_index, weights, soft
     if softmax_max_index is not None:
         if softmax_max_index.dtype != torch.float32 or softmax_sum_index.dtype != torch.float32:
             raise TypeError("softmax_max_index and softmax_sum_index must be float32")
-        mx = _reshape_dense_index_stat(softmax_max_index, B, S1, "softmax_max_index")
-        sm = _reshape_dense_index_stat(softmax_sum_index, B, S1, "softmax_sum_index")
+        mx = _row_stat(softmax_max_index, B, S1, "softmax_max_index")
+        sm = _row_stat(softmax_sum_index, B, S1, "softmax_sum_index")
     act_q = _seq_tensor(actual_seq_qlen, device)
     act_k = _seq_tensor(actual_seq_klen, device)
     d_qi = torch.empty_like(query_index)

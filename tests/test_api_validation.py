@@ -111,3 +111,92 @@ def test_module_constructors_take_the_reference_positional_order():
             kl.deterministic) == (0.5, "BSND", 3, 7, 8, True)
     for m in (li, sfa, g, kl):
         assert type(m).construct is type(m).forward
+
+
+# ---------------------------------------------------------------------------
+# dense warm-up stage: every guard, in the reference's order (the first
+# failing check decides the exception type; dense_loss_backward_triton.py:
+# 658-753), on CPU tensors (the guards run before the device check)
+# ---------------------------------------------------------------------------
+def _dense_ok():
+    z = lambda *s, dt=BF: torch.zeros(*s, dtype=dt)  # noqa: E731
+    return dict(q=z(1, 2, 4, 128), k=z(1, 8, 1, 128), qi=z(1, 2, 32, 128), ki=z(1, 8, 1, 128),
+                w=z(1, 2, 32, dt=torch.float32), smax=z(1, 1, 2, 4, dt=torch.float32),
+                ssum=z(1, 1, 2, 4, dt=torch.float32), qr=z(1, 2, 4, 64), kr=z(1, 8, 1, 64))
+
+
+def _dense_bwd(a, **kw):
+    return dsa.dense_loss_backward_triton(a["q"], a["k"], a["qi"], a["ki"], a["w"], a["smax"], a["ssum"],
+                                          query_rope=a["qr"], key_rope=a["kr"], **kw)
+
+
+@pytest.mark.parametrize("change,kw,exc", [
+    ({}, {"layout": "TND"}, ValueError),
+    ({}, {"sparse_mode": 0}, ValueError),
+    ({}, {"pre_tokens": 5}, ValueError),
+    ({"q": torch.zeros(2, 4, 128, dtype=BF)}, {}, ValueError),                # query rank
+    ({"qi": torch.zeros(2, 32, 128, dtype=BF)}, {}, ValueError),              # index rank
+    ({"w": torch.zeros(1, 2, 32, 1)}, {}, ValueError),                        # weights rank
+    ({"ki": torch.zeros(1, 8, 2, 128, dtype=BF)}, {}, ValueError),            # key_index N2 != 1
+    ({"w": torch.zeros(1, 2, 16)}, {}, ValueError),                           # weights shape
+    ({"ki": torch.zeros(1, 8, 1, 256, dtype=BF)}, {}, ValueError),            # D_idx differs
+    ({"qi": torch.zeros(1, 2, 16, 128, dtype=BF), "w": torch.zeros(1, 2, 16)}, {}, ValueError),  # Nidx1
+    ({"qi": torch.zeros(1, 2, 32, 64, dtype=BF), "ki": torch.zeros(1, 8, 1, 64, dtype=BF)}, {}, ValueError),
+    ({"q": torch.zeros(1, 2, 4, 128)}, {}, TypeError),                        # query dtype
+    ({"k": torch.zeros(1, 8, 1, 128, dtype=torch.float16)}, {}, TypeError),  # shared dtype
+    ({"w": torch.zeros(1, 2, 32, dtype=torch.float16)}, {}, TypeError),      # weights dtype
+    ({"smax": torch.zeros(1, 1, 2, 4, dtype=BF)}, {}, TypeError),             # stats dtype
+    ({"k": torch.zeros(1, 8, 1, 256, dtype=BF)}, {}, ValueError),             # key D
+    ({"k": torch.zeros(1, 8, 3, 128, dtype=BF)}, {}, ValueError),             # N1 % N2
+    ({"qi": torch.zeros(1, 3, 32, 128, dtype=BF), "w": torch.zeros(1, 3, 32)}, {}, ValueError),  # S1
+    ({"ki": torch.zeros(1, 9, 1, 128, dtype=BF)}, {}, ValueError),            # key_index S2
+    ({"smax": torch.zeros(1, 1, 4, 2)}, {}, ValueError),                      # stats shape
+    ({"q": torch.zeros(1, 2, 4, 96, dtype=BF), "k": torch.zeros(1, 8, 1, 96, dtype=BF)}, {}, ValueError),
+    ({"q": torch.zeros(1, 2, 256, 128, dtype=BF), "smax": torch.zeros(1, 1, 2, 256),
+      "ssum": torch.zeros(1, 1, 2, 256), "qr": torch.zeros(1, 2, 256, 64, dtype=BF)}, {}, ValueError),  # N1
+    ({"kr": None}, {}, ValueError),                                           # rope pair
+    ({"qr": torch.zeros(1, 2, 4, 32, dtype=BF), "kr": torch.zeros(1, 8, 1, 32, dtype=BF)}, {}, ValueError),
+    ({"qr": torch.zeros(1, 2, 4, 64)}, {}, TypeError),                        # rope dtype
+    ({}, {"softmax_max_index": torch.zeros(1, 2)}, ValueError),               # one of the two stats
+])
+def test_dense_guards_in_order(change, kw, exc):
+    a = _dense_ok()
+    a.update(change)
+    with pytest.raises(exc) as ei:
+        _dense_bwd(a, **kw)
+    assert "GPU device" not in str(ei.value), "a guard must fire before the device check"
+
+
+def test_dense_valid_arguments_reach_the_device_check():
+    """The unchanged arguments pass every guard (so each case above fails on
+    its own guard, not on the CPU tensors)."""
+    with pytest.raises(ValueError, match="GPU device"):
+        _dense_bwd(_dense_ok())
+    a = _dense_ok()
+    with pytest.raises(ValueError, match="GPU device"):
+        dsa.dense_lightning_indexer_softmax_lse_triton(a["qi"], a["ki"], a["w"])
+
+
+def test_dense_guards_order_layout_before_dtype():
+    """Several faults at once: the earliest check in the reference's order
+    decides (a bad layout is a ValueError even with an fp32 query)."""
+    a = _dense_ok()
+    a["q"] = a["q"].float()
+    with pytest.raises(ValueError, match="BSND"):
+        _dense_bwd(a, layout="TND")
+    with pytest.raises(TypeError):  # dtype before the attention shapes
+        a["k"] = torch.zeros(1, 8, 3, 128, dtype=BF)
+        _dense_bwd(a)
+
+
+def test_dense_lse_guards():
+    a = _dense_ok()
+    f = dsa.dense_lightning_indexer_softmax_lse_triton
+    with pytest.raises(ValueError, match="BSND"):
+        f(a["qi"], a["ki"], a["w"], layout="TND")
+    with pytest.raises(TypeError):
+        f(a["qi"].float(), a["ki"].float(), a["w"])
+    with pytest.raises(TypeError):
+        f(a["qi"], a["ki"].half(), a["w"])
+    with pytest.raises(TypeError):
+        f(a["qi"], a["ki"], a["w"].half())

@@ -206,5 +206,10 @@ def test_dense_guards():
         f(q, k, qi, ki, w, st.reshape(1, 1, 2, 4), st.reshape(1, 1, 2, 4))
     with pytest.raises(ValueError):
         f(q, k, qi, ki, w, st, st, softmax_max_index=z(1, 2, dt=torch.float32))
+    with pytest.raises(ValueError):  # index statistics not [B, S1] (or an accepted reshape of it)
+        f(q, k, qi, ki, w, st, st, softmax_max_index=z(1, 3, dt=torch.float32),
+          softmax_sum_index=z(1, 3, dt=torch.float32))
+    with pytest.raises(TypeError):
+        f(q, k, qi, ki, w, st, st, softmax_max_index=z(1, 2), softmax_sum_index=z(1, 2))
     with pytest.raises(ValueError):
         dsa.dense_lightning_indexer_softmax_lse_triton(qi, ki, w, layout="TND")

@@ -389,3 +389,77 @@ def test_indexer_paged_decode_scores():
     assert np.all(np.abs(got[fin] - ref[fin]) <= 1e-5 * np.abs(ref[fin]) + tol[fin])
     # the -1 block of batch 0 (keys 64..127) scores exactly zero
     assert np.all(got[0, page:2 * page] == 0.0)
+
+
+# ---------------------------------------------------------------------------
+# the reference's large grid (test_li_triton.py:47-56): (S1, S2) = (4096, 8192)
+# and (16384, 16384), N1 = 64, N2 = 1, D = 128, k = 2048, B in {1, 3}, modes
+# 0 and 3, fp16 and fp32 inputs (fp16-representable values, weights of the
+# input dtype, test_li_triton.py:28-34)
+# ---------------------------------------------------------------------------
+def _every_row_layout(idx, val, S1, S2, k, mode):
+    """Device-side checks of every row: the first min(visible, k) entries are
+    distinct in-range indices with non-increasing values, the rest -1 with
+    -inf values."""
+    B = idx.shape[0]
+    s1 = torch.arange(S1, device=idx.device)
+    lim = torch.full_like(s1, S2) if mode == 0 else torch.clamp(S2 - S1 + s1 + 1, 0, S2)
+    nval = torch.clamp(lim, max=k)                                    # [S1]
+    i = idx[:, :, 0].long()                                           # [B, S1, k]
+    v = val[:, :, 0].float()
+    j = torch.arange(k, device=idx.device)
+    want = (j[None, None, :] < nval[None, :, None]).expand(B, S1, k)
+    assert torch.equal(i >= 0, want), "valid entries are not exactly the row's first min(visible, k) slots"
+    assert bool((i < lim[None, :, None]).all()), "index beyond the row's visible keys"
+    assert bool(torch.isneginf(v[~want]).all()), "padding values must be -inf"
+    assert not bool(torch.isnan(v).any())
+    dec = (v[..., 1:] <= v[..., :-1]) | ~want[..., 1:]
+    assert bool(dec.all()), "values are not non-increasing"
+    srt = torch.sort(torch.where(want, i, -1 - j[None, None, :]), dim=-1).values
+    assert bool((srt[..., 1:] != srt[..., :-1]).all()), "duplicate index within a row"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["fp16", "fp32"])
+@pytest.mark.parametrize("mode", [0, 3])
+@pytest.mark.parametrize("B", [1, 3])
+@pytest.mark.parametrize("S1,S2", [(4096, 8192), (16384, 16384)], ids=["4k_8k", "16k_16k"])
+def test_indexer_reference_large_grid(S1, S2, B, mode, dtype):
+    dsa = _api()
+    N1, D, K = 64, 128, 2048
+    print(f"[li large grid] S1={S1} S2={S2} B={B} mode={mode} {dtype}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(1000 * B + 10 * mode + (dtype == torch.float32))
+    rnd = lambda *s: torch.randn(*s, generator=g, device="cuda").half().to(dtype)  # noqa: E731
+    q, k, w = rnd(B, S1, N1, D), rnd(B, S2, 1, D), rnd(B, S1, N1)
+    idx, val = dsa.lightning_indexer_triton(q, k, w, sparse_count=K, sparse_mode=mode, return_value=True)
+    torch.cuda.synchronize()
+    assert idx.shape == (B, S1, 1, K) and idx.dtype == torch.int32
+    _every_row_layout(idx, val, S1, S2, K, mode)
+    # sampled rows (edges included) against the oracle's top-k of its fp32 scores
+    rng = np.random.RandomState(S1 + B + mode)
+    rows = sorted({(b, int(s)) for b in range(B) for s in list(rng.randint(0, S1, 3)) + [0, S1 - 1]})
+    kh = k.float().cpu().numpy()
+    ih, vh = idx.cpu().numpy(), val.float().cpu().numpy()
+    flips = 0
+    for b, s in rows:
+        qb = q[b, s].float().cpu().numpy()[None, None]                 # [1, 1, N1, D]
+        wb = w[b, s].float().cpu().numpy()[None, None]                 # [1, 1, N1]
+        lim = S2 if mode == 0 else min(S2, S2 - S1 + s + 1)
+        sc = np.full((1, S2), -np.inf, np.float32)
+        sc[0, :lim] = indexer_scores(qb, kh[b:b + 1, :lim], wb, [1], [lim], 0)[0, 0, 0]
+        a = np.abs(qb[0, 0]) * np.abs(wb[0, 0])[:, None]                # [N1, D]
+        tol = 1e-5 * (a.sum(0) @ np.abs(kh[b, :lim, 0]).T).max() + 1e-6 + 1e-5 * np.abs(sc[0, :lim]).max()
+        ie, _ = stable_topk(sc, K)
+        d = np.nonzero(ih[b, s, 0] != ie[0])[0]
+        for jj in d:
+            x, y = ih[b, s, 0, jj], ie[0, jj]
+            assert x >= 0 and y >= 0, f"row ({b},{s}) slot {jj}: -1 mismatch ({x} vs {y})"
+            assert abs(float(sc[0, x]) - float(sc[0, y])) <= 2 * tol, f"row ({b},{s}) slot {jj}: {x} vs {y}"
+        flips += len(d)
+        ok = ie[0] >= 0
+        ev = sc[0, np.maximum(ie[0], 0)]
+        ev = ev.astype(np.float16).astype(np.float32) if dtype == torch.float16 else ev
+        gv = vh[b, s, 0]
+        same = ih[b, s, 0] == ie[0]
+        assert np.all(np.abs(gv[ok & same] - ev[ok & same]) <= 2e-3 * np.abs(ev[ok & same]) + 1e-3)
+    print(f"  tie flips {flips} of {len(rows) * K} sampled entries", flush=True)
+    assert flips <= max(4, len(rows) * K // 500)

@@ -75,9 +75,21 @@ def test_noalloc_matches_workspace_entry_point(shapes):
 
 
 def test_noalloc_validates_like_dsa_sfa_fwd():
+    """An unsupported head dim (D = 96) is rejected before any launch; the
+    operands are real device tensors of the declared shapes, so the call
+    stays in bounds whatever the order of the checks."""
     from dsa_triton_ascend_amd import _lib as L
     lib = L.load()
-    stream = L.stream_handle(torch.device("cuda:0"))
-    st = lib.dsa_sfa_fwd_noalloc(1, 1, 1, 1, 1, 1, None, None, None, None, None, 1, 4, 256, 8, 96, 64, 64, 4,
-                                 256, 0, 0, 1, 0, INT64_MAX, INT64_MAX, 0, 0, 0, 0.1, 0, stream)
+    dv = torch.device("cuda:0")
+    stream = L.stream_handle(dv)
+    B, S1, S2, N1, D, DR, K = 1, 4, 256, 8, 96, 64, 64
+    q = torch.zeros(B, S1, N1, D, dtype=torch.bfloat16, device=dv)
+    qr = torch.zeros(B, S1, N1, DR, dtype=torch.bfloat16, device=dv)
+    k = torch.zeros(B, S2, 1, D, dtype=torch.bfloat16, device=dv)
+    kr = torch.zeros(B, S2, 1, DR, dtype=torch.bfloat16, device=dv)
+    si = torch.zeros(B, S1, 1, K, dtype=torch.int32, device=dv)
+    out = torch.empty_like(q)
+    st = lib.dsa_sfa_fwd_noalloc(q.data_ptr(), qr.data_ptr(), k.data_ptr(), kr.data_ptr(), si.data_ptr(),
+                                 out.data_ptr(), None, None, None, None, None, B, S1, S2, N1, D, DR, K, B * S1,
+                                 B * S2, 0, 0, 1, 0, INT64_MAX, INT64_MAX, 0, 0, 0, 0.1, 0, stream)
     assert st == L.DSA_ERR_UNSUPPORTED and b"D must be" in lib.dsa_last_error()
