@@ -85,16 +85,23 @@ template <> struct Mfma16<f16> {
 // Hardware exp2 (v_exp_f32); callers keep arguments <= 0 or -inf.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Butterfly max/sum across the four 16-lane groups that share lane%16.
+// Butterfly max/sum across the four 16-lane groups that share lane%16, on
+// the VALU lane-swap instructions of gfx950: v_permlane16_swap with both
+// operands v returns (v[l], v[l ^ 16]) on every lane and v_permlane32_swap
+// (v[l], v[l ^ 32]).  The pairs and their order match the __shfl_xor(16)
+// then __shfl_xor(32) butterfly, which goes through the LDS crossbar
+// (ds_swizzle / ds_bpermute) instead, so results are bit-identical.
 __device__ __forceinline__ float xgroup_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float xgroup_sum(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // Butterfly max/sum over all 64 lanes of a wave.

@@ -291,6 +291,182 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
   li_store_chunk(p, ri, btab, s_sc, srow, c0, c1);
 }
 
+// ---------------------------------------------------------------------------
+// Multi-row score kernel (BSND query, several query rows per batch, exact
+// head dims 64 / 128 / 256, 16-bit inputs).  One workgroup = 8 consecutive
+// query rows s0 .. s0+7 of one (batch, key head); wave w owns row s0 + w.
+// The rows share every key tile: tiles of 64 keys go HBM/L2 -> LDS by
+// LDS-DMA (global_load_lds_dwordx4, 1 KB per instruction) into a 3-buffer
+// ring, and each wave reads its K fragments (B operands) from LDS while its
+// row's G heads of Q stay in registers (A operands).  One query row per
+// workgroup (the chunked kernel above) re-reads every visible key per row,
+// which at the cfg2 prefill shape is 4.3 GB of L2 reads; here each key row
+// is read once per 8 query rows.  Key rows are stored in LDS with 16-byte
+// chunk c of tile row r at chunk c ^ (r & 15) (r & 7 at D = 64), so the 16
+// lanes of a fragment read (16 rows, one chunk column) hit distinct banks.
+// Workgroups run the longest causal rows first.  A wave's vector-memory
+// operations per tile are exactly its NDW DMAs and one 64-key score store
+// (inline asm, so the count cannot change), which the ring's vmcnt waits
+// count on.
+// ---------------------------------------------------------------------------
+constexpr int kLiRows = 8;       // query rows per workgroup (one per wave)
+constexpr int kLiRowTile = 64;   // keys per LDS tile
+
+__device__ __forceinline__ void li_dma16(unsigned lds_base, const void* gaddr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(lds_base), "v"(gaddr) : "memory");
+}
+__device__ __forceinline__ void li_store_f32(float* addr, float v) {
+  asm volatile("global_store_dword %0, %1, off" :: "v"(addr), "v"(v) : "memory");
+}
+template <int N> __device__ __forceinline__ void li_wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+// Zero key row: the DMA source of keys in -1 (or out-of-range) pages of a
+// paged cache, which de-paging leaves as zero rows (score 0 while visible).
+__device__ __attribute__((aligned(16))) unsigned char g_li_zero_row[512];
+
+template <int D, typename T, int GT>
+__global__ __launch_bounds__(kLiRows * 64, 1) void li_score_rows_kernel(LiParams p) {
+  using E = Elem<T>;
+  using V8 = typename E::v8;
+  constexpr int KS = D / 32;                       // k-steps
+  constexpr int CPR = D / 8;                       // 16-byte chunks per key row
+  constexpr int RPD = 64 / CPR;                    // key rows per 1 KB DMA
+  constexpr int TB = kLiRowTile * D * 2;           // tile bytes
+  constexpr int NDW = TB / 1024 / kLiRows;         // DMAs per wave per tile
+  constexpr int SWM = CPR < 16 ? CPR - 1 : 15;     // chunk swizzle mask
+  constexpr int NBUF = 3;
+  static_assert(NDW >= 1 && NDW * kLiRows * 1024 == TB, "tile DMAs");
+  __shared__ __attribute__((aligned(1024))) unsigned char s_k[NBUF][TB];
+  __shared__ int s_lim[kLiRows];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  const int nbk = p.batch * p.n2;
+  const int ngroups = (p.s1 + kLiRows - 1) / kLiRows;
+  const int bk = blockIdx.x % nbk;
+  const int grp = ngroups - 1 - (int)(blockIdx.x / nbk);  // longest rows first
+  const int b = bk / p.n2, kh = bk - b * p.n2;
+  const int s1 = grp * kLiRows + wave;
+  const bool active = s1 < p.s1;
+  const int row = b * p.s1 + (active ? s1 : 0);
+  const LiRow ri = li_row_info(p, row);
+  const int lim = active ? ri.lim : 0;
+  if (lane == 0) s_lim[wave] = lim;
+  float* srow = p.scores + ((int64_t)row * p.n2 + kh) * p.s2;
+
+  // weights (C-layout rows of this lane) and Q fragments (A operands)
+  const int64_t wbase = (int64_t)row * p.n1 + kh * p.g;
+  float wv[GT][4];
+#pragma unroll
+  for (int ht = 0; ht < GT; ++ht)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int gg = ht * 16 + lg * 4 + r;
+      const float x = li_load_w(p, wbase + (gg < p.g ? gg : 0));
+      wv[ht][r] = gg < p.g ? x : 0.f;
+    }
+  V8 qf[GT][KS];
+#pragma unroll
+  for (int ht = 0; ht < GT; ++ht) {
+    const int g = ht * 16 + li;
+    const int64_t qrow = (int64_t)row * p.n1 + kh * p.g + (g < p.g ? g : 0);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      const u32x4 v = *(const u32x4*)((const T*)p.q + qrow * D + ks * 32 + lg * 8);
+      qf[ht][ks] = as_v8<V8>(g < p.g ? v : z);
+    }
+  }
+  lds_barrier();
+  int kend = 0;
+#pragma unroll
+  for (int w = 0; w < kLiRows; ++w) kend = max(kend, s_lim[w]);
+  const int ntiles = (kend + kLiRowTile - 1) / kLiRowTile;
+
+  // DMA j of this wave covers tile rows (j * kLiRows + wave) * RPD .. +RPD-1;
+  // lane L: row + L / CPR, LDS chunk L % CPR <- source chunk (L % CPR) ^ swz
+  const bool paged = p.layout_k == DSA_LAYOUT_PA_BSND;
+  const int32_t* btab = paged ? p.block_table + (int64_t)ri.b * p.max_blocks : nullptr;
+  const int lastkey = kend > 0 ? kend - 1 : 0;
+  auto issue_tile = [&](int t, int buf) {
+#pragma unroll
+    for (int j = 0; j < NDW; ++j) {
+      const int d = j * kLiRows + wave;
+      const int tr = d * RPD + lane / CPR;
+      int key = t * kLiRowTile + tr;
+      key = key < lastkey ? key : lastkey;  // past the rows' keys: reload the last one
+      const int64_t krow = li_key_row(p, ri, btab, key);
+      const int ch = (lane % CPR) ^ (tr & SWM);
+      const T* src = (const T*)p.k + (krow * p.n2 + kh) * D + ch * 8;
+      if (paged) {
+        const int blk = btab[key / p.page_size];
+        if (blk < 0 || (int64_t)blk >= p.k_rows / p.page_size) src = (const T*)g_li_zero_row + ch * 8;
+      }
+      li_dma16((unsigned)(uintptr_t)&s_k[buf][d * 1024], src);
+    }
+  };
+  issue_tile(0, 0);
+  issue_tile(1, 1);
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t % NBUF;
+    if (active) {
+      if (t == 0) li_wait_vm<NDW>();
+      else if (t == 1) li_wait_vm<NDW + 1>();
+      else li_wait_vm<NDW + 2>();
+    } else {
+      li_wait_vm<NDW>();
+    }
+    lds_barrier();
+    issue_tile(t + 2, (t + 2) % NBUF);  // into the buffer tile t-1 used
+    if (!active) continue;
+    const unsigned char* tb = s_k[buf];
+    auto kread = [&](int kg, int ks) -> V8 {
+      const int tr = kg * 16 + li;
+      const int c = ks * 4 + lg;
+      return as_v8<V8>(*(const u32x4*)(tb + tr * (D * 2) + ((c ^ (tr & SWM)) * 16)));
+    };
+    float outv = -INFINITY;
+    V8 kf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = kread(0, ks);
+#pragma unroll
+    for (int kg = 0; kg < kLiRowTile / 16; ++kg) {
+      f32x4 acc[GT];
+#pragma unroll
+      for (int ht = 0; ht < GT; ++ht) acc[ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const V8 bv = kf[ks];
+        if (kg + 1 < kLiRowTile / 16) kf[ks] = kread(kg + 1, ks);
+#pragma unroll
+        for (int ht = 0; ht < GT; ++ht) acc[ht] = E::mfma(qf[ht][ks], bv, acc[ht]);
+      }
+      float s = 0.f;
+#pragma unroll
+      for (int ht = 0; ht < GT; ++ht)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s += fmaxf(acc[ht][r], 0.f) * wv[ht][r];
+      s = xgroup_sum(s);
+      const int key = t * kLiRowTile + kg * 16 + li;
+      if (lg == kg) outv = key < lim ? s : -INFINITY;
+    }
+    // lane L holds key t*64 + L; lanes past the row's end store the last
+    // entry's value to the last entry (one store instruction per tile)
+    const int key = t * kLiRowTile + lane;
+    const int last = p.s2 - 1 - t * kLiRowTile;
+    const float vlast = __shfl(outv, last < 63 ? last : 63);
+    li_store_f32(srow + (key < p.s2 ? key : p.s2 - 1), key < p.s2 ? outv : vlast);
+  }
+  li_wait_vm<0>();
+  // keys past the tiles are masked
+  if (active)
+    for (int key = ntiles * kLiRowTile + lane; key < p.s2; key += 64) srow[key] = -INFINITY;
+}
+
 // fp32 query / key (and weights): the products run on v_mfma_f32_16x16x4f32
 // in full fp32.  A lane loads 16 bytes (4 consecutive d) of a Q row and of a
 // K row, as the 16-bit kernel does, and feeds them to four MFMAs, element t
@@ -998,6 +1174,255 @@ __global__ __launch_bounds__(kTopkThreads) void li_topk_kernel(TopkParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Short rows (prefill): four rows per workgroup, one per 256-thread quarter,
+// with the fast selection above scaled down (2048 bins, KPT keys per thread
+// for rows of up to 256 * KPT scores, K <= kQuadMaxK).  A quarter needs
+// about 36 KB of LDS where the one-row kernel needs 114 KB, so a CU holds
+// four rows at a time instead of one, and their barrier waits and memory
+// round trips overlap.  Each bin keeps one cursor word: it starts at the
+// bin's first slot and ends one past its last, so the bin's start is the
+// cursor minus the count.  A selected entry's value is recovered from its
+// key (the map is invertible except that -0.0 shares +0.0's key, so zero
+// keys read the score itself).  Every barrier is workgroup-wide and reached
+// by every thread (the four rows advance in step).  A row whose candidates
+// overflow the buffer or crowd into one bin is marked, and after the four
+// fast rows the whole workgroup runs the general selection on each marked
+// row.
+// ---------------------------------------------------------------------------
+constexpr int kQuadRows = 4;
+constexpr int kQuadThr = kTopkThreads / kQuadRows;  // 256 per row
+constexpr int kQuadBins = 2048;
+constexpr int kQuadBinBits = 11;
+constexpr int kQuadBpt = kQuadBins / kQuadThr;      // bins per thread in the scan
+constexpr int kQuadCap = 2560;                      // candidates per row
+constexpr int kQuadCpt = kQuadCap / kQuadThr;       // candidates per thread in the rank pass
+constexpr int kQuadMaxK = 2048;
+constexpr int kQuadWaves = kQuadThr / 64;
+constexpr size_t kQuadRowLds = 2 * (size_t)kQuadBins * 4 + (size_t)kQuadCap * 8 + 16 * 4;
+constexpr size_t kQuadLds = kQuadRows * kQuadRowLds + 64;
+static_assert(kQuadCap % kQuadThr == 0 && kQuadBins % kQuadThr == 0 && (1 << kQuadBinBits) == kQuadBins, "quad");
+
+// the score of a key (inverse of sort_key; +0.0 for the zero key)
+__device__ __forceinline__ float unsort_key(unsigned k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+constexpr unsigned kZeroKey = 0x80000000u;  // sort_key(+0.0) == sort_key(-0.0)
+
+// Marked rows of a four-row workgroup: the general selection with the whole
+// workgroup, one row at a time (the LDS of the fast rows is dead by then).
+// Not inlined: inside the fast kernel the general path's registers would be
+// allocated for the whole kernel (128 VGPRs with spills against 60); it runs
+// only for rows with crowded keys.
+// The parameters go by value: taking the address of the kernel's copy would
+// put it in scratch and turn every pointer of the fast path into a generic
+// (flat) one, whose stores also count on the LDS counter, so each LDS wait
+// of the output loop would wait for the stores to complete.
+__device__ __attribute__((noinline)) void topk_quad_fallback(TopkParams p, unsigned marked, unsigned char* smem) {
+  for (int r = 0; r < kQuadRows; ++r) {
+    if (!((marked >> r) & 1u)) continue;
+    __syncthreads();
+    topk_row_generic<true>(p, (int64_t)blockIdx.x * kQuadRows + r, smem);
+  }
+}
+
+template <int KPT>
+__global__ __launch_bounds__(kTopkThreads) void li_topk_quad_kernel(TopkParams p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char tk_smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int q = tid / kQuadThr, tq = tid - q * kQuadThr, wq = tq >> 6;  // quarter, thread and wave in it
+  const int64_t row = (int64_t)blockIdx.x * kQuadRows + q;
+  const bool live = row < p.rows;
+  const int S = p.s2, K = p.k;
+  unsigned char* qb = tk_smem + q * kQuadRowLds;
+  unsigned* const hcount = (unsigned*)qb;                          // kQuadBins
+  unsigned* const cursor = hcount + kQuadBins;                     // kQuadBins
+  unsigned long long* const cand = (unsigned long long*)(cursor + kQuadBins);  // kQuadCap
+  unsigned* const misc = (unsigned*)(cand + kQuadCap);             // 16 words
+  unsigned* const flags = (unsigned*)(tk_smem + kQuadRows * kQuadRowLds);  // kQuadRows
+  const float* srow = p.scores + (live ? row : 0) * (int64_t)S;
+
+  // keys in registers: entry u * 256 + tq (coalesced over the quarter).  The
+  // loads are unconditional (index clamped into the row), so all of them are
+  // in flight together: under a lane condition each one was issued in its
+  // own branch and waited for there.
+  unsigned kr[KPT];
+  {
+    float kv[KPT];
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const int j = u * kQuadThr + tq;
+      kv[u] = srow[j < S ? j : S - 1];
+    }
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) kr[u] = (live && u * kQuadThr + tq < S) ? sort_key(kv[u]) : kNegInfKey;
+  }
+  for (int i = tq; i < kQuadBins; i += kQuadThr) hcount[i] = 0u;
+  if (tid < kQuadRows) flags[tid] = 0u;
+
+  // ---- 1. count and range of the finite keys ----
+  int nv = 0;
+  unsigned kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+  for (int u = 0; u < KPT; ++u) {
+    const bool v = kr[u] > kNegInfKey;
+    nv += v;
+    kmin = v ? min(kmin, kr[u]) : kmin;
+    kmax = v ? max(kmax, kr[u]) : kmax;
+  }
+  {
+    const unsigned tn = wave_reduce_to63((unsigned)nv, 0u, [](unsigned a, unsigned b) { return a + b; });
+    const unsigned tmin = wave_reduce_to63(kmin, 0xffffffffu, [](unsigned a, unsigned b) { return min(a, b); });
+    const unsigned tmax = wave_reduce_to63(kmax, 0u, [](unsigned a, unsigned b) { return max(a, b); });
+    if (lane == 63) {
+      misc[wq] = tn;
+      misc[4 + wq] = tmin;
+      misc[8 + wq] = tmax;
+    }
+  }
+  __syncthreads();
+  int n_valid = 0;
+  kmin = 0xffffffffu;
+  kmax = 0u;
+#pragma unroll
+  for (int w = 0; w < kQuadWaves; ++w) {
+    n_valid += (int)misc[w];
+    kmin = min(kmin, misc[4 + w]);
+    kmax = max(kmax, misc[8 + w]);
+  }
+  const int take = min(K, n_valid);
+  const unsigned diff = kmin ^ kmax;
+  const int hb = diff ? 32 - __clz((int)diff) : 0;
+  const int shift = hb > kQuadBinBits ? hb - kQuadBinBits : 0;
+  auto digit = [&](unsigned kk) { return (kk >> shift) & (unsigned)(kQuadBins - 1); };
+
+  // ---- 2. histogram, bin starts (descending), threshold bin ----
+  if (take > 0) {
+#pragma unroll
+    for (int u = 0; u < KPT; ++u)
+      if (kr[u] > kNegInfKey) atomicAdd(&hcount[digit(kr[u])], 1u);
+  }
+  __syncthreads();  // also: the misc reads are done before misc is rewritten
+  // thread tq owns bins kQuadBins - 1 - kQuadBpt * tq - i (descending)
+  unsigned c[kQuadBpt], ex[kQuadBpt];
+  unsigned loc = 0;
+#pragma unroll
+  for (int i = 0; i < kQuadBpt; ++i) {
+    c[i] = hcount[kQuadBins - 1 - kQuadBpt * tq - i];
+    loc += c[i];
+  }
+  const unsigned incl = wave_incl_scan(loc);
+  if (lane == 63) misc[12 + wq] = incl;
+  __syncthreads();
+  {
+    unsigned run = incl - loc;
+#pragma unroll
+    for (int w = 0; w < kQuadWaves; ++w) run += w < wq ? misc[12 + w] : 0u;
+#pragma unroll
+    for (int i = 0; i < kQuadBpt; ++i) {
+      ex[i] = run;
+      run += c[i];
+    }
+  }
+  __syncthreads();  // the wave totals are read before misc is rewritten
+#pragma unroll
+  for (int i = 0; i < kQuadBpt; ++i) {
+    const int b = kQuadBins - 1 - kQuadBpt * tq - i;
+    cursor[b] = ex[i];
+    if (take > 0 && ex[i] < (unsigned)take && ex[i] + c[i] >= (unsigned)take) {
+      misc[0] = (unsigned)b;    // b*
+      misc[1] = ex[i] + c[i];   // keys in bins >= b*
+    }
+  }
+  if (tq == 0) misc[2] = 0u;
+  __syncthreads();
+  const unsigned bstar = take > 0 ? misc[0] : 0u;
+  const int ncand = take > 0 ? (int)misc[1] : 0;
+  {
+    unsigned cm = 0;
+#pragma unroll
+    for (int i = 0; i < kQuadBpt; ++i) cm = (unsigned)(kQuadBins - 1 - kQuadBpt * tq - i) >= bstar ? max(cm, c[i]) : cm;
+    cm = wave_reduce_to63(cm, 0u, [](unsigned a, unsigned b) { return max(a, b); });
+    if (lane == 63 && cm && take > 0) atomicMax(&misc[2], cm);
+  }
+  __syncthreads();
+  const bool fallback = live && take > 0 && (ncand > kQuadCap || misc[2] > (unsigned)kSegCap);
+  const bool fast = live && !fallback;
+
+  // ---- 3. counting sort of the candidates by bin: every cursor atomic of a
+  // thread first, then its candidate writes ----
+  if (fast && take > 0) {
+    unsigned slot[KPT];
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const bool is_c = kr[u] > kNegInfKey && digit(kr[u]) >= bstar;
+      slot[u] = is_c ? atomicAdd(&cursor[digit(kr[u])], 1u) : 0xffffffffu;
+    }
+#pragma unroll
+    for (int u = 0; u < KPT; ++u)
+      if (slot[u] != 0xffffffffu) cand[slot[u]] = ((unsigned long long)(~kr[u]) << 32) | (unsigned)(u * kQuadThr + tq);
+  }
+  __syncthreads();
+
+  // ---- 4. rank within the bin (bin start = cursor - count), then outputs ----
+  int32_t* irow = p.indices + (live ? row : 0) * (int64_t)K;
+  auto put = [&](int i, int idx, float val) {
+    irow[i] = idx;
+    if (p.values) {
+      const int64_t o = row * (int64_t)K + i;
+      if (p.val_dtype == DSA_DTYPE_FP32) ((float*)p.values)[o] = val;
+      else if (p.val_dtype == DSA_DTYPE_BF16) ((bf16*)p.values)[o] = (bf16)val;
+      else ((f16*)p.values)[o] = (f16)val;
+    }
+  };
+  if (fast) {
+    // the thread's candidates q = i * 256 + tq; each is ranked against its
+    // bin's entries, four reads in flight per step (the reads of a step past
+    // the bin's end are clamped into it and not counted)
+    unsigned long long cv_r[kQuadCpt];
+    int s0_r[kQuadCpt], rank_r[kQuadCpt];
+#pragma unroll
+    for (int i = 0; i < kQuadCpt; ++i) cv_r[i] = cand[min(i * kQuadThr + tq, kQuadCap - 1)];
+#pragma unroll
+    for (int i = 0; i < kQuadCpt; ++i) {
+      rank_r[i] = 0;
+      s0_r[i] = 0;
+      if (i * kQuadThr + tq < ncand) {
+        const unsigned long long cv = cv_r[i];
+        const unsigned d = digit(~(unsigned)(cv >> 32));
+        const int nb = (int)hcount[d];
+        const int s0 = (int)cursor[d] - nb;
+        int rank = 0;
+        for (int r = 0; r < nb; r += 4) {
+          unsigned long long e[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) e[j] = cand[s0 + min(r + j, nb - 1)];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) rank += (r + j < nb && e[j] < cv) ? 1 : 0;
+        }
+        s0_r[i] = s0;
+        rank_r[i] = rank;
+      }
+    }
+    int pos_r[kQuadCpt];
+#pragma unroll
+    for (int i = 0; i < kQuadCpt; ++i) pos_r[i] = i * kQuadThr + tq < ncand ? s0_r[i] + rank_r[i] : -1;
+#pragma unroll
+    for (int i = 0; i < kQuadCpt; ++i) {
+      if (pos_r[i] >= 0 && pos_r[i] < take) {
+        const unsigned key = ~(unsigned)(cv_r[i] >> 32);
+        const int idx = (int)(unsigned)(cv_r[i] & 0xffffffffull);
+        put(pos_r[i], idx, key == kZeroKey ? srow[idx] : unsort_key(key));
+      }
+    }
+    for (int i = take + tq; i < K; i += kQuadThr) put(i, -1, -INFINITY);
+  }
+  if (fallback && tq == 0) flags[q] = 1u;
+  __syncthreads();
+  const unsigned marked = flags[0] | (flags[1] << 1) | (flags[2] << 2) | (flags[3] << 3);
+  if (marked) topk_quad_fallback(p, marked, tk_smem);  // uniform
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 static int64_t pow2_at_least(int64_t x) {
@@ -1031,6 +1456,19 @@ int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_
   // dynamic LDS above 64 KB needs the per-function limit raised (to the
   // full budget; set on every call, which also covers every device and
   // concurrent callers: a host-side setting, cheap next to the launch)
+  // many short rows: four per workgroup (the general path of a marked row
+  // runs in the same LDS, so it must fit there with the row kept in LDS)
+  if (rows > (int64_t)device_cu_count() && s2 <= 32 * kQuadThr && k <= kQuadMaxK &&
+      li_topk_fixed_bytes(k) + (size_t)s2 * 4 <= (size_t)kQuadRows * kQuadRowLds) {
+    const void* fq = s2 <= 8 * kQuadThr    ? (const void*)li_topk_quad_kernel<8>
+                     : s2 <= 16 * kQuadThr ? (const void*)li_topk_quad_kernel<16>
+                                           : (const void*)li_topk_quad_kernel<32>;
+    DSA_HIP(hipFuncSetAttribute(fq, hipFuncAttributeMaxDynamicSharedMemorySize, kTopkLdsBudget));
+    void* args[] = {&p};
+    DSA_HIP(hipLaunchKernel(fq, dim3((unsigned)((rows + kQuadRows - 1) / kQuadRows)), dim3(kTopkThreads), args,
+                            kQuadLds, stream));
+    return DSA_OK;
+  }
   const bool in_lds = li_topk_row_in_lds(s2, k);
   size_t lds = li_topk_fixed_bytes(k) + (in_lds ? (size_t)s2 * 4 : 0);  // general path
   if (lds < kFastLds) lds = kFastLds;
@@ -1067,6 +1505,17 @@ static hipError_t launch_score(const LiParams& p, hipStream_t stream) {
   // one query row per batch: no key is read twice (exact head dims only)
   if (!PAD && p.q_rows == p.batch)
     return launch_score_kernel((const void*)li_score_kernel<D, T, GT, false, true>, p, stream);
+  // several query rows per batch (BSND): rows share key tiles through LDS,
+  // while the row's Q fragments fit the registers (GT * D / 32 <= 16)
+  if constexpr (!PAD && GT * (D / 32) <= 16) {
+    if (p.layout_q == DSA_LAYOUT_BSND && p.s1 >= 4) {
+      LiParams q = p;
+      const unsigned grid = (unsigned)((int64_t)p.batch * p.n2 * ((p.s1 + kLiRows - 1) / kLiRows));
+      void* args[] = {&q};
+      return hipLaunchKernel((const void*)li_score_rows_kernel<D, T, GT>, dim3(grid), dim3(kLiRows * 64), args, 0,
+                             stream);
+    }
+  }
   return launch_score_kernel((const void*)li_score_kernel<D, T, GT, PAD, false>, p, stream);
 }
 

@@ -88,6 +88,40 @@ def test_topk_bit_exact(S2, k, kind):
     np.testing.assert_array_equal(vg, ve)
 
 
+@pytest.mark.parametrize("S2,k", [(300, 64), (2049, 2048), (4096, 2048), (4096, 1), (8192, 2048), (1500, 2048)])
+def test_topk_many_short_rows_bit_exact(S2, k):
+    """More rows than CUs (the four-rows-per-workgroup selection): every row
+    kind in one launch, so the four rows of a workgroup mix fast rows with
+    rows that take the general path (all-equal keys crowd one bin), rows
+    with few or no visible keys, exact ties, signed zeros and narrow ranges.
+    Bit-exact against np.lexsort on the same fp32 scores."""
+    print(f"[li topk many rows] S2={S2} k={k}", flush=True)
+    rng = np.random.RandomState(S2 * 7 + k)
+    R = 600
+    sc = (rng.randn(R, S2) * 10).astype(np.float32)
+    kinds = rng.randint(0, 7, R)
+    for r in range(R):
+        if kinds[r] == 1:      # ties
+            sc[r] = rng.randint(0, 7, S2).astype(np.float32) * 0.5
+        elif kinds[r] == 2:    # all equal: one crowded bin
+            sc[r] = 3.25
+        elif kinds[r] == 3:    # visible prefix of random length
+            sc[r, rng.randint(0, S2 + 1):] = -np.inf
+        elif kinds[r] == 4:    # narrow range (a few ulps)
+            sc[r] = np.float32(100.0) + rng.randint(0, 40, S2).astype(np.float32) * np.float32(2 ** -17)
+        elif kinds[r] == 5:    # signed zeros and a block of exact ties
+            sc[r, ::5] = -0.0
+            sc[r, 1::5] = 0.0
+            sc[r, :50] = 1.5
+        elif kinds[r] == 6:    # nothing visible
+            sc[r] = -np.inf
+    sc = sc.astype(np.float32)
+    ie, ve = stable_topk(sc, k)
+    ig, vg = _topk_gpu(sc, k)
+    np.testing.assert_array_equal(ig, ie)
+    np.testing.assert_array_equal(vg, ve)
+
+
 # ---------------------------------------------------------------------------
 # scores
 # ---------------------------------------------------------------------------
