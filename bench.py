@@ -53,8 +53,8 @@ def parse():
     ap.add_argument("--long-steps", type=int, default=10,
                     help="timed steps of the prefill / backward legs (each step is milliseconds)")
     ap.add_argument("--no-long", action="store_true", help="skip the prefill / backward legs")
-    ap.add_argument("--legs", default="prefill,bwd,bwd_merged,kl,dense",
-                    help="comma list of the long legs to run (prefill, bwd, bwd_merged, kl, dense)")
+    ap.add_argument("--legs", default="prefill,prefill_blocks,bwd,bwd_merged,kl,dense",
+                    help="comma list of the long legs to run (prefill, prefill_blocks, bwd, bwd_merged, kl, dense)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain copy kernel of known size (for PMC calibration)")
     return ap.parse_args()
@@ -485,6 +485,26 @@ def causal_indices(S, K, g, device):
     return idx, int(nval.sum())
 
 
+def causal_block_indices(S, K, bs, g, device):
+    """Block-wise causal indices: row s1 holds min(K, nb) distinct uniform
+    block ids from [0, nb), nb = ceil((s1 + 1) / bs), sorted and -1-padded
+    to K; returns them and the valid (row, token) pairs (the tokens of a
+    block at or before s1)."""
+    import torch
+    nblk = (S + bs - 1) // bs
+    ar = torch.arange(S, device=device)
+    nb = (ar + bs) // bs                                           # visible blocks per row
+    r = torch.rand(S, nblk, generator=g, device=device)
+    r[torch.arange(nblk, device=device)[None, :] >= nb[:, None]] = 2.0
+    idx = torch.sort(torch.argsort(r, dim=1)[:, :K], dim=1).values.to(torch.int32)
+    del r
+    nsel = torch.clamp(nb, max=K)
+    idx[torch.arange(K, device=device)[None, :] >= nsel[:, None]] = -1
+    tok = ar[:, None] + 1 - idx.long() * bs                        # tokens of the block at or before s1
+    pairs = torch.where(idx >= 0, torch.clamp(tok, 0, bs), torch.zeros_like(tok)).sum()
+    return idx, int(pairs)
+
+
 def time_call(fn, steps, warmup):
     import torch
     for _ in range(warmup):
@@ -513,7 +533,7 @@ def leg(metric, workload, flops, ms, n):
             "algorithmic_flops": int(flops), "valid_pairs": n, "config": {"workload": workload}}
 
 
-def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense"), cpu_s=0.0):
+def long_legs(dev, steps, legs=("prefill", "prefill_blocks", "bwd", "bwd_merged", "kl", "dense"), cpu_s=0.0):
     """The prefill forward and the backward legs; with cpu_s > 0 each also
     gets a CPU baseline (oracle on a seeded row sample, about cpu_s seconds)."""
     import numpy as np
@@ -543,6 +563,25 @@ def long_legs(dev, steps, legs=("prefill", "bwd", "bwd_merged", "kl", "dense"), 
                                      "causal, sparse_mode 3, stats returned", flops, ms, n)
         if cpu_s > 0:
             out["sfa_fwd_prefill"]["cpu_baseline"] = cpu_fwd_rows(q, qr, k, kr, si, scale, T, flops, n, cpu_s)
+    # the same prefill with block-wise indices over more than 2048 positions
+    # per row (2048 block ids of 2 tokens): each row's range is split in two
+    # one-list pieces and merged by the combine kernel
+    if "prefill_blocks" in legs:
+        BS2 = 2
+        bidx, nb2 = causal_block_indices(T, K, BS2, g, dev)
+        sib = bidx.reshape(T, 1, K).contiguous()
+
+        def fwd_blocks():
+            return dsa.sparse_flash_attention_triton(q, k, k, sib, scale_value=scale, actual_seq_lengths_query=cu,
+                                                     actual_seq_lengths_kv=cu, query_rope=qr, key_rope=kr,
+                                                     sparse_block_size=BS2, layout_query="TND", layout_kv="TND",
+                                                     sparse_mode=3, return_softmax_lse=True)
+        ms = time_call(fwd_blocks, steps, 2)
+        out["sfa_fwd_prefill_blocks"] = leg("SFA fwd TFLOP/s (prefill, 2048 blocks of 2: 4096 positions per row)",
+                                            "sfa_fwd prefill: TND one sequence T=8192, N1=128, D=512+64, topK=2048 "
+                                            "causal block ids, sparse_block_size 2, sparse_mode 3, stats returned",
+                                            2.0 * N1 * (2 * D + DR) * nb2, ms, nb2)
+        del bidx, sib
     del q, qr, k, kr, idx, si
     torch.cuda.empty_cache()
     # cfg5a / cfg5b: backward pair at S=4096

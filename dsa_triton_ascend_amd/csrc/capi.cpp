@@ -44,8 +44,8 @@ int device_cu_count() {
 
 // sfa_fwd.hip
 struct SfaFwdParams;
-int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos);
-size_t sfa_fwd_workspace_bytes(int64_t rows, int64_t n1, int64_t d, int64_t total_pos);
+int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos, bool one_list);
+size_t sfa_fwd_workspace_bytes(int64_t rows, int64_t n1, int64_t d, int64_t total_pos, bool one_list);
 size_t sfa_fwd_scratch_bytes();
 int sfa_fwd_scratch(void** ptr);
 int sfa_fwd_run(const void* query, const void* query_rope, const void* key, const void* key_rope,
@@ -56,7 +56,7 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
                 int64_t max_blocks, int64_t page_size, int32_t sparse_block_size,
                 int32_t sparse_mode, int64_t pre_tokens, int64_t next_tokens, int32_t layout_query,
                 int32_t layout_kv, int32_t dtype, float scale_value, int32_t return_lse, void* workspace,
-                hipStream_t stream);
+                hipStream_t stream, bool one_list);
 
 // sfa_bwd.hip
 size_t sfa_bwd_workspace_bytes(int64_t q_rows, int64_t kv_rows, int64_t n1, int64_t d, int64_t total_pos,
@@ -246,7 +246,7 @@ size_t dsa_sfa_fwd_workspace_size(int64_t q_rows, int64_t n1, int64_t d, int64_t
   if (q_rows <= 0 || q_rows >= (1ll << 31) || n1 <= 0 || n1 > 128 || d <= 0 || d > 512 || sparse_count <= 0 ||
       sparse_block_size <= 0 || !mul_le(sparse_count, sparse_block_size, 1ll << 30))
     return 0;
-  return sfa_fwd_workspace_bytes(q_rows, n1, d, sparse_count * (int64_t)sparse_block_size);
+  return sfa_fwd_workspace_bytes(q_rows, n1, d, sparse_count * (int64_t)sparse_block_size, true);
 }
 
 int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, const void* key_rope,
@@ -264,7 +264,7 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, cons
                                  sparse_count, q_rows, kv_rows, max_blocks, page_size, sparse_block_size,
                                  sparse_mode, layout_query, layout_kv, dtype, return_lse);
   if (st != DSA_OK) return st;
-  const size_t need = sfa_fwd_workspace_bytes(q_rows, n1, d, sparse_count * (int64_t)sparse_block_size);
+  const size_t need = sfa_fwd_workspace_bytes(q_rows, n1, d, sparse_count * (int64_t)sparse_block_size, true);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     set_error("workspace of %zu bytes required, %zu given", need, workspace_bytes);
     return DSA_ERR_WORKSPACE;
@@ -273,7 +273,7 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key, cons
                      softmax_sum, actual_seq_q, actual_seq_kv, block_table, batch, s1, s2, n1, d,
                      sparse_count, q_rows, kv_rows, max_blocks, page_size, sparse_block_size,
                      sparse_mode, pre_tokens, next_tokens, layout_query, layout_kv, dtype, scale_value, return_lse,
-                     workspace, (hipStream_t)stream);
+                     workspace, (hipStream_t)stream, true);
 }
 
 int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* key, const void* key_rope,
@@ -291,7 +291,11 @@ int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* k
                                  sparse_count, q_rows, kv_rows, max_blocks, page_size, sparse_block_size,
                                  sparse_mode, layout_query, layout_kv, dtype, return_lse);
   if (st != DSA_OK) return st;
-  const size_t need = sfa_fwd_workspace_bytes(q_rows, n1, d, sparse_count * (int64_t)sparse_block_size);
+  // the one-list splits when their partials fit the scratch, else the
+  // splits that fill the CUs (long ranges then run chunked)
+  const int64_t total_pos = sparse_count * (int64_t)sparse_block_size;
+  const bool one_list = sfa_fwd_workspace_bytes(q_rows, n1, d, total_pos, true) <= sfa_fwd_scratch_bytes();
+  const size_t need = sfa_fwd_workspace_bytes(q_rows, n1, d, total_pos, one_list);
   void* ws = nullptr;
   if (need > 0) {
     DSA_CHECK_SUPPORTED(need <= sfa_fwd_scratch_bytes(),
@@ -305,7 +309,7 @@ int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* k
                      softmax_sum, actual_seq_q, actual_seq_kv, block_table, batch, s1, s2, n1, d,
                      sparse_count, q_rows, kv_rows, max_blocks, page_size, sparse_block_size,
                      sparse_mode, pre_tokens, next_tokens, layout_query, layout_kv, dtype, scale_value, return_lse, ws,
-                     (hipStream_t)stream);
+                     (hipStream_t)stream, one_list);
 }
 
 size_t dsa_sfa_bwd_workspace_size(int64_t q_rows, int64_t kv_rows, int64_t n1, int64_t d, int64_t sparse_count,

@@ -1406,8 +1406,15 @@ __global__ __launch_bounds__(256) void sfa_combine_kernel(SfaFwdParams p) {
   constexpr int PER = D / 64;
   typedef _Float16 hvec __attribute__((ext_vector_type(PER)));
   const int lane = threadIdx.x & 63;
-  const int64_t rh = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (rh >= p.rows * p.n1) return;
+  // (row, head) of this wave, with the forward launch's XCD mapping (rows
+  // rows_per_xcd * x .. of XCD x = blockIdx & 7), so the partials a wave
+  // reads were written through the same XCD's L2
+  const int bpr = (p.n1 + 3) / 4;  // blocks per row
+  const int jb = (int)(blockIdx.x >> 3);
+  const int64_t crow = (int64_t)(blockIdx.x & 7) * p.rows_per_xcd + jb / bpr;
+  const int chead = (jb % bpr) * 4 + (int)(threadIdx.x >> 6);
+  if (crow >= p.rows || chead >= p.n1) return;
+  const int64_t rh = crow * p.n1 + chead;
   const int64_t sstride = p.rows * p.n1;  // (row, head) records per split
   if (p.splits <= 8) {
     // every load up front (lane s < splits: the record of split s; all
@@ -1598,14 +1605,36 @@ static int sfa_fwd_heads_per_wg(int64_t rows, int64_t n1, int64_t d, int64_t tot
   return sfa_fwd_kind(rows, n1, d, total_pos) == kFwdDs64 ? kSfaDsHeads : kSfaHeadsPerWg;
 }
 
-int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
-  return sfa_fwd_plan_splits(rows, n1, total_pos, sfa_fwd_heads_per_wg(rows, n1, d, total_pos));
-}
-
-size_t sfa_fwd_workspace_bytes(int64_t rows, int64_t n1, int64_t d, int64_t total_pos) {
-  const int splits = sfa_fwd_splits(rows, n1, d, total_pos);
+static size_t sfa_fwd_ws_for(int64_t splits, int64_t rows, int64_t n1, int64_t d) {
   if (splits <= 1) return 0;
   return (size_t)splits * rows * n1 * (d * sizeof(_Float16) + 4 * sizeof(float));
+}
+
+// At D = 512 the kernels that compact and run a split's positions in
+// several pieces (a range above kSfaMaxList) run out of registers and spill
+// (56 - 628 bytes per lane), so a D = 512 launch takes at least
+// ceil(total_pos / kSfaMaxList) token splits and every workgroup's range
+// fits the list in one piece (the combine kernel merges the splits).
+// one_list = false keeps the splits that fill the CUs and lets the chunked
+// kernel take long ranges: the no-alloc entry point falls back to it when
+// the extra splits' partials would not fit its scratch, and so does any
+// launch whose extra partials would pass kSfaOneListMaxWs.
+constexpr size_t kSfaOneListMaxWs = 4ull << 30;
+static int sfa_fwd_splits_for(int64_t rows, int64_t n1, int64_t d, int64_t total_pos, bool one_list) {
+  const int fill = sfa_fwd_plan_splits(rows, n1, total_pos, sfa_fwd_heads_per_wg(rows, n1, d, total_pos));
+  if (!one_list || d != 512 || (test_flags() & kTestFwdWide)) return fill;
+  const int64_t need = (total_pos + kSfaMaxList - 1) / kSfaMaxList;
+  if (need <= fill) return fill;
+  if (sfa_fwd_ws_for(need, rows, n1, d) > kSfaOneListMaxWs) return fill;
+  return (int)need;
+}
+
+int sfa_fwd_splits(int64_t rows, int64_t n1, int64_t d, int64_t total_pos, bool one_list) {
+  return sfa_fwd_splits_for(rows, n1, d, total_pos, one_list);
+}
+
+size_t sfa_fwd_workspace_bytes(int64_t rows, int64_t n1, int64_t d, int64_t total_pos, bool one_list) {
+  return sfa_fwd_ws_for(sfa_fwd_splits_for(rows, n1, d, total_pos, one_list), rows, n1, d);
 }
 
 template <int D, typename T>
@@ -1646,7 +1675,7 @@ static hipError_t launch_sfa_fwd(SfaFwdParams& p, SfaFwdKind kind, hipStream_t s
     hipLaunchKernelGGL((sfa_fwd_kernel<D, T, C::HT, C::NW, false, true>), grid, block, 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) return e;
-  const int64_t cblocks = (p.rows * p.n1 + 3) / 4;
+  const int64_t cblocks = 8 * rows_per_xcd * ((p.n1 + 3) / 4);
   hipLaunchKernelGGL((sfa_combine_kernel<D, T>), dim3((unsigned)cblocks), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
@@ -1659,7 +1688,7 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
                 int64_t max_blocks, int64_t page_size, int32_t sparse_block_size,
                 int32_t sparse_mode, int64_t pre_tokens, int64_t next_tokens, int32_t layout_query,
                 int32_t layout_kv, int32_t dtype, float scale_value, int32_t return_lse, void* workspace,
-                hipStream_t stream) {
+                hipStream_t stream, bool one_list) {
   SfaFwdParams p;
   p.q = query;
   p.qr = query_rope;
@@ -1689,7 +1718,7 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
   p.page_size = (int32_t)page_size;
   const int64_t total_pos = sparse_count * (int64_t)sparse_block_size;
   const SfaFwdKind kind = sfa_fwd_kind(q_rows, n1, d, total_pos);
-  p.splits = sfa_fwd_plan_splits(q_rows, n1, total_pos, kind == kFwdDs64 ? kSfaDsHeads : kSfaHeadsPerWg);
+  p.splits = sfa_fwd_splits_for(q_rows, n1, d, total_pos, one_list);
   p.pos_per_split = (int32_t)((total_pos + p.splits - 1) / p.splits);
   p.part_o = nullptr;
   p.part_ml = nullptr;

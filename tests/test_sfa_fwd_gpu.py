@@ -506,17 +506,59 @@ def test_fwd_block_indices_span_chunks(B, S1, S2, N1, K, bs, mode, D):
 
 
 def test_fwd_split_workspace_is_bounded():
-    """The split workspace stays below 1.5 CUs' worth of partial rows for any
-    index length (no split is forced by the list length)."""
+    """The split workspace: below 1.5 CUs' worth of partial rows while the
+    positions per row fit one list (2048); at D = 512 longer lists take
+    ceil(positions / 2048) splits (so no workgroup runs the chunked kernel),
+    up to 4 GiB of partials, beyond which the chunked kernel runs with the
+    splits that fill the CUs."""
     from dsa_triton_ascend_amd import _lib
     lib = _lib.load()
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    bound = int(1.5 * cus) * 128 * (512 * 2 + 16)
+    per_split_row = 128 * (512 * 2 + 16)
+    bound = int(1.5 * cus) * per_split_row
     for rows in (1, 7, 32, 100, 128, 129, 255, 256, 8192):
-        for k, bs in ((2048, 1), (2048, 128), (4096, 1), (64, 64)):
+        for k, bs in ((2048, 1), (2048, 128), (4096, 1), (64, 64), (1500, 2)):
             ws = lib.dsa_sfa_fwd_workspace_size(rows, 128, 512, k, bs)
-            assert ws <= bound, (rows, k, bs, ws)
-    assert lib.dsa_sfa_fwd_workspace_size(8192, 128, 512, 2048, 128) == 0
+            need = -(-(k * bs) // 2048)
+            if need * rows * per_split_row <= 4 << 30:
+                assert ws <= max(bound, need * rows * per_split_row), (rows, k, bs, ws)
+                assert ws >= (need * rows * per_split_row if need > 1 else 0), (rows, k, bs, ws)
+            else:
+                assert ws <= bound, (rows, k, bs, ws)
+            # D < 512 never splits by list length
+            assert lib.dsa_sfa_fwd_workspace_size(rows, 128, 256, k, bs) <= int(1.5 * cus) * 128 * (256 * 2 + 16)
+    assert lib.dsa_sfa_fwd_workspace_size(8192, 128, 512, 2048, 1) == 0
+    assert lib.dsa_sfa_fwd_workspace_size(8192, 128, 512, 2048, 2) == 2 * 8192 * per_split_row
+    assert lib.dsa_sfa_fwd_workspace_size(8192, 128, 512, 2048, 128) == 0  # chunked: 128 splits would be 137 GB
+
+
+# D = 512 with more than 2048 positions per row and rows that fill the CUs
+# (one split each by occupancy): the launch takes ceil(positions / 2048)
+# splits and the combine kernel merges them.
+LONG_D512_CASES = [
+    # B, S1, S2, N1, K, bs, mode
+    (1, 300, 6000, 128, 3000, 1, 3),
+    (1, 260, 5000, 128, 1500, 2, 0),
+]
+
+
+@pytest.mark.parametrize("B,S1,S2,N1,K,bs,mode", LONG_D512_CASES)
+def test_fwd_d512_long_lists_split(B, S1, S2, N1, K, bs, mode):
+    print(f"[sfa_fwd long d512] B={B} S1={S1} S2={S2} N1={N1} K={K} bs={bs} mode={mode}", flush=True)
+    dtype, D = torch.bfloat16, 512
+    q, k, qr, kr = sfa_inputs(B, S1, S2, N1, D, dtype, seed=111)
+    si = sparse_indices(B, S1, S2, K, bs, mode, seed=112)
+    scale = 1.0 / np.sqrt(D + 64)
+    out, smax, ssum = _run(q, k, qr, kr, si, dtype, scale, mode, bs)
+    rows = [(0, s) for s in (0, 1, S1 // 3, S1 // 2, S1 - 2, S1 - 1)]
+    ref = sfa_fwd_bsnd(q, k, si, qr, kr, scale, [S1] * B, [S2] * B, bs, mode, True, "float32",
+                       positions="kernel", rows=rows)
+    sel = tuple(np.array(rows).T)
+    assert_close(out[sel], ref[0][sel], RTOL, ATOL, "attention_out")
+    assert_close(smax[0, 0][[r[1] for r in rows]], ref[1][0, 0][[r[1] for r in rows]], RTOL, ATOL, "softmax_max")
+    assert_close(ssum[0, 0][[r[1] for r in rows]], ref[2][0, 0][[r[1] for r in rows]], RTOL, ATOL, "softmax_sum")
+    # every row: finite output and statistics
+    assert np.isfinite(out).all() and np.isfinite(smax).all() and (ssum > 0).all()
 
 
 GLOBAL_GATHER_CASES = [CASES[0], CASES[2], CASES[3], CASES[10]]
