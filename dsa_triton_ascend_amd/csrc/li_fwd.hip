@@ -59,6 +59,11 @@ struct LiParams {
 };
 
 constexpr int kLiThreads = 256;
+
+// max(x, 0) as one integer max on the bits: a negative float (-0.0
+// included) is a negative int32.  Equal to fmaxf(x, 0.f) for every non-NaN
+// x, which the compiler lowers with an extra canonicalising max of x.
+__device__ __forceinline__ float relu_bits(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
 constexpr int kLiChunk = 1024;  // default keys per workgroup (resized at launch)
 
 struct LiRow {
@@ -274,7 +279,7 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
 #pragma unroll
     for (int ht = 0; ht < GT; ++ht)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s += fmaxf(acc[ht][r], 0.f) * wv[ht][r];
+      for (int r = 0; r < 4; ++r) s += relu_bits(acc[ht][r]) * wv[ht][r];
     s = xgroup_sum(s);
     const int key = c0 + gi * 16 + li;
     if (lg == 0 && key < c1) s_sc[gi * 16 + li] = key < ri.lim ? s : -INFINITY;
@@ -293,15 +298,17 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
 
 // ---------------------------------------------------------------------------
 // Multi-row score kernel (BSND query, several query rows per batch, exact
-// head dims 64 / 128 / 256, 16-bit inputs).  One workgroup = 8 consecutive
-// query rows s0 .. s0+7 of one (batch, key head); wave w owns row s0 + w.
-// The rows share every key tile: tiles of 64 keys go HBM/L2 -> LDS by
-// LDS-DMA (global_load_lds_dwordx4, 1 KB per instruction) into a 3-buffer
-// ring, and each wave reads its K fragments (B operands) from LDS while its
-// row's G heads of Q stay in registers (A operands).  One query row per
-// workgroup (the chunked kernel above) re-reads every visible key per row,
-// which at the cfg2 prefill shape is 4.3 GB of L2 reads; here each key row
-// is read once per 8 query rows.  Key rows are stored in LDS with 16-byte
+// head dims 64 / 128 / 256, 16-bit inputs).  One workgroup = kLiRows (4)
+// consecutive query rows s0 .. s0+3 of one (batch, key head); wave w owns
+// row s0 + w.  The rows share every key tile: tiles of 64 keys go HBM/L2 ->
+// LDS by LDS-DMA (global_load_lds_dwordx4, 1 KB per instruction) into a
+// 3-buffer ring, and each wave reads its K fragments (B operands) from LDS
+// while its row's G heads of Q stay in registers (A operands).  One query
+// row per workgroup (the chunked kernel above) re-reads every visible key
+// per row, which at the cfg2 prefill shape is 4.3 GB of L2 reads; here each
+// key row is read once per 4 query rows.  Four rows (one wave per SIMD, 49
+// KB of LDS, three workgroups per CU) measured faster than eight (two waves
+// per SIMD, one workgroup per CU): cfg2 373 -> 351 us.  Key rows are stored in LDS with 16-byte
 // chunk c of tile row r at chunk c ^ (r & 15) (r & 7 at D = 64), so the 16
 // lanes of a fragment read (16 rows, one chunk column) hit distinct banks.
 // Workgroups run the longest causal rows first.  A wave's vector-memory
@@ -309,7 +316,7 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
 // (inline asm, so the count cannot change), which the ring's vmcnt waits
 // count on.
 // ---------------------------------------------------------------------------
-constexpr int kLiRows = 8;       // query rows per workgroup (one per wave)
+constexpr int kLiRows = 4;       // query rows per workgroup (one per wave, one wave per SIMD)
 constexpr int kLiRowTile = 64;   // keys per LDS tile
 
 __device__ __forceinline__ void li_dma16(unsigned lds_base, const void* gaddr) {
@@ -327,7 +334,7 @@ template <int N> __device__ __forceinline__ void li_wait_vm() {
 __device__ __attribute__((aligned(16))) unsigned char g_li_zero_row[512];
 
 template <int D, typename T, int GT>
-__global__ __launch_bounds__(kLiRows * 64, 1) void li_score_rows_kernel(LiParams p) {
+__global__ __launch_bounds__(kLiRows * 64) void li_score_rows_kernel(LiParams p) {
   using E = Elem<T>;
   using V8 = typename E::v8;
   constexpr int KS = D / 32;                       // k-steps
@@ -390,20 +397,36 @@ __global__ __launch_bounds__(kLiRows * 64, 1) void li_score_rows_kernel(LiParams
   // lane L: row + L / CPR, LDS chunk L % CPR <- source chunk (L % CPR) ^ swz
   const bool paged = p.layout_k == DSA_LAYOUT_PA_BSND;
   const int32_t* btab = paged ? p.block_table + (int64_t)ri.b * p.max_blocks : nullptr;
-  const int lastkey = kend > 0 ? kend - 1 : 0;
+  const int64_t nblk = paged ? p.k_rows / p.page_size : 0;
+  // the last key a DMA loads: the rows' last visible key, kept inside the
+  // key tensor (dense keys: row kbase + key <= k_rows - 1, as li_key_row
+  // clamps inconsistent cumulative lengths)
+  int lastkey = kend > 0 ? kend - 1 : 0;
+  const int64_t kbase = ri.k_base < p.k_rows ? ri.k_base : p.k_rows - 1;
+  if (!paged && kbase + lastkey > p.k_rows - 1) lastkey = (int)(p.k_rows - 1 - kbase);
+  // loop-invariant per DMA: tile row, source chunk, and (dense keys) the
+  // address of key 0's chunk; a key adds key * n2 * D elements
+  int tr_j[NDW], ch_j[NDW];
+  const T* base_j[NDW];
+#pragma unroll
+  for (int j = 0; j < NDW; ++j) {
+    tr_j[j] = (j * kLiRows + wave) * RPD + lane / CPR;
+    ch_j[j] = (lane % CPR) ^ (tr_j[j] & SWM);
+    base_j[j] = (const T*)p.k + (kbase * p.n2 + kh) * D + ch_j[j] * 8;
+  }
+  const int64_t key_stride = (int64_t)p.n2 * D;
   auto issue_tile = [&](int t, int buf) {
 #pragma unroll
     for (int j = 0; j < NDW; ++j) {
       const int d = j * kLiRows + wave;
-      const int tr = d * RPD + lane / CPR;
-      int key = t * kLiRowTile + tr;
+      int key = t * kLiRowTile + tr_j[j];
       key = key < lastkey ? key : lastkey;  // past the rows' keys: reload the last one
-      const int64_t krow = li_key_row(p, ri, btab, key);
-      const int ch = (lane % CPR) ^ (tr & SWM);
-      const T* src = (const T*)p.k + (krow * p.n2 + kh) * D + ch * 8;
+      const T* src = base_j[j] + key * key_stride;
       if (paged) {
         const int blk = btab[key / p.page_size];
-        if (blk < 0 || (int64_t)blk >= p.k_rows / p.page_size) src = (const T*)g_li_zero_row + ch * 8;
+        const bool zero = blk < 0 || (int64_t)blk >= nblk;
+        const int64_t krow = (int64_t)(zero ? 0 : blk) * p.page_size + key % p.page_size;
+        src = zero ? (const T*)g_li_zero_row + ch_j[j] * 8 : (const T*)p.k + (krow * p.n2 + kh) * D + ch_j[j] * 8;
       }
       li_dma16((unsigned)(uintptr_t)&s_k[buf][d * 1024], src);
     }
@@ -429,30 +452,40 @@ __global__ __launch_bounds__(kLiRows * 64, 1) void li_score_rows_kernel(LiParams
       const int c = ks * 4 + lg;
       return as_v8<V8>(*(const u32x4*)(tb + tr * (D * 2) + ((c ^ (tr & SWM)) * 16)));
     };
+    // software-pipelined over the tile's four key groups: the MFMAs of
+    // group kg + 1 go out before the ReLU / weight / head sum of group kg,
+    // so the wave does not wait on its own products
     float outv = -INFINITY;
-    V8 kf[KS];
+    constexpr int NKG = kLiRowTile / 16;
+    auto products = [&](int kg, f32x4 (&acc)[GT]) {
+      V8 kf[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kf[ks] = kread(0, ks);
-#pragma unroll
-    for (int kg = 0; kg < kLiRowTile / 16; ++kg) {
-      f32x4 acc[GT];
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = kread(kg, ks);
 #pragma unroll
       for (int ht = 0; ht < GT; ++ht) acc[ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const V8 bv = kf[ks];
-        if (kg + 1 < kLiRowTile / 16) kf[ks] = kread(kg + 1, ks);
+      for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-        for (int ht = 0; ht < GT; ++ht) acc[ht] = E::mfma(qf[ht][ks], bv, acc[ht]);
-      }
+        for (int ht = 0; ht < GT; ++ht) acc[ht] = E::mfma(qf[ht][ks], kf[ks], acc[ht]);
+    };
+    auto head_sum = [&](int kg, const f32x4 (&acc)[GT]) {
       float s = 0.f;
 #pragma unroll
       for (int ht = 0; ht < GT; ++ht)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s += fmaxf(acc[ht][r], 0.f) * wv[ht][r];
+        for (int r = 0; r < 4; ++r) s += relu_bits(acc[ht][r]) * wv[ht][r];
       s = xgroup_sum(s);
       const int key = t * kLiRowTile + kg * 16 + li;
       if (lg == kg) outv = key < lim ? s : -INFINITY;
+    };
+    f32x4 acc0[GT], acc1[GT];
+    products(0, acc0);
+#pragma unroll
+    for (int kg = 0; kg < NKG; kg += 2) {
+      products(kg + 1, acc1);
+      head_sum(kg, acc0);
+      if (kg + 2 < NKG) products(kg + 2, acc0);
+      head_sum(kg + 1, acc1);
     }
     // lane L holds key t*64 + L; lanes past the row's end store the last
     // entry's value to the last entry (one store instruction per tile)
@@ -546,7 +579,7 @@ __global__ __launch_bounds__(kLiThreads) void li_score_f32_kernel(LiParams p) {
             for (int t = 0; t < 4; ++t) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[c][t], kf[i][c][t], acc, 0, 0, 0);
           float s = 0.f;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) s += fmaxf(acc[r], 0.f) * wv[r];
+          for (int r = 0; r < 4; ++r) s += relu_bits(acc[r]) * wv[r];
           s = xgroup_sum(s);
           const int key = c0 + gi * 16 + li;
           // the same lane owns this key in every pass: no barrier needed
