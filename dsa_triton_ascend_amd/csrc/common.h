@@ -82,6 +82,11 @@ template <> struct Mfma16<f16> {
   }
 };
 
+// max(x, 0) as one integer max on the bits: a negative float (-0.0
+// included) is a negative int32.  Equal to fmaxf(x, 0.f) for every non-NaN
+// x; fmaxf of an MFMA result is lowered with an extra canonicalising max.
+__device__ __forceinline__ float relu_bits(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
+
 // Hardware exp2 (v_exp_f32); callers keep arguments <= 0 or -inf.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

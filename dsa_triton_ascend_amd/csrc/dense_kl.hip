@@ -196,7 +196,7 @@ __global__ __launch_bounds__(kDkThreads, 1) void dense_index_kernel(DkParams p) 
       for (int tt = 0; tt < 2; ++tt) {
         Split3 sp;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) split3_set(sp, r, wr[r] * fmaxf(acc[tt][r], 0.f));
+        for (int r = 0; r < 4; ++r) split3_set(sp, r, wr[r] * relu_bits(acc[tt][r]));
         const f32x4 sum = split3_rowsum(sp);
         if (li == 0) *(f32x4*)&s_redi[wave][tt * 16 + lg * 4] = sum;
       }
@@ -555,7 +555,7 @@ __global__ __launch_bounds__(kDkThreads, 1) void dense_index_grad_kernel(DkParam
       for (int j = 0; j < 8; ++j) {
         const int tt = j >> 2, r = j & 3;
         const int tk = tt * 16 + lg * 4 + r;
-        const float relu = fmaxf(acc[tt][r], 0.f);
+        const float relu = relu_bits(acc[tt][r]);
         const float di = gv ? s_di[tk] : 0.f;  // zero past the visible range
         dw_acc += di * relu;
         const float ds = relu > 0.f ? di * wg * ds_scale : 0.f;

@@ -401,7 +401,7 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
         for (int ks = 0; ks < DI / 32; ++ks) acc = E::mfma(qf_i[ks], as_v8<V8>(kfi[tt][ks]), acc);
         Split3 sp;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) split3_set(sp, r, wr[r] * fmaxf(acc[r], 0.f));
+        for (int r = 0; r < 4; ++r) split3_set(sp, r, wr[r] * relu_bits(acc[r]));
         const f32x4 sum = split3_rowsum(sp);
         if (li == 0) *(f32x4*)&s_redi[t & 1][hg4][tt * 16 + lg * 4] = sum;
       }
@@ -610,7 +610,7 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
         const int tt = j >> 2, r = j & 3;
         const int tk = tt * 16 + lg * 4 + r;
         const int k = t * TILE + tk;
-        const float relu = fmaxf(acc[tt][r], 0.f);
+        const float relu = relu_bits(acc[tt][r]);
         const float di = (k < n && gv) ? dis[j] : 0.f;
         dw_acc += di * relu;
         const float ds = relu > 0.f ? di * wg * ds_scale : 0.f;

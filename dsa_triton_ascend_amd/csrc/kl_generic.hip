@@ -165,7 +165,7 @@ __global__ __launch_bounds__(kGenThreads) void kl_gen_score_kernel(KlGenParams p
       for (int ks = 0; ks < KSI_MAX; ++ks)
         if (ks < ksi) acc = E::mfma(as_v8<V8>(*(const u32x4*)(s_ki + sl * RI + (ks * 32 + lg * 8) * 2)), qif[ks], acc);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) iacc[mt][r] += row16_sum(wg * fmaxf(acc[r], 0.f));
+      for (int r = 0; r < 4; ++r) iacc[mt][r] += row16_sum(wg * relu_bits(acc[r]));
     }
   }
   if (li == 0) {
@@ -337,7 +337,7 @@ __global__ __launch_bounds__(kGenThreads) void kl_gen_row_kernel(KlGenParams p) 
 #pragma unroll
             for (int e = 0; e < 8; ++e) s = fmaf(E::to_f32(a[e]), E::to_f32(b[e]), s);
           }
-          const float relu = fmaxf(s, 0.f);
+          const float relu = relu_bits(s);
           dw_acc[j] = fmaf(dI, relu, dw_acc[j]);
           s_ds[ks_ * DSR + g] = s > 0.f ? dI * s_w[g] : 0.f;
         }

@@ -60,10 +60,6 @@ struct LiParams {
 
 constexpr int kLiThreads = 256;
 
-// max(x, 0) as one integer max on the bits: a negative float (-0.0
-// included) is a negative int32.  Equal to fmaxf(x, 0.f) for every non-NaN
-// x, which the compiler lowers with an extra canonicalising max of x.
-__device__ __forceinline__ float relu_bits(float x) { return __int_as_float(max(__float_as_int(x), 0)); }
 constexpr int kLiChunk = 1024;  // default keys per workgroup (resized at launch)
 
 struct LiRow {
