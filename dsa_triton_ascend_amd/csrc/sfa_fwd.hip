@@ -982,6 +982,12 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
     rsrc_r = __builtin_amdgcn_make_buffer_rsrc((void*)p.kr, (short)0, (int)(p.kv_rows * DR * 2), 0x00020000);
   }
   constexpr int NDMA = NIW + 1;  // DMA slots per wave (the last one: rope, waves 0..3)
+  // The DMAs of tile t+2 go out during tile t: slots 0 .. G1D-1 between
+  // the GEMM1 MFMAs, the rest between the GEMM2 MFMAs.  Issued in GEMM2
+  // alone, the LDS-DMA issue stalls lengthened that phase (decode 41.0 ->
+  // 40.3 us with two slots in GEMM1; prefill unchanged).
+  constexpr int G1D = 2;
+  static_assert(G1D >= 0 && G1D < NDMA, "DMA slots issued during GEMM1");
   auto dma_phys = [&](int t, bool live, int j) -> int {
     int v;
     if (j < NIW) v = __builtin_amdgcn_readfirstlane(s_list[t * TILE + j * NW + wave_s]);
@@ -1097,7 +1103,7 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
   // k-step st / NTT of sub-tile st % NTT.  No scheduling barriers (the
   // compiler's interleaving of the fragment reads measured faster than the
   // fixed prefetch order at 64 heads).
-  auto gemm1 = [&](int b, f32x4 (&s_out)[NTT]) {
+  auto gemm1 = [&](int b, f32x4 (&s_out)[NTT], const int (&dph)[NDMA], int bn) {
     const int ln = fresh_lane();
     const int g1b = g1_base(ln), g1rb = g1r_base(ln), qlb = ql_base(ln);
     V8 ql[QL];
@@ -1116,6 +1122,10 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
       const V8 av = as_v8<V8>(fa[st % PF]);
       if (st + PF < NS) fa[st % PF] = a1s(st + PF);
       acc[st & 1] = E::mfma(av, ks < KQR ? qf[ks < KQR ? ks : 0] : ql[ks < KQR ? 0 : ks - KQR], acc[st & 1]);
+      if constexpr (G1D > 0) {
+        constexpr int kStep1 = NS / G1D;
+        if (st % kStep1 == kStep1 / 2 && st / kStep1 < G1D) dma_issue(st / kStep1, dph[st / kStep1], bn);
+      }
       if constexpr (NTT == 2) __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (NTT == 1) s_out[0] = acc[0] + acc[1];
@@ -1185,17 +1195,15 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
   };
 
   // ---- GEMM2: O^T [64 columns x HG heads] += V^T . P^T ----
-  // With DMA, this wave's DMAs of tile tn (into buffer bn) go out between
-  // the MFMAs: every wave stalls on its DMA issue for a while (the CU's
-  // gather path is shared), and here the other wave of the SIMD has MFMAs
-  // to run meanwhile.  TWO: the lo part of P sits in the second buffer and
-  // is multiplied in the same pass.
+  // With DMA, this wave's remaining DMAs of tile t+2 (slots G1D.., into
+  // buffer bn) go out between the MFMAs: every wave stalls on its DMA issue
+  // for a while (the CU's gather path is shared), and here the other wave
+  // of the SIMD has MFMAs to run meanwhile.  TWO: the lo part of P sits in
+  // the second buffer and is multiplied in the same pass.
   V8 va[NDW];
-  auto gemm2 = [&](int b, auto two, auto with_dma, int tn, int bn) {
+  auto gemm2 = [&](int b, auto two, auto with_dma, const int (&dph)[NDMA], int bn) {
     constexpr bool kTwo = decltype(two)::value;
     constexpr bool kDma = decltype(with_dma)::value;
-    int dph[NDMA];
-    if constexpr (kDma) dma_plan(tn, dph);
     const int ln = fresh_lane();
     const int pb = p_base(ln);
     if constexpr (kDma) {
@@ -1218,9 +1226,10 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
         acc_o[j][ht] = E::mfma(va[j], ch, acc_o[j][ht]);
         if constexpr (kTwo) acc_o[j][ht] = E::mfma(va[j], cl, acc_o[j][ht]);
         if constexpr (kDma) {
-          constexpr int kStep = HGT * NDW / NDMA;
+          constexpr int NR = NDMA - G1D;
+          constexpr int kStep = HGT * NDW / NR;
           const int st = ht * NDW + j;
-          if (st % kStep == 0 && st / kStep < NDMA) dma_issue(st / kStep, dph[st / kStep], bn);
+          if (st % kStep == 0 && st / kStep < NR) dma_issue(G1D + st / kStep, dph[G1D + st / kStep], bn);
         }
       }
     }
@@ -1244,18 +1253,20 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
         tile_sync(t);
         f32x4 sc[NTT];
         T4 lo[NTT];
-        gemm1(b, sc);
+        int dph[NDMA];
+        dma_plan(t + 2, dph);
+        gemm1(b, sc, dph, next_buf(b));
         softmax_p(t, sc, with_lo, lo);
         lds_barrier();
         if constexpr (kLo && NPB == 2) {
-          gemm2(b, On{}, On{}, t + 2, next_buf(b));
+          gemm2(b, On{}, On{}, dph, next_buf(b));
         } else {
-          gemm2(b, Off{}, On{}, t + 2, next_buf(b));
+          gemm2(b, Off{}, On{}, dph, next_buf(b));
           if constexpr (kLo) {
             lds_barrier();
             write_lo(lo);
             lds_barrier();
-            gemm2(b, Off{}, Off{}, 0, 0);
+            gemm2(b, Off{}, Off{}, dph, 0);
           }
         }
       }
