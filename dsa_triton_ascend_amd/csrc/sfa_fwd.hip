@@ -894,7 +894,18 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
   };
   // ---- compaction of the split's positions (as in sfa_fwd_kernel) ----
   const int n_chunks = p1 > p0 ? (CH ? (p1 - p0 + kSfaMaxList - 1) / kSfaMaxList : 1) : 0;
-  const int first_id = p0 + tid < p1 ? sfa_load_id(p, idx_row, p0 + tid) : -1;
+  // the index entries of the first chunk, all loaded up front (one memory
+  // round trip instead of one per compaction step)
+  constexpr int kIdPre = kSfaMaxList / NTHR;
+  int first_ids[kIdPre];
+  {
+    const int ce0 = min(p1, p0 + kSfaMaxList);
+#pragma unroll
+    for (int u = 0; u < kIdPre; ++u) {
+      const int pos = p0 + u * NTHR + tid;
+      first_ids[u] = pos < ce0 ? sfa_load_id(p, idx_row, pos) : -1;
+    }
+  }
   const int32_t* tab = nullptr;
   const bool paged = p.layout_kv == DSA_LAYOUT_PA_BSND;
   const int32_t* gtab = paged ? p.block_table + (int64_t)ri.b * p.max_blocks : nullptr;
@@ -928,7 +939,15 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
       int pos = c0 + tid;
       int phys = 0;
       bool valid = false;
-      const int id = (first && c0 == cb) ? first_id : (pos < ce ? sfa_load_id(p, irow, pos) : -1);
+      int id;
+      if (first) {
+        const int it = (c0 - cb) / NTHR;
+        id = first_ids[0];
+#pragma unroll
+        for (int u = 1; u < kIdPre; ++u) id = it == u ? first_ids[u] : id;
+      } else {
+        id = pos < ce ? sfa_load_id(p, irow, pos) : -1;
+      }
       if (rc.active && pos < ce) valid = sfa_resolve_id(p, rc, id, pos, &phys, tb);
       unsigned long long m = __ballot(valid);
       if (lane == 0) s_wcnt[wave] = __popcll(m);
