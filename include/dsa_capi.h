@@ -118,7 +118,11 @@ int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key,
                 float scale_value, int32_t return_lse, void* workspace,
                 size_t workspace_bytes, void* stream);
 
-/* Workspace bytes dsa_sfa_fwd needs for these sizes on the current device. */
+/* Workspace bytes dsa_sfa_fwd needs for these sizes on the current device:
+ * the split partials of rows split into token ranges, which happens when
+ * there are fewer rows than CUs and, at d = 512, when a row's positions
+ * (sparse_count * sparse_block_size) exceed one 2048-entry index list; 0
+ * when no row is split. */
 size_t dsa_sfa_fwd_workspace_size(int64_t q_rows, int64_t n1, int64_t d,
                                   int64_t sparse_count, int32_t sparse_block_size);
 
@@ -129,12 +133,14 @@ size_t dsa_sfa_fwd_workspace_size(int64_t q_rows, int64_t n1, int64_t d,
  * that forbid hipMalloc).  Arguments and results are dsa_sfa_fwd's; the
  * split partials go to a fixed 64 MiB device array inside the library (one
  * per GPU, held until the process ends), whose address is looked up on the
- * first call on each device.  Sizes whose split workspace
- * (dsa_sfa_fwd_workspace_size) exceeds 64 MiB are rejected with
- * DSA_ERR_UNSUPPORTED; on a 256-CU MI355X no supported shape needs more
- * than about 51 MB.  The array is shared by every call on a GPU: calls that
- * overlap on one device (concurrent streams or threads) race and must be
- * serialised by the caller.
+ * first call on each device (make one eager call on a device before
+ * capturing this entry point into a HIP graph).  Rows longer than one index
+ * list whose split partials would exceed 64 MiB run one split per row
+ * through the chunked kernel instead; sizes whose workspace still exceeds
+ * 64 MiB are rejected with DSA_ERR_UNSUPPORTED (on a 256-CU MI355X no
+ * supported shape needs more than about 51 MB).  The array is shared by
+ * every call on a GPU: calls that overlap on one device (concurrent streams
+ * or threads) race and must be serialised by the caller.
  */
 int dsa_sfa_fwd_noalloc(const void* query, const void* query_rope, const void* key,
                         const void* key_rope, const int32_t* sparse_indices,
