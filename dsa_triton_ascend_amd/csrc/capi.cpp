@@ -107,6 +107,13 @@ int li_scores_run(const void* query, const void* key, const void* weights, const
                   int64_t max_blocks = 0, int64_t page_size = 1);
 int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_t* indices,
                 void* values, int32_t val_dtype, hipStream_t stream);
+// scores and top-k: one fused launch where the shapes allow, else the two
+int li_fwd_run(const void* query, const void* key, const void* weights, const int32_t* act_q,
+               const int32_t* act_k, float* scores, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
+               int64_t n2, int64_t d, int64_t q_rows, int64_t k_rows, int32_t sparse_mode, int32_t layout_q,
+               int32_t layout_k, int32_t dtype, int32_t w_dtype, int64_t k, int32_t* indices, void* values,
+               hipStream_t stream, const int32_t* block_table = nullptr, int64_t max_blocks = 0,
+               int64_t page_size = 1);
 constexpr int64_t kLiMaxK = 16384;  // the top-k sorts up to 16384 entries (LDS and per-wave registers)
 // calib.hip
 int calib_stream_read_run(const void* buf, size_t bytes, int nontemporal, unsigned* sink, hipStream_t stream);
@@ -628,12 +635,9 @@ int dsa_li_fwd(const void* query, const void* key, const void* weights, const in
     return DSA_ERR_WORKSPACE;
   }
   float* scores = (float*)workspace;
-  st = li_scores_run(query, key, weights, actual_seq_q, actual_seq_k, scores, batch, s1, s2, n1, n2, d,
-                     q_rows, k_rows, sparse_mode, layout_query, layout_key, dtype, weights_dtype,
-                     (hipStream_t)stream);
-  if (st != DSA_OK) return st;
-  return li_topk_run(scores, q_rows * n2, s2, sparse_count, sparse_indices,
-                     return_value ? sparse_values : nullptr, dtype, (hipStream_t)stream);
+  return li_fwd_run(query, key, weights, actual_seq_q, actual_seq_k, scores, batch, s1, s2, n1, n2, d, q_rows,
+                    k_rows, sparse_mode, layout_query, layout_key, dtype, weights_dtype, sparse_count,
+                    sparse_indices, return_value ? sparse_values : nullptr, (hipStream_t)stream);
 }
 
 static int li_check_paged(const int32_t* block_table, int64_t num_blocks, int64_t page_size,
@@ -690,12 +694,10 @@ int dsa_li_fwd_paged(const void* query, const void* key_cache, const void* weigh
     return DSA_ERR_WORKSPACE;
   }
   float* scores = (float*)workspace;
-  st = li_scores_run(query, key_cache, weights, actual_seq_q, actual_seq_k, scores, batch, s1, s2, n1, n2, d,
-                     q_rows, k_rows, sparse_mode, layout_query, DSA_LAYOUT_PA_BSND, dtype, weights_dtype,
-                     (hipStream_t)stream, block_table, max_blocks, page_size);
-  if (st != DSA_OK) return st;
-  return li_topk_run(scores, q_rows * n2, s2, sparse_count, sparse_indices,
-                     return_value ? sparse_values : nullptr, dtype, (hipStream_t)stream);
+  return li_fwd_run(query, key_cache, weights, actual_seq_q, actual_seq_k, scores, batch, s1, s2, n1, n2, d,
+                    q_rows, k_rows, sparse_mode, layout_query, DSA_LAYOUT_PA_BSND, dtype, weights_dtype,
+                    sparse_count, sparse_indices, return_value ? sparse_values : nullptr, (hipStream_t)stream,
+                    block_table, max_blocks, page_size);
 }
 
 int dsa_calib_stream_read(const void* buffer, size_t bytes, int32_t nontemporal, uint32_t* sink, void* stream) {

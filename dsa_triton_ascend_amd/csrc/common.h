@@ -159,6 +159,7 @@ constexpr int kTestForceGlobalGather = 1;  // gather with 64-bit addresses even 
 constexpr int kTestSmallBwdChunks = 2;     // backward rows in chunks of a 64 KiB workspace budget
 constexpr int kTestKlGeneric = 4;          // the KL backward takes its generic path at every shape
 constexpr int kTestFwdWide = 8;            // D = 512 forwards run sfa_fwd_kernel (no column split)
+constexpr int kTestLiUnfused = 16;         // the indexer runs its scores and its top-k as two launches
 int test_flags();
 }  // namespace dsa
 

@@ -329,20 +329,24 @@ template <int N> __device__ __forceinline__ void li_wait_vm() {
 // paged cache, which de-paging leaves as zero rows (score 0 while visible).
 __device__ __attribute__((aligned(16))) unsigned char g_li_zero_row[512];
 
+constexpr int kLiRowBufs = 3;   // LDS ring of key tiles
+template <int D> constexpr int li_row_tile_bytes() { return kLiRowTile * D * 2; }
+
+// The score rows of one workgroup (body of the kernels below): s_k is the
+// kLiRowBufs-tile ring, s_lim kLiRows words.
 template <int D, typename T, int GT>
-__global__ __launch_bounds__(kLiRows * 64) void li_score_rows_kernel(LiParams p) {
+__device__ __forceinline__ void li_rows_scores(const LiParams& p, unsigned char (*s_k)[li_row_tile_bytes<D>()],
+                                               int* s_lim) {
   using E = Elem<T>;
   using V8 = typename E::v8;
   constexpr int KS = D / 32;                       // k-steps
   constexpr int CPR = D / 8;                       // 16-byte chunks per key row
   constexpr int RPD = 64 / CPR;                    // key rows per 1 KB DMA
-  constexpr int TB = kLiRowTile * D * 2;           // tile bytes
+  constexpr int TB = li_row_tile_bytes<D>();       // tile bytes
   constexpr int NDW = TB / 1024 / kLiRows;         // DMAs per wave per tile
   constexpr int SWM = CPR < 16 ? CPR - 1 : 15;     // chunk swizzle mask
-  constexpr int NBUF = 3;
+  constexpr int NBUF = kLiRowBufs;
   static_assert(NDW >= 1 && NDW * kLiRows * 1024 == TB, "tile DMAs");
-  __shared__ __attribute__((aligned(1024))) unsigned char s_k[NBUF][TB];
-  __shared__ int s_lim[kLiRows];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -494,6 +498,13 @@ __global__ __launch_bounds__(kLiRows * 64) void li_score_rows_kernel(LiParams p)
   // keys past the tiles are masked
   if (active)
     for (int key = ntiles * kLiRowTile + lane; key < p.s2; key += 64) srow[key] = -INFINITY;
+}
+
+template <int D, typename T, int GT>
+__global__ __launch_bounds__(kLiRows * 64) void li_score_rows_kernel(LiParams p) {
+  __shared__ __attribute__((aligned(1024))) unsigned char s_k[kLiRowBufs][li_row_tile_bytes<D>()];
+  __shared__ int s_lim[kLiRows];
+  li_rows_scores<D, T, GT>(p, s_k, s_lim);
 }
 
 // fp32 query / key (and weights): the products run on v_mfma_f32_16x16x4f32
@@ -1254,20 +1265,20 @@ __device__ __attribute__((noinline)) void topk_quad_fallback(TopkParams p, unsig
   }
 }
 
+// The fast selection of one row by 256 threads (tq = 0 .. 255), with the
+// row's buffers at qb (kQuadRowLds bytes of LDS).  Every thread of the
+// workgroup calls it in step: its barriers are workgroup-wide.  Returns true
+// (uniform) for a live row whose candidates overflow the buffer or crowd
+// into one bin; such a row's outputs are left to the general selection.
 template <int KPT>
-__global__ __launch_bounds__(kTopkThreads) void li_topk_quad_kernel(TopkParams p) {
-  extern __shared__ __attribute__((aligned(16))) unsigned char tk_smem[];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int q = tid / kQuadThr, tq = tid - q * kQuadThr, wq = tq >> 6;  // quarter, thread and wave in it
-  const int64_t row = (int64_t)blockIdx.x * kQuadRows + q;
-  const bool live = row < p.rows;
+__device__ __forceinline__ bool topk_row256(const TopkParams& p, const int64_t row, const bool live, const int tq,
+                                            unsigned char* qb) {
+  const int lane = tq & 63, wq = tq >> 6;
   const int S = p.s2, K = p.k;
-  unsigned char* qb = tk_smem + q * kQuadRowLds;
   unsigned* const hcount = (unsigned*)qb;                          // kQuadBins
   unsigned* const cursor = hcount + kQuadBins;                     // kQuadBins
   unsigned long long* const cand = (unsigned long long*)(cursor + kQuadBins);  // kQuadCap
   unsigned* const misc = (unsigned*)(cand + kQuadCap);             // 16 words
-  unsigned* const flags = (unsigned*)(tk_smem + kQuadRows * kQuadRowLds);  // kQuadRows
   const float* srow = p.scores + (live ? row : 0) * (int64_t)S;
 
   // keys in registers: entry u * 256 + tq (coalesced over the quarter).  The
@@ -1286,7 +1297,6 @@ __global__ __launch_bounds__(kTopkThreads) void li_topk_quad_kernel(TopkParams p
     for (int u = 0; u < KPT; ++u) kr[u] = (live && u * kQuadThr + tq < S) ? sort_key(kv[u]) : kNegInfKey;
   }
   for (int i = tq; i < kQuadBins; i += kQuadThr) hcount[i] = 0u;
-  if (tid < kQuadRows) flags[tid] = 0u;
 
   // ---- 1. count and range of the finite keys ----
   int nv = 0;
@@ -1445,10 +1455,88 @@ __global__ __launch_bounds__(kTopkThreads) void li_topk_quad_kernel(TopkParams p
     }
     for (int i = take + tq; i < K; i += kQuadThr) put(i, -1, -INFINITY);
   }
+  return fallback;
+}
+
+template <int KPT>
+__global__ __launch_bounds__(kTopkThreads) void li_topk_quad_kernel(TopkParams p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char tk_smem[];
+  const int tid = threadIdx.x;
+  const int q = tid / kQuadThr, tq = tid - q * kQuadThr;  // quarter, thread in it
+  const int64_t row = (int64_t)blockIdx.x * kQuadRows + q;
+  unsigned* const flags = (unsigned*)(tk_smem + kQuadRows * kQuadRowLds);  // kQuadRows
+  if (tid < kQuadRows) flags[tid] = 0u;  // ordered before the writes below by the row's barriers
+  const bool fallback = topk_row256<KPT>(p, row, row < p.rows, tq, tk_smem + q * kQuadRowLds);
   if (fallback && tq == 0) flags[q] = 1u;
   __syncthreads();
   const unsigned marked = flags[0] | (flags[1] << 1) | (flags[2] << 2) | (flags[3] << 3);
   if (marked) topk_quad_fallback(p, marked, tk_smem);  // uniform
+}
+
+// ---------------------------------------------------------------------------
+// Scores and top-k in one launch (BSND rows sharing key tiles, many rows):
+// after its score rows, the workgroup selects their top-k itself, one row at
+// a time with all 256 threads and the fast selection above, its buffers in
+// the idle key-tile ring.  The rows' scores were written by this workgroup
+// (through its CU's L2) just before, and the selection of one workgroup
+// overlaps the score products of the CU's other workgroups, where the two
+// launches ran the products and the selections one after the other with
+// the score rows going through memory in between.  A row that needs the
+// general selection gets kTopkMark as its first index, and
+// li_topk_marked_kernel finishes it.
+// ---------------------------------------------------------------------------
+constexpr int32_t kTopkMark = -2147483647 - 1;  // below every index (-1 pads)
+
+template <int D, typename T, int GT, int KPT>
+__global__ __launch_bounds__(kLiRows * 64) void li_score_rows_topk_kernel(LiParams p, TopkParams tp) {
+  constexpr int TB = li_row_tile_bytes<D>();
+  static_assert(kLiRowBufs * TB >= (int)kQuadRowLds, "one row's selection buffers fit the tile ring");
+  __shared__ __attribute__((aligned(1024))) unsigned char s_k[kLiRowBufs][TB];
+  __shared__ int s_lim[kLiRows];
+  li_rows_scores<D, T, GT>(p, s_k, s_lim);
+  // the workgroup's rows, as li_rows_scores maps them
+  const int nbk = p.batch * p.n2;
+  const int ngroups = (p.s1 + kLiRows - 1) / kLiRows;
+  const int bk = blockIdx.x % nbk;
+  const int grp = ngroups - 1 - (int)(blockIdx.x / nbk);
+  const int b = bk / p.n2, kh = bk - b * p.n2;
+  // every score store of the workgroup is complete and visible before any
+  // thread reads a row back (workgroup-scope release / acquire)
+  __syncthreads();
+  for (int r = 0; r < kLiRows; ++r) {
+    const int s1r = grp * kLiRows + r;
+    const bool live = s1r < p.s1;
+    const int64_t srn = (int64_t)(b * p.s1 + (live ? s1r : 0)) * p.n2 + kh;
+    if (r > 0) __syncthreads();  // the previous row's buffers are read
+    const bool fb = topk_row256<KPT>(tp, srn, live, (int)threadIdx.x, &s_k[0][0]);
+    if (fb && threadIdx.x == 0) tp.indices[srn * tp.k] = kTopkMark;
+  }
+}
+
+// Rows the fused launch left to the general selection: a workgroup checks
+// 64 rows' first indices and runs the general selection (whole workgroup,
+// the row in LDS) on each marked one.
+__global__ __launch_bounds__(kTopkThreads) void li_topk_marked_kernel(TopkParams p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char tk_smem[];
+  __shared__ unsigned s_mark[2];
+  const int64_t r0 = (int64_t)blockIdx.x * 64;
+  if (threadIdx.x < 64) {
+    const int64_t row = r0 + threadIdx.x;
+    const bool m = row < p.rows && p.indices[row * p.k] == kTopkMark;
+    const unsigned long long bal = __ballot(m);
+    if (threadIdx.x == 0) {
+      s_mark[0] = (unsigned)bal;
+      s_mark[1] = (unsigned)(bal >> 32);
+    }
+  }
+  __syncthreads();
+  unsigned long long marked = (unsigned long long)s_mark[0] | ((unsigned long long)s_mark[1] << 32);
+  while (marked) {  // uniform
+    const int i = __builtin_ctzll(marked);
+    marked &= marked - 1ull;
+    __syncthreads();
+    topk_row_generic<true>(p, r0 + i, tk_smem);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1470,9 +1558,8 @@ static bool li_topk_row_in_lds(int64_t s2, int64_t k) {
   return li_topk_fixed_bytes(k) + (size_t)s2 * 4 <= (size_t)kTopkLdsBudget;
 }
 
-int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_t* indices,
-                void* values, int32_t val_dtype, hipStream_t stream) {
-  if (rows <= 0) return DSA_OK;
+static TopkParams topk_params(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_t* indices,
+                              void* values, int32_t val_dtype) {
   TopkParams p;
   p.scores = scores;
   p.indices = indices;
@@ -1482,13 +1569,26 @@ int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_
   p.k = (int32_t)k;
   p.val_dtype = val_dtype;
   p.sel_cap = (int32_t)pow2_at_least(k);
+  return p;
+}
+
+// Many short rows go four to a workgroup (li_topk_quad_kernel); the general
+// path of a marked row then runs in the same LDS, so it must fit there with
+// the row kept in LDS.
+static bool li_topk_quad_fits(int64_t rows, int64_t s2, int64_t k) {
+  return rows > (int64_t)device_cu_count() && s2 <= 32 * kQuadThr && k <= kQuadMaxK &&
+         li_topk_fixed_bytes(k) + (size_t)s2 * 4 <= (size_t)kQuadRows * kQuadRowLds;
+}
+
+int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_t* indices,
+                void* values, int32_t val_dtype, hipStream_t stream) {
+  if (rows <= 0) return DSA_OK;
+  TopkParams p = topk_params(scores, rows, s2, k, indices, values, val_dtype);
   // dynamic LDS above 64 KB needs the per-function limit raised (to the
   // full budget; set on every call, which also covers every device and
   // concurrent callers: a host-side setting, cheap next to the launch)
-  // many short rows: four per workgroup (the general path of a marked row
-  // runs in the same LDS, so it must fit there with the row kept in LDS)
-  if (rows > (int64_t)device_cu_count() && s2 <= 32 * kQuadThr && k <= kQuadMaxK &&
-      li_topk_fixed_bytes(k) + (size_t)s2 * 4 <= (size_t)kQuadRows * kQuadRowLds) {
+  // many short rows: four per workgroup
+  if (li_topk_quad_fits(rows, s2, k)) {
     const void* fq = s2 <= 8 * kQuadThr    ? (const void*)li_topk_quad_kernel<8>
                      : s2 <= 16 * kQuadThr ? (const void*)li_topk_quad_kernel<16>
                                            : (const void*)li_topk_quad_kernel<32>;
@@ -1583,6 +1683,12 @@ static hipError_t launch_score_d(const LiParams& p, int64_t d, hipStream_t strea
   }
 }
 
+static LiParams li_params(const void* query, const void* key, const void* weights, const int32_t* act_q,
+                          const int32_t* act_k, float* scores, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
+                          int64_t n2, int64_t d, int64_t q_rows, int64_t k_rows, int32_t sparse_mode,
+                          int32_t layout_q, int32_t layout_k, int32_t w_dtype, const int32_t* block_table,
+                          int64_t max_blocks, int64_t page_size);
+
 int li_scores_run(const void* query, const void* key, const void* weights, const int32_t* act_q,
                   const int32_t* act_k, float* scores, int64_t batch, int64_t s1, int64_t s2,
                   int64_t n1, int64_t n2, int64_t d, int64_t q_rows, int64_t k_rows,
@@ -1590,6 +1696,20 @@ int li_scores_run(const void* query, const void* key, const void* weights, const
                   int32_t w_dtype, hipStream_t stream, const int32_t* block_table,
                   int64_t max_blocks, int64_t page_size) {
   if (q_rows <= 0 || s2 <= 0) return DSA_OK;
+  const LiParams p = li_params(query, key, weights, act_q, act_k, scores, batch, s1, s2, n1, n2, d, q_rows, k_rows,
+                               sparse_mode, layout_q, layout_k, w_dtype, block_table, max_blocks, page_size);
+  hipError_t e = dtype == DSA_DTYPE_BF16   ? launch_score_d<bf16>(p, d, stream)
+                 : dtype == DSA_DTYPE_FP16 ? launch_score_d<f16>(p, d, stream)
+                                           : launch_score_d<float>(p, d, stream);
+  DSA_HIP(e);
+  return DSA_OK;
+}
+
+static LiParams li_params(const void* query, const void* key, const void* weights, const int32_t* act_q,
+                          const int32_t* act_k, float* scores, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
+                          int64_t n2, int64_t d, int64_t q_rows, int64_t k_rows, int32_t sparse_mode,
+                          int32_t layout_q, int32_t layout_k, int32_t w_dtype, const int32_t* block_table,
+                          int64_t max_blocks, int64_t page_size) {
   LiParams p;
   p.q = query;
   p.k = key;
@@ -1614,10 +1734,57 @@ int li_scores_run(const void* query, const void* key, const void* weights, const
   p.page_size = (int32_t)(page_size > 0 ? page_size : 1);
   p.chunk = kLiChunk;
   p.d = (int32_t)d;
-  hipError_t e = dtype == DSA_DTYPE_BF16   ? launch_score_d<bf16>(p, d, stream)
-                 : dtype == DSA_DTYPE_FP16 ? launch_score_d<f16>(p, d, stream)
-                                           : launch_score_d<float>(p, d, stream);
+  return p;
+}
+
+// The fused launch: exact head dim 128, 16-bit inputs, G = 33 .. 64 heads per
+// key head (the DSA indexer's 64), BSND query rows sharing key tiles (as
+// launch_score picks li_score_rows_kernel), rows that the top-k would give
+// four to a workgroup and enough of them that the workgroups fill the CUs
+// several times over.
+template <typename T, int KPT>
+static hipError_t launch_fused(const LiParams& p, const TopkParams& tp, hipStream_t stream) {
+  LiParams q = p;
+  TopkParams t = tp;
+  const unsigned grid = (unsigned)((int64_t)p.batch * p.n2 * ((p.s1 + kLiRows - 1) / kLiRows));
+  void* args[] = {&q, &t};
+  return hipLaunchKernel((const void*)li_score_rows_topk_kernel<128, T, 4, KPT>, dim3(grid), dim3(kLiRows * 64),
+                         args, 0, stream);
+}
+
+int li_fwd_run(const void* query, const void* key, const void* weights, const int32_t* act_q,
+               const int32_t* act_k, float* scores, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
+               int64_t n2, int64_t d, int64_t q_rows, int64_t k_rows, int32_t sparse_mode, int32_t layout_q,
+               int32_t layout_k, int32_t dtype, int32_t w_dtype, int64_t k, int32_t* indices, void* values,
+               hipStream_t stream, const int32_t* block_table, int64_t max_blocks, int64_t page_size) {
+  const int64_t rows = q_rows * n2;
+  const int64_t g = n2 > 0 ? n1 / n2 : 0;
+  const bool fuse = q_rows > 0 && s2 > 0 && (dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_FP16) && d == 128 &&
+                    g > 32 && g <= 64 && layout_q == DSA_LAYOUT_BSND && s1 >= 4 && q_rows != batch &&
+                    rows >= 4 * (int64_t)device_cu_count() && s2 <= 16 * kQuadThr && li_topk_quad_fits(rows, s2, k) &&
+                    !(test_flags() & kTestLiUnfused);
+  if (!fuse) {
+    int st = li_scores_run(query, key, weights, act_q, act_k, scores, batch, s1, s2, n1, n2, d, q_rows, k_rows,
+                           sparse_mode, layout_q, layout_k, dtype, w_dtype, stream, block_table, max_blocks,
+                           page_size);
+    if (st != DSA_OK) return st;
+    return li_topk_run(scores, rows, s2, k, indices, values, dtype, stream);
+  }
+  const LiParams p = li_params(query, key, weights, act_q, act_k, scores, batch, s1, s2, n1, n2, d, q_rows, k_rows,
+                               sparse_mode, layout_q, layout_k, w_dtype, block_table, max_blocks, page_size);
+  const TopkParams tp = topk_params(scores, rows, s2, k, indices, values, dtype);
+  const bool bf = dtype == DSA_DTYPE_BF16;
+  // rows of up to 4096 scores (16 per thread: 158 VGPRs, three workgroups per
+  // CU as the score kernel alone; 32 per thread took 224 and two)
+  hipError_t e = s2 <= 8 * kQuadThr ? (bf ? launch_fused<bf16, 8>(p, tp, stream) : launch_fused<f16, 8>(p, tp, stream))
+                                    : (bf ? launch_fused<bf16, 16>(p, tp, stream) : launch_fused<f16, 16>(p, tp, stream));
   DSA_HIP(e);
+  // the rows marked for the general selection (the row kept in LDS)
+  const size_t lds = li_topk_fixed_bytes(k) + (size_t)s2 * 4;
+  DSA_HIP(hipFuncSetAttribute((const void*)li_topk_marked_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)lds));
+  hipLaunchKernelGGL(li_topk_marked_kernel, dim3((unsigned)((rows + 63) / 64)), dim3(kTopkThreads), lds, stream, tp);
+  DSA_HIP(hipGetLastError());
   return DSA_OK;
 }
 

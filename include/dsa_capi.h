@@ -74,6 +74,9 @@ int dsa_abi_version(void);
  * column-split P.V product (the D < 512 kernel) instead of the column-split
  * kernels; set it around both the workspace query and the call. */
 #define DSA_TEST_FWD_WIDE 8
+/* Bit 4: dsa_li_fwd / dsa_li_fwd_paged run the scores and the top-k as two
+ * launches even where one launch does both. */
+#define DSA_TEST_LI_UNFUSED 16
 void dsa_set_test_flags(int32_t flags);
 
 /*
