@@ -953,7 +953,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(lip_tf, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(lip_tf / PEAK_BF16_TFLOPS, 4),
                      "traffic": measured_traffic("lightning_indexer_prefill_traffic"),
-                     "kernel": "li_score_rows_kernel + li_topk_quad_kernel (one step)",
+                     "kernel": "li_score_rows_topk_kernel + li_topk_marked_kernel (one step)",
                      "algorithmic_flops_per_launch": int(lip_flops), "causal_pairs": int(lip_pairs),
                      "algorithmic_bytes_per_launch": int(lip_bytes)},
     }
