@@ -29,15 +29,19 @@
 //    tile's index scores (cheaper than storing Nidx1 x topK ReLUs), form
 //    dS and accumulate dW, while waves 4-7 take the previous tile: dQi
 //    (dQi^T = Ki^T . dS^T through the transposing LDS read) in registers,
-//    and the per-slot dKi contributions c[k] = dS[:,k]^T . Qi, written to a
-//    workspace as fp16 scaled by a per-row power of two.
-//  * dKi without floating-point atomics: the slots are bucketed by target
-//    token (count, scan, fill), and a token's contributions are summed in
-//    int64 fixed point, with the exponent fixed by the largest row maximum
-//    among the token's slots and their count (long tokens split over up to
-//    16 waves whose partial sums meet in integer atomics): integer addition
-//    is exact and associative, so the result does not depend on the bucket
-//    order or the split and the output is deterministic.
+//    and the per-slot dKi contributions c[k] = dS[:,k]^T . Qi, written to
+//    their token's bucket as fp16 scaled by a per-row power of two.
+//  * dKi without floating-point atomics: before the row kernel the slots are
+//    bucketed by target token (an integer count that records each slot's
+//    place, and a scan), the row kernel stores each contribution at its
+//    place, so a token's contributions are consecutive, and a token's
+//    contributions are summed in int64 fixed point, with the exponent fixed
+//    by the largest row maximum among the token's slots (raised by the row
+//    kernel with integer atomics on the float bits) and their count (long
+//    tokens split over up to 16 waves whose partial sums meet in integer
+//    atomics): integer addition is exact and associative, so the result
+//    does not depend on the bucket order or the split and the output is
+//    deterministic.
 //  * The loss is written per row and summed by one workgroup in a fixed
 //    order (the reference adds rows with an atomic).
 #include "kl_generic.h"
@@ -60,11 +64,18 @@ struct KlParams {
   const float* ssum;
   void* dqi;
   void* dw;
-  // [rows][topK][128] dKi contribution c of each slot, stored as fp16
-  // c * 2^e_row, with e_row set from an a-priori bound of |c| over the row
+  // dKi contribution c of each slot (128 values), stored as fp16 c * 2^e_row
+  // (e_row set from an a-priori bound of |c| over the row) at the slot's
+  // place in its token's bucket: row offs[token] + rank[slot]
   _Float16* cbuf;
   float* rowmax;     // [rows] max |c| over the row's slots
   int32_t* rowexp;   // [rows] e_row
+  const int32_t* offs;  // [tokens + 1] bucket starts
+  const int32_t* rank;  // [rows * topK] the slot's place in its token's bucket (within its row chunk)
+  const int32_t* cbase; // [chunks][tokens] the row chunk's start within each bucket, or null
+  int32_t chunk_rows, tokens;
+  int32_t* posrow;      // [rows * topK] row of the contribution at each bucket position
+  uint32_t* tokmax;     // [tokens] largest row maximum among the token's slots (float bits)
   float* loss_part;  // [rows]
   int32_t n1, nidx, topk, w_dtype;
   float scale_log2;  // scale * log2(e)
@@ -476,6 +487,19 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     for (int w2 = 0; w2 < kKlWaves; ++w2) s += s_misc[w2];
     p.loss_part[row] = s;
   }
+  // Each slot's place in its token's bucket (the buckets were counted and
+  // scanned before this kernel), into p's array, dead after the loop above:
+  // the contributions go straight to their token's range, which the
+  // reduction then reads contiguously.  A slot of a -1 page has none.
+  int* const s_pos = (int*)s_p;
+  for (int k = tid; k < n; k += NT) {
+    const int t = s_tok[k];
+    const int pos = t < 0 ? -1
+                    : p.offs[t] + p.rank[(int64_t)row * p.topk + k] +
+                          (p.cbase ? p.cbase[(int64_t)(row / p.chunk_rows) * p.tokens + t] : 0);
+    s_pos[k] = pos;
+    if (pos >= 0) p.posrow[pos] = row;
+  }
   // fp16 operands: dS is carried as 2^es * dS so that hi/lo parts stay in
   // the fp16 normal range; the products are scaled back by 2^-es.
   float ds_scale = 1.f, ds_unscale = 1.f;
@@ -672,6 +696,7 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
       for (int tt = 0; tt < 2; ++tt) {
         const int k = tp * TILE + tt * 16 + li;
         if (k < n) {
+          const int pos = s_pos[k];
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct) {
             _Float16 h[4];
@@ -681,8 +706,8 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
               cmax = __builtin_elementwise_maximum(cmax, fabsf(c));  // NaN-propagating
               h[r] = (_Float16)(c * c_scale);
             }
-            *(uint2*)(p.cbuf + ((int64_t)row * p.topk + k) * DI + (wave & 3) * 32 + ct * 16 + lg * 4) =
-                __builtin_bit_cast(uint2, h);
+            if (pos >= 0)
+              *(uint2*)(p.cbuf + (int64_t)pos * DI + (wave & 3) * 32 + ct * 16 + lg * 4) = __builtin_bit_cast(uint2, h);
           }
         }
       }
@@ -716,6 +741,15 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
     for (int w2 = 0; w2 < kKlWaves; ++w2) m = fmaxf(m, s_misc[w2]);
     p.rowmax[row] = m;
     p.rowexp[row] = c_exp;
+    s_misc[3 * kKlWaves] = m;
+  }
+  // the row maximum raises its tokens' maxima (non-negative floats order as
+  // their bit patterns), which fix the reduction's fixed-point exponents
+  lds_barrier();
+  const unsigned mbits = __float_as_uint(s_misc[3 * kKlWaves]);
+  for (int k = tid; k < n; k += NT) {
+    const int t = s_tok[k];
+    if (t >= 0) atomicMax(&p.tokmax[t], mbits);
   }
 }
 
@@ -725,12 +759,8 @@ __global__ __launch_bounds__(kKlWaves * 64, 1) void kl_bwd_row_kernel(KlParams p
 struct KlScatter {
   KlMap m;
   const int32_t* idx;
-  const float* rowmax;  // [rows]
   int32_t* cnt;         // [tokens]
-  int32_t* offs;        // [tokens + 1]
-  uint32_t* tokmax;     // [tokens] largest row maximum among the token's slots (float bits)
   int32_t* rank;        // [rows * topK] the slot's place among its token's slots
-  int32_t* list;        // [rows * topK]
 };
 
 __global__ __launch_bounds__(256) void kl_zero_kernel(int32_t* a, int64_t n) {
@@ -738,7 +768,8 @@ __global__ __launch_bounds__(256) void kl_zero_kernel(int32_t* a, int64_t n) {
   if (i < n) a[i] = 0;
 }
 
-template <bool FILL>
+// the count's old value is the slot's place in the token's bucket (run
+// before the row kernel, which stores each contribution at that place)
 __global__ __launch_bounds__(256) void kl_bucket_kernel(KlScatter s) {
   const int row = blockIdx.x;
   const int k = blockIdx.y * 256 + threadIdx.x;
@@ -746,14 +777,80 @@ __global__ __launch_bounds__(256) void kl_bucket_kernel(KlScatter s) {
   if (k >= r.n) return;
   const int t = kl_token(s.m, r, s.idx, row, k);
   if (t < 0) return;  // a -1 page: no gradient target
-  const int64_t slot = (int64_t)row * s.m.topk + k;
-  if (!FILL) {
-    // the count's old value is the slot's place in the token's bucket
-    s.rank[slot] = atomicAdd(&s.cnt[t], 1);
-    // non-negative floats order as their bit patterns
-    atomicMax(&s.tokmax[t], __float_as_uint(s.rowmax[row]));
-  } else {
-    s.list[s.offs[t] + s.rank[slot]] = (int32_t)slot;
+  s.rank[(int64_t)row * s.m.topk + k] = atomicAdd(&s.cnt[t], 1);
+}
+
+// Ranks without global atomics on hot counters (a causal row set sends
+// thousands of rows' slots to each early token, and the returning global
+// atomics of kl_bucket_kernel serialise on those counters): a workgroup
+// owns a chunk of consecutive rows, counts their slots per token in LDS
+// (the slot's rank within the chunk is the LDS counter's old value) and
+// writes the chunk's counts; kl_rank_scan_kernel turns them into each
+// chunk's start within each bucket and the buckets' totals.  For key sets
+// up to kKlRankMaxTok tokens (the LDS counters).
+constexpr int kKlRankMaxTok = 16384;
+constexpr int kKlRankMaxChunks = 512;
+constexpr int kKlRankThreads = 512;
+
+__global__ __launch_bounds__(kKlRankThreads) void kl_rank_local_kernel(KlScatter s, int32_t* ccnt, int chunk_rows,
+                                                                       int tokens) {
+  extern __shared__ int s_cnt[];  // [tokens]
+  constexpr int U = 8;            // slots per thread in flight
+  const int tid = threadIdx.x;
+  const int r0 = blockIdx.x * chunk_rows, r1 = min(s.m.rows, r0 + chunk_rows);
+  for (int i = tid; i < tokens; i += kKlRankThreads) s_cnt[i] = 0;
+  __syncthreads();
+  const int64_t total = (int64_t)(r1 - r0) * s.m.topk;
+  for (int64_t e0 = 0; e0 < total; e0 += (int64_t)kKlRankThreads * U) {
+    int tk[U];
+    int64_t slot[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t e = e0 + (int64_t)u * kKlRankThreads + tid;
+      const int rr = (int)(e / s.m.topk), k = (int)(e - (int64_t)rr * s.m.topk);
+      const int row = r0 + rr;
+      tk[u] = -1;
+      slot[u] = (int64_t)row * s.m.topk + k;
+      if (e < total) {
+        const KlRow r = kl_row_info(s.m, row);
+        if (k < r.n) tk[u] = kl_token(s.m, r, s.idx, row, k);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (tk[u] >= 0) s.rank[slot[u]] = atomicAdd(&s_cnt[tk[u]], 1);
+  }
+  __syncthreads();
+  for (int i = tid; i < tokens; i += kKlRankThreads) ccnt[(int64_t)blockIdx.x * tokens + i] = s_cnt[i];
+}
+
+// ccnt[c][t] -> the start of chunk c within token t's bucket (exclusive
+// prefix over the chunks), cnt[t] = the bucket's size.  A workgroup takes 64
+// tokens; each of its 16 waves a contiguous run of chunks.
+__global__ __launch_bounds__(1024) void kl_rank_scan_kernel(int32_t* ccnt, int32_t* cnt, int nchunks, int tokens) {
+  __shared__ int32_t s_part[16][64];
+  const int lane = threadIdx.x & 63, part = threadIdx.x >> 6;
+  const int t = blockIdx.x * 64 + lane;
+  const int per = (nchunks + 15) / 16;
+  const int c0 = min(nchunks, part * per), c1 = min(nchunks, c0 + per);
+  int32_t sum = 0;
+  if (t < tokens)
+    for (int c = c0; c < c1; ++c) sum += ccnt[(int64_t)c * tokens + t];
+  s_part[part][lane] = sum;
+  __syncthreads();
+  int32_t run = 0, tot = 0;
+  for (int q = 0; q < 16; ++q) {
+    run += q < part ? s_part[q][lane] : 0;
+    tot += s_part[q][lane];
+  }
+  if (t < tokens) {
+    for (int c = c0; c < c1; ++c) {
+      int32_t* a = ccnt + (int64_t)c * tokens + t;
+      const int32_t v = *a;
+      *a = run;
+      run += v;
+    }
+    if (part == 0) cnt[t] = tot;
   }
 }
 
@@ -809,8 +906,8 @@ __device__ __forceinline__ int kl_fixed_exp(float bm, int len) {
 template <typename T>
 __global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, const int32_t* rowexp,
                                                         const uint32_t* tokmax, const int32_t* offs,
-                                                        const int32_t* list, long long* acc, T* dki, int ntok,
-                                                        int topk, int parts, int di) {
+                                                        const int32_t* posrow, long long* acc, T* dki, int ntok,
+                                                        int parts, int di) {
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int t = w / parts, part = w - t * parts;
   const int lane = threadIdx.x & 63;
@@ -839,21 +936,21 @@ __global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, co
       // A contribution is c16 * 2^-e_row; its fixed-point value is
       // round(c16 * 2^(e - e_row)), exact through double (an integer
       // shift-and-round per element measured slower, with branches and
-      // branch-free).  64 list entries and their row exponents come in with
-      // one load per lane and are broadcast with readlane; 16 contribution
-      // rows are in flight at a time.
+      // branch-free).  The token's contributions are consecutive rows; the
+      // rows' exponents of 64 positions come in with one load per lane and
+      // are broadcast with readlane; 16 contribution rows are in flight at a
+      // time.
       typedef _Float16 h2 __attribute__((ext_vector_type(2)));
       constexpr int U = 16;
       for (int base = part * L; base < i1; base += 64) {
         const int cnt = min(64, i1 - base);
-        const int slv = lane < cnt ? list[o0 + base + lane] : 0;
-        const int kv = lane < cnt ? e - rowexp[slv / topk] : 0;
+        const int kv = lane < cnt ? e - rowexp[posrow[o0 + base + lane]] : 0;
         for (int u0 = 0; u0 < cnt; u0 += U) {
           h2 v[U];
   #pragma unroll
           for (int u = 0; u < U; ++u) {
-            const int sl = __builtin_amdgcn_readlane(slv, u0 + u);
-            v[u] = (u0 + u < cnt && cv) ? *(const h2*)(cbuf + (int64_t)sl * di + col) : (h2){0, 0};
+            const int64_t pos = (int64_t)o0 + base + u0 + u;
+            v[u] = (u0 + u < cnt && cv) ? *(const h2*)(cbuf + pos * di + col) : (h2){0, 0};
           }
   #pragma unroll
           for (int u = 0; u < U; ++u) {
@@ -919,7 +1016,8 @@ __global__ __launch_bounds__(256) void kl_loss_kernel(const float* part, int row
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct KlWs {
-  size_t cbuf, rowmax, rowexp, loss, cnt, tokmax, acc, offs, rank, list, pi, total;
+  size_t cbuf, rowmax, rowexp, loss, cnt, tokmax, acc, offs, rank, posrow, pi, ccnt, total;
+  int32_t chunk_rows, nchunks;  // row chunks of the LDS ranking (0: global atomics)
 };
 
 // pi (the generic path's per-slot p / I) is laid out for every call: the
@@ -945,10 +1043,20 @@ static KlWs kl_ws_layout(int64_t rows, int64_t tokens, int64_t topk, int64_t di)
   o += align256((size_t)(tokens + 1) * sizeof(int32_t));
   w.rank = o;
   o += align256((size_t)rows * topk * sizeof(int32_t));
-  w.list = o;
+  w.posrow = o;
   o += align256((size_t)rows * topk * sizeof(int32_t));
   w.pi = o;
   o += align256((size_t)rows * topk * 2 * sizeof(float));
+  // the LDS ranking's per-chunk counts: at most kKlRankMaxChunks chunks of
+  // at least 16 rows
+  w.chunk_rows = 0;
+  w.nchunks = 0;
+  if (tokens <= kKlRankMaxTok && rows > 0) {
+    w.chunk_rows = (int32_t)std::max<int64_t>(16, (rows + kKlRankMaxChunks - 1) / kKlRankMaxChunks);
+    w.nchunks = (int32_t)((rows + w.chunk_rows - 1) / w.chunk_rows);
+  }
+  w.ccnt = o;
+  o += align256((size_t)w.nchunks * tokens * sizeof(int32_t));
   w.total = o;
   return w;
 }
@@ -1060,12 +1168,19 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   s.m = m;
   s.idx = sparse_indices;
   s.cnt = (int32_t*)(ws + L.cnt);
-  s.offs = (int32_t*)(ws + L.offs);
-  s.tokmax = (uint32_t*)(ws + L.tokmax);
   s.rank = (int32_t*)(ws + L.rank);
-  s.rowmax = p.rowmax;
-  s.list = (int32_t*)(ws + L.list);
+  int32_t* const offs = (int32_t*)(ws + L.offs);
+  uint32_t* const tokmax = (uint32_t*)(ws + L.tokmax);
+  int32_t* const posrow = (int32_t*)(ws + L.posrow);
   long long* acc = (long long*)(ws + L.acc);
+  int32_t* const ccnt = L.nchunks > 0 ? (int32_t*)(ws + L.ccnt) : nullptr;
+  p.offs = offs;
+  p.rank = s.rank;
+  p.cbase = ccnt;
+  p.chunk_rows = L.chunk_rows > 0 ? L.chunk_rows : 1;
+  p.tokens = (int32_t)tokens;
+  p.posrow = posrow;
+  p.tokmax = tokmax;
 
   // parts per token of the dKi reduction: about avg_slots / 64,
   // 1..kKlReduceParts (long causal rows give every early token thousands of
@@ -1074,11 +1189,29 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
   const int parts = (int)std::max<int64_t>(1, std::min<int64_t>(kKlReduceParts, (avg + 63) / 64));
   // counters, token maxima and (when tokens are split) the accumulators,
   // cnt .. acc or cnt .. offs, cleared by a kernel (no memset nodes when the
-  // caller captures).  The count pass records each slot's rank in its
-  // bucket and the token maxima; the fill pass then places the slots
-  // without atomics.
+  // caller captures).  The count pass records each slot's place in its
+  // token's bucket and the scan the buckets' starts, before the row kernel:
+  // it stores each contribution at its place and raises its tokens' maxima.
   const int64_t zn = (int64_t)(((parts > 1 ? L.offs : L.acc) - L.cnt) / sizeof(int32_t));
   hipLaunchKernelGGL(kl_zero_kernel, dim3((unsigned)((zn + 255) / 256)), dim3(256), 0, stream, s.cnt, zn);
+  DSA_HIP(hipGetLastError());
+  if (ccnt) {
+    const size_t lds = (size_t)tokens * sizeof(int32_t);
+    if (lds > 64 * 1024)
+      DSA_HIP(hipFuncSetAttribute((const void*)kl_rank_local_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)lds));
+    hipLaunchKernelGGL(kl_rank_local_kernel, dim3((unsigned)L.nchunks), dim3(kKlRankThreads), lds, stream, s, ccnt,
+                       (int)L.chunk_rows, (int)tokens);
+    DSA_HIP(hipGetLastError());
+    hipLaunchKernelGGL(kl_rank_scan_kernel, dim3((unsigned)((tokens + 63) / 64)), dim3(1024), 0, stream, ccnt, s.cnt,
+                       (int)L.nchunks, (int)tokens);
+    DSA_HIP(hipGetLastError());
+  } else {
+    const dim3 bgrid((unsigned)rows, (unsigned)((topk + 255) / 256));
+    hipLaunchKernelGGL(kl_bucket_kernel, bgrid, dim3(256), 0, stream, s);
+    DSA_HIP(hipGetLastError());
+  }
+  hipLaunchKernelGGL(kl_scan_kernel, dim3(1), dim3(1024), 0, stream, s.cnt, offs, (int)tokens);
   DSA_HIP(hipGetLastError());
   const bool bf = dtype == DSA_DTYPE_BF16;
   // the fused row kernel where it applies (d_idx = 128, Nidx1 <= 64, topK
@@ -1106,6 +1239,13 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
     g.cbuf = p.cbuf;
     g.rowmax = p.rowmax;
     g.rowexp = p.rowexp;
+    g.offs = offs;
+    g.rank = s.rank;
+    g.cbase = ccnt;
+    g.chunk_rows = p.chunk_rows;
+    g.tokens = (int32_t)tokens;
+    g.posrow = posrow;
+    g.tokmax = tokmax;
     g.loss_part = p.loss_part;
     g.pi = (float*)(ws + L.pi);
     g.n1 = (int32_t)n1;
@@ -1118,26 +1258,19 @@ int kl_bwd_run(const void* query, const void* key, const void* query_rope, const
     e = kl_gen_run(g, (int)rows, (int)d, (int)d_rope, bf, stream);
   }
   DSA_HIP(e);
-  const dim3 bgrid((unsigned)rows, (unsigned)((topk + 255) / 256));
-  hipLaunchKernelGGL(kl_bucket_kernel<false>, bgrid, dim3(256), 0, stream, s);
-  DSA_HIP(hipGetLastError());
-  hipLaunchKernelGGL(kl_scan_kernel, dim3(1), dim3(1024), 0, stream, s.cnt, s.offs, (int)tokens);
-  DSA_HIP(hipGetLastError());
-  hipLaunchKernelGGL(kl_bucket_kernel<true>, bgrid, dim3(256), 0, stream, s);
-  DSA_HIP(hipGetLastError());
   const dim3 rgrid((unsigned)((tokens * parts + 3) / 4));
   const dim3 fgrid((unsigned)((tokens + 3) / 4));
   if (bf) {
-    hipLaunchKernelGGL(kl_reduce_kernel<bf16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowexp, s.tokmax, s.offs,
-                       s.list, acc, (bf16*)d_key_index, (int)tokens, (int)topk, parts, (int)d_idx);
+    hipLaunchKernelGGL(kl_reduce_kernel<bf16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowexp, tokmax, offs,
+                       posrow, acc, (bf16*)d_key_index, (int)tokens, parts, (int)d_idx);
     DSA_HIP(hipGetLastError());
-    hipLaunchKernelGGL(kl_reduce_finish_kernel<bf16>, fgrid, dim3(256), 0, stream, s.tokmax, s.offs, acc,
+    hipLaunchKernelGGL(kl_reduce_finish_kernel<bf16>, fgrid, dim3(256), 0, stream, tokmax, offs, acc,
                        (bf16*)d_key_index, (int)tokens, parts, (int)d_idx);
   } else {
-    hipLaunchKernelGGL(kl_reduce_kernel<f16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowexp, s.tokmax, s.offs,
-                       s.list, acc, (f16*)d_key_index, (int)tokens, (int)topk, parts, (int)d_idx);
+    hipLaunchKernelGGL(kl_reduce_kernel<f16>, rgrid, dim3(256), 0, stream, p.cbuf, p.rowexp, tokmax, offs,
+                       posrow, acc, (f16*)d_key_index, (int)tokens, parts, (int)d_idx);
     DSA_HIP(hipGetLastError());
-    hipLaunchKernelGGL(kl_reduce_finish_kernel<f16>, fgrid, dim3(256), 0, stream, s.tokmax, s.offs, acc,
+    hipLaunchKernelGGL(kl_reduce_finish_kernel<f16>, fgrid, dim3(256), 0, stream, tokmax, offs, acc,
                        (f16*)d_key_index, (int)tokens, parts, (int)d_idx);
   }
   DSA_HIP(hipGetLastError());

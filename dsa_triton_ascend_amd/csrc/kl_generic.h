@@ -101,9 +101,15 @@ struct KlGenParams {
   const float* ssum;
   void* dqi;
   void* dw;
-  _Float16* cbuf;    // [rows][topK][di] dKi contribution c as fp16 c * 2^rowexp
+  _Float16* cbuf;    // dKi contribution c (di values) as fp16 c * 2^rowexp, at the slot's bucket place
   float* rowmax;     // [rows] max |c|
   int32_t* rowexp;   // [rows]
+  const int32_t* offs;  // [tokens + 1] bucket starts
+  const int32_t* rank;  // [rows * topK] the slot's place in its token's bucket (within its row chunk)
+  const int32_t* cbase; // [chunks][tokens] the row chunk's start within each bucket, or null
+  int32_t chunk_rows, tokens;
+  int32_t* posrow;      // [rows * topK] row of the contribution at each bucket position
+  uint32_t* tokmax;     // [tokens] largest row maximum among the token's slots (float bits)
   float* loss_part;  // [rows]
   float* pi;         // [rows][topK][2]: teacher p (then dI) and index score I
   int32_t n1, nidx, di, dip, topk, w_dtype;

@@ -6,8 +6,9 @@
 // 119-136, 219-262); the semantics are the fused kernel's (the formulas are
 // listed at the top of kl_bwd.hip).  The two kernels here write what the
 // fused kernel writes (dQi, dW, the per-row KL term, the per-slot dKi
-// contributions c as fp16 scaled by 2^rowexp, and the row maxima of |c|),
-// so the bucket, fixed-point reduce and loss kernels of kl_bwd.hip finish
+// contributions c as fp16 scaled by 2^rowexp at the slot's place in its
+// token's bucket, the row maxima of |c| and, through them, the token
+// maxima), so the fixed-point reduce and loss kernels of kl_bwd.hip finish
 // the job unchanged.
 //  * kl_gen_score_kernel: one workgroup per (row, 64 slots).  The slots'
 //    K, K_rope and K_index rows are gathered into LDS; the teacher score
@@ -216,6 +217,7 @@ __global__ __launch_bounds__(kGenThreads) void kl_gen_row_kernel(KlGenParams p) 
   __shared__ float s_red[4];
   __shared__ float s_dI[TL];
   __shared__ int s_tok[TL];
+  __shared__ int s_pos[TL];  // the slots' places in their tokens' buckets
   __shared__ float s_w[kGenMaxNidx];
   const int tid = threadIdx.x;
   const int row = blockIdx.x;
@@ -310,7 +312,13 @@ __global__ __launch_bounds__(kGenThreads) void kl_gen_row_kernel(KlGenParams p) 
     __syncthreads();  // the previous tile's Ki / dS are consumed
     if (tid < TL) {
       const int k = t0 + tid;
-      s_tok[tid] = k < n ? kl_token(p.m, ri, p.idx, row, k) : -1;
+      const int tok = k < n ? kl_token(p.m, ri, p.idx, row, k) : -1;
+      const int pos = tok < 0 ? -1
+                      : p.offs[tok] + p.rank[(int64_t)row * p.topk + k] +
+                            (p.cbase ? p.cbase[(int64_t)(row / p.chunk_rows) * p.tokens + tok] : 0);
+      s_tok[tid] = tok;
+      s_pos[tid] = pos;
+      if (pos >= 0) p.posrow[pos] = row;
       s_dI[tid] = k < n ? pi[k].x : 0.f;
     }
     __syncthreads();
@@ -365,7 +373,8 @@ __global__ __launch_bounds__(kGenThreads) void kl_gen_row_kernel(KlGenParams p) 
               cmax = __builtin_elementwise_maximum(cmax, fabsf(a[e]));  // NaN-propagating
               h[e] = (_Float16)(a[e] * c_scale);
             }
-            *(H8*)(p.cbuf + ((int64_t)row * p.topk + k) * di + c * 8) = h;
+            const int pos = s_pos[ks_];
+            if (pos >= 0) *(H8*)(p.cbuf + (int64_t)pos * di + c * 8) = h;
           }
         }
       }
@@ -418,6 +427,12 @@ __global__ __launch_bounds__(kGenThreads) void kl_gen_row_kernel(KlGenParams p) 
     p.loss_part[row] = kl;
     p.rowmax[row] = cmax;
     p.rowexp[row] = c_exp;
+  }
+  // the row maximum raises its tokens' maxima (non-negative floats order as
+  // their bit patterns)
+  for (int k = tid; k < n; k += kGenThreads) {
+    const int tok = kl_token(p.m, ri, p.idx, row, k);
+    if (tok >= 0) atomicMax(&p.tokmax[tok], __float_as_uint(cmax));
   }
 }
 
