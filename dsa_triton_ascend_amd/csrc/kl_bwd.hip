@@ -35,13 +35,14 @@
 //    bucketed by target token (an integer count that records each slot's
 //    place, and a scan), the row kernel stores each contribution at its
 //    place, so a token's contributions are consecutive, and a token's
-//    contributions are summed in int64 fixed point, with the exponent fixed
-//    by the largest row maximum among the token's slots (raised by the row
-//    kernel with integer atomics on the float bits) and their count (long
-//    tokens split over up to 16 waves whose partial sums meet in integer
-//    atomics): integer addition is exact and associative, so the result
-//    does not depend on the bucket order or the split and the output is
-//    deterministic.
+//    contributions are summed in fixed point (each rounded to a grid 2^-e
+//    and added as integer-valued doubles below 2^52), with the exponent
+//    fixed by the largest row maximum among the token's slots (raised by
+//    the row kernel with integer atomics on the float bits) and their count
+//    (long tokens split over up to 16 waves whose partial sums meet in
+//    int64 atomics): these additions are exact and associative, so the
+//    result does not depend on the bucket order or the split and the output
+//    is deterministic.
 //  * The loss is written per row and summed by one workgroup in a fixed
 //    order (the reference adds rows with an atomic).
 #include "kl_generic.h"
@@ -878,9 +879,9 @@ __global__ __launch_bounds__(1024) void kl_scan_kernel(const int32_t* cnt, int32
   if (tid == 1023) offs[n] = s_sum[1023];
 }
 
-// dKi[t] = sum of the token's slot contributions, in int64 fixed point with
-// the exponent fixed by the token's largest row maximum and slot count (no
-// partial sum can overflow).  A token's slots are split into up to
+// dKi[t] = sum of the token's slot contributions, in fixed point with the
+// exponent fixed by the token's largest row maximum and slot count (every
+// partial sum is an integer below 2^52, exact as a double and as an int64).  A token's slots are split into up to
 // `parts` (at most kKlReduceParts) parts of at least kKlReduceChunk slots,
 // one wave each; the host sets `parts` from the average slots per token, so
 // that sparsely hit tokens keep a grid of one wave per token: a
@@ -894,11 +895,12 @@ constexpr int kKlReduceChunk = 256;
 __device__ __forceinline__ int kl_reduce_parts(int len, int parts) {
   return max(1, min(parts, (len + kKlReduceChunk - 1) / kKlReduceChunk));
 }
-// fixed-point exponent: len * bm < 2^(62 - e)
+// fixed-point exponent: len * bm < 2^(52 - e), so every partial sum of
+// terms rounded to the grid 2^-e is an integer below 2^52, exact in a double
 __device__ __forceinline__ int kl_fixed_exp(float bm, int len) {
   int ex;
   frexp((double)bm * (double)len, &ex);
-  return 62 - ex;
+  return 52 - ex;
 }
 
 // di: contribution columns (the index head dim), a multiple of 8; a wave
@@ -927,19 +929,21 @@ __global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, co
       }
       continue;
     }
-    long long a0 = 0, a1 = 0;
+    double a0 = 0.0, a1 = 0.0;
     int e = 0;
     if (bm > 0.f) {
       e = kl_fixed_exp(bm, len);
       const int L = (len + np - 1) / np;
       const int i1 = min(len, (part + 1) * L);
       // A contribution is c16 * 2^-e_row; its fixed-point value is
-      // round(c16 * 2^(e - e_row)), exact through double (an integer
-      // shift-and-round per element measured slower, with branches and
-      // branch-free).  The token's contributions are consecutive rows; the
-      // rows' exponents of 64 positions come in with one load per lane and
-      // are broadcast with readlane; 16 contribution rows are in flight at a
-      // time.
+      // rint(c16 * 2^(e - e_row)), an integer-valued double, and the sums
+      // of such values stay below 2^52 (the exponent's bound), so the
+      // double additions are exact and their order does not matter (an
+      // integer shift-and-round per element, with branches or branch-free,
+      // and a conversion to int64 per element measured slower).  The
+      // token's contributions are consecutive rows; the rows' exponents of
+      // 64 positions come in with one load per lane and are broadcast with
+      // readlane; 16 contribution rows are in flight at a time.
       typedef _Float16 h2 __attribute__((ext_vector_type(2)));
       constexpr int U = 16;
       for (int base = part * L; base < i1; base += 64) {
@@ -955,8 +959,8 @@ __global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, co
   #pragma unroll
           for (int u = 0; u < U; ++u) {
             const double sc = ldexp(1.0, __builtin_amdgcn_readlane(kv, u0 + u));
-            a0 += __double2ll_rn((double)v[u].x * sc);
-            a1 += __double2ll_rn((double)v[u].y * sc);
+            a0 += __builtin_rint((double)v[u].x * sc);
+            a1 += __builtin_rint((double)v[u].y * sc);
           }
         }
       }
@@ -964,12 +968,13 @@ __global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, co
     if (!cv) continue;
     if (np == 1) {
       const double us = ldexp(1.0, -e);
-      dst[0] = Elem<T>::from_f32((float)((double)a0 * us));
-      dst[1] = Elem<T>::from_f32((float)((double)a1 * us));
+      dst[0] = Elem<T>::from_f32((float)(a0 * us));
+      dst[1] = Elem<T>::from_f32((float)(a1 * us));
     } else {
+      // the parts' exact integer sums meet in int64 atomics
       unsigned long long* ap = (unsigned long long*)acc + (int64_t)t * di + col;
-      atomicAdd(ap, (unsigned long long)a0);
-      atomicAdd(ap + 1, (unsigned long long)a1);
+      atomicAdd(ap, (unsigned long long)(long long)a0);
+      atomicAdd(ap + 1, (unsigned long long)(long long)a1);
     }
   }
 }
