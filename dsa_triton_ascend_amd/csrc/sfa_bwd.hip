@@ -32,8 +32,9 @@
 //     scaled by a power of two per (record, slice), so the stored values
 //     keep 11 bits relative to the slice's largest entry.
 //  C. sfa_bwd_reduce_kernel: one wave per (key token, slice) sums the
-//     token's records in int64 fixed point (exact and associative, so the
-//     bucket order does not matter) and writes the key gradients.
+//     token's records in fixed point (integer-valued doubles below 2^52:
+//     exact and associative, so the bucket order does not matter) and
+//     writes the key gradients.
 // Rows are processed in chunks whose workspace stays within a budget; the
 // chunks' sums are added in chunk order in fp32.
 #include <atomic>
@@ -742,9 +743,11 @@ __global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) 
 // C. per key token: the sum of its records, one wave per column slice
 // ---------------------------------------------------------------------------
 // Records of token t are rec[offs[t] .. offs[t+1]); a slice value is
-// fp16 * 2^e.  They are summed in int64 fixed point with 2^-F resolution,
-// F chosen from the largest slice exponent and the record count so that no
-// partial sum overflows; integer addition is exact and associative.  A lane
+// fp16 * 2^e.  They are summed in fixed point with 2^-F resolution: each
+// term rounded to the grid (rint of a double), F chosen from the largest
+// slice exponent and the record count so that every partial sum is an
+// integer below 2^52, so the double additions are exact and associative (a
+// conversion to int64 per element measured slower).  A lane
 // reads 16 bytes (8 columns) of a record, so one load instruction covers
 // 64 / (width / 8) records of the slice; the lanes holding the same columns
 // are summed through LDS at the end.  The chunk's sum is added to the
@@ -755,7 +758,7 @@ __global__ __launch_bounds__(kRecSlices * 64) void sfa_bwd_reduce_kernel(SfaBwdP
   using SL = RecSlices<D, MERGE>;
   constexpr int DR = 64;
   constexpr int U = 4;  // loads in flight per lane
-  __shared__ long long s_red[kRecSlices][64][8];
+  __shared__ double s_red[kRecSlices][64][8];
   const int lane = threadIdx.x & 63;
   const int s = threadIdx.x >> 6;  // slice
   const int64_t t = blockIdx.x;
@@ -774,10 +777,14 @@ __global__ __launch_bounds__(kRecSlices * 64) void sfa_bwd_reduce_kernel(SfaBwdP
   const bool nonfinite = emax == kRecNonFinite;
   int lb = 0;
   while ((1 << lb) < len) ++lb;
-  const int F = 61 - emax - lb;  // |sum| < len * 2^emax <= 2^(emax + lb)
+  // every term is rounded to the grid 2^-F and the sums of such integers,
+  // |sum| < len * 2^emax * 2^F <= 2^52, are exact in a double: the
+  // additions do not depend on their order (the records' order in the
+  // bucket, the lanes' split of them)
+  const int F = 52 - emax - lb;
   // pass 2
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-  long long a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  double a[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
   if (len > 0 && !nonfinite && act) {
     const _Float16* src = p.rec + (int64_t)o0 * p.nc + c0 + ch * 8;
     const int16_t* ex = p.rexp + (int64_t)o0 * kRecSlices + s;
@@ -795,7 +802,7 @@ __global__ __launch_bounds__(kRecSlices * 64) void sfa_bwd_reduce_kernel(SfaBwdP
       for (int k = 0; k < U; ++k) {
         const double sc = ldexp(1.0, ev[k] + F);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) a[e] += __double2ll_rn((double)v[k][e] * sc);
+        for (int e = 0; e < 8; ++e) a[e] += __builtin_rint((double)v[k][e] * sc);
       }
     }
   }
@@ -803,7 +810,7 @@ __global__ __launch_bounds__(kRecSlices * 64) void sfa_bwd_reduce_kernel(SfaBwdP
   for (int e = 0; e < 8; ++e) s_red[s][lane][e] = a[e];
   __syncthreads();
   if (lane >= cps) return;
-  long long sum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  double sum[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
   for (int k = 0; k < rpi; ++k)
 #pragma unroll
     for (int e = 0; e < 8; ++e) sum[e] += s_red[s][k * cps + ch][e];
@@ -811,7 +818,7 @@ __global__ __launch_bounds__(kRecSlices * 64) void sfa_bwd_reduce_kernel(SfaBwdP
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int c = c0 + ch * 8 + e;  // record column
-    float v = len == 0 ? 0.f : (nonfinite ? NAN : (float)((double)sum[e] * us));
+    float v = len == 0 ? 0.f : (nonfinite ? NAN : (float)(sum[e] * us));
     float* ap = p.acc + t * p.nc + c;
     if (!FIRST) v += *ap;
     if (!FINAL) {
