@@ -265,11 +265,26 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void sfa_bwd_dq_kernel(SfaBwdPar
     // ---- compact this range of positions into s_list (stable order) ----
     const int64_t c1 = min(total_pos, c0 + (int64_t)kBwdList);
     int n_valid = 0;
-    for (int64_t b0 = c0; b0 < c1; b0 += NT) {
+    // The range's index entries are all loaded first (unconditional, at
+    // clamped positions), and the slots' bucket ranks are stored after the
+    // whole range's atomics are in flight: a load or atomic whose value is
+    // used right away is waited for on the spot, which had cost two memory
+    // round trips per 256 positions.
+    constexpr int RPT = kBwdList / NT;
+    static_assert(RPT * NT == kBwdList, "positions per thread");
+    int idv[RPT], rkv[RPT], jv[RPT];
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) idv[u] = sfa_load_id(p, idx_row, (int)min(c0 + u * NT + tid, c1 - 1));
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) {
+      const int64_t b0 = c0 + (int64_t)u * NT;
+      jv[u] = -1;
+      rkv[u] = 0;
+      if (b0 >= c1) continue;  // uniform
       const int64_t pos = b0 + tid;
       int phys = 0;
       bool valid = false;
-      if (ri.active && pos < c1) valid = sfa_resolve(p, ri, idx_row, (int)pos, &phys);
+      if (ri.active && pos < c1) valid = sfa_resolve_id(p, ri, idv[u], (int)pos, &phys, (const int32_t*)nullptr);
       const unsigned long long m = __ballot(valid);
       if (lane == 0) s_wcnt[wave] = __popcll(m);
       lds_barrier();
@@ -287,12 +302,16 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void sfa_bwd_dq_kernel(SfaBwdPar
           // the token list and, from the token's count, the slot's place in
           // its bucket (integer counts: their order does not matter)
           list_row[jbase + j] = phys;
-          rank_row[jbase + j] = atomicAdd(&p.cnt[phys], 1);
+          rkv[u] = atomicAdd(&p.cnt[phys], 1);
+          jv[u] = jbase + j;
         }
       }
       n_valid += tot;
       lds_barrier();
     }
+#pragma unroll
+    for (int u = 0; u < RPT; ++u)
+      if (jv[u] >= 0) rank_row[jv[u]] = rkv[u];
     if (tid < TILE) s_list[n_valid + tid] = -1;
     lds_barrier();
     const int n_tiles = (n_valid + TILE - 1) / TILE;
@@ -540,18 +559,31 @@ __global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) 
   V8 xa[MT][KH];                          // Q nope / Q rope / dO columns
   V8 xo[MERGE ? MT : 1][KH];              // merged nope columns: dO
   constexpr int CPR = XC / 8;             // 16-byte chunks per staged row
+  // A thread's chunks of the 32 heads are all loaded before any is written:
+  // a load under a condition, or written to LDS right away, is waited for
+  // on the spot, and the staging then took one memory round trip per chunk
+  // (per-row timeline: 120 k cycles before the tile loop, against about
+  // 8.5 k per tile).  Heads >= N1 load head 0 and are zeroed at the write.
+  constexpr int XPT = (32 * CPR + NW * 64 - 1) / (NW * 64);  // chunks per thread
   for (int ks = 0; ks < KH; ++ks) {
-    for (int e = tid; e < 32 * CPR; e += NW * 64) {
-      const int hh = e / CPR, c = (e - hh * CPR) * 8;
+    u32x4 xv[XPT];
+#pragma unroll
+    for (int u = 0; u < XPT; ++u) {
+      const int e = u * NW * 64 + tid;
+      const int ec = e < 32 * CPR ? e : 0;
+      const int hh = ec / CPR, c = (ec - hh * CPR) * 8;
       const int h = ks * 32 + hh;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (h < p.n1) {
-        const int64_t r = row * p.n1 + h;
-        if (c < D) v = *(const u32x4*)((const T*)p.q + r * D + c);
-        else if (c < D + DR) v = *(const u32x4*)((const T*)p.qr + r * DR + (c - D));
-        else v = *(const u32x4*)((const T*)p.dout + r * D + (c - D - DR));
-      }
-      *(u32x4*)&s_x[hh * XROW + c] = v;
+      const int64_t r = row * p.n1 + (h < p.n1 ? h : 0);
+      const T* src = c < D ? (const T*)p.q + r * D + c
+                   : c < D + DR ? (const T*)p.qr + r * DR + (c - D)
+                                : (const T*)p.dout + r * D + (c - D - DR);
+      xv[u] = *(const u32x4*)src;
+    }
+#pragma unroll
+    for (int u = 0; u < XPT; ++u) {
+      const int e = u * NW * 64 + tid;
+      const int hh = e / CPR, c = (e - hh * CPR) * 8;
+      if (e < 32 * CPR) *(u32x4*)&s_x[hh * XROW + c] = ks * 32 + hh < p.n1 ? xv[u] : (u32x4){0u, 0u, 0u, 0u};
     }
     lds_barrier();
     const int r1 = lg * 4 + (li >> 2);
@@ -635,10 +667,24 @@ __global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) 
     lds_barrier();
     if ((t % (NPOS / TILE)) == 0) {
       // bucket positions of the next 64 tiles' slots (every wave is past
-      // the reads of the previous ones)
-      for (int e = tid; e < NPOS; e += NW * 64) {
-        const int j = t * TILE + e;
-        s_pos[e] = j < nv ? p.offs[list_row[j]] + rank_row[j] : 0;
+      // the reads of the previous ones); every load of a round is issued
+      // before its values are used (two memory round trips, not two per
+      // slot)
+      constexpr int PPT = NPOS / (NW * 64);
+      int lt[PPT], lr[PPT];
+#pragma unroll
+      for (int u = 0; u < PPT; ++u) {
+        const int j = t * TILE + u * NW * 64 + tid;
+        const int jc = j < nv ? j : 0;
+        lt[u] = list_row[jc];
+        lr[u] = rank_row[jc];
+      }
+#pragma unroll
+      for (int u = 0; u < PPT; ++u) lt[u] = p.offs[lt[u]];
+#pragma unroll
+      for (int u = 0; u < PPT; ++u) {
+        const int j = t * TILE + u * NW * 64 + tid;
+        s_pos[u * NW * 64 + tid] = j < nv ? lt[u] + lr[u] : 0;
       }
       lds_barrier();
     }
