@@ -182,15 +182,21 @@ __global__ __launch_bounds__(kBwdWaves * 64, 1) void sfa_bwd_dq_kernel(SfaBwdPar
     else v = *(const u32x4*)((const T*)p.qr + hrow * DR + (ks - KSN) * 32 + lg * 8);
     qf[ks] = as_v8<V8>(hv ? v : z4);
   }
+  // every dO and O load is issued before any is used (used one by one, the
+  // loads had come back a few at a time, one memory round trip each)
+  u32x4 ov[KSN];
+#pragma unroll
+  for (int ks = 0; ks < KSN; ++ks) {
+    dof[ks] = as_v8<V8>(*(const u32x4*)((const T*)p.dout + hrow * D + ks * 32 + lg * 8));
+    ov[ks] = *(const u32x4*)((const T*)p.out + hrow * D + ks * 32 + lg * 8);
+  }
   float delta = 0.f;
 #pragma unroll
   for (int ks = 0; ks < KSN; ++ks) {
-    const u32x4 v = *(const u32x4*)((const T*)p.dout + hrow * D + ks * 32 + lg * 8);
-    const u32x4 o = *(const u32x4*)((const T*)p.out + hrow * D + ks * 32 + lg * 8);
-    dof[ks] = as_v8<V8>(hv ? v : z4);
-    const V8 dv8 = as_v8<V8>(v), ov8 = as_v8<V8>(o);
+    const V8 ov8 = as_v8<V8>(ov[ks]);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) delta += E::to_f32(dv8[j]) * E::to_f32(ov8[j]);
+    for (int j = 0; j < 8; ++j) delta += E::to_f32(dof[ks][j]) * E::to_f32(ov8[j]);
+    if (!hv) dof[ks] = as_v8<V8>(z4);
   }
   delta = xgroup_sum(delta);  // lanes li, li+16, li+32, li+48 cover all D columns
   float m2 = 0.f, inv = 0.f;
