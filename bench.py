@@ -15,8 +15,8 @@ step's dominant kernel, sfa_fwd_ds_kernel (64 heads per workgroup, four
 token splits), together with the sfa_combine_kernel that merges its splits.
 
 Beside the headline, each leg of the operator set is timed the same way:
-the lightning indexer at 32K context (decode, secondary metric) and at the
-cfg2 prefill shape, the SFA prefill forward, the SFA backward (reference API
+the lightning indexer at 32K context (decode, secondary metric; also with
+S1 = 2 and 4 query rows per batch) and at the cfg2 prefill shape, the SFA prefill forward, the SFA backward (reference API
 and training path), the sparse KL-loss backward and the dense warm-up stage.
 Each leg carries a CPU baseline: the numpy oracle (a tests-only restatement
 of the reference goldens) on the host cores, over the whole batch or a
@@ -381,6 +381,36 @@ def li_prefill_algorithmic():
     nbytes = (LIP_B * LIP_S * LIP_N1 * (LIP_D * 2 + 4) + LIP_B * LIP_S * LIP_D * 2
               + LIP_B * LIP_S * LIP_K * 4)
     return pairs, flops, nbytes
+
+
+def time_li_s1(s1, nsets, steps, warmup, device):
+    """The decode indexer step with S1 query rows per batch (multi-token
+    decode: B=32, S2=32768, mode 3), over nsets rotating input sets; ms per
+    step."""
+    import torch
+    g = torch.Generator(device=device).manual_seed(4321 + s1)
+    fns = []
+    idx = torch.empty(LI_B, s1, 1, LI_K, dtype=torch.int32, device=device)
+    keep = []
+    for _ in range(nsets):
+        q = torch.randn(LI_B, s1, LI_N1, LI_D, generator=g, device=device).to(torch.bfloat16)
+        k = torch.randn(LI_B, LI_S2, 1, LI_D, generator=g, device=device).to(torch.bfloat16)
+        w = torch.rand(LI_B, s1, LI_N1, generator=g, device=device)
+        keep.append((q, k, w))
+        fns.append(li_step_fn(q, k, w, idx, LI_B, s1, LI_S2, LI_N1, LI_D, LI_K, 3))
+    for i in range(max(warmup, 2)):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        fns[i % len(fns)]()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    del keep, fns, idx
+    return ms
 
 
 def time_li_prefill(sets, steps, warmup):
@@ -921,12 +951,24 @@ def main():
     li_ms_after, _ = time_li(li_sets, args.steps, args.warmup)
     del li_sets
     torch.cuda.empty_cache()
+    # multi-token decode: S1 = 2 and 4 query rows per batch share the batch's
+    # keys (the per-row kernel re-reads them; L2 / Infinity Cache serve the
+    # repeats)
+    li_s1 = {}
+    for s1 in (2, 4):
+        ms_s1 = time_li_s1(s1, 2, args.steps, args.warmup, dev)
+        li_s1[str(s1)] = {"ms_per_step": round(ms_s1, 5), "us_per_query": round(ms_s1 * 1e3 / (LI_B * s1), 4),
+                          "key_GBps": round(LI_B * LI_S2 * LI_D * 2 / (ms_s1 * 1e-3) / 1e9, 1)}
+        torch.cuda.empty_cache()
     li_flops, li_bytes = li_algorithmic()
     li_gbs = li_bytes / (li_ms * 1e-3) / 1e9
     result["lightning_indexer"] = {
         "metric": "lightning_indexer us/query at 32K ctx (decode)",
         "value": round(li_ms * 1e3 / LI_B, 4), "unit": "us/query", "higher_is_better": False,
         "ms_per_step": round(li_ms, 5),
+        "s1_sweep": dict(li_s1, note="B=32, S2=32768, mode 3, S1 query rows per batch (2 input sets); "
+                                     "us_per_query per query row; key_GBps: the keys' bytes once per step "
+                                     "over the step time"),
         "after_decode_leg": {"value": round(li_ms_after * 1e3 / LI_B, 4), "ms_per_step": round(li_ms_after, 5),
                              "note": "the same step on inputs allocated after the decode leg's inputs (about "
                                      "7 GB) were freed and released to the driver; the headline value is "

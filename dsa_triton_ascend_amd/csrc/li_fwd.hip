@@ -52,6 +52,7 @@ struct LiParams {
   int32_t d;           // head dim (the row stride of q and k)
   int32_t mode, layout_q, layout_k, w_dtype;
   int32_t chunk;       // keys per workgroup
+  int32_t row_tiles;   // multi-row kernel: 64-key tiles per workgroup (blockIdx.y), 0 = the whole row
   // PA_BSND key cache [blocks, page, N2, D]: key s2 of batch b is row
   // block_table[b, s2 / page] * page + s2 % page (k_rows = blocks * page)
   const int32_t* block_table;
@@ -391,7 +392,15 @@ __device__ __forceinline__ void li_rows_scores(const LiParams& p, unsigned char 
   int kend = 0;
 #pragma unroll
   for (int w = 0; w < kLiRows; ++w) kend = max(kend, s_lim[w]);
+  // this workgroup's tiles [tb, te) of the rows' ntiles: all of them, or
+  // (p.row_tiles > 0, few rows per batch) chunk blockIdx.y of row_tiles
+  // tiles, so that the chunks fill the CUs; keys of the chunk past the
+  // rows' visible keys are masked below
   const int ntiles = (kend + kLiRowTile - 1) / kLiRowTile;
+  const int ct = p.row_tiles > 0 ? p.row_tiles : (p.s2 + kLiRowTile - 1) / kLiRowTile;
+  const int tb = (int)blockIdx.y * ct;
+  const int te = max(tb, min(ntiles, tb + ct));
+  const int key_end = (int)min((int64_t)p.s2, (int64_t)(tb + ct) * kLiRowTile);
 
   // DMA j of this wave covers tile rows (j * kLiRows + wave) * RPD .. +RPD-1;
   // lane L: row + L / CPR, LDS chunk L % CPR <- source chunk (L % CPR) ^ swz
@@ -431,20 +440,21 @@ __device__ __forceinline__ void li_rows_scores(const LiParams& p, unsigned char 
       li_dma16((unsigned)(uintptr_t)&s_k[buf][d * 1024], src);
     }
   };
-  issue_tile(0, 0);
-  issue_tile(1, 1);
+  issue_tile(tb, 0);
+  issue_tile(tb + 1, 1);
 
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t % NBUF;
+  for (int t = tb; t < te; ++t) {
+    const int it = t - tb;
+    const int buf = it % NBUF;
     if (active) {
-      if (t == 0) li_wait_vm<NDW>();
-      else if (t == 1) li_wait_vm<NDW + 1>();
+      if (it == 0) li_wait_vm<NDW>();
+      else if (it == 1) li_wait_vm<NDW + 1>();
       else li_wait_vm<NDW + 2>();
     } else {
       li_wait_vm<NDW>();
     }
     lds_barrier();
-    issue_tile(t + 2, (t + 2) % NBUF);  // into the buffer tile t-1 used
+    issue_tile(t + 2, (it + 2) % NBUF);  // into the buffer tile t-1 used
     if (!active) continue;
     const unsigned char* tb = s_k[buf];
     auto kread = [&](int kg, int ks) -> V8 {
@@ -495,9 +505,9 @@ __device__ __forceinline__ void li_rows_scores(const LiParams& p, unsigned char 
     li_store_f32(srow + (key < p.s2 ? key : p.s2 - 1), key < p.s2 ? outv : vlast);
   }
   li_wait_vm<0>();
-  // keys past the tiles are masked
+  // keys of the chunk past the tiles are masked
   if (active)
-    for (int key = ntiles * kLiRowTile + lane; key < p.s2; key += 64) srow[key] = -INFINITY;
+    for (int key = te * kLiRowTile + lane; key < key_end; key += 64) srow[key] = -INFINITY;
 }
 
 template <int D, typename T, int GT>
@@ -1640,9 +1650,21 @@ static hipError_t launch_score(const LiParams& p, hipStream_t stream) {
     if (p.layout_q == DSA_LAYOUT_BSND && p.s1 >= 4) {
       LiParams q = p;
       const unsigned grid = (unsigned)((int64_t)p.batch * p.n2 * ((p.s1 + kLiRows - 1) / kLiRows));
+      // few query rows per batch (multi-token decode): the rows' keys split
+      // into chunks of at least 8 tiles, so that about two workgroups per CU
+      // run (one workgroup per row group left most CUs idle)
+      const int64_t want = 2 * (int64_t)device_cu_count();
+      const int tiles = (p.s2 + kLiRowTile - 1) / kLiRowTile;
+      unsigned chunks = 1;
+      if ((int64_t)grid < want) {
+        const int64_t c = (want + grid - 1) / grid;
+        q.row_tiles = (int32_t)std::max<int64_t>(8, (tiles + c - 1) / c);
+        chunks = (unsigned)((tiles + q.row_tiles - 1) / q.row_tiles);
+        if (chunks <= 1) q.row_tiles = 0;
+      }
       void* args[] = {&q};
-      return hipLaunchKernel((const void*)li_score_rows_kernel<D, T, GT>, dim3(grid), dim3(kLiRows * 64), args, 0,
-                             stream);
+      return hipLaunchKernel((const void*)li_score_rows_kernel<D, T, GT>, dim3(grid, chunks), dim3(kLiRows * 64),
+                             args, 0, stream);
     }
   }
   return launch_score_kernel((const void*)li_score_kernel<D, T, GT, PAD, false>, p, stream);
@@ -1733,6 +1755,7 @@ static LiParams li_params(const void* query, const void* key, const void* weight
   p.max_blocks = (int32_t)max_blocks;
   p.page_size = (int32_t)(page_size > 0 ? page_size : 1);
   p.chunk = kLiChunk;
+  p.row_tiles = 0;
   p.d = (int32_t)d;
   return p;
 }

@@ -177,8 +177,11 @@ def test_scores_match_oracle(B, S1, S2, N1, N2, D, mode, dtype, wdtype):
 # ---------------------------------------------------------------------------
 # full operator
 # ---------------------------------------------------------------------------
-def _check_topk_with_ties(idx_g, sc_rows, k, score_tol_rows, what):
-    """idx_g [R, k] from the GPU; sc_rows [R, S2] oracle fp32 scores."""
+def _check_topk_with_ties(idx_g, sc_rows, k, score_tol_rows, what, max_flips=None):
+    """idx_g [R, k] from the GPU; sc_rows [R, S2] oracle fp32 scores.  Every
+    differing entry must be a near tie (score gap within twice the
+    reassociation bound); the count of such flips only guards against a
+    systematic mismatch (max_flips, default max(4, entries / 500))."""
     ie, _ = stable_topk(sc_rows, k)
     flips = 0
     for r in range(ie.shape[0]):
@@ -192,11 +195,11 @@ def _check_topk_with_ties(idx_g, sc_rows, k, score_tol_rows, what):
             assert gap <= 2 * score_tol_rows[r], f"{what}: row {r} pos {j}: {a} vs {b}, score gap {gap:.3g}"
         flips += len(d)
     print(f"  {what}: tie flips {flips} of {idx_g.size} entries", flush=True)
-    assert flips <= max(4, idx_g.size // 500)
+    assert flips <= (max(4, idx_g.size // 500) if max_flips is None else max_flips)
 
 
 def _full_case(B, S1, S2, N1, N2, D, k, mode, dtype, rows=None, act_q=None, act_k=None, seed=42,
-               wdtype=torch.float32):
+               wdtype=torch.float32, max_flips=None):
     dsa = _api()
     q, k_, w = _inputs(B, S1, S2, N1, N2, D, dtype, wdtype, seed=seed)
     idx, val = dsa.lightning_indexer_triton(
@@ -217,7 +220,7 @@ def _full_case(B, S1, S2, N1, N2, D, k, mode, dtype, rows=None, act_q=None, act_
         t = 1e-5 * np.einsum("nd,tnd->nt", a, np.abs(k_[b])) + 1e-6                       # [N2, S2]
         _check_topk_with_ties(idx[b, s], rs, k, (np.where(np.isfinite(rs), t, 0.0).max(axis=1)
                                                  + 1e-5 * np.abs(np.where(np.isfinite(rs), rs, 0)).max()),
-                              f"row ({b},{s})")
+                              f"row ({b},{s})", max_flips)
         # values: the query dtype rounding of the score at the returned index
         for n2 in range(N2):
             ii = idx[b, s, n2]
@@ -227,6 +230,19 @@ def _full_case(B, S1, S2, N1, N2, D, k, mode, dtype, rows=None, act_q=None, act_
                 ok = (ii < 0) | (np.abs(val[b, s, n2] - exp_v) <= 1e-2 * np.abs(exp_v) + 1e-3)
             assert ok.all() and np.array_equal(np.isneginf(val[b, s, n2]), ii < 0)
     return idx
+
+
+@pytest.mark.parametrize("B,S1,S2", [(4, 4, 16384), (2, 8, 9000)], ids=["mtp4_16k", "s1_8_9000"])
+def test_indexer_multi_token_decode(B, S1, S2):
+    """A few query rows per batch over a long key range (multi-token
+    decode): the multi-row score kernel splits each row group's keys into
+    chunks over the CUs; every row against the oracle (top-k with the tie
+    rule, values)."""
+    print(f"[li mtp] B={B} S1={S1} S2={S2}", flush=True)
+    # every differing index is a near tie (checked); up to 16 per row of
+    # 2048 (0.8 %) are allowed, where the 32K decode batch sees about one
+    _full_case(B, S1, S2, 64, 1, 128, 2048, 3, torch.bfloat16, act_k=[S2 - 5 * b for b in range(B)],
+               max_flips=16)
 
 
 def test_indexer_small_mode3_hidden_rows():
