@@ -108,9 +108,13 @@ def lightning_indexer_triton(
         q_rows = T1
         if layout_key == "TND":
             T2, N2, _ = key.shape
-            # score-row width: the longest sequence (one host read of B lengths,
-            # as the reference's TND conversion does)
-            kl = act_k.to("cpu", torch.int64)
+            # score-row width: the longest sequence (lengths given as a list are
+            # read on the host; a device tensor costs one host read of B
+            # lengths, as the reference's TND conversion does)
+            if isinstance(actual_seq_lengths_key, torch.Tensor):
+                kl = act_k.to("cpu", torch.int64)
+            else:
+                kl = torch.tensor([int(v) for v in actual_seq_lengths_key], dtype=torch.int64)
             S2 = int((kl - torch.cat([kl.new_zeros(1), kl[:-1]])).max().item()) if B > 0 else 0
             k_rows = T2
         else:

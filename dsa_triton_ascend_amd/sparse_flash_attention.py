@@ -32,12 +32,27 @@ _D_ROPE = 64
 _VALID_N1 = (1, 2, 4, 8, 16, 32, 64, 128)
 
 
+# Device copies of sequence-length lists, by (device, lengths): building one
+# is a host-to-device copy from pageable memory, which waits for the stream's
+# queued work, so a call with a plain list would otherwise serialise with
+# the kernels of the previous call.  The kernels only read these tensors.
+_SEQ_CACHE = {}
+_SEQ_CACHE_MAX = 64
+
+
 def _seq_tensor(x, device):
     if x is None:
         return None
     if isinstance(x, torch.Tensor):
         return x.to(device=device, dtype=torch.int32).contiguous()
-    return torch.tensor(list(x), dtype=torch.int32, device=device)
+    key = (str(torch.device(device)), tuple(int(v) for v in x))
+    t = _SEQ_CACHE.get(key)
+    if t is None:
+        t = torch.tensor(list(key[1]), dtype=torch.int32, device=device)
+        if len(_SEQ_CACHE) >= _SEQ_CACHE_MAX:
+            _SEQ_CACHE.pop(next(iter(_SEQ_CACHE)))
+        _SEQ_CACHE[key] = t
+    return t
 
 
 def _expect_shape(t, shape, name):
