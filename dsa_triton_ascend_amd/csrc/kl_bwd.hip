@@ -936,8 +936,9 @@ __global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, co
       const int L = (len + np - 1) / np;
       const int i1 = min(len, (part + 1) * L);
       // A contribution is c16 * 2^-e_row; its fixed-point value is
-      // rint(c16 * 2^(e - e_row)), an integer-valued double, and the sums
-      // of such values stay below 2^52 (the exponent's bound), so the
+      // rint(c16 * 2^(e - e_row)) (scaled and rounded in fp32, where it is
+      // exact, then widened to a double; an integer below 2^52 either way),
+      // and the sums of such values stay below 2^52 (the exponent's bound), so the
       // double additions are exact and their order does not matter (an
       // integer shift-and-round per element, with branches or branch-free,
       // and a conversion to int64 per element measured slower).  The
@@ -958,9 +959,9 @@ __global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, co
           }
   #pragma unroll
           for (int u = 0; u < U; ++u) {
-            const double sc = ldexp(1.0, __builtin_amdgcn_readlane(kv, u0 + u));
-            a0 += __builtin_rint((double)v[u].x * sc);
-            a1 += __builtin_rint((double)v[u].y * sc);
+            const float sc = ldexpf(1.f, __builtin_amdgcn_readlane(kv, u0 + u));
+            a0 += (double)__builtin_rintf((float)v[u].x * sc);
+            a1 += (double)__builtin_rintf((float)v[u].y * sc);
           }
         }
       }

@@ -796,10 +796,11 @@ __global__ __launch_bounds__(8 * 64, 1) void sfa_bwd_rec_kernel(SfaBwdParams p) 
 // ---------------------------------------------------------------------------
 // Records of token t are rec[offs[t] .. offs[t+1]); a slice value is
 // fp16 * 2^e.  They are summed in fixed point with 2^-F resolution: each
-// term rounded to the grid (rint of a double), F chosen from the largest
-// slice exponent and the record count so that every partial sum is an
-// integer below 2^52, so the double additions are exact and associative (a
-// conversion to int64 per element measured slower).  A lane
+// term rounded to the grid (scaled and rounded in fp32, where the fp16
+// value times a power of two is exact, then widened to a double), F chosen
+// from the largest slice exponent and the record count so that every
+// partial sum is an integer below 2^52, so the double additions are exact
+// and associative (a conversion to int64 per element measured slower).  A lane
 // reads 16 bytes (8 columns) of a record, so one load instruction covers
 // 64 / (width / 8) records of the slice; the lanes holding the same columns
 // are summed through LDS at the end.  The chunk's sum is added to the
@@ -852,9 +853,9 @@ __global__ __launch_bounds__(kRecSlices * 64) void sfa_bwd_reduce_kernel(SfaBwdP
       }
 #pragma unroll
       for (int k = 0; k < U; ++k) {
-        const double sc = ldexp(1.0, ev[k] + F);
+        const float sc = ldexpf(1.f, ev[k] + F);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) a[e] += __builtin_rint((double)v[k][e] * sc);
+        for (int e = 0; e < 8; ++e) a[e] += (double)__builtin_rintf((float)v[k][e] * sc);
       }
     }
   }
