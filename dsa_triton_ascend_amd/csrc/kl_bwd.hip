@@ -959,7 +959,10 @@ __global__ __launch_bounds__(256) void kl_reduce_kernel(const _Float16* cbuf, co
           }
   #pragma unroll
           for (int u = 0; u < U; ++u) {
-            const float sc = ldexpf(1.f, __builtin_amdgcn_readlane(kv, u0 + u));
+            // a nonzero c16 (>= 2^-24) has c16 * 2^kv < 2^52, so kv < 76;
+            // a zero one may come with a larger kv, which must not reach
+            // fp32's infinity (0 * inf is NaN)
+            const float sc = ldexpf(1.f, min(__builtin_amdgcn_readlane(kv, u0 + u), 80));
             a0 += (double)__builtin_rintf((float)v[u].x * sc);
             a1 += (double)__builtin_rintf((float)v[u].y * sc);
           }

@@ -853,7 +853,9 @@ __global__ __launch_bounds__(kRecSlices * 64) void sfa_bwd_reduce_kernel(SfaBwdP
       }
 #pragma unroll
       for (int k = 0; k < U; ++k) {
-        const float sc = ldexpf(1.f, ev[k] + F);
+        // ev + F <= 52 for every record of the token; idle lanes (ev = 0)
+        // hold zeros, and 2^F can exceed fp32's range (0 * inf is NaN)
+        const float sc = ldexpf(1.f, min(ev[k] + F, 60));
 #pragma unroll
         for (int e = 0; e < 8; ++e) a[e] += (double)__builtin_rintf((float)v[k][e] * sc);
       }
