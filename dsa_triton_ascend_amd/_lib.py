@@ -192,7 +192,19 @@ def ptr(t):
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device):
+    """The current stream of ``device`` as a raw handle.  torch's raw-stream
+    query takes about 0.2 us where building the Stream object takes about 2
+    (a decode call makes one per call); the public form is the fallback."""
+    if _raw_stream is not None:
+        if isinstance(device, torch.device):
+            idx = device.index
+        else:
+            idx = device if isinstance(device, int) else torch.device(device).index
+        return _raw_stream(torch.cuda.current_device() if idx is None else idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 

@@ -106,14 +106,14 @@ int li_scores_run(const void* query, const void* key, const void* weights, const
                   int32_t w_dtype, hipStream_t stream, const int32_t* block_table = nullptr,
                   int64_t max_blocks = 0, int64_t page_size = 1);
 int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_t* indices,
-                void* values, int32_t val_dtype, hipStream_t stream);
+                void* values, int32_t val_dtype, hipStream_t stream, bool values_zero = false);
 // scores and top-k: one fused launch where the shapes allow, else the two
 int li_fwd_run(const void* query, const void* key, const void* weights, const int32_t* act_q,
                const int32_t* act_k, float* scores, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
                int64_t n2, int64_t d, int64_t q_rows, int64_t k_rows, int32_t sparse_mode, int32_t layout_q,
                int32_t layout_k, int32_t dtype, int32_t w_dtype, int64_t k, int32_t* indices, void* values,
                hipStream_t stream, const int32_t* block_table = nullptr, int64_t max_blocks = 0,
-               int64_t page_size = 1);
+               int64_t page_size = 1, bool values_zero = false);
 constexpr int64_t kLiMaxK = 16384;  // the top-k sorts up to 16384 entries (LDS and per-wave registers)
 // calib.hip
 int calib_stream_read_run(const void* buf, size_t bytes, int nontemporal, unsigned* sink, hipStream_t stream);
@@ -637,7 +637,8 @@ int dsa_li_fwd(const void* query, const void* key, const void* weights, const in
   float* scores = (float*)workspace;
   return li_fwd_run(query, key, weights, actual_seq_q, actual_seq_k, scores, batch, s1, s2, n1, n2, d, q_rows,
                     k_rows, sparse_mode, layout_query, layout_key, dtype, weights_dtype, sparse_count,
-                    sparse_indices, return_value ? sparse_values : nullptr, (hipStream_t)stream);
+                    sparse_indices, sparse_values, (hipStream_t)stream, nullptr, 0, 1,
+                    !return_value && sparse_values);
 }
 
 static int li_check_paged(const int32_t* block_table, int64_t num_blocks, int64_t page_size,
@@ -696,8 +697,8 @@ int dsa_li_fwd_paged(const void* query, const void* key_cache, const void* weigh
   float* scores = (float*)workspace;
   return li_fwd_run(query, key_cache, weights, actual_seq_q, actual_seq_k, scores, batch, s1, s2, n1, n2, d,
                     q_rows, k_rows, sparse_mode, layout_query, DSA_LAYOUT_PA_BSND, dtype, weights_dtype,
-                    sparse_count, sparse_indices, return_value ? sparse_values : nullptr, (hipStream_t)stream,
-                    block_table, max_blocks, page_size);
+                    sparse_count, sparse_indices, sparse_values, (hipStream_t)stream, block_table, max_blocks,
+                    page_size, !return_value && sparse_values);
 }
 
 int dsa_calib_stream_read(const void* buffer, size_t bytes, int32_t nontemporal, uint32_t* sink, void* stream) {

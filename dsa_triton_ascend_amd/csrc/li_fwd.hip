@@ -637,6 +637,7 @@ struct TopkParams {
   void* values;         // [rows, k] in val_dtype, or null
   int64_t rows;
   int32_t s2, k, val_dtype;
+  int32_t val_zero;     // values get zeros (not requested, buffer given)
   int32_t sel_cap;      // power of two >= k: entries of the LDS sort buffer
 };
 
@@ -963,9 +964,10 @@ __device__ void topk_row_generic(const TopkParams& p, const int64_t row, unsigne
     irow[i] = idx;
     if (p.values) {
       const int64_t o = row * (int64_t)K + i;
-      if (p.val_dtype == DSA_DTYPE_FP32) ((float*)p.values)[o] = v;
-      else if (p.val_dtype == DSA_DTYPE_BF16) ((bf16*)p.values)[o] = (bf16)v;
-      else ((f16*)p.values)[o] = (f16)v;
+      const float w = p.val_zero ? 0.f : v;
+      if (p.val_dtype == DSA_DTYPE_FP32) ((float*)p.values)[o] = w;
+      else if (p.val_dtype == DSA_DTYPE_BF16) ((bf16*)p.values)[o] = (bf16)w;
+      else ((f16*)p.values)[o] = (f16)w;
     }
   }
 }
@@ -1216,9 +1218,10 @@ __global__ __launch_bounds__(kTopkThreads) void li_topk_kernel(TopkParams p) {
     irow[i] = idx;
     if (p.values) {
       const int64_t o = row * (int64_t)K + i;
-      if (p.val_dtype == DSA_DTYPE_FP32) ((float*)p.values)[o] = val;
-      else if (p.val_dtype == DSA_DTYPE_BF16) ((bf16*)p.values)[o] = (bf16)val;
-      else ((f16*)p.values)[o] = (f16)val;
+      const float w = p.val_zero ? 0.f : val;
+      if (p.val_dtype == DSA_DTYPE_FP32) ((float*)p.values)[o] = w;
+      else if (p.val_dtype == DSA_DTYPE_BF16) ((bf16*)p.values)[o] = (bf16)w;
+      else ((f16*)p.values)[o] = (f16)w;
     }
   }
 }
@@ -1418,9 +1421,10 @@ __device__ __forceinline__ bool topk_row256(const TopkParams& p, const int64_t r
     irow[i] = idx;
     if (p.values) {
       const int64_t o = row * (int64_t)K + i;
-      if (p.val_dtype == DSA_DTYPE_FP32) ((float*)p.values)[o] = val;
-      else if (p.val_dtype == DSA_DTYPE_BF16) ((bf16*)p.values)[o] = (bf16)val;
-      else ((f16*)p.values)[o] = (f16)val;
+      const float w = p.val_zero ? 0.f : val;
+      if (p.val_dtype == DSA_DTYPE_FP32) ((float*)p.values)[o] = w;
+      else if (p.val_dtype == DSA_DTYPE_BF16) ((bf16*)p.values)[o] = (bf16)w;
+      else ((f16*)p.values)[o] = (f16)w;
     }
   };
   if (fast) {
@@ -1569,11 +1573,12 @@ static bool li_topk_row_in_lds(int64_t s2, int64_t k) {
 }
 
 static TopkParams topk_params(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_t* indices,
-                              void* values, int32_t val_dtype) {
+                              void* values, int32_t val_dtype, bool values_zero) {
   TopkParams p;
   p.scores = scores;
   p.indices = indices;
   p.values = values;
+  p.val_zero = values_zero ? 1 : 0;
   p.rows = rows;
   p.s2 = (int32_t)s2;
   p.k = (int32_t)k;
@@ -1591,9 +1596,9 @@ static bool li_topk_quad_fits(int64_t rows, int64_t s2, int64_t k) {
 }
 
 int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_t* indices,
-                void* values, int32_t val_dtype, hipStream_t stream) {
+                void* values, int32_t val_dtype, hipStream_t stream, bool values_zero) {
   if (rows <= 0) return DSA_OK;
-  TopkParams p = topk_params(scores, rows, s2, k, indices, values, val_dtype);
+  TopkParams p = topk_params(scores, rows, s2, k, indices, values, val_dtype, values_zero);
   // dynamic LDS above 64 KB needs the per-function limit raised (to the
   // full budget; set on every call, which also covers every device and
   // concurrent callers: a host-side setting, cheap next to the launch)
@@ -1779,7 +1784,8 @@ int li_fwd_run(const void* query, const void* key, const void* weights, const in
                const int32_t* act_k, float* scores, int64_t batch, int64_t s1, int64_t s2, int64_t n1,
                int64_t n2, int64_t d, int64_t q_rows, int64_t k_rows, int32_t sparse_mode, int32_t layout_q,
                int32_t layout_k, int32_t dtype, int32_t w_dtype, int64_t k, int32_t* indices, void* values,
-               hipStream_t stream, const int32_t* block_table, int64_t max_blocks, int64_t page_size) {
+               hipStream_t stream, const int32_t* block_table, int64_t max_blocks, int64_t page_size,
+               bool values_zero) {
   const int64_t rows = q_rows * n2;
   const int64_t g = n2 > 0 ? n1 / n2 : 0;
   const bool fuse = q_rows > 0 && s2 > 0 && (dtype == DSA_DTYPE_BF16 || dtype == DSA_DTYPE_FP16) && d == 128 &&
@@ -1791,11 +1797,11 @@ int li_fwd_run(const void* query, const void* key, const void* weights, const in
                            sparse_mode, layout_q, layout_k, dtype, w_dtype, stream, block_table, max_blocks,
                            page_size);
     if (st != DSA_OK) return st;
-    return li_topk_run(scores, rows, s2, k, indices, values, dtype, stream);
+    return li_topk_run(scores, rows, s2, k, indices, values, dtype, stream, values_zero);
   }
   const LiParams p = li_params(query, key, weights, act_q, act_k, scores, batch, s1, s2, n1, n2, d, q_rows, k_rows,
                                sparse_mode, layout_q, layout_k, w_dtype, block_table, max_blocks, page_size);
-  const TopkParams tp = topk_params(scores, rows, s2, k, indices, values, dtype);
+  const TopkParams tp = topk_params(scores, rows, s2, k, indices, values, dtype, values_zero);
   const bool bf = dtype == DSA_DTYPE_BF16;
   // rows of up to 4096 scores (16 per thread: 158 VGPRs, three workgroups per
   // CU as the score kernel alone; 32 per thread took 224 and two)

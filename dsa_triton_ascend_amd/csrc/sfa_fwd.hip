@@ -64,7 +64,7 @@ struct SfaFwdParams {
   int32_t max_blocks, page_size;
   int32_t splits, rows_per_xcd, pos_per_split;
   float scale_log2;
-  int32_t return_lse;
+  int32_t return_lse;  // 0: no statistics, 1: the statistics, 2: zeros
 };
 
 constexpr int kSfaTile = 32;
@@ -706,7 +706,7 @@ __global__ __launch_bounds__(NW * 64, 1) void sfa_fwd_kernel(SfaFwdParams p) {
       const int64_t orow = row * p.n1 + head;
       if (p.splits == 1) {
         if (p.return_lse) {
-          const bool any = l_tot > 0.f;
+          const bool any = p.return_lse == 1 && l_tot > 0.f;
           p.smax[orow] = any ? m_true[ht] * kLn2 : 0.f;
           p.ssum[orow] = any ? l_tot * fast_exp2(m_ref[ht] - m_true[ht]) : 0.f;
         }
@@ -1368,7 +1368,7 @@ __global__ __launch_bounds__(512, 1) void sfa_fwd_ds_kernel(SfaFwdParams p) {
       const int64_t orow = row * p.n1 + head;
       if (p.splits == 1) {
         if (p.return_lse) {
-          const bool any = l_tot > 0.f;
+          const bool any = p.return_lse == 1 && l_tot > 0.f;
           p.smax[orow] = any ? mt * kLn2 : 0.f;
           p.ssum[orow] = any ? l_tot * fast_exp2(mr - mt) : 0.f;
         }
@@ -1489,8 +1489,9 @@ __global__ __launch_bounds__(256) void sfa_combine_kernel(SfaFwdParams p) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) op8[j] = E::from_f32(acc8[j] * inv8);
     if (p.return_lse && lane == 0) {
-      p.smax[rh] = L8 > 0.f ? mtrue8 * kLn2 : 0.f;
-      p.ssum[rh] = L8 > 0.f ? L8 * fast_exp2(mref8 - mtrue8) : 0.f;
+      const bool any = p.return_lse == 1 && L8 > 0.f;
+      p.smax[rh] = any ? mtrue8 * kLn2 : 0.f;
+      p.ssum[rh] = any ? L8 * fast_exp2(mref8 - mtrue8) : 0.f;
     }
     return;
   }
@@ -1543,8 +1544,9 @@ __global__ __launch_bounds__(256) void sfa_combine_kernel(SfaFwdParams p) {
 #pragma unroll
   for (int j = 0; j < PER; ++j) op[j] = E::from_f32(acc[j] * inv);
   if (p.return_lse && lane == 0) {
-    p.smax[rh] = L > 0.f ? mtrue * kLn2 : 0.f;
-    p.ssum[rh] = L > 0.f ? L * fast_exp2(mref - mtrue) : 0.f;
+    const bool any = p.return_lse == 1 && L > 0.f;
+    p.smax[rh] = any ? mtrue * kLn2 : 0.f;
+    p.ssum[rh] = any ? L * fast_exp2(mref - mtrue) : 0.f;
   }
 }
 
@@ -1765,7 +1767,9 @@ int sfa_fwd_run(const void* query, const void* query_rope, const void* key, cons
     p.part_ml = (float*)(p.part_o + (size_t)p.splits * q_rows * n1 * d);
   }
   p.scale_log2 = scale_value * kLog2e;
-  p.return_lse = return_lse;
+  // 1: write the statistics; 2: write zeros to the caller's buffers (given
+  // without return_lse), so that the caller needs no fill of its own
+  p.return_lse = return_lse ? 1 : (softmax_max && softmax_sum ? 2 : 0);
   p.rows_per_xcd = 0;
   hipError_t e;
   if (dtype == DSA_DTYPE_BF16) {

@@ -143,10 +143,13 @@ def lightning_indexer_triton(
     K = _check_k(sparse_count)
 
     out_shape = (q_rows, N2, K) if is_tnd else (B, S1, N2, K)
+    # the library writes every entry: the selected scores, or zeros when they
+    # are not requested (no fill kernel of torch's own per call)
     indices = torch.empty(out_shape, dtype=torch.int32, device=device)
-    values = torch.zeros(out_shape, dtype=query.dtype, device=device)
+    values = torch.empty(out_shape, dtype=query.dtype, device=device)
     if q_rows == 0 or S2 == 0:
         indices.fill_(-1)
+        values.zero_()
         return indices, values
 
     lib = _lib.load()
@@ -155,7 +158,7 @@ def lightning_indexer_triton(
     qc, kc, wc = query.contiguous(), key.contiguous(), weights.contiguous()
     st = lib.dsa_li_fwd(
         qc.data_ptr(), kc.data_ptr(), wc.data_ptr(), _lib.ptr(act_q), _lib.ptr(act_k),
-        indices.data_ptr(), values.data_ptr() if return_value else None,
+        indices.data_ptr(), values.data_ptr(),
         B, S1, S2, N1, N2, D, K, q_rows, k_rows, sparse_mode,
         _lib.LAYOUT[layout_query], _lib.LAYOUT[layout_key], _lib.dtype_code(query.dtype),
         _weights_code(weights.dtype), 1 if return_value else 0,
@@ -208,7 +211,7 @@ def _lightning_indexer_paged(query, key, weights, actual_seq_lengths_query, actu
         raise ValueError(f"weights must have shape {w_shape}, got {tuple(weights.shape)}")
     K = _check_k(sparse_count)
     indices = torch.empty(out_shape, dtype=torch.int32, device=device)
-    values = torch.zeros(out_shape, dtype=query.dtype, device=device)
+    values = torch.empty(out_shape, dtype=query.dtype, device=device)
     if q_rows == 0:
         return indices, values
     lib = _lib.load()
@@ -219,7 +222,7 @@ def _lightning_indexer_paged(query, key, weights, actual_seq_lengths_query, actu
     bt = block_table.to(torch.int32).contiguous()
     st = lib.dsa_li_fwd_paged(
         qc.data_ptr(), kc.data_ptr(), wc.data_ptr(), _lib.ptr(act_q), act_k.data_ptr(), bt.data_ptr(),
-        indices.data_ptr(), values.data_ptr() if return_value else None,
+        indices.data_ptr(), values.data_ptr(),
         B, S1, N1, N2, D, K, q_rows, num_blocks, page, max_blocks, sparse_mode,
         _lib.LAYOUT[layout_query], _lib.dtype_code(query.dtype), _weights_code(weights.dtype),
         1 if return_value else 0, ws.data_ptr(), ws_bytes, _lib.stream_handle(device))

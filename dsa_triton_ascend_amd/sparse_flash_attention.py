@@ -225,12 +225,10 @@ def sparse_flash_attention_triton(
     out_shape = (q_rows, N1, D) if is_tnd_q else (B, S1, N1, D)
     lse_shape = (1, q_rows, N1) if is_tnd_q else (B, 1, S1, N1)
     out = torch.empty(out_shape, dtype=query.dtype, device=device)
-    if return_softmax_lse:
-        smax = torch.empty(lse_shape, dtype=torch.float32, device=device)
-        ssum = torch.empty(lse_shape, dtype=torch.float32, device=device)
-    else:
-        smax = torch.zeros(lse_shape, dtype=torch.float32, device=device)
-        ssum = torch.zeros(lse_shape, dtype=torch.float32, device=device)
+    # the library writes the statistics, or zeros when they are not
+    # requested (no fill kernels of torch's own per call)
+    smax = torch.empty(lse_shape, dtype=torch.float32, device=device)
+    ssum = torch.empty(lse_shape, dtype=torch.float32, device=device)
     if q_rows == 0:
         return out, smax, ssum
 
@@ -239,8 +237,7 @@ def sparse_flash_attention_triton(
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device) if ws_bytes else None
     status = lib.dsa_sfa_fwd(
         _lib.ptr(q), _lib.ptr(qr), _lib.ptr(k), _lib.ptr(kr), _lib.ptr(si),
-        _lib.ptr(out), _lib.ptr(smax) if return_softmax_lse else None,
-        _lib.ptr(ssum) if return_softmax_lse else None,
+        _lib.ptr(out), _lib.ptr(smax), _lib.ptr(ssum),
         _lib.ptr(act_q), _lib.ptr(act_k), _lib.ptr(bt),
         B, S1, S2, N1, D, D_ROPE, K, q_rows, kv_rows, max_blocks, page,
         sparse_block_size, sparse_mode, pre_tokens, next_tokens, _lib.LAYOUT[layout_query],

@@ -105,8 +105,10 @@ int dsa_calib_stream_read(const void* buffer, size_t bytes, int32_t nontemporal,
  * band of the Ascend FlashAttention operators).  INT64_MAX on a side leaves
  * it open; negative values are allowed.
  * Writes attention_out [R, N1, D]; when return_lse != 0 also softmax_max /
- * softmax_sum [R, N1] (entries of rows without a visible token are 0; the
- * caller pre-zeroes them when return_lse == 0).
+ * softmax_sum [R, N1] (entries of rows without a visible token are 0).  With
+ * return_lse == 0, softmax_max and softmax_sum, when both are given, receive
+ * zeros (the reference's outputs when the statistics are not requested), so
+ * the caller needs no fill of its own; NULL leaves them unwritten.
  */
 int dsa_sfa_fwd(const void* query, const void* query_rope, const void* key,
                 const void* key_rope, const int32_t* sparse_indices,
@@ -326,6 +328,9 @@ size_t dsa_dense_kl_bwd_workspace_size(int64_t batch, int64_t s1, int64_t s2, in
  *   score rows).
  * Writes sparse_indices [R1, N2, K] int32 and, when return_value != 0,
  * sparse_values [R1, N2, K] in the query dtype (-inf where the index is -1).
+ * With return_value == 0, a sparse_values buffer that is given receives
+ * zeros (the reference's values when they are not requested), so the caller
+ * needs no fill of its own; NULL leaves it unwritten.
  * The workspace holds the fp32 scores [R1*N2, s2].  K <= 16384.
  */
 int dsa_li_fwd(const void* query, const void* key, const void* weights,
