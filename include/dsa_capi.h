@@ -211,9 +211,10 @@ size_t dsa_sfa_bwd_workspace_size(int64_t q_rows, int64_t kv_rows, int64_t n1, i
  * softmax_max / softmax_sum [B,1,S1,N1] fp32, actual_seq_qlen /
  * actual_seq_klen [B] (NULL = full lengths).  Writes d_query_index (query
  * index dtype), d_key_index (key index dtype), d_weights (weights dtype)
- * and loss[1] fp32 (sum over rows).  dKi is reduced without atomics in a
- * fixed-point sum, so every output is deterministic.  The workspace
- * (dsa_kl_bwd_workspace_size) holds rows * topK * d_idx fp16 slot
+ * and loss[1] fp32 (sum over rows).  dKi is reduced in a fixed-point sum
+ * (no floating-point atomics; the parts of long tokens meet in int64
+ * atomics, whose order does not matter), so every output is deterministic.
+ * The workspace (dsa_kl_bwd_workspace_size) holds rows * topK * d_idx fp16 slot
  * contributions (scaled by a per-row power of two), the token buckets and
  * kv_rows * d_idx int64 accumulators.  query/key/rope/index tensors share
  * one dtype (bf16 or fp16); D in {128, 256, 512}; N1 <= 128; d_idx a
