@@ -53,6 +53,7 @@ struct LiParams {
   int32_t mode, layout_q, layout_k, w_dtype;
   int32_t chunk;       // keys per workgroup
   int32_t row_tiles;   // multi-row kernel: 64-key tiles per workgroup (blockIdx.y), 0 = the whole row
+  int32_t xcd_group;   // one-row kernel: query rows per batch placed on one XCD (0: blockIdx.x order)
   // PA_BSND key cache [blocks, page, N2, D]: key s2 of batch b is row
   // block_table[b, s2 / page] * page + s2 % page (k_rows = blocks * page)
   const int32_t* block_table;
@@ -178,7 +179,15 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
-  const int rn = blockIdx.x;  // row * n2 + n2 index
+  // row * n2 + n2 index.  With xcd_group = G (BSND, N2 = 1, G query rows
+  // per batch, rows a multiple of 8 G) the G rows of a batch, which read the
+  // same keys, go to one XCD (workgroup x runs on XCD x % 8) so that the
+  // keys one of them brings into that XCD's L2 serve the others
+  int rn = blockIdx.x;
+  if (p.xcd_group > 1) {
+    const int G = p.xcd_group, xcd = rn & 7, j = rn >> 3;
+    rn = ((j / G) * 8 + xcd) * G + j % G;
+  }
   const int row = rn / p.n2;
   const int kh = rn - row * p.n2;
   const LiRow ri = li_row_info(p, row);
@@ -1672,7 +1681,12 @@ static hipError_t launch_score(const LiParams& p, hipStream_t stream) {
                              args, 0, stream);
     }
   }
-  return launch_score_kernel((const void*)li_score_kernel<D, T, GT, PAD, false>, p, stream);
+  // a few query rows per batch (BSND, one key head): a batch's rows on one
+  // XCD, where the second and later reads of its keys hit in L2
+  LiParams q = p;
+  if (p.layout_q == DSA_LAYOUT_BSND && p.n2 == 1 && p.s1 > 1 && p.q_rows % (8 * (int64_t)p.s1) == 0)
+    q.xcd_group = p.s1;
+  return launch_score_kernel((const void*)li_score_kernel<D, T, GT, PAD, false>, q, stream);
 }
 
 template <int D, typename T, bool PAD>
@@ -1761,6 +1775,7 @@ static LiParams li_params(const void* query, const void* key, const void* weight
   p.page_size = (int32_t)(page_size > 0 ? page_size : 1);
   p.chunk = kLiChunk;
   p.row_tiles = 0;
+  p.xcd_group = 0;
   p.d = (int32_t)d;
   return p;
 }

@@ -232,12 +232,15 @@ def _full_case(B, S1, S2, N1, N2, D, k, mode, dtype, rows=None, act_q=None, act_
     return idx
 
 
-@pytest.mark.parametrize("B,S1,S2", [(4, 4, 16384), (2, 8, 9000)], ids=["mtp4_16k", "s1_8_9000"])
+@pytest.mark.parametrize("B,S1,S2", [(4, 4, 16384), (2, 8, 9000), (16, 2, 8192), (8, 3, 5000)],
+                         ids=["mtp4_16k", "s1_8_9000", "mtp2_b16", "s1_3_b8"])
 def test_indexer_multi_token_decode(B, S1, S2):
     """A few query rows per batch over a long key range (multi-token
-    decode): the multi-row score kernel splits each row group's keys into
-    chunks over the CUs; every row against the oracle (top-k with the tie
-    rule, values)."""
+    decode): from four rows per batch the multi-row score kernel splits each
+    row group's keys into chunks over the CUs; two or three rows per batch
+    run the one-row kernel with a batch's rows placed on one XCD (the
+    remapped workgroup order); every row against the oracle (top-k with the
+    tie rule, values)."""
     print(f"[li mtp] B={B} S1={S1} S2={S2}", flush=True)
     # every differing index is a near tie (checked); up to 16 per row of
     # 2048 (0.8 %) are allowed, where the 32K decode batch sees about one
