@@ -30,6 +30,7 @@ TEST_SMALL_BWD_CHUNKS = 2
 TEST_KL_GENERIC = 4
 TEST_FWD_WIDE = 8
 TEST_LI_UNFUSED = 16
+TEST_LI_NO_PAIR = 32
 
 _c = ctypes
 _vp = _c.c_void_p

@@ -160,6 +160,7 @@ constexpr int kTestSmallBwdChunks = 2;     // backward rows in chunks of a 64 Ki
 constexpr int kTestKlGeneric = 4;          // the KL backward takes its generic path at every shape
 constexpr int kTestFwdWide = 8;            // D = 512 forwards run sfa_fwd_kernel (no column split)
 constexpr int kTestLiUnfused = 16;         // the indexer runs its scores and its top-k as two launches
+constexpr int kTestLiNoPair = 32;          // two query rows per batch run the one-row score kernel
 int test_flags();
 }  // namespace dsa
 

@@ -303,6 +303,136 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Two query rows per batch (BSND query, N2 = 1, S1 = 2: multi-token decode
+// with one draft token; exact head dims, 16-bit inputs).  A workgroup takes
+// both rows of a batch over one key chunk: every K fragment is loaded once
+// (non-temporal: no other workgroup reads these keys) and multiplied with
+// both rows' Q fragments, where the one-row kernel streamed each key once
+// per row.  The key range is the union of the two rows' visible ranges;
+// each row masks its own limit.  NP groups of 16 keys in flight per wave.
+// ---------------------------------------------------------------------------
+constexpr int kLiPairMaxChunk = 4096;  // keys per workgroup (two LDS score rows)
+constexpr int kLiPairRing = 4;         // groups of 16 keys in flight per wave
+
+template <int D, typename T, int GT, int NP>
+__global__ __launch_bounds__(kLiThreads) void li_score_pair_kernel(LiParams p) {
+  using E = Elem<T>;
+  using V8 = typename E::v8;
+  constexpr int KS = D / 32;
+  __shared__ __attribute__((aligned(16))) float s_sc[2][kLiPairMaxChunk];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int row0 = 2 * (int)blockIdx.x;
+  const LiRow ri0 = li_row_info(p, row0);
+  const LiRow ri1 = li_row_info(p, row0 + 1);
+  const int lim = max(ri0.lim, ri1.lim);
+  const int c0 = blockIdx.y * p.chunk;
+  const int c1 = min(p.s2, c0 + p.chunk);
+  float* srow0 = p.scores + (int64_t)row0 * p.s2;
+  float* srow1 = srow0 + p.s2;
+  if (c0 >= lim) {
+    for (int j = c0 + threadIdx.x; j < c1; j += kLiThreads) {
+      srow0[j] = -INFINITY;
+      srow1[j] = -INFINITY;
+    }
+    return;
+  }
+  // weights as raw bits (converted after the first key groups are issued)
+  uint32_t wraw[2][GT][4];
+  auto load_w = [&](auto* wp) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int ht = 0; ht < GT; ++ht)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int gg = ht * 16 + lg * 4 + e;
+          wraw[r][ht][e] = wp[(int64_t)(row0 + r) * p.n1 + (gg < p.g ? gg : 0)];
+        }
+  };
+  if (p.w_dtype == DSA_DTYPE_FP32) load_w((const uint32_t*)p.w);
+  else load_w((const uint16_t*)p.w);
+  V8 qf[2][GT][KS];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int ht = 0; ht < GT; ++ht) {
+      const int g = ht * 16 + li;
+      const bool gv = g < p.g;
+      const int64_t qrow = (int64_t)(row0 + r) * p.n1 + (gv ? g : 0);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        const u32x4 v = *(const u32x4*)((const T*)p.q + qrow * D + ks * 32 + lg * 8);
+        qf[r][ht][ks] = as_v8<V8>(gv ? v : z);
+      }
+    }
+  const int ngroups = (c1 - c0 + 15) >> 4;
+  const int lastvis = lim - 1;
+  const bool paged = p.layout_k == DSA_LAYOUT_PA_BSND;
+  const int32_t* btab = paged ? p.block_table + (int64_t)ri0.b * p.max_blocks : nullptr;
+  auto kload = [&](int grp, u32x4 (&kf)[KS]) {
+    int key = c0 + grp * 16 + li;
+    key = key < lastvis ? key : lastvis;
+    const int64_t krow = li_key_row(p, ri0, btab, key);
+    const T* kp = (const T*)p.k + krow * D + lg * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = __builtin_nontemporal_load((const u32x4*)(kp + ks * 32));
+  };
+  u32x4 kf[NP][KS];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) kload(min(wave + 4 * i, ngroups - 1), kf[i]);
+  float wv[2][GT][4];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int ht = 0; ht < GT; ++ht)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t b = wraw[r][ht][e];
+        const float x = p.w_dtype == DSA_DTYPE_FP32 ? __uint_as_float(b)
+                        : p.w_dtype == DSA_DTYPE_BF16 ? __uint_as_float(b << 16)
+                                                      : (float)__builtin_bit_cast(f16, (uint16_t)b);
+        wv[r][ht][e] = ht * 16 + lg * 4 + e < p.g ? x : 0.f;
+      }
+  auto process = [&](int gi, const u32x4 (&kf)[KS]) {
+    const int key = c0 + gi * 16 + li;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      f32x4 acc[GT];
+#pragma unroll
+      for (int ht = 0; ht < GT; ++ht) acc[ht] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const V8 bv = as_v8<V8>(kf[ks]);
+#pragma unroll
+        for (int ht = 0; ht < GT; ++ht) acc[ht] = E::mfma(qf[r][ht][ks], bv, acc[ht]);
+      }
+      float sc = 0.f;
+#pragma unroll
+      for (int ht = 0; ht < GT; ++ht)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sc += relu_bits(acc[ht][e]) * wv[r][ht][e];
+      sc = xgroup_sum(sc);
+      const int rl = r == 0 ? ri0.lim : ri1.lim;
+      if (lg == 0 && key < c1) s_sc[r][gi * 16 + li] = key < rl ? sc : -INFINITY;
+    }
+  };
+  for (int grp = wave; grp < ngroups; grp += 4 * NP) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int gi = grp + 4 * i;
+      if (gi < ngroups) process(gi, kf[i]);
+      kload(min(gi + 4 * NP, ngroups - 1), kf[i]);
+    }
+  }
+  __syncthreads();
+  li_store_chunk(p, ri0, btab, s_sc[0], srow0, c0, c1);
+  li_store_chunk(p, ri1, btab, s_sc[1], srow1, c0, c1);
+}
+
+// ---------------------------------------------------------------------------
 // Multi-row score kernel (BSND query, several query rows per batch, exact
 // head dims 64 / 128 / 256, 16-bit inputs).  One workgroup = kLiRows (4)
 // consecutive query rows s0 .. s0+3 of one (batch, key head); wave w owns
@@ -1679,6 +1809,25 @@ static hipError_t launch_score(const LiParams& p, hipStream_t stream) {
       void* args[] = {&q};
       return hipLaunchKernel((const void*)li_score_rows_kernel<D, T, GT>, dim3(grid, chunks), dim3(kLiRows * 64),
                              args, 0, stream);
+    }
+  }
+  // two query rows per batch (BSND, one key head): one workgroup per
+  // batch and key chunk runs both rows on each loaded key fragment, the
+  // chunk sized so that the grid puts one workgroup on every CU
+  if constexpr (!PAD && GT * (D / 32) <= 16) {
+    if (p.layout_q == DSA_LAYOUT_BSND && p.n2 == 1 && p.s1 == 2 && !(test_flags() & kTestLiNoPair)) {
+      LiParams q = p;
+      const int64_t pairs = p.q_rows / 2;
+      const int64_t target = (int64_t)device_cu_count();
+      const int64_t per = pairs >= target ? 1 : (target + pairs - 1) / pairs;
+      int64_t chunk = (p.s2 + per - 1) / per;
+      chunk = ((chunk + 63) / 64) * 64;
+      chunk = chunk < 64 ? 64 : chunk;
+      q.chunk = (int32_t)(chunk > kLiPairMaxChunk ? kLiPairMaxChunk : chunk);
+      const unsigned chunks = (unsigned)((p.s2 + q.chunk - 1) / q.chunk);
+      void* args[] = {&q};
+      return hipLaunchKernel((const void*)li_score_pair_kernel<D, T, GT, kLiPairRing>, dim3((unsigned)pairs, chunks),
+                             dim3(kLiThreads), args, 0, stream);
     }
   }
   // a few query rows per batch (BSND, one key head): a batch's rows on one

@@ -77,6 +77,9 @@ int dsa_abi_version(void);
 /* Bit 4: dsa_li_fwd / dsa_li_fwd_paged run the scores and the top-k as two
  * launches even where one launch does both. */
 #define DSA_TEST_LI_UNFUSED 16
+/* Bit 5: the indexer's scores of two query rows per batch (S1 = 2) run the
+ * one-row kernel (each row streams its keys) instead of the two-row one. */
+#define DSA_TEST_LI_NO_PAIR 32
 void dsa_set_test_flags(int32_t flags);
 
 /*

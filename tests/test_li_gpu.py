@@ -579,3 +579,57 @@ def test_indexer_fused_matches_two_launches(B, S1, S2, N1, K, mode, dtype, kind,
         vis = S2 if mode == 0 else None
         if vis is not None:
             np.testing.assert_array_equal(i1[0, 0, 0, :min(K, S2)], np.arange(min(K, S2)))
+
+
+@pytest.mark.parametrize("B,S2,N1,D,mode,paged,acts", [
+    (16, 8192, 64, 128, 3, False, False),   # multi-token decode shape
+    (4, 3000, 32, 128, 0, False, True),     # row lengths: the two rows see different ranges
+    (8, 5056, 64, 64, 3, True, False),      # paged keys (79 pages of 64) with a -1 page, D = 64
+    (2, 700, 16, 256, 3, False, True),      # D = 256, short rows, act_q hiding the second row
+])
+def test_indexer_two_rows_per_batch_match_one_row_kernel(B, S2, N1, D, mode, paged, acts):
+    """S1 = 2 runs the two-row score kernel (each key fragment serves both
+    rows); bit-identical indices and values against the one-row kernel
+    (test flag), and the indices against the oracle on every row."""
+    from dsa_triton_ascend_amd import _lib as L
+    dsa = _api()
+    lib = L.load()
+    print(f"[li pair] B={B} S2={S2} N1={N1} D={D} mode={mode} paged={paged} acts={acts}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(B + S2 + N1 + D)
+    bf = torch.bfloat16
+    q = torch.randn(B, 2, N1, D, generator=g, device="cuda").half().to(bf)
+    k = torch.randn(B, S2, 1, D, generator=g, device="cuda").half().to(bf)
+    w = torch.rand(B, 2, N1, generator=g, device="cuda")
+    K = 512
+    kw = dict(sparse_count=K, sparse_mode=mode, return_value=True)
+    if acts:
+        kw.update(actual_seq_lengths_query=[2 if b % 2 == 0 else 1 for b in range(B)],
+                  actual_seq_lengths_key=[S2 - 37 * b for b in range(B)])
+    kin = k
+    if paged:
+        page = 64
+        nblk = B * S2 // page
+        perm = torch.randperm(nblk, generator=g, device="cuda")
+        table = perm.to(torch.int32).reshape(B, S2 // page).contiguous()
+        cache = torch.empty(nblk, page, 1, D, dtype=bf, device="cuda")
+        cache[perm.long()] = k.reshape(nblk, page, 1, D)
+        table[1, 3] = -1
+        kw.update(block_table=table, layout_key="PA_BSND", actual_seq_lengths_key=[S2] * B)
+        kin = cache
+    outs = []
+    for flags in (0, L.TEST_LI_NO_PAIR):
+        lib.dsa_set_test_flags(flags)
+        try:
+            idx, val = dsa.lightning_indexer_triton(q, kin, w, **kw)
+            torch.cuda.synchronize()
+        finally:
+            lib.dsa_set_test_flags(0)
+        outs.append((idx.cpu().numpy(), val.float().cpu().numpy()))
+    (i1, v1), (i2, v2) = outs
+    np.testing.assert_array_equal(i1, i2)
+    np.testing.assert_array_equal(v1.view(np.uint32), v2.view(np.uint32))
+    assert (i1 >= -1).all() and (i1 < S2).all()
+    if not paged:
+        # every row against the oracle (near-tie flips allowed as in the full cases)
+        _full_case(B, 2, S2, N1, 1, D, K, mode, bf, act_q=kw.get("actual_seq_lengths_query"),
+                   act_k=kw.get("actual_seq_lengths_key"), max_flips=16, seed=B + S2 + N1 + D)
