@@ -16,7 +16,7 @@ token splits), together with the sfa_combine_kernel that merges its splits.
 
 Beside the headline, each leg of the operator set is timed the same way:
 the lightning indexer at 32K context (decode, secondary metric; also with
-S1 = 2 and 4 query rows per batch) and at the cfg2 prefill shape, the SFA prefill forward, the SFA backward (reference API
+S1 = 2, 3 and 4 query rows per batch) and at the cfg2 prefill shape, the SFA prefill forward, the SFA backward (reference API
 and training path), the sparse KL-loss backward and the dense warm-up stage.
 Each leg carries a CPU baseline: the numpy oracle (a tests-only restatement
 of the reference goldens) on the host cores, over the whole batch or a
@@ -951,11 +951,11 @@ def main():
     li_ms_after, _ = time_li(li_sets, args.steps, args.warmup)
     del li_sets
     torch.cuda.empty_cache()
-    # multi-token decode: S1 = 2 and 4 query rows per batch share the batch's
-    # keys (the per-row kernel re-reads them; L2 / Infinity Cache serve the
-    # repeats)
+    # multi-token decode: S1 = 2, 3 and 4 query rows per batch share the
+    # batch's keys (two rows: one workgroup runs both on each key fragment;
+    # three and more: the multi-row kernel shares key tiles through LDS)
     li_s1 = {}
-    for s1 in (2, 4):
+    for s1 in (2, 3, 4):
         ms_s1 = time_li_s1(s1, 2, args.steps, args.warmup, dev)
         li_s1[str(s1)] = {"ms_per_step": round(ms_s1, 5), "us_per_query": round(ms_s1 * 1e3 / (LI_B * s1), 4),
                           "key_GBps": round(LI_B * LI_S2 * LI_D * 2 / (ms_s1 * 1e-3) / 1e9, 1)}

@@ -1788,10 +1788,12 @@ static hipError_t launch_score(const LiParams& p, hipStream_t stream) {
   // one query row per batch: no key is read twice (exact head dims only)
   if (!PAD && p.q_rows == p.batch)
     return launch_score_kernel((const void*)li_score_kernel<D, T, GT, false, true>, p, stream);
-  // several query rows per batch (BSND): rows share key tiles through LDS,
-  // while the row's Q fragments fit the registers (GT * D / 32 <= 16)
+  // three or more query rows per batch (BSND): rows share key tiles through
+  // LDS, while the row's Q fragments fit the registers (GT * D / 32 <= 16);
+  // at three rows one of the four waves idles (multi-token decode S1 = 3 at
+  // B = 32: 140 us with the one-row kernel, 84 us here)
   if constexpr (!PAD && GT * (D / 32) <= 16) {
-    if (p.layout_q == DSA_LAYOUT_BSND && p.s1 >= 4) {
+    if (p.layout_q == DSA_LAYOUT_BSND && p.s1 >= 3) {
       LiParams q = p;
       const unsigned grid = (unsigned)((int64_t)p.batch * p.n2 * ((p.s1 + kLiRows - 1) / kLiRows));
       // few query rows per batch (multi-token decode): the rows' keys split
