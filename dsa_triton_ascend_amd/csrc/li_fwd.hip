@@ -128,15 +128,19 @@ constexpr int kLiMaxChunk = 8192;  // keys per workgroup (LDS score buffer)
 // Scores of the chunk [c0, c1) from s_sc to the row, in coalesced 16-byte
 // stores where the destination is 16-byte aligned; keys in -1 (or
 // out-of-range) pages of a paged cache are zero rows, score 0 while visible.
+// s_bt: the chunk's block-table entries staged in LDS from entry bt0 (null:
+// read the table in memory).
 __device__ __forceinline__ void li_store_chunk(const LiParams& p, const LiRow& ri, const int32_t* btab, float* s_sc,
-                                               float* srow, int c0, int c1) {
+                                               float* srow, int c0, int c1, const int* s_bt = nullptr,
+                                               int bt0 = 0) {
   const int n = c1 - c0;
   if (p.layout_k == DSA_LAYOUT_PA_BSND) {
     const int64_t nblk = p.k_rows / p.page_size;
     for (int j = threadIdx.x; j < n; j += kLiThreads) {
       const int key = c0 + j;
       if (key < ri.lim) {
-        const int blk = btab[key / p.page_size];
+        const int e = key / p.page_size;
+        const int blk = s_bt ? s_bt[e - bt0] : btab[e];
         if (blk < 0 || blk >= nblk) s_sc[j] = 0.f;
       }
     }
@@ -166,6 +170,42 @@ __device__ __forceinline__ int64_t li_key_row(const LiParams& p, const LiRow& ri
   return krow < p.k_rows ? krow : p.k_rows - 1;  // inconsistent cumulative lengths stay in bounds
 }
 
+// Paged keys: the block-table entries a chunk's key loads use, staged in
+// LDS before the key ring starts, so that each key load waits for an LDS
+// read instead of a dependent load of its table entry from memory (and the
+// page check at the store reads LDS too).  Launches keep a chunk within
+// kLiBtStage - 2 pages.
+constexpr int kLiBtStage = 1024;
+constexpr int kLiBtPer = kLiBtStage / kLiThreads;  // entries per thread
+
+__device__ __forceinline__ int64_t li_key_row_staged(const LiParams& p, const LiRow& ri, const int* s_bt, int bt0,
+                                                     int key) {
+  int64_t krow = ri.k_base + key;
+  if (p.layout_k == DSA_LAYOUT_PA_BSND) {
+    const int blk = s_bt[key / p.page_size - bt0];  // a -1 page reads row 0; scored 0 at the store
+    krow = (int64_t)(blk < 0 ? 0 : blk) * p.page_size + key % p.page_size;
+  }
+  return krow < p.k_rows ? krow : p.k_rows - 1;
+}
+
+// The table loads of the chunk's keys [c0, kend), issued unconditionally
+// (indices clamped into the range: a load under a lane condition is waited
+// for on the spot); li_tab_stage_store writes them to LDS after the
+// caller's other prologue loads are issued, then a barrier.
+__device__ __forceinline__ void li_tab_stage_load(const LiParams& p, const int32_t* btab, int c0, int kend,
+                                                  int (&tv)[kLiBtPer], int& bt0, int& ne) {
+  bt0 = c0 / p.page_size;
+  ne = min((kend - 1) / p.page_size - bt0 + 1, kLiBtStage);  // the launch cap keeps it below the bound
+#pragma unroll
+  for (int u = 0; u < kLiBtPer; ++u) tv[u] = btab[bt0 + min(u * kLiThreads + (int)threadIdx.x, ne - 1)];
+}
+__device__ __forceinline__ void li_tab_stage_store(int* s_bt, const int (&tv)[kLiBtPer], int ne) {
+#pragma unroll
+  for (int u = 0; u < kLiBtPer; ++u)
+    if (u * kLiThreads + (int)threadIdx.x < ne) s_bt[u * kLiThreads + threadIdx.x] = tv[u];
+  __syncthreads();
+}
+
 // NT: non-temporal key loads, for launches where no other query row reads
 // the same keys (one query row per batch, as at decode): the keys then have
 // no reuse to keep in the caches.
@@ -176,6 +216,7 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
   constexpr int KS = D / 32;
   const int dstride = PAD ? p.d : D;
   __shared__ __attribute__((aligned(16))) float s_sc[kLiMaxChunk];
+  __shared__ int s_bt[kLiBtStage];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
@@ -200,6 +241,13 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
     return;
   }
 
+  // paged keys: the chunk's table entries are loaded first (staged in LDS
+  // after the weight and Q loads are issued)
+  const bool paged = p.layout_k == DSA_LAYOUT_PA_BSND;
+  const int32_t* btab = paged ? p.block_table + (int64_t)ri.b * p.max_blocks : nullptr;
+  const int ngroups = (c1 - c0 + 15) >> 4;
+  int tv[kLiBtPer], bt0 = 0, ne = 0;
+  if (paged) li_tab_stage_load(p, btab, c0, min(c0 + 16 * ngroups, ri.lim), tv, bt0, ne);
   // weight of head ht*16 + 4*lg + r (the C-layout rows of this lane),
   // loaded first, as raw bits under one width branch, and converted only
   // after the first key groups are issued: loads issued before the branch,
@@ -233,19 +281,17 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
     }
   }
 
+  if (paged) li_tab_stage_store(s_bt, tv, ne);
   // key groups of 16: wave w takes groups w, w+4, ...; K fragment of group
   // kg (B operand): lane -> key kg*16 + li, d = ks*32 + 8*lg ..
-  const int ngroups = (c1 - c0 + 15) >> 4;
   const int lastvis = ri.lim - 1;
   // NP groups in flight per wave (ring of K fragment registers).  Loads are
   // issued unconditionally (groups past the end reload the last one), so no
   // load sits under a branch.
-  const bool paged = p.layout_k == DSA_LAYOUT_PA_BSND;
-  const int32_t* btab = paged ? p.block_table + (int64_t)ri.b * p.max_blocks : nullptr;
   auto kload = [&](int grp, u32x4 (&kf)[KS]) {
     int key = c0 + grp * 16 + li;
     key = key < lastvis ? key : lastvis;  // stays in the batch's rows; masked below
-    const int64_t krow = li_key_row(p, ri, btab, key);
+    const int64_t krow = li_key_row_staged(p, ri, s_bt, bt0, key);
     const T* kp = (const T*)p.k + (krow * p.n2 + kh) * dstride + lg * 8;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -299,7 +345,7 @@ __global__ __launch_bounds__(kLiThreads) void li_score_kernel(LiParams p) {
     }
   }
   __syncthreads();
-  li_store_chunk(p, ri, btab, s_sc, srow, c0, c1);
+  li_store_chunk(p, ri, btab, s_sc, srow, c0, c1, s_bt, bt0);
 }
 
 // ---------------------------------------------------------------------------
@@ -320,6 +366,7 @@ __global__ __launch_bounds__(kLiThreads) void li_score_pair_kernel(LiParams p) {
   using V8 = typename E::v8;
   constexpr int KS = D / 32;
   __shared__ __attribute__((aligned(16))) float s_sc[2][kLiPairMaxChunk];
+  __shared__ int s_bt[kLiBtStage];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
@@ -338,6 +385,11 @@ __global__ __launch_bounds__(kLiThreads) void li_score_pair_kernel(LiParams p) {
     }
     return;
   }
+  const bool paged = p.layout_k == DSA_LAYOUT_PA_BSND;
+  const int32_t* btab = paged ? p.block_table + (int64_t)ri0.b * p.max_blocks : nullptr;
+  const int ngroups = (c1 - c0 + 15) >> 4;
+  int tv[kLiBtPer], bt0 = 0, ne = 0;
+  if (paged) li_tab_stage_load(p, btab, c0, min(c0 + 16 * ngroups, lim), tv, bt0, ne);
   // weights as raw bits (converted after the first key groups are issued)
   uint32_t wraw[2][GT][4];
   auto load_w = [&](auto* wp) {
@@ -368,14 +420,12 @@ __global__ __launch_bounds__(kLiThreads) void li_score_pair_kernel(LiParams p) {
         qf[r][ht][ks] = as_v8<V8>(gv ? v : z);
       }
     }
-  const int ngroups = (c1 - c0 + 15) >> 4;
+  if (paged) li_tab_stage_store(s_bt, tv, ne);
   const int lastvis = lim - 1;
-  const bool paged = p.layout_k == DSA_LAYOUT_PA_BSND;
-  const int32_t* btab = paged ? p.block_table + (int64_t)ri0.b * p.max_blocks : nullptr;
   auto kload = [&](int grp, u32x4 (&kf)[KS]) {
     int key = c0 + grp * 16 + li;
     key = key < lastvis ? key : lastvis;
-    const int64_t krow = li_key_row(p, ri0, btab, key);
+    const int64_t krow = li_key_row_staged(p, ri0, s_bt, bt0, key);
     const T* kp = (const T*)p.k + krow * D + lg * 8;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) kf[ks] = __builtin_nontemporal_load((const u32x4*)(kp + ks * 32));
@@ -428,8 +478,8 @@ __global__ __launch_bounds__(kLiThreads) void li_score_pair_kernel(LiParams p) {
     }
   }
   __syncthreads();
-  li_store_chunk(p, ri0, btab, s_sc[0], srow0, c0, c1);
-  li_store_chunk(p, ri1, btab, s_sc[1], srow1, c0, c1);
+  li_store_chunk(p, ri0, btab, s_sc[0], srow0, c0, c1, s_bt, bt0);
+  li_store_chunk(p, ri1, btab, s_sc[1], srow1, c0, c1, s_bt, bt0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1770,6 +1820,13 @@ int li_topk_run(const float* scores, int64_t rows, int64_t s2, int64_t k, int32_
 // measured slower: they start together, but one streams ahead while the
 // other waits behind it, so the grid ran as two serial rounds with a long
 // tail (decode step 72.5 -> 66.6 us with one per CU).
+// Largest chunk (a multiple of 64 keys) whose key loads, 16-key groups
+// included, stay within the kLiBtStage staged table entries.
+static int64_t li_paged_chunk_cap(int64_t page) {
+  const int64_t cap = ((kLiBtStage - 3) * page / 64) * 64;
+  return cap < 64 ? 64 : cap;
+}
+
 static hipError_t launch_score_kernel(const void* fn, LiParams p, hipStream_t stream) {
   const int64_t rows = p.q_rows * p.n2;
   const int64_t target = (int64_t)device_cu_count();
@@ -1778,6 +1835,7 @@ static hipError_t launch_score_kernel(const void* fn, LiParams p, hipStream_t st
   chunk = ((chunk + 63) / 64) * 64;
   chunk = chunk < 64 ? 64 : chunk;
   p.chunk = (int32_t)(chunk > kLiMaxChunk ? kLiMaxChunk : chunk);
+  if (p.layout_k == DSA_LAYOUT_PA_BSND) p.chunk = (int32_t)std::min<int64_t>(p.chunk, li_paged_chunk_cap(p.page_size));
   const unsigned chunks = (unsigned)((p.s2 + p.chunk - 1) / p.chunk);
   void* args[] = {&p};
   return hipLaunchKernel(fn, dim3((unsigned)rows, chunks), dim3(kLiThreads), args, 0, stream);
@@ -1826,6 +1884,7 @@ static hipError_t launch_score(const LiParams& p, hipStream_t stream) {
       chunk = ((chunk + 63) / 64) * 64;
       chunk = chunk < 64 ? 64 : chunk;
       q.chunk = (int32_t)(chunk > kLiPairMaxChunk ? kLiPairMaxChunk : chunk);
+      if (p.layout_k == DSA_LAYOUT_PA_BSND) q.chunk = (int32_t)std::min<int64_t>(q.chunk, li_paged_chunk_cap(p.page_size));
       const unsigned chunks = (unsigned)((p.s2 + q.chunk - 1) / q.chunk);
       void* args[] = {&q};
       return hipLaunchKernel((const void*)li_score_pair_kernel<D, T, GT, kLiPairRing>, dim3((unsigned)pairs, chunks),
