@@ -58,7 +58,20 @@ struct LiParams {
   // block_table[b, s2 / page] * page + s2 % page (k_rows = blocks * page)
   const int32_t* block_table;
   int32_t max_blocks, page_size;
+  int32_t page_shift;  // log2(page_size) for a power of two, else -1
 };
+
+// Page of key `key` and its row in the page: a shift and a mask for the
+// usual power-of-two page sizes, where an integer division by the runtime
+// page size costs some tens of instructions per key
+__device__ __forceinline__ int li_page(const LiParams& p, int key) {
+  if (p.page_shift >= 0) return key >> p.page_shift;
+  return key / p.page_size;
+}
+__device__ __forceinline__ int li_in_page(const LiParams& p, int key) {
+  if (p.page_shift >= 0) return key & (p.page_size - 1);
+  return key % p.page_size;
+}
 
 constexpr int kLiThreads = 256;
 
@@ -139,7 +152,7 @@ __device__ __forceinline__ void li_store_chunk(const LiParams& p, const LiRow& r
     for (int j = threadIdx.x; j < n; j += kLiThreads) {
       const int key = c0 + j;
       if (key < ri.lim) {
-        const int e = key / p.page_size;
+        const int e = li_page(p, key);
         const int blk = s_bt ? s_bt[e - bt0] : btab[e];
         if (blk < 0 || blk >= nblk) s_sc[j] = 0.f;
       }
@@ -182,8 +195,8 @@ __device__ __forceinline__ int64_t li_key_row_staged(const LiParams& p, const Li
                                                      int key) {
   int64_t krow = ri.k_base + key;
   if (p.layout_k == DSA_LAYOUT_PA_BSND) {
-    const int blk = s_bt[key / p.page_size - bt0];  // a -1 page reads row 0; scored 0 at the store
-    krow = (int64_t)(blk < 0 ? 0 : blk) * p.page_size + key % p.page_size;
+    const int blk = s_bt[li_page(p, key) - bt0];  // a -1 page reads row 0; scored 0 at the store
+    krow = (int64_t)(blk < 0 ? 0 : blk) * p.page_size + li_in_page(p, key);
   }
   return krow < p.k_rows ? krow : p.k_rows - 1;
 }
@@ -523,10 +536,13 @@ constexpr int kLiRowBufs = 3;   // LDS ring of key tiles
 template <int D> constexpr int li_row_tile_bytes() { return kLiRowTile * D * 2; }
 
 // The score rows of one workgroup (body of the kernels below): s_k is the
-// kLiRowBufs-tile ring, s_lim kLiRows words.
-template <int D, typename T, int GT>
+// kLiRowBufs-tile ring, s_lim kLiRows words, s_bt kLiBtRows words.
+constexpr int kLiBtRows = kLiRows * 64;  // staged table entries (one per thread)
+// PG: the keys are a paged cache (a separate instantiation, so that the
+// dense-key code carries none of the page handling)
+template <int D, typename T, int GT, bool PG>
 __device__ __forceinline__ void li_rows_scores(const LiParams& p, unsigned char (*s_k)[li_row_tile_bytes<D>()],
-                                               int* s_lim) {
+                                               int* s_lim, int* s_bt) {
   using E = Elem<T>;
   using V8 = typename E::v8;
   constexpr int KS = D / 32;                       // k-steps
@@ -593,7 +609,7 @@ __device__ __forceinline__ void li_rows_scores(const LiParams& p, unsigned char 
 
   // DMA j of this wave covers tile rows (j * kLiRows + wave) * RPD .. +RPD-1;
   // lane L: row + L / CPR, LDS chunk L % CPR <- source chunk (L % CPR) ^ swz
-  const bool paged = p.layout_k == DSA_LAYOUT_PA_BSND;
+  constexpr bool paged = PG;
   const int32_t* btab = paged ? p.block_table + (int64_t)ri.b * p.max_blocks : nullptr;
   const int64_t nblk = paged ? p.k_rows / p.page_size : 0;
   // the last key a DMA loads: the rows' last visible key, kept inside the
@@ -602,6 +618,24 @@ __device__ __forceinline__ void li_rows_scores(const LiParams& p, unsigned char 
   int lastkey = kend > 0 ? kend - 1 : 0;
   const int64_t kbase = ri.k_base < p.k_rows ? ri.k_base : p.k_rows - 1;
   if (!paged && kbase + lastkey > p.k_rows - 1) lastkey = (int)(p.k_rows - 1 - kbase);
+  // paged keys: the table entries of every key this workgroup's DMAs load
+  // (tiles tb .. te + 1, clamped to lastkey) staged in LDS where they fit
+  // (kLiBtRows entries), so that a tile's DMAs wait for LDS reads rather
+  // than for dependent loads of their entries from memory
+  int bt0 = 0;
+  bool staged = false;
+  if (paged) {
+    const int klo = min(tb * kLiRowTile, lastkey);
+    const int khi = min(lastkey, (te + 2) * kLiRowTile - 1);
+    bt0 = klo / p.page_size;
+    const int ne = khi / p.page_size - bt0 + 1;
+    staged = ne <= kLiBtRows;
+    if (staged) {
+      const int v = btab[bt0 + min((int)threadIdx.x, ne - 1)];
+      if ((int)threadIdx.x < ne) s_bt[threadIdx.x] = v;
+      lds_barrier();
+    }
+  }
   // loop-invariant per DMA: tile row, source chunk, and (dense keys) the
   // address of key 0's chunk; a key adds key * n2 * D elements
   int tr_j[NDW], ch_j[NDW];
@@ -621,9 +655,11 @@ __device__ __forceinline__ void li_rows_scores(const LiParams& p, unsigned char 
       key = key < lastkey ? key : lastkey;  // past the rows' keys: reload the last one
       const T* src = base_j[j] + key * key_stride;
       if (paged) {
-        const int blk = btab[key / p.page_size];
+        int blk;
+        if (staged) blk = s_bt[li_page(p, key) - bt0];
+        else blk = btab[li_page(p, key)];
         const bool zero = blk < 0 || (int64_t)blk >= nblk;
-        const int64_t krow = (int64_t)(zero ? 0 : blk) * p.page_size + key % p.page_size;
+        const int64_t krow = (int64_t)(zero ? 0 : blk) * p.page_size + li_in_page(p, key);
         src = zero ? (const T*)g_li_zero_row + ch_j[j] * 8 : (const T*)p.k + (krow * p.n2 + kh) * D + ch_j[j] * 8;
       }
       li_dma16((unsigned)(uintptr_t)&s_k[buf][d * 1024], src);
@@ -699,11 +735,12 @@ __device__ __forceinline__ void li_rows_scores(const LiParams& p, unsigned char 
     for (int key = te * kLiRowTile + lane; key < key_end; key += 64) srow[key] = -INFINITY;
 }
 
-template <int D, typename T, int GT>
+template <int D, typename T, int GT, bool PG>
 __global__ __launch_bounds__(kLiRows * 64) void li_score_rows_kernel(LiParams p) {
   __shared__ __attribute__((aligned(1024))) unsigned char s_k[kLiRowBufs][li_row_tile_bytes<D>()];
   __shared__ int s_lim[kLiRows];
-  li_rows_scores<D, T, GT>(p, s_k, s_lim);
+  __shared__ int s_bt[kLiBtRows];
+  li_rows_scores<D, T, GT, PG>(p, s_k, s_lim, s_bt);
 }
 
 // fp32 query / key (and weights): the products run on v_mfma_f32_16x16x4f32
@@ -1690,13 +1727,14 @@ __global__ __launch_bounds__(kTopkThreads) void li_topk_quad_kernel(TopkParams p
 // ---------------------------------------------------------------------------
 constexpr int32_t kTopkMark = -2147483647 - 1;  // below every index (-1 pads)
 
-template <int D, typename T, int GT, int KPT>
+template <int D, typename T, int GT, int KPT, bool PG>
 __global__ __launch_bounds__(kLiRows * 64) void li_score_rows_topk_kernel(LiParams p, TopkParams tp) {
   constexpr int TB = li_row_tile_bytes<D>();
   static_assert(kLiRowBufs * TB >= (int)kQuadRowLds, "one row's selection buffers fit the tile ring");
   __shared__ __attribute__((aligned(1024))) unsigned char s_k[kLiRowBufs][TB];
   __shared__ int s_lim[kLiRows];
-  li_rows_scores<D, T, GT>(p, s_k, s_lim);
+  __shared__ int s_bt[kLiBtRows];
+  li_rows_scores<D, T, GT, PG>(p, s_k, s_lim, s_bt);
   // the workgroup's rows, as li_rows_scores maps them
   const int nbk = p.batch * p.n2;
   const int ngroups = (p.s1 + kLiRows - 1) / kLiRows;
@@ -1867,7 +1905,9 @@ static hipError_t launch_score(const LiParams& p, hipStream_t stream) {
         if (chunks <= 1) q.row_tiles = 0;
       }
       void* args[] = {&q};
-      return hipLaunchKernel((const void*)li_score_rows_kernel<D, T, GT>, dim3(grid, chunks), dim3(kLiRows * 64),
+      const void* fn = p.layout_k == DSA_LAYOUT_PA_BSND ? (const void*)li_score_rows_kernel<D, T, GT, true>
+                                                        : (const void*)li_score_rows_kernel<D, T, GT, false>;
+      return hipLaunchKernel(fn, dim3(grid, chunks), dim3(kLiRows * 64),
                              args, 0, stream);
     }
   }
@@ -1983,6 +2023,7 @@ static LiParams li_params(const void* query, const void* key, const void* weight
   p.block_table = block_table;
   p.max_blocks = (int32_t)max_blocks;
   p.page_size = (int32_t)(page_size > 0 ? page_size : 1);
+  p.page_shift = (p.page_size & (p.page_size - 1)) == 0 ? __builtin_ctz((unsigned)p.page_size) : -1;
   p.chunk = kLiChunk;
   p.row_tiles = 0;
   p.xcd_group = 0;
@@ -2001,8 +2042,9 @@ static hipError_t launch_fused(const LiParams& p, const TopkParams& tp, hipStrea
   TopkParams t = tp;
   const unsigned grid = (unsigned)((int64_t)p.batch * p.n2 * ((p.s1 + kLiRows - 1) / kLiRows));
   void* args[] = {&q, &t};
-  return hipLaunchKernel((const void*)li_score_rows_topk_kernel<128, T, 4, KPT>, dim3(grid), dim3(kLiRows * 64),
-                         args, 0, stream);
+  const void* fn = p.layout_k == DSA_LAYOUT_PA_BSND ? (const void*)li_score_rows_topk_kernel<128, T, 4, KPT, true>
+                                                    : (const void*)li_score_rows_topk_kernel<128, T, 4, KPT, false>;
+  return hipLaunchKernel(fn, dim3(grid), dim3(kLiRows * 64), args, 0, stream);
 }
 
 int li_fwd_run(const void* query, const void* key, const void* weights, const int32_t* act_q,

@@ -366,12 +366,13 @@ def _paged_case(B, page, max_blocks, N2, D, dtype, seed, holes=True):
     return cache, table, dense
 
 
-@pytest.mark.parametrize("layout_q", ["BSND", "TND"])
-def test_indexer_paged_matches_depaged(layout_q):
-    print(f"[li paged] query {layout_q}", flush=True)
+# page 24: not a power of two (the kernels divide instead of shifting)
+@pytest.mark.parametrize("layout_q,page", [("BSND", 16), ("TND", 16), ("BSND", 24)])
+def test_indexer_paged_matches_depaged(layout_q, page):
+    print(f"[li paged] query {layout_q} page {page}", flush=True)
     dsa = _api()
     dtype = torch.bfloat16
-    B, S1, N1, N2, D, page, mb, K = 3, 4, 16, 1, 128, 16, 8, 48
+    B, S1, N1, N2, D, mb, K = 3, 4, 16, 1, 128, 8, 48
     cache, table, dense = _paged_case(B, page, mb, N2, D, dtype, seed=41)
     S2 = mb * page
     q, _, w = _inputs(B, S1, S2, N1, N2, D, dtype, seed=43)
@@ -416,12 +417,13 @@ def test_indexer_paged_matches_depaged(layout_q):
     assert flips <= max(2, got.size // 200)
 
 
-def test_indexer_paged_decode_scores():
-    print("[li paged] decode scores", flush=True)
+@pytest.mark.parametrize("page", [64, 48])
+def test_indexer_paged_decode_scores(page):
+    print(f"[li paged] decode scores page {page}", flush=True)
     dsa = _api()
     from dsa_triton_ascend_amd import _lib
     dtype = torch.bfloat16
-    B, N1, D, page, mb = 4, 64, 128, 64, 16
+    B, N1, D, mb = 4, 64, 128, 16
     cache, table, dense = _paged_case(B, page, mb, 1, D, dtype, seed=47)
     S2 = mb * page
     q, _, w = _inputs(B, 1, S2, N1, 1, D, dtype, seed=49)
