@@ -542,7 +542,7 @@ constexpr int kLiBtRows = kLiRows * 64;  // staged table entries (one per thread
 // dense-key code carries none of the page handling)
 template <int D, typename T, int GT, bool PG>
 __device__ __forceinline__ void li_rows_scores(const LiParams& p, unsigned char (*s_k)[li_row_tile_bytes<D>()],
-                                               int* s_lim, int* s_bt) {
+                                               int* s_lim, int* s_bt, int tnd_seq = -1) {
   using E = Elem<T>;
   using V8 = typename E::v8;
   constexpr int KS = D / 32;                       // k-steps
@@ -557,15 +557,34 @@ __device__ __forceinline__ void li_rows_scores(const LiParams& p, unsigned char 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int li = lane & 15, lg = lane >> 4;
-  const int nbk = p.batch * p.n2;
-  const int ngroups = (p.s1 + kLiRows - 1) / kLiRows;
-  const int bk = blockIdx.x % nbk;
-  const int grp = ngroups - 1 - (int)(blockIdx.x / nbk);  // longest rows first
-  const int b = bk / p.n2, kh = bk - b * p.n2;
-  const int s1 = grp * kLiRows + wave;
-  const bool active = s1 < p.s1;
-  const int row = b * p.s1 + (active ? s1 : 0);
-  const LiRow ri = li_row_info(p, row);
+  int kh = 0, row;
+  bool active;
+  LiRow ri, rs;  // this wave's row; a row of the sequence whose keys the tiles hold
+  if (tnd_seq < 0) {
+    const int nbk = p.batch * p.n2;
+    const int ngroups = (p.s1 + kLiRows - 1) / kLiRows;
+    const int bk = blockIdx.x % nbk;
+    const int grp = ngroups - 1 - (int)(blockIdx.x / nbk);  // longest rows first
+    const int b = bk / p.n2;
+    kh = bk - b * p.n2;
+    const int s1 = grp * kLiRows + wave;
+    active = s1 < p.s1;
+    row = b * p.s1 + (active ? s1 : 0);
+    ri = li_row_info(p, row);
+    rs = ri;
+  } else {
+    // packed (TND) rows, one key head: group g = four consecutive rows, the
+    // last groups (longest causal ranges) first; a group whose rows span
+    // several sequences runs once per sequence (tnd_seq), with the rows of
+    // the other sequences idle
+    const int g = (int)((p.q_rows + kLiRows - 1) / kLiRows) - 1 - (int)blockIdx.x;
+    const int prow = g * kLiRows + wave;
+    row = prow < p.q_rows ? prow : g * kLiRows;
+    ri = li_row_info(p, row);
+    active = prow < p.q_rows && ri.b == tnd_seq;
+    const int qstart = tnd_seq > 0 ? p.act_q[tnd_seq - 1] : 0;
+    rs = li_row_info(p, max(g * kLiRows, qstart));
+  }
   const int lim = active ? ri.lim : 0;
   if (lane == 0) s_lim[wave] = lim;
   float* srow = p.scores + ((int64_t)row * p.n2 + kh) * p.s2;
@@ -610,13 +629,13 @@ __device__ __forceinline__ void li_rows_scores(const LiParams& p, unsigned char 
   // DMA j of this wave covers tile rows (j * kLiRows + wave) * RPD .. +RPD-1;
   // lane L: row + L / CPR, LDS chunk L % CPR <- source chunk (L % CPR) ^ swz
   constexpr bool paged = PG;
-  const int32_t* btab = paged ? p.block_table + (int64_t)ri.b * p.max_blocks : nullptr;
+  const int32_t* btab = paged ? p.block_table + (int64_t)rs.b * p.max_blocks : nullptr;
   const int64_t nblk = paged ? p.k_rows / p.page_size : 0;
   // the last key a DMA loads: the rows' last visible key, kept inside the
   // key tensor (dense keys: row kbase + key <= k_rows - 1, as li_key_row
   // clamps inconsistent cumulative lengths)
   int lastkey = kend > 0 ? kend - 1 : 0;
-  const int64_t kbase = ri.k_base < p.k_rows ? ri.k_base : p.k_rows - 1;
+  const int64_t kbase = rs.k_base < p.k_rows ? rs.k_base : p.k_rows - 1;
   if (!paged && kbase + lastkey > p.k_rows - 1) lastkey = (int)(p.k_rows - 1 - kbase);
   // paged keys: the table entries of every key this workgroup's DMAs load
   // (tiles tb .. te + 1, clamped to lastkey) staged in LDS where they fit
@@ -740,7 +759,20 @@ __global__ __launch_bounds__(kLiRows * 64) void li_score_rows_kernel(LiParams p)
   __shared__ __attribute__((aligned(1024))) unsigned char s_k[kLiRowBufs][li_row_tile_bytes<D>()];
   __shared__ int s_lim[kLiRows];
   __shared__ int s_bt[kLiBtRows];
-  li_rows_scores<D, T, GT, PG>(p, s_k, s_lim, s_bt);
+  if (p.layout_q != DSA_LAYOUT_TND) {
+    li_rows_scores<D, T, GT, PG>(p, s_k, s_lim, s_bt);
+    return;
+  }
+  // packed rows: one pass per sequence among the group's four rows
+  const int g = (int)((p.q_rows + kLiRows - 1) / kLiRows) - 1 - (int)blockIdx.x;
+  const int seq0 = li_row_info(p, g * kLiRows).b;
+  const int seq1 = li_row_info(p, (int)min((int64_t)g * kLiRows + kLiRows - 1, p.q_rows - 1)).b;
+  for (int sq = seq0; sq <= seq1; ++sq) {
+    const int qs = sq > 0 ? p.act_q[sq - 1] : 0;
+    if (p.act_q[sq] == qs) continue;  // an empty sequence (uniform: same for every thread)
+    __syncthreads();                  // the previous pass's LDS reads are done
+    li_rows_scores<D, T, GT, PG>(p, s_k, s_lim, s_bt, sq);
+  }
 }
 
 // fp32 query / key (and weights): the products run on v_mfma_f32_16x16x4f32
@@ -1889,9 +1921,14 @@ static hipError_t launch_score(const LiParams& p, hipStream_t stream) {
   // at three rows one of the four waves idles (multi-token decode S1 = 3 at
   // B = 32: 140 us with the one-row kernel, 84 us here)
   if constexpr (!PAD && GT * (D / 32) <= 16) {
-    if (p.layout_q == DSA_LAYOUT_BSND && p.s1 >= 3) {
+    // packed (TND) queries with one key head and three or more rows per
+    // sequence on average: groups of four consecutive rows, a group that
+    // spans sequences running once per sequence
+    const bool tnd_rows = p.layout_q == DSA_LAYOUT_TND && p.n2 == 1 && p.q_rows >= 3 * (int64_t)p.batch;
+    if ((p.layout_q == DSA_LAYOUT_BSND && p.s1 >= 3) || tnd_rows) {
       LiParams q = p;
-      const unsigned grid = (unsigned)((int64_t)p.batch * p.n2 * ((p.s1 + kLiRows - 1) / kLiRows));
+      const unsigned grid = tnd_rows ? (unsigned)((p.q_rows + kLiRows - 1) / kLiRows)
+                                     : (unsigned)((int64_t)p.batch * p.n2 * ((p.s1 + kLiRows - 1) / kLiRows));
       // few query rows per batch (multi-token decode): the rows' keys split
       // into chunks of at least 8 tiles, so that about two workgroups per CU
       // run (one workgroup per row group left most CUs idle)

@@ -326,6 +326,42 @@ def test_indexer_tnd_matches_bsnd():
         off += lens_q[b]
 
 
+@pytest.mark.parametrize("lens_q,extra_k", [
+    ([300, 0, 1, 517, 2, 1200], [0, 5, 0, 40, 3, 0]),   # groups of four rows that span sequences, an empty one
+    ([4096, 4096], [0, 0]),                              # cfg2 packed
+])
+def test_indexer_tnd_multirow_matches_per_sequence(lens_q, extra_k):
+    """Packed (TND) queries run the multi-row kernel in groups of four
+    consecutive rows (a group spanning sequences runs once per sequence):
+    bit-identical to each sequence run on its own in BSND."""
+    print(f"[li tnd] lens {lens_q}", flush=True)
+    dsa = _api()
+    dtype = torch.bfloat16
+    lens_k = [a + e for a, e in zip(lens_q, extra_k)]
+    N1, D, K = 64, 128, 256
+    rng = np.random.RandomState(sum(lens_q))
+    qs = [to_dtype_np(rng.randn(L, N1, D).astype(np.float32), dtype) for L in lens_q]
+    ks = [to_dtype_np(rng.randn(L, 1, D).astype(np.float32), dtype) for L in lens_k]
+    ws = [rng.rand(L, N1).astype(np.float32) for L in lens_q]
+    cq, ck = [int(x) for x in np.cumsum(lens_q)], [int(x) for x in np.cumsum(lens_k)]
+    idx_t, val_t = dsa.lightning_indexer_triton(
+        dev(np.concatenate(qs), dtype), dev(np.concatenate(ks), dtype), dev(np.concatenate(ws), torch.float32),
+        cq, ck, layout_query="TND", layout_key="TND", sparse_count=K, sparse_mode=3, return_value=True)
+    torch.cuda.synchronize()
+    idx_t, val_t = idx_t.cpu().numpy(), val_t.float().cpu().numpy()
+    off = 0
+    for b, L in enumerate(lens_q):
+        if L > 0:
+            i_b, v_b = dsa.lightning_indexer_triton(
+                dev(qs[b][None], dtype), dev(ks[b][None], dtype), dev(ws[b][None], torch.float32),
+                sparse_count=K, sparse_mode=3, return_value=True)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(idx_t[off:off + L], i_b.cpu().numpy()[0])
+            np.testing.assert_array_equal(val_t[off:off + L].view(np.uint32),
+                                          v_b.float().cpu().numpy()[0].view(np.uint32))
+        off += L
+
+
 def test_indexer_guards():
     dsa = _api()
     q = torch.zeros(1, 2, 8, 128, dtype=torch.bfloat16, device="cuda")
