@@ -186,8 +186,8 @@ __device__ __forceinline__ int64_t li_key_row(const LiParams& p, const LiRow& ri
 // Paged keys: the block-table entries a chunk's key loads use, staged in
 // LDS before the key ring starts, so that each key load waits for an LDS
 // read instead of a dependent load of its table entry from memory (and the
-// page check at the store reads LDS too).  Launches keep a chunk within
-// kLiBtStage - 2 pages.
+// page check at the store reads LDS too).  Launches size the chunks so that
+// their entries fit kLiBtStage (li_paged_chunk_cap).
 constexpr int kLiBtStage = 1024;
 constexpr int kLiBtPer = kLiBtStage / kLiThreads;  // entries per thread
 
