@@ -1466,12 +1466,15 @@ __global__ __launch_bounds__(kTopkThreads) void li_topk_kernel(TopkParams p) {
 
   // ---- outputs ----
   int32_t* irow = p.indices + row * (int64_t)K;
+  const bool want_val = p.values != nullptr && !p.val_zero;
   for (int i = tid; i < K; i += kTopkThreads) {
     int idx = -1;
     float val = -INFINITY;
     if (i < take) {
       idx = (int)(unsigned)(outb[i] & 0xffffffffull);
-      val = srow[idx];  // the score itself (keeps the sign of a zero)
+      // the score itself (keeps the sign of a zero), read only where values
+      // are requested: the load would otherwise hold the next iteration
+      if (want_val) val = srow[idx];
     }
     irow[i] = idx;
     if (p.values) {
